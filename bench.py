@@ -1,0 +1,190 @@
+"""Fine-tuning throughput of the Laya ModernBERT decision model on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one full optimizer step over one synthetic batch: forward, the decision head's soft
+cross-entropy gradient, backward, global-norm clip and AdamW (fwd+bwd+AdamW), all on the device.
+Workload: ModernBERT-base (22 layers, d 768, 12 heads × 64, GeGLU 1152, vocab 50368, every third
+layer global, the rest a 128-token sliding window) plus the two-layer decision head, fp32, batch
+32 × seq 512 with a trailing-padding fraction U[0, 0.3] per sequence (padding is never computed:
+sequences are packed), items cycling choice K=8 / score K=4 / noul K=2, summed cross-entropy,
+AdamW lr 3e-5 wd 0.01, clip 1.0, head dropout 0.1. Weights N(0, 0.02) from a fixed seed.
+
+Prints one JSON line. `value` counts real (unpadded) tokens per second over the timed steps, with
+every input already resident; `roofline` describes the kernel with the largest share of device
+time, measured live with HIP events on the library's stream; `cpu_baseline` times the C++ oracle
+(the reference algorithm restated, per-layer recompute included) on a bounded sample of the same
+workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "fine-tune tokens/sec (fwd+bwd+AdamW), 1 MI355X; bwd MFMA util % & HBM GB/s"
+PEAK_FP32_MFMA = 157.3e12
+PEAK_HBM = 8.0e12
+MFMA_KERNELS = ("gemm_nt", "gemm_nn", "gemm_tn", "attention_fwd", "attention_bwd_dkv", "attention_bwd_dq")
+
+
+def make_batch(rng, batch=32, seq=512, vocab=50368, pad_max=0.3):
+    from laya_amd.batch import Batch
+    fractions = rng.uniform(0.0, pad_max, size=batch)
+    lengths = (seq - np.floor(seq * fractions)).astype(np.int32)
+    kinds = [(0, 8), (1, 4), (2, 2)]  # choice K=8, score K=4, noul K=2
+    qtypes = np.array([kinds[i % 3][0] for i in range(batch)], np.int32)
+    n_options = np.array([kinds[i % 3][1] for i in range(batch)], np.int32)
+    tokens = rng.integers(0, vocab, size=int(lengths.sum()), dtype=np.int64).astype(np.int32)
+    markers = np.concatenate([1 + 2 * np.arange(k) for k in n_options]).astype(np.int32)
+    labels = [rng.integers(0, k) for k in n_options]
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[lab] for k, lab in zip(n_options, labels)])
+    return Batch(lengths=lengths, tokens=tokens, n_options=n_options, markers=markers, qtypes=qtypes), targets
+
+
+def cpu_baseline(mc, batch, targets, items: int):
+    """The oracle (reference algorithm, fp32, OpenMP over the host cores) on the first `items`
+    sequences of the batch: one full step (forward, CE, backward with per-layer recompute, clip, AdamW)."""
+    import oracle
+    from laya_amd.batch import Batch
+    sub = Batch(lengths=batch.lengths[:items], tokens=batch.tokens[:int(batch.lengths[:items].sum())],
+                n_options=batch.n_options[:items], markers=batch.markers[:int(batch.n_options[:items].sum())],
+                qtypes=batch.qtypes[:items])
+    o = oracle.OracleModel(mc)
+    prng = np.random.default_rng(1)
+    o.set_params({n: (np.ones(s, np.float32) if ("norm" in n and n.endswith("weight")) or n == "scorer.0.weight"
+                      or n == "temperature" else
+                      np.zeros(s, np.float32) if n.endswith("bias") else
+                      (0.02 * prng.standard_normal(s)).astype(np.float32)) for n, s in o.shapes.items()})
+    o.set_head_dropout(0.1)
+    o.adamw(0.0, 0.0)  # allocates the moments, as the reference's first step does, outside the timed step
+    t_sub = targets[:sub.n_markers]
+    t0 = time.perf_counter()
+    logits = o.forward(sub, training=True, keep_tape=True, seed=1).astype(np.float32)
+    _, g = oracle.cross_entropy(sub.n_options, logits, t_sub, 1.0, float(sub.n_items))
+    o.backward(g)
+    o.clip(1.0)
+    o.adamw(3e-5, 3e-5)
+    dt = time.perf_counter() - t0
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": sub.n_tokens / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"one full fp32 step (fwd+CE+bwd with per-layer recompute+clip+AdamW over all 164M params) "
+                      f"of the first {items} sequences ({sub.n_tokens} real tokens) of the same batch, "
+                      f"{dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
+    ap.add_argument("--cpu-items", type=int, default=8)
+    ap.add_argument("--no-profile", action="store_true", help="time without per-launch events")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from laya_amd.config import modernbert_base
+    from laya_amd.device import Context
+    from laya_amd.model import TrainableDecisionModel
+
+    rng = np.random.default_rng(2024)
+    mc = modernbert_base()
+    batches = [make_batch(rng) for _ in range(args.warmup + args.steps)]
+    ctx = Context(0)
+    model = TrainableDecisionModel.synthetic(mc, seed=42, std=0.02, ctx=ctx)
+    model.head_dropout = 0.1
+    prepared = [(b, t, model.batch_args(b)) for b, t in batches]
+
+    def step(i):
+        b, t, a = prepared[i]
+        model.train_step(b, t, seed=1000 + i, ce_weight=1.0, loss_scale=float(b.n_items), max_norm=1.0,
+                         lr_encoder=3e-5, lr_head=3e-5, weight_decay=0.01, _args=a)
+
+    print(f"warmup {args.warmup} steps", file=sys.stderr, flush=True)
+    for i in range(args.warmup):
+        step(i)
+    ctx.sync()
+    if not args.no_profile:
+        ctx.profile_begin()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, args.warmup + args.steps):
+        step(i)
+    ctx.sync()
+    elapsed = time.perf_counter() - t0
+    prof = ctx.profile_end() if not args.no_profile else {}
+    tokens = sum(b.n_tokens for b, _, _ in prepared[args.warmup:])
+    loss = model.train_step(*prepared[0][:2], seed=7, want_loss=True, _args=prepared[0][2])
+    print(f"timed {args.steps} steps in {elapsed:.3f} s, {tokens} real tokens, loss after {loss:.4f}",
+          file=sys.stderr, flush=True)
+
+    roofline, breakdown = None, {}
+    if prof:
+        total_ms = sum(k["ms"] for k in prof.values())
+        for name, k in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+            print(f"  {name:22s} {k['launches']:6d} launches {k['ms']:9.2f} ms "
+                  f"{k['ms'] / total_ms * 100:5.1f}%  "
+                  + (f"{k['flops'] / k['ms'] / 1e9:8.1f} TFLOP/s" if k["flops"] else
+                     f"{k['bytes'] / k['ms'] / 1e6:8.1f} GB/s"), file=sys.stderr)
+        name, k = max(prof.items(), key=lambda kv: kv[1]["ms"])
+        per_launch_s = k["ms"] / k["launches"] / 1e3
+        if k["flops"]:
+            achieved = k["flops"] / k["launches"] / per_launch_s
+            roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved / 1e12, 2),
+                        "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
+                        "traffic": None, "avg_launch_ms": round(per_launch_s * 1e3, 4), "launches": k["launches"]}
+        else:
+            achieved = k["bytes"] / k["launches"] / per_launch_s
+            roofline = {"bound": "hbm", "kernel": name, "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
+                        "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                        "avg_launch_ms": round(per_launch_s * 1e3, 4), "launches": k["launches"]}
+        bwd = [prof[n] for n in ("gemm_nn", "gemm_tn") if n in prof]
+        if bwd:
+            f = sum(x["flops"] for x in bwd)
+            ms = sum(x["ms"] for x in bwd)
+            breakdown["bwd_gemm_mfma_util"] = round(f / (ms / 1e3) / PEAK_FP32_MFMA, 4)
+        attn = [prof[n] for n in ("attention_bwd_dkv", "attention_bwd_dq") if n in prof]
+        if attn:
+            f = sum(x["flops"] for x in attn)
+            ms = sum(x["ms"] for x in attn)
+            breakdown["attention_bwd_mfma_util"] = round(f / (ms / 1e3) / PEAK_FP32_MFMA, 4)
+        ew = [prof[n] for n in ("layernorm_bwd", "geglu_bwd", "relu_dropout_bwd") if n in prof]
+        if ew:
+            b = sum(x["bytes"] for x in ew)
+            ms = sum(x["ms"] for x in ew)
+            breakdown["elementwise_bwd_hbm_gbs"] = round(b / (ms / 1e3) / 1e9, 1)
+        breakdown["kernel_share"] = {n: round(k["ms"] / total_ms, 4) for n, k in
+                                     sorted(prof.items(), key=lambda kv: -kv[1]["ms"])[:8]}
+
+    cpu = None
+    if not args.no_cpu:
+        print(f"cpu baseline: oracle on {args.cpu_items} sequences", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(mc, *batches[args.warmup], items=args.cpu_items)
+
+    value = tokens / elapsed
+    line = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 3), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": "ModernBERT-base Laya encoder + decision head fp32 fine-tune step, batch 32 x "
+                                   "seq 512, trailing padding U[0,0.3], heads choice8/score4/noul2, summed CE, "
+                                   "AdamW lr 3e-5 wd 0.01, clip 1.0",
+                       "global_batch": 32, "seq_len": 512, "parallelism": "none (1 GPU)",
+                       "real_tokens_per_step": round(tokens / args.steps, 1)},
+            "roofline": roofline, "cpu_baseline": cpu, "breakdown": breakdown}
+    print(json.dumps(line), flush=True)
+    model.close()
+    ctx.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,236 @@
+/* laya_hip.h — C-ABI of liblaya_hip.so, the MI355X (gfx950) fine-tuning library for the Laya
+ * ModernBERT decision model.
+ *
+ * The reference has no FFI: its swap point is the C# op surface `internal static class Ops`
+ * (src/StructuredDecisions.Laya.Training/Ops.cs:17), plus `AdamW.Step` (AdamW.cs:29) and
+ * `Gradients.ClipByGlobalNorm` (AdamW.cs:103). Each entry point below replaces one of those
+ * methods (cited beside it) and keeps its argument meaning and its accumulate/overwrite
+ * convention (Ops.cs:12-15): a forward writes its output; laya_linear_bwd OVERWRITES dx; every
+ * other backward ADDS into its input gradient; parameter gradients always ACCUMULATE.
+ *
+ * Conventions of this ABI:
+ *  - Every function returns an int status (LAYA_OK = 0); laya_last_error() gives a thread-local
+ *    message for the last failure on the calling thread.
+ *  - Tensor arguments are DEVICE pointers (from laya_alloc) to row-major fp32 data unless noted;
+ *    sizes are element counts. Segment tables are device int32 arrays.
+ *  - Calls are ordered on the context's single HIP stream and asynchronous until laya_sync().
+ *    A context is not re-entrant; separate contexts are independent.
+ *  - Results do not depend on launch configuration: no floating-point atomics; every reduction
+ *    over rows runs in a fixed order.
+ */
+#ifndef LAYA_HIP_H
+#define LAYA_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. The C# binding rethrows them as the reference's exception types. */
+#define LAYA_OK 0
+#define LAYA_ERR_ARGUMENT 1     /* ArgumentException (size mismatch, PackedMatrix.cs:124-126) */
+#define LAYA_ERR_OUT_OF_RANGE 2 /* ArgumentOutOfRangeException (token id, TrainableDecisionModel.cs:281) */
+#define LAYA_ERR_MEMORY 3       /* out of device memory, or over the context's allocation cap */
+#define LAYA_ERR_HIP 4          /* a HIP runtime error */
+#define LAYA_ERR_NOT_FINITE 5   /* a non-finite gradient norm */
+#define LAYA_ERR_STATE 6        /* call order (backward with no tape) */
+#define LAYA_ERR_MISSING 7      /* InvalidDataException: missing tensor (TrainableDecisionModel.cs:184-186) */
+
+typedef struct laya_ctx laya_ctx;
+typedef struct laya_rotary laya_rotary;
+typedef struct laya_model laya_model;
+
+const char* laya_last_error(void);
+const char* laya_version(void);
+
+/* ---------------------------------------------------------------- context, memory, stream */
+int laya_ctx_create(int device, laya_ctx** out);
+int laya_ctx_destroy(laya_ctx* ctx);
+/* Caps the bytes laya_alloc may hold (0 = no cap); an allocation over it fails with LAYA_ERR_MEMORY. */
+int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes);
+int laya_ctx_memory_in_use(laya_ctx* ctx, size_t* bytes);
+int laya_alloc(laya_ctx* ctx, size_t bytes, void** out);
+int laya_free(laya_ctx* ctx, void* ptr);
+int laya_upload(laya_ctx* ctx, void* dst, const void* src_host, size_t bytes);
+int laya_download(laya_ctx* ctx, void* dst_host, const void* src, size_t bytes);
+int laya_fill(laya_ctx* ctx, float* dst, float value, size_t count);
+int laya_sync(laya_ctx* ctx);
+/* Stage timers: laya_timer_begin/end bracket stream work with HIP events; elapsed in ms. */
+int laya_timer_begin(laya_ctx* ctx, int slot);
+int laya_timer_end(laya_ctx* ctx, int slot);
+int laya_timer_elapsed(laya_ctx* ctx, int slot, float* ms);
+
+/* Live kernel profile: while enabled, every launch is bracketed by HIP events on the context's
+ * stream and tagged with its algorithmic work (flops for matrix-core kernels, compulsory HBM bytes
+ * for memory-bound ones). laya_profile_summary aggregates per kernel name, after a sync. */
+int laya_profile_begin(laya_ctx* ctx);
+int laya_profile_end(laya_ctx* ctx);
+int laya_profile_count(laya_ctx* ctx, int* kernels);
+int laya_profile_get(laya_ctx* ctx, int i, const char** name, int* launches, double* total_ms, double* flops,
+                     double* bytes);
+
+/* ---------------------------------------------------------------------------- ops (Ops.cs) */
+
+/* Ops.Linear (Ops.cs:22-27): y[rows,out] = x[rows,in] · W[out,in]ᵀ (+ b[out]) (+ residual[rows,out]).
+ * b and residual may be NULL; residual may alias y (the skip add of TrainableDecisionModel.cs:384, 401). */
+int laya_linear_fwd(laya_ctx* ctx, const float* x, int rows, int in, const float* W, int out, const float* b,
+                    const float* residual, float* y);
+
+/* Ops.LinearBackward (Ops.cs:33-69): dx = dy·W (OVERWRITE; skipped when dx is NULL),
+ * dW += dyᵀ·x and db += Σ_rows dy (each skipped when NULL). */
+int laya_linear_bwd(laya_ctx* ctx, const float* x, const float* dy, int rows, int in, int out, const float* W,
+                    float* dx, float* dW, float* db);
+
+/* Ops.LayerNorm (Ops.cs:103-110; SimdOps.cs:234-272): torch LayerNorm, biased variance, eps inside
+ * the square root, b may be NULL. mean/rstd (may be NULL) receive the row statistics. */
+int laya_layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps,
+                       float* y, float* mean, float* rstd);
+
+/* Ops.LayerNormBackward (Ops.cs:117-186): dx += rstd·(g − mean(g) − x̂·mean(g·x̂)), g = dy·γ;
+ * dgamma += Σ dy·x̂; dbeta += Σ dy (each may be NULL). mean/rstd from laya_layernorm_fwd, or NULL to
+ * recompute them from x. */
+int laya_layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
+                       float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd);
+
+/* SimdOps.Gelu (SimdOps.cs:305-323), exact erf GELU: y = gelu(x). y may alias x. */
+int laya_gelu_fwd(laya_ctx* ctx, const float* x, size_t n, float* y);
+/* Ops.GeluBackward (Ops.cs:194-218): grad *= Φ(u) + u·φ(u) (in place). */
+int laya_gelu_bwd(laya_ctx* ctx, const float* u, float* grad, size_t n);
+
+/* GeGLU (TrainableDecisionModel.cs:390-398): act[t,i] = gelu(wide[t,i]) · wide[t,I+i], halves [input | gate]. */
+int laya_geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act);
+/* GeGLU backward (TrainableDecisionModel.cs:564-579): dwide = [dact·gate·gelu'(input) | dact·gelu(input)] (overwrite). */
+int laya_geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide);
+
+/* Ops.Uniform / Ops.Mix (Ops.cs:227-241): host-side counter RNG, bit-identical to the device kernels. */
+float laya_uniform(uint64_t seed, uint64_t index);
+uint64_t laya_mix(uint64_t seed, uint64_t salt);
+/* Ops.Dropout (Ops.cs:244-258): in place, x·keep/(1−p) with keep = Uniform(seed, i) ≥ p; its own backward. */
+int laya_dropout(laya_ctx* ctx, float* values, size_t n, float p, uint64_t seed);
+/* Head FFN activation (TrainableDecisionModel.cs:449-451): dropped = Dropout(ReLU(wide)). */
+int laya_relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped);
+/* Its backward (TrainableDecisionModel.cs:620-624): grad = Dropout(grad), then 0 where wide ≤ 0 (in place). */
+int laya_relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* grad, size_t n, float p, uint64_t seed);
+/* SimdOps.Add (SimdOps.cs:84-93): dst += src. */
+int laya_add(laya_ctx* ctx, float* dst, const float* src, size_t n);
+
+/* Rotary (Ops.cs:446-504): cos/sin tables built in double and rounded to float, θ_i = θ^(−2i/d). */
+int laya_rotary_create(laya_ctx* ctx, int head_dim, double theta, int positions, laya_rotary** out);
+int laya_rotary_destroy(laya_ctx* ctx, laya_rotary* rot);
+/* Rotary.Apply (Ops.cs:489-503) on rows of [rows, head_dim] at positions pos[rows] (device int32). */
+int laya_rotary_apply(laya_ctx* ctx, const laya_rotary* rot, float* vec, int rows, const int* pos, int inverse);
+
+/* Ops.AttentionForward (Ops.cs:275-277, 329-366): multi-head attention per segment over qkv rows
+ * [q | k | v] (head slice at head·d_h), RoPE with segment-local positions (rot NULL: none), window
+ * [t − w, t + w] clipped to the segment (half_window < 0: none), softmax(scale·qkᵀ), prob-dropout p
+ * with the counter RNG at index head<<42 | row<<21 | key (Ops.cs:318).
+ * seg_start/seg_len: device int32 [nseg]; max_len ≥ every seg_len. lse [rows·heads] receives the
+ * row log-sum-exp (base 2, of the scaled scores) the backward reuses. */
+int laya_attention_fwd(laya_ctx* ctx, const float* qkv, const int* seg_start, const int* seg_len, int nseg,
+                       int max_len, int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
+                       float p_drop, uint64_t seed, float* context, float* lse);
+/* Ops.AttentionBackward (Ops.cs:280-282, 368-438): dq, dk, dv WRITTEN (not added) into dqkv, with
+ * inverse RoPE on dq and dk. Needs the forward's context and lse. */
+int laya_attention_bwd(laya_ctx* ctx, const float* qkv, const int* seg_start, const int* seg_len, int nseg,
+                       int max_len, int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
+                       float p_drop, uint64_t seed, const float* context, const float* lse, const float* dcontext,
+                       float* dqkv);
+
+/* Embedding gather (TrainableDecisionModel.cs:277-283): out[t] = E[ids[t]]; ids are checked on the
+ * device: an id outside [0, vocab) writes zeros and sets *bad_count (device int32, may be NULL). */
+int laya_embedding_fwd(laya_ctx* ctx, const int* ids, int n, const float* E, int vocab, int hidden, float* out,
+                       int* bad_count);
+/* Deterministic scatter plan on the host: token positions stably sorted by id, the unique ids and
+ * their run offsets (offsets has n_unique + 1 entries). */
+int laya_embedding_plan(const int* ids, int n, int vocab, int* sorted_pos, int* unique_ids, int* offsets,
+                        int* n_unique);
+/* Embedding-gradient scatter (TrainableDecisionModel.cs:543-547): grad[id] += Σ d[t] over that id's
+ * tokens, in token order. Plan arrays are device copies of laya_embedding_plan's output. */
+int laya_embedding_bwd(laya_ctx* ctx, const int* sorted_pos, const int* unique_ids, const int* offsets, int n_unique,
+                       const float* d, int hidden, float* grad);
+
+/* Marker gather (TrainableDecisionModel.cs:315) and scatter-add (500-504), in marker order. */
+int laya_gather_rows(laya_ctx* ctx, const float* src, const int* rows_idx, int n, int width, float* dst);
+int laya_scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows_idx, int n, int width, float* dst);
+
+/* Soft cross-entropy gradient of RlcdObjective (RlcdObjective.cs:139-148, 150), policy term off:
+ * g_o = ce_weight·(p_o·Σt − t_o)/n_items·scale with p = softmax(logits). Device arrays; options
+ * concatenated, option_offsets[n_items + 1]. loss (device, may be NULL) receives the cross-entropy. */
+int laya_softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets, const int* option_offsets,
+                        int n_items, float ce_weight, float scale, float* grad, float* loss);
+
+/* Gradients.ClipByGlobalNorm (AdamW.cs:103-130) over a flat arena: Σg² in double, in a fixed order.
+ * Writes the norm (double) and the clip coefficient (float, 1 when not clipping) to device memory.
+ * Sets LAYA_ERR_NOT_FINITE only through laya_grad_norm_status. */
+int laya_grad_norm(laya_ctx* ctx, const float* grads, size_t n, double max_norm, double* norm_out, float* coef_out);
+/* Multi-tensor AdamW (AdamW.cs:29-73) over a flat arena split into parameter groups:
+ * element i of group g (ranges [begin[g], end[g])) uses lr[g]; g_i is scaled by *coef (device, may be
+ * NULL = 1) as the clip does; zero_grads clears the gradient after it is read. */
+int laya_adamw(laya_ctx* ctx, float* params, float* grads, float* m, float* v, int n_groups, const size_t* begin,
+               const size_t* end, const double* lr, double beta1, double beta2, double eps, double weight_decay,
+               int step, const float* coef, int zero_grads);
+
+/* ---------------------------------------------- model (TrainableDecisionModel.cs, Trainer.cs) */
+
+typedef struct {
+    int vocab, hidden, intermediate, layers, heads;
+    int local_attention;    /* full sliding window (ModernBertConfig.cs:51: a token sees ±local_attention/2) */
+    int global_every;       /* when layer_kinds is NULL: layer l is global iff l % global_every == 0 */
+    const int* layer_kinds; /* host [layers]: 0 global, 1 sliding; may be NULL */
+    double theta_global, theta_local;
+    float norm_eps;
+    int norm_bias, attention_bias, mlp_bias;
+    int head_layers, head_ff, n_act;
+} laya_model_config;
+
+typedef struct {
+    int n_items;
+    const int* lengths;   /* host [n_items] */
+    const int* tokens;    /* host [Σ lengths], concatenated with no padding */
+    const int* n_options; /* host [n_items] */
+    const int* markers;   /* host [Σ n_options], positions inside each item */
+    const int* qtypes;    /* host [n_items]: 0 choice, 1 score, 2 noul */
+} laya_batch;
+
+/* TrainableDecisionModel constructor (TrainableDecisionModel.cs:105-182). Parameters live in one
+ * device arena in module order; names follow the checkpoint's state-dict names. */
+int laya_model_create(laya_ctx* ctx, const laya_model_config* cfg, laya_model** out);
+int laya_model_destroy(laya_model* model);
+int laya_model_num_params(laya_model* model, int* count);
+int laya_model_param_info(laya_model* model, int i, const char** name, int* ndim, int* dims /* [4] */,
+                          size_t* offset, size_t* numel, int* trainable);
+int laya_model_find_param(laya_model* model, const char* name, int* index);
+int laya_model_set_param(laya_model* model, int i, const float* host);
+int laya_model_get_param(laya_model* model, int i, float* host);
+int laya_model_get_grad(laya_model* model, int i, float* host);
+int laya_model_has_grad(laya_model* model, int i, int* has);
+/* Synthetic init: matrices and embeddings N(0, std) from the counter RNG, norm weights 1, biases 0. */
+int laya_model_init_random(laya_model* model, uint64_t seed, float std);
+/* SetTrainableEncoderLayers (TrainableDecisionModel.cs:206-231); n < 0 trains everything. */
+int laya_model_set_trainable_encoder_layers(laya_model* model, int n);
+int laya_model_set_head_dropout(laya_model* model, float p);
+/* Forward (TrainableDecisionModel.cs:248-353). Keeps every activation the backward needs resident
+ * in HBM (no recompute). logits_host (may be NULL) receives Σ n_options floats and synchronises. */
+int laya_model_forward(laya_model* model, const laya_batch* batch, int training, uint64_t seed, float* logits_host);
+/* Backward (TrainableDecisionModel.cs:479-549): dlogits_host has Σ n_options floats. */
+int laya_model_backward(laya_model* model, const float* dlogits_host);
+/* Gradients.ClipByGlobalNorm (AdamW.cs:103-130); norm_out (may be NULL) synchronises. */
+int laya_model_clip_grad_norm(laya_model* model, double max_norm, double* norm_out);
+/* AdamW.Step (AdamW.cs:29-73) with the trainer's groups (Trainer.cs:96-100): "encoder." parameters at
+ * lr_encoder, the rest at lr_head. Applies the clip coefficient of the last clip, if any. */
+int laya_model_adamw_step(laya_model* model, double lr_encoder, double lr_head, double beta1, double beta2,
+                          double eps, double weight_decay);
+int laya_model_zero_grad(laya_model* model);
+/* One full optimizer step (Trainer.cs:131-144 with GradAccum = 1): forward, soft cross-entropy
+ * gradient on the device (targets_host: Σ n_options floats), backward, clip, AdamW, zero grads.
+ * Synchronises only when loss_out is non-NULL. */
+int laya_model_train_step(laya_model* model, const laya_batch* batch, const float* targets_host, float ce_weight,
+                          float loss_scale, uint64_t seed, double max_norm, double lr_encoder, double lr_head,
+                          double beta1, double beta2, double eps, double weight_decay, float* loss_out);
+int laya_model_steps(laya_model* model, int* steps);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,561 @@
+// Attention forward and backward on CDNA4 matrix cores (fp32, v_mfma_f32_32x32x2_f32).
+//
+// Restates Ops.AttentionForward / Ops.AttentionBackward (src/StructuredDecisions.Laya.Training/Ops.cs:263-438)
+// flash-style: per (segment, head), q·k scores over the window [t − w, t + w] clipped to the segment
+// (Ops.cs:315-316), RoPE with segment-local positions applied as tiles are loaded (Gather, Ops.cs:297-313),
+// softmax with an online max and sum, probability dropout regenerated from the counter RNG at
+// head<<42 | row<<21 | key (Ops.cs:318, 355, 401), and the inverse RoPE on dq and dk (Ops.cs:421-427).
+// The forward saves each row's base-2 log-sum-exp; the backward recomputes P from it instead of
+// re-running the row softmax.
+//
+// Layout trick: the forward computes Sᵀ = K·Qᵀ, so in the 32×32 accumulator a lane owns one query
+// (its column) and 16 keys (its rows). Those registers are exactly the B operand of Oᵀ = Vᵀ·Pᵀ, so
+// P never leaves registers, and each query's running max / sum live in one lane pair.
+// The backward runs two kernels, both without atomics (deterministic):
+//   dkv: each wave owns 32 keys (K, V in registers) and sweeps the query tiles: S = Q·Kᵀ,
+//        dVᵀ += dOᵀ·P, dP = dO·Vᵀ, dS, dKᵀ += Qᵀ·dS;
+//   dq:  each wave owns 32 queries (Q, dO in registers) and sweeps the key tiles: Sᵀ, dPᵀ, dSᵀ,
+//        dQᵀ += Kᵀ·dSᵀ.
+#include "common.hpp"
+
+namespace laya {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int THREADS = 256;
+constexpr int WAVE_ROWS = 32;   // queries (or keys) owned by one wave
+constexpr int BLOCK_ROWS = 128; // 4 waves
+constexpr int TILE = 64;        // rows of the streamed operand per LDS tile
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+struct Params {
+    const float* qkv;
+    const int* seg_start;
+    const int* seg_len;
+    int hidden, heads, half_window;  // half_window < 0: no window
+    float scale, scale_log2, p_drop, keep;
+    uint64_t seed;
+    const float* cos_t;
+    const float* sin_t;
+    float* context;
+    float* lse;
+    const float* dcontext;
+    const float* dots;  // Σ_d dO·O per (row, head)
+    float* dqkv;
+};
+
+template <int D> struct Shape {
+    static constexpr int G = D / 8;     // float4 groups per lane (the lane's half of d)
+    static constexpr int ND = D / 32;   // 32-row d tiles of an accumulator
+    static constexpr int GP = D / 16;   // group offset of the rotary partner d + D/2
+    static constexpr int FP = D / 4;    // flat accumulator offset of the rotary partner
+    static constexpr int KS = D + 4;    // LDS stride of tiles read as b128 fragments
+    static constexpr int VS = D + 8;    // LDS stride of tiles read as b32 columns
+};
+
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+
+__device__ __forceinline__ f32x16 mfma(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bool in_window(int q, int key, int L, int hw) {
+    return q < L && key >= 0 && key < L && (hw < 0 || (key - q <= hw && q - key <= hw));
+}
+
+// Loads `rows` rows [row0, row0 + rows) of one head's q, k or v slice into LDS with stride S,
+// applying RoPE (position = segment-local row) when `rope`; rows outside [0, L) become zeros.
+template <int D, int S>
+__device__ __forceinline__ void load_rows(const Params& p, float* lds, int start, int L, int row0, int rows, int col,
+                                          bool rope) {
+    const long stride = 3L * p.hidden;
+    if (rope) {
+        constexpr int units_per_row = D / 8;
+        for (int u = threadIdx.x; u < rows * units_per_row; u += THREADS) {
+            const int r = u / units_per_row, j = (u - r * units_per_row) * 4;
+            const int t = row0 + r;
+            f32x4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
+            if (t >= 0 && t < L) {
+                const float* src = p.qkv + (long)(start + t) * stride + col;
+                a = ld4(src + j);
+                b = ld4(src + D / 2 + j);
+                const f32x4 c = ld4(p.cos_t + (long)t * (D / 2) + j);
+                const f32x4 s = ld4(p.sin_t + (long)t * (D / 2) + j);
+                const f32x4 na = a * c - b * s;
+                const f32x4 nb = b * c + a * s;
+                a = na;
+                b = nb;
+            }
+            st4(lds + r * S + j, a);
+            st4(lds + r * S + D / 2 + j, b);
+        }
+    } else {
+        constexpr int units_per_row = D / 4;
+        for (int u = threadIdx.x; u < rows * units_per_row; u += THREADS) {
+            const int r = u / units_per_row, j = (u - r * units_per_row) * 4;
+            const int t = row0 + r;
+            f32x4 a = {0, 0, 0, 0};
+            if (t >= 0 && t < L) a = ld4(p.qkv + (long)(start + t) * stride + col + j);
+            st4(lds + r * S + j, a);
+        }
+    }
+}
+
+// Loads the lane's own row (d = 8g + 4h + c) into registers, with RoPE at position t.
+template <int D>
+__device__ __forceinline__ void load_lane_row(const float* src, const Params& p, int t, bool valid, bool rope, int h,
+                                              f32x4 (&v)[Shape<D>::G]) {
+    using S = Shape<D>;
+#pragma unroll
+    for (int g = 0; g < S::G; ++g) v[g] = valid ? ld4(src + 8 * g + 4 * h) : f32x4{0, 0, 0, 0};
+    if (rope && valid) {
+#pragma unroll
+        for (int g = 0; g < S::GP; ++g) {
+            const int i = 8 * g + 4 * h;
+            const f32x4 c = ld4(p.cos_t + (long)t * (D / 2) + i);
+            const f32x4 s = ld4(p.sin_t + (long)t * (D / 2) + i);
+            const f32x4 a = v[g], b = v[g + S::GP];
+            v[g] = a * c - b * s;
+            v[g + S::GP] = b * c + a * s;
+        }
+    }
+}
+
+// Inverse RoPE on an accumulator whose column is the lane's row t and whose rows are d.
+template <int D>
+__device__ __forceinline__ void inverse_rope_acc(f32x16 (&acc)[Shape<D>::ND], const Params& p, int t, int h) {
+    using S = Shape<D>;
+#pragma unroll
+    for (int f = 0; f < S::FP; ++f) {
+        const int dt = f >> 4, r = f & 15;
+        const int pf = f + S::FP, pdt = pf >> 4, pr = pf & 15;
+        const int i = dt * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        const float c = p.cos_t[(long)t * (D / 2) + i], s = p.sin_t[(long)t * (D / 2) + i];
+        const float a = acc[dt][r], b = acc[pdt][pr];
+        acc[dt][r] = a * c + b * s;
+        acc[pdt][pr] = b * c - a * s;
+    }
+}
+
+// Writes an accumulator (rows d, column = the lane's row) into row `row` of dst at column `col`.
+template <int D>
+__device__ __forceinline__ void store_acc(const f32x16 (&acc)[Shape<D>::ND], float* dst_row, int h, float scale) {
+#pragma unroll
+    for (int dt = 0; dt < Shape<D>::ND; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x4 v = {acc[dt][4 * r4] * scale, acc[dt][4 * r4 + 1] * scale, acc[dt][4 * r4 + 2] * scale,
+                             acc[dt][4 * r4 + 3] * scale};
+            st4(dst_row + dt * 32 + 8 * r4 + 4 * h, v);
+        }
+}
+
+// ------------------------------------------------------------------------------------ forward
+
+template <int D>
+__global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
+    using S = Shape<D>;
+    __shared__ __attribute__((aligned(16))) float Ks[TILE * S::KS];
+    __shared__ __attribute__((aligned(16))) float Vs[TILE * S::VS];
+
+    const int seg = blockIdx.y, head = blockIdx.z;
+    const int start = p.seg_start[seg], L = p.seg_len[seg];
+    const int qb0 = blockIdx.x * BLOCK_ROWS;
+    if (qb0 >= L) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
+    const int q0w = qb0 + wave * WAVE_ROWS;
+    const int q = q0w + lr;
+    const bool qvalid = q < L;
+    const bool rope = p.cos_t != nullptr;
+    const int hw = p.half_window;
+    const long stride = 3L * p.hidden;
+    const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
+
+    f32x4 qv[S::G];
+    load_lane_row<D>(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, p, q, qvalid, rope, h, qv);
+
+    int kbeg = 0, kend = L;
+    int wbeg = 0, wend = L;
+    if (hw >= 0) {
+        kbeg = max(0, qb0 - hw);
+        kend = min(L, qb0 + BLOCK_ROWS + hw);
+        wbeg = max(0, q0w - hw);
+        wend = min(L, q0w + WAVE_ROWS + hw);
+    }
+
+    f32x16 o[S::ND];
+#pragma unroll
+    for (int dt = 0; dt < S::ND; ++dt) o[dt] = f32x16{};
+    float m = -1e30f, l = 0.0f;
+
+    for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
+        __syncthreads();
+        load_rows<D, S::KS>(p, Ks, start, L, kt0, TILE, kcol, rope);
+        load_rows<D, S::VS>(p, Vs, start, L, kt0, TILE, vcol, false);
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < TILE / 32; ++st) {
+            const int kbs = kt0 + 32 * st;
+            if (kbs >= wend || kbs + 32 <= wbeg || kbs >= kend) continue;  // wave-uniform
+            f32x16 s = f32x16{};
+            const float* krow = Ks + (32 * st + lr) * S::KS + 4 * h;
+#pragma unroll
+            for (int g = 0; g < S::G; ++g) {
+                const f32x4 kf = ld4(krow + 8 * g);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) s = mfma(kf[c], qv[g][c], s);
+            }
+            float t[16];
+            float mx = -1e30f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
+                t[r] = in_window(q, key, L, hw) ? s[r] * p.scale_log2 : NEG_INF;
+                mx = fmaxf(mx, t[r]);
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mnew = fmaxf(m, mx);
+            const float alpha = exp2f(m - mnew);
+            float pr[16];
+            float sum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                pr[r] = exp2f(t[r] - mnew);
+                sum += pr[r];
+            }
+            l = l * alpha + sum;
+            m = mnew;
+#pragma unroll
+            for (int dt = 0; dt < S::ND; ++dt) o[dt] *= alpha;
+            if (p.p_drop > 0.0f) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const float u = uniform01(p.seed, attn_dropout_index(head, start + q, key));
+                    pr[r] = u < p.p_drop ? 0.0f : pr[r] * p.keep;
+                }
+            }
+#pragma unroll
+            for (int dt = 0; dt < S::ND; ++dt) {
+                const float* vcolp = Vs + (32 * st + 4 * h) * S::VS + dt * 32 + lr;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt] = mfma(vcolp[(8 * (r >> 2) + (r & 3)) * S::VS], pr[r], o[dt]);
+            }
+        }
+    }
+
+    const float lt = l + __shfl_xor(l, 32, 64);
+    if (qvalid) {
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        store_acc<D>(o, p.context + (long)(start + q) * p.hidden + qcol, h, inv);
+        if (h == 0) p.lse[(long)(start + q) * p.heads + head] = lt > 0.0f ? m + log2f(lt) : __builtin_huge_valf();
+    }
+}
+
+// ------------------------------------------------------------------------------------ backward
+
+// dots[row, head] = Σ_d dO · O: the row constant c = Σ_j p_j·dp_j of Ops.cs:408-409.
+template <int D>
+__global__ __launch_bounds__(THREADS) void attn_dot_kernel(const float* __restrict__ dctx, const float* __restrict__ ctx,
+                                                           int rows, int hidden, int heads, float* __restrict__ dots) {
+    const long i = blockIdx.x * (long)THREADS + threadIdx.x;
+    const long total = (long)rows * hidden;
+    float v = i < total ? dctx[i] * ctx[i] : 0.0f;
+#pragma unroll
+    for (int o = D / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    if (i < total && (i % D) == 0) {
+        const long row = i / hidden;
+        const int head = (int)((i - row * hidden) / D);
+        dots[row * heads + head] = v;
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
+    using S = Shape<D>;
+    __shared__ __attribute__((aligned(16))) float Qs[TILE * S::KS];
+    __shared__ __attribute__((aligned(16))) float Os[TILE * S::VS];  // dO rows
+    __shared__ float lse_s[TILE], dot_s[TILE];
+
+    const int seg = blockIdx.y, head = blockIdx.z;
+    const int start = p.seg_start[seg], L = p.seg_len[seg];
+    const int kb0 = blockIdx.x * BLOCK_ROWS;
+    if (kb0 >= L) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
+    const int k0w = kb0 + wave * WAVE_ROWS;
+    const int key = k0w + lr;
+    const bool kvalid = key < L;
+    const bool rope = p.cos_t != nullptr;
+    const int hw = p.half_window;
+    const long stride = 3L * p.hidden;
+    const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
+
+    f32x4 kv[S::G], vv[S::G];
+    const long krow = (long)(start + (kvalid ? key : 0)) * stride;
+    load_lane_row<D>(p.qkv + krow + kcol, p, key, kvalid, rope, h, kv);
+    load_lane_row<D>(p.qkv + krow + vcol, p, key, kvalid, false, h, vv);
+
+    int qbeg = 0, qend = L, wbeg = 0, wend = L;
+    if (hw >= 0) {
+        qbeg = max(0, kb0 - hw);
+        qend = min(L, kb0 + BLOCK_ROWS + hw);
+        wbeg = max(0, k0w - hw);
+        wend = min(L, k0w + WAVE_ROWS + hw);
+    }
+
+    f32x16 dk[S::ND], dv[S::ND];
+#pragma unroll
+    for (int dt = 0; dt < S::ND; ++dt) {
+        dk[dt] = f32x16{};
+        dv[dt] = f32x16{};
+    }
+
+    for (int qt0 = qbeg; qt0 < qend; qt0 += TILE) {
+        __syncthreads();
+        load_rows<D, S::KS>(p, Qs, start, L, qt0, TILE, qcol, rope);
+        // dO rows come from dcontext [rows, hidden]; load them through the same helper layout.
+        for (int u = threadIdx.x; u < TILE * (D / 4); u += THREADS) {
+            const int r = u / (D / 4), j = (u - r * (D / 4)) * 4;
+            const int t = qt0 + r;
+            f32x4 a = {0, 0, 0, 0};
+            if (t < L) a = ld4(p.dcontext + (long)(start + t) * p.hidden + qcol + j);
+            st4(Os + r * S::VS + j, a);
+        }
+        for (int r = threadIdx.x; r < TILE; r += THREADS) {
+            const int t = qt0 + r;
+            lse_s[r] = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
+            dot_s[r] = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < TILE / 32; ++st) {
+            const int qbs = qt0 + 32 * st;
+            if (qbs >= wend || qbs + 32 <= wbeg || qbs >= qend) continue;  // wave-uniform
+            // S[q][key] = Q·Kᵀ: lane column = its key, rows = 16 queries.
+            f32x16 s = f32x16{}, dp = f32x16{};
+            const float* qrow = Qs + (32 * st + lr) * S::KS + 4 * h;
+            const float* orow = Os + (32 * st + lr) * S::VS + 4 * h;
+#pragma unroll
+            for (int g = 0; g < S::G; ++g) {
+                const f32x4 qf = ld4(qrow + 8 * g);
+                const f32x4 of = ld4(orow + 8 * g);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    s = mfma(qf[c], kv[g][c], s);
+                    dp = mfma(of[c], vv[g][c], dp);
+                }
+            }
+            float pm[16], ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ql = 32 * st + 8 * (r >> 2) + 4 * h + (r & 3);
+                const int qq = qt0 + ql;
+                const bool ok = in_window(qq, key, L, hw) && kvalid;
+                const float pr = ok ? exp2f(s[r] * p.scale_log2 - lse_s[ql]) : 0.0f;
+                float mask = 1.0f;
+                if (p.p_drop > 0.0f && ok)
+                    mask = uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
+                pm[r] = pr * mask;
+                ds[r] = pr * (dp[r] * mask - dot_s[ql]) * p.scale;
+            }
+            // dVᵀ += dOᵀ·(P∘M) and dKᵀ += Qᵀ·dS, reducing over the 32 queries of this subtile.
+#pragma unroll
+            for (int dt = 0; dt < S::ND; ++dt) {
+                const float* ocol = Os + (32 * st + 4 * h) * S::VS + dt * 32 + lr;
+                const float* qcolp = Qs + (32 * st + 4 * h) * S::KS + dt * 32 + lr;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int rr = 8 * (r >> 2) + (r & 3);
+                    dv[dt] = mfma(ocol[rr * S::VS], pm[r], dv[dt]);
+                    dk[dt] = mfma(qcolp[rr * S::KS], ds[r], dk[dt]);
+                }
+            }
+        }
+    }
+
+    if (kvalid) {
+        if (rope) inverse_rope_acc<D>(dk, p, key, h);
+        float* dst = p.dqkv + (long)(start + key) * stride;
+        store_acc<D>(dk, dst + kcol, h, 1.0f);
+        store_acc<D>(dv, dst + vcol, h, 1.0f);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(THREADS) void attn_bwd_dq_kernel(Params p) {
+    using S = Shape<D>;
+    __shared__ __attribute__((aligned(16))) float Ks[TILE * S::KS];
+    __shared__ __attribute__((aligned(16))) float Vs[TILE * S::KS];
+
+    const int seg = blockIdx.y, head = blockIdx.z;
+    const int start = p.seg_start[seg], L = p.seg_len[seg];
+    const int qb0 = blockIdx.x * BLOCK_ROWS;
+    if (qb0 >= L) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
+    const int q0w = qb0 + wave * WAVE_ROWS;
+    const int q = q0w + lr;
+    const bool qvalid = q < L;
+    const bool rope = p.cos_t != nullptr;
+    const int hw = p.half_window;
+    const long stride = 3L * p.hidden;
+    const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
+
+    f32x4 qv[S::G], ov[S::G];
+    const int qs = start + (qvalid ? q : 0);
+    load_lane_row<D>(p.qkv + (long)qs * stride + qcol, p, q, qvalid, rope, h, qv);
+    load_lane_row<D>(p.dcontext + (long)qs * p.hidden + qcol, p, q, qvalid, false, h, ov);
+    const float lse = qvalid ? p.lse[(long)qs * p.heads + head] : __builtin_huge_valf();
+    const float dot = qvalid ? p.dots[(long)qs * p.heads + head] : 0.0f;
+
+    int kbeg = 0, kend = L, wbeg = 0, wend = L;
+    if (hw >= 0) {
+        kbeg = max(0, qb0 - hw);
+        kend = min(L, qb0 + BLOCK_ROWS + hw);
+        wbeg = max(0, q0w - hw);
+        wend = min(L, q0w + WAVE_ROWS + hw);
+    }
+
+    f32x16 dq[S::ND];
+#pragma unroll
+    for (int dt = 0; dt < S::ND; ++dt) dq[dt] = f32x16{};
+
+    for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
+        __syncthreads();
+        load_rows<D, S::KS>(p, Ks, start, L, kt0, TILE, kcol, rope);
+        load_rows<D, S::KS>(p, Vs, start, L, kt0, TILE, vcol, false);
+        __syncthreads();
+#pragma unroll
+        for (int st = 0; st < TILE / 32; ++st) {
+            const int kbs = kt0 + 32 * st;
+            if (kbs >= wend || kbs + 32 <= wbeg || kbs >= kend) continue;  // wave-uniform
+            f32x16 s = f32x16{}, dp = f32x16{};
+            const float* krow = Ks + (32 * st + lr) * S::KS + 4 * h;
+            const float* vrow = Vs + (32 * st + lr) * S::KS + 4 * h;
+#pragma unroll
+            for (int g = 0; g < S::G; ++g) {
+                const f32x4 kf = ld4(krow + 8 * g);
+                const f32x4 vf = ld4(vrow + 8 * g);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    s = mfma(kf[c], qv[g][c], s);
+                    dp = mfma(vf[c], ov[g][c], dp);
+                }
+            }
+            float ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
+                const bool ok = in_window(q, key, L, hw);
+                const float pr = ok ? exp2f(s[r] * p.scale_log2 - lse) : 0.0f;
+                float mask = 1.0f;
+                if (p.p_drop > 0.0f && ok)
+                    mask = uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
+                ds[r] = pr * (dp[r] * mask - dot) * p.scale;
+            }
+#pragma unroll
+            for (int dt = 0; dt < S::ND; ++dt) {
+                const float* kcolp = Ks + (32 * st + 4 * h) * S::KS + dt * 32 + lr;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) dq[dt] = mfma(kcolp[(8 * (r >> 2) + (r & 3)) * S::KS], ds[r], dq[dt]);
+            }
+        }
+    }
+
+    if (qvalid) {
+        if (rope) inverse_rope_acc<D>(dq, p, q, h);
+        store_acc<D>(dq, p.dqkv + (long)(start + q) * stride + qcol, h, 1.0f);
+    }
+}
+
+Params make_params(const AttentionArgs& a) {
+    Params p{};
+    p.qkv = a.qkv;
+    p.seg_start = a.seg_start;
+    p.seg_len = a.seg_len;
+    p.hidden = a.hidden;
+    p.heads = a.heads;
+    p.half_window = a.half_window;
+    p.scale = a.scale;
+    p.scale_log2 = a.scale * 1.4426950408889634f;
+    p.p_drop = a.p_drop;
+    p.keep = a.p_drop > 0.0f ? 1.0f / (1.0f - a.p_drop) : 1.0f;
+    p.seed = a.seed;
+    p.cos_t = a.cos_table;
+    p.sin_t = a.sin_table;
+    return p;
+}
+
+void check_args(const AttentionArgs& a) {
+    LAYA_REQUIRE(a.heads > 0 && a.hidden == a.heads * a.head_dim, "attention: hidden must equal heads × head_dim");
+    LAYA_REQUIRE(a.head_dim == 32 || a.head_dim == 64, "attention: head_dim must be 32 or 64");
+    LAYA_REQUIRE(a.max_len >= 0 && a.nseg >= 0, "attention: negative size");
+    LAYA_REQUIRE(a.heads <= 65535 && a.nseg <= 65535, "attention: too many heads or segments for one launch");
+    LAYA_REQUIRE(a.p_drop >= 0.0f && a.p_drop < 1.0f, "attention: dropout must be in [0, 1)");
+    LAYA_REQUIRE(a.cos_table == nullptr || a.positions >= a.max_len, "attention: rotary table shorter than max_len");
+}
+
+}  // namespace
+
+void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse) {
+    check_args(a);
+    if (a.nseg == 0 || a.max_len == 0) return;
+    Params p = make_params(a);
+    p.context = context;
+    p.lse = lse;
+    dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
+    ProfileScope scope(ctx, "attention_fwd", 4.0 * a.hidden * a.keys, 0.0);
+    if (a.head_dim == 64)
+        hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+    else
+        hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
+    check_launch("attn_fwd_kernel");
+}
+
+void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,
+                        const float* dcontext, float* dqkv) {
+    check_args(a);
+    if (a.nseg == 0 || a.max_len == 0 || rows == 0) return;
+    Params p = make_params(a);
+    p.lse = const_cast<float*>(lse);
+    p.dcontext = dcontext;
+    p.dqkv = dqkv;
+    float* dots = static_cast<float*>(ctx->workspace(3, sizeof(float) * (size_t)rows * a.heads));
+    p.dots = dots;
+    const long total = (long)rows * a.hidden;
+    const unsigned dot_blocks = (unsigned)((total + THREADS - 1) / THREADS);
+    dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
+    // Model flops of the backward, 8·d·Σkeys, split as the kernels do the work: dK/dV (4 products of
+    // which 2 recompute the forward's) and dQ (3 products, 2 recomputed).
+    const double fb = 2.0 * a.hidden * a.keys;
+    {
+        ProfileScope scope(ctx, "attention_bwd_dots", 0.0, 8.0 * total);
+        if (a.head_dim == 64)
+            hipLaunchKernelGGL(attn_dot_kernel<64>, dim3(dot_blocks), dim3(THREADS), 0, ctx->stream, dcontext, context,
+                               rows, a.hidden, a.heads, dots);
+        else
+            hipLaunchKernelGGL(attn_dot_kernel<32>, dim3(dot_blocks), dim3(THREADS), 0, ctx->stream, dcontext, context,
+                               rows, a.hidden, a.heads, dots);
+        check_launch("attn_dot_kernel");
+    }
+    {
+        ProfileScope scope(ctx, "attention_bwd_dkv", 2.0 * fb, 0.0);
+        if (a.head_dim == 64)
+            hipLaunchKernelGGL(attn_bwd_dkv_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        else
+            hipLaunchKernelGGL(attn_bwd_dkv_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
+        check_launch("attn_bwd_dkv_kernel");
+    }
+    {
+        ProfileScope scope(ctx, "attention_bwd_dq", 2.0 * fb, 0.0);
+        if (a.head_dim == 64)
+            hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        else
+            hipLaunchKernelGGL(attn_bwd_dq_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
+        check_launch("attn_bwd_dq_kernel");
+    }
+}
+
+}  // namespace laya

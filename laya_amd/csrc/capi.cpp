@@ -1,0 +1,621 @@
+// The C-ABI of liblaya_hip (include/laya_hip.h): context, memory, stream, and one entry point per
+// reference op. Every entry point validates its arguments on the host before any launch, so a bad
+// call returns a status code instead of reaching the device.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "elementwise.hpp"
+
+namespace laya {
+static thread_local std::string g_last_error;
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+}  // namespace laya
+
+using namespace laya;
+
+void* laya_ctx::alloc(size_t bytes) {
+    if (bytes == 0) bytes = 16;
+    if (cap && in_use + bytes > cap)
+        throw Error(LAYA_ERR_MEMORY, "allocation of " + std::to_string(bytes) + " bytes exceeds the context cap of " +
+                                         std::to_string(cap) + " bytes (" + std::to_string(in_use) + " in use)");
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        throw Error(LAYA_ERR_MEMORY, "hipMalloc(" + std::to_string(bytes) + ") failed: " + hipGetErrorString(e));
+    }
+    allocations[p] = bytes;
+    in_use += bytes;
+    return p;
+}
+
+void laya_ctx::release(void* p) {
+    if (!p) return;
+    auto it = allocations.find(p);
+    if (it == allocations.end()) throw Error(LAYA_ERR_ARGUMENT, "free of a pointer this context did not allocate");
+    LAYA_HIP(hipStreamSynchronize(stream));
+    LAYA_HIP(hipFree(p));
+    in_use -= it->second;
+    allocations.erase(it);
+}
+
+void* laya_ctx::workspace(int slot, size_t bytes) {
+    Workspace& w = scratch[slot];
+    if (w.bytes >= bytes && w.ptr) return w.ptr;
+    if (w.ptr) release(w.ptr);
+    w.ptr = nullptr;
+    w.bytes = 0;
+    size_t grow = std::max(bytes, (size_t)1 << 20);
+    w.ptr = alloc(grow);
+    w.bytes = grow;
+    return w.ptr;
+}
+
+namespace laya {
+
+static int take_event(laya_ctx* ctx) {
+    if (ctx->next_event >= (int)ctx->event_pool.size()) {
+        hipEvent_t e;
+        LAYA_HIP(hipEventCreate(&e));
+        ctx->event_pool.push_back(e);
+    }
+    return ctx->next_event++;
+}
+
+ProfileScope::ProfileScope(laya_ctx* c, const char* n, double f, double b) : ctx(c), name(n), flops(f), bytes(b) {
+    if (!ctx->profiling) return;
+    start = take_event(ctx);
+    LAYA_HIP(hipEventRecord(ctx->event_pool[start], ctx->stream));
+}
+
+ProfileScope::~ProfileScope() {
+    if (start < 0 || !ctx->profiling) return;
+    try {
+        const int stop = take_event(ctx);
+        if (hipEventRecord(ctx->event_pool[stop], ctx->stream) == hipSuccess)
+            ctx->launches.push_back({name, start, stop, flops, bytes});
+    } catch (...) {
+    }
+}
+
+// Rotary tables (Ops.cs:462-484): angles in double, cos/sin rounded to float.
+void build_rotary(laya_ctx* ctx, laya_rotary* r, int head_dim, double theta, int positions) {
+    LAYA_REQUIRE(head_dim > 0 && head_dim % 2 == 0, "rotary: head_dim must be even");
+    LAYA_REQUIRE(positions > 0, "rotary: positions must be positive");
+    const int half = head_dim / 2;
+    std::vector<float> c((size_t)positions * half), s((size_t)positions * half);
+    for (int i = 0; i < half; ++i) {
+        const double inv = 1.0 / std::pow(theta, 2.0 * i / head_dim);
+        for (int p = 0; p < positions; ++p) {
+            const double angle = p * inv;
+            c[(size_t)p * half + i] = (float)std::cos(angle);
+            s[(size_t)p * half + i] = (float)std::sin(angle);
+        }
+    }
+    if (r->cos_t) ctx->release(r->cos_t);
+    if (r->sin_t) ctx->release(r->sin_t);
+    r->cos_t = static_cast<float*>(ctx->alloc(c.size() * sizeof(float)));
+    r->sin_t = static_cast<float*>(ctx->alloc(s.size() * sizeof(float)));
+    LAYA_HIP(hipMemcpyAsync(r->cos_t, c.data(), c.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    LAYA_HIP(hipMemcpyAsync(r->sin_t, s.data(), s.size() * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+    LAYA_HIP(hipStreamSynchronize(ctx->stream));
+    r->head_dim = head_dim;
+    r->theta = theta;
+    r->positions = positions;
+}
+
+void free_rotary(laya_ctx* ctx, laya_rotary* r) {
+    if (r->cos_t) ctx->release(r->cos_t);
+    if (r->sin_t) ctx->release(r->sin_t);
+    r->cos_t = r->sin_t = nullptr;
+}
+
+}  // namespace laya
+
+static void require_ctx(laya_ctx* ctx) { LAYA_REQUIRE(ctx != nullptr, "null context"); }
+
+extern "C" {
+
+const char* laya_last_error(void) { return g_last_error.c_str(); }
+const char* laya_version(void) { return "laya_hip 0.1 gfx950"; }
+
+int laya_ctx_create(int device, laya_ctx** out) {
+    return guarded([&] {
+        LAYA_REQUIRE(out != nullptr, "null output pointer");
+        int count = 0;
+        LAYA_HIP(hipGetDeviceCount(&count));
+        LAYA_REQUIRE(device >= 0 && device < count, "device index out of range");
+        LAYA_HIP(hipSetDevice(device));
+        auto* c = new laya_ctx();
+        c->device = device;
+        LAYA_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->cu_count = prop.multiProcessorCount;
+        *out = c;
+    });
+}
+
+int laya_ctx_destroy(laya_ctx* ctx) {
+    return guarded([&] {
+        if (!ctx) return;
+        hipSetDevice(ctx->device);
+        hipStreamSynchronize(ctx->stream);
+        for (auto& kv : ctx->allocations) hipFree(kv.first);
+        for (auto& t : ctx->timers)
+            for (auto& e : t)
+                if (e) hipEventDestroy(e);
+        for (auto& e : ctx->event_pool) hipEventDestroy(e);
+        hipStreamDestroy(ctx->stream);
+        delete ctx;
+    });
+}
+
+int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes) {
+    return guarded([&] {
+        require_ctx(ctx);
+        ctx->cap = bytes;
+    });
+}
+
+int laya_ctx_memory_in_use(laya_ctx* ctx, size_t* bytes) {
+    return guarded([&] {
+        require_ctx(ctx);
+        *bytes = ctx->in_use;
+    });
+}
+
+int laya_alloc(laya_ctx* ctx, size_t bytes, void** out) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(out != nullptr, "null output pointer");
+        *out = ctx->alloc(bytes);
+    });
+}
+
+int laya_free(laya_ctx* ctx, void* ptr) {
+    return guarded([&] {
+        require_ctx(ctx);
+        ctx->release(ptr);
+    });
+}
+
+int laya_upload(laya_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        require_ctx(ctx);
+        if (!bytes) return;
+        LAYA_REQUIRE(dst && src, "null pointer");
+        LAYA_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
+
+int laya_download(laya_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        require_ctx(ctx);
+        if (!bytes) return;
+        LAYA_REQUIRE(dst && src, "null pointer");
+        LAYA_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
+
+int laya_fill(laya_ctx* ctx, float* dst, float value, size_t count) {
+    return guarded([&] {
+        require_ctx(ctx);
+        fill(ctx, dst, value, count);
+    });
+}
+
+int laya_sync(laya_ctx* ctx) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_HIP(hipStreamSynchronize(ctx->stream));
+    });
+}
+
+int laya_timer_begin(laya_ctx* ctx, int slot) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(slot >= 0 && slot < 16, "timer slot out of range");
+        for (auto& e : ctx->timers[slot])
+            if (!e) LAYA_HIP(hipEventCreate(&e));
+        LAYA_HIP(hipEventRecord(ctx->timers[slot][0], ctx->stream));
+    });
+}
+
+int laya_timer_end(laya_ctx* ctx, int slot) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(slot >= 0 && slot < 16 && ctx->timers[slot][1], "timer slot not started");
+        LAYA_HIP(hipEventRecord(ctx->timers[slot][1], ctx->stream));
+    });
+}
+
+int laya_timer_elapsed(laya_ctx* ctx, int slot, float* ms) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(slot >= 0 && slot < 16 && ctx->timers[slot][1], "timer slot not started");
+        LAYA_HIP(hipEventSynchronize(ctx->timers[slot][1]));
+        LAYA_HIP(hipEventElapsedTime(ms, ctx->timers[slot][0], ctx->timers[slot][1]));
+    });
+}
+
+namespace {
+struct KernelSummary {
+    std::string name;
+    int launches = 0;
+    double ms = 0, flops = 0, bytes = 0;
+};
+thread_local std::vector<KernelSummary> g_summary;
+}  // namespace
+
+int laya_profile_begin(laya_ctx* ctx) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_HIP(hipStreamSynchronize(ctx->stream));
+        ctx->launches.clear();
+        ctx->next_event = 0;
+        ctx->profiling = true;
+    });
+}
+
+int laya_profile_end(laya_ctx* ctx) {
+    return guarded([&] {
+        require_ctx(ctx);
+        ctx->profiling = false;
+        LAYA_HIP(hipStreamSynchronize(ctx->stream));
+        g_summary.clear();
+        for (const auto& r : ctx->launches) {
+            float ms = 0.0f;
+            LAYA_HIP(hipEventElapsedTime(&ms, ctx->event_pool[r.start], ctx->event_pool[r.stop]));
+            auto it = std::find_if(g_summary.begin(), g_summary.end(),
+                                   [&](const KernelSummary& k) { return k.name == r.name; });
+            if (it == g_summary.end()) {
+                g_summary.push_back({r.name});
+                it = g_summary.end() - 1;
+            }
+            it->launches++;
+            it->ms += ms;
+            it->flops += r.flops;
+            it->bytes += r.bytes;
+        }
+        ctx->launches.clear();
+        ctx->next_event = 0;
+    });
+}
+
+int laya_profile_count(laya_ctx* ctx, int* kernels) {
+    return guarded([&] {
+        require_ctx(ctx);
+        *kernels = (int)g_summary.size();
+    });
+}
+
+int laya_profile_get(laya_ctx* ctx, int i, const char** name, int* launches, double* total_ms, double* flops,
+                     double* bytes) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(i >= 0 && i < (int)g_summary.size(), "profile index out of range");
+        const auto& k = g_summary[i];
+        if (name) *name = k.name.c_str();
+        if (launches) *launches = k.launches;
+        if (total_ms) *total_ms = k.ms;
+        if (flops) *flops = k.flops;
+        if (bytes) *bytes = k.bytes;
+    });
+}
+
+// ------------------------------------------------------------------------------------- ops
+
+int laya_linear_fwd(laya_ctx* ctx, const float* x, int rows, int in, const float* W, int out, const float* b,
+                    const float* residual, float* y) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && in > 0 && out > 0, "linear: bad size");
+        LAYA_REQUIRE(x && W && y, "linear: null tensor");
+        gemm(ctx, GemmLayout::NT, GemmEpilogue::Store, rows, out, in, x, in, W, in, y, out, b, residual, out);
+    });
+}
+
+int laya_linear_bwd(laya_ctx* ctx, const float* x, const float* dy, int rows, int in, int out, const float* W,
+                    float* dx, float* dW, float* db) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && in > 0 && out > 0, "linear_bwd: bad size");
+        LAYA_REQUIRE(dy && W, "linear_bwd: null tensor");
+        if (dx) gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in);
+        if (dW) {
+            LAYA_REQUIRE(x, "linear_bwd: dW needs x");
+            gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
+        }
+        if (db) column_sum_add(ctx, dy, rows, out, db);
+    });
+}
+
+int laya_layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps,
+                       float* y, float* mean, float* rstd) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && x && w && y, "layernorm: bad arguments");
+        layernorm_fwd(ctx, x, rows, n, w, b, eps, y, mean, rstd);
+    });
+}
+
+int laya_layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
+                       float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && x && w && dy && dx, "layernorm_bwd: bad arguments");
+        LAYA_REQUIRE((mean == nullptr) == (rstd == nullptr), "layernorm_bwd: pass both mean and rstd, or neither");
+        layernorm_bwd(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd);
+    });
+}
+
+int laya_gelu_fwd(laya_ctx* ctx, const float* x, size_t n, float* y) {
+    return guarded([&] {
+        require_ctx(ctx);
+        gelu_fwd(ctx, x, n, y);
+    });
+}
+
+int laya_gelu_bwd(laya_ctx* ctx, const float* u, float* grad, size_t n) {
+    return guarded([&] {
+        require_ctx(ctx);
+        gelu_bwd(ctx, u, grad, n);
+    });
+}
+
+int laya_geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && inter > 0, "geglu: bad size");
+        geglu_fwd(ctx, wide, rows, inter, act);
+    });
+}
+
+int laya_geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && inter > 0, "geglu_bwd: bad size");
+        geglu_bwd(ctx, wide, dact, rows, inter, dwide);
+    });
+}
+
+float laya_uniform(uint64_t seed, uint64_t index) { return uniform01(seed, index); }
+uint64_t laya_mix(uint64_t seed, uint64_t salt) { return mix64(seed, salt); }
+
+int laya_dropout(laya_ctx* ctx, float* values, size_t n, float p, uint64_t seed) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(p >= 0.0f && p < 1.0f, "dropout: p must be in [0, 1)");
+        dropout(ctx, values, n, p, seed);
+    });
+}
+
+int laya_relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(p >= 0.0f && p < 1.0f, "dropout: p must be in [0, 1)");
+        relu_dropout_fwd(ctx, wide, n, p, seed, dropped);
+    });
+}
+
+int laya_relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* grad, size_t n, float p, uint64_t seed) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(p >= 0.0f && p < 1.0f, "dropout: p must be in [0, 1)");
+        relu_dropout_bwd(ctx, wide, grad, n, p, seed);
+    });
+}
+
+int laya_add(laya_ctx* ctx, float* dst, const float* src, size_t n) {
+    return guarded([&] {
+        require_ctx(ctx);
+        add(ctx, dst, src, n);
+    });
+}
+
+int laya_rotary_create(laya_ctx* ctx, int head_dim, double theta, int positions, laya_rotary** out) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(out != nullptr, "null output pointer");
+        auto* r = new laya_rotary();
+        try {
+            build_rotary(ctx, r, head_dim, theta, positions);
+        } catch (...) {
+            delete r;
+            throw;
+        }
+        *out = r;
+    });
+}
+
+int laya_rotary_destroy(laya_ctx* ctx, laya_rotary* rot) {
+    return guarded([&] {
+        require_ctx(ctx);
+        if (!rot) return;
+        free_rotary(ctx, rot);
+        delete rot;
+    });
+}
+
+int laya_rotary_apply(laya_ctx* ctx, const laya_rotary* rot, float* vec, int rows, const int* pos, int inverse) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rot && vec && pos && rows >= 0, "rotary: bad arguments");
+        rotary_apply(ctx, rot->cos_t, rot->sin_t, rot->head_dim, vec, rows, pos, inverse);
+    });
+}
+
+static AttentionArgs attention_args(const float* qkv, const int* seg_start, const int* seg_len, int nseg, int max_len,
+                                    int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
+                                    float p_drop, uint64_t seed) {
+    LAYA_REQUIRE(qkv && seg_start && seg_len, "attention: null tensor");
+    LAYA_REQUIRE(heads > 0 && hidden % heads == 0, "attention: hidden must be a multiple of heads");
+    AttentionArgs a{};
+    a.qkv = qkv;
+    a.seg_start = seg_start;
+    a.seg_len = seg_len;
+    a.nseg = nseg;
+    a.max_len = max_len;
+    a.hidden = hidden;
+    a.heads = heads;
+    a.head_dim = hidden / heads;
+    a.half_window = half_window;
+    a.scale = scale;
+    a.p_drop = p_drop;
+    a.seed = seed;
+    if (rot) {
+        LAYA_REQUIRE(rot->head_dim == a.head_dim, "attention: rotary head_dim mismatch");
+        a.cos_table = rot->cos_t;
+        a.sin_table = rot->sin_t;
+        a.positions = rot->positions;
+    }
+    return a;
+}
+
+int laya_attention_fwd(laya_ctx* ctx, const float* qkv, const int* seg_start, const int* seg_len, int nseg,
+                       int max_len, int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
+                       float p_drop, uint64_t seed, float* context, float* lse) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(context && lse, "attention: null output");
+        AttentionArgs a = attention_args(qkv, seg_start, seg_len, nseg, max_len, hidden, heads, scale, half_window,
+                                         rot, p_drop, seed);
+        if (ctx->profiling && nseg > 0) {
+            std::vector<int> ln(nseg);
+            LAYA_HIP(hipMemcpyAsync(ln.data(), seg_len, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
+            LAYA_HIP(hipStreamSynchronize(ctx->stream));
+            for (int L : ln) a.keys += window_keys(L, half_window);
+        }
+        attention_fwd(ctx, a, context, lse);
+    });
+}
+
+int laya_attention_bwd(laya_ctx* ctx, const float* qkv, const int* seg_start, const int* seg_len, int nseg,
+                       int max_len, int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
+                       float p_drop, uint64_t seed, const float* context, const float* lse, const float* dcontext,
+                       float* dqkv) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(context && lse && dcontext && dqkv, "attention_bwd: null tensor");
+        // The rows the segment table covers: read it back (small) to size the row-constant pass.
+        std::vector<int> st(nseg), ln(nseg);
+        if (nseg > 0) {
+            LAYA_HIP(hipMemcpyAsync(st.data(), seg_start, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
+            LAYA_HIP(hipMemcpyAsync(ln.data(), seg_len, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
+            LAYA_HIP(hipStreamSynchronize(ctx->stream));
+        }
+        int rows = 0;
+        for (int i = 0; i < nseg; ++i) {
+            LAYA_REQUIRE(ln[i] >= 0 && ln[i] <= max_len && st[i] >= 0, "attention_bwd: bad segment table");
+            rows = std::max(rows, st[i] + ln[i]);
+        }
+        AttentionArgs a = attention_args(qkv, seg_start, seg_len, nseg, max_len, hidden, heads, scale, half_window,
+                                         rot, p_drop, seed);
+        for (int L : ln) a.keys += window_keys(L, half_window);
+        attention_bwd(ctx, a, rows, context, lse, dcontext, dqkv);
+    });
+}
+
+int laya_embedding_fwd(laya_ctx* ctx, const int* ids, int n, const float* E, int vocab, int hidden, float* out,
+                       int* bad_count) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(n >= 0 && vocab > 0 && hidden > 0, "embedding: bad size");
+        embedding_fwd(ctx, ids, n, E, vocab, hidden, out, bad_count);
+    });
+}
+
+int laya_embedding_plan(const int* ids, int n, int vocab, int* sorted_pos, int* unique_ids, int* offsets,
+                        int* n_unique) {
+    return guarded([&] {
+        LAYA_REQUIRE(n >= 0 && vocab > 0, "embedding_plan: bad size");
+        // Counting sort by id: stable, so each id's positions stay in token order.
+        std::vector<int> count((size_t)vocab + 1, 0);
+        for (int t = 0; t < n; ++t) {
+            const int id = ids[t];
+            if ((unsigned)id >= (unsigned)vocab)
+                throw Error(LAYA_ERR_OUT_OF_RANGE, "token id " + std::to_string(id) + " is outside the vocabulary.");
+            count[id + 1]++;
+        }
+        for (int v = 0; v < vocab; ++v) count[v + 1] += count[v];
+        std::vector<int> cursor(count.begin(), count.end() - 1);
+        for (int t = 0; t < n; ++t) sorted_pos[cursor[ids[t]]++] = t;
+        int u = 0;
+        for (int v = 0; v < vocab; ++v) {
+            if (count[v + 1] > count[v]) {
+                unique_ids[u] = v;
+                offsets[u] = count[v];
+                ++u;
+            }
+        }
+        offsets[u] = n;
+        *n_unique = u;
+    });
+}
+
+int laya_embedding_bwd(laya_ctx* ctx, const int* sorted_pos, const int* unique_ids, const int* offsets, int n_unique,
+                       const float* d, int hidden, float* grad) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(n_unique >= 0 && hidden > 0, "embedding_bwd: bad size");
+        embedding_bwd(ctx, sorted_pos, unique_ids, offsets, n_unique, d, hidden, grad);
+    });
+}
+
+int laya_gather_rows(laya_ctx* ctx, const float* src, const int* rows_idx, int n, int width, float* dst) {
+    return guarded([&] {
+        require_ctx(ctx);
+        gather_rows(ctx, src, rows_idx, n, width, dst);
+    });
+}
+
+int laya_scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows_idx, int n, int width, float* dst) {
+    return guarded([&] {
+        require_ctx(ctx);
+        scatter_add_rows(ctx, src, rows_idx, n, width, dst);
+    });
+}
+
+int laya_softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets, const int* option_offsets,
+                        int n_items, float ce_weight, float scale_, float* grad, float* loss) {
+    return guarded([&] {
+        require_ctx(ctx);
+        softmax_ce_bwd(ctx, logits, targets, option_offsets, n_items, ce_weight, scale_, grad, loss);
+    });
+}
+
+int laya_grad_norm(laya_ctx* ctx, const float* grads, size_t n, double max_norm, double* norm_out, float* coef_out) {
+    return guarded([&] {
+        require_ctx(ctx);
+        grad_norm(ctx, grads, n, max_norm, norm_out, coef_out, nullptr);
+    });
+}
+
+int laya_adamw(laya_ctx* ctx, float* params, float* grads, float* m, float* v, int n_groups, const size_t* begin,
+               const size_t* end, const double* lr, double beta1, double beta2, double eps, double weight_decay,
+               int step, const float* coef, int zero_grads) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(n_groups >= 0 && n_groups <= 4, "adamw: at most 4 groups");
+        LAYA_REQUIRE(step >= 1, "adamw: step counts from 1");
+        const double c1 = 1.0 - std::pow(beta1, step), c2 = 1.0 - std::pow(beta2, step);
+        AdamGroups g{};
+        g.n = n_groups;
+        size_t n = 0;
+        for (int k = 0; k < n_groups; ++k) {
+            g.begin[k] = begin[k];
+            g.end[k] = end[k];
+            g.decay[k] = (float)(1.0 - lr[k] * weight_decay);
+            g.step_size[k] = (float)(lr[k] / c1);
+            n = std::max(n, end[k]);
+        }
+        adamw_arena(ctx, params, grads, m, v, n, g, (float)beta1, (float)beta2, (float)eps, (float)std::sqrt(c2), coef,
+                    zero_grads);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,218 @@
+// Shared definitions of liblaya_hip: status handling, the context, and device helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/laya_hip.h"
+
+namespace laya {
+
+// A failure carried up to the C-ABI boundary, where it becomes a status code plus laya_last_error().
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void set_last_error(const std::string& msg);
+
+#define LAYA_HIP(expr)                                                                                   \
+    do {                                                                                                 \
+        hipError_t e_ = (expr);                                                                          \
+        if (e_ != hipSuccess)                                                                            \
+            throw ::laya::Error(LAYA_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_));        \
+    } while (0)
+
+#define LAYA_REQUIRE(cond, msg)                                                                          \
+    do {                                                                                                 \
+        if (!(cond)) throw ::laya::Error(LAYA_ERR_ARGUMENT, msg);                                        \
+    } while (0)
+
+// Runs a body at the C-ABI boundary and turns exceptions into status codes.
+template <typename F> int guarded(F&& f) {
+    try {
+        f();
+        return LAYA_OK;
+    } catch (const Error& e) {
+        set_last_error(e.what());
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        set_last_error("host allocation failed");
+        return LAYA_ERR_MEMORY;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return LAYA_ERR_ARGUMENT;
+    }
+}
+
+// After a launch: surfaces launch-configuration errors immediately.
+inline void check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error(LAYA_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Workspace that grows on demand and is reused across calls on one context.
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+// One profiled launch: events around it on the context's stream and its algorithmic work
+// (flops for matrix-core kernels, compulsory HBM bytes for memory-bound ones).
+struct LaunchRecord {
+    const char* name;
+    int start, stop;  // indices into the context's event pool
+    double flops, bytes;
+};
+
+}  // namespace laya
+
+// One context: a device, one stream, an allocation ledger and reusable scratch.
+struct laya_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    size_t cap = 0, in_use = 0;
+    std::unordered_map<void*, size_t> allocations;
+    laya::Workspace scratch[4];
+    hipEvent_t timers[16][2] = {};
+    int cu_count = 256;
+    bool profiling = false;
+    std::vector<hipEvent_t> event_pool;
+    std::vector<laya::LaunchRecord> launches;
+    int next_event = 0;
+
+    // Device scratch slot `slot` of at least `bytes`, reallocated (not preserved) when it grows.
+    void* workspace(int slot, size_t bytes);
+    void* alloc(size_t bytes);
+    void release(void* p);
+};
+
+// Rotary tables on the device (Ops.cs:446-504).
+struct laya_rotary {
+    int head_dim = 0, positions = 0;
+    double theta = 0;
+    float* cos_t = nullptr;
+    float* sin_t = nullptr;
+};
+
+namespace laya {
+
+// ------------------------------------------------------------------------------ device helpers
+
+// Ops.Uniform (Ops.cs:227-234): SplitMix64 finaliser over seed + (index + 1)·φ, top 24 bits.
+__host__ __device__ inline float uniform01(uint64_t seed, uint64_t index) {
+    uint64_t z = seed + (index + 1ull) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (float)(z >> 40) * (1.0f / 16777216.0f);
+}
+
+// Ops.Mix (Ops.cs:236-241).
+__host__ __device__ inline uint64_t mix64(uint64_t seed, uint64_t salt) {
+    uint64_t z = seed ^ (salt * 0xD1B54A32D192ED03ull + 0x8CB92BA72F3D8DD7ull);
+    z = (z ^ (z >> 33)) * 0xFF51AFD7ED558CCDull;
+    return z ^ (z >> 33);
+}
+
+// Ops.DropoutIndex (Ops.cs:318).
+__host__ __device__ inline uint64_t attn_dropout_index(int head, int row, int key) {
+    return ((uint64_t)head << 42) | ((uint64_t)(uint32_t)row << 21) | (uint64_t)(uint32_t)key;
+}
+
+// Exact GELU x·Φ(x) and its derivative Φ(x) + x·φ(x), on ROCm's device erff / expf.
+__device__ inline float gelu_f(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+__device__ inline float gelu_grad_f(float x) {
+    float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+    float pdf = 0.39894228040143268f * __expf(-0.5f * x * x);
+    return cdf + x * pdf;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+inline unsigned blocks_for(size_t n, unsigned per_block, unsigned cap = 65535u * 16u) {
+    size_t b = (n + per_block - 1) / per_block;
+    if (b == 0) b = 1;
+    return (unsigned)(b > cap ? cap : b);
+}
+
+// Brackets one kernel launch with events when the context is profiling (laya_profile_begin).
+struct ProfileScope {
+    laya_ctx* ctx;
+    int start = -1;
+    const char* name;
+    double flops, bytes;
+    ProfileScope(laya_ctx* c, const char* n, double f, double b);
+    ~ProfileScope();
+};
+
+// ------------------------------------------------------------------------ internal launchers
+
+enum class GemmLayout {
+    NT,  // C[M,N] = A[M,K] · B[N,K]ᵀ          (forward:  y  = x · Wᵀ)
+    NN,  // C[M,N] = A[M,K] · B[K,N]           (backward: dx = dy · W)
+    TN,  // C[M,N] = A[K,M]ᵀ · B[K,N]          (backward: dW = dyᵀ · x)
+};
+
+enum class GemmEpilogue {
+    Store,       // C = acc (+ bias[n]) (+ R[m, n])
+    Accumulate,  // C += acc, deterministically (split-K partials reduced in a fixed order)
+};
+
+void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
+          const float* B, long ldb, float* C, long ldc, const float* bias = nullptr, const float* R = nullptr,
+          long ldr = 0);
+
+// Σ over rows of a [rows, n] matrix added into out[n], deterministic (bias gradients).
+void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out);
+
+void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps, float* y,
+                   float* mean, float* rstd, const int* gather_ids = nullptr, const float* add_table = nullptr,
+                   const int* add_index = nullptr);
+void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
+                   float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
+                   const int* gather_ids = nullptr);
+
+struct AttentionArgs {
+    const float* qkv;
+    const int* seg_start;
+    const int* seg_len;
+    int nseg, max_len, hidden, heads, head_dim, half_window;
+    float scale, p_drop;
+    uint64_t seed;
+    const float* cos_table;  // [positions, head_dim/2] or null
+    const float* sin_table;
+    int positions;
+    double keys;  // Σ over queries of the keys each one attends to (for the profile's flop count)
+};
+
+// Σ_q |window(q) ∩ segment| for one segment (Ops.cs:315-316).
+inline double window_keys(int L, int hw) {
+    if (hw < 0 || hw >= L) return (double)L * L;
+    double s = 0;
+    for (int q = 0; q < L; ++q) s += std::min(L - 1, q + hw) - std::max(0, q - hw) + 1;
+    return s;
+}
+void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse);
+// rows: the number of rows of qkv / context / dcontext (the dO·O row constants span all of them).
+void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,
+                   const float* dcontext, float* dqkv);
+
+}  // namespace laya

@@ -1,0 +1,43 @@
+// Launchers of the memory-bound kernels (elementwise.hip) and the optimizer kernels (optim.hip).
+#pragma once
+#include "common.hpp"
+
+namespace laya {
+
+void fill(laya_ctx* ctx, float* dst, float v, size_t n);
+void add(laya_ctx* ctx, float* dst, const float* src, size_t n);
+void scale(laya_ctx* ctx, float* dst, float s, size_t n);
+void gelu_fwd(laya_ctx* ctx, const float* x, size_t n, float* y);
+void gelu_bwd(laya_ctx* ctx, const float* u, float* g, size_t n);
+void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act);
+void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide);
+void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed);
+void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped);
+void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, float p, uint64_t seed);
+void rotary_apply(laya_ctx* ctx, const float* cos_t, const float* sin_t, int head_dim, float* vec, int rows,
+                  const int* pos, int inverse);
+void embedding_fwd(laya_ctx* ctx, const int* ids, int n, const float* E, int vocab, int hidden, float* out, int* bad);
+void embedding_bwd(laya_ctx* ctx, const int* sorted_pos, const int* unique_ids, const int* offsets, int n_unique,
+                   const float* d, int hidden, float* grad);
+void gather_rows(laya_ctx* ctx, const float* src, const int* rows, int n, int width, float* dst);
+void scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows, int n, int width, float* dst);
+void type_embedding_bwd(laya_ctx* ctx, const float* d, const int* seg_start, const int* seg_len, const int* qtypes,
+                        int nseg, int width, float* grad);
+void softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets, const int* offsets, int n_items,
+                    float ce_weight, float scale, float* grad, float* loss);
+void init_param(laya_ctx* ctx, float* dst, size_t n, int kind, float std, uint64_t seed);
+
+// Σ g² over the arena in double, in a fixed order; writes norm, the clip coefficient
+// min(1, max/(norm + 1e-6)) as the reference computes it, and a non-finite flag.
+void grad_norm(laya_ctx* ctx, const float* g, size_t n, double max_norm, double* norm, float* coef, int* nonfinite);
+
+struct AdamGroups {
+    int n;
+    size_t begin[4], end[4];
+    float decay[4], step_size[4];
+};
+// Elements outside every group are left alone (frozen parameters); zero_grads clears all n gradients.
+void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n, const AdamGroups& groups,
+                 float beta1, float beta2, float eps, float sqrt_c2, const float* coef, int zero_grads);
+
+}  // namespace laya

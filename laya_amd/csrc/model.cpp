@@ -1,0 +1,922 @@
+// The model driver: TrainableDecisionModel (src/StructuredDecisions.Laya.Training/TrainableDecisionModel.cs),
+// AdamW / Gradients (AdamW.cs) and the trainer's micro-step (Trainer.cs:125-154), restated as host C++ over
+// the library's kernels.
+//
+// What changes from the reference, MI355X-first:
+//  - parameters, gradients and both Adam moments live in four flat fp32 arenas in HBM, in module
+//    order, so the optimizer and the norm are single launches over contiguous memory;
+//  - the forward keeps every activation the backward needs resident in HBM (about 0.85 MB per token
+//    for 22 layers at d = 768) instead of checkpointing each layer's input and recomputing it, which
+//    removes the reference's extra forward pass (TrainableDecisionModel.cs:551-557, 605-612);
+//  - LayerNorm statistics are saved by the forward, attention saves its row log-sum-exp;
+//  - the skip adds are fused into the epilogue of the GEMM that produces the branch.
+// The order of operations, the accumulate/overwrite conventions and every parity trap of the
+// reference are kept: layer 0 has no attn_norm, the head uses ReLU and biased norms with eps 1e-5,
+// the act head gets no gradient but is weight-decayed, the temperature buffer is frozen.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <vector>
+
+#include "elementwise.hpp"
+
+namespace laya {
+void build_rotary(laya_ctx* ctx, laya_rotary* r, int head_dim, double theta, int positions);
+void free_rotary(laya_ctx* ctx, laya_rotary* r);
+}  // namespace laya
+
+using namespace laya;
+
+namespace {
+
+enum InitKind { INIT_NORMAL = 0, INIT_ONES = 1, INIT_ZEROS = 2 };
+
+struct Param {
+    std::string name;
+    std::vector<int> shape;
+    size_t offset = 0, numel = 0;
+    bool trainable = true, touched = false;
+    int init = INIT_NORMAL;
+};
+
+// Carves one device allocation into 256-byte aligned tensors.
+struct Carver {
+    size_t bytes = 0;
+    std::vector<std::pair<float**, size_t>> slots;
+    void add(float*& p, size_t floats) {
+        slots.push_back({&p, bytes});
+        bytes += (floats * sizeof(float) + 255) / 256 * 256;
+    }
+    void bind(char* base) {
+        for (auto& s : slots) *s.first = reinterpret_cast<float*>(base + s.second);
+    }
+};
+
+}  // namespace
+
+struct laya_model {
+    laya_ctx* ctx = nullptr;
+    laya_model_config cfg{};
+    std::vector<int> kinds;
+    std::vector<Param> params;
+    std::map<std::string, int> by_name;
+    size_t total = 0;
+    float* P = nullptr;
+    float* G = nullptr;
+    float* M1 = nullptr;
+    float* M2 = nullptr;
+    laya_rotary rot_global, rot_local;
+    int head_heads = 1, head_dim = 0;
+    float head_dropout = 0.1f;
+    int first_trainable = 0;
+    bool embeddings_trainable = true;
+    int steps = 0;
+
+    struct Enc {
+        int attn_norm = -1, attn_norm_b = -1, wqkv, wqkv_b = -1, wo, wo_b = -1, mlp_norm, mlp_norm_b = -1, wi,
+            wi_b = -1, mlp_wo, mlp_wo_b = -1, kind;
+    };
+    struct Head {
+        int norm1, norm1_b, in_proj, in_proj_b, out_proj, out_proj_b, norm2, norm2_b, linear1, linear1_b, linear2,
+            linear2_b;
+    };
+    std::vector<Enc> enc;
+    std::vector<Head> head;
+    int tok_emb, emb_norm, emb_norm_b = -1, final_norm, final_norm_b = -1, type_emb, sc_norm, sc_norm_b, sc1, sc1_b,
+        sc2, sc2_b;
+
+    // ----- activations (capacity-sized, reused across steps)
+    int cap_tokens = 0, cap_markers = 0, cap_segs = 0;
+    void* act_block = nullptr;
+    struct EncAct {
+        float *x, *normed, *mean1, *rstd1, *qkv, *ctx, *lse, *res, *mlpn, *mean2, *rstd2, *wide, *act;
+    };
+    struct HeadAct {
+        float *x, *n1, *mean1, *rstd1, *qkv, *ctx, *lse, *res, *n2, *mean2, *rstd2, *wide, *drop;
+    };
+    std::vector<EncAct> ea;
+    std::vector<HeadAct> ha;
+    float *x_final = nullptr, *emb_mean = nullptr, *emb_rstd = nullptr, *fin_mean = nullptr, *fin_rstd = nullptr;
+    float *head_out = nullptr;
+    float *s_in = nullptr, *s_mean = nullptr, *s_rstd = nullptr, *s_norm = nullptr, *s_pre = nullptr, *s_act = nullptr,
+          *scores = nullptr;
+    // backward scratch
+    float *dS = nullptr, *dE = nullptr, *dqkv = nullptr, *dctx = nullptr, *dwide = nullptr, *dact = nullptr,
+          *dn = nullptr, *dy = nullptr;
+    float *ds_scores = nullptr, *ds_act = nullptr, *ds_norm = nullptr, *ds_mark = nullptr, *targets = nullptr;
+    // batch tables (device int32)
+    int *d_tokens = nullptr, *d_seg_start = nullptr, *d_seg_len = nullptr, *d_row_type = nullptr,
+        *d_marker_rows = nullptr, *d_qtypes = nullptr, *d_opt_off = nullptr, *d_sorted = nullptr,
+        *d_unique = nullptr, *d_uoff = nullptr;
+    // optimizer scalars
+    double* d_norm = nullptr;
+    float* d_coef = nullptr;
+    float* d_loss = nullptr;
+    int* d_nonfinite = nullptr;
+    bool coef_valid = false;
+
+    // ----- the batch of the last forward
+    bool has_tape = false, training = false;
+    uint64_t seed = 0;
+    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0;
+    double keys_full = 0, keys_local = 0;  // Σ_q attended keys of the batch, full and sliding window
+    std::vector<int> h_tokens, h_start, h_len, h_marker_rows, h_qtypes, h_nopt, h_opt_off, h_row_type, h_sorted,
+        h_unique, h_uoff;
+
+    int d() const { return cfg.hidden; }
+    int I() const { return cfg.intermediate; }
+
+    int add_param(const std::string& name, std::vector<int> shape, int init) {
+        Param p;
+        p.name = name;
+        p.shape = std::move(shape);
+        p.numel = 1;
+        for (int s : p.shape) p.numel *= (size_t)s;
+        p.offset = total;
+        p.init = init;
+        total += (p.numel + 63) / 64 * 64;  // 256-byte aligned tensors for vector loads
+        by_name[name] = (int)params.size();
+        params.push_back(p);
+        return (int)params.size() - 1;
+    }
+
+    float* W(int i) const { return i >= 0 ? P + params[i].offset : nullptr; }
+    // Parameter.GradientBuffer (Parameter.cs:177): the gradient of a trainable parameter, else null.
+    float* Gt(int i) {
+        if (i < 0 || !params[i].trainable) return nullptr;
+        params[i].touched = true;
+        return G + params[i].offset;
+    }
+};
+
+namespace {
+
+void build_layout(laya_model* m) {
+    const auto& c = m->cfg;
+    const int d = c.hidden, I = c.intermediate;
+    const std::string e = "encoder.";
+    m->tok_emb = m->add_param(e + "embeddings.tok_embeddings.weight", {c.vocab, d}, INIT_NORMAL);
+    m->emb_norm = m->add_param(e + "embeddings.norm.weight", {d}, INIT_ONES);
+    if (c.norm_bias) m->emb_norm_b = m->add_param(e + "embeddings.norm.bias", {d}, INIT_ZEROS);
+    for (int l = 0; l < c.layers; ++l) {
+        const std::string p = e + "layers." + std::to_string(l) + ".";
+        laya_model::Enc L;
+        if (l > 0) {
+            L.attn_norm = m->add_param(p + "attn_norm.weight", {d}, INIT_ONES);
+            if (c.norm_bias) L.attn_norm_b = m->add_param(p + "attn_norm.bias", {d}, INIT_ZEROS);
+        }
+        L.wqkv = m->add_param(p + "attn.Wqkv.weight", {3 * d, d}, INIT_NORMAL);
+        if (c.attention_bias) L.wqkv_b = m->add_param(p + "attn.Wqkv.bias", {3 * d}, INIT_ZEROS);
+        L.wo = m->add_param(p + "attn.Wo.weight", {d, d}, INIT_NORMAL);
+        if (c.attention_bias) L.wo_b = m->add_param(p + "attn.Wo.bias", {d}, INIT_ZEROS);
+        L.mlp_norm = m->add_param(p + "mlp_norm.weight", {d}, INIT_ONES);
+        if (c.norm_bias) L.mlp_norm_b = m->add_param(p + "mlp_norm.bias", {d}, INIT_ZEROS);
+        L.wi = m->add_param(p + "mlp.Wi.weight", {2 * I, d}, INIT_NORMAL);
+        if (c.mlp_bias) L.wi_b = m->add_param(p + "mlp.Wi.bias", {2 * I}, INIT_ZEROS);
+        L.mlp_wo = m->add_param(p + "mlp.Wo.weight", {d, I}, INIT_NORMAL);
+        if (c.mlp_bias) L.mlp_wo_b = m->add_param(p + "mlp.Wo.bias", {d}, INIT_ZEROS);
+        L.kind = m->kinds[l];
+        m->enc.push_back(L);
+    }
+    m->final_norm = m->add_param(e + "final_norm.weight", {d}, INIT_ONES);
+    if (c.norm_bias) m->final_norm_b = m->add_param(e + "final_norm.bias", {d}, INIT_ZEROS);
+    for (int l = 0; l < c.head_layers; ++l) {
+        const std::string p = "head.layers." + std::to_string(l) + ".";
+        laya_model::Head H;
+        H.in_proj = m->add_param(p + "self_attn.in_proj_weight", {3 * d, d}, INIT_NORMAL);
+        H.in_proj_b = m->add_param(p + "self_attn.in_proj_bias", {3 * d}, INIT_ZEROS);
+        H.out_proj = m->add_param(p + "self_attn.out_proj.weight", {d, d}, INIT_NORMAL);
+        H.out_proj_b = m->add_param(p + "self_attn.out_proj.bias", {d}, INIT_ZEROS);
+        H.linear1 = m->add_param(p + "linear1.weight", {c.head_ff, d}, INIT_NORMAL);
+        H.linear1_b = m->add_param(p + "linear1.bias", {c.head_ff}, INIT_ZEROS);
+        H.linear2 = m->add_param(p + "linear2.weight", {d, c.head_ff}, INIT_NORMAL);
+        H.linear2_b = m->add_param(p + "linear2.bias", {d}, INIT_ZEROS);
+        H.norm1 = m->add_param(p + "norm1.weight", {d}, INIT_ONES);
+        H.norm1_b = m->add_param(p + "norm1.bias", {d}, INIT_ZEROS);
+        H.norm2 = m->add_param(p + "norm2.weight", {d}, INIT_ONES);
+        H.norm2_b = m->add_param(p + "norm2.bias", {d}, INIT_ZEROS);
+        m->head.push_back(H);
+    }
+    m->type_emb = m->add_param("type_emb.weight", {3, d}, INIT_NORMAL);
+    m->sc_norm = m->add_param("scorer.0.weight", {d}, INIT_ONES);
+    m->sc_norm_b = m->add_param("scorer.0.bias", {d}, INIT_ZEROS);
+    m->sc1 = m->add_param("scorer.1.weight", {d, d}, INIT_NORMAL);
+    m->sc1_b = m->add_param("scorer.1.bias", {d}, INIT_ZEROS);
+    m->sc2 = m->add_param("scorer.3.weight", {1, d}, INIT_NORMAL);
+    m->sc2_b = m->add_param("scorer.3.bias", {1}, INIT_ZEROS);
+    m->add_param("act_head.0.weight", {256, d + 4}, INIT_NORMAL);
+    m->add_param("act_head.0.bias", {256}, INIT_ZEROS);
+    m->add_param("act_head.2.weight", {c.n_act, 256}, INIT_NORMAL);
+    m->add_param("act_head.2.bias", {c.n_act}, INIT_ZEROS);
+    const int temp = m->add_param("temperature", {3}, INIT_ONES);
+    m->params[temp].trainable = false;  // a buffer, not a parameter (TrainableDecisionModel.cs:117-118)
+}
+
+void ensure_rotary(laya_model* m, int positions) {
+    if (m->rot_global.positions >= positions && m->rot_global.cos_t) return;
+    const int p = std::max(positions, std::max(1024, m->rot_global.positions * 2));
+    const int hd = m->cfg.hidden / m->cfg.heads;
+    build_rotary(m->ctx, &m->rot_global, hd, m->cfg.theta_global, p);
+    build_rotary(m->ctx, &m->rot_local, hd, m->cfg.theta_local, p);
+}
+
+void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
+    if (T <= m->cap_tokens && nmark <= m->cap_markers && nseg <= m->cap_segs && m->act_block) return;
+    if (m->act_block) {
+        m->ctx->release(m->act_block);
+        m->act_block = nullptr;
+    }
+    const int Tc = std::max(T, m->cap_tokens), Mc = std::max(std::max(nmark, m->cap_markers), 1),
+              Sc = std::max(std::max(nseg, m->cap_segs), 1);
+    const size_t d = m->d(), I = m->I(), ff = m->cfg.head_ff, Tz = Tc;
+    const size_t H = m->cfg.heads, HH = m->head_heads;
+    Carver cv;
+    m->ea.assign(m->cfg.layers, {});
+    for (auto& a : m->ea) {
+        cv.add(a.x, Tz * d);
+        cv.add(a.normed, Tz * d);
+        cv.add(a.mean1, Tz);
+        cv.add(a.rstd1, Tz);
+        cv.add(a.qkv, Tz * 3 * d);
+        cv.add(a.ctx, Tz * d);
+        cv.add(a.lse, Tz * H);
+        cv.add(a.res, Tz * d);
+        cv.add(a.mlpn, Tz * d);
+        cv.add(a.mean2, Tz);
+        cv.add(a.rstd2, Tz);
+        cv.add(a.wide, Tz * 2 * I);
+        cv.add(a.act, Tz * I);
+    }
+    m->ha.assign(m->cfg.head_layers, {});
+    for (auto& a : m->ha) {
+        cv.add(a.x, Tz * d);
+        cv.add(a.n1, Tz * d);
+        cv.add(a.mean1, Tz);
+        cv.add(a.rstd1, Tz);
+        cv.add(a.qkv, Tz * 3 * d);
+        cv.add(a.ctx, Tz * d);
+        cv.add(a.lse, Tz * HH);
+        cv.add(a.res, Tz * d);
+        cv.add(a.n2, Tz * d);
+        cv.add(a.mean2, Tz);
+        cv.add(a.rstd2, Tz);
+        cv.add(a.wide, Tz * ff);
+        cv.add(a.drop, Tz * ff);
+    }
+    cv.add(m->x_final, Tz * d);
+    cv.add(m->emb_mean, Tz);
+    cv.add(m->emb_rstd, Tz);
+    cv.add(m->fin_mean, Tz);
+    cv.add(m->fin_rstd, Tz);
+    cv.add(m->head_out, Tz * d);
+    cv.add(m->s_in, (size_t)Mc * d);
+    cv.add(m->s_mean, Mc);
+    cv.add(m->s_rstd, Mc);
+    cv.add(m->s_norm, (size_t)Mc * d);
+    cv.add(m->s_pre, (size_t)Mc * d);
+    cv.add(m->s_act, (size_t)Mc * d);
+    cv.add(m->scores, Mc);
+    cv.add(m->dS, Tz * d);
+    cv.add(m->dE, Tz * d);
+    cv.add(m->dqkv, Tz * 3 * d);
+    cv.add(m->dctx, Tz * d);
+    cv.add(m->dwide, Tz * std::max(2 * I, ff));
+    cv.add(m->dact, Tz * std::max(I, ff));
+    cv.add(m->dn, Tz * d);
+    cv.add(m->dy, Tz * d);
+    cv.add(m->ds_scores, Mc);
+    cv.add(m->ds_act, (size_t)Mc * d);
+    cv.add(m->ds_norm, (size_t)Mc * d);
+    cv.add(m->ds_mark, (size_t)Mc * d);
+    cv.add(m->targets, Mc);
+    // int tables share the carve (4-byte elements)
+    float *tok, *st, *ln, *rt, *mr, *qt, *oo, *so, *un, *uo;
+    cv.add(tok, Tz);
+    cv.add(st, Sc);
+    cv.add(ln, Sc);
+    cv.add(rt, Tz);
+    cv.add(mr, Mc);
+    cv.add(qt, Sc);
+    cv.add(oo, (size_t)Sc + 1);
+    cv.add(so, Tz);
+    cv.add(un, Tz + 1);
+    cv.add(uo, Tz + 2);
+    m->act_block = m->ctx->alloc(cv.bytes);
+    cv.bind(static_cast<char*>(m->act_block));
+    m->d_tokens = reinterpret_cast<int*>(tok);
+    m->d_seg_start = reinterpret_cast<int*>(st);
+    m->d_seg_len = reinterpret_cast<int*>(ln);
+    m->d_row_type = reinterpret_cast<int*>(rt);
+    m->d_marker_rows = reinterpret_cast<int*>(mr);
+    m->d_qtypes = reinterpret_cast<int*>(qt);
+    m->d_opt_off = reinterpret_cast<int*>(oo);
+    m->d_sorted = reinterpret_cast<int*>(so);
+    m->d_unique = reinterpret_cast<int*>(un);
+    m->d_uoff = reinterpret_cast<int*>(uo);
+    m->cap_tokens = Tc;
+    m->cap_markers = Mc;
+    m->cap_segs = Sc;
+}
+
+void upload_ints(laya_model* m, int* dst, const std::vector<int>& src) {
+    if (src.empty()) return;
+    LAYA_HIP(hipMemcpyAsync(dst, src.data(), src.size() * sizeof(int), hipMemcpyHostToDevice, m->ctx->stream));
+}
+
+// The batch layout of Forward (TrainableDecisionModel.cs:254-274), with the checks that run before any math.
+void prepare_batch(laya_model* m, const laya_batch* b) {
+    LAYA_REQUIRE(b && b->n_items > 0, "forward: empty batch");
+    LAYA_REQUIRE(b->lengths && b->tokens && b->n_options && b->markers && b->qtypes, "forward: null batch array");
+    const int n = b->n_items;
+    m->h_start.assign(n, 0);
+    m->h_len.assign(b->lengths, b->lengths + n);
+    m->h_qtypes.assign(b->qtypes, b->qtypes + n);
+    m->h_nopt.assign(b->n_options, b->n_options + n);
+    long total = 0, marks = 0;
+    int longest = 0;
+    for (int i = 0; i < n; ++i) {
+        LAYA_REQUIRE(b->lengths[i] > 0, "forward: an item has no tokens");
+        LAYA_REQUIRE(b->n_options[i] >= 0, "forward: negative option count");
+        LAYA_REQUIRE(b->qtypes[i] >= 0 && b->qtypes[i] < 3, "forward: question type outside [0, 3)");
+        m->h_start[i] = (int)total;
+        total += b->lengths[i];
+        marks += b->n_options[i];
+        longest = std::max(longest, b->lengths[i]);
+    }
+    m->T = (int)total;
+    m->nseg = n;
+    m->nmark = (int)marks;
+    m->max_len = longest;
+    m->h_tokens.assign(b->tokens, b->tokens + total);
+    for (int t = 0; t < m->T; ++t)
+        if ((unsigned)m->h_tokens[t] >= (unsigned)m->cfg.vocab)
+            throw Error(LAYA_ERR_OUT_OF_RANGE,
+                        "token id " + std::to_string(m->h_tokens[t]) + " is outside the vocabulary.");
+    m->h_marker_rows.assign(m->nmark, 0);
+    m->h_opt_off.assign(n + 1, 0);
+    for (int i = 0, k = 0; i < n; ++i) {
+        m->h_opt_off[i + 1] = m->h_opt_off[i] + b->n_options[i];
+        for (int o = 0; o < b->n_options[i]; ++o, ++k) {
+            const int pos = std::max(0, b->markers[k]);
+            LAYA_REQUIRE(pos < b->lengths[i], "forward: a marker lies beyond its item");
+            m->h_marker_rows[k] = m->h_start[i] + pos;
+        }
+    }
+    m->h_row_type.assign(m->T, 0);
+    for (int i = 0; i < n; ++i)
+        for (int t = 0; t < b->lengths[i]; ++t) m->h_row_type[m->h_start[i] + t] = b->qtypes[i];
+    // Embedding-gradient plan: positions stably sorted by id (counting sort), one run per unique id.
+    m->h_sorted.assign(m->T, 0);
+    m->h_unique.assign(m->T + 1, 0);
+    m->h_uoff.assign(m->T + 2, 0);
+    int nu = 0;
+    if (laya_embedding_plan(m->h_tokens.data(), m->T, m->cfg.vocab, m->h_sorted.data(), m->h_unique.data(),
+                            m->h_uoff.data(), &nu) != LAYA_OK)
+        throw Error(LAYA_ERR_OUT_OF_RANGE, laya_last_error());
+    m->n_unique = nu;
+    m->keys_full = m->keys_local = 0;
+    for (int i = 0; i < n; ++i) {
+        m->keys_full += window_keys(m->h_len[i], -1);
+        m->keys_local += window_keys(m->h_len[i], m->cfg.local_attention / 2);
+    }
+
+    ensure_activations(m, m->T, m->nmark, m->nseg);
+    ensure_rotary(m, longest);
+    upload_ints(m, m->d_tokens, m->h_tokens);
+    upload_ints(m, m->d_seg_start, m->h_start);
+    upload_ints(m, m->d_seg_len, m->h_len);
+    upload_ints(m, m->d_row_type, m->h_row_type);
+    upload_ints(m, m->d_marker_rows, m->h_marker_rows);
+    upload_ints(m, m->d_qtypes, m->h_qtypes);
+    upload_ints(m, m->d_opt_off, m->h_opt_off);
+    upload_ints(m, m->d_sorted, m->h_sorted);
+    upload_ints(m, m->d_unique, m->h_unique);
+    upload_ints(m, m->d_uoff, m->h_uoff);
+}
+
+AttentionArgs enc_attention(laya_model* m, const float* qkv, int kind) {
+    AttentionArgs a{};
+    a.qkv = qkv;
+    a.seg_start = m->d_seg_start;
+    a.seg_len = m->d_seg_len;
+    a.nseg = m->nseg;
+    a.max_len = m->max_len;
+    a.hidden = m->d();
+    a.heads = m->cfg.heads;
+    a.head_dim = m->d() / m->cfg.heads;
+    a.half_window = kind == 1 ? m->cfg.local_attention / 2 : -1;
+    a.keys = kind == 1 ? m->keys_local : m->keys_full;
+    a.scale = 1.0f / std::sqrt((float)a.head_dim);
+    a.p_drop = 0.0f;
+    a.seed = 0;
+    const laya_rotary& r = kind == 0 ? m->rot_global : m->rot_local;
+    a.cos_table = r.cos_t;
+    a.sin_table = r.sin_t;
+    a.positions = r.positions;
+    return a;
+}
+
+uint64_t salt(uint64_t seed, int layer, int site) { return mix64(seed, (uint64_t)(layer * 16 + site + 1)); }
+
+AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p, uint64_t seed) {
+    AttentionArgs a{};
+    a.qkv = qkv;
+    a.seg_start = m->d_seg_start;
+    a.seg_len = m->d_seg_len;
+    a.nseg = m->nseg;
+    a.max_len = m->max_len;
+    a.hidden = m->d();
+    a.heads = m->head_heads;
+    a.head_dim = m->d() / m->head_heads;
+    a.half_window = -1;
+    a.keys = m->keys_full;
+    a.scale = 1.0f / std::sqrt((float)(m->d() / m->head_heads));
+    a.p_drop = p;
+    a.seed = salt(seed, index, 0);
+    return a;
+}
+
+void linear(laya_model* m, const float* x, int rows, int in, int wi, int bi, int out, const float* residual, float* y) {
+    gemm(m->ctx, GemmLayout::NT, GemmEpilogue::Store, rows, out, in, x, in, m->W(wi), in, y, out, m->W(bi), residual,
+         out);
+}
+
+// Ops.LinearBackward (Ops.cs:33-69): dx = dy·W (overwrite; + residual when given), dW += dyᵀ·x, db += Σ dy.
+void linear_backward(laya_model* m, const float* x, const float* dy, int rows, int in, int out, int wi, int bi,
+                     float* dx, const float* dx_residual = nullptr) {
+    if (dx)
+        gemm(m->ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, m->W(wi), in, dx, in, nullptr,
+             dx_residual, in);
+    if (float* dW = m->Gt(wi)) gemm(m->ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
+    if (float* db = m->Gt(bi)) column_sum_add(m->ctx, dy, rows, out, db);
+}
+
+void dropout_copy(laya_model* m, const float* src, float* dst, size_t n, float p, uint64_t seed) {
+    LAYA_HIP(hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToDevice, m->ctx->stream));
+    dropout(m->ctx, dst, n, p, seed);
+}
+
+// Forward (TrainableDecisionModel.cs:248-353) with EncoderLayerForward (361-414) and HeadLayerForward (428-468).
+void forward(laya_model* m, const laya_batch* b, bool train, uint64_t seed) {
+    prepare_batch(m, b);
+    laya_ctx* ctx = m->ctx;
+    const int T = m->T, d = m->d(), I = m->I(), ff = m->cfg.head_ff;
+    const float eps = m->cfg.norm_eps;
+    m->training = train;
+    m->seed = seed;
+
+    // Embedding gather fused into the embedding LayerNorm.
+    float* x0 = m->cfg.layers > 0 ? m->ea[0].x : m->x_final;
+    layernorm_fwd(ctx, m->W(m->tok_emb), T, d, m->W(m->emb_norm), m->W(m->emb_norm_b), eps, x0, m->emb_mean,
+                  m->emb_rstd, m->d_tokens);
+    for (int l = 0; l < m->cfg.layers; ++l) {
+        auto& L = m->enc[l];
+        auto& a = m->ea[l];
+        float* out = l + 1 < m->cfg.layers ? m->ea[l + 1].x : m->x_final;
+        const float* normed = a.x;
+        if (L.attn_norm >= 0) {
+            layernorm_fwd(ctx, a.x, T, d, m->W(L.attn_norm), m->W(L.attn_norm_b), eps, a.normed, a.mean1, a.rstd1);
+            normed = a.normed;
+        }
+        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv);
+        attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse);
+        linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res);  // x1 = x + attn
+        layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2);
+        linear(m, a.mlpn, T, d, L.wi, L.wi_b, 2 * I, nullptr, a.wide);
+        geglu_fwd(ctx, a.wide, T, I, a.act);
+        linear(m, a.act, T, I, L.mlp_wo, L.mlp_wo_b, d, a.res, out);  // x2 = x1 + mlp
+    }
+    // Final norm, then each question's type vector on its rows (TrainableDecisionModel.cs:294-304).
+    float* h0 = m->cfg.head_layers > 0 ? m->ha[0].x : m->head_out;
+    layernorm_fwd(ctx, m->x_final, T, d, m->W(m->final_norm), m->W(m->final_norm_b), eps, h0, m->fin_mean, m->fin_rstd,
+                  nullptr, m->W(m->type_emb), m->d_row_type);
+    const float p = train ? m->head_dropout : 0.0f;
+    for (int j = 0; j < m->cfg.head_layers; ++j) {
+        auto& H = m->head[j];
+        auto& a = m->ha[j];
+        float* out = j + 1 < m->cfg.head_layers ? m->ha[j + 1].x : m->head_out;
+        layernorm_fwd(ctx, a.x, T, d, m->W(H.norm1), m->W(H.norm1_b), 1e-5f, a.n1, a.mean1, a.rstd1);
+        linear(m, a.n1, T, d, H.in_proj, H.in_proj_b, 3 * d, nullptr, a.qkv);
+        attention_fwd(ctx, head_attention(m, a.qkv, j, p, seed), a.ctx, a.lse);
+        if (p > 0.0f) {
+            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, nullptr, a.res);
+            dropout(ctx, a.res, (size_t)T * d, p, salt(seed, j, 1));
+            add(ctx, a.res, a.x, (size_t)T * d);
+        } else {
+            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, a.x, a.res);
+        }
+        layernorm_fwd(ctx, a.res, T, d, m->W(H.norm2), m->W(H.norm2_b), 1e-5f, a.n2, a.mean2, a.rstd2);
+        linear(m, a.n2, T, d, H.linear1, H.linear1_b, ff, nullptr, a.wide);
+        relu_dropout_fwd(ctx, a.wide, (size_t)T * ff, p, salt(seed, j, 2), a.drop);
+        if (p > 0.0f) {
+            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, nullptr, out);
+            dropout(ctx, out, (size_t)T * d, p, salt(seed, j, 3));
+            add(ctx, out, a.res, (size_t)T * d);
+        } else {
+            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, a.res, out);
+        }
+    }
+    // Scorer at the option markers (TrainableDecisionModel.cs:313-323).
+    const int M = m->nmark;
+    gather_rows(ctx, m->head_out, m->d_marker_rows, M, d, m->s_in);
+    layernorm_fwd(ctx, m->s_in, M, d, m->W(m->sc_norm), m->W(m->sc_norm_b), 1e-5f, m->s_norm, m->s_mean, m->s_rstd);
+    linear(m, m->s_norm, M, d, m->sc1, m->sc1_b, d, nullptr, m->s_pre);
+    gelu_fwd(ctx, m->s_pre, (size_t)M * d, m->s_act);
+    linear(m, m->s_act, M, d, m->sc2, m->sc2_b, 1, nullptr, m->scores);
+    m->has_tape = true;
+}
+
+// EncoderLayerBackward (TrainableDecisionModel.cs:551-603); dS holds dOutput and becomes dx.
+void encoder_backward(laya_model* m, int l, bool need_input) {
+    laya_ctx* ctx = m->ctx;
+    auto& L = m->enc[l];
+    auto& a = m->ea[l];
+    const int T = m->T, d = m->d(), I = m->I();
+    const float eps = m->cfg.norm_eps;
+    linear_backward(m, a.act, m->dS, T, I, d, L.mlp_wo, L.mlp_wo_b, m->dact);
+    geglu_bwd(ctx, a.wide, m->dact, T, I, m->dwide);
+    linear_backward(m, a.mlpn, m->dwide, T, d, 2 * I, L.wi, L.wi_b, m->dn);
+    layernorm_bwd(ctx, a.res, T, d, m->W(L.mlp_norm), eps, m->dn, m->dS, m->Gt(L.mlp_norm), m->Gt(L.mlp_norm_b),
+                  a.mean2, a.rstd2);
+    linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx);
+    attention_bwd(ctx, enc_attention(m, a.qkv, L.kind), T, a.ctx, a.lse, m->dctx, m->dqkv);
+    const float* normed = L.attn_norm >= 0 ? a.normed : a.x;
+    if (!need_input) {
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, nullptr);
+        return;
+    }
+    if (L.attn_norm < 0) {
+        // Layer 0: nn.Identity, so dx = dResidual + dNormed, fused as the GEMM's residual.
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dS, m->dS);
+    } else {
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dn);
+        layernorm_bwd(ctx, a.x, T, d, m->W(L.attn_norm), eps, m->dn, m->dS, m->Gt(L.attn_norm), m->Gt(L.attn_norm_b),
+                      a.mean1, a.rstd1);
+    }
+}
+
+// HeadLayerBackward (TrainableDecisionModel.cs:605-640); dS holds dOutput and becomes dx.
+void head_backward(laya_model* m, int j) {
+    laya_ctx* ctx = m->ctx;
+    auto& H = m->head[j];
+    auto& a = m->ha[j];
+    const int T = m->T, d = m->d(), ff = m->cfg.head_ff;
+    const float p = m->training ? m->head_dropout : 0.0f;
+    const size_t nd = (size_t)T * d;
+    const float* dy = m->dS;
+    if (p > 0.0f) {
+        dropout_copy(m, m->dS, m->dy, nd, p, salt(m->seed, j, 3));
+        dy = m->dy;
+    }
+    linear_backward(m, a.drop, dy, T, ff, d, H.linear2, H.linear2_b, m->dact);
+    relu_dropout_bwd(ctx, a.wide, m->dact, (size_t)T * ff, p, salt(m->seed, j, 2));
+    linear_backward(m, a.n2, m->dact, T, d, ff, H.linear1, H.linear1_b, m->dn);
+    layernorm_bwd(ctx, a.res, T, d, m->W(H.norm2), 1e-5f, m->dn, m->dS, m->Gt(H.norm2), m->Gt(H.norm2_b), a.mean2,
+                  a.rstd2);
+    const float* datt = m->dS;
+    if (p > 0.0f) {
+        dropout_copy(m, m->dS, m->dy, nd, p, salt(m->seed, j, 1));
+        datt = m->dy;
+    }
+    linear_backward(m, a.ctx, datt, T, d, d, H.out_proj, H.out_proj_b, m->dctx);
+    attention_bwd(ctx, head_attention(m, a.qkv, j, p, m->seed), T, a.ctx, a.lse, m->dctx, m->dqkv);
+    linear_backward(m, a.n1, m->dqkv, T, d, 3 * d, H.in_proj, H.in_proj_b, m->dn);
+    layernorm_bwd(ctx, a.x, T, d, m->W(H.norm1), 1e-5f, m->dn, m->dS, m->Gt(H.norm1), m->Gt(H.norm1_b), a.mean1,
+                  a.rstd1);
+}
+
+// Backward (TrainableDecisionModel.cs:479-549), from dscores already on the device.
+void backward(laya_model* m) {
+    LAYA_REQUIRE(m->has_tape, "backward: run forward first");
+    laya_ctx* ctx = m->ctx;
+    const int T = m->T, d = m->d(), M = m->nmark;
+    const float eps = m->cfg.norm_eps;
+    linear_backward(m, m->s_act, m->ds_scores, M, d, 1, m->sc2, m->sc2_b, m->ds_act);
+    gelu_bwd(ctx, m->s_pre, m->ds_act, (size_t)M * d);
+    linear_backward(m, m->s_norm, m->ds_act, M, d, d, m->sc1, m->sc1_b, m->ds_norm);
+    fill(ctx, m->ds_mark, 0.0f, (size_t)M * d);
+    layernorm_bwd(ctx, m->s_in, M, d, m->W(m->sc_norm), 1e-5f, m->ds_norm, m->ds_mark, m->Gt(m->sc_norm),
+                  m->Gt(m->sc_norm_b), m->s_mean, m->s_rstd);
+    fill(ctx, m->dS, 0.0f, (size_t)T * d);
+    scatter_add_rows(ctx, m->ds_mark, m->d_marker_rows, M, d, m->dS);
+    for (int j = m->cfg.head_layers - 1; j >= 0; --j) head_backward(m, j);
+    if (float* g = m->Gt(m->type_emb))
+        type_embedding_bwd(ctx, m->dS, m->d_seg_start, m->d_seg_len, m->d_qtypes, m->nseg, d, g);
+    if (m->first_trainable >= m->cfg.layers) return;  // the encoder is frozen
+    fill(ctx, m->dE, 0.0f, (size_t)T * d);
+    layernorm_bwd(ctx, m->x_final, T, d, m->W(m->final_norm), eps, m->dS, m->dE, m->Gt(m->final_norm),
+                  m->Gt(m->final_norm_b), m->fin_mean, m->fin_rstd);
+    std::swap(m->dS, m->dE);
+    for (int l = m->cfg.layers - 1; l >= m->first_trainable; --l)
+        encoder_backward(m, l, l > m->first_trainable || m->embeddings_trainable);
+    if (m->embeddings_trainable && m->first_trainable == 0) {
+        fill(ctx, m->dE, 0.0f, (size_t)T * d);
+        layernorm_bwd(ctx, m->W(m->tok_emb), T, d, m->W(m->emb_norm), eps, m->dS, m->dE, m->Gt(m->emb_norm),
+                      m->Gt(m->emb_norm_b), m->emb_mean, m->emb_rstd, m->d_tokens);
+        if (float* g = m->Gt(m->tok_emb))
+            embedding_bwd(ctx, m->d_sorted, m->d_unique, m->d_uoff, m->n_unique, m->dE, d, g);
+    }
+}
+
+// The trainer's groups (Trainer.cs:96-100) as contiguous trainable ranges of the arena.
+AdamGroups adam_groups(laya_model* m, double lr_enc, double lr_head, double wd, double c1, size_t* n_out) {
+    AdamGroups g{};
+    std::vector<std::pair<size_t, size_t>> ranges[2];
+    for (const auto& p : m->params) {
+        if (!p.trainable) continue;
+        const int grp = p.name.find("encoder.") != std::string::npos ? 0 : 1;
+        auto& r = ranges[grp];
+        const size_t b = p.offset, e = p.offset + (p.numel + 63) / 64 * 64;
+        if (!r.empty() && r.back().second == b)
+            r.back().second = e;
+        else
+            r.push_back({b, e});
+    }
+    for (int grp = 0; grp < 2; ++grp) {
+        const double lr = grp == 0 ? lr_enc : lr_head;
+        for (auto& r : ranges[grp]) {
+            LAYA_REQUIRE(g.n < 4, "adamw: trainable parameters form more than 4 ranges");
+            g.begin[g.n] = r.first;
+            g.end[g.n] = r.second;
+            g.decay[g.n] = (float)(1.0 - lr * wd);
+            g.step_size[g.n] = (float)(lr / c1);
+            g.n++;
+        }
+    }
+    *n_out = m->total;
+    return g;
+}
+
+void ensure_moments(laya_model* m) {
+    if (m->M1) return;
+    m->M1 = static_cast<float*>(m->ctx->alloc(m->total * sizeof(float)));
+    m->M2 = static_cast<float*>(m->ctx->alloc(m->total * sizeof(float)));
+    fill(m->ctx, m->M1, 0.0f, m->total);
+    fill(m->ctx, m->M2, 0.0f, m->total);
+}
+
+void adamw_step(laya_model* m, double lr_enc, double lr_head, double b1, double b2, double eps, double wd,
+                bool zero_grads) {
+    ensure_moments(m);
+    m->steps++;
+    const double c1 = 1.0 - std::pow(b1, m->steps), c2 = 1.0 - std::pow(b2, m->steps);
+    size_t n = 0;
+    AdamGroups g = adam_groups(m, lr_enc, lr_head, wd, c1, &n);
+    adamw_arena(m->ctx, m->P, m->G, m->M1, m->M2, n, g, (float)b1, (float)b2, (float)eps, (float)std::sqrt(c2),
+                m->coef_valid ? m->d_coef : nullptr, zero_grads ? 1 : 0);
+    m->coef_valid = false;
+}
+
+laya_model* checked(laya_model* m) {
+    LAYA_REQUIRE(m != nullptr, "null model");
+    LAYA_HIP(hipSetDevice(m->ctx->device));
+    return m;
+}
+
+}  // namespace
+
+extern "C" {
+
+int laya_model_create(laya_ctx* ctx, const laya_model_config* cfg, laya_model** out) {
+    return guarded([&] {
+        LAYA_REQUIRE(ctx && cfg && out, "null argument");
+        LAYA_REQUIRE(cfg->vocab > 0 && cfg->hidden > 0 && cfg->intermediate > 0 && cfg->layers >= 0 && cfg->heads > 0,
+                     "model: bad configuration");
+        LAYA_REQUIRE(cfg->hidden % cfg->heads == 0, "model: hidden must be a multiple of heads");
+        auto* m = new laya_model();
+        m->ctx = ctx;
+        m->cfg = *cfg;
+        m->cfg.layer_kinds = nullptr;
+        m->kinds.resize(cfg->layers);
+        for (int l = 0; l < cfg->layers; ++l)
+            m->kinds[l] = cfg->layer_kinds ? cfg->layer_kinds[l] : (l % std::max(1, cfg->global_every) == 0 ? 0 : 1);
+        m->head_heads = std::max(1, cfg->hidden / 64);  // TrainableDecisionModel.cs:109
+        build_layout(m);
+        try {
+            m->P = static_cast<float*>(ctx->alloc(m->total * sizeof(float)));
+            m->G = static_cast<float*>(ctx->alloc(m->total * sizeof(float)));
+            fill(ctx, m->P, 0.0f, m->total);
+            fill(ctx, m->G, 0.0f, m->total);
+            m->d_norm = static_cast<double*>(ctx->alloc(64));
+            m->d_coef = static_cast<float*>(ctx->alloc(64));
+            m->d_loss = static_cast<float*>(ctx->alloc(64));
+            m->d_nonfinite = static_cast<int*>(ctx->alloc(64));
+            ensure_rotary(m, 1024);
+        } catch (...) {
+            for (void* p : {(void*)m->P, (void*)m->G, (void*)m->d_norm, (void*)m->d_coef, (void*)m->d_loss,
+                            (void*)m->d_nonfinite})
+                if (p) ctx->release(p);
+            delete m;
+            throw;
+        }
+        *out = m;
+    });
+}
+
+int laya_model_destroy(laya_model* m) {
+    return guarded([&] {
+        if (!m) return;
+        laya_ctx* ctx = m->ctx;
+        for (void* p : {(void*)m->P, (void*)m->G, (void*)m->M1, (void*)m->M2, m->act_block, (void*)m->d_norm,
+                        (void*)m->d_coef, (void*)m->d_loss, (void*)m->d_nonfinite})
+            if (p) ctx->release(p);
+        free_rotary(ctx, &m->rot_global);
+        free_rotary(ctx, &m->rot_local);
+        delete m;
+    });
+}
+
+int laya_model_num_params(laya_model* m, int* count) {
+    return guarded([&] { *count = (int)checked(m)->params.size(); });
+}
+
+int laya_model_param_info(laya_model* m, int i, const char** name, int* ndim, int* dims, size_t* offset, size_t* numel,
+                          int* trainable) {
+    return guarded([&] {
+        LAYA_REQUIRE(m && i >= 0 && i < (int)m->params.size(), "param index out of range");
+        const Param& p = m->params[i];
+        if (name) *name = p.name.c_str();
+        if (ndim) *ndim = (int)p.shape.size();
+        if (dims)
+            for (size_t k = 0; k < p.shape.size() && k < 4; ++k) dims[k] = p.shape[k];
+        if (offset) *offset = p.offset;
+        if (numel) *numel = p.numel;
+        if (trainable) *trainable = p.trainable ? 1 : 0;
+    });
+}
+
+int laya_model_find_param(laya_model* m, const char* name, int* index) {
+    return guarded([&] {
+        LAYA_REQUIRE(m && name && index, "null argument");
+        auto it = m->by_name.find(name);
+        if (it == m->by_name.end())
+            throw Error(LAYA_ERR_MISSING, std::string("the checkpoint has no '") + name + "' tensor");
+        *index = it->second;
+    });
+}
+
+int laya_model_set_param(laya_model* m, int i, const float* host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(i >= 0 && i < (int)m->params.size() && host, "set_param: bad argument");
+        const Param& p = m->params[i];
+        LAYA_HIP(hipMemcpyAsync(m->P + p.offset, host, p.numel * sizeof(float), hipMemcpyHostToDevice, m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+    });
+}
+
+int laya_model_get_param(laya_model* m, int i, float* host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(i >= 0 && i < (int)m->params.size() && host, "get_param: bad argument");
+        const Param& p = m->params[i];
+        LAYA_HIP(hipMemcpyAsync(host, m->P + p.offset, p.numel * sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+    });
+}
+
+int laya_model_get_grad(laya_model* m, int i, float* host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(i >= 0 && i < (int)m->params.size() && host, "get_grad: bad argument");
+        const Param& p = m->params[i];
+        LAYA_HIP(hipMemcpyAsync(host, m->G + p.offset, p.numel * sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+    });
+}
+
+int laya_model_has_grad(laya_model* m, int i, int* has) {
+    return guarded([&] {
+        LAYA_REQUIRE(m && i >= 0 && i < (int)m->params.size() && has, "has_grad: bad argument");
+        *has = m->params[i].touched ? 1 : 0;
+    });
+}
+
+int laya_model_init_random(laya_model* m, uint64_t seed, float std) {
+    return guarded([&] {
+        checked(m);
+        for (size_t i = 0; i < m->params.size(); ++i) {
+            const Param& p = m->params[i];
+            init_param(m->ctx, m->P + p.offset, p.numel, p.init, std, mix64(seed, (uint64_t)i + 1));
+        }
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+    });
+}
+
+// SetTrainableEncoderLayers (TrainableDecisionModel.cs:206-231).
+int laya_model_set_trainable_encoder_layers(laya_model* m, int n) {
+    return guarded([&] {
+        checked(m);
+        const int count = m->cfg.layers;
+        const int trainable = n < 0 ? count : std::clamp(n, 0, count);
+        m->first_trainable = count - trainable;
+        const bool all = n < 0 || (trainable == count && n >= count);
+        for (auto& p : m->params) {
+            if (p.name == "temperature") continue;
+            if (p.name.rfind("encoder.", 0) != 0) {
+                p.trainable = true;
+                continue;
+            }
+            bool train;
+            if (p.name.rfind("encoder.embeddings.", 0) == 0)
+                train = all;
+            else if (p.name.rfind("encoder.final_norm.", 0) == 0)
+                train = trainable > 0;
+            else
+                train = std::stoi(p.name.substr(15, p.name.find('.', 15) - 15)) >= m->first_trainable;
+            if (!train && p.trainable) fill(m->ctx, m->G + p.offset, 0.0f, p.numel);
+            p.trainable = train;
+            if (!train) p.touched = false;
+        }
+        m->embeddings_trainable = m->params[m->tok_emb].trainable;
+    });
+}
+
+int laya_model_set_head_dropout(laya_model* m, float p) {
+    return guarded([&] {
+        LAYA_REQUIRE(m && p >= 0.0f && p < 1.0f, "head dropout must be in [0, 1)");
+        m->head_dropout = p;
+    });
+}
+
+int laya_model_forward(laya_model* m, const laya_batch* batch, int training, uint64_t seed, float* logits_host) {
+    return guarded([&] {
+        checked(m);
+        forward(m, batch, training != 0, seed);
+        if (logits_host) {
+            LAYA_HIP(hipMemcpyAsync(logits_host, m->scores, sizeof(float) * m->nmark, hipMemcpyDeviceToHost,
+                                    m->ctx->stream));
+            LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+        }
+    });
+}
+
+int laya_model_backward(laya_model* m, const float* dlogits_host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(m->has_tape, "backward: run forward first");
+        LAYA_REQUIRE(dlogits_host || m->nmark == 0, "backward: null logit gradients");
+        if (m->nmark)
+            LAYA_HIP(hipMemcpyAsync(m->ds_scores, dlogits_host, sizeof(float) * m->nmark, hipMemcpyHostToDevice,
+                                    m->ctx->stream));
+        backward(m);
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+    });
+}
+
+int laya_model_clip_grad_norm(laya_model* m, double max_norm, double* norm_out) {
+    return guarded([&] {
+        checked(m);
+        grad_norm(m->ctx, m->G, m->total, max_norm, m->d_norm, m->d_coef, m->d_nonfinite);
+        m->coef_valid = true;
+        if (norm_out) {
+            LAYA_HIP(hipMemcpyAsync(norm_out, m->d_norm, sizeof(double), hipMemcpyDeviceToHost, m->ctx->stream));
+            LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+        }
+    });
+}
+
+int laya_model_adamw_step(laya_model* m, double lr_encoder, double lr_head, double beta1, double beta2, double eps,
+                          double weight_decay) {
+    return guarded([&] {
+        checked(m);
+        adamw_step(m, lr_encoder, lr_head, beta1, beta2, eps, weight_decay, false);
+    });
+}
+
+int laya_model_zero_grad(laya_model* m) {
+    return guarded([&] {
+        checked(m);
+        fill(m->ctx, m->G, 0.0f, m->total);
+    });
+}
+
+int laya_model_train_step(laya_model* m, const laya_batch* batch, const float* targets_host, float ce_weight,
+                          float loss_scale, uint64_t seed, double max_norm, double lr_encoder, double lr_head,
+                          double beta1, double beta2, double eps, double weight_decay, float* loss_out) {
+    return guarded([&] {
+        checked(m);
+        forward(m, batch, true, seed);
+        LAYA_REQUIRE(targets_host || m->nmark == 0, "train_step: null targets");
+        if (m->nmark)
+            LAYA_HIP(hipMemcpyAsync(m->targets, targets_host, sizeof(float) * m->nmark, hipMemcpyHostToDevice,
+                                    m->ctx->stream));
+        softmax_ce_bwd(m->ctx, m->scores, m->targets, m->d_opt_off, m->nseg, ce_weight, loss_scale, m->ds_scores,
+                       m->d_loss);
+        backward(m);
+        grad_norm(m->ctx, m->G, m->total, max_norm, m->d_norm, m->d_coef, m->d_nonfinite);
+        m->coef_valid = true;
+        adamw_step(m, lr_encoder, lr_head, beta1, beta2, eps, weight_decay, true);
+        if (loss_out) {
+            LAYA_HIP(hipMemcpyAsync(loss_out, m->d_loss, sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));
+            LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+        }
+    });
+}
+
+int laya_model_steps(laya_model* m, int* steps) {
+    return guarded([&] { *steps = checked(m)->steps; });
+}
+
+}  // extern "C"

@@ -1,0 +1,271 @@
+// LayerNorm forward and backward, one 64-lane wavefront per row.
+//
+// Forward restates SimdOps.LayerNorm (src/StructuredDecisions.Base/Numerics/SimdOps.cs:234-272):
+// biased variance, eps inside the square root, optional bias; it also saves the row mean and
+// rstd so the backward reads x once instead of recomputing statistics (the reference recomputes
+// them in double, Ops.cs:124-136). Optional fusions: gathering input rows by token id (the
+// embedding lookup, TrainableDecisionModel.cs:277-285) and adding a per-row table vector after
+// the norm (the type embedding, TrainableDecisionModel.cs:300-304).
+//
+// Backward restates Ops.LayerNormBackward (Ops.cs:117-186) in one pass: each wave writes dx for
+// its rows and keeps dγ/dβ partials in registers for a fixed row stride; a second kernel sums the
+// partials in wave order. Bytes per row: x, dy, dx in, dx out = 16·n.
+#include "common.hpp"
+
+namespace laya {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+__device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+
+template <int NCH>
+__global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x, int rows, int n,
+                                                     const float* __restrict__ w, const float* __restrict__ b,
+                                                     float eps, float* __restrict__ y, float* __restrict__ mean_out,
+                                                     float* __restrict__ rstd_out, const int* __restrict__ gather_ids,
+                                                     int gather_rows, const float* __restrict__ add_table,
+                                                     const int* __restrict__ add_index) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* src = x + (long)row * n;
+    bool zero = false;
+    if (gather_ids) {
+        const int id = gather_ids[row];
+        zero = (unsigned)id >= (unsigned)gather_rows;
+        src = x + (long)(zero ? 0 : id) * n;
+    }
+    f32x4 v[NCH];
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int col = (c * 64 + lane) * 4;
+        v[c] = (col < n && !zero) ? ld4(src + col) : f32x4{0, 0, 0, 0};
+        s += (v[c][0] + v[c][1]) + (v[c][2] + v[c][3]);
+    }
+    const float mean = wave_sum(s) / (float)n;
+    float q = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < n) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = v[c][e] - mean;
+                q += d * d;
+            }
+        }
+    }
+    const float var = wave_sum(q) / (float)n;
+    const float rstd = 1.0f / sqrtf(var + eps);
+    const float* add = add_table ? add_table + (long)add_index[row] * n : nullptr;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < n) {
+            f32x4 g = ld4(w + col);
+            f32x4 o = (v[c] - mean) * rstd * g;
+            if (b) o += ld4(b + col);
+            if (add) o += ld4(add + col);
+            st4(y + (long)row * n + col, o);
+        }
+    }
+    if (lane == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = rstd;
+    }
+}
+
+template <int NCH>
+__global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x, int rows, int n,
+                                                     const float* __restrict__ w, float eps,
+                                                     const float* __restrict__ dy, float* __restrict__ dx,
+                                                     const float* __restrict__ mean_in,
+                                                     const float* __restrict__ rstd_in,
+                                                     const int* __restrict__ gather_ids, int gather_rows,
+                                                     int total_waves, float* __restrict__ part_g,
+                                                     float* __restrict__ part_b) {
+    // total_waves is a multiple of 4 (whole blocks); a wave past the last row only adds zeros.
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    f32x4 gacc[NCH], bacc[NCH], gm[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        gacc[c] = f32x4{0, 0, 0, 0};
+        bacc[c] = f32x4{0, 0, 0, 0};
+        const int col = (c * 64 + lane) * 4;
+        gm[c] = col < n ? ld4(w + col) : f32x4{0, 0, 0, 0};
+    }
+    const float inv_n = 1.0f / (float)n;
+    for (int row = wave; row < rows; row += total_waves) {
+        const float* src = x + (long)row * n;
+        bool zero = false;
+        if (gather_ids) {
+            const int id = gather_ids[row];
+            zero = (unsigned)id >= (unsigned)gather_rows;
+            src = x + (long)(zero ? 0 : id) * n;
+        }
+        f32x4 xv[NCH], gv[NCH];
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int col = (c * 64 + lane) * 4;
+            xv[c] = (col < n && !zero) ? ld4(src + col) : f32x4{0, 0, 0, 0};
+            gv[c] = col < n ? ld4(dy + (long)row * n + col) : f32x4{0, 0, 0, 0};
+            s += (xv[c][0] + xv[c][1]) + (xv[c][2] + xv[c][3]);
+        }
+        float mean, rstd;
+        if (mean_in) {
+            mean = mean_in[row];
+            rstd = rstd_in[row];
+        } else {
+            mean = wave_sum(s) * inv_n;
+            float q = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int col = (c * 64 + lane) * 4;
+                if (col < n) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float d = xv[c][e] - mean;
+                        q += d * d;
+                    }
+                }
+            }
+            rstd = 1.0f / sqrtf(wave_sum(q) * inv_n + eps);
+        }
+        float sg = 0.0f, sgx = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int col = (c * 64 + lane) * 4;
+            if (col < n) {
+                const f32x4 xh = (xv[c] - mean) * rstd;
+                const f32x4 g = gv[c] * gm[c];
+                sg += (g[0] + g[1]) + (g[2] + g[3]);
+                const f32x4 gx = g * xh;
+                sgx += (gx[0] + gx[1]) + (gx[2] + gx[3]);
+                gacc[c] += gv[c] * xh;
+                bacc[c] += gv[c];
+            }
+        }
+        const float mg = wave_sum(sg) * inv_n, mgx = wave_sum(sgx) * inv_n;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            const int col = (c * 64 + lane) * 4;
+            if (col < n) {
+                const f32x4 xh = (xv[c] - mean) * rstd;
+                float* o = dx + (long)row * n + col;
+                st4(o, ld4(o) + rstd * (gv[c] * gm[c] - mg - xh * mgx));
+            }
+        }
+    }
+    // The block's 4 waves combine their dγ/dβ partials in LDS (in wave order): one partial per block.
+    if (!part_g && !part_b) return;
+    extern __shared__ __attribute__((aligned(16))) float red[];  // [2][4][n]
+    const int wv = threadIdx.x >> 6;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < n) {
+            st4(red + (long)wv * n + col, gacc[c]);
+            st4(red + (long)(4 + wv) * n + col, bacc[c]);
+        }
+    }
+    __syncthreads();
+    for (int col = threadIdx.x; col < n; col += 256) {
+        if (part_g) part_g[(long)blockIdx.x * n + col] = ((red[col] + red[n + col]) + red[2 * n + col]) + red[3 * n + col];
+        if (part_b)
+            part_b[(long)blockIdx.x * n + col] =
+                ((red[4 * n + col] + red[5 * n + col]) + red[6 * n + col]) + red[7 * n + col];
+    }
+}
+
+// out[c] += Σ_k part[k][c]: 16 groups of 64 columns each sum every 16th partial in order, then the
+// group sums are added in group order, so the result is independent of timing.
+constexpr int RED_COLS = 64, RED_GROUPS = 16;
+__global__ __launch_bounds__(RED_COLS* RED_GROUPS) void partial_reduce_kernel(const float* __restrict__ part,
+                                                                              int count, int n,
+                                                                              float* __restrict__ out) {
+    __shared__ float sums[RED_GROUPS][RED_COLS];
+    const int lc = threadIdx.x % RED_COLS, g = threadIdx.x / RED_COLS;
+    const int c = blockIdx.x * RED_COLS + lc;
+    float s = 0.0f;
+    if (c < n)
+        for (int k = g; k < count; k += RED_GROUPS) s += part[(long)k * n + c];
+    sums[g][lc] = s;
+    __syncthreads();
+    if (g == 0 && c < n) {
+        float t = 0.0f;
+        for (int k = 0; k < RED_GROUPS; ++k) t += sums[k][lc];
+        out[c] += t;
+    }
+}
+
+int chunks_for(int n) {
+    LAYA_REQUIRE(n > 0 && n % 4 == 0, "layernorm: the row width must be a positive multiple of 4");
+    const int nch = (n + 255) / 256;
+    LAYA_REQUIRE(nch <= 8, "layernorm: rows wider than 2048 are not supported");
+    return nch;
+}
+
+}  // namespace
+
+void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps, float* y,
+                   float* mean, float* rstd, const int* gather_ids, const float* add_table, const int* add_index) {
+    if (rows <= 0) return;
+    const int nch = chunks_for(n);
+    // With gather_ids, x is a table of `gather_rows` rows; the caller validates ids on the host.
+    const int gather_rows = gather_ids ? INT32_MAX : 0;
+    dim3 grid((rows + 3) / 4), block(256);
+    ProfileScope scope(ctx, "layernorm_fwd", 0.0, (8.0 * n + 8.0) * rows + 4.0 * n * (b ? 2 : 1));
+#define LN_FWD(C)                                                                                                 \
+    case C:                                                                                                       \
+        hipLaunchKernelGGL(ln_fwd_kernel<C>, grid, block, 0, ctx->stream, x, rows, n, w, b, eps, y, mean, rstd, \
+                           gather_ids, gather_rows, add_table, add_index);                                       \
+        break;
+    switch (nch) { LN_FWD(1) LN_FWD(2) LN_FWD(3) LN_FWD(4) LN_FWD(5) LN_FWD(6) LN_FWD(7) LN_FWD(8) }
+#undef LN_FWD
+    check_launch("ln_fwd_kernel");
+}
+
+void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
+                   float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
+                   const int* gather_ids) {
+    if (rows <= 0) return;
+    const int nch = chunks_for(n);
+    const int gather_rows = gather_ids ? INT32_MAX : 0;
+    // A fixed row → wave assignment (wave w takes rows w, w + W, …) keeps dγ/dβ independent of timing.
+    const int waves = (std::min(rows, 2048) + 3) / 4 * 4;
+    const int blocks = waves / 4;
+    float* pg = nullptr;
+    float* pb = nullptr;
+    if (dgamma || dbeta) {
+        float* ws = static_cast<float*>(ctx->workspace(2, sizeof(float) * 2 * (size_t)blocks * n));
+        if (dgamma) pg = ws;
+        if (dbeta) pb = ws + (size_t)blocks * n;
+    }
+    const size_t lds = (pg || pb) ? sizeof(float) * 8 * (size_t)n : 0;
+    dim3 grid(blocks), block(256);
+    ProfileScope scope(ctx, "layernorm_bwd", 0.0, (16.0 * n + (mean ? 8.0 : 0.0)) * rows + 4.0 * n);
+#define LN_BWD(C)                                                                                                \
+    case C:                                                                                                      \
+        hipLaunchKernelGGL(ln_bwd_kernel<C>, grid, block, lds, ctx->stream, x, rows, n, w, eps, dy, dx, mean,  \
+                           rstd, gather_ids, gather_rows, waves, pg, pb);                                        \
+        break;
+    switch (nch) { LN_BWD(1) LN_BWD(2) LN_BWD(3) LN_BWD(4) LN_BWD(5) LN_BWD(6) LN_BWD(7) LN_BWD(8) }
+#undef LN_BWD
+    check_launch("ln_bwd_kernel");
+    const dim3 rgrid((n + RED_COLS - 1) / RED_COLS), rblock(RED_COLS * RED_GROUPS);
+    if (pg) {
+        hipLaunchKernelGGL(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pg, blocks, n, dgamma);
+        check_launch("partial_reduce_kernel");
+    }
+    if (pb) {
+        hipLaunchKernelGGL(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pb, blocks, n, dbeta);
+        check_launch("partial_reduce_kernel");
+    }
+}
+
+}  // namespace laya

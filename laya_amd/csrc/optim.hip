@@ -1,0 +1,99 @@
+// The optimizer step over the flat parameter arena.
+//
+// grad_norm restates Gradients.ClipByGlobalNorm (src/StructuredDecisions.Laya.Training/AdamW.cs:103-130):
+// Σg² accumulated in double over a fixed partition of the arena (results do not depend on timing),
+// the norm, and the coefficient max/(‖g‖ + 1e-6) rounded to float when it is below 1. Instead of a
+// separate scaling pass over the gradients, the coefficient is handed to the AdamW kernel, which
+// multiplies each gradient by it as it reads it — the same float product the reference's
+// SimdOps.Scale writes back.
+//
+// adamw restates AdamW.Step (AdamW.cs:29-73) for several parameter groups in one launch:
+// decoupled decay, both moments, bias-corrected update, optional clearing of the gradient
+// (ZeroGradients, TrainableDecisionModel.cs:237-240) in the same pass. 32 bytes per parameter.
+#include "elementwise.hpp"
+
+namespace laya {
+namespace {
+
+constexpr int NORM_BLOCKS = 1024;
+
+__global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ g, size_t n, size_t chunk,
+                                                    double* __restrict__ partial) {
+    __shared__ double red[4];
+    const size_t b = blockIdx.x * chunk, e = min(n, b + chunk);
+    double s = 0.0;
+    for (size_t i = b + threadIdx.x; i < e; i += 256) {
+        const double v = g[i];
+        s += v * v;
+    }
+    s = wave_sum_d(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ void norm_finish_kernel(const double* __restrict__ partial, int count, double max_norm, double* norm,
+                                   float* coef, int* nonfinite) {
+    if (threadIdx.x != 0) return;
+    double s = 0.0;
+    for (int i = 0; i < count; ++i) s += partial[i];
+    const double nrm = sqrt(s);
+    const double c = max_norm / (nrm + 1e-6);
+    if (norm) *norm = nrm;
+    if (coef) *coef = c < 1.0 ? (float)c : 1.0f;
+    if (nonfinite) *nonfinite = isfinite(nrm) ? 0 : 1;
+}
+
+__global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ m,
+                                                    float* __restrict__ v, size_t n, AdamGroups groups, float b1,
+                                                    float b2, float eps, float sqrt_c2, const float* coef,
+                                                    int zero_grads) {
+    const float cf = coef ? *coef : 1.0f;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        int grp = -1;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (k < groups.n && i >= groups.begin[k] && i < groups.end[k]) grp = k;
+        const float gi = g[i];
+        if (grp >= 0) {
+            const float gs = gi * cf;
+            float w = p[i] * groups.decay[grp];
+            const float mi = b1 * m[i] + (1.0f - b1) * gs;
+            const float vi = b2 * v[i] + (1.0f - b2) * gs * gs;
+            w -= groups.step_size[grp] * mi / (sqrtf(vi) / sqrt_c2 + eps);
+            p[i] = w;
+            m[i] = mi;
+            v[i] = vi;
+        }
+        if (zero_grads) g[i] = 0.0f;
+    }
+}
+
+}  // namespace
+
+void grad_norm(laya_ctx* ctx, const float* g, size_t n, double max_norm, double* norm, float* coef, int* nonfinite) {
+    double* partial = static_cast<double*>(ctx->workspace(1, sizeof(double) * NORM_BLOCKS));
+    size_t chunk = (n + NORM_BLOCKS - 1) / NORM_BLOCKS;
+    chunk = (chunk + 1023) / 1024 * 1024;
+    if (chunk == 0) chunk = 1024;
+    ProfileScope scope(ctx, "grad_norm", 0.0, 4.0 * n);
+    hipLaunchKernelGGL(sumsq_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx->stream, g, n, chunk, partial);
+    check_launch("sumsq_kernel");
+    hipLaunchKernelGGL(norm_finish_kernel, dim3(1), dim3(64), 0, ctx->stream, partial, NORM_BLOCKS, max_norm, norm,
+                       coef, nonfinite);
+    check_launch("norm_finish_kernel");
+}
+
+void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n, const AdamGroups& groups,
+                 float beta1, float beta2, float eps, float sqrt_c2, const float* coef, int zero_grads) {
+    LAYA_REQUIRE(groups.n >= 0 && groups.n <= 4, "adamw: at most 4 parameter groups");
+    for (int k = 0; k < groups.n; ++k)
+        LAYA_REQUIRE(groups.begin[k] <= groups.end[k] && groups.end[k] <= n, "adamw: group range outside the arena");
+    if (!n) return;
+    ProfileScope scope(ctx, "adamw", 0.0, (zero_grads ? 32.0 : 28.0) * n);
+    hipLaunchKernelGGL(adamw_kernel, dim3(blocks_for(n, 256, 8192)), dim3(256), 0, ctx->stream, p, g, m, v, n, groups,
+                       beta1, beta2, eps, sqrt_c2, coef, zero_grads);
+    check_launch("adamw_kernel");
+}
+
+}  // namespace laya

@@ -1,0 +1,212 @@
+"""The trainable decision model on the GPU, mirroring the reference's ``TrainableDecisionModel``
+(src/StructuredDecisions.Laya.Training/TrainableDecisionModel.cs) over liblaya_hip's model driver.
+
+Parameters, gradients and optimizer moments live in device arenas; the forward keeps every
+activation the backward needs in HBM (no per-layer recompute); only token ids, segment tables and
+marker rows go in, and logits come out (dlogits go back in).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Dict, List, Optional, Sequence
+
+import numpy as np
+
+from ._native import BatchC, ModelConfigC, check, lib
+from .batch import Batch, TrainingItem
+from .config import ModelConfig
+from .device import Context
+from .safetensors_io import SafetensorsFile
+
+
+def _config_struct(mc: ModelConfig):
+    e = mc.encoder
+    kinds = (ctypes.c_int * max(1, e.num_hidden_layers))(*e.layer_kinds)
+    c = ModelConfigC(vocab=e.vocab_size, hidden=e.hidden_size, intermediate=e.intermediate_size,
+                     layers=e.num_hidden_layers, heads=e.num_attention_heads, local_attention=e.local_attention,
+                     global_every=e.global_attn_every_n_layers, layer_kinds=kinds,
+                     theta_global=e.global_rope_theta, theta_local=e.local_rope_theta, norm_eps=e.norm_eps,
+                     norm_bias=int(e.norm_bias), attention_bias=int(e.attention_bias), mlp_bias=int(e.mlp_bias),
+                     head_layers=mc.head_layers, head_ff=mc.head_ff, n_act=mc.n_act)
+    return c, kinds
+
+
+class _BatchArgs:
+    """Keeps the host arrays of a batch alive while the C struct points into them."""
+
+    def __init__(self, batch: Batch):
+        self.arrays = [np.ascontiguousarray(a, dtype=np.int32) for a in
+                       (batch.lengths, batch.tokens, batch.n_options, batch.markers, batch.qtypes)]
+        self.struct = BatchC(batch.n_items, *[a.ctypes.data for a in self.arrays])
+
+
+def _as_batch(items) -> Batch:
+    if isinstance(items, Batch):
+        return items
+    return Batch.from_items(list(items))
+
+
+class TrainableDecisionModel:
+    def __init__(self, config: ModelConfig, ctx: Optional[Context] = None):
+        self.config = config
+        self.ctx = ctx or Context(0)
+        cs, self._kinds = _config_struct(config)
+        h = ctypes.c_void_p()
+        check(lib().laya_model_create(self.ctx.handle, ctypes.byref(cs), ctypes.byref(h)))
+        self.handle = h.value
+        self.ctx.register(self)
+        n = ctypes.c_int()
+        check(lib().laya_model_num_params(self.handle, ctypes.byref(n)))
+        self.names: List[str] = []
+        self.shapes: Dict[str, tuple] = {}
+        self.index: Dict[str, int] = {}
+        for i in range(n.value):
+            name = ctypes.c_char_p()
+            ndim = ctypes.c_int()
+            dims = (ctypes.c_int * 4)()
+            off, numel, tr = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_int()
+            check(lib().laya_model_param_info(self.handle, i, ctypes.byref(name), ctypes.byref(ndim), dims,
+                                              ctypes.byref(off), ctypes.byref(numel), ctypes.byref(tr)))
+            nm = name.value.decode()
+            self.names.append(nm)
+            self.shapes[nm] = tuple(dims[k] for k in range(ndim.value))
+            self.index[nm] = i
+        self._batch: Optional[Batch] = None
+        self._head_dropout = 0.1
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) and getattr(self.ctx, "handle", None):
+            lib().laya_model_destroy(self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ------------------------------------------------------------------ construction / IO
+
+    @classmethod
+    def from_directory(cls, directory: str, ctx: Optional[Context] = None) -> "TrainableDecisionModel":
+        """TrainableDecisionModel.FromDirectory (TrainableDecisionModel.cs:191-197)."""
+        model = cls(ModelConfig.from_directory(directory), ctx)
+        st = SafetensorsFile(os.path.join(directory, "model.safetensors"))
+        for name in model.names:
+            if name not in st.entries:
+                if name == "temperature":
+                    continue
+                raise KeyError(f"the checkpoint has no '{name}' tensor; is it a laya decision model?")
+            model.set_param(name, st.read_float32(name))
+        return model
+
+    @classmethod
+    def synthetic(cls, config: ModelConfig, seed: int = 0, std: float = 0.02,
+                  ctx: Optional[Context] = None) -> "TrainableDecisionModel":
+        """Random init on the device: N(0, std) matrices, unit norm weights, zero biases."""
+        model = cls(config, ctx)
+        check(lib().laya_model_init_random(model.handle, seed & (2 ** 64 - 1), std))
+        return model
+
+    def set_param(self, name: str, values: np.ndarray) -> None:
+        a = np.ascontiguousarray(values, np.float32).reshape(-1)
+        if a.size != int(np.prod(self.shapes[name])):
+            raise ValueError(f"{name}: {a.size} values for shape {self.shapes[name]}")
+        check(lib().laya_model_set_param(self.handle, self.index[name], a.ctypes.data))
+
+    def set_params(self, params: Dict[str, np.ndarray]) -> None:
+        for name in self.names:
+            if name in params:
+                self.set_param(name, params[name])
+
+    def param(self, name: str) -> np.ndarray:
+        out = np.empty(self.shapes[name], np.float32)
+        check(lib().laya_model_get_param(self.handle, self.index[name], out.ctypes.data))
+        return out
+
+    def grad(self, name: str) -> np.ndarray:
+        out = np.empty(self.shapes[name], np.float32)
+        check(lib().laya_model_get_grad(self.handle, self.index[name], out.ctypes.data))
+        return out
+
+    def has_grad(self, name: str) -> bool:
+        v = ctypes.c_int()
+        check(lib().laya_model_has_grad(self.handle, self.index[name], ctypes.byref(v)))
+        return bool(v.value)
+
+    def trainable(self, name: str) -> bool:
+        tr = ctypes.c_int()
+        check(lib().laya_model_param_info(self.handle, self.index[name], None, None, None, None, None,
+                                          ctypes.byref(tr)))
+        return bool(tr.value)
+
+    @property
+    def parameter_count(self) -> int:
+        return sum(int(np.prod(s)) for n, s in self.shapes.items() if n != "temperature")
+
+    # ------------------------------------------------------------------------ training
+
+    def set_trainable_encoder_layers(self, n: Optional[int]) -> None:
+        check(lib().laya_model_set_trainable_encoder_layers(self.handle, -1 if n is None else int(n)))
+
+    @property
+    def head_dropout(self) -> float:
+        return self._head_dropout
+
+    @head_dropout.setter
+    def head_dropout(self, p: float) -> None:
+        check(lib().laya_model_set_head_dropout(self.handle, float(p)))
+        self._head_dropout = float(p)
+
+    def forward(self, items, training: bool = False, seed: int = 0, want_logits: bool = True):
+        """Forward (TrainableDecisionModel.cs:248-353): returns the per-option logits, concatenated."""
+        batch = _as_batch(items)
+        args = _BatchArgs(batch)
+        logits = np.zeros(max(1, batch.n_markers), np.float32) if want_logits else None
+        check(lib().laya_model_forward(self.handle, ctypes.byref(args.struct), int(training),
+                                       seed & (2 ** 64 - 1), None if logits is None else logits.ctypes.data))
+        self._batch = batch
+        return None if logits is None else logits[:batch.n_markers]
+
+    def backward(self, logit_gradients) -> None:
+        """Backward (TrainableDecisionModel.cs:479-549): per-option dL/dlogit, concatenated or per item."""
+        if isinstance(logit_gradients, (list, tuple)):
+            logit_gradients = np.concatenate([np.asarray(g, np.float32).reshape(-1) for g in logit_gradients])
+        d = np.ascontiguousarray(logit_gradients, np.float32)
+        check(lib().laya_model_backward(self.handle, d.ctypes.data))
+
+    def zero_gradients(self) -> None:
+        check(lib().laya_model_zero_grad(self.handle))
+
+    def clip_grad_norm(self, max_norm: float) -> float:
+        """Gradients.ClipByGlobalNorm (AdamW.cs:103-130); the scaling is applied by the next AdamW step."""
+        v = ctypes.c_double()
+        check(lib().laya_model_clip_grad_norm(self.handle, float(max_norm), ctypes.byref(v)))
+        return v.value
+
+    def adamw_step(self, lr_encoder: float, lr_head: float, beta1: float = 0.9, beta2: float = 0.999,
+                   eps: float = 1e-8, weight_decay: float = 0.01) -> None:
+        check(lib().laya_model_adamw_step(self.handle, lr_encoder, lr_head, beta1, beta2, eps, weight_decay))
+
+    @property
+    def steps(self) -> int:
+        v = ctypes.c_int()
+        check(lib().laya_model_steps(self.handle, ctypes.byref(v)))
+        return v.value
+
+    def train_step(self, batch: Batch, targets: np.ndarray, seed: int, ce_weight: float = 1.0,
+                   loss_scale: float = 1.0, max_norm: float = 1.0, lr_encoder: float = 3e-5, lr_head: float = 3e-5,
+                   beta1: float = 0.9, beta2: float = 0.999, eps: float = 1e-8, weight_decay: float = 0.01,
+                   want_loss: bool = False, _args: Optional[_BatchArgs] = None) -> Optional[float]:
+        """One micro-step with GradAccum = 1 (Trainer.cs:131-144), CE objective on the device."""
+        args = _args or _BatchArgs(batch)
+        t = np.ascontiguousarray(targets, np.float32)
+        loss = ctypes.c_float()
+        check(lib().laya_model_train_step(self.handle, ctypes.byref(args.struct), t.ctypes.data, ce_weight,
+                                          loss_scale, seed & (2 ** 64 - 1), max_norm, lr_encoder, lr_head, beta1,
+                                          beta2, eps, weight_decay, ctypes.byref(loss) if want_loss else None))
+        return float(loss.value) if want_loss else None
+
+    def batch_args(self, batch: Batch) -> _BatchArgs:
+        return _BatchArgs(batch)

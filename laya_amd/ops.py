@@ -1,0 +1,272 @@
+"""The differentiable op surface, mirroring the reference's ``Ops``
+(src/StructuredDecisions.Laya.Training/Ops.cs:17-504) over device arrays.
+
+Same names, argument meaning and conventions: a forward writes its output; ``linear_backward``
+OVERWRITES its input gradient; every other backward ADDS into its input gradient; parameter
+gradients always ACCUMULATE (Ops.cs:8-16). Each call is one C-ABI entry point of liblaya_hip.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+from ._native import check, lib, ptr
+from .device import Context, DeviceArray
+
+
+class Parameter:
+    """Parameter.cs:14-70: device values plus a lazily allocated, accumulating device gradient."""
+
+    def __init__(self, ctx: Context, name: str, data: np.ndarray, trainable: bool = True):
+        self.ctx = ctx
+        self.name = name
+        self.shape = tuple(np.shape(data))
+        self.data = DeviceArray.from_numpy(ctx, np.asarray(data, np.float32))
+        self.trainable = trainable
+        self._grad: Optional[DeviceArray] = None
+
+    @property
+    def gradient(self) -> Optional[DeviceArray]:
+        return self._grad
+
+    def gradient_buffer(self) -> DeviceArray:
+        if self._grad is None:
+            self._grad = DeviceArray(self.ctx, self.shape)
+        return self._grad
+
+    def zero_gradient(self) -> None:
+        if self._grad is not None:
+            self._grad.fill(0.0)
+
+
+def _h(ctx: Context):
+    return ctx.handle
+
+
+# ----------------------------------------------------------------------------------- linear
+
+def linear(weight: Parameter, bias: Optional[Parameter], x: DeviceArray, rows: int, y: DeviceArray,
+           residual: Optional[DeviceArray] = None) -> None:
+    """Ops.Linear (Ops.cs:22-27): y = x·Wᵀ + b (+ residual, the skip add fused into the epilogue)."""
+    out, inn = weight.shape
+    check(lib().laya_linear_fwd(_h(weight.ctx), x.ptr, rows, inn, weight.data.ptr, out,
+                                None if bias is None else bias.data.ptr, ptr(residual), y.ptr))
+
+
+def linear_backward(weight: Parameter, bias: Optional[Parameter], x: DeviceArray, dy: DeviceArray, rows: int,
+                    dx: Optional[DeviceArray]) -> None:
+    """Ops.LinearBackward (Ops.cs:33-69): dx = dy·W (overwritten), dW += dyᵀ·x, db += Σ dy."""
+    out, inn = weight.shape
+    dW = weight.gradient_buffer().ptr if weight.trainable else None
+    db = bias.gradient_buffer().ptr if (bias is not None and bias.trainable) else None
+    check(lib().laya_linear_bwd(_h(weight.ctx), x.ptr, dy.ptr, rows, inn, out, weight.data.ptr, ptr(dx), dW, db))
+
+
+# ------------------------------------------------------------------------------- layer norm
+
+def layer_norm(x: DeviceArray, rows: int, n: int, weight: Parameter, bias: Optional[Parameter], epsilon: float,
+               y: DeviceArray, mean: Optional[DeviceArray] = None, rstd: Optional[DeviceArray] = None) -> None:
+    """Ops.LayerNorm (Ops.cs:103-110); optionally keeps the row statistics for the backward."""
+    check(lib().laya_layernorm_fwd(_h(weight.ctx), x.ptr, rows, n, weight.data.ptr,
+                                   None if bias is None else bias.data.ptr, epsilon, y.ptr, ptr(mean), ptr(rstd)))
+
+
+def layer_norm_backward(x: DeviceArray, rows: int, n: int, weight: Parameter, bias: Optional[Parameter],
+                        epsilon: float, dy: DeviceArray, dx: DeviceArray, mean: Optional[DeviceArray] = None,
+                        rstd: Optional[DeviceArray] = None) -> None:
+    """Ops.LayerNormBackward (Ops.cs:117-186): dx += …, dγ += Σ dy·x̂, dβ += Σ dy."""
+    dg = weight.gradient_buffer().ptr if weight.trainable else None
+    dbeta = bias.gradient_buffer().ptr if (bias is not None and bias.trainable) else None
+    check(lib().laya_layernorm_bwd(_h(weight.ctx), x.ptr, rows, n, weight.data.ptr, epsilon, dy.ptr, dx.ptr, dg,
+                                   dbeta, ptr(mean), ptr(rstd)))
+
+
+# ------------------------------------------------------------------------------ activations
+
+def gelu(ctx: Context, x: DeviceArray, y: Optional[DeviceArray] = None) -> None:
+    """SimdOps.Gelu (SimdOps.cs:305-323), exact erf GELU (in place when y is None)."""
+    check(lib().laya_gelu_fwd(_h(ctx), x.ptr, x.size, (y or x).ptr))
+
+
+def gelu_backward(ctx: Context, u: DeviceArray, grad: DeviceArray) -> None:
+    """Ops.GeluBackward (Ops.cs:194-218): grad *= Φ(u) + u·φ(u)."""
+    check(lib().laya_gelu_bwd(_h(ctx), u.ptr, grad.ptr, grad.size))
+
+
+def geglu(ctx: Context, wide: DeviceArray, rows: int, intermediate: int, act: DeviceArray) -> None:
+    check(lib().laya_geglu_fwd(_h(ctx), wide.ptr, rows, intermediate, act.ptr))
+
+
+def geglu_backward(ctx: Context, wide: DeviceArray, dact: DeviceArray, rows: int, intermediate: int,
+                   dwide: DeviceArray) -> None:
+    check(lib().laya_geglu_bwd(_h(ctx), wide.ptr, dact.ptr, rows, intermediate, dwide.ptr))
+
+
+# ---------------------------------------------------------------------------------- dropout
+
+def uniform(seed: int, index: int) -> float:
+    """Ops.Uniform (Ops.cs:227-234)."""
+    return lib().laya_uniform(seed & (2 ** 64 - 1), index & (2 ** 64 - 1))
+
+
+def mix(seed: int, salt: int) -> int:
+    """Ops.Mix (Ops.cs:236-241)."""
+    return lib().laya_mix(seed & (2 ** 64 - 1), salt & (2 ** 64 - 1))
+
+
+def dropout(ctx: Context, values: DeviceArray, length: int, probability: float, seed: int) -> None:
+    """Ops.Dropout (Ops.cs:244-258), in place; its own backward."""
+    if probability <= 0:
+        return
+    check(lib().laya_dropout(_h(ctx), values.ptr, length, probability, seed & (2 ** 64 - 1)))
+
+
+# -------------------------------------------------------------------------------- attention
+
+class Rotary:
+    """Rotary (Ops.cs:446-504): device cos/sin tables built in double, rounded to float."""
+
+    def __init__(self, ctx: Context, head_dim: int, theta: float, positions: int = 1024):
+        import ctypes
+        self.ctx = ctx
+        self.head_dim = head_dim
+        self.theta = theta
+        h = ctypes.c_void_p()
+        check(lib().laya_rotary_create(_h(ctx), head_dim, float(theta), max(1, positions), ctypes.byref(h)))
+        self.handle = h.value
+        self.positions = max(1, positions)
+        ctx.register(self)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) and getattr(self.ctx, "handle", None):
+            lib().laya_rotary_destroy(self.ctx.handle, self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def ensure(self, positions: int) -> None:
+        if positions > self.positions:
+            self.close()
+            self.__init__(self.ctx, self.head_dim, self.theta, max(positions, 2 * self.positions))
+
+    def apply(self, vec: DeviceArray, rows: int, positions: DeviceArray, inverse: bool) -> None:
+        check(lib().laya_rotary_apply(_h(self.ctx), self.handle, vec.ptr, rows, positions.ptr, int(inverse)))
+
+
+@dataclass
+class AttentionShape:
+    """Ops.AttentionShape (Ops.cs:263-267). half_window < 0 (or None) means no window."""
+    hidden: int
+    heads: int
+    scale: float
+    half_window: Optional[int]
+    rotary: Optional[Rotary]
+    dropout: float
+    seed: int
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden // self.heads
+
+
+class Segments:
+    """The concatenated items of a batch (ModernBertEncoder.Segment), as device tables."""
+
+    def __init__(self, ctx: Context, lengths: Sequence[int]):
+        lengths = np.asarray(lengths, np.int32)
+        self.lengths = lengths
+        self.starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int32) if len(lengths) else \
+            np.zeros(0, np.int32)
+        self.d_start = DeviceArray.from_numpy(ctx, self.starts if len(lengths) else np.zeros(1, np.int32))
+        self.d_len = DeviceArray.from_numpy(ctx, lengths if len(lengths) else np.zeros(1, np.int32))
+        self.count = len(lengths)
+        self.max_len = int(lengths.max()) if len(lengths) else 0
+        self.rows = int(lengths.sum())
+
+
+def _hw(shape: AttentionShape) -> int:
+    return -1 if shape.half_window is None or shape.half_window < 0 else int(shape.half_window)
+
+
+def attention_forward(qkv: DeviceArray, segments: Segments, shape: AttentionShape, context: DeviceArray,
+                      lse: DeviceArray) -> None:
+    """Ops.AttentionForward (Ops.cs:275-277); also writes the row log-sum-exp the backward reuses."""
+    if shape.rotary is not None:
+        shape.rotary.ensure(segments.max_len)
+    check(lib().laya_attention_fwd(_h(qkv.ctx), qkv.ptr, segments.d_start.ptr, segments.d_len.ptr, segments.count,
+                                   segments.max_len, shape.hidden, shape.heads, shape.scale, _hw(shape),
+                                   None if shape.rotary is None else shape.rotary.handle, shape.dropout,
+                                   shape.seed & (2 ** 64 - 1), context.ptr, lse.ptr))
+
+
+def attention_backward(qkv: DeviceArray, segments: Segments, shape: AttentionShape, context: DeviceArray,
+                       lse: DeviceArray, dcontext: DeviceArray, dqkv: DeviceArray) -> None:
+    """Ops.AttentionBackward (Ops.cs:280-282): dq, dk, dv written (not added) into dqkv."""
+    if shape.rotary is not None:
+        shape.rotary.ensure(segments.max_len)
+    check(lib().laya_attention_bwd(_h(qkv.ctx), qkv.ptr, segments.d_start.ptr, segments.d_len.ptr, segments.count,
+                                   segments.max_len, shape.hidden, shape.heads, shape.scale, _hw(shape),
+                                   None if shape.rotary is None else shape.rotary.handle, shape.dropout,
+                                   shape.seed & (2 ** 64 - 1), context.ptr, lse.ptr, dcontext.ptr, dqkv.ptr))
+
+
+def default_scale(head_dim: int) -> float:
+    """1/√d_h as the reference computes it in float (TrainableDecisionModel.cs:417)."""
+    return float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+
+
+# ------------------------------------------------------------------ rows, embeddings, objective
+
+def gather_rows(ctx: Context, src: DeviceArray, rows: DeviceArray, n: int, width: int, dst: DeviceArray) -> None:
+    check(lib().laya_gather_rows(_h(ctx), src.ptr, rows.ptr, n, width, dst.ptr))
+
+
+def scatter_add_rows(ctx: Context, src: DeviceArray, rows: DeviceArray, n: int, width: int, dst: DeviceArray) -> None:
+    check(lib().laya_scatter_add_rows(_h(ctx), src.ptr, rows.ptr, n, width, dst.ptr))
+
+
+def embedding_plan(ids: np.ndarray, vocab: int):
+    """Token positions stably sorted by id, the unique ids and their run offsets."""
+    import ctypes
+    ids = np.ascontiguousarray(ids, np.int32)
+    n = ids.size
+    sorted_pos = np.zeros(max(n, 1), np.int32)
+    unique = np.zeros(max(n, 1), np.int32)
+    offsets = np.zeros(n + 1, np.int32)
+    nu = ctypes.c_int()
+    check(lib().laya_embedding_plan(ids.ctypes.data, n, vocab, sorted_pos.ctypes.data, unique.ctypes.data,
+                                    offsets.ctypes.data, ctypes.byref(nu)))
+    return sorted_pos[:n], unique[:nu.value], offsets[:nu.value + 1]
+
+
+def embedding_backward(ctx: Context, ids: np.ndarray, d: DeviceArray, hidden: int, grad: DeviceArray,
+                       vocab: int) -> None:
+    """grad[id] += Σ d[t] over that id's tokens, in token order (TrainableDecisionModel.cs:543-547)."""
+    sp, un, off = embedding_plan(ids, vocab)
+    if un.size == 0:
+        return
+    a, b, c = (DeviceArray.from_numpy(ctx, x) for x in (sp, un, off))
+    check(lib().laya_embedding_bwd(_h(ctx), a.ptr, b.ptr, c.ptr, un.size, d.ptr, hidden, grad.ptr))
+    ctx.sync()
+
+
+def softmax_ce_backward(ctx: Context, logits: DeviceArray, targets: DeviceArray, option_offsets: DeviceArray,
+                        n_items: int, ce_weight: float, scale: float, grad: DeviceArray,
+                        loss: Optional[DeviceArray] = None) -> None:
+    check(lib().laya_softmax_ce_bwd(_h(ctx), logits.ptr, targets.ptr, option_offsets.ptr, n_items, ce_weight, scale,
+                                    grad.ptr, ptr(loss)))
+
+
+def layer_norm_eps_default() -> float:
+    return 1e-5
+
+
+def attention_scale(hidden: int, heads: int) -> float:
+    return 1.0 / math.sqrt(hidden // heads)

@@ -9,9 +9,12 @@
 // the reference's (any exact fp32 GEMM is acceptable there; parity is at tolerance level).
 //
 // Compiled with -ffp-contract=fast so the micro-kernel uses FMA, as the reference GEMM does.
+#include <immintrin.h>
+
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 #include <omp.h>
 
@@ -27,42 +30,62 @@ template <> struct VecTraits<double> {
     static constexpr int W = 4;
 };
 
+// 6 × (2 vectors) register tile with AVX2 FMA: 12 named accumulators stay in ymm registers.
+#define OGEMM_MICRO(NAME, R, V, LOAD, STORE, BCAST, FMA, ZERO, ADD, W)                                        \
+    static inline void NAME(int kc, const R* __restrict ap, const R* __restrict bp, R* c, long ldc, int mr,    \
+                            int nr) {                                                                        \
+        V c00 = ZERO(), c01 = ZERO(), c10 = ZERO(), c11 = ZERO(), c20 = ZERO(), c21 = ZERO();                 \
+        V c30 = ZERO(), c31 = ZERO(), c40 = ZERO(), c41 = ZERO(), c50 = ZERO(), c51 = ZERO();                 \
+        for (int k = 0; k < kc; ++k) {                                                                        \
+            const R* b = bp + (long)k * 2 * W;                                                                \
+            const R* a = ap + (long)k * 6;                                                                    \
+            const V b0 = LOAD(b), b1 = LOAD(b + W);                                                           \
+            V x = BCAST(a + 0);                                                                               \
+            c00 = FMA(x, b0, c00);                                                                            \
+            c01 = FMA(x, b1, c01);                                                                            \
+            x = BCAST(a + 1);                                                                                 \
+            c10 = FMA(x, b0, c10);                                                                            \
+            c11 = FMA(x, b1, c11);                                                                            \
+            x = BCAST(a + 2);                                                                                 \
+            c20 = FMA(x, b0, c20);                                                                            \
+            c21 = FMA(x, b1, c21);                                                                            \
+            x = BCAST(a + 3);                                                                                 \
+            c30 = FMA(x, b0, c30);                                                                            \
+            c31 = FMA(x, b1, c31);                                                                            \
+            x = BCAST(a + 4);                                                                                 \
+            c40 = FMA(x, b0, c40);                                                                            \
+            c41 = FMA(x, b1, c41);                                                                            \
+            x = BCAST(a + 5);                                                                                 \
+            c50 = FMA(x, b0, c50);                                                                            \
+            c51 = FMA(x, b1, c51);                                                                            \
+        }                                                                                                     \
+        V acc[12] = {c00, c01, c10, c11, c20, c21, c30, c31, c40, c41, c50, c51};                             \
+        if (mr == 6 && nr == 2 * W) {                                                                         \
+            for (int i = 0; i < 6; ++i) {                                                                     \
+                STORE(c + i * ldc, ADD(LOAD(c + i * ldc), acc[2 * i]));                                       \
+                STORE(c + i * ldc + W, ADD(LOAD(c + i * ldc + W), acc[2 * i + 1]));                           \
+            }                                                                                                 \
+        } else {                                                                                              \
+            for (int i = 0; i < mr; ++i) {                                                                    \
+                R tmp[2 * W];                                                                                 \
+                STORE(tmp, acc[2 * i]);                                                                       \
+                STORE(tmp + W, acc[2 * i + 1]);                                                               \
+                for (int j = 0; j < nr; ++j) c[i * ldc + j] += tmp[j];                                        \
+            }                                                                                                 \
+        }                                                                                                     \
+    }
+
+OGEMM_MICRO(micro_f32, float, __m256, _mm256_loadu_ps, _mm256_storeu_ps, _mm256_broadcast_ss, _mm256_fmadd_ps,
+            _mm256_setzero_ps, _mm256_add_ps, 8)
+OGEMM_MICRO(micro_f64, double, __m256d, _mm256_loadu_pd, _mm256_storeu_pd, _mm256_broadcast_sd, _mm256_fmadd_pd,
+            _mm256_setzero_pd, _mm256_add_pd, 4)
+
 template <typename R>
-static inline void micro_kernel(int kc, const R* __restrict ap, const R* __restrict bp, R* c, long ldc, int mr, int nr) {
-    using T = VecTraits<R>;
-    using V = typename T::V;
-    constexpr int W = T::W, NR = 2 * W, MR = 6;
-    V acc[MR][2];
-    for (int i = 0; i < MR; ++i) acc[i][0] = acc[i][1] = V{} ;
-    for (int k = 0; k < kc; ++k) {
-        V b0, b1;
-        std::memcpy(&b0, bp + (long)k * NR, sizeof(V));
-        std::memcpy(&b1, bp + (long)k * NR + W, sizeof(V));
-        const R* a = ap + (long)k * MR;
-        for (int i = 0; i < MR; ++i) {
-            V av = V{} + a[i];
-            acc[i][0] += av * b0;
-            acc[i][1] += av * b1;
-        }
-    }
-    if (mr == MR && nr == NR) {
-        for (int i = 0; i < MR; ++i) {
-            V c0, c1;
-            std::memcpy(&c0, c + i * ldc, sizeof(V));
-            std::memcpy(&c1, c + i * ldc + W, sizeof(V));
-            c0 += acc[i][0];
-            c1 += acc[i][1];
-            std::memcpy(c + i * ldc, &c0, sizeof(V));
-            std::memcpy(c + i * ldc + W, &c1, sizeof(V));
-        }
-    } else {
-        for (int i = 0; i < mr; ++i) {
-            R tmp[2 * W];
-            std::memcpy(tmp, &acc[i][0], sizeof(V));
-            std::memcpy(tmp + W, &acc[i][1], sizeof(V));
-            for (int j = 0; j < nr; ++j) c[i * ldc + j] += tmp[j];
-        }
-    }
+static inline void micro_kernel(int kc, const R* ap, const R* bp, R* c, long ldc, int mr, int nr) {
+    if constexpr (std::is_same<R, float>::value)
+        micro_f32(kc, ap, bp, c, ldc, mr, nr);
+    else
+        micro_f64(kc, ap, bp, c, ldc, mr, nr);
 }
 
 // C[m*ldc + n] = (accumulate ? C : 0) + Σ_k A[m*sam + k*sak] · B[k*sbk + n*sbn]

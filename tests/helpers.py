@@ -1,0 +1,35 @@
+"""Shared test helpers: seeded parameters and model shapes."""
+import numpy as np
+
+from laya_amd.batch import synthetic_batch
+from laya_amd.config import EncoderConfig, ModelConfig
+
+
+def random_params(shapes: dict, seed: int, std: float = 0.08) -> dict:
+    """Every tensor non-trivial (norm weights 1 + 0.2·N(0,1), the rest std·N(0,1)), as the reference's
+    fixture generator does (tools/dump_training_reference.py:51-56)."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, shape in shapes.items():
+        if len(shape) == 1 and "norm" in name and name.endswith("weight") or name.startswith("scorer.0.weight"):
+            out[name] = (1.0 + 0.2 * rng.standard_normal(shape)).astype(np.float32)
+        elif name == "temperature":
+            out[name] = np.ones(shape, np.float32)
+        else:
+            out[name] = (std * rng.standard_normal(shape)).astype(np.float32)
+    return out
+
+
+def mid_config(layers: int = 3, hidden: int = 768, heads: int = 12, inter: int = 1152, vocab: int = 1000,
+               window: int = 128, head_layers: int = 2) -> ModelConfig:
+    """ModernBERT-base widths at a few layers: global first, then sliding (θ 160000 / 10000)."""
+    enc = EncoderConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=inter, num_hidden_layers=layers,
+                        num_attention_heads=heads, local_attention=window, global_attn_every_n_layers=3)
+    return ModelConfig(encoder=enc, head_layers=head_layers, n_act=2)
+
+
+def mixed_batch(rng, lengths, vocab, options=(8, 4, 2)):
+    n = len(lengths)
+    opts = [min(options[i % len(options)], max(1, (lengths[i] - 1) // 2)) for i in range(n)]
+    qtypes = [i % 3 for i in range(n)]
+    return synthetic_batch(rng, lengths, opts, qtypes, vocab)

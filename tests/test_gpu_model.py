@@ -1,0 +1,191 @@
+"""Model-level parity on the GPU: the reference's golden fixture, and the oracle at ModernBERT-base
+widths, through the model driver of the C-ABI.
+
+Bar (fp32): relative L2 ≤ 1e-4 per gradient tensor, and the reference test's own
+max|Δ|/max|g| < 1e-4 on the golden fixture (TrainingGradientTests.cs:58-85).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from fixtures import max_rel, rel_l2, tiny_batch, tiny_config, tiny_grads, tiny_params, TINY
+from helpers import mid_config, mixed_batch, random_params
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from laya_amd.device import Context
+    print("GPU model tests: creating context on device 0", flush=True)
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def test_tiny_fixture_logits_and_every_gradient(ctx):
+    from laya_amd.model import TrainableDecisionModel
+    print("model: training-tiny fixture", flush=True)
+    m = TrainableDecisionModel.from_directory(TINY, ctx)
+    m.set_trainable_encoder_layers(None)
+    batch, coeff, torch_logits = tiny_batch()
+    logits = m.forward(batch, training=False)
+    assert np.abs(logits - torch_logits).max() < 1e-4
+    m.backward(coeff)
+    grads = tiny_grads()
+    for name, expected in grads.items():
+        got = m.grad(name)
+        assert max_rel(expected, got) < 1e-4, name
+        assert rel_l2(expected, got) < 1e-4, name
+    for name in m.names:
+        if name.startswith("act_head."):
+            assert not np.any(m.grad(name))
+
+
+def test_tiny_freezing_the_encoder(ctx):
+    from laya_amd.model import TrainableDecisionModel
+    m = TrainableDecisionModel.from_directory(TINY, ctx)
+    m.set_trainable_encoder_layers(1)
+    batch, coeff, _ = tiny_batch()
+    m.forward(batch)
+    m.backward(coeff)
+    assert not m.has_grad("encoder.layers.0.attn.Wqkv.weight")
+    assert not m.has_grad("encoder.embeddings.tok_embeddings.weight")
+    assert m.has_grad("encoder.layers.3.attn.Wqkv.weight")
+    expected = tiny_grads()["encoder.layers.3.mlp.Wi.weight"]
+    assert rel_l2(expected, m.grad("encoder.layers.3.mlp.Wi.weight")) < 1e-4
+
+
+@pytest.mark.parametrize("dropout", [0.0, 0.3])
+def test_tiny_training_mode_matches_the_oracle(ctx, dropout):
+    """Training mode regenerates the same counter-RNG masks as the oracle (bit-exact integer work),
+    so GPU and oracle gradients agree to fp32 rounding."""
+    from laya_amd.model import TrainableDecisionModel
+    m = TrainableDecisionModel.from_directory(TINY, ctx)
+    m.head_dropout = dropout
+    o = oracle.OracleModel(tiny_config())
+    o.set_params(tiny_params())
+    o.set_trainable_encoder_layers(None)
+    o.set_head_dropout(dropout)
+    batch, coeff, _ = tiny_batch()
+    seed = 12345
+    lg = m.forward(batch, training=True, seed=seed)
+    lo = o.forward(batch, training=True, keep_tape=True, seed=seed)
+    assert np.abs(lg - lo).max() < 1e-5
+    m.backward(coeff)
+    o.backward(coeff)
+    for name in m.names:
+        if name == "temperature" or name.startswith("act_head"):
+            continue
+        assert rel_l2(o.grad(name), m.grad(name)) < 1e-4, name
+
+
+def _mid_case(layers=3, lengths=(300, 200, 129, 64, 17), seed=0, std=0.02):
+    mc = mid_config(layers=layers)
+    o = oracle.OracleModel(mc)
+    params = random_params(o.shapes, seed, std=std)
+    rng = np.random.default_rng(seed + 1)
+    batch = mixed_batch(rng, list(lengths), mc.encoder.vocab_size)
+    return mc, o, params, batch
+
+
+def test_modernbert_base_width_gradients_match_the_oracle(ctx):
+    """d = 768, 12 heads × 64, GeGLU 1152, 3 layers (global θ 160000, then sliding ±64 θ 10000),
+    5 ragged segments (longer and shorter than the window), head dropout 0.1 in training mode.
+
+    The head's ReLU makes the gradient discontinuous: a pre-activation within fp32 rounding of zero
+    can flip between any two fp32 implementations. So each tensor is held to the exact (fp64 oracle)
+    result at max(1e-4, 4 × the error of the reference-faithful fp32 oracle itself)."""
+    from laya_amd.model import TrainableDecisionModel
+    print("model: d=768, 3 layers (global, sliding, sliding), 5 ragged segments", flush=True)
+    mc, o, params, batch = _mid_case()
+    o64 = oracle.OracleModel(mc, double=True)
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    m.head_dropout = 0.1
+    rng = np.random.default_rng(7)
+    dlogits = rng.standard_normal(batch.n_markers).astype(np.float32)
+    for ref in (o, o64):
+        ref.set_params(params)
+        ref.set_head_dropout(0.1)
+        ref.forward(batch, training=True, keep_tape=True, seed=99)
+        ref.backward(dlogits)
+    lg = m.forward(batch, training=True, seed=99)
+    assert rel_l2(o64.forward(batch, training=True, keep_tape=False, seed=99), lg) < 1e-5
+    m.backward(dlogits)
+    worst = 0.0
+    for name in m.names:
+        if name == "temperature" or name.startswith("act_head"):
+            continue
+        exact = o64.grad(name)
+        bar = max(1e-4, 4 * rel_l2(exact, o.grad(name)))
+        r = rel_l2(exact, m.grad(name))
+        worst = max(worst, r)
+        assert r < bar, (name, r, bar)
+    print(f"worst relative L2 vs fp64 over {len(m.names)} tensors: {worst:.2e}", flush=True)
+
+
+def test_full_train_step_matches_the_oracle(ctx):
+    """fwd → soft-CE gradient → bwd → clip → AdamW (Trainer.cs:131-144), then the updated weights."""
+    from laya_amd.model import TrainableDecisionModel
+    mc, o, params, batch = _mid_case(layers=2, lengths=(150, 90, 33))
+    o.set_params(params)
+    o.set_trainable_encoder_layers(None)
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    rng = np.random.default_rng(3)
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+    seed, lr = 5, 3e-3
+    loss_gpu = m.train_step(batch, targets, seed, loss_scale=float(batch.n_items), max_norm=1.0, lr_encoder=lr,
+                            lr_head=lr, want_loss=True)
+    logits = o.forward(batch, training=True, keep_tape=True, seed=seed).astype(np.float32)
+    ce, g = oracle.cross_entropy(batch.n_options, logits, targets, 1.0, float(batch.n_items))
+    assert abs(loss_gpu - ce) < 1e-4 * max(1.0, abs(ce))
+    o.backward(g)
+    o.clip(1.0)
+    o.adamw(lr, lr)
+    for name in m.names:
+        if name == "scorer.3.bias":
+            # Σ over an item's options of the soft-CE gradient is exactly 0, so this bias's gradient is
+            # rounding noise in both implementations and Adam's first step normalises it to ±lr.
+            continue
+        delta_o = o.param(name) - params[name]
+        delta_g = m.param(name).astype(np.float64) - params[name]
+        if np.linalg.norm(delta_o) == 0:
+            assert np.linalg.norm(delta_g) == 0, name
+            continue
+        # Step 1 of Adam moves each weight by ≈ ±lr·sign(g), so a gradient within fp32 noise of zero may
+        # flip; require agreement on all but a vanishing fraction of elements.
+        flipped = np.mean(np.abs(delta_o - delta_g) > 0.5 * lr)
+        assert flipped < 1e-3, (name, flipped)
+        assert rel_l2(delta_o, delta_g) < 0.05, name
+    # The step cleared the gradients.
+    assert not np.any(m.grad("scorer.1.weight"))
+
+
+def test_gradients_are_bitwise_deterministic(ctx):
+    from laya_amd.model import TrainableDecisionModel
+    mc, o, params, batch = _mid_case(layers=2, lengths=(256, 100))
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    d = np.random.default_rng(1).standard_normal(batch.n_markers).astype(np.float32)
+    runs = []
+    for _ in range(2):
+        m.zero_gradients()
+        m.forward(batch, training=True, seed=4)
+        m.backward(d)
+        runs.append({n: m.grad(n) for n in ("encoder.layers.0.attn.Wqkv.weight", "encoder.embeddings.norm.weight",
+                                             "encoder.embeddings.tok_embeddings.weight", "type_emb.weight")})
+    for n in runs[0]:
+        np.testing.assert_array_equal(runs[0][n], runs[1][n])
+
+
+def test_out_of_vocabulary_token_is_rejected_before_any_math(ctx):
+    from laya_amd._native import LayaOutOfRangeError
+    from laya_amd.batch import Batch
+    from laya_amd.model import TrainableDecisionModel
+    m = TrainableDecisionModel.from_directory(TINY, ctx)
+    bad = Batch(lengths=np.array([3], np.int32), tokens=np.array([1, 97, 2], np.int32),
+                n_options=np.array([1], np.int32), markers=np.array([0], np.int32), qtypes=np.array([0], np.int32))
+    with pytest.raises(LayaOutOfRangeError):
+        m.forward(bad)

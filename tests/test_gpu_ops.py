@@ -1,0 +1,262 @@
+"""Op-level parity of the HIP kernels against the oracle, through the C-ABI.
+
+Floating-point ops are compared with the fp64 oracle by relative L2 (fp32 bar 1e-4, the targets
+here are tighter); integer work (dropout masks, row gathers, scatter order) is compared bit-exactly.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from fixtures import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+laya = pytest.importorskip("laya_amd.ops")
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from laya_amd.device import Context
+    print("GPU op tests: creating context on device 0", flush=True)
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def dev(ctx, a):
+    from laya_amd.device import DeviceArray
+    return DeviceArray.from_numpy(ctx, np.asarray(a))
+
+
+def param(ctx, name, a, trainable=True):
+    return laya.Parameter(ctx, name, np.asarray(a, np.float32), trainable)
+
+
+@pytest.mark.parametrize("rows,inn,out", [(37, 96, 130), (300, 128, 384), (1000, 768, 2304), (5, 768, 1),
+                                          (2048, 1152, 768)])
+def test_linear_forward_and_backward(ctx, rows, inn, out):
+    print(f"linear rows={rows} in={inn} out={out}", flush=True)
+    rng = np.random.default_rng(rows + inn + out)
+    x = rng.standard_normal((rows, inn)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+    b = rng.standard_normal(out).astype(np.float32)
+    res = rng.standard_normal((rows, out)).astype(np.float32)
+    dy = rng.standard_normal((rows, out)).astype(np.float32)
+    w, bias = param(ctx, "w", W), param(ctx, "b", b)
+    dx_, y_ = dev(ctx, np.zeros((rows, inn), np.float32)), dev(ctx, np.zeros((rows, out), np.float32))
+    xd, rd, dyd = dev(ctx, x), dev(ctx, res), dev(ctx, dy)
+    laya.linear(w, bias, xd, rows, y_, residual=rd)
+    y_ref = oracle.linear(x, W, b, double=True) + res
+    assert rel_l2(y_ref, y_.numpy()) < 1e-6
+    # Accumulation: two backward calls add twice into dW/db; dx is overwritten.
+    laya.linear_backward(w, bias, xd, dyd, rows, dx_)
+    laya.linear_backward(w, bias, xd, dyd, rows, dx_)
+    dW = np.zeros((out, inn)); db = np.zeros(out)
+    dx_ref = oracle.linear_backward(x, dy, W, True, dW, db, double=True)
+    assert rel_l2(dx_ref, dx_.numpy()) < 1e-6
+    assert rel_l2(2 * dW, w.gradient.numpy()) < 1e-6
+    assert rel_l2(2 * db, bias.gradient.numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("rows,n,with_bias,saved", [(33, 128, False, True), (513, 768, True, True),
+                                                    (200, 768, False, False), (7, 1024, True, False)])
+def test_layernorm_forward_and_backward(ctx, rows, n, with_bias, saved):
+    print(f"layernorm rows={rows} n={n}", flush=True)
+    rng = np.random.default_rng(rows * n)
+    x = (2 + 3 * rng.standard_normal((rows, n))).astype(np.float32)
+    g = (1 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    bb = rng.standard_normal(n).astype(np.float32) if with_bias else None
+    dy = rng.standard_normal((rows, n)).astype(np.float32)
+    dx0 = rng.standard_normal((rows, n)).astype(np.float32)
+    w = param(ctx, "g", g)
+    bias = param(ctx, "b", bb) if with_bias else None
+    xd, yd = dev(ctx, x), dev(ctx, np.zeros_like(x))
+    mean, rstd = dev(ctx, np.zeros(rows, np.float32)), dev(ctx, np.zeros(rows, np.float32))
+    laya.layer_norm(xd, rows, n, w, bias, 1e-5, yd, mean, rstd)
+    assert rel_l2(oracle.layernorm(x, g, bb, 1e-5, double=True), yd.numpy()) < 1e-6
+    dxd = dev(ctx, dx0)
+    laya.layer_norm_backward(xd, rows, n, w, bias, 1e-5, dev(ctx, dy), dxd, mean if saved else None,
+                             rstd if saved else None)
+    dx_ref = dx0.astype(np.float64).copy()
+    dg = np.zeros(n)
+    dbeta = np.zeros(n) if with_bias else None
+    oracle.layernorm_backward(x, g, 1e-5, dy, dx_ref, dg, dbeta, double=True)
+    assert rel_l2(dx_ref, dxd.numpy()) < 1e-5
+    assert rel_l2(dg, w.gradient.numpy()) < 1e-5
+    if with_bias:
+        assert rel_l2(dbeta, bias.gradient.numpy()) < 1e-5
+
+
+def test_gelu_and_geglu(ctx):
+    rng = np.random.default_rng(3)
+    rows, inter = 129, 1152
+    wide = (2 * rng.standard_normal((rows, 2 * inter))).astype(np.float32)
+    dact = rng.standard_normal((rows, inter)).astype(np.float32)
+    wd, ad, dwd = dev(ctx, wide), dev(ctx, np.zeros((rows, inter), np.float32)), dev(ctx, np.zeros_like(wide))
+    laya.geglu(ctx, wd, rows, inter, ad)
+    assert rel_l2(oracle.geglu(wide, double=True), ad.numpy()) < 1e-6
+    laya.geglu_backward(ctx, wd, dev(ctx, dact), rows, inter, dwd)
+    assert rel_l2(oracle.geglu_backward(wide, dact, double=True), dwd.numpy()) < 1e-6
+    u = (3 * rng.standard_normal(1000)).astype(np.float32)
+    g = rng.standard_normal(1000).astype(np.float32)
+    gd = dev(ctx, g)
+    laya.gelu_backward(ctx, dev(ctx, u), gd)
+    assert rel_l2(oracle.gelu_backward(u, g, double=True), gd.numpy()) < 1e-6
+    yd = dev(ctx, u)
+    laya.gelu(ctx, yd)
+    assert rel_l2(oracle.gelu(u, double=True), yd.numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("p,seed", [(0.1, 12345), (0.3, 2 ** 63 + 17), (0.5, 0)])
+def test_dropout_is_bit_exact(ctx, p, seed):
+    rng = np.random.default_rng(1)
+    v = rng.standard_normal(100_003).astype(np.float32)
+    d = dev(ctx, v)
+    laya.dropout(ctx, d, v.size, p, seed)
+    got = d.numpy()
+    ref = oracle.dropout(v, p, seed)
+    np.testing.assert_array_equal(got == 0, ref == 0)
+    np.testing.assert_array_equal(got, ref)
+    assert laya.uniform(seed, 7) == oracle.uniform(seed, 7)
+    assert laya.mix(seed, 9) == oracle.mix(seed, 9)
+
+
+ATTENTION_CASES = [
+    # (head_dim, heads, lengths, half_window, theta, dropout)
+    (32, 4, [21, 13, 9], 4, 160000.0, 0.0),
+    (64, 12, [300, 129, 64, 1, 200], 64, 10000.0, 0.0),
+    (64, 12, [300, 129, 64, 1, 200], -1, 160000.0, 0.0),
+    (64, 2, [77, 5, 130], -1, 0.0, 0.1),
+    (64, 12, [512, 400], 64, 10000.0, 0.0),
+    (32, 2, [40, 200], 8, 10000.0, 0.3),
+]
+
+
+@pytest.mark.parametrize("hd,heads,lengths,hw,theta,p", ATTENTION_CASES)
+def test_attention_forward_and_backward(ctx, hd, heads, lengths, hw, theta, p):
+    print(f"attention hd={hd} heads={heads} lengths={lengths} hw={hw} theta={theta} p={p}", flush=True)
+    rng = np.random.default_rng(hd * 1000 + sum(lengths))
+    hidden = hd * heads
+    T = sum(lengths)
+    qkv = rng.standard_normal((T, 3 * hidden)).astype(np.float32)
+    dctx = rng.standard_normal((T, hidden)).astype(np.float32)
+    scale = laya.default_scale(hd)
+    seed = 987654321
+    segs = laya.Segments(ctx, lengths)
+    rot = laya.Rotary(ctx, hd, theta, max(lengths)) if theta > 0 else None
+    shape = laya.AttentionShape(hidden, heads, scale, hw, rot, p, seed)
+    qd = dev(ctx, qkv)
+    cd = dev(ctx, np.zeros((T, hidden), np.float32))
+    lse = dev(ctx, np.zeros(T * heads, np.float32))
+    laya.attention_forward(qd, segs, shape, cd, lse)
+    ref = oracle.attention_forward(qkv, lengths, heads, scale, hw, theta, p, seed, double=True)
+    assert rel_l2(ref, cd.numpy()) < 1e-5
+    dq = dev(ctx, np.zeros_like(qkv))
+    laya.attention_backward(qd, segs, shape, cd, lse, dev(ctx, dctx), dq)
+    dref = oracle.attention_backward(qkv, dctx, lengths, heads, scale, hw, theta, p, seed, double=True)
+    got = dq.numpy()
+    for part, sl in (("q", slice(0, hidden)), ("k", slice(hidden, 2 * hidden)), ("v", slice(2 * hidden, None))):
+        assert rel_l2(dref[:, sl], got[:, sl]) < 1e-5, part
+
+
+def test_attention_is_deterministic(ctx):
+    rng = np.random.default_rng(5)
+    lengths, heads, hd = [384, 100], 12, 64
+    hidden, T = heads * hd, 484
+    qkv = rng.standard_normal((T, 3 * hidden)).astype(np.float32)
+    dctx = rng.standard_normal((T, hidden)).astype(np.float32)
+    segs = laya.Segments(ctx, lengths)
+    rot = laya.Rotary(ctx, hd, 160000.0, 512)
+    shape = laya.AttentionShape(hidden, heads, laya.default_scale(hd), -1, rot, 0.0, 0)
+    outs = []
+    for _ in range(2):
+        qd, cd = dev(ctx, qkv), dev(ctx, np.zeros((T, hidden), np.float32))
+        lse, dq = dev(ctx, np.zeros(T * heads, np.float32)), dev(ctx, np.zeros_like(qkv))
+        laya.attention_forward(qd, segs, shape, cd, lse)
+        laya.attention_backward(qd, segs, shape, cd, lse, dev(ctx, dctx), dq)
+        outs.append((cd.numpy(), dq.numpy()))
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+
+
+def test_embedding_scatter_is_in_token_order(ctx):
+    rng = np.random.default_rng(11)
+    vocab, hidden, n = 500, 64, 4000
+    ranks = np.arange(1, vocab + 1) ** -1.1
+    ids = rng.choice(vocab, size=n, p=ranks / ranks.sum()).astype(np.int32)
+    d = rng.standard_normal((n, hidden)).astype(np.float32)
+    g0 = rng.standard_normal((vocab, hidden)).astype(np.float32)
+    gd = dev(ctx, g0)
+    laya.embedding_backward(ctx, ids, dev(ctx, d), hidden, gd, vocab)
+    ref = g0.copy()
+    for t in range(n):  # serial, token order (TrainableDecisionModel.cs:544-547)
+        ref[ids[t]] += d[t]
+    np.testing.assert_array_equal(ref, gd.numpy())
+
+
+def test_embedding_plan_rejects_out_of_vocabulary_ids():
+    from laya_amd._native import LayaOutOfRangeError
+    with pytest.raises(LayaOutOfRangeError):
+        laya.embedding_plan(np.array([1, 2, 97], np.int32), 97)
+
+
+def test_row_gather_and_scatter(ctx):
+    rng = np.random.default_rng(2)
+    src = rng.standard_normal((50, 33)).astype(np.float32)
+    rows = np.array([3, 0, 0, 49, 3, 7], np.int32)
+    out = dev(ctx, np.zeros((6, 33), np.float32))
+    laya.gather_rows(ctx, dev(ctx, src), dev(ctx, rows), 6, 33, out)
+    np.testing.assert_array_equal(out.numpy(), src[rows])
+    dst0 = rng.standard_normal((50, 33)).astype(np.float32)
+    dd = dev(ctx, dst0)
+    add = rng.standard_normal((6, 33)).astype(np.float32)
+    laya.scatter_add_rows(ctx, dev(ctx, add), dev(ctx, rows), 6, 33, dd)
+    ref = dst0.copy()
+    for r in range(6):
+        ref[rows[r]] += add[r]
+    np.testing.assert_array_equal(ref, dd.numpy())
+
+
+def test_softmax_cross_entropy_gradient(ctx):
+    rng = np.random.default_rng(4)
+    ks = np.array([8, 4, 2, 5], np.int32)
+    logits = rng.standard_normal(ks.sum()).astype(np.float32)
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in ks])
+    off = np.concatenate([[0], np.cumsum(ks)]).astype(np.int32)
+    g = dev(ctx, np.zeros_like(logits))
+    loss = dev(ctx, np.zeros(1, np.float32))
+    laya.softmax_ce_backward(ctx, dev(ctx, logits), dev(ctx, targets), dev(ctx, off), len(ks), 1.0, 4.0, g, loss)
+    ce, gref = oracle.cross_entropy(ks, logits, targets, 1.0, 4.0)
+    np.testing.assert_allclose(g.numpy(), gref, rtol=1e-5, atol=1e-7)
+    assert abs(loss.numpy()[0] - ce) < 1e-5
+
+
+def test_adamw_and_clip_match_the_oracle(ctx):
+    import ctypes
+    from laya_amd._native import check, lib
+    rng = np.random.default_rng(9)
+    n = 10_000
+    p = rng.standard_normal(n).astype(np.float32)
+    g = (3 * rng.standard_normal(n)).astype(np.float32)
+    pd, gd = dev(ctx, p), dev(ctx, g)
+    md, vd = dev(ctx, np.zeros(n, np.float32)), dev(ctx, np.zeros(n, np.float32))
+    norm, coef = dev(ctx, np.zeros(2, np.float32)), dev(ctx, np.zeros(1, np.float32))
+    check(lib().laya_grad_norm(ctx.handle, gd.ptr, n, 1.0, norm.ptr, coef.ptr))
+    nrm = norm.numpy().view(np.float64)[0]
+    assert abs(nrm - np.sqrt((g.astype(np.float64) ** 2).sum())) < 1e-9 * nrm
+    gc = g.copy()
+    oracle.clip([gc], 1.0)
+    begin = (ctypes.c_size_t * 2)(0, 6000)
+    end = (ctypes.c_size_t * 2)(6000, n)
+    lr = (ctypes.c_double * 2)(1e-3, 1e-4)
+    pr, mr, vr = p.copy(), np.zeros(n, np.float32), np.zeros(n, np.float32)
+    for step in (1, 2, 3):
+        check(lib().laya_adamw(ctx.handle, pd.ptr, gd.ptr, md.ptr, vd.ptr, 2, begin, end, lr, 0.9, 0.999, 1e-8, 0.01,
+                               step, coef.ptr, 0))
+        oracle.adamw_tensor(pr[:6000], gc[:6000], mr[:6000], vr[:6000], 1e-3, step)
+        a, b, c = pr[6000:].copy(), mr[6000:].copy(), vr[6000:].copy()
+        oracle.adamw_tensor(a, gc[6000:].copy(), b, c, 1e-4, step)
+        pr[6000:], mr[6000:], vr[6000:] = a, b, c
+    assert rel_l2(pr, pd.numpy()) < 1e-6
+    assert rel_l2(mr, md.numpy()) < 1e-6
+    assert rel_l2(vr, vd.numpy()) < 1e-6
