@@ -32,7 +32,8 @@ sys.path.insert(0, ROOT)
 METRIC = "fine-tune tokens/sec (fwd+bwd+AdamW), 1 MI355X; bwd MFMA util % & HBM GB/s"
 PEAK_FP32_MFMA = 157.3e12
 PEAK_HBM = 8.0e12
-MFMA_KERNELS = ("gemm_nt", "gemm_nn", "gemm_tn", "attention_fwd", "attention_bwd_dkv", "attention_bwd_dq")
+MFMA_KERNELS = ("gemm_nt", "gemm_nn", "gemm_tn", "gemm_bwd_pair", "attention_fwd", "attention_bwd_dkv",
+                "attention_bwd_dq")
 
 
 def make_batch(rng, batch=32, seq=512, vocab=50368, pad_max=0.3):
@@ -148,7 +149,7 @@ def main():
             roofline = {"bound": "hbm", "kernel": name, "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
                         "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
                         "avg_launch_ms": round(per_launch_s * 1e3, 4), "launches": k["launches"]}
-        bwd = [prof[n] for n in ("gemm_nn", "gemm_tn") if n in prof]
+        bwd = [prof[n] for n in ("gemm_nn", "gemm_tn", "gemm_bwd_pair") if n in prof]
         if bwd:
             f = sum(x["flops"] for x in bwd)
             ms = sum(x["ms"] for x in bwd)

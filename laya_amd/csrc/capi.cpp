@@ -325,11 +325,13 @@ int laya_linear_bwd(laya_ctx* ctx, const float* x, const float* dy, int rows, in
         require_ctx(ctx);
         LAYA_REQUIRE(rows >= 0 && in > 0 && out > 0, "linear_bwd: bad size");
         LAYA_REQUIRE(dy && W, "linear_bwd: null tensor");
-        if (dx) gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in);
-        if (dW) {
-            LAYA_REQUIRE(x, "linear_bwd: dW needs x");
+        LAYA_REQUIRE(!dW || x, "linear_bwd: dW needs x");
+        if (dx && dW)
+            gemm_backward_pair(ctx, rows, in, out, dy, W, x, dx, nullptr, dW);
+        else if (dx)
+            gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in);
+        else if (dW)
             gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
-        }
         if (db) column_sum_add(ctx, dy, rows, out, db);
     });
 }

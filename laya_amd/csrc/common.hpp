@@ -180,6 +180,11 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
           const float* B, long ldb, float* C, long ldc, const float* bias = nullptr, const float* R = nullptr,
           long ldr = 0);
 
+// The two products of Ops.LinearBackward in one launch: dx = dy·W (+ dx_residual) and dW += dyᵀ·x,
+// for dy [rows, out], W [out, in], x [rows, in]; split-K partials of dW reduced in a fixed order.
+void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
+                        float* dx, const float* dx_residual, float* dW);
+
 // Σ over rows of a [rows, n] matrix added into out[n], deterministic (bias gradients).
 void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out);
 

@@ -87,15 +87,17 @@ __device__ __forceinline__ f32x4 read_frag(const float* lds, int mn, int k) {
     return f32x4{lds[k * MNPAD + mn], lds[(k + 1) * MNPAD + mn], lds[(k + 2) * MNPAD + mn], lds[(k + 3) * MNPAD + mn]};
 }
 
-template <bool AK, bool BKC>
-__global__ __launch_bounds__(THREADS, 2) void gemm_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
-
-    // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs, so give each XCD a contiguous
-    // run of logical tiles (n fastest); tiles sharing an A row-panel then share one XCD's L2.
+// XCD-aware order: workgroups are dealt round-robin to the 8 XCDs, so give each XCD a contiguous run
+// of logical tiles (n fastest); tiles sharing an A row-panel then share one XCD's L2.
+__device__ __forceinline__ int xcd_logical_block() {
     const int nblocks = gridDim.x, bid = blockIdx.x;
     const int xcd = bid & 7, local = bid >> 3, per = nblocks >> 3, rem = nblocks & 7;
-    const int logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
+    return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
+}
+
+// One 128×128 output tile (or one split-K slice of it) of C = op(A)·op(B).
+template <bool AK, bool BKC>
+__device__ __forceinline__ void gemm_tile(const GemmParams& p, int logical, float (*smem)[2][STAGE]) {
     const int tiles = p.tiles_m * p.tiles_n;
     const int split = logical / tiles, t = logical - split * tiles;
     const int tile_m = t / p.tiles_n, tile_n = t - tile_m * p.tiles_n;
@@ -181,6 +183,24 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_kernel(GemmParams p) {
     }
 }
 
+template <bool AK, bool BKC>
+__global__ __launch_bounds__(THREADS, 2) void gemm_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
+    gemm_tile<AK, BKC>(p, xcd_logical_block(), smem);
+}
+
+// dX = dY·W (NN) and dW += dYᵀ·X (TN, split-K partials) in one grid: the first `blocks0` logical
+// blocks are dX tiles, the rest dW slices. The two products are independent, and one grid lets their
+// tiles fill the CUs together instead of each leaving a partial last wave.
+__global__ __launch_bounds__(THREADS, 2) void gemm_pair_kernel(GemmParams nn, GemmParams tn, int blocks0) {
+    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
+    const int logical = xcd_logical_block();
+    if (logical < blocks0)
+        gemm_tile<true, false>(nn, logical, smem);
+    else
+        gemm_tile<false, false>(tn, logical - blocks0, smem);
+}
+
 // C[m, n] += Σ_s P[s][m][n], s in order.
 __global__ void splitk_reduce_kernel(const float* __restrict__ P, int splits, int M, int N, float* C, long ldc) {
     const long total = (long)M * N;
@@ -226,12 +246,9 @@ template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int
 
 inline bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
-}  // namespace
-
-void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
-          const float* B, long ldb, float* C, long ldc, const float* bias, const float* R, long ldr) {
+GemmParams make_params(int M, int N, int K, const float* A, long lda, const float* B, long ldb, float* C, long ldc,
+                       const float* bias, const float* R, long ldr) {
     LAYA_REQUIRE(M >= 0 && N >= 0 && K >= 0, "gemm: negative size");
-    if (M == 0 || N == 0) return;
     GemmParams p{};
     p.A = A;
     p.B = B;
@@ -249,33 +266,60 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
     p.tiles_n = (N + BN - 1) / BN;
     p.vec_a = (lda % 4 == 0) && aligned16(A);
     p.vec_b = (ldb % 4 == 0) && aligned16(B);
-    const int tiles = p.tiles_m * p.tiles_n;
+    p.splits = 1;
+    p.k_per_split = std::max(BK, (K + BK - 1) / BK * BK);
+    return p;
+}
 
-    int splits = 1;
+// Splits K into `splits` slices of a multiple of BK; returns the realised split count.
+int set_splits(GemmParams& p, int splits) {
+    int kps = (p.K + splits - 1) / splits;
+    kps = std::max(BK, (kps + BK - 1) / BK * BK);
+    p.k_per_split = kps;
+    p.splits = std::max(1, (p.K + kps - 1) / kps);
+    return p.splits;
+}
+
+// An accumulating product: one writer per element (mode 1), or split-K partials into workspace slot 0
+// (mode 2) to be reduced by finish_accumulate.
+float* prepare_accumulate(laya_ctx* ctx, GemmParams& p) {
+    if (p.splits == 1) {
+        p.mode = 1;
+        return nullptr;
+    }
+    p.mode = 2;
+    float* partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)p.splits * p.M * p.N));
+    float* out = p.C;
+    p.C = partial;
+    return out;
+}
+
+void finish_accumulate(laya_ctx* ctx, const GemmParams& p, float* out, long ldc) {
+    if (p.mode != 2) return;
+    const long total = (long)p.M * p.N;
+    ProfileScope scope(ctx, "gemm_splitk_reduce", 0.0, 4.0 * total * (p.splits + 2));
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
+                       p.splits, p.M, p.N, out, ldc);
+    check_launch("splitk_reduce_kernel");
+}
+
+}  // namespace
+
+void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
+          const float* B, long ldb, float* C, long ldc, const float* bias, const float* R, long ldr) {
+    if (M == 0 || N == 0) return;
+    GemmParams p = make_params(M, N, K, A, lda, B, ldb, C, ldc, bias, R, ldr);
+    const int tiles = p.tiles_m * p.tiles_n;
+    float* out = C;
     if (ep == GemmEpilogue::Accumulate) {
         // Fill the chip: aim for ≥ 2 workgroups per CU, but keep ≥ 512 of K per split.
         const int want = (2 * ctx->cu_count + tiles - 1) / tiles;
-        const int max_by_k = std::max(1, K / 512);
-        splits = std::max(1, std::min(want, max_by_k));
-    }
-    int kps = (K + splits - 1) / splits;
-    kps = (kps + BK - 1) / BK * BK;
-    if (kps == 0) kps = BK;
-    splits = std::max(1, (K + kps - 1) / kps);
-    p.splits = splits;
-    p.k_per_split = kps;
-
-    float* partial = nullptr;
-    if (ep == GemmEpilogue::Store) {
-        p.mode = 0;
-    } else if (splits == 1) {
-        p.mode = 1;
+        set_splits(p, std::max(1, std::min(want, std::max(1, K / 512))));
+        out = prepare_accumulate(ctx, p);
     } else {
-        p.mode = 2;
-        partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)splits * M * N));
-        p.C = partial;
+        p.mode = 0;
     }
-    const int blocks = tiles * splits;
+    const int blocks = tiles * p.splits;
     {
         static const char* names[3] = {"gemm_nt", "gemm_nn", "gemm_tn"};
         ProfileScope scope(ctx, names[(int)layout], 2.0 * M * N * (double)K, 0.0);
@@ -285,13 +329,47 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
             case GemmLayout::TN: launch<false, false>(ctx, p, blocks); break;
         }
     }
-    if (p.mode == 2) {
-        const long total = (long)M * N;
-        ProfileScope scope(ctx, "gemm_splitk_reduce", 0.0, 4.0 * total * (splits + 2));
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream,
-                           partial, splits, M, N, C, ldc);
-        check_launch("splitk_reduce_kernel");
+    finish_accumulate(ctx, p, out, ldc);
+}
+
+void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
+                        float* dx, const float* dx_residual, float* dW) {
+    if (rows == 0) return;
+    // dx[rows, in] = dy[rows, out] · W[out, in]       (NN, K = out)
+    GemmParams nn = make_params(rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual, in);
+    nn.mode = 0;
+    // dW[out, in] += dy[rows, out]ᵀ · x[rows, in]     (TN, K = rows)
+    GemmParams tn = make_params(out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr, 0);
+    const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
+    // Choose the dW split so its slices are as long as a dX tile's K loop, then minimise the rounds of
+    // 2-blocks-per-CU the combined grid needs times the longest block.
+    const long slots = 2L * ctx->cu_count;
+    const long knn = std::max(BK, (out + BK - 1) / BK * BK);
+    int best_s = 1;
+    double best = 1e300;
+    for (int s = 1; s <= 64; ++s) {
+        GemmParams t = tn;
+        const int real = set_splits(t, s);
+        if (real != s) continue;
+        const long total = n0 + (long)n1 * s;
+        // Rounds × the longest block's K, plus the split-K reduce traffic in the same K units (a round
+        // of two 128×128 blocks per CU costs ≈ 1.2e-7 s per unit of K; the reduce moves 4·out·in·s bytes).
+        const double est = (double)((total + slots - 1) / slots) * std::max<long>(knn, t.k_per_split) +
+                           6.8e-6 * s * (double)out * in;
+        if (est < best) {
+            best = est;
+            best_s = s;
+        }
     }
+    set_splits(tn, best_s);
+    float* dW_out = prepare_accumulate(ctx, tn);
+    const int blocks = n0 + n1 * tn.splits;
+    {
+        ProfileScope scope(ctx, "gemm_bwd_pair", 2.0 * 2.0 * rows * (double)in * out, 0.0);
+        hipLaunchKernelGGL(gemm_pair_kernel, dim3(blocks), dim3(THREADS), 0, ctx->stream, nn, tn, n0);
+        check_launch("gemm_pair_kernel");
+    }
+    finish_accumulate(ctx, tn, dW_out, in);
 }
 
 void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out) {

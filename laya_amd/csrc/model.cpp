@@ -445,10 +445,15 @@ void linear(laya_model* m, const float* x, int rows, int in, int wi, int bi, int
 // Ops.LinearBackward (Ops.cs:33-69): dx = dy·W (overwrite; + residual when given), dW += dyᵀ·x, db += Σ dy.
 void linear_backward(laya_model* m, const float* x, const float* dy, int rows, int in, int out, int wi, int bi,
                      float* dx, const float* dx_residual = nullptr) {
-    if (dx)
+    float* dW = m->Gt(wi);
+    if (dx && dW) {
+        gemm_backward_pair(m->ctx, rows, in, out, dy, m->W(wi), x, dx, dx_residual, dW);
+    } else if (dx) {
         gemm(m->ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, m->W(wi), in, dx, in, nullptr,
              dx_residual, in);
-    if (float* dW = m->Gt(wi)) gemm(m->ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
+    } else if (dW) {
+        gemm(m->ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
+    }
     if (float* db = m->Gt(bi)) column_sum_add(m->ctx, dy, rows, out, db);
 }
 
