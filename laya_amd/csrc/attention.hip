@@ -66,41 +66,72 @@ __device__ __forceinline__ bool in_window(int q, int key, int L, int hw) {
     return q < L && key >= 0 && key < L && (hw < 0 || (key - q <= hw && q - key <= hw));
 }
 
-// Loads `rows` rows [row0, row0 + rows) of one head's q, k or v slice into LDS with stride S,
-// applying RoPE (position = segment-local row) when `rope`; rows outside [0, L) become zeros.
+// A TILE-row slice of one head staged in registers between its global fetch and its LDS commit, so
+// the next tile's loads are in flight while the current tile is computed. Rows outside [0, L) are
+// zeros. With RoPE, each unit is a (d, d + D/2) float4 pair plus its cos/sin, rotated at commit.
+template <int D> struct RopeStage {
+    static constexpr int U = TILE * (D / 8) / THREADS;
+    f32x4 a[U], b[U], c[U], s[U];
+};
+template <int D> struct PlainStage {
+    static constexpr int U = TILE * (D / 4) / THREADS;
+    f32x4 v[U];
+};
+
+template <int D>
+__device__ __forceinline__ void fetch_rope(RopeStage<D>& st, const Params& p, const float* base, long stride, int L,
+                                           int row0, bool rope) {
+#pragma unroll
+    for (int i = 0; i < RopeStage<D>::U; ++i) {
+        const int u = threadIdx.x + i * THREADS;
+        const int r = u / (D / 8), j = (u % (D / 8)) * 4;
+        const int t = row0 + r;
+        const bool ok = t >= 0 && t < L;
+        const float* src = base + (long)(ok ? t : 0) * stride;
+        st.a[i] = ok ? ld4(src + j) : f32x4{0, 0, 0, 0};
+        st.b[i] = ok ? ld4(src + D / 2 + j) : f32x4{0, 0, 0, 0};
+        if (rope) {
+            st.c[i] = ok ? ld4(p.cos_t + (long)t * (D / 2) + j) : f32x4{1, 1, 1, 1};
+            st.s[i] = ok ? ld4(p.sin_t + (long)t * (D / 2) + j) : f32x4{0, 0, 0, 0};
+        }
+    }
+}
+
 template <int D, int S>
-__device__ __forceinline__ void load_rows(const Params& p, float* lds, int start, int L, int row0, int rows, int col,
-                                          bool rope) {
-    const long stride = 3L * p.hidden;
-    if (rope) {
-        constexpr int units_per_row = D / 8;
-        for (int u = threadIdx.x; u < rows * units_per_row; u += THREADS) {
-            const int r = u / units_per_row, j = (u - r * units_per_row) * 4;
-            const int t = row0 + r;
-            f32x4 a = {0, 0, 0, 0}, b = {0, 0, 0, 0};
-            if (t >= 0 && t < L) {
-                const float* src = p.qkv + (long)(start + t) * stride + col;
-                a = ld4(src + j);
-                b = ld4(src + D / 2 + j);
-                const f32x4 c = ld4(p.cos_t + (long)t * (D / 2) + j);
-                const f32x4 s = ld4(p.sin_t + (long)t * (D / 2) + j);
-                const f32x4 na = a * c - b * s;
-                const f32x4 nb = b * c + a * s;
-                a = na;
-                b = nb;
-            }
-            st4(lds + r * S + j, a);
-            st4(lds + r * S + D / 2 + j, b);
+__device__ __forceinline__ void commit_rope(const RopeStage<D>& st, float* lds, bool rope) {
+#pragma unroll
+    for (int i = 0; i < RopeStage<D>::U; ++i) {
+        const int u = threadIdx.x + i * THREADS;
+        const int r = u / (D / 8), j = (u % (D / 8)) * 4;
+        f32x4 a = st.a[i], b = st.b[i];
+        if (rope) {
+            const f32x4 na = a * st.c[i] - b * st.s[i];
+            const f32x4 nb = b * st.c[i] + a * st.s[i];
+            a = na;
+            b = nb;
         }
-    } else {
-        constexpr int units_per_row = D / 4;
-        for (int u = threadIdx.x; u < rows * units_per_row; u += THREADS) {
-            const int r = u / units_per_row, j = (u - r * units_per_row) * 4;
-            const int t = row0 + r;
-            f32x4 a = {0, 0, 0, 0};
-            if (t >= 0 && t < L) a = ld4(p.qkv + (long)(start + t) * stride + col + j);
-            st4(lds + r * S + j, a);
-        }
+        st4(lds + r * S + j, a);
+        st4(lds + r * S + D / 2 + j, b);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void fetch_plain(PlainStage<D>& st, const float* base, long stride, int L, int row0) {
+#pragma unroll
+    for (int i = 0; i < PlainStage<D>::U; ++i) {
+        const int u = threadIdx.x + i * THREADS;
+        const int r = u / (D / 4), j = (u % (D / 4)) * 4;
+        const int t = row0 + r;
+        st.v[i] = (t >= 0 && t < L) ? ld4(base + (long)t * stride + j) : f32x4{0, 0, 0, 0};
+    }
+}
+
+template <int D, int S>
+__device__ __forceinline__ void commit_plain(const PlainStage<D>& st, float* lds) {
+#pragma unroll
+    for (int i = 0; i < PlainStage<D>::U; ++i) {
+        const int u = threadIdx.x + i * THREADS;
+        st4(lds + (u / (D / 4)) * S + (u % (D / 4)) * 4, st.v[i]);
     }
 }
 
@@ -191,11 +222,21 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
     for (int dt = 0; dt < S::ND; ++dt) o[dt] = f32x16{};
     float m = -1e30f, l = 0.0f;
 
+    const float* kbase = p.qkv + (long)start * stride + kcol;
+    const float* vbase = p.qkv + (long)start * stride + vcol;
+    RopeStage<D> kst;
+    PlainStage<D> vst;
+    fetch_rope<D>(kst, p, kbase, stride, L, kbeg, rope);
+    fetch_plain<D>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
         __syncthreads();
-        load_rows<D, S::KS>(p, Ks, start, L, kt0, TILE, kcol, rope);
-        load_rows<D, S::VS>(p, Vs, start, L, kt0, TILE, vcol, false);
+        commit_rope<D, S::KS>(kst, Ks, rope);
+        commit_plain<D, S::VS>(vst, Vs);
         __syncthreads();
+        if (kt0 + TILE < kend) {  // block-uniform: the next tile's loads overlap this tile's products
+            fetch_rope<D>(kst, p, kbase, stride, L, kt0 + TILE, rope);
+            fetch_plain<D>(vst, vbase, stride, L, kt0 + TILE);
+        }
 #pragma unroll
         for (int st = 0; st < TILE / 32; ++st) {
             const int kbs = kt0 + 32 * st;
@@ -313,23 +354,33 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
         dv[dt] = f32x16{};
     }
 
+    // Q rows (RoPE at commit), dO rows from dcontext [rows, hidden], and the per-row lse / dots,
+    // fetched one tile ahead of the products.
+    const float* qbase = p.qkv + (long)start * stride + qcol;
+    const float* obase = p.dcontext + (long)start * p.hidden + qcol;
+    RopeStage<D> qst;
+    PlainStage<D> ost;
+    float lse_r = 0.0f, dot_r = 0.0f;
+    auto fetch = [&](int t0) {
+        fetch_rope<D>(qst, p, qbase, stride, L, t0, rope);
+        fetch_plain<D>(ost, obase, p.hidden, L, t0);
+        const int t = t0 + (int)threadIdx.x;
+        if (threadIdx.x < TILE) {
+            lse_r = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
+            dot_r = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
+        }
+    };
+    fetch(qbeg);
     for (int qt0 = qbeg; qt0 < qend; qt0 += TILE) {
         __syncthreads();
-        load_rows<D, S::KS>(p, Qs, start, L, qt0, TILE, qcol, rope);
-        // dO rows come from dcontext [rows, hidden]; load them through the same helper layout.
-        for (int u = threadIdx.x; u < TILE * (D / 4); u += THREADS) {
-            const int r = u / (D / 4), j = (u - r * (D / 4)) * 4;
-            const int t = qt0 + r;
-            f32x4 a = {0, 0, 0, 0};
-            if (t < L) a = ld4(p.dcontext + (long)(start + t) * p.hidden + qcol + j);
-            st4(Os + r * S::VS + j, a);
-        }
-        for (int r = threadIdx.x; r < TILE; r += THREADS) {
-            const int t = qt0 + r;
-            lse_s[r] = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
-            dot_s[r] = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
+        commit_rope<D, S::KS>(qst, Qs, rope);
+        commit_plain<D, S::VS>(ost, Os);
+        if (threadIdx.x < TILE) {
+            lse_s[threadIdx.x] = lse_r;
+            dot_s[threadIdx.x] = dot_r;
         }
         __syncthreads();
+        if (qt0 + TILE < qend) fetch(qt0 + TILE);  // block-uniform
 #pragma unroll
         for (int st = 0; st < TILE / 32; ++st) {
             const int qbs = qt0 + 32 * st;
@@ -385,7 +436,7 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
 }
 
 template <int D>
-__global__ __launch_bounds__(THREADS) void attn_bwd_dq_kernel(Params p) {
+__global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
     using S = Shape<D>;
     __shared__ __attribute__((aligned(16))) float Ks[TILE * S::KS];
     __shared__ __attribute__((aligned(16))) float Vs[TILE * S::KS];
@@ -422,11 +473,21 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dq_kernel(Params p) {
 #pragma unroll
     for (int dt = 0; dt < S::ND; ++dt) dq[dt] = f32x16{};
 
+    const float* kbase = p.qkv + (long)start * stride + kcol;
+    const float* vbase = p.qkv + (long)start * stride + vcol;
+    RopeStage<D> kst;
+    PlainStage<D> vst;
+    fetch_rope<D>(kst, p, kbase, stride, L, kbeg, rope);
+    fetch_plain<D>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
         __syncthreads();
-        load_rows<D, S::KS>(p, Ks, start, L, kt0, TILE, kcol, rope);
-        load_rows<D, S::KS>(p, Vs, start, L, kt0, TILE, vcol, false);
+        commit_rope<D, S::KS>(kst, Ks, rope);
+        commit_plain<D, S::KS>(vst, Vs);
         __syncthreads();
+        if (kt0 + TILE < kend) {  // block-uniform
+            fetch_rope<D>(kst, p, kbase, stride, L, kt0 + TILE, rope);
+            fetch_plain<D>(vst, vbase, stride, L, kt0 + TILE);
+        }
 #pragma unroll
         for (int st = 0; st < TILE / 32; ++st) {
             const int kbs = kt0 + 32 * st;
