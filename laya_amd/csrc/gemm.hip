@@ -13,6 +13,15 @@
 // (k-contiguous rows read as b128 fragments; mn-contiguous rows read as 4 conflict-free b32),
 // double-buffered with a register prefetch of the next K tile. Split-K partials are reduced in a
 // fixed order, so results never depend on timing.
+//
+// Two kernel families. The main one is branch-free in its K loop: rows and columns past the matrix
+// edge are clamped to the last valid one (their products only reach outputs that are never stored),
+// and a ragged final K tile is peeled off the loop and zero-filled with selects. It needs float4
+// access (leading dimensions and the contiguous extent of each operand a multiple of 4, 16-byte
+// aligned bases, fewer than 2³¹ elements per operand). Every other shape takes the generic kernel,
+// which tests each element. Keeping each kernel to one loop and one store path matters: the same
+// loop in a kernel that also carries unused boundary code and runtime epilogue branches measured a
+// fifth slower on short-K products.
 #include "common.hpp"
 
 namespace laya {
@@ -26,6 +35,9 @@ constexpr int STAGE = BM * KPAD;  // ≥ BK * MNPAD
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Epilogue modes, fixed at compile time so each kernel carries only its own store path.
+enum : int { STORE = 0, ACCUMULATE = 1, PARTIAL = 2 };
+
 struct GemmParams {
     const float* A;
     const float* B;
@@ -35,38 +47,11 @@ struct GemmParams {
     long lda, ldb, ldc, ldr;
     int M, N, K;
     int tiles_m, tiles_n, splits, k_per_split;
-    int mode;  // 0 store, 1 accumulate in place (one writer per element), 2 split-K partial
+    int mode;  // STORE, ACCUMULATE in place (one writer per element), or PARTIAL split-K slices
     int vec_a, vec_b;
 };
 
-// Loads one 128×32 operand tile into 4 float4 registers per thread (zero outside the matrix).
-template <bool KCONTIG>
-__device__ __forceinline__ void load_tile(const float* __restrict__ src, long ld, int mn0, int MN, int k0, int kend,
-                                          bool vec, f32x4 (&reg)[4], int tid) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int idx = tid + THREADS * i;
-        if (KCONTIG) {
-            int mn = mn0 + (idx >> 3);
-            int k = k0 + ((idx & 7) << 2);
-            if (vec && mn < MN && k + 3 < kend) {
-                reg[i] = *reinterpret_cast<const f32x4*>(src + (long)mn * ld + k);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) reg[i][e] = (mn < MN && k + e < kend) ? src[(long)mn * ld + k + e] : 0.0f;
-            }
-        } else {
-            int k = k0 + (idx >> 5);
-            int mn = mn0 + ((idx & 31) << 2);
-            if (vec && k < kend && mn + 3 < MN) {
-                reg[i] = *reinterpret_cast<const f32x4*>(src + (long)k * ld + mn);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) reg[i][e] = (k < kend && mn + e < MN) ? src[(long)k * ld + mn + e] : 0.0f;
-            }
-        }
-    }
-}
+// ------------------------------------------------------------------------------ shared pieces
 
 template <bool KCONTIG>
 __device__ __forceinline__ void store_tile(float* lds, const f32x4 (&reg)[4], int tid) {
@@ -95,17 +80,253 @@ __device__ __forceinline__ int xcd_logical_block() {
     return (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
 }
 
-// One 128×128 output tile (or one split-K slice of it) of C = op(A)·op(B).
-template <bool AK, bool BKC>
-__device__ __forceinline__ void gemm_tile(const GemmParams& p, int logical, float (*smem)[2][STAGE]) {
-    const int tiles = p.tiles_m * p.tiles_n;
-    const int split = logical / tiles, t = logical - split * tiles;
-    const int tile_m = t / p.tiles_n, tile_n = t - tile_m * p.tiles_n;
-    const int m0 = tile_m * BM, n0 = tile_n * BN;
-    const int kb = split * p.k_per_split;
-    const int ke = min(p.K, kb + p.k_per_split);
-    const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
+// Where one logical block works: its output tile and its K range.
+struct TileCoord {
+    int split, t, m0, n0, kb, ke;
+};
 
+__device__ __forceinline__ TileCoord tile_coord(const GemmParams& p, int logical) {
+    TileCoord c;
+    const int tiles = p.tiles_m * p.tiles_n;
+    c.split = logical / tiles;
+    c.t = logical - c.split * tiles;
+    const int tile_m = c.t / p.tiles_n;
+    c.m0 = tile_m * BM;
+    c.n0 = (c.t - tile_m * p.tiles_n) * BN;
+    c.kb = c.split * p.k_per_split;
+    c.ke = min(p.K, c.kb + p.k_per_split);
+    return c;
+}
+
+// 64 MFMAs of one wave over one LDS stage (K = 32).
+template <bool AK, bool BKC>
+__device__ __forceinline__ void mma_stage(const float* As, const float* Bs, f32x16 (&acc)[2][2], int wm, int wn,
+                                          int lr, int kh) {
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 8) {
+        const int k = kk + kh;
+        f32x4 a0 = read_frag<AK>(As, wm * 64 + lr, k);
+        f32x4 a1 = read_frag<AK>(As, wm * 64 + 32 + lr, k);
+        f32x4 b0 = read_frag<BKC>(Bs, wn * 64 + lr, k);
+        f32x4 b1 = read_frag<BKC>(Bs, wn * 64 + 32 + lr, k);
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[cc], b0[cc], acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[cc], b1[cc], acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[cc], b0[cc], acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[cc], b1[cc], acc[1][1], 0, 0, 0);
+        }
+    }
+}
+
+// Writes the wave's 64×64 accumulators. Accumulator layout of a 32×32 tile: lane holds column
+// lane%32, rows 8(r/4) + 4(lane/32) + r%4, so every element sits at a fixed 32-bit offset from one
+// base pointer. GUARD drops elements outside the matrix; RES adds the residual R (STORE only).
+template <int MODE, bool RES, bool GUARD>
+__device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[2][2], int wm,
+                                          int wn, int lr, int kh) {
+    const int row0 = c.m0 + wm * 64 + kh, col0 = c.n0 + wn * 64 + lr;
+    const int ldo = MODE == PARTIAL ? p.N : (int)p.ldc;
+    float* base = (MODE == PARTIAL ? p.C + (long)c.split * p.M * p.N : p.C) + (long)row0 * ldo + col0;
+    float bj[2] = {0.0f, 0.0f};
+    if (MODE == STORE && p.bias) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (!GUARD || col0 + j * 32 < p.N) bj[j] = p.bias[col0 + j * 32];
+    }
+    const float* rbase = RES ? p.R + (long)row0 * p.ldr + col0 : nullptr;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
+                if (GUARD && (row0 + dr >= p.M || col0 + j * 32 >= p.N)) continue;
+                float* dst = base + dr * ldo + j * 32;
+                if (MODE == STORE) {
+                    float v = acc[i][j][r] + bj[j];
+                    if (RES) v += rbase[dr * (int)p.ldr + j * 32];
+                    *dst = v;
+                } else if (MODE == ACCUMULATE) {
+                    *dst += acc[i][j][r];
+                } else {
+                    *dst = acc[i][j][r];
+                }
+            }
+}
+
+// ------------------------------------------------------------------------------ main kernel
+
+// One thread's share of a 128×32 operand tile: four float4 loads at offsets fixed for the whole K loop
+// except for the K position. Rows (k-contiguous) or columns (mn-contiguous) past the edge are clamped.
+template <bool KCONTIG>
+struct Loader {
+    const float* src;
+    unsigned off[4];  // k-contiguous: row offsets + kq; mn-contiguous: column offset
+    unsigned ld;
+    int kq;           // k-contiguous: this thread's k within the tile; mn-contiguous: its first k row
+
+    __device__ __forceinline__ Loader(const float* s, long ldl, int mn0, int MN, int tid) : src(s), ld((unsigned)ldl) {
+        if (KCONTIG) {
+            kq = (tid & 7) << 2;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = min(mn0 + (tid >> 3) + 32 * i, MN - 1);
+                off[i] = (unsigned)row * ld + kq;
+            }
+        } else {
+            kq = tid >> 5;
+            const int col = min(mn0 + ((tid & 31) << 2), MN - 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) off[i] = (unsigned)col;
+        }
+    }
+
+    // A K tile that lies entirely inside [kb, ke).
+    __device__ __forceinline__ void full(int k0, f32x4 (&reg)[4]) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const unsigned o = KCONTIG ? off[i] + (unsigned)k0 : off[i] + (unsigned)(k0 + kq + 8 * i) * ld;
+            reg[i] = *reinterpret_cast<const f32x4*>(src + o);
+        }
+    }
+
+    // The ragged last K tile: positions at or past `kend` read an in-bounds neighbour and become 0.
+    __device__ __forceinline__ void tail(int k0, int kend, f32x4 (&reg)[4]) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (KCONTIG) {
+                const int k = k0 + kq;  // kend is a multiple of 4, so k < kend covers k..k+3
+                const f32x4 v = *reinterpret_cast<const f32x4*>(src + off[i] - kq + (unsigned)min(k, kend - 4));
+                reg[i] = k < kend ? v : f32x4{0, 0, 0, 0};
+            } else {
+                const int k = k0 + kq + 8 * i;
+                const f32x4 v = *reinterpret_cast<const f32x4*>(src + off[i] + (unsigned)min(k, kend - 1) * ld);
+                reg[i] = k < kend ? v : f32x4{0, 0, 0, 0};
+            }
+        }
+    }
+};
+
+// One 128×128 output tile (or one split-K slice of it) of C = op(A)·op(B).
+//
+// Each tile walks its full K tiles starting at its own offset (rotation by the tile index), then the
+// ragged tail if any. Operand rows are often a multiple of 1 KiB apart (768 or 2304 floats), so blocks
+// that all fetched the same K columns at once would hit the same few memory channels; staggered
+// starts spread them. The sum order is fixed per tile, so results stay deterministic.
+template <bool AK, bool BKC, int MODE, bool RES>
+__device__ __forceinline__ void gemm_tile(const GemmParams& p, int logical, float (*smem)[2][STAGE]) {
+    const TileCoord c = tile_coord(p, logical);
+    const int len = max(0, c.ke - c.kb);
+    const int nfull = len / BK, ntiles = nfull + (len % BK != 0 ? 1 : 0);
+    const int rot = nfull > 0 ? c.t % nfull : 0;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, kh = (lane >> 5) << 2;
+
+    const Loader<AK> la(p.A, p.lda, c.m0, p.M, tid);
+    const Loader<BKC> lb(p.B, p.ldb, c.n0, p.N, tid);
+    f32x4 ra[4], rb[4];
+    auto fetch = [&](int j) {  // block-uniform branch
+        if (j < nfull) {
+            int q = j + rot;
+            if (q >= nfull) q -= nfull;
+            la.full(c.kb + q * BK, ra);
+            lb.full(c.kb + q * BK, rb);
+        } else {
+            la.tail(c.kb + nfull * BK, c.ke, ra);
+            lb.tail(c.kb + nfull * BK, c.ke, rb);
+        }
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+    if (ntiles > 0) {
+        fetch(0);
+        store_tile<AK>(smem[0][0], ra, tid);
+        store_tile<BKC>(smem[0][1], rb, tid);
+    }
+    __syncthreads();
+    for (int j = 0; j < ntiles; ++j) {
+        const int cur = j & 1;
+        if (j + 1 < ntiles) fetch(j + 1);
+        mma_stage<AK, BKC>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, kh);
+        if (j + 1 < ntiles) {
+            store_tile<AK>(smem[cur ^ 1][0], ra, tid);
+            store_tile<BKC>(smem[cur ^ 1][1], rb, tid);
+        }
+        __syncthreads();
+    }
+
+    if (c.m0 + BM <= p.M && c.n0 + BN <= p.N)
+        store_acc<MODE, RES, false>(p, c, acc, wm, wn, lr, kh);
+    else
+        store_acc<MODE, RES, true>(p, c, acc, wm, wn, lr, kh);
+}
+
+template <bool AK, bool BKC, int MODE, bool RES>
+__global__ __launch_bounds__(THREADS, 2) void gemm_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
+    gemm_tile<AK, BKC, MODE, RES>(p, xcd_logical_block(), smem);
+}
+
+// dX = dY·W (NN, + residual when RES) and dW += dYᵀ·X (TN, accumulated in place or as split-K
+// partials) in one grid: the first `blocks0` logical blocks are dX tiles, the rest dW slices. The two
+// products are independent, and one grid lets their tiles fill the CUs together instead of each
+// leaving a partial last wave.
+template <int TN_MODE, bool RES>
+__global__ __launch_bounds__(THREADS, 2) void gemm_pair_kernel(GemmParams nn, GemmParams tn, int blocks0) {
+    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
+    const int logical = xcd_logical_block();
+    if (logical < blocks0)
+        gemm_tile<true, false, STORE, RES>(nn, logical, smem);
+    else
+        gemm_tile<false, false, TN_MODE, false>(tn, logical - blocks0, smem);
+}
+
+// ------------------------------------------------------------------------------ generic kernel
+
+// Loads one 128×32 operand tile into 4 float4 registers per thread, testing every element.
+template <bool KCONTIG>
+__device__ __forceinline__ void load_tile_checked(const float* __restrict__ src, long ld, int mn0, int MN, int k0,
+                                                  int kend, bool vec, f32x4 (&reg)[4], int tid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int idx = tid + THREADS * i;
+        if (KCONTIG) {
+            int mn = mn0 + (idx >> 3);
+            int k = k0 + ((idx & 7) << 2);
+            if (vec && mn < MN && k + 3 < kend) {
+                reg[i] = *reinterpret_cast<const f32x4*>(src + (long)mn * ld + k);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) reg[i][e] = (mn < MN && k + e < kend) ? src[(long)mn * ld + k + e] : 0.0f;
+            }
+        } else {
+            int k = k0 + (idx >> 5);
+            int mn = mn0 + ((idx & 31) << 2);
+            if (vec && k < kend && mn + 3 < MN) {
+                reg[i] = *reinterpret_cast<const f32x4*>(src + (long)k * ld + mn);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) reg[i][e] = (k < kend && mn + e < MN) ? src[(long)k * ld + mn + e] : 0.0f;
+            }
+        }
+    }
+}
+
+// Any shape and alignment; K tiles in natural order; runtime residual.
+template <bool AK, bool BKC, int MODE>
+__global__ __launch_bounds__(THREADS, 2) void gemm_generic_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
+    const TileCoord c = tile_coord(p, xcd_logical_block());
+    const int nk = c.ke > c.kb ? (c.ke - c.kb + BK - 1) / BK : 0;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 31, kh = (lane >> 5) << 2;
@@ -115,91 +336,35 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int logical, floa
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
     f32x4 ra[4], rb[4];
     if (nk > 0) {
-        load_tile<AK>(p.A, p.lda, m0, p.M, kb, ke, p.vec_a, ra, tid);
-        load_tile<BKC>(p.B, p.ldb, n0, p.N, kb, ke, p.vec_b, rb, tid);
+        load_tile_checked<AK>(p.A, p.lda, c.m0, p.M, c.kb, c.ke, p.vec_a, ra, tid);
+        load_tile_checked<BKC>(p.B, p.ldb, c.n0, p.N, c.kb, c.ke, p.vec_b, rb, tid);
         store_tile<AK>(smem[0][0], ra, tid);
         store_tile<BKC>(smem[0][1], rb, tid);
     }
     __syncthreads();
-
     for (int kt = 0; kt < nk; ++kt) {
         const int cur = kt & 1;
         if (kt + 1 < nk) {
-            const int k0 = kb + (kt + 1) * BK;
-            load_tile<AK>(p.A, p.lda, m0, p.M, k0, ke, p.vec_a, ra, tid);
-            load_tile<BKC>(p.B, p.ldb, n0, p.N, k0, ke, p.vec_b, rb, tid);
+            const int k0 = c.kb + (kt + 1) * BK;
+            load_tile_checked<AK>(p.A, p.lda, c.m0, p.M, k0, c.ke, p.vec_a, ra, tid);
+            load_tile_checked<BKC>(p.B, p.ldb, c.n0, p.N, k0, c.ke, p.vec_b, rb, tid);
         }
-        const float* As = smem[cur][0];
-        const float* Bs = smem[cur][1];
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 8) {
-            const int k = kk + kh;
-            f32x4 a0 = read_frag<AK>(As, wm * 64 + lr, k);
-            f32x4 a1 = read_frag<AK>(As, wm * 64 + 32 + lr, k);
-            f32x4 b0 = read_frag<BKC>(Bs, wn * 64 + lr, k);
-            f32x4 b1 = read_frag<BKC>(Bs, wn * 64 + 32 + lr, k);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[c], b0[c], acc[0][0], 0, 0, 0);
-                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[c], b1[c], acc[0][1], 0, 0, 0);
-                acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[c], b0[c], acc[1][0], 0, 0, 0);
-                acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[c], b1[c], acc[1][1], 0, 0, 0);
-            }
-        }
+        mma_stage<AK, BKC>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, kh);
         if (kt + 1 < nk) {
             store_tile<AK>(smem[cur ^ 1][0], ra, tid);
             store_tile<BKC>(smem[cur ^ 1][1], rb, tid);
         }
         __syncthreads();
     }
-
-    // Accumulator layout of a 32×32 tile: lane holds column lane%32, rows 8(r/4) + 4(lane/32) + r%4.
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + j * 32 + lr;
-            if (n >= p.N) continue;
-            const float bn = (p.mode == 0 && p.bias) ? p.bias[n] : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + kh + (r & 3);
-                if (m >= p.M) continue;
-                float v = acc[i][j][r];
-                if (p.mode == 0) {
-                    v += bn;
-                    if (p.R) v += p.R[(long)m * p.ldr + n];
-                    p.C[(long)m * p.ldc + n] = v;
-                } else if (p.mode == 1) {
-                    p.C[(long)m * p.ldc + n] += v;
-                } else {
-                    p.C[(long)split * p.M * p.N + (long)m * p.N + n] = v;
-                }
-            }
-        }
-    }
-}
-
-template <bool AK, bool BKC>
-__global__ __launch_bounds__(THREADS, 2) void gemm_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
-    gemm_tile<AK, BKC>(p, xcd_logical_block(), smem);
-}
-
-// dX = dY·W (NN) and dW += dYᵀ·X (TN, split-K partials) in one grid: the first `blocks0` logical
-// blocks are dX tiles, the rest dW slices. The two products are independent, and one grid lets their
-// tiles fill the CUs together instead of each leaving a partial last wave.
-__global__ __launch_bounds__(THREADS, 2) void gemm_pair_kernel(GemmParams nn, GemmParams tn, int blocks0) {
-    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
-    const int logical = xcd_logical_block();
-    if (logical < blocks0)
-        gemm_tile<true, false>(nn, logical, smem);
+    if (MODE == STORE && p.R)
+        store_acc<MODE, true, true>(p, c, acc, wm, wn, lr, kh);
     else
-        gemm_tile<false, false>(tn, logical - blocks0, smem);
+        store_acc<MODE, false, true>(p, c, acc, wm, wn, lr, kh);
 }
+
+// ------------------------------------------------------------------------------ reductions
 
 // C[m, n] += Σ_s P[s][m][n], s in order.
 __global__ void splitk_reduce_kernel(const float* __restrict__ P, int splits, int M, int N, float* C, long ldc) {
@@ -239,12 +404,48 @@ __global__ void column_reduce_kernel(const float* __restrict__ part, int chunks,
     out[c] += s;
 }
 
-template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int blocks) {
-    hipLaunchKernelGGL((gemm_kernel<AK, BKC>), dim3(blocks), dim3(THREADS), 0, ctx->stream, p);
-    check_launch("gemm_kernel");
-}
+// ------------------------------------------------------------------------------ host side
 
 inline bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+// The main kernel's requirements for operand `src` (extent `mn` × K, contiguous along K when kcontig).
+bool operand_fast(const float* src, long ld, bool vec, bool kcontig, int mn, int K) {
+    const long contiguous = kcontig ? K : mn;
+    const long lines = kcontig ? mn : K;
+    return vec && contiguous % 4 == 0 && contiguous >= 4 && lines >= 1 && ld >= contiguous &&
+           (lines - 1) * ld + contiguous < (1L << 31) && src != nullptr;
+}
+
+bool gemm_fast(const GemmParams& p, bool ak, bool bkc) {
+    return operand_fast(p.A, p.lda, p.vec_a, ak, p.M, p.K) && operand_fast(p.B, p.ldb, p.vec_b, bkc, p.N, p.K) &&
+           (long)p.M * p.ldc < (1L << 31) && (p.R == nullptr || (long)p.M * p.ldr < (1L << 31));
+}
+
+template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int blocks) {
+    const dim3 g(blocks), b(THREADS);
+    if (!gemm_fast(p, AK, BKC)) {
+        switch (p.mode) {
+            case STORE: hipLaunchKernelGGL((gemm_generic_kernel<AK, BKC, STORE>), g, b, 0, ctx->stream, p); break;
+            case ACCUMULATE:
+                hipLaunchKernelGGL((gemm_generic_kernel<AK, BKC, ACCUMULATE>), g, b, 0, ctx->stream, p);
+                break;
+            default: hipLaunchKernelGGL((gemm_generic_kernel<AK, BKC, PARTIAL>), g, b, 0, ctx->stream, p);
+        }
+        check_launch("gemm_generic_kernel");
+        return;
+    }
+    switch (p.mode) {
+        case STORE:
+            if (p.R)
+                hipLaunchKernelGGL((gemm_kernel<AK, BKC, STORE, true>), g, b, 0, ctx->stream, p);
+            else
+                hipLaunchKernelGGL((gemm_kernel<AK, BKC, STORE, false>), g, b, 0, ctx->stream, p);
+            break;
+        case ACCUMULATE: hipLaunchKernelGGL((gemm_kernel<AK, BKC, ACCUMULATE, false>), g, b, 0, ctx->stream, p); break;
+        default: hipLaunchKernelGGL((gemm_kernel<AK, BKC, PARTIAL, false>), g, b, 0, ctx->stream, p);
+    }
+    check_launch("gemm_kernel");
+}
 
 GemmParams make_params(int M, int N, int K, const float* A, long lda, const float* B, long ldb, float* C, long ldc,
                        const float* bias, const float* R, long ldr) {
@@ -280,14 +481,14 @@ int set_splits(GemmParams& p, int splits) {
     return p.splits;
 }
 
-// An accumulating product: one writer per element (mode 1), or split-K partials into workspace slot 0
-// (mode 2) to be reduced by finish_accumulate.
+// An accumulating product: one writer per element (ACCUMULATE), or split-K partials into workspace
+// slot 0 (PARTIAL) to be reduced by finish_accumulate.
 float* prepare_accumulate(laya_ctx* ctx, GemmParams& p) {
     if (p.splits == 1) {
-        p.mode = 1;
+        p.mode = ACCUMULATE;
         return nullptr;
     }
-    p.mode = 2;
+    p.mode = PARTIAL;
     float* partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)p.splits * p.M * p.N));
     float* out = p.C;
     p.C = partial;
@@ -295,7 +496,7 @@ float* prepare_accumulate(laya_ctx* ctx, GemmParams& p) {
 }
 
 void finish_accumulate(laya_ctx* ctx, const GemmParams& p, float* out, long ldc) {
-    if (p.mode != 2) return;
+    if (p.mode != PARTIAL) return;
     const long total = (long)p.M * p.N;
     ProfileScope scope(ctx, "gemm_splitk_reduce", 0.0, 4.0 * total * (p.splits + 2));
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
@@ -317,7 +518,7 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
         set_splits(p, std::max(1, std::min(want, std::max(1, K / 512))));
         out = prepare_accumulate(ctx, p);
     } else {
-        p.mode = 0;
+        p.mode = STORE;
     }
     const int blocks = tiles * p.splits;
     {
@@ -337,9 +538,15 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
     if (rows == 0) return;
     // dx[rows, in] = dy[rows, out] · W[out, in]       (NN, K = out)
     GemmParams nn = make_params(rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual, in);
-    nn.mode = 0;
+    nn.mode = STORE;
     // dW[out, in] += dy[rows, out]ᵀ · x[rows, in]     (TN, K = rows)
     GemmParams tn = make_params(out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr, 0);
+    if (!gemm_fast(nn, true, false) || !gemm_fast(tn, false, false)) {
+        gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual,
+             in);
+        gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
+        return;
+    }
     const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
     // Choose the dW split so its slices are as long as a dX tile's K loop, then minimise the rounds of
     // 2-blocks-per-CU the combined grid needs times the longest block.
@@ -366,7 +573,18 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
     const int blocks = n0 + n1 * tn.splits;
     {
         ProfileScope scope(ctx, "gemm_bwd_pair", 2.0 * 2.0 * rows * (double)in * out, 0.0);
-        hipLaunchKernelGGL(gemm_pair_kernel, dim3(blocks), dim3(THREADS), 0, ctx->stream, nn, tn, n0);
+        const dim3 g(blocks), b(THREADS);
+        if (tn.mode == ACCUMULATE) {
+            if (dx_residual)
+                hipLaunchKernelGGL((gemm_pair_kernel<ACCUMULATE, true>), g, b, 0, ctx->stream, nn, tn, n0);
+            else
+                hipLaunchKernelGGL((gemm_pair_kernel<ACCUMULATE, false>), g, b, 0, ctx->stream, nn, tn, n0);
+        } else {
+            if (dx_residual)
+                hipLaunchKernelGGL((gemm_pair_kernel<PARTIAL, true>), g, b, 0, ctx->stream, nn, tn, n0);
+            else
+                hipLaunchKernelGGL((gemm_pair_kernel<PARTIAL, false>), g, b, 0, ctx->stream, nn, tn, n0);
+        }
         check_launch("gemm_pair_kernel");
     }
     finish_accumulate(ctx, tn, dW_out, in);

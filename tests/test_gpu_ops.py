@@ -33,7 +33,7 @@ def param(ctx, name, a, trainable=True):
 
 
 @pytest.mark.parametrize("rows,inn,out", [(37, 96, 130), (300, 128, 384), (1000, 768, 2304), (5, 768, 1),
-                                          (2048, 1152, 768)])
+                                          (2048, 1152, 768), (333, 100, 260)])
 def test_linear_forward_and_backward(ctx, rows, inn, out):
     print(f"linear rows={rows} in={inn} out={out}", flush=True)
     rng = np.random.default_rng(rows + inn + out)
@@ -56,6 +56,26 @@ def test_linear_forward_and_backward(ctx, rows, inn, out):
     assert rel_l2(dx_ref, dx_.numpy()) < 1e-6
     assert rel_l2(2 * dW, w.gradient.numpy()) < 1e-6
     assert rel_l2(2 * db, bias.gradient.numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("rows,inn,out", [(4100, 64, 96), (1500, 256, 132)])
+def test_linear_backward_one_product(ctx, rows, inn, out):
+    """dW alone (split-K partials over a ragged last slice) and dx alone (frozen weight)."""
+    print(f"linear one-product rows={rows} in={inn} out={out}", flush=True)
+    rng = np.random.default_rng(rows * 7 + inn)
+    x = rng.standard_normal((rows, inn)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+    dy = rng.standard_normal((rows, out)).astype(np.float32)
+    dW = np.zeros((out, inn)); db = np.zeros(out)
+    dx_ref = oracle.linear_backward(x, dy, W, True, dW, db, double=True)
+    xd, dyd = dev(ctx, x), dev(ctx, dy)
+    w = param(ctx, "w", W)
+    laya.linear_backward(w, None, xd, dyd, rows, None)
+    assert rel_l2(dW, w.gradient.numpy()) < 1e-6
+    frozen = param(ctx, "wf", W, trainable=False)
+    dx_ = dev(ctx, np.zeros((rows, inn), np.float32))
+    laya.linear_backward(frozen, None, xd, dyd, rows, dx_)
+    assert rel_l2(dx_ref, dx_.numpy()) < 1e-6
 
 
 @pytest.mark.parametrize("rows,n,with_bias,saved", [(33, 128, False, True), (513, 768, True, True),
