@@ -10,9 +10,10 @@
 //
 // Block tile 128×128×32, 256 threads = 4 waves in 2×2, each wave 64×64 = 2×2 tiles of
 // v_mfma_f32_32x32x2_f32. Operand tiles are staged through LDS in their global orientation
-// (k-contiguous rows read as b128 fragments; mn-contiguous rows read as 4 conflict-free b32),
-// double-buffered with a register prefetch of the next K tile. Split-K partials are reduced in a
-// fixed order, so results never depend on timing.
+// (k-contiguous rows read as b128 fragments of 4 k; mn-contiguous rows read as b64 pairs of
+// neighbouring rows/columns, which then land in two interleaved MFMA tiles), double-buffered with a
+// register prefetch of the next K tile. Split-K partials are reduced in a fixed order, so results
+// never depend on timing.
 //
 // Two kernel families. The main one is branch-free in its K loop: rows and columns past the matrix
 // edge are clamped to the last valid one (their products only reach outputs that are never stored),
@@ -65,13 +66,6 @@ __device__ __forceinline__ void store_tile(float* lds, const f32x4 (&reg)[4], in
     }
 }
 
-// The 4 consecutive-k values lane (mn, k..k+3) contributes to 4 successive MFMAs.
-template <bool KCONTIG>
-__device__ __forceinline__ f32x4 read_frag(const float* lds, int mn, int k) {
-    if (KCONTIG) return *reinterpret_cast<const f32x4*>(lds + mn * KPAD + k);
-    return f32x4{lds[k * MNPAD + mn], lds[(k + 1) * MNPAD + mn], lds[(k + 2) * MNPAD + mn], lds[(k + 3) * MNPAD + mn]};
-}
-
 // XCD-aware order: workgroups are dealt round-robin to the 8 XCDs, so give each XCD a contiguous run
 // of logical tiles (n fastest); tiles sharing an A row-panel then share one XCD's L2.
 __device__ __forceinline__ int xcd_logical_block() {
@@ -98,55 +92,120 @@ __device__ __forceinline__ TileCoord tile_coord(const GemmParams& p, int logical
     return c;
 }
 
-// 64 MFMAs of one wave over one LDS stage (K = 32).
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// 64 MFMAs of one wave over one LDS stage (K = 32), in steps of 8 k. Within a step lane half h holds
+// k = 8s + 4h + c for c = 0..3 and MFMA c pairs the two halves, so a k-contiguous operand gives each
+// lane one b128 read per 32-row tile. An mn-contiguous operand is read as b64 pairs (mn = 2·lane,
+// 2·lane + 1) of one k row, one read per c: its two MFMA tiles are the even and the odd rows (or
+// columns) of the wave's 64, which halves the LDS reads of the per-element b32 form.
 template <bool AK, bool BKC>
 __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, f32x16 (&acc)[2][2], int wm, int wn,
                                           int lr, int kh) {
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 8) {
         const int k = kk + kh;
-        f32x4 a0 = read_frag<AK>(As, wm * 64 + lr, k);
-        f32x4 a1 = read_frag<AK>(As, wm * 64 + 32 + lr, k);
-        f32x4 b0 = read_frag<BKC>(Bs, wn * 64 + lr, k);
-        f32x4 b1 = read_frag<BKC>(Bs, wn * 64 + 32 + lr, k);
+        float a[4][2], b[4][2];  // [c][tile]
+        if (AK) {
+            const f32x4 a0 = *reinterpret_cast<const f32x4*>(As + (wm * 64 + lr) * KPAD + k);
+            const f32x4 a1 = *reinterpret_cast<const f32x4*>(As + (wm * 64 + 32 + lr) * KPAD + k);
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[cc], b0[cc], acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0[cc], b1[cc], acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[cc], b0[cc], acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1[cc], b1[cc], acc[1][1], 0, 0, 0);
+            for (int cc = 0; cc < 4; ++cc) {
+                a[cc][0] = a0[cc];
+                a[cc][1] = a1[cc];
+            }
+        } else {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const f32x2 v = *reinterpret_cast<const f32x2*>(As + (k + cc) * MNPAD + wm * 64 + 2 * lr);
+                a[cc][0] = v[0];
+                a[cc][1] = v[1];
+            }
         }
+        if (BKC) {
+            const f32x4 b0 = *reinterpret_cast<const f32x4*>(Bs + (wn * 64 + lr) * KPAD + k);
+            const f32x4 b1 = *reinterpret_cast<const f32x4*>(Bs + (wn * 64 + 32 + lr) * KPAD + k);
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                b[cc][0] = b0[cc];
+                b[cc][1] = b1[cc];
+            }
+        } else {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const f32x2 v = *reinterpret_cast<const f32x2*>(Bs + (k + cc) * MNPAD + wn * 64 + 2 * lr);
+                b[cc][0] = v[0];
+                b[cc][1] = v[1];
+            }
+        }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[cc][i], b[cc][j], acc[i][j], 0, 0, 0);
     }
 }
 
-// Writes the wave's 64×64 accumulators. Accumulator layout of a 32×32 tile: lane holds column
-// lane%32, rows 8(r/4) + 4(lane/32) + r%4, so every element sits at a fixed 32-bit offset from one
-// base pointer. GUARD drops elements outside the matrix; RES adds the residual R (STORE only).
-template <int MODE, bool RES, bool GUARD>
+// Writes the wave's 64×64 accumulators. In a 32×32 accumulator tile the lane holds column lane%32 and
+// rows q = 8(r/4) + 4(lane/32) + r%4; the tile maps to the wave's rows as 32i + q (k-contiguous A) or
+// 2q + i (mn-contiguous A), and to its columns as 32j + lane%32 or 2·(lane%32) + j. Every element sits
+// at a fixed 32-bit offset from one base pointer. With an mn-contiguous B and VEC2, a lane's two
+// column tiles are adjacent columns and go out as one float2. GUARD drops elements outside the
+// matrix; RES adds the residual R (STORE only).
+template <bool AK, bool BKC, int MODE, bool RES, bool GUARD, bool VEC2>
 __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[2][2], int wm,
                                           int wn, int lr, int kh) {
-    const int row0 = c.m0 + wm * 64 + kh, col0 = c.n0 + wn * 64 + lr;
+    auto rowoff = [&](int i, int r) {
+        const int q = 8 * (r >> 2) + kh + (r & 3);
+        return AK ? wm * 64 + 32 * i + q : wm * 64 + 2 * q + i;
+    };
+    auto coloff = [&](int j) { return BKC ? wn * 64 + 32 * j + lr : wn * 64 + 2 * lr + j; };
     const int ldo = MODE == PARTIAL ? p.N : (int)p.ldc;
-    float* base = (MODE == PARTIAL ? p.C + (long)c.split * p.M * p.N : p.C) + (long)row0 * ldo + col0;
+    const int ldr = RES ? (int)p.ldr : 0;
+    float* base = (MODE == PARTIAL ? p.C + (long)c.split * p.M * p.N : p.C) + (long)c.m0 * ldo + c.n0;
+    const float* rbase = RES ? p.R + (long)c.m0 * p.ldr + c.n0 : nullptr;
     float bj[2] = {0.0f, 0.0f};
     if (MODE == STORE && p.bias) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            if (!GUARD || col0 + j * 32 < p.N) bj[j] = p.bias[col0 + j * 32];
+            if (!GUARD || c.n0 + coloff(j) < p.N) bj[j] = p.bias[c.n0 + coloff(j)];
     }
-    const float* rbase = RES ? p.R + (long)row0 * p.ldr + col0 : nullptr;
+    if (VEC2 && !BKC) {
+        const int col = coloff(0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rowoff(i, r);
+                if (GUARD && (c.m0 + row >= p.M || c.n0 + col >= p.N)) continue;
+                f32x2* dst = reinterpret_cast<f32x2*>(base + row * ldo + col);
+                f32x2 v = {acc[i][0][r], acc[i][1][r]};
+                if (MODE == STORE) {
+                    v += f32x2{bj[0], bj[1]};
+                    if (RES) v += *reinterpret_cast<const f32x2*>(rbase + row * ldr + col);
+                    *dst = v;
+                } else if (MODE == ACCUMULATE) {
+                    *dst = *dst + v;
+                } else {
+                    *dst = v;
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int dr = i * 32 + 8 * (r >> 2) + (r & 3);
-                if (GUARD && (row0 + dr >= p.M || col0 + j * 32 >= p.N)) continue;
-                float* dst = base + dr * ldo + j * 32;
+                const int row = rowoff(i, r), col = coloff(j);
+                if (GUARD && (c.m0 + row >= p.M || c.n0 + col >= p.N)) continue;
+                float* dst = base + row * ldo + col;
                 if (MODE == STORE) {
                     float v = acc[i][j][r] + bj[j];
-                    if (RES) v += rbase[dr * (int)p.ldr + j * 32];
+                    if (RES) v += rbase[row * ldr + col];
                     *dst = v;
                 } else if (MODE == ACCUMULATE) {
                     *dst += acc[i][j][r];
@@ -209,15 +268,16 @@ struct Loader {
     }
 };
 
-// One 128×128 output tile (or one split-K slice of it) of C = op(A)·op(B).
+// The 128×128 accumulators of one output tile over the K range [c.kb, c.ke) of C = op(A)·op(B).
 //
 // Each tile walks its full K tiles starting at its own offset (rotation by the tile index), then the
 // ragged tail if any. Operand rows are often a multiple of 1 KiB apart (768 or 2304 floats), so blocks
 // that all fetched the same K columns at once would hit the same few memory channels; staggered
-// starts spread them. The sum order is fixed per tile, so results stay deterministic.
-template <bool AK, bool BKC, int MODE, bool RES>
-__device__ __forceinline__ void gemm_tile(const GemmParams& p, int logical, float (*smem)[2][STAGE]) {
-    const TileCoord c = tile_coord(p, logical);
+// starts spread them. The sum order is fixed per tile, so results stay deterministic. Ends with a
+// barrier, so the caller may start another tile on the same LDS.
+template <bool AK, bool BKC>
+__device__ __forceinline__ void tile_mma(const GemmParams& p, const TileCoord& c, float (*smem)[2][STAGE],
+                                         f32x16 (&acc)[2][2]) {
     const int len = max(0, c.ke - c.kb);
     const int nfull = len / BK, ntiles = nfull + (len % BK != 0 ? 1 : 0);
     const int rot = nfull > 0 ? c.t % nfull : 0;
@@ -241,7 +301,6 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int logical, floa
         }
     };
 
-    f32x16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -263,17 +322,26 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int logical, floa
         }
         __syncthreads();
     }
+}
 
+// The epilogue of one tile: unguarded when the tile lies inside C.
+template <bool AK, bool BKC, int MODE, bool RES>
+__device__ __forceinline__ void tile_store(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[2][2]) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, kh = (lane >> 5) << 2;
     if (c.m0 + BM <= p.M && c.n0 + BN <= p.N)
-        store_acc<MODE, RES, false>(p, c, acc, wm, wn, lr, kh);
+        store_acc<AK, BKC, MODE, RES, false, true>(p, c, acc, wm, wn, lr, kh);
     else
-        store_acc<MODE, RES, true>(p, c, acc, wm, wn, lr, kh);
+        store_acc<AK, BKC, MODE, RES, true, true>(p, c, acc, wm, wn, lr, kh);
 }
 
 template <bool AK, bool BKC, int MODE, bool RES>
 __global__ __launch_bounds__(THREADS, 2) void gemm_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
-    gemm_tile<AK, BKC, MODE, RES>(p, xcd_logical_block(), smem);
+    const TileCoord c = tile_coord(p, xcd_logical_block());
+    f32x16 acc[2][2];
+    tile_mma<AK, BKC>(p, c, smem, acc);
+    tile_store<AK, BKC, MODE, RES>(p, c, acc);
 }
 
 // dX = dY·W (NN, + residual when RES) and dW += dYᵀ·X (TN, accumulated in place or as split-K
@@ -284,10 +352,154 @@ template <int TN_MODE, bool RES>
 __global__ __launch_bounds__(THREADS, 2) void gemm_pair_kernel(GemmParams nn, GemmParams tn, int blocks0) {
     __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
     const int logical = xcd_logical_block();
-    if (logical < blocks0)
-        gemm_tile<true, false, STORE, RES>(nn, logical, smem);
-    else
-        gemm_tile<false, false, TN_MODE, false>(tn, logical - blocks0, smem);
+    const bool is_nn = logical < blocks0;
+    const GemmParams& p = is_nn ? nn : tn;
+    const TileCoord c = tile_coord(p, is_nn ? logical : logical - blocks0);
+    f32x16 acc[2][2];
+    if (is_nn) {
+        tile_mma<true, false>(nn, c, smem, acc);
+        tile_store<true, false, STORE, RES>(nn, c, acc);
+    } else {
+        tile_mma<false, false>(tn, c, smem, acc);
+        tile_store<false, false, TN_MODE, false>(tn, c, acc);
+    }
+}
+
+// ------------------------------------------------------------------------------ planned pair
+//
+// A static, balanced schedule for the backward pair. The grid is exactly the G = 2·CUs workgroups that
+// fit at once. Work is counted in units of one 128×128×32 MFMA step. Worker g takes whole dX tiles
+// g, g + G, g + 2G, … and then a contiguous run of the dW unit sequence (tile t, K step a) sized so
+// every worker ends up with floor((g+1)·W/G) − floor(g·W/G) units in total. A dW tile covered by one
+// worker is accumulated in place; a dW tile cut between workers gets one partial per covering worker
+// (a worker holds at most two: its first and its last dW tile) and `pair_fixup_kernel` adds them in
+// worker order. No workgroup ever waits on another, and the sums do not depend on timing.
+
+struct PairPlan {
+    int G;                   // workers = grid size
+    int nn_tiles, nn_units;  // dX tiles and K units per dX tile
+    int tn_tiles, tn_units;  // dW tiles and K units per dW tile
+    int q, r;                // nn_tiles = q·G + r
+    int W;                   // total units (G·W < 2³¹, checked on the host)
+    float* partial;          // [G][2][BM·BN] dW partial tiles, lane order
+};
+
+// First dW unit of worker g (the end of worker g is the start of worker g + 1).
+__device__ __forceinline__ int plan_tn_lo(const PairPlan& s, int g) {
+    return g * s.W / s.G - s.nn_units * (g * s.q + min(g, s.r));
+}
+
+__device__ __forceinline__ TileCoord unit_coord(const GemmParams& p, int t, int a, int b) {
+    TileCoord c;
+    c.split = 0;
+    c.t = t;
+    const int tile_m = t / p.tiles_n;
+    c.m0 = tile_m * BM;
+    c.n0 = (t - tile_m * p.tiles_n) * BN;
+    c.kb = a * BK;
+    c.ke = min(p.K, b * BK);
+    return c;
+}
+
+// Accumulators in lane order: thread tid's 64 values as 16 float4 at (q·256 + tid)·4, q = (2i + j)·4 + r/4.
+__device__ __forceinline__ void write_partial(float* slot, const f32x16 (&acc)[2][2]) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int i = q >> 3, j = (q >> 2) & 1, r = (q & 3) * 4;
+        *reinterpret_cast<f32x4*>(slot + (q * THREADS + threadIdx.x) * 4) =
+            f32x4{acc[i][j][r], acc[i][j][r + 1], acc[i][j][r + 2], acc[i][j][r + 3]};
+    }
+}
+
+template <bool RES>
+__global__ __launch_bounds__(THREADS, 2) void gemm_pair_planned_kernel(GemmParams nn, GemmParams tn, PairPlan s) {
+    __shared__ __attribute__((aligned(16))) float smem[2][2][STAGE];
+    const int g = xcd_logical_block();
+    const int count = s.q + (g < s.r ? 1 : 0);
+    for (int n = 0; n < count; ++n) {
+        const TileCoord c = unit_coord(nn, g + n * s.G, 0, s.nn_units);
+        f32x16 acc[2][2];
+        tile_mma<true, false>(nn, c, smem, acc);
+        tile_store<true, false, STORE, RES>(nn, c, acc);
+    }
+    const int lo = plan_tn_lo(s, g), hi = plan_tn_lo(s, g + 1);
+    for (int u = lo; u < hi;) {
+        const int t = u / s.tn_units;
+        const int a = u - t * s.tn_units;
+        const int b = min(s.tn_units, a + (hi - u));
+        const TileCoord c = unit_coord(tn, t, a, b);
+        f32x16 acc[2][2];
+        tile_mma<false, false>(tn, c, smem, acc);
+        if (a == 0 && b == s.tn_units)
+            tile_store<false, false, ACCUMULATE, false>(tn, c, acc);
+        else
+            write_partial(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (BM * BN), acc);
+        u += b - a;
+    }
+}
+
+// Adds the partials of the workers that shared a dW tile, in worker order, into dW. Eight workgroups
+// per tile (blockIdx.y = 4i + r/4): each thread sums the two float4 groups (j = 0, 1) of its lanes'
+// accumulator rows and adds them to dW as four column pairs, in the layout `store_acc` uses.
+__global__ __launch_bounds__(THREADS) void pair_fixup_kernel(GemmParams tn, PairPlan s) {
+    const int t = blockIdx.x, i = blockIdx.y >> 2, r4 = blockIdx.y & 3;
+    const int a = t * s.tn_units, b = a + s.tn_units;
+    // First worker whose dW run ends after a (runs are ordered and contiguous).
+    int lo = 0, hi = s.G - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (plan_tn_lo(s, mid + 1) > a) hi = mid; else lo = mid + 1;
+    }
+    int covering = 0;
+    for (int g = lo; g < s.G && plan_tn_lo(s, g) < b; ++g)
+        if (plan_tn_lo(s, g + 1) > plan_tn_lo(s, g)) ++covering;
+    if (covering <= 1) return;  // one worker held the whole tile and accumulated it in place
+
+    // The covering workers' partial slots in worker order, in batches of 8 so the loads of a batch are
+    // in flight together; the sum order stays the worker order.
+    const int tid = threadIdx.x;
+    const long off0 = ((2 * i) * 4 + r4) * THREADS + tid, off1 = ((2 * i + 1) * 4 + r4) * THREADS + tid;
+    f32x4 sum[2] = {f32x4{0, 0, 0, 0}, f32x4{0, 0, 0, 0}};
+    int g = lo;
+    while (g < s.G) {
+        int slots[8];
+        int n = 0;
+        for (; g < s.G && n < 8; ++g) {
+            const int glo = plan_tn_lo(s, g), ghi = plan_tn_lo(s, g + 1);
+            if (glo >= b) {
+                g = s.G;
+                break;
+            }
+            if (ghi <= glo || ghi <= a) continue;
+            slots[n++] = g * 2 + (glo / s.tn_units == t ? 0 : 1);
+        }
+        f32x4 v[8][2];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k < n) {
+                const f32x4* slot = reinterpret_cast<const f32x4*>(s.partial + (long)slots[k] * (BM * BN));
+                v[k][0] = slot[off0];
+                v[k][1] = slot[off1];
+            }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k < n) {
+                sum[0] += v[k][0];
+                sum[1] += v[k][1];
+            }
+    }
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, kh = (lane >> 5) << 2;
+    const TileCoord c = unit_coord(tn, t, 0, s.tn_units);
+    const int col = c.n0 + wn * 64 + 2 * lr;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int row = c.m0 + wm * 64 + 2 * (8 * r4 + kh + e) + i;
+        if (row < tn.M && col < tn.N) {
+            f32x2* dst = reinterpret_cast<f32x2*>(tn.C + (long)row * tn.ldc + col);
+            *dst = *dst + f32x2{sum[0][e], sum[1][e]};
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------ generic kernel
@@ -359,9 +571,9 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_generic_kernel(GemmParams p) 
         __syncthreads();
     }
     if (MODE == STORE && p.R)
-        store_acc<MODE, true, true>(p, c, acc, wm, wn, lr, kh);
+        store_acc<AK, BKC, MODE, true, true, false>(p, c, acc, wm, wn, lr, kh);
     else
-        store_acc<MODE, false, true>(p, c, acc, wm, wn, lr, kh);
+        store_acc<AK, BKC, MODE, false, true, false>(p, c, acc, wm, wn, lr, kh);
 }
 
 // ------------------------------------------------------------------------------ reductions
@@ -407,6 +619,7 @@ __global__ void column_reduce_kernel(const float* __restrict__ part, int chunks,
 // ------------------------------------------------------------------------------ host side
 
 inline bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+inline bool aligned8(const void* ptr) { return ((uintptr_t)ptr & 7u) == 0; }
 
 // The main kernel's requirements for operand `src` (extent `mn` × K, contiguous along K when kcontig).
 bool operand_fast(const float* src, long ld, bool vec, bool kcontig, int mn, int K) {
@@ -417,8 +630,11 @@ bool operand_fast(const float* src, long ld, bool vec, bool kcontig, int mn, int
 }
 
 bool gemm_fast(const GemmParams& p, bool ak, bool bkc) {
+    // An mn-contiguous B makes the epilogue store column pairs (float2): C, R and bias must allow it.
+    const bool pairs_ok = bkc || (p.ldc % 2 == 0 && aligned8(p.C) && (p.R == nullptr || (p.ldr % 2 == 0 && aligned8(p.R))) &&
+                                  (p.bias == nullptr || aligned8(p.bias)));
     return operand_fast(p.A, p.lda, p.vec_a, ak, p.M, p.K) && operand_fast(p.B, p.ldb, p.vec_b, bkc, p.N, p.K) &&
-           (long)p.M * p.ldc < (1L << 31) && (p.R == nullptr || (long)p.M * p.ldr < (1L << 31));
+           (long)p.M * p.ldc < (1L << 31) && (p.R == nullptr || (long)p.M * p.ldr < (1L << 31)) && pairs_ok;
 }
 
 template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int blocks) {
@@ -548,6 +764,53 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
         return;
     }
     const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
+    {
+        // The balanced static schedule, when every worker's whole dX tiles fit in its share of the work.
+        PairPlan s{};
+        s.G = 2 * ctx->cu_count;
+        s.nn_tiles = n0;
+        s.nn_units = (out + BK - 1) / BK;
+        s.tn_tiles = n1;
+        s.tn_units = (rows + BK - 1) / BK;
+        s.q = n0 / s.G;
+        s.r = n0 % s.G;
+        const long W = (long)n0 * s.nn_units + (long)n1 * s.tn_units;
+        s.W = (int)std::min<long>(W, 1L << 30);
+        const long need_min = W / s.G - (long)(s.q + (s.r > 0 ? 1 : 0)) * s.nn_units;
+        if (need_min >= 0 && s.nn_units > 0 && W * s.G < (1L << 31)) {
+            s.partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)s.G * 2 * BM * BN));
+            tn.mode = ACCUMULATE;
+            {
+                ProfileScope scope(ctx, "gemm_bwd_pair", 2.0 * 2.0 * rows * (double)in * out, 0.0);
+                const dim3 g(s.G), b(THREADS);
+                if (dx_residual)
+                    hipLaunchKernelGGL((gemm_pair_planned_kernel<true>), g, b, 0, ctx->stream, nn, tn, s);
+                else
+                    hipLaunchKernelGGL((gemm_pair_planned_kernel<false>), g, b, 0, ctx->stream, nn, tn, s);
+                check_launch("gemm_pair_planned_kernel");
+            }
+            // Compulsory bytes of the fixup: every partial tile read once, every shared dW tile read and
+            // written once (the same walk over the workers' runs the kernels make).
+            long partials = 0, shared = 0;
+            auto tn_lo = [&](long g) { return g * W / s.G - (long)s.nn_units * (g * s.q + std::min<long>(g, s.r)); };
+            for (int g = 0; ctx->profiling && g < s.G; ++g) {
+                const long lo = tn_lo(g), hi = tn_lo(g + 1);
+                for (long u = lo; u < hi;) {
+                    const long t = u / s.tn_units, a = u - t * s.tn_units;
+                    const long b = std::min<long>(s.tn_units, a + (hi - u));
+                    if (!(a == 0 && b == s.tn_units)) {
+                        ++partials;
+                        if (a == 0) ++shared;  // count each shared tile at its first piece
+                    }
+                    u += b - a;
+                }
+            }
+            ProfileScope scope(ctx, "gemm_pair_fixup", 0.0, 4.0 * BM * BN * (double)(partials + 2 * shared));
+            hipLaunchKernelGGL(pair_fixup_kernel, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
+            check_launch("pair_fixup_kernel");
+            return;
+        }
+    }
     // Choose the dW split so its slices are as long as a dX tile's K loop, then minimise the rounds of
     // 2-blocks-per-CU the combined grid needs times the longest block.
     const long slots = 2L * ctx->cu_count;

@@ -33,7 +33,9 @@ def param(ctx, name, a, trainable=True):
 
 
 @pytest.mark.parametrize("rows,inn,out", [(37, 96, 130), (300, 128, 384), (1000, 768, 2304), (5, 768, 1),
-                                          (2048, 1152, 768), (333, 100, 260)])
+                                          (2048, 1152, 768), (333, 100, 260),
+                                          # large enough for the balanced static schedule of dX + dW
+                                          (8000, 768, 768), (9000, 768, 2304)])
 def test_linear_forward_and_backward(ctx, rows, inn, out):
     print(f"linear rows={rows} in={inn} out={out}", flush=True)
     rng = np.random.default_rng(rows + inn + out)
