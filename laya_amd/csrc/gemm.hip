@@ -154,6 +154,12 @@ __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, f32x
 // at a fixed 32-bit offset from one base pointer. With an mn-contiguous B and VEC2, a lane's two
 // column tiles are adjacent columns and go out as one float2. GUARD drops elements outside the
 // matrix; RES adds the residual R (STORE only).
+//
+// Whatever the epilogue reads (the residual, or C itself when accumulating) is loaded for all of the
+// lane's elements before the first store: the memory counter the wait instructions use also counts
+// stores, so a load issued after stores waits for all of them, and interleaving load-add-store per
+// element would serialise the epilogue. Each element is read and written by its own lane only, so
+// this order is also right when R is C.
 template <bool AK, bool BKC, int MODE, bool RES, bool GUARD, bool VEC2>
 __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[2][2], int wm,
                                           int wn, int lr, int kh) {
@@ -166,6 +172,9 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
     const int ldr = RES ? (int)p.ldr : 0;
     float* base = (MODE == PARTIAL ? p.C + (long)c.split * p.M * p.N : p.C) + (long)c.m0 * ldo + c.n0;
     const float* rbase = RES ? p.R + (long)c.m0 * p.ldr + c.n0 : nullptr;
+    constexpr bool READS = RES || MODE == ACCUMULATE;
+    const float* src = MODE == ACCUMULATE ? base : rbase;  // what the epilogue adds besides bias
+    const int lds_ = MODE == ACCUMULATE ? ldo : ldr;
     float bj[2] = {0.0f, 0.0f};
     if (MODE == STORE && p.bias) {
 #pragma unroll
@@ -174,45 +183,49 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
     }
     if (VEC2 && !BKC) {
         const int col = coloff(0);
+        auto inside = [&](int i, int r) { return !GUARD || (c.m0 + rowoff(i, r) < p.M && c.n0 + col < p.N); };
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i) {  // two halves bound the registers the reads hold
+            f32x2 add[16];
+            if (READS) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    add[r] = inside(i, r) ? *reinterpret_cast<const f32x2*>(src + rowoff(i, r) * lds_ + col)
+                                          : f32x2{0.0f, 0.0f};
+            }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int row = rowoff(i, r);
-                if (GUARD && (c.m0 + row >= p.M || c.n0 + col >= p.N)) continue;
-                f32x2* dst = reinterpret_cast<f32x2*>(base + row * ldo + col);
-                f32x2 v = {acc[i][0][r], acc[i][1][r]};
-                if (MODE == STORE) {
-                    v += f32x2{bj[0], bj[1]};
-                    if (RES) v += *reinterpret_cast<const f32x2*>(rbase + row * ldr + col);
-                    *dst = v;
-                } else if (MODE == ACCUMULATE) {
-                    *dst = *dst + v;
-                } else {
-                    *dst = v;
-                }
+                if (!inside(i, r)) continue;
+                f32x2 v = {acc[i][0][r] + bj[0], acc[i][1][r] + bj[1]};
+                if (READS) v += add[r];
+                *reinterpret_cast<f32x2*>(base + rowoff(i, r) * ldo + col) = v;
             }
+        }
         return;
     }
+    auto inside = [&](int i, int j, int r) {
+        return !GUARD || (c.m0 + rowoff(i, r) < p.M && c.n0 + coloff(j) < p.N);
+    };
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i) {
+        float add[2][16];
+        if (READS) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    add[j][r] = inside(i, j, r) ? src[rowoff(i, r) * lds_ + coloff(j)] : 0.0f;
+        }
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int row = rowoff(i, r), col = coloff(j);
-                if (GUARD && (c.m0 + row >= p.M || c.n0 + col >= p.N)) continue;
-                float* dst = base + row * ldo + col;
-                if (MODE == STORE) {
-                    float v = acc[i][j][r] + bj[j];
-                    if (RES) v += rbase[row * ldr + col];
-                    *dst = v;
-                } else if (MODE == ACCUMULATE) {
-                    *dst += acc[i][j][r];
-                } else {
-                    *dst = acc[i][j][r];
-                }
+                if (!inside(i, j, r)) continue;
+                float v = acc[i][j][r] + bj[j];
+                if (READS) v += add[j][r];
+                base[rowoff(i, r) * ldo + coloff(j)] = v;
             }
+    }
 }
 
 // ------------------------------------------------------------------------------ main kernel
@@ -268,6 +281,15 @@ struct Loader {
     }
 };
 
+// The thread index passed through an empty asm statement. Addresses derived from it then cannot be
+// hoisted out of a loop over tiles (the persistent kernels), which would keep dozens of per-lane
+// values live for the whole kernel and push it into spills.
+__device__ __forceinline__ int opaque_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // The 128×128 accumulators of one output tile over the K range [c.kb, c.ke) of C = op(A)·op(B).
 //
 // Each tile walks its full K tiles starting at its own offset (rotation by the tile index), then the
@@ -282,7 +304,7 @@ __device__ __forceinline__ void tile_mma(const GemmParams& p, const TileCoord& c
     const int nfull = len / BK, ntiles = nfull + (len % BK != 0 ? 1 : 0);
     const int rot = nfull > 0 ? c.t % nfull : 0;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 31, kh = (lane >> 5) << 2;
 
@@ -327,7 +349,7 @@ __device__ __forceinline__ void tile_mma(const GemmParams& p, const TileCoord& c
 // The epilogue of one tile: unguarded when the tile lies inside C.
 template <bool AK, bool BKC, int MODE, bool RES>
 __device__ __forceinline__ void tile_store(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[2][2]) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, kh = (lane >> 5) << 2;
     if (c.m0 + BM <= p.M && c.n0 + BN <= p.N)
         store_acc<AK, BKC, MODE, RES, false, true>(p, c, acc, wm, wn, lr, kh);
@@ -430,10 +452,7 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_pair_planned_kernel(GemmParam
         const TileCoord c = unit_coord(tn, t, a, b);
         f32x16 acc[2][2];
         tile_mma<false, false>(tn, c, smem, acc);
-        if (a == 0 && b == s.tn_units)
-            tile_store<false, false, ACCUMULATE, false>(tn, c, acc);
-        else
-            write_partial(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (BM * BN), acc);
+        write_partial(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (BM * BN), acc);
         u += b - a;
     }
 }
@@ -492,13 +511,18 @@ __global__ __launch_bounds__(THREADS) void pair_fixup_kernel(GemmParams tn, Pair
     const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, kh = (lane >> 5) << 2;
     const TileCoord c = unit_coord(tn, t, 0, s.tn_units);
     const int col = c.n0 + wn * 64 + 2 * lr;
+    f32x2 cur[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {  // all reads before the first write (see store_acc)
+        const int row = c.m0 + wm * 64 + 2 * (8 * r4 + kh + e) + i;
+        cur[e] = row < tn.M && col < tn.N ? *reinterpret_cast<const f32x2*>(tn.C + (long)row * tn.ldc + col)
+                                          : f32x2{0.0f, 0.0f};
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int row = c.m0 + wm * 64 + 2 * (8 * r4 + kh + e) + i;
-        if (row < tn.M && col < tn.N) {
-            f32x2* dst = reinterpret_cast<f32x2*>(tn.C + (long)row * tn.ldc + col);
-            *dst = *dst + f32x2{sum[0][e], sum[1][e]};
-        }
+        if (row < tn.M && col < tn.N)
+            *reinterpret_cast<f32x2*>(tn.C + (long)row * tn.ldc + col) = cur[e] + f32x2{sum[0][e], sum[1][e]};
     }
 }
 
