@@ -2,9 +2,11 @@
 //
 // Restates Ops.AttentionForward / Ops.AttentionBackward (src/StructuredDecisions.Laya.Training/Ops.cs:263-438)
 // flash-style: per (segment, head), q·k scores over the window [t − w, t + w] clipped to the segment
-// (Ops.cs:315-316), RoPE with segment-local positions applied as tiles are loaded (Gather, Ops.cs:297-313),
-// softmax with an online max and sum, probability dropout regenerated from the counter RNG at
-// head<<42 | row<<21 | key (Ops.cs:318, 355, 401), and the inverse RoPE on dq and dk (Ops.cs:421-427).
+// (Ops.cs:315-316), softmax with an online max and sum, probability dropout regenerated from the counter
+// RNG at head<<42 | row<<21 | key (Ops.cs:318, 355, 401), and the inverse RoPE on dq and dk
+// (Ops.cs:421-427). The kernels read q and k with RoPE (segment-local positions, Gather, Ops.cs:297-313)
+// already applied: the model's QKV projection applies it in its epilogue, and the op-level entry points
+// rotate a copy first (`rope_rows_kernel`).
 // The forward saves each row's base-2 log-sum-exp; the backward recomputes P from it instead of
 // re-running the row softmax.
 //
@@ -49,7 +51,6 @@ struct Params {
 template <int D> struct Shape {
     static constexpr int G = D / 8;     // float4 groups per lane (the lane's half of d)
     static constexpr int ND = D / 32;   // 32-row d tiles of an accumulator
-    static constexpr int GP = D / 16;   // group offset of the rotary partner d + D/2
     static constexpr int FP = D / 4;    // flat accumulator offset of the rotary partner
     static constexpr int KS = D + 4;    // LDS stride of tiles read as b128 fragments
     static constexpr int VS = D + 8;    // LDS stride of tiles read as b32 columns
@@ -67,53 +68,11 @@ __device__ __forceinline__ bool in_window(int q, int key, int L, int hw) {
 }
 
 // A TILE-row slice of one head staged in registers between its global fetch and its LDS commit, so
-// the next tile's loads are in flight while the current tile is computed. Rows outside [0, L) are
-// zeros. With RoPE, each unit is a (d, d + D/2) float4 pair plus its cos/sin, rotated at commit.
-template <int D> struct RopeStage {
-    static constexpr int U = TILE * (D / 8) / THREADS;
-    f32x4 a[U], b[U], c[U], s[U];
-};
+// the next tile's loads are in flight while the current tile is computed. Rows outside [0, L) are zeros.
 template <int D> struct PlainStage {
     static constexpr int U = TILE * (D / 4) / THREADS;
     f32x4 v[U];
 };
-
-template <int D>
-__device__ __forceinline__ void fetch_rope(RopeStage<D>& st, const Params& p, const float* base, long stride, int L,
-                                           int row0, bool rope) {
-#pragma unroll
-    for (int i = 0; i < RopeStage<D>::U; ++i) {
-        const int u = threadIdx.x + i * THREADS;
-        const int r = u / (D / 8), j = (u % (D / 8)) * 4;
-        const int t = row0 + r;
-        const bool ok = t >= 0 && t < L;
-        const float* src = base + (long)(ok ? t : 0) * stride;
-        st.a[i] = ok ? ld4(src + j) : f32x4{0, 0, 0, 0};
-        st.b[i] = ok ? ld4(src + D / 2 + j) : f32x4{0, 0, 0, 0};
-        if (rope) {
-            st.c[i] = ok ? ld4(p.cos_t + (long)t * (D / 2) + j) : f32x4{1, 1, 1, 1};
-            st.s[i] = ok ? ld4(p.sin_t + (long)t * (D / 2) + j) : f32x4{0, 0, 0, 0};
-        }
-    }
-}
-
-template <int D, int S>
-__device__ __forceinline__ void commit_rope(const RopeStage<D>& st, float* lds, bool rope) {
-#pragma unroll
-    for (int i = 0; i < RopeStage<D>::U; ++i) {
-        const int u = threadIdx.x + i * THREADS;
-        const int r = u / (D / 8), j = (u % (D / 8)) * 4;
-        f32x4 a = st.a[i], b = st.b[i];
-        if (rope) {
-            const f32x4 na = a * st.c[i] - b * st.s[i];
-            const f32x4 nb = b * st.c[i] + a * st.s[i];
-            a = na;
-            b = nb;
-        }
-        st4(lds + r * S + j, a);
-        st4(lds + r * S + D / 2 + j, b);
-    }
-}
 
 template <int D>
 __device__ __forceinline__ void fetch_plain(PlainStage<D>& st, const float* base, long stride, int L, int row0) {
@@ -135,24 +94,11 @@ __device__ __forceinline__ void commit_plain(const PlainStage<D>& st, float* lds
     }
 }
 
-// Loads the lane's own row (d = 8g + 4h + c) into registers, with RoPE at position t.
+// Loads the lane's own row (d = 8g + 4h + c) into registers (zeros when !valid).
 template <int D>
-__device__ __forceinline__ void load_lane_row(const float* src, const Params& p, int t, bool valid, bool rope, int h,
-                                              f32x4 (&v)[Shape<D>::G]) {
-    using S = Shape<D>;
+__device__ __forceinline__ void load_lane_row(const float* src, bool valid, int h, f32x4 (&v)[Shape<D>::G]) {
 #pragma unroll
-    for (int g = 0; g < S::G; ++g) v[g] = valid ? ld4(src + 8 * g + 4 * h) : f32x4{0, 0, 0, 0};
-    if (rope && valid) {
-#pragma unroll
-        for (int g = 0; g < S::GP; ++g) {
-            const int i = 8 * g + 4 * h;
-            const f32x4 c = ld4(p.cos_t + (long)t * (D / 2) + i);
-            const f32x4 s = ld4(p.sin_t + (long)t * (D / 2) + i);
-            const f32x4 a = v[g], b = v[g + S::GP];
-            v[g] = a * c - b * s;
-            v[g + S::GP] = b * c + a * s;
-        }
-    }
+    for (int g = 0; g < Shape<D>::G; ++g) v[g] = valid ? ld4(src + 8 * g + 4 * h) : f32x4{0, 0, 0, 0};
 }
 
 // Inverse RoPE on an accumulator whose column is the lane's row t and whose rows are d.
@@ -200,13 +146,12 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
     const int q0w = qb0 + wave * WAVE_ROWS;
     const int q = q0w + lr;
     const bool qvalid = q < L;
-    const bool rope = p.cos_t != nullptr;
     const int hw = p.half_window;
     const long stride = 3L * p.hidden;
     const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
 
     f32x4 qv[S::G];
-    load_lane_row<D>(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, p, q, qvalid, rope, h, qv);
+    load_lane_row<D>(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, qvalid, h, qv);
 
     int kbeg = 0, kend = L;
     int wbeg = 0, wend = L;
@@ -224,17 +169,16 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
 
     const float* kbase = p.qkv + (long)start * stride + kcol;
     const float* vbase = p.qkv + (long)start * stride + vcol;
-    RopeStage<D> kst;
-    PlainStage<D> vst;
-    fetch_rope<D>(kst, p, kbase, stride, L, kbeg, rope);
+    PlainStage<D> kst, vst;
+    fetch_plain<D>(kst, kbase, stride, L, kbeg);
     fetch_plain<D>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
         __syncthreads();
-        commit_rope<D, S::KS>(kst, Ks, rope);
+        commit_plain<D, S::KS>(kst, Ks);
         commit_plain<D, S::VS>(vst, Vs);
         __syncthreads();
         if (kt0 + TILE < kend) {  // block-uniform: the next tile's loads overlap this tile's products
-            fetch_rope<D>(kst, p, kbase, stride, L, kt0 + TILE, rope);
+            fetch_plain<D>(kst, kbase, stride, L, kt0 + TILE);
             fetch_plain<D>(vst, vbase, stride, L, kt0 + TILE);
         }
 #pragma unroll
@@ -336,8 +280,8 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
 
     f32x4 kv[S::G], vv[S::G];
     const long krow = (long)(start + (kvalid ? key : 0)) * stride;
-    load_lane_row<D>(p.qkv + krow + kcol, p, key, kvalid, rope, h, kv);
-    load_lane_row<D>(p.qkv + krow + vcol, p, key, kvalid, false, h, vv);
+    load_lane_row<D>(p.qkv + krow + kcol, kvalid, h, kv);
+    load_lane_row<D>(p.qkv + krow + vcol, kvalid, h, vv);
 
     int qbeg = 0, qend = L, wbeg = 0, wend = L;
     if (hw >= 0) {
@@ -354,15 +298,14 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
         dv[dt] = f32x16{};
     }
 
-    // Q rows (RoPE at commit), dO rows from dcontext [rows, hidden], and the per-row lse / dots,
-    // fetched one tile ahead of the products.
+    // Q rows, dO rows from dcontext [rows, hidden], and the per-row lse / dots, fetched one tile ahead
+    // of the products.
     const float* qbase = p.qkv + (long)start * stride + qcol;
     const float* obase = p.dcontext + (long)start * p.hidden + qcol;
-    RopeStage<D> qst;
-    PlainStage<D> ost;
+    PlainStage<D> qst, ost;
     float lse_r = 0.0f, dot_r = 0.0f;
     auto fetch = [&](int t0) {
-        fetch_rope<D>(qst, p, qbase, stride, L, t0, rope);
+        fetch_plain<D>(qst, qbase, stride, L, t0);
         fetch_plain<D>(ost, obase, p.hidden, L, t0);
         const int t = t0 + (int)threadIdx.x;
         if (threadIdx.x < TILE) {
@@ -373,7 +316,7 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
     fetch(qbeg);
     for (int qt0 = qbeg; qt0 < qend; qt0 += TILE) {
         __syncthreads();
-        commit_rope<D, S::KS>(qst, Qs, rope);
+        commit_plain<D, S::KS>(qst, Qs);
         commit_plain<D, S::VS>(ost, Os);
         if (threadIdx.x < TILE) {
             lse_s[threadIdx.x] = lse_r;
@@ -456,8 +399,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
 
     f32x4 qv[S::G], ov[S::G];
     const int qs = start + (qvalid ? q : 0);
-    load_lane_row<D>(p.qkv + (long)qs * stride + qcol, p, q, qvalid, rope, h, qv);
-    load_lane_row<D>(p.dcontext + (long)qs * p.hidden + qcol, p, q, qvalid, false, h, ov);
+    load_lane_row<D>(p.qkv + (long)qs * stride + qcol, qvalid, h, qv);
+    load_lane_row<D>(p.dcontext + (long)qs * p.hidden + qcol, qvalid, h, ov);
     const float lse = qvalid ? p.lse[(long)qs * p.heads + head] : __builtin_huge_valf();
     const float dot = qvalid ? p.dots[(long)qs * p.heads + head] : 0.0f;
 
@@ -475,17 +418,16 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
 
     const float* kbase = p.qkv + (long)start * stride + kcol;
     const float* vbase = p.qkv + (long)start * stride + vcol;
-    RopeStage<D> kst;
-    PlainStage<D> vst;
-    fetch_rope<D>(kst, p, kbase, stride, L, kbeg, rope);
+    PlainStage<D> kst, vst;
+    fetch_plain<D>(kst, kbase, stride, L, kbeg);
     fetch_plain<D>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
         __syncthreads();
-        commit_rope<D, S::KS>(kst, Ks, rope);
+        commit_plain<D, S::KS>(kst, Ks);
         commit_plain<D, S::KS>(vst, Vs);
         __syncthreads();
         if (kt0 + TILE < kend) {  // block-uniform
-            fetch_rope<D>(kst, p, kbase, stride, L, kt0 + TILE, rope);
+            fetch_plain<D>(kst, kbase, stride, L, kt0 + TILE);
             fetch_plain<D>(vst, vbase, stride, L, kt0 + TILE);
         }
 #pragma unroll
@@ -531,6 +473,36 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
     }
 }
 
+// RoPE at segment-local positions on the q and k columns of one segment's qkv rows, written to `out`
+// together with an unchanged copy of v (Gather, Ops.cs:297-313). One thread per float4 unit of a row:
+// the first hidden/4 units are (d, d + D/2) pairs of q and then k, the next hidden/4 copy v.
+__global__ void rope_rows_kernel(const float* __restrict__ qkv, const int* __restrict__ seg_start,
+                                 const int* __restrict__ seg_len, int hidden, int head_dim,
+                                 const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                 float* __restrict__ out) {
+    const int seg = blockIdx.y;
+    const int start = seg_start[seg], L = seg_len[seg];
+    const int units = hidden / 2;  // per row
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int t = (int)(idx / units), u = (int)(idx - (long)t * units);
+    if (t >= L) return;
+    const long row = (long)(start + t) * 3 * hidden;
+    const int half = head_dim / 2;
+    if (u < hidden / 4) {
+        const int per_part = hidden / 8;                 // float4 pair units in q (or k)
+        const int part = u / per_part, v = u - part * per_part;
+        const int head = v / (half / 4), j = (v - head * (half / 4)) * 4;
+        const long col = (long)part * hidden + head * head_dim + j;
+        const f32x4 a = ld4(qkv + row + col), b = ld4(qkv + row + col + half);
+        const f32x4 c = ld4(cos_t + (long)t * half + j), s = ld4(sin_t + (long)t * half + j);
+        st4(out + row + col, a * c - b * s);
+        st4(out + row + col + half, b * c + a * s);
+    } else {
+        const long col = 2L * hidden + (long)(u - hidden / 4) * 4;
+        st4(out + row + col, ld4(qkv + row + col));
+    }
+}
+
 Params make_params(const AttentionArgs& a) {
     Params p{};
     p.qkv = a.qkv;
@@ -549,6 +521,22 @@ Params make_params(const AttentionArgs& a) {
     return p;
 }
 
+// The qkv the kernels read: `a.qkv` itself when RoPE is already applied (or absent), else a rotated
+// copy of its segment rows in workspace slot 4.
+const float* rotated_qkv(laya_ctx* ctx, const AttentionArgs& a) {
+    if (a.cos_table == nullptr || a.rotated) return a.qkv;
+    LAYA_REQUIRE(a.rows >= 0, "attention: row count needed to rotate q and k");
+    LAYA_REQUIRE(a.hidden % 8 == 0 && (a.head_dim / 2) % 4 == 0, "attention: RoPE needs head_dim % 8 == 0");
+    float* out = static_cast<float*>(ctx->workspace(4, sizeof(float) * (size_t)std::max(a.rows, 1) * 3 * a.hidden));
+    const long threads = (long)a.max_len * (a.hidden / 2);
+    dim3 grid((unsigned)((threads + 255) / 256), a.nseg);
+    ProfileScope scope(ctx, "attention_rope", 0.0, 4.0 * 3.0 * a.hidden * (double)a.rows * 2.0);
+    hipLaunchKernelGGL(rope_rows_kernel, grid, dim3(256), 0, ctx->stream, a.qkv, a.seg_start, a.seg_len, a.hidden,
+                       a.head_dim, a.cos_table, a.sin_table, out);
+    check_launch("rope_rows_kernel");
+    return out;
+}
+
 void check_args(const AttentionArgs& a) {
     LAYA_REQUIRE(a.heads > 0 && a.hidden == a.heads * a.head_dim, "attention: hidden must equal heads × head_dim");
     LAYA_REQUIRE(a.head_dim == 32 || a.head_dim == 64, "attention: head_dim must be 32 or 64");
@@ -564,6 +552,7 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
     check_args(a);
     if (a.nseg == 0 || a.max_len == 0) return;
     Params p = make_params(a);
+    p.qkv = rotated_qkv(ctx, a);
     p.context = context;
     p.lse = lse;
     dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
@@ -580,6 +569,9 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     check_args(a);
     if (a.nseg == 0 || a.max_len == 0 || rows == 0) return;
     Params p = make_params(a);
+    AttentionArgs ar = a;
+    if (ar.rows < 0) ar.rows = rows;
+    p.qkv = rotated_qkv(ctx, ar);
     p.lse = const_cast<float*>(lse);
     p.dcontext = dcontext;
     p.dqkv = dqkv;

@@ -486,11 +486,18 @@ int laya_attention_fwd(laya_ctx* ctx, const float* qkv, const int* seg_start, co
         LAYA_REQUIRE(context && lse, "attention: null output");
         AttentionArgs a = attention_args(qkv, seg_start, seg_len, nseg, max_len, hidden, heads, scale, half_window,
                                          rot, p_drop, seed);
-        if (ctx->profiling && nseg > 0) {
-            std::vector<int> ln(nseg);
+        if ((ctx->profiling || rot) && nseg > 0) {
+            // The segment table (small) sizes the profile's flop count and the rotated copy of q and k.
+            std::vector<int> st(nseg), ln(nseg);
+            LAYA_HIP(hipMemcpyAsync(st.data(), seg_start, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
             LAYA_HIP(hipMemcpyAsync(ln.data(), seg_len, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
             LAYA_HIP(hipStreamSynchronize(ctx->stream));
-            for (int L : ln) a.keys += window_keys(L, half_window);
+            a.rows = 0;
+            for (int i = 0; i < nseg; ++i) {
+                LAYA_REQUIRE(ln[i] >= 0 && ln[i] <= max_len && st[i] >= 0, "attention: bad segment table");
+                a.rows = std::max(a.rows, st[i] + ln[i]);
+                a.keys += window_keys(ln[i], half_window);
+            }
         }
         attention_fwd(ctx, a, context, lse);
     });

@@ -80,7 +80,7 @@ struct laya_ctx {
     hipStream_t stream = nullptr;
     size_t cap = 0, in_use = 0;
     std::unordered_map<void*, size_t> allocations;
-    laya::Workspace scratch[4];
+    laya::Workspace scratch[6];
     hipEvent_t timers[16][2] = {};
     int cu_count = 256;
     bool profiling = false;
@@ -180,6 +180,12 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
           const float* B, long ldb, float* C, long ldc, const float* bias = nullptr, const float* R = nullptr,
           long ldr = 0);
 
+// y = x·Wᵀ + b for x [M, K], W [N, K] with RoPE applied in the epilogue to output columns [0, rope_cols)
+// taken as heads of 64 (d and d + 32 rotated at position pos[row]; tables [positions][32]). The fused
+// QKV projection: q and k leave the GEMM already rotated (Ops.cs:297-313).
+void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* B, float* C, const float* bias,
+               const int* pos, const float* cos_t, const float* sin_t, int rope_cols);
+
 // The two products of Ops.LinearBackward in one launch: dx = dy·W (+ dx_residual) and dW += dyᵀ·x,
 // for dy [rows, out], W [out, in], x [rows, in]; split-K partials of dW reduced in a fixed order.
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
@@ -205,7 +211,9 @@ struct AttentionArgs {
     const float* cos_table;  // [positions, head_dim/2] or null
     const float* sin_table;
     int positions;
-    double keys;  // Σ over queries of the keys each one attends to (for the profile's flop count)
+    bool rotated = false;  // q and k in qkv already carry RoPE (the model's fused projection)
+    int rows = -1;         // rows of qkv, needed to rotate a copy when !rotated
+    double keys;           // Σ over queries of the keys each one attends to (for the profile's flop count)
 };
 
 // Σ_q |window(q) ∩ segment| for one segment (Ops.cs:315-316).

@@ -37,7 +37,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Epilogue modes, fixed at compile time so each kernel carries only its own store path.
-enum : int { STORE = 0, ACCUMULATE = 1, PARTIAL = 2 };
+enum : int { STORE = 0, ACCUMULATE = 1, PARTIAL = 2, STORE_ROPE = 3 };
 
 struct GemmParams {
     const float* A;
@@ -48,8 +48,14 @@ struct GemmParams {
     long lda, ldb, ldc, ldr;
     int M, N, K;
     int tiles_m, tiles_n, splits, k_per_split;
-    int mode;  // STORE, ACCUMULATE in place (one writer per element), or PARTIAL split-K slices
+    int mode;  // STORE, ACCUMULATE in place (one writer per element), PARTIAL split-K slices, STORE_ROPE
     int vec_a, vec_b;
+    // STORE_ROPE: RoPE on output columns [0, rope_cols) in heads of 64, position rope_pos[row]; tables
+    // [positions][32].
+    const int* rope_pos;
+    const float* rope_cos;
+    const float* rope_sin;
+    int rope_cols;
 };
 
 // ------------------------------------------------------------------------------ shared pieces
@@ -176,10 +182,45 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
     const float* src = MODE == ACCUMULATE ? base : rbase;  // what the epilogue adds besides bias
     const int lds_ = MODE == ACCUMULATE ? ldo : ldr;
     float bj[2] = {0.0f, 0.0f};
-    if (MODE == STORE && p.bias) {
+    if ((MODE == STORE || MODE == STORE_ROPE) && p.bias) {
 #pragma unroll
         for (int j = 0; j < 2; ++j)
             if (!GUARD || c.n0 + coloff(j) < p.N) bj[j] = p.bias[c.n0 + coloff(j)];
+    }
+    if constexpr (MODE == STORE_ROPE) {
+        // Row-major NT output: the wave's 64 columns are one head, and a lane's column tiles j = 0, 1
+        // are the rotation partners d = lane%32 and d + 32 of every row it holds.
+        static_assert(AK && BKC, "STORE_ROPE is an NT epilogue");
+        const bool rot = c.n0 + wn * 64 < p.rope_cols;  // wave-uniform
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            float cs[16], sn[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                cs[r] = 1.0f;
+                sn[r] = 0.0f;
+            }
+            if (rot) {
+                int pos[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    pos[r] = (!GUARD || c.m0 + rowoff(i, r) < p.M) ? p.rope_pos[c.m0 + rowoff(i, r)] : 0;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    cs[r] = p.rope_cos[pos[r] * 32 + lr];
+                    sn[r] = p.rope_sin[pos[r] * 32 + lr];
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rowoff(i, r);
+                if (GUARD && c.m0 + row >= p.M) continue;
+                const float a = acc[i][0][r] + bj[0], b = acc[i][1][r] + bj[1];
+                if (!GUARD || c.n0 + coloff(0) < p.N) base[row * ldo + coloff(0)] = a * cs[r] - b * sn[r];
+                if (!GUARD || c.n0 + coloff(1) < p.N) base[row * ldo + coloff(1)] = b * cs[r] + a * sn[r];
+            }
+        }
+        return;
     }
     if (VEC2 && !BKC) {
         const int col = coloff(0);
@@ -771,6 +812,23 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
         }
     }
     finish_accumulate(ctx, p, out, ldc);
+}
+
+void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* B, float* C, const float* bias,
+               const int* pos, const float* cos_t, const float* sin_t, int rope_cols) {
+    if (M == 0 || N == 0) return;
+    GemmParams p = make_params(M, N, K, A, K, B, K, C, N, bias, nullptr, 0);
+    LAYA_REQUIRE(gemm_fast(p, true, true), "gemm_rope: operands must allow the vectorised kernel");
+    LAYA_REQUIRE(rope_cols % 64 == 0 && rope_cols <= N && pos && cos_t && sin_t, "gemm_rope: bad rotary layout");
+    p.mode = STORE_ROPE;
+    p.rope_pos = pos;
+    p.rope_cos = cos_t;
+    p.rope_sin = sin_t;
+    p.rope_cols = rope_cols;
+    ProfileScope scope(ctx, "gemm_nt", 2.0 * M * N * (double)K, 0.0);
+    hipLaunchKernelGGL((gemm_kernel<true, true, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n), dim3(THREADS), 0,
+                       ctx->stream, p);
+    check_launch("gemm_kernel");
 }
 
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,

@@ -108,7 +108,7 @@ struct laya_model {
     // batch tables (device int32)
     int *d_tokens = nullptr, *d_seg_start = nullptr, *d_seg_len = nullptr, *d_row_type = nullptr,
         *d_marker_rows = nullptr, *d_qtypes = nullptr, *d_opt_off = nullptr, *d_sorted = nullptr,
-        *d_unique = nullptr, *d_uoff = nullptr;
+        *d_unique = nullptr, *d_uoff = nullptr, *d_pos = nullptr;
     // optimizer scalars
     double* d_norm = nullptr;
     float* d_coef = nullptr;
@@ -122,7 +122,7 @@ struct laya_model {
     int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0;
     double keys_full = 0, keys_local = 0;  // Σ_q attended keys of the batch, full and sliding window
     std::vector<int> h_tokens, h_start, h_len, h_marker_rows, h_qtypes, h_nopt, h_opt_off, h_row_type, h_sorted,
-        h_unique, h_uoff;
+        h_unique, h_uoff, h_pos;
 
     int d() const { return cfg.hidden; }
     int I() const { return cfg.intermediate; }
@@ -291,8 +291,9 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     cv.add(m->ds_mark, (size_t)Mc * d);
     cv.add(m->targets, Mc);
     // int tables share the carve (4-byte elements)
-    float *tok, *st, *ln, *rt, *mr, *qt, *oo, *so, *un, *uo;
+    float *tok, *st, *ln, *rt, *mr, *qt, *oo, *so, *un, *uo, *ps;
     cv.add(tok, Tz);
+    cv.add(ps, Tz);
     cv.add(st, Sc);
     cv.add(ln, Sc);
     cv.add(rt, Tz);
@@ -314,6 +315,7 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     m->d_sorted = reinterpret_cast<int*>(so);
     m->d_unique = reinterpret_cast<int*>(un);
     m->d_uoff = reinterpret_cast<int*>(uo);
+    m->d_pos = reinterpret_cast<int*>(ps);
     m->cap_tokens = Tc;
     m->cap_markers = Mc;
     m->cap_segs = Sc;
@@ -376,9 +378,11 @@ void prepare_batch(laya_model* m, const laya_batch* b) {
         throw Error(LAYA_ERR_OUT_OF_RANGE, laya_last_error());
     m->n_unique = nu;
     m->keys_full = m->keys_local = 0;
+    m->h_pos.assign(m->T, 0);
     for (int i = 0; i < n; ++i) {
         m->keys_full += window_keys(m->h_len[i], -1);
         m->keys_local += window_keys(m->h_len[i], m->cfg.local_attention / 2);
+        for (int t = 0; t < m->h_len[i]; ++t) m->h_pos[m->h_start[i] + t] = t;  // segment-local RoPE position
     }
 
     ensure_activations(m, m->T, m->nmark, m->nseg);
@@ -393,7 +397,12 @@ void prepare_batch(laya_model* m, const laya_batch* b) {
     upload_ints(m, m->d_sorted, m->h_sorted);
     upload_ints(m, m->d_unique, m->h_unique);
     upload_ints(m, m->d_uoff, m->h_uoff);
+    upload_ints(m, m->d_pos, m->h_pos);
 }
+
+// The encoder's QKV projection applies RoPE in its epilogue when a head is 64 wide (the epilogue's
+// layout); other widths rotate a copy inside the attention entry points.
+bool fused_rope(const laya_model* m) { return m->d() / m->cfg.heads == 64; }
 
 AttentionArgs enc_attention(laya_model* m, const float* qkv, int kind) {
     AttentionArgs a{};
@@ -414,6 +423,8 @@ AttentionArgs enc_attention(laya_model* m, const float* qkv, int kind) {
     a.cos_table = r.cos_t;
     a.sin_table = r.sin_t;
     a.positions = r.positions;
+    a.rotated = fused_rope(m);  // q and k left the QKV projection rotated
+    a.rows = m->T;
     return a;
 }
 
@@ -484,7 +495,13 @@ void forward(laya_model* m, const laya_batch* b, bool train, uint64_t seed) {
             layernorm_fwd(ctx, a.x, T, d, m->W(L.attn_norm), m->W(L.attn_norm_b), eps, a.normed, a.mean1, a.rstd1);
             normed = a.normed;
         }
-        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv);
+        if (fused_rope(m)) {
+            const laya_rotary& r = L.kind == 0 ? m->rot_global : m->rot_local;
+            gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->d_pos, r.cos_t, r.sin_t,
+                      2 * d);
+        } else {
+            linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv);
+        }
         attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse);
         linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res);  // x1 = x + attn
         layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2);
