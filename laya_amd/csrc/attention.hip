@@ -67,6 +67,16 @@ __device__ __forceinline__ bool in_window(int q, int key, int L, int hw) {
     return q < L && key >= 0 && key < L && (hw < 0 || (key - q <= hw && q - key <= hw));
 }
 
+// Wave-uniform: every (query, key) pair of the 32 queries from q0 and 32 keys from k0 lies inside the
+// segment and the window, so the subtile needs no per-element test.
+__device__ __forceinline__ bool subtile_inside(int q0, int k0, int L, int hw) {
+    return q0 + 32 <= L && k0 >= 0 && k0 + 32 <= L && (hw < 0 || (k0 + 31 - q0 <= hw && q0 + 31 - k0 <= hw));
+}
+
+// 2^x on the hardware exponential (v_exp_f32): arguments here are finite or −inf (→ 0), and results
+// below the normal range only arise for probabilities far under the fp32 parity tolerance.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // A TILE-row slice of one head staged in registers between its global fetch and its LDS commit, so
 // the next tile's loads are in flight while the current tile is computed. Rows outside [0, L) are zeros.
 template <int D> struct PlainStage {
@@ -195,20 +205,28 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
             }
             float t[16];
             float mx = -1e30f;
+            if (subtile_inside(q0w, kbs, L, hw)) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
-                t[r] = in_window(q, key, L, hw) ? s[r] * p.scale_log2 : NEG_INF;
-                mx = fmaxf(mx, t[r]);
+                for (int r = 0; r < 16; ++r) {
+                    t[r] = s[r] * p.scale_log2;
+                    mx = fmaxf(mx, t[r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
+                    t[r] = in_window(q, key, L, hw) ? s[r] * p.scale_log2 : NEG_INF;
+                    mx = fmaxf(mx, t[r]);
+                }
             }
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
             const float mnew = fmaxf(m, mx);
-            const float alpha = exp2f(m - mnew);
+            const float alpha = fast_exp2(m - mnew);
             float pr[16];
             float sum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                pr[r] = exp2f(t[r] - mnew);
+                pr[r] = fast_exp2(t[r] - mnew);
                 sum += pr[r];
             }
             l = l * alpha + sum;
@@ -343,17 +361,27 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
                 }
             }
             float pm[16], ds[16];
+            if (p.p_drop == 0.0f && subtile_inside(qbs, k0w, L, hw)) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int ql = 32 * st + 8 * (r >> 2) + 4 * h + (r & 3);
-                const int qq = qt0 + ql;
-                const bool ok = in_window(qq, key, L, hw) && kvalid;
-                const float pr = ok ? exp2f(s[r] * p.scale_log2 - lse_s[ql]) : 0.0f;
-                float mask = 1.0f;
-                if (p.p_drop > 0.0f && ok)
-                    mask = uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
-                pm[r] = pr * mask;
-                ds[r] = pr * (dp[r] * mask - dot_s[ql]) * p.scale;
+                for (int r = 0; r < 16; ++r) {
+                    const int ql = 32 * st + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const float pr = fast_exp2(s[r] * p.scale_log2 - lse_s[ql]);
+                    pm[r] = pr;
+                    ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int ql = 32 * st + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const int qq = qt0 + ql;
+                    const bool ok = in_window(qq, key, L, hw) && kvalid;
+                    const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse_s[ql]) : 0.0f;
+                    float mask = 1.0f;
+                    if (p.p_drop > 0.0f && ok)
+                        mask = uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
+                    pm[r] = pr * mask;
+                    ds[r] = pr * (dp[r] * mask - dot_s[ql]) * p.scale;
+                }
             }
             // dVᵀ += dOᵀ·(P∘M) and dKᵀ += Qᵀ·dS, reducing over the 32 queries of this subtile.
 #pragma unroll
@@ -448,15 +476,20 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
                 }
             }
             float ds[16];
+            if (p.p_drop == 0.0f && subtile_inside(q0w, kbs, L, hw)) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
-                const bool ok = in_window(q, key, L, hw);
-                const float pr = ok ? exp2f(s[r] * p.scale_log2 - lse) : 0.0f;
-                float mask = 1.0f;
-                if (p.p_drop > 0.0f && ok)
-                    mask = uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
-                ds[r] = pr * (dp[r] * mask - dot) * p.scale;
+                for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * p.scale_log2 - lse) * (dp[r] - dot) * p.scale;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const bool ok = in_window(q, key, L, hw);
+                    const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse) : 0.0f;
+                    float mask = 1.0f;
+                    if (p.p_drop > 0.0f && ok)
+                        mask = uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
+                    ds[r] = pr * (dp[r] * mask - dot) * p.scale;
+                }
             }
 #pragma unroll
             for (int dt = 0; dt < S::ND; ++dt) {
