@@ -230,6 +230,17 @@ int laya_model_train_step(laya_model* model, const laya_batch* batch, const floa
                           double beta1, double beta2, double eps, double weight_decay, float* loss_out);
 int laya_model_steps(laya_model* model, int* steps);
 
+/* Device-resident batches. No counterpart in the reference, whose batches are host arrays: these split
+ * laya_model_train_step's host work (validation, layout, embedding-gradient plan, uploads) from the
+ * step, so a caller that prepares batches ahead (a data loader, a benchmark) runs steps on inputs
+ * already in HBM. stage_batch validates exactly as train_step does, uploads the batch and its targets
+ * once and returns a slot; train_step_staged is train_step on that slot; release_batch frees it. */
+int laya_model_stage_batch(laya_model* model, const laya_batch* batch, const float* targets_host, int* slot);
+int laya_model_train_step_staged(laya_model* model, int slot, float ce_weight, float loss_scale, uint64_t seed,
+                                 double max_norm, double lr_encoder, double lr_head, double beta1, double beta2,
+                                 double eps, double weight_decay, float* loss_out);
+int laya_model_release_batch(laya_model* model, int slot);
+
 #ifdef __cplusplus
 }
 #endif

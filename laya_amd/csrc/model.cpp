@@ -55,6 +55,49 @@ struct Carver {
 
 }  // namespace
 
+// The device int32 tables of one batch (TrainableDecisionModel.cs:254-274 layout).
+struct BatchTables {
+    int *tokens, *seg_start, *seg_len, *row_type, *marker_rows, *qtypes, *opt_off, *sorted, *unique, *uoff, *pos;
+};
+
+// A batch planned on the host and uploaded once, ahead of the steps that use it.
+struct StagedBatch {
+    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0;
+    double keys_full = 0, keys_local = 0;
+    void* block = nullptr;  // the tables, then the soft-CE targets
+    BatchTables tables{};
+    float* targets = nullptr;
+};
+
+// Host-side layout of one batch: every table the kernels read, before upload.
+struct BatchPlan {
+    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0;
+    double keys_full = 0, keys_local = 0;
+    std::vector<int> tokens, start, len, marker_rows, qtypes, opt_off, row_type, sorted, unique, uoff, pos;
+};
+
+// The int tables of one batch inside a Carver, sized for Tz tokens, Mc markers and Sc items.
+struct TableCarve {
+    float *tok, *ps, *st, *ln, *rt, *mr, *qt, *oo, *so, *un, *uo;
+    void add(Carver& cv, size_t Tz, size_t Mc, size_t Sc) {
+        cv.add(tok, Tz);
+        cv.add(ps, Tz);
+        cv.add(st, Sc);
+        cv.add(ln, Sc);
+        cv.add(rt, Tz);
+        cv.add(mr, Mc);
+        cv.add(qt, Sc);
+        cv.add(oo, Sc + 1);
+        cv.add(so, Tz);
+        cv.add(un, Tz + 1);
+        cv.add(uo, Tz + 2);
+    }
+    BatchTables bind() const {
+        auto i = [](float* p) { return reinterpret_cast<int*>(p); };
+        return {i(tok), i(st), i(ln), i(rt), i(mr), i(qt), i(oo), i(so), i(un), i(uo), i(ps)};
+    }
+};
+
 struct laya_model {
     laya_ctx* ctx = nullptr;
     laya_model_config cfg{};
@@ -105,10 +148,10 @@ struct laya_model {
     float *dS = nullptr, *dE = nullptr, *dqkv = nullptr, *dctx = nullptr, *dwide = nullptr, *dact = nullptr,
           *dn = nullptr, *dy = nullptr;
     float *ds_scores = nullptr, *ds_act = nullptr, *ds_norm = nullptr, *ds_mark = nullptr, *targets = nullptr;
-    // batch tables (device int32)
-    int *d_tokens = nullptr, *d_seg_start = nullptr, *d_seg_len = nullptr, *d_row_type = nullptr,
-        *d_marker_rows = nullptr, *d_qtypes = nullptr, *d_opt_off = nullptr, *d_sorted = nullptr,
-        *d_unique = nullptr, *d_uoff = nullptr, *d_pos = nullptr;
+    // batch tables (device int32): `own` lives in the activation block and takes uploads of batches
+    // passed by value; `cur` is what the kernels read (own, or a staged batch's tables)
+    BatchTables own{}, cur{};
+    std::vector<StagedBatch> staged;  // laya_model_stage_batch slots; a null block marks a free slot
     // optimizer scalars
     double* d_norm = nullptr;
     float* d_coef = nullptr;
@@ -121,8 +164,6 @@ struct laya_model {
     uint64_t seed = 0;
     int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0;
     double keys_full = 0, keys_local = 0;  // Σ_q attended keys of the batch, full and sliding window
-    std::vector<int> h_tokens, h_start, h_len, h_marker_rows, h_qtypes, h_nopt, h_opt_off, h_row_type, h_sorted,
-        h_unique, h_uoff, h_pos;
 
     int d() const { return cfg.hidden; }
     int I() const { return cfg.intermediate; }
@@ -223,6 +264,7 @@ void ensure_rotary(laya_model* m, int positions) {
 
 void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     if (T <= m->cap_tokens && nmark <= m->cap_markers && nseg <= m->cap_segs && m->act_block) return;
+    m->has_tape = false;  // the activations of the last forward go with the old block
     if (m->act_block) {
         m->ctx->release(m->act_block);
         m->act_block = nullptr;
@@ -291,31 +333,12 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     cv.add(m->ds_mark, (size_t)Mc * d);
     cv.add(m->targets, Mc);
     // int tables share the carve (4-byte elements)
-    float *tok, *st, *ln, *rt, *mr, *qt, *oo, *so, *un, *uo, *ps;
-    cv.add(tok, Tz);
-    cv.add(ps, Tz);
-    cv.add(st, Sc);
-    cv.add(ln, Sc);
-    cv.add(rt, Tz);
-    cv.add(mr, Mc);
-    cv.add(qt, Sc);
-    cv.add(oo, (size_t)Sc + 1);
-    cv.add(so, Tz);
-    cv.add(un, Tz + 1);
-    cv.add(uo, Tz + 2);
+    TableCarve tc;
+    tc.add(cv, Tz, Mc, Sc);
     m->act_block = m->ctx->alloc(cv.bytes);
     cv.bind(static_cast<char*>(m->act_block));
-    m->d_tokens = reinterpret_cast<int*>(tok);
-    m->d_seg_start = reinterpret_cast<int*>(st);
-    m->d_seg_len = reinterpret_cast<int*>(ln);
-    m->d_row_type = reinterpret_cast<int*>(rt);
-    m->d_marker_rows = reinterpret_cast<int*>(mr);
-    m->d_qtypes = reinterpret_cast<int*>(qt);
-    m->d_opt_off = reinterpret_cast<int*>(oo);
-    m->d_sorted = reinterpret_cast<int*>(so);
-    m->d_unique = reinterpret_cast<int*>(un);
-    m->d_uoff = reinterpret_cast<int*>(uo);
-    m->d_pos = reinterpret_cast<int*>(ps);
+    m->own = tc.bind();
+    m->cur = m->own;
     m->cap_tokens = Tc;
     m->cap_markers = Mc;
     m->cap_segs = Sc;
@@ -327,77 +350,97 @@ void upload_ints(laya_model* m, int* dst, const std::vector<int>& src) {
 }
 
 // The batch layout of Forward (TrainableDecisionModel.cs:254-274), with the checks that run before any math.
-void prepare_batch(laya_model* m, const laya_batch* b) {
+BatchPlan plan_batch(const laya_model* m, const laya_batch* b) {
     LAYA_REQUIRE(b && b->n_items > 0, "forward: empty batch");
     LAYA_REQUIRE(b->lengths && b->tokens && b->n_options && b->markers && b->qtypes, "forward: null batch array");
+    BatchPlan bp;
     const int n = b->n_items;
-    m->h_start.assign(n, 0);
-    m->h_len.assign(b->lengths, b->lengths + n);
-    m->h_qtypes.assign(b->qtypes, b->qtypes + n);
-    m->h_nopt.assign(b->n_options, b->n_options + n);
+    bp.start.assign(n, 0);
+    bp.len.assign(b->lengths, b->lengths + n);
+    bp.qtypes.assign(b->qtypes, b->qtypes + n);
     long total = 0, marks = 0;
     int longest = 0;
     for (int i = 0; i < n; ++i) {
         LAYA_REQUIRE(b->lengths[i] > 0, "forward: an item has no tokens");
         LAYA_REQUIRE(b->n_options[i] >= 0, "forward: negative option count");
         LAYA_REQUIRE(b->qtypes[i] >= 0 && b->qtypes[i] < 3, "forward: question type outside [0, 3)");
-        m->h_start[i] = (int)total;
+        bp.start[i] = (int)total;
         total += b->lengths[i];
         marks += b->n_options[i];
         longest = std::max(longest, b->lengths[i]);
     }
-    m->T = (int)total;
-    m->nseg = n;
-    m->nmark = (int)marks;
-    m->max_len = longest;
-    m->h_tokens.assign(b->tokens, b->tokens + total);
-    for (int t = 0; t < m->T; ++t)
-        if ((unsigned)m->h_tokens[t] >= (unsigned)m->cfg.vocab)
-            throw Error(LAYA_ERR_OUT_OF_RANGE,
-                        "token id " + std::to_string(m->h_tokens[t]) + " is outside the vocabulary.");
-    m->h_marker_rows.assign(m->nmark, 0);
-    m->h_opt_off.assign(n + 1, 0);
+    bp.T = (int)total;
+    bp.nseg = n;
+    bp.nmark = (int)marks;
+    bp.max_len = longest;
+    bp.tokens.assign(b->tokens, b->tokens + total);
+    for (int t = 0; t < bp.T; ++t)
+        if ((unsigned)bp.tokens[t] >= (unsigned)m->cfg.vocab)
+            throw Error(LAYA_ERR_OUT_OF_RANGE, "token id " + std::to_string(bp.tokens[t]) + " is outside the vocabulary.");
+    bp.marker_rows.assign(bp.nmark, 0);
+    bp.opt_off.assign(n + 1, 0);
     for (int i = 0, k = 0; i < n; ++i) {
-        m->h_opt_off[i + 1] = m->h_opt_off[i] + b->n_options[i];
+        bp.opt_off[i + 1] = bp.opt_off[i] + b->n_options[i];
         for (int o = 0; o < b->n_options[i]; ++o, ++k) {
             const int pos = std::max(0, b->markers[k]);
             LAYA_REQUIRE(pos < b->lengths[i], "forward: a marker lies beyond its item");
-            m->h_marker_rows[k] = m->h_start[i] + pos;
+            bp.marker_rows[k] = bp.start[i] + pos;
         }
     }
-    m->h_row_type.assign(m->T, 0);
-    for (int i = 0; i < n; ++i)
-        for (int t = 0; t < b->lengths[i]; ++t) m->h_row_type[m->h_start[i] + t] = b->qtypes[i];
-    // Embedding-gradient plan: positions stably sorted by id (counting sort), one run per unique id.
-    m->h_sorted.assign(m->T, 0);
-    m->h_unique.assign(m->T + 1, 0);
-    m->h_uoff.assign(m->T + 2, 0);
-    int nu = 0;
-    if (laya_embedding_plan(m->h_tokens.data(), m->T, m->cfg.vocab, m->h_sorted.data(), m->h_unique.data(),
-                            m->h_uoff.data(), &nu) != LAYA_OK)
-        throw Error(LAYA_ERR_OUT_OF_RANGE, laya_last_error());
-    m->n_unique = nu;
-    m->keys_full = m->keys_local = 0;
-    m->h_pos.assign(m->T, 0);
+    bp.row_type.assign(bp.T, 0);
+    bp.pos.assign(bp.T, 0);
     for (int i = 0; i < n; ++i) {
-        m->keys_full += window_keys(m->h_len[i], -1);
-        m->keys_local += window_keys(m->h_len[i], m->cfg.local_attention / 2);
-        for (int t = 0; t < m->h_len[i]; ++t) m->h_pos[m->h_start[i] + t] = t;  // segment-local RoPE position
+        bp.keys_full += window_keys(bp.len[i], -1);
+        bp.keys_local += window_keys(bp.len[i], m->cfg.local_attention / 2);
+        for (int t = 0; t < b->lengths[i]; ++t) {
+            bp.row_type[bp.start[i] + t] = b->qtypes[i];
+            bp.pos[bp.start[i] + t] = t;  // segment-local RoPE position
+        }
     }
+    // Embedding-gradient plan: positions stably sorted by id (counting sort), one run per unique id.
+    bp.sorted.assign(bp.T, 0);
+    bp.unique.assign(bp.T + 1, 0);
+    bp.uoff.assign(bp.T + 2, 0);
+    int nu = 0;
+    if (laya_embedding_plan(bp.tokens.data(), bp.T, m->cfg.vocab, bp.sorted.data(), bp.unique.data(), bp.uoff.data(),
+                            &nu) != LAYA_OK)
+        throw Error(LAYA_ERR_OUT_OF_RANGE, laya_last_error());
+    bp.n_unique = nu;
+    return bp;
+}
 
-    ensure_activations(m, m->T, m->nmark, m->nseg);
-    ensure_rotary(m, longest);
-    upload_ints(m, m->d_tokens, m->h_tokens);
-    upload_ints(m, m->d_seg_start, m->h_start);
-    upload_ints(m, m->d_seg_len, m->h_len);
-    upload_ints(m, m->d_row_type, m->h_row_type);
-    upload_ints(m, m->d_marker_rows, m->h_marker_rows);
-    upload_ints(m, m->d_qtypes, m->h_qtypes);
-    upload_ints(m, m->d_opt_off, m->h_opt_off);
-    upload_ints(m, m->d_sorted, m->h_sorted);
-    upload_ints(m, m->d_unique, m->h_unique);
-    upload_ints(m, m->d_uoff, m->h_uoff);
-    upload_ints(m, m->d_pos, m->h_pos);
+void upload_tables(laya_model* m, const BatchTables& t, const BatchPlan& bp) {
+    upload_ints(m, t.tokens, bp.tokens);
+    upload_ints(m, t.seg_start, bp.start);
+    upload_ints(m, t.seg_len, bp.len);
+    upload_ints(m, t.row_type, bp.row_type);
+    upload_ints(m, t.marker_rows, bp.marker_rows);
+    upload_ints(m, t.qtypes, bp.qtypes);
+    upload_ints(m, t.opt_off, bp.opt_off);
+    upload_ints(m, t.sorted, bp.sorted);
+    upload_ints(m, t.unique, bp.unique);
+    upload_ints(m, t.uoff, bp.uoff);
+    upload_ints(m, t.pos, bp.pos);
+}
+
+// Makes a batch's sizes the model's current ones and sizes the activations and rotary tables for it.
+template <typename B> void set_batch_sizes(laya_model* m, const B& b) {
+    m->T = b.T;
+    m->nseg = b.nseg;
+    m->nmark = b.nmark;
+    m->max_len = b.max_len;
+    m->n_unique = b.n_unique;
+    m->keys_full = b.keys_full;
+    m->keys_local = b.keys_local;
+    ensure_activations(m, b.T, b.nmark, b.nseg);
+    ensure_rotary(m, b.max_len);
+}
+
+void prepare_batch(laya_model* m, const laya_batch* b) {
+    const BatchPlan bp = plan_batch(m, b);
+    set_batch_sizes(m, bp);
+    m->cur = m->own;
+    upload_tables(m, m->cur, bp);
 }
 
 // The encoder's QKV projection applies RoPE in its epilogue when a head is 64 wide (the epilogue's
@@ -407,8 +450,8 @@ bool fused_rope(const laya_model* m) { return m->d() / m->cfg.heads == 64; }
 AttentionArgs enc_attention(laya_model* m, const float* qkv, int kind) {
     AttentionArgs a{};
     a.qkv = qkv;
-    a.seg_start = m->d_seg_start;
-    a.seg_len = m->d_seg_len;
+    a.seg_start = m->cur.seg_start;
+    a.seg_len = m->cur.seg_len;
     a.nseg = m->nseg;
     a.max_len = m->max_len;
     a.hidden = m->d();
@@ -433,8 +476,8 @@ uint64_t salt(uint64_t seed, int layer, int site) { return mix64(seed, (uint64_t
 AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p, uint64_t seed) {
     AttentionArgs a{};
     a.qkv = qkv;
-    a.seg_start = m->d_seg_start;
-    a.seg_len = m->d_seg_len;
+    a.seg_start = m->cur.seg_start;
+    a.seg_len = m->cur.seg_len;
     a.nseg = m->nseg;
     a.max_len = m->max_len;
     a.hidden = m->d();
@@ -474,8 +517,8 @@ void dropout_copy(laya_model* m, const float* src, float* dst, size_t n, float p
 }
 
 // Forward (TrainableDecisionModel.cs:248-353) with EncoderLayerForward (361-414) and HeadLayerForward (428-468).
-void forward(laya_model* m, const laya_batch* b, bool train, uint64_t seed) {
-    prepare_batch(m, b);
+// Forward over the current batch (prepare_batch or a staged batch made it current).
+void forward(laya_model* m, bool train, uint64_t seed) {
     laya_ctx* ctx = m->ctx;
     const int T = m->T, d = m->d(), I = m->I(), ff = m->cfg.head_ff;
     const float eps = m->cfg.norm_eps;
@@ -485,7 +528,7 @@ void forward(laya_model* m, const laya_batch* b, bool train, uint64_t seed) {
     // Embedding gather fused into the embedding LayerNorm.
     float* x0 = m->cfg.layers > 0 ? m->ea[0].x : m->x_final;
     layernorm_fwd(ctx, m->W(m->tok_emb), T, d, m->W(m->emb_norm), m->W(m->emb_norm_b), eps, x0, m->emb_mean,
-                  m->emb_rstd, m->d_tokens);
+                  m->emb_rstd, m->cur.tokens);
     for (int l = 0; l < m->cfg.layers; ++l) {
         auto& L = m->enc[l];
         auto& a = m->ea[l];
@@ -497,7 +540,7 @@ void forward(laya_model* m, const laya_batch* b, bool train, uint64_t seed) {
         }
         if (fused_rope(m)) {
             const laya_rotary& r = L.kind == 0 ? m->rot_global : m->rot_local;
-            gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->d_pos, r.cos_t, r.sin_t,
+            gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->cur.pos, r.cos_t, r.sin_t,
                       2 * d);
         } else {
             linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv);
@@ -512,7 +555,7 @@ void forward(laya_model* m, const laya_batch* b, bool train, uint64_t seed) {
     // Final norm, then each question's type vector on its rows (TrainableDecisionModel.cs:294-304).
     float* h0 = m->cfg.head_layers > 0 ? m->ha[0].x : m->head_out;
     layernorm_fwd(ctx, m->x_final, T, d, m->W(m->final_norm), m->W(m->final_norm_b), eps, h0, m->fin_mean, m->fin_rstd,
-                  nullptr, m->W(m->type_emb), m->d_row_type);
+                  nullptr, m->W(m->type_emb), m->cur.row_type);
     const float p = train ? m->head_dropout : 0.0f;
     for (int j = 0; j < m->cfg.head_layers; ++j) {
         auto& H = m->head[j];
@@ -541,7 +584,7 @@ void forward(laya_model* m, const laya_batch* b, bool train, uint64_t seed) {
     }
     // Scorer at the option markers (TrainableDecisionModel.cs:313-323).
     const int M = m->nmark;
-    gather_rows(ctx, m->head_out, m->d_marker_rows, M, d, m->s_in);
+    gather_rows(ctx, m->head_out, m->cur.marker_rows, M, d, m->s_in);
     layernorm_fwd(ctx, m->s_in, M, d, m->W(m->sc_norm), m->W(m->sc_norm_b), 1e-5f, m->s_norm, m->s_mean, m->s_rstd);
     linear(m, m->s_norm, M, d, m->sc1, m->sc1_b, d, nullptr, m->s_pre);
     gelu_fwd(ctx, m->s_pre, (size_t)M * d, m->s_act);
@@ -621,10 +664,10 @@ void backward(laya_model* m) {
     layernorm_bwd(ctx, m->s_in, M, d, m->W(m->sc_norm), 1e-5f, m->ds_norm, m->ds_mark, m->Gt(m->sc_norm),
                   m->Gt(m->sc_norm_b), m->s_mean, m->s_rstd);
     fill(ctx, m->dS, 0.0f, (size_t)T * d);
-    scatter_add_rows(ctx, m->ds_mark, m->d_marker_rows, M, d, m->dS);
+    scatter_add_rows(ctx, m->ds_mark, m->cur.marker_rows, M, d, m->dS);
     for (int j = m->cfg.head_layers - 1; j >= 0; --j) head_backward(m, j);
     if (float* g = m->Gt(m->type_emb))
-        type_embedding_bwd(ctx, m->dS, m->d_seg_start, m->d_seg_len, m->d_qtypes, m->nseg, d, g);
+        type_embedding_bwd(ctx, m->dS, m->cur.seg_start, m->cur.seg_len, m->cur.qtypes, m->nseg, d, g);
     if (m->first_trainable >= m->cfg.layers) return;  // the encoder is frozen
     fill(ctx, m->dE, 0.0f, (size_t)T * d);
     layernorm_bwd(ctx, m->x_final, T, d, m->W(m->final_norm), eps, m->dS, m->dE, m->Gt(m->final_norm),
@@ -635,9 +678,9 @@ void backward(laya_model* m) {
     if (m->embeddings_trainable && m->first_trainable == 0) {
         fill(ctx, m->dE, 0.0f, (size_t)T * d);
         layernorm_bwd(ctx, m->W(m->tok_emb), T, d, m->W(m->emb_norm), eps, m->dS, m->dE, m->Gt(m->emb_norm),
-                      m->Gt(m->emb_norm_b), m->emb_mean, m->emb_rstd, m->d_tokens);
+                      m->Gt(m->emb_norm_b), m->emb_mean, m->emb_rstd, m->cur.tokens);
         if (float* g = m->Gt(m->tok_emb))
-            embedding_bwd(ctx, m->d_sorted, m->d_unique, m->d_uoff, m->n_unique, m->dE, d, g);
+            embedding_bwd(ctx, m->cur.sorted, m->cur.unique, m->cur.uoff, m->n_unique, m->dE, d, g);
     }
 }
 
@@ -743,6 +786,8 @@ int laya_model_destroy(laya_model* m) {
         for (void* p : {(void*)m->P, (void*)m->G, (void*)m->M1, (void*)m->M2, m->act_block, (void*)m->d_norm,
                         (void*)m->d_coef, (void*)m->d_loss, (void*)m->d_nonfinite})
             if (p) ctx->release(p);
+        for (auto& s : m->staged)
+            if (s.block) ctx->release(s.block);
         free_rotary(ctx, &m->rot_global);
         free_rotary(ctx, &m->rot_local);
         delete m;
@@ -865,7 +910,8 @@ int laya_model_set_head_dropout(laya_model* m, float p) {
 int laya_model_forward(laya_model* m, const laya_batch* batch, int training, uint64_t seed, float* logits_host) {
     return guarded([&] {
         checked(m);
-        forward(m, batch, training != 0, seed);
+        prepare_batch(m, batch);
+        forward(m, training != 0, seed);
         if (logits_host) {
             LAYA_HIP(hipMemcpyAsync(logits_host, m->scores, sizeof(float) * m->nmark, hipMemcpyDeviceToHost,
                                     m->ctx->stream));
@@ -914,26 +960,113 @@ int laya_model_zero_grad(laya_model* m) {
     });
 }
 
+}  // extern "C"
+
+namespace {
+
+// The optimizer step of Trainer.cs:131-144 on the current batch: forward, soft-CE gradient against
+// `targets` (device), backward, global-norm clip and AdamW.
+void train_step_current(laya_model* m, const float* targets, float ce_weight, float loss_scale, uint64_t seed,
+                        double max_norm, double lr_encoder, double lr_head, double beta1, double beta2, double eps,
+                        double weight_decay, float* loss_out) {
+    forward(m, true, seed);
+    softmax_ce_bwd(m->ctx, m->scores, targets, m->cur.opt_off, m->nseg, ce_weight, loss_scale, m->ds_scores,
+                   m->d_loss);
+    backward(m);
+    grad_norm(m->ctx, m->G, m->total, max_norm, m->d_norm, m->d_coef, m->d_nonfinite);
+    m->coef_valid = true;
+    adamw_step(m, lr_encoder, lr_head, beta1, beta2, eps, weight_decay, true);
+    if (loss_out) {
+        LAYA_HIP(hipMemcpyAsync(loss_out, m->d_loss, sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+    }
+}
+
+StagedBatch& staged_slot(laya_model* m, int slot) {
+    LAYA_REQUIRE(slot >= 0 && slot < (int)m->staged.size() && m->staged[slot].block,
+                 "staged batch: no such slot (never staged or already released)");
+    return m->staged[slot];
+}
+
+}  // namespace
+
+extern "C" {
+
 int laya_model_train_step(laya_model* m, const laya_batch* batch, const float* targets_host, float ce_weight,
                           float loss_scale, uint64_t seed, double max_norm, double lr_encoder, double lr_head,
                           double beta1, double beta2, double eps, double weight_decay, float* loss_out) {
     return guarded([&] {
         checked(m);
-        forward(m, batch, true, seed);
+        prepare_batch(m, batch);
         LAYA_REQUIRE(targets_host || m->nmark == 0, "train_step: null targets");
         if (m->nmark)
             LAYA_HIP(hipMemcpyAsync(m->targets, targets_host, sizeof(float) * m->nmark, hipMemcpyHostToDevice,
                                     m->ctx->stream));
-        softmax_ce_bwd(m->ctx, m->scores, m->targets, m->d_opt_off, m->nseg, ce_weight, loss_scale, m->ds_scores,
-                       m->d_loss);
-        backward(m);
-        grad_norm(m->ctx, m->G, m->total, max_norm, m->d_norm, m->d_coef, m->d_nonfinite);
-        m->coef_valid = true;
-        adamw_step(m, lr_encoder, lr_head, beta1, beta2, eps, weight_decay, true);
-        if (loss_out) {
-            LAYA_HIP(hipMemcpyAsync(loss_out, m->d_loss, sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));
-            LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+        train_step_current(m, m->targets, ce_weight, loss_scale, seed, max_norm, lr_encoder, lr_head, beta1, beta2,
+                           eps, weight_decay, loss_out);
+    });
+}
+
+int laya_model_stage_batch(laya_model* m, const laya_batch* batch, const float* targets_host, int* slot) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(slot, "stage_batch: null slot");
+        const BatchPlan bp = plan_batch(m, batch);
+        LAYA_REQUIRE(targets_host || bp.nmark == 0, "stage_batch: null targets");
+        // Size the shared activations now, so a step on this batch never allocates.
+        ensure_activations(m, bp.T, bp.nmark, bp.nseg);
+        ensure_rotary(m, bp.max_len);
+        StagedBatch s;
+        s.T = bp.T;
+        s.nseg = bp.nseg;
+        s.nmark = bp.nmark;
+        s.max_len = bp.max_len;
+        s.n_unique = bp.n_unique;
+        s.keys_full = bp.keys_full;
+        s.keys_local = bp.keys_local;
+        Carver cv;
+        TableCarve tc;
+        tc.add(cv, (size_t)bp.T, (size_t)std::max(bp.nmark, 1), (size_t)bp.nseg);
+        cv.add(s.targets, (size_t)std::max(bp.nmark, 1));
+        s.block = m->ctx->alloc(cv.bytes);
+        cv.bind(static_cast<char*>(s.block));
+        s.tables = tc.bind();
+        upload_tables(m, s.tables, bp);
+        if (bp.nmark)
+            LAYA_HIP(hipMemcpyAsync(s.targets, targets_host, sizeof(float) * bp.nmark, hipMemcpyHostToDevice,
+                                    m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));  // the host vectors go out of scope
+        int k = 0;
+        while (k < (int)m->staged.size() && m->staged[k].block) ++k;
+        if (k == (int)m->staged.size()) m->staged.emplace_back();
+        m->staged[k] = s;
+        *slot = k;
+    });
+}
+
+int laya_model_release_batch(laya_model* m, int slot) {
+    return guarded([&] {
+        checked(m);
+        StagedBatch& s = staged_slot(m, slot);
+        if (m->cur.tokens == s.tables.tokens) {  // it was the current batch: its tape goes with it
+            m->cur = m->own;
+            m->has_tape = false;
         }
+        m->ctx->release(s.block);
+        s = StagedBatch{};
+    });
+}
+
+int laya_model_train_step_staged(laya_model* m, int slot, float ce_weight, float loss_scale, uint64_t seed,
+                                 double max_norm, double lr_encoder, double lr_head, double beta1, double beta2,
+                                 double eps, double weight_decay, float* loss_out) {
+    return guarded([&] {
+        checked(m);
+        const StagedBatch& s = staged_slot(m, slot);
+        set_batch_sizes(m, s);
+        m->cur = s.tables;
+        train_step_current(m, s.targets, ce_weight, loss_scale, seed, max_norm, lr_encoder, lr_head, beta1, beta2,
+                           eps, weight_decay, loss_out);
     });
 }
 

@@ -210,3 +210,26 @@ class TrainableDecisionModel:
 
     def batch_args(self, batch: Batch) -> _BatchArgs:
         return _BatchArgs(batch)
+
+    def stage_batch(self, batch: Batch, targets: np.ndarray) -> int:
+        """Validates and uploads a batch and its soft-CE targets once; returns the slot train_step_staged
+        takes. The checks and errors are train_step's."""
+        args = _BatchArgs(batch)
+        t = np.ascontiguousarray(targets, np.float32)
+        slot = ctypes.c_int()
+        check(lib().laya_model_stage_batch(self.handle, ctypes.byref(args.struct), t.ctypes.data, ctypes.byref(slot)))
+        return slot.value
+
+    def train_step_staged(self, slot: int, seed: int, ce_weight: float = 1.0, loss_scale: float = 1.0,
+                          max_norm: float = 1.0, lr_encoder: float = 3e-5, lr_head: float = 3e-5, beta1: float = 0.9,
+                          beta2: float = 0.999, eps: float = 1e-8, weight_decay: float = 0.01,
+                          want_loss: bool = False) -> Optional[float]:
+        """train_step on a staged batch: every input is already in device memory."""
+        loss = ctypes.c_float()
+        check(lib().laya_model_train_step_staged(self.handle, slot, ce_weight, loss_scale, seed & (2 ** 64 - 1),
+                                                 max_norm, lr_encoder, lr_head, beta1, beta2, eps, weight_decay,
+                                                 ctypes.byref(loss) if want_loss else None))
+        return float(loss.value) if want_loss else None
+
+    def release_batch(self, slot: int) -> None:
+        check(lib().laya_model_release_batch(self.handle, slot))

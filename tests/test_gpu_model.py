@@ -189,3 +189,37 @@ def test_out_of_vocabulary_token_is_rejected_before_any_math(ctx):
                 n_options=np.array([1], np.int32), markers=np.array([0], np.int32), qtypes=np.array([0], np.int32))
     with pytest.raises(LayaOutOfRangeError):
         m.forward(bad)
+
+
+def test_staged_batches_train_exactly_like_batches_passed_by_value(ctx):
+    """A staged batch (validated and uploaded once) gives the same step as the batch passed by value:
+    same kernels on the same inputs, so identical losses and weights; two staged batches alternate;
+    a released slot is refused; staging validates like train_step."""
+    from laya_amd._native import LayaOutOfRangeError
+    from laya_amd.batch import Batch
+    from laya_amd.model import TrainableDecisionModel
+    mc, o, params, batch = _mid_case(layers=2, lengths=(150, 90, 33))
+    _, _, _, batch2 = _mid_case(layers=2, lengths=(64, 200), seed=3)
+    rng = np.random.default_rng(3)
+    t1 = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+    t2 = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch2.n_options])
+    a = TrainableDecisionModel(mc, ctx)
+    b = TrainableDecisionModel(mc, ctx)
+    a.set_params(params)
+    b.set_params(params)
+    s1, s2 = b.stage_batch(batch, t1), b.stage_batch(batch2, t2)
+    kw = dict(max_norm=1.0, lr_encoder=1e-3, lr_head=1e-3)
+    for seed, (bt, tt, slot) in enumerate([(batch, t1, s1), (batch2, t2, s2), (batch, t1, s1)]):
+        la = a.train_step(bt, tt, seed, loss_scale=float(bt.n_items), want_loss=True, **kw)
+        lb = b.train_step_staged(slot, seed, loss_scale=float(bt.n_items), want_loss=True, **kw)
+        assert la == lb
+    for name in a.names:
+        np.testing.assert_array_equal(a.param(name), b.param(name))
+    b.release_batch(s1)
+    with pytest.raises(ValueError):
+        b.train_step_staged(s1, 0)
+    bad = Batch(lengths=np.array([3], np.int32), tokens=np.array([1, mc.encoder.vocab_size, 2], np.int32),
+                n_options=np.array([1], np.int32), markers=np.array([0], np.int32), qtypes=np.array([0], np.int32))
+    with pytest.raises(LayaOutOfRangeError):
+        b.stage_batch(bad, np.ones(1, np.float32))
+    b.release_batch(s2)
