@@ -35,6 +35,12 @@ PEAK_FP32_MFMA = 157.3e12
 PEAK_HBM = 8.0e12
 MFMA_KERNELS = ("gemm_nt", "gemm_nn", "gemm_tn", "gemm_bwd_pair", "attention_fwd", "attention_bwd_dkv",
                 "attention_bwd_dq")
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload and
+# calibrated against a copy-like kernel of known size (the commands and the calibration sit in
+# profiles/gemm_bwd_pair_hbm_traffic.md). Counters cannot be read from inside the process, so the
+# figure is carried here for the kernel it was measured on and is reported only when that kernel is
+# the dominant one; any other dominant kernel reports null.
+MEASURED_TRAFFIC = {"gemm_bwd_pair": 1.753e9}
 
 
 def make_batch(rng, batch=32, seq=512, vocab=50368, pad_max=0.3):
@@ -88,8 +94,14 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
-    ap.add_argument("--cpu-items", type=int, default=8)
+    ap.add_argument("--cpu-items", type=int, default=16)
     ap.add_argument("--no-profile", action="store_true", help="time without per-launch events")
+    ap.add_argument("--by-value", action="store_true",
+                    help="pass each batch as host arrays (laya_model_train_step: host planning and uploads inside "
+                         "every step), to measure the PCIe-inclusive rate; the default stages batches first")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="before the steps, run one dst += src over 2^26 floats (add_kernel: 512 MiB read, 256 MiB "
+                         "written) whose HBM counters calibrate FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {args.gpus}).",
@@ -106,12 +118,29 @@ def main():
     ctx = Context(0)
     model = TrainableDecisionModel.synthetic(mc, seed=42, std=0.02, ctx=ctx)
     model.head_dropout = 0.1
+    if args.traffic_probe:
+        import ctypes
+        from laya_amd._native import check, lib
+        from laya_amd.device import DeviceArray
+        n = 1 << 26
+        dst, src = DeviceArray(ctx, (n,)), DeviceArray(ctx, (n,))
+        check(lib().laya_add(ctx.handle, dst.ptr, src.ptr, ctypes.c_size_t(n)))
+        ctx.sync()
+        dst.free()
+        src.free()
     # Every batch is validated, laid out and uploaded (with its targets) before timing: the timed steps
     # run on inputs already resident in HBM.
     slots = [model.stage_batch(b, t) for b, t in batches]
     ctx.sync()
 
+    by_value = [(b, t, model.batch_args(b)) for b, t in batches] if args.by_value else None
+
     def step(i):
+        if by_value:
+            b, t, a = by_value[i]
+            model.train_step(b, t, seed=1000 + i, ce_weight=1.0, loss_scale=float(b.n_items), max_norm=1.0,
+                             lr_encoder=3e-5, lr_head=3e-5, weight_decay=0.01, _args=a)
+            return
         model.train_step_staged(slots[i], seed=1000 + i, ce_weight=1.0, loss_scale=float(batches[i][0].n_items),
                                 max_norm=1.0, lr_encoder=3e-5, lr_head=3e-5, weight_decay=0.01)
 
@@ -152,11 +181,12 @@ def main():
             achieved = k["flops"] / k["launches"] / per_launch_s
             roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved / 1e12, 2),
                         "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
-                        "traffic": None, "avg_launch_ms": round(per_launch_s * 1e3, 4), "launches": k["launches"]}
+                        "traffic": MEASURED_TRAFFIC.get(name), "avg_launch_ms": round(per_launch_s * 1e3, 4),
+                        "launches": k["launches"]}
         else:
             achieved = k["bytes"] / k["launches"] / per_launch_s
             roofline = {"bound": "hbm", "kernel": name, "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
-                        "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
+                        "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": MEASURED_TRAFFIC.get(name),
                         "avg_launch_ms": round(per_launch_s * 1e3, 4), "launches": k["launches"]}
         bwd = [prof[n] for n in ("gemm_nn", "gemm_tn", "gemm_bwd_pair") if n in prof]
         if bwd:
@@ -189,7 +219,9 @@ def main():
                                    "seq 512, trailing padding U[0,0.3], heads choice8/score4/noul2, summed CE, "
                                    "AdamW lr 3e-5 wd 0.01, clip 1.0",
                        "global_batch": 32, "seq_len": 512, "parallelism": "none (1 GPU)",
-                       "real_tokens_per_step": round(tokens / args.steps, 1)},
+                       "real_tokens_per_step": round(tokens / args.steps, 1),
+                       "inputs": ("host arrays passed every step (PCIe-inclusive)" if args.by_value else
+                                  "staged in HBM before the timed steps")},
             "roofline": roofline, "cpu_baseline": cpu, "breakdown": breakdown}
     print(json.dumps(line), flush=True)
     model.close()
