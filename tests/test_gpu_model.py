@@ -125,6 +125,25 @@ def test_modernbert_base_width_gradients_match_the_oracle(ctx):
     print(f"worst relative L2 vs fp64 over {len(m.names)} tensors: {worst:.2e}", flush=True)
 
 
+def _assert_step_matches(o, m, params, lr):
+    """The weights after one optimizer step on the GPU against the oracle's step."""
+    for name in m.names:
+        if name == "scorer.3.bias":
+            # Σ over an item's options of the soft-CE gradient is exactly 0, so this bias's gradient is
+            # rounding noise in both implementations and Adam's first step normalises it to ±lr.
+            continue
+        delta_o = o.param(name) - params[name]
+        delta_g = m.param(name).astype(np.float64) - params[name]
+        if np.linalg.norm(delta_o) == 0:
+            assert np.linalg.norm(delta_g) == 0, name
+            continue
+        # Step 1 of Adam moves each weight by ≈ ±lr·sign(g), so a gradient within fp32 noise of zero may
+        # flip; require agreement on all but a vanishing fraction of elements.
+        flipped = np.mean(np.abs(delta_o - delta_g) > 0.5 * lr)
+        assert flipped < 1e-3, (name, flipped)
+        assert rel_l2(delta_o, delta_g) < 0.05, name
+
+
 def test_full_train_step_matches_the_oracle(ctx):
     """fwd → soft-CE gradient → bwd → clip → AdamW (Trainer.cs:131-144), then the updated weights."""
     from laya_amd.model import TrainableDecisionModel
@@ -144,23 +163,45 @@ def test_full_train_step_matches_the_oracle(ctx):
     o.backward(g)
     o.clip(1.0)
     o.adamw(lr, lr)
-    for name in m.names:
-        if name == "scorer.3.bias":
-            # Σ over an item's options of the soft-CE gradient is exactly 0, so this bias's gradient is
-            # rounding noise in both implementations and Adam's first step normalises it to ±lr.
-            continue
-        delta_o = o.param(name) - params[name]
-        delta_g = m.param(name).astype(np.float64) - params[name]
-        if np.linalg.norm(delta_o) == 0:
-            assert np.linalg.norm(delta_g) == 0, name
-            continue
-        # Step 1 of Adam moves each weight by ≈ ±lr·sign(g), so a gradient within fp32 noise of zero may
-        # flip; require agreement on all but a vanishing fraction of elements.
-        flipped = np.mean(np.abs(delta_o - delta_g) > 0.5 * lr)
-        assert flipped < 1e-3, (name, flipped)
-        assert rel_l2(delta_o, delta_g) < 0.05, name
+    _assert_step_matches(o, m, params, lr)
     # The step cleared the gradients.
     assert not np.any(m.grad("scorer.1.weight"))
+
+
+def test_full_modernbert_base_step_at_4x128_matches_the_oracle(ctx):
+    """The CPU-runnable configuration at full model size: ModernBERT-base (22 layers, vocab 50368,
+    164M parameters) plus the decision head, 4 sequences × 128 tokens without padding, ids U[0, 50368),
+    one choice head with K = 5 per item, labels U[0, 5), mean CE, head dropout 0.1, weights N(0, 0.02):
+    one optimizer step on the GPU against the oracle's."""
+    from laya_amd.batch import Batch
+    from laya_amd.config import modernbert_base
+    from laya_amd.model import TrainableDecisionModel
+    print("model: ModernBERT-base 22 layers, 4 x 128 tokens, one step", flush=True)
+    mc = modernbert_base()
+    o = oracle.OracleModel(mc)
+    params = random_params(o.shapes, 11, std=0.02)
+    rng = np.random.default_rng(12)
+    n, L, K = 4, 128, 5
+    batch = Batch(lengths=np.full(n, L, np.int32), tokens=rng.integers(0, 50368, n * L).astype(np.int32),
+                  n_options=np.full(n, K, np.int32), markers=np.tile(1 + 2 * np.arange(K), n).astype(np.int32),
+                  qtypes=np.zeros(n, np.int32))
+    targets = np.concatenate([np.eye(K, dtype=np.float32)[rng.integers(K)] for _ in range(n)])
+    seed, lr = 21, 1e-3
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    m.head_dropout = 0.1
+    loss_gpu = m.train_step(batch, targets, seed, loss_scale=1.0, max_norm=1.0, lr_encoder=lr, lr_head=lr,
+                            want_loss=True)
+    o.set_params(params)
+    o.set_head_dropout(0.1)
+    logits = o.forward(batch, training=True, keep_tape=True, seed=seed).astype(np.float32)
+    ce, g = oracle.cross_entropy(batch.n_options, logits, targets, 1.0, 1.0)
+    assert abs(loss_gpu - ce) < 1e-4 * max(1.0, abs(ce))
+    o.backward(g)
+    o.clip(1.0)
+    o.adamw(lr, lr)
+    _assert_step_matches(o, m, params, lr)
+    m.close()
 
 
 def test_gradients_are_bitwise_deterministic(ctx):

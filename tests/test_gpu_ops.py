@@ -151,6 +151,11 @@ ATTENTION_CASES = [
     (64, 2, [77, 5, 130], -1, 0.0, 0.1),
     (64, 12, [512, 400], 64, 10000.0, 0.0),
     (32, 2, [40, 200], 8, 10000.0, 0.3),
+    # Long-context shapes (2 × 8192, global θ 160000 and sliding ±64 θ 10000): RoPE positions to 8191,
+    # the dropout index's 21-bit key field near its top, and 64 query blocks per segment.
+    (64, 1, [8192, 8192], -1, 160000.0, 0.0),
+    (64, 2, [8192, 8192], 64, 10000.0, 0.0),
+    (64, 1, [8192], -1, 0.0, 0.1),
 ]
 
 
