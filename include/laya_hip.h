@@ -160,6 +160,15 @@ int laya_scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows_idx, 
 int laya_softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets, const int* option_offsets,
                         int n_items, float ce_weight, float scale, float* grad, float* loss);
 
+/* RlcdObjective.Compute (RlcdObjective.cs:57-155) with supplied draws, all operands on the device:
+ * option_offsets [n_items + 1] and qtypes [n_items] (int), logits / targets [total_options], draws
+ * [groups][total_options] (double); grad [total_options] = ∂loss/∂logit · scale; losses [4] (double):
+ * total, policy, cross-entropy, mean reward. max_options (≤ 64) bounds any item's option count. */
+int laya_rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets, const int* option_offsets,
+                        const int* qtypes, int n_items, int total_options, int max_options, int groups,
+                        const double* draws, double sigma, double spherical_weight, double rps_weight,
+                        double ce_weight, double scale, float* grad, double* losses);
+
 /* Gradients.ClipByGlobalNorm (AdamW.cs:103-130) over a flat arena: Σg² in double, in a fixed order.
  * Writes the norm (double) and the clip coefficient (float, 1 when not clipping) to device memory.
  * Sets LAYA_ERR_NOT_FINITE only through laya_grad_norm_status. */
@@ -229,6 +238,18 @@ int laya_model_train_step(laya_model* model, const laya_batch* batch, const floa
                           float loss_scale, uint64_t seed, double max_norm, double lr_encoder, double lr_head,
                           double beta1, double beta2, double eps, double weight_decay, float* loss_out);
 int laya_model_steps(laya_model* model, int* steps);
+
+/* RlcdObjective.Compute on the last forward's logits (RlcdObjective.cs:57-155, as Trainer.cs:134-136 calls it),
+ * with the standard-normal draws supplied as in its second overload: targets_host [Σ n_options], draws_host
+ * [groups][Σ n_options] (double). The scaled logit gradient stays on the device for
+ * laya_model_backward_from_objective; losses_host [4] = total, policy, cross-entropy, mean reward (may be
+ * NULL; non-NULL synchronises). At most 64 options per item. */
+int laya_model_objective_rlcd(laya_model* model, const float* targets_host, const double* draws_host, int groups,
+                              double sigma, double spherical_weight, double rps_weight, double ce_weight,
+                              double scale, double* losses_host);
+/* TrainableDecisionModel.Backward (TrainableDecisionModel.cs:479-549) from the logit gradient the last
+ * objective left on the device (no host round trip). */
+int laya_model_backward_from_objective(laya_model* model);
 
 /* Device-resident batches. No counterpart in the reference, whose batches are host arrays: these split
  * laya_model_train_step's host work (validation, layout, embedding-gradient plan, uploads) from the

@@ -108,6 +108,8 @@ SIGNATURES = {
     "laya_gather_rows": (c_int, [P, P, P, c_int, c_int, P]),
     "laya_scatter_add_rows": (c_int, [P, P, P, c_int, c_int, P]),
     "laya_softmax_ce_bwd": (c_int, [P, P, P, P, c_int, c_float, c_float, P, P]),
+    "laya_rlcd_objective": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_double, c_double, c_double,
+                                    c_double, c_double, P, P]),
     "laya_grad_norm": (c_int, [P, P, c_size, c_double, P, P]),
     "laya_adamw": (c_int, [P, P, P, P, P, c_int, P, P, P, c_double, c_double, c_double, c_double, c_int, P, c_int]),
     "laya_model_create": (c_int, [P, ctypes.POINTER(ModelConfigC), PP]),
@@ -126,6 +128,8 @@ SIGNATURES = {
     "laya_model_set_head_dropout": (c_int, [P, c_float]),
     "laya_model_forward": (c_int, [P, ctypes.POINTER(BatchC), c_int, c_u64, P]),
     "laya_model_backward": (c_int, [P, P]),
+    "laya_model_objective_rlcd": (c_int, [P, P, P, c_int, c_double, c_double, c_double, c_double, c_double, P]),
+    "laya_model_backward_from_objective": (c_int, [P]),
     "laya_model_clip_grad_norm": (c_int, [P, c_double, ctypes.POINTER(c_double)]),
     "laya_model_adamw_step": (c_int, [P, c_double, c_double, c_double, c_double, c_double, c_double]),
     "laya_model_zero_grad": (c_int, [P]),

@@ -597,6 +597,19 @@ int laya_softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets
     });
 }
 
+int laya_rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets, const int* option_offsets,
+                        const int* qtypes, int n_items, int total_options, int max_options, int groups,
+                        const double* draws, double sigma, double spherical_weight, double rps_weight,
+                        double ce_weight, double scale, float* grad, double* losses) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(n_items == 0 || (logits && targets && option_offsets && qtypes && draws && grad && losses),
+                     "rlcd: null tensor");
+        rlcd_objective(ctx, logits, targets, option_offsets, qtypes, n_items, total_options, max_options, groups, draws,
+                       sigma, spherical_weight, rps_weight, ce_weight, scale, grad, losses);
+    });
+}
+
 int laya_grad_norm(laya_ctx* ctx, const float* grads, size_t n, double max_norm, double* norm_out, float* coef_out) {
     return guarded([&] {
         require_ctx(ctx);

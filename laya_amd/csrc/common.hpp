@@ -224,6 +224,12 @@ inline double window_keys(int L, int hw) {
     return s;
 }
 void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse);
+
+// RlcdObjective.Compute (RlcdObjective.cs:57-155) with supplied standard-normal draws [groups][Σ K], all
+// operands on the device; grad [Σ K]; losses [4] = total, policy, cross-entropy, mean reward.
+void rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets, const int* offsets, const int* qtypes,
+                    int n_items, int total_options, int max_options, int groups, const double* draws, double sigma,
+                    double spherical, double rps, double ce_weight, double scale, float* grad, double* losses);
 // rows: the number of rows of qkv / context / dcontext (the dO·O row constants span all of them).
 void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,
                    const float* dcontext, float* dqkv);

@@ -62,7 +62,7 @@ struct BatchTables {
 
 // A batch planned on the host and uploaded once, ahead of the steps that use it.
 struct StagedBatch {
-    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0;
+    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0;
     double keys_full = 0, keys_local = 0;
     void* block = nullptr;  // the tables, then the soft-CE targets
     BatchTables tables{};
@@ -71,7 +71,7 @@ struct StagedBatch {
 
 // Host-side layout of one batch: every table the kernels read, before upload.
 struct BatchPlan {
-    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0;
+    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0;
     double keys_full = 0, keys_local = 0;
     std::vector<int> tokens, start, len, marker_rows, qtypes, opt_off, row_type, sorted, unique, uoff, pos;
 };
@@ -162,8 +162,12 @@ struct laya_model {
     // ----- the batch of the last forward
     bool has_tape = false, training = false;
     uint64_t seed = 0;
-    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0;
+    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0;
     double keys_full = 0, keys_local = 0;  // Σ_q attended keys of the batch, full and sliding window
+    // RLCD objective: the draws of the last call (device, grown on demand) and its losses
+    double* d_draws = nullptr;
+    size_t draws_cap = 0;
+    double* d_rlcd_losses = nullptr;
 
     int d() const { return cfg.hidden; }
     int I() const { return cfg.intermediate; }
@@ -368,6 +372,7 @@ BatchPlan plan_batch(const laya_model* m, const laya_batch* b) {
         total += b->lengths[i];
         marks += b->n_options[i];
         longest = std::max(longest, b->lengths[i]);
+        bp.max_opts = std::max(bp.max_opts, b->n_options[i]);
     }
     bp.T = (int)total;
     bp.nseg = n;
@@ -430,6 +435,7 @@ template <typename B> void set_batch_sizes(laya_model* m, const B& b) {
     m->nmark = b.nmark;
     m->max_len = b.max_len;
     m->n_unique = b.n_unique;
+    m->max_opts = b.max_opts;
     m->keys_full = b.keys_full;
     m->keys_local = b.keys_local;
     ensure_activations(m, b.T, b.nmark, b.nseg);
@@ -788,6 +794,8 @@ int laya_model_destroy(laya_model* m) {
             if (p) ctx->release(p);
         for (auto& s : m->staged)
             if (s.block) ctx->release(s.block);
+        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses})
+            if (p) ctx->release(p);
         free_rotary(ctx, &m->rot_global);
         free_rotary(ctx, &m->rot_local);
         delete m;
@@ -1022,6 +1030,7 @@ int laya_model_stage_batch(laya_model* m, const laya_batch* batch, const float* 
         s.nmark = bp.nmark;
         s.max_len = bp.max_len;
         s.n_unique = bp.n_unique;
+        s.max_opts = bp.max_opts;
         s.keys_full = bp.keys_full;
         s.keys_local = bp.keys_local;
         Carver cv;
@@ -1041,6 +1050,46 @@ int laya_model_stage_batch(laya_model* m, const laya_batch* batch, const float* 
         if (k == (int)m->staged.size()) m->staged.emplace_back();
         m->staged[k] = s;
         *slot = k;
+    });
+}
+
+int laya_model_objective_rlcd(laya_model* m, const float* targets_host, const double* draws_host, int groups,
+                              double sigma, double spherical_weight, double rps_weight, double ce_weight,
+                              double scale, double* losses_host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(m->has_tape, "objective: run forward first");
+        LAYA_REQUIRE(groups >= 1, "objective: at least one group");
+        LAYA_REQUIRE(m->nmark == 0 || (targets_host && draws_host), "objective: null targets or draws");
+        const size_t draws = (size_t)groups * m->nmark;
+        if (m->draws_cap < draws) {
+            if (m->d_draws) m->ctx->release(m->d_draws);
+            m->d_draws = static_cast<double*>(m->ctx->alloc(sizeof(double) * draws));
+            m->draws_cap = draws;
+        }
+        if (!m->d_rlcd_losses) m->d_rlcd_losses = static_cast<double*>(m->ctx->alloc(sizeof(double) * 4));
+        if (m->nmark) {
+            LAYA_HIP(hipMemcpyAsync(m->targets, targets_host, sizeof(float) * m->nmark, hipMemcpyHostToDevice,
+                                    m->ctx->stream));
+            LAYA_HIP(hipMemcpyAsync(m->d_draws, draws_host, sizeof(double) * draws, hipMemcpyHostToDevice,
+                                    m->ctx->stream));
+        }
+        rlcd_objective(m->ctx, m->scores, m->targets, m->cur.opt_off, m->cur.qtypes, m->nseg, m->nmark, m->max_opts,
+                       groups, m->d_draws, sigma, spherical_weight, rps_weight, ce_weight, scale, m->ds_scores,
+                       m->d_rlcd_losses);
+        if (losses_host) {
+            LAYA_HIP(hipMemcpyAsync(losses_host, m->d_rlcd_losses, sizeof(double) * 4, hipMemcpyDeviceToHost,
+                                    m->ctx->stream));
+            LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+        }
+    });
+}
+
+int laya_model_backward_from_objective(laya_model* m) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(m->has_tape, "backward: run forward first");
+        backward(m);
     });
 }
 

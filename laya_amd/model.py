@@ -176,6 +176,23 @@ class TrainableDecisionModel:
         d = np.ascontiguousarray(logit_gradients, np.float32)
         check(lib().laya_model_backward(self.handle, d.ctypes.data))
 
+    def objective_rlcd(self, targets, draws, sigma: float, spherical_weight: float = 0.75, rps_weight: float = 1.0,
+                       ce_weight: float = 1.0, scale: float = 1.0) -> tuple:
+        """RlcdObjective.Compute on the last forward's logits, on the device (RlcdObjective.cs:57-155):
+        targets [Σ n_options], draws [groups][Σ n_options] standard normal. The logit gradient stays on
+        the device for backward_from_objective. Returns (loss, policy, cross-entropy, mean reward)."""
+        t = np.ascontiguousarray(targets, np.float32).reshape(-1)
+        z = np.ascontiguousarray(draws, np.float64)
+        groups = z.shape[0] if z.ndim > 1 else max(1, z.size // max(1, t.size))
+        out = np.zeros(4, np.float64)
+        check(lib().laya_model_objective_rlcd(self.handle, t.ctypes.data, z.ctypes.data, groups, sigma,
+                                              spherical_weight, rps_weight, ce_weight, scale, out.ctypes.data))
+        return tuple(float(v) for v in out)
+
+    def backward_from_objective(self) -> None:
+        """Backward from the logit gradient objective_rlcd left on the device."""
+        check(lib().laya_model_backward_from_objective(self.handle))
+
     def zero_gradients(self) -> None:
         check(lib().laya_model_zero_grad(self.handle))
 

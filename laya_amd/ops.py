@@ -264,6 +264,26 @@ def softmax_ce_backward(ctx: Context, logits: DeviceArray, targets: DeviceArray,
                                     grad.ptr, ptr(loss)))
 
 
+def rlcd_objective(ctx: Context, logits: DeviceArray, targets: DeviceArray, option_offsets: DeviceArray,
+                   qtypes: DeviceArray, n_options, draws: DeviceArray, groups: int, sigma: float,
+                   spherical_weight: float = 0.75, rps_weight: float = 1.0, ce_weight: float = 1.0,
+                   scale: float = 1.0, grad: Optional[DeviceArray] = None) -> tuple:
+    """RlcdObjective.Compute (RlcdObjective.cs:57-155) with supplied standard-normal draws
+    [groups][Σ n_options] (a float64 device array), on the device. Returns (losses, grad): losses =
+    (total, policy, cross-entropy, mean reward), grad the scaled logit gradient (device)."""
+    n_options = np.asarray(n_options, np.int64)
+    total, longest = int(n_options.sum()), int(n_options.max()) if n_options.size else 0
+    grad = grad or DeviceArray(ctx, (max(total, 1),))
+    losses = DeviceArray(ctx, (8,))  # four doubles
+    check(lib().laya_rlcd_objective(_h(ctx), logits.ptr, targets.ptr, option_offsets.ptr, qtypes.ptr, len(n_options),
+                                    total, longest, groups, draws.ptr, sigma, spherical_weight, rps_weight, ce_weight,
+                                    scale, grad.ptr, losses.ptr))
+    out = np.zeros(4, np.float64)
+    check(lib().laya_download(_h(ctx), out.ctypes.data, losses.ptr, 32))
+    losses.free()
+    return tuple(float(v) for v in out), grad
+
+
 def layer_norm_eps_default() -> float:
     return 1e-5
 

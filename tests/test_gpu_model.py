@@ -264,3 +264,30 @@ def test_staged_batches_train_exactly_like_batches_passed_by_value(ctx):
     with pytest.raises(LayaOutOfRangeError):
         b.stage_batch(bad, np.ones(1, np.float32))
     b.release_batch(s2)
+
+
+def test_rlcd_step_on_the_device_matches_the_host_objective(ctx):
+    """Forward → RLCD objective on the device → backward from the device gradient gives the gradients of
+    forward → the oracle's objective on the host logits → backward (Trainer.cs:134-137)."""
+    from laya_amd.model import TrainableDecisionModel
+    mc, o, params, batch = _mid_case(layers=2, lengths=(150, 90, 33))
+    rng = np.random.default_rng(4)
+    targets = np.concatenate([rng.dirichlet(np.ones(k)) for k in batch.n_options]).astype(np.float32)
+    draws = rng.standard_normal((4, batch.n_markers))
+    a = TrainableDecisionModel(mc, ctx)
+    b = TrainableDecisionModel(mc, ctx)
+    a.set_params(params)
+    b.set_params(params)
+    logits = a.forward(batch, training=True, seed=6)
+    losses = a.objective_rlcd(targets, draws, 0.3, scale=0.5)
+    a.backward_from_objective()
+    b.forward(batch, training=True, seed=6)
+    out, g = oracle.rlcd(batch.n_options, batch.qtypes, logits, targets, draws.reshape(-1), 0.3, scale=0.5)
+    np.testing.assert_allclose(losses, out, rtol=1e-5, atol=1e-6)
+    b.backward(g)
+    for name in a.names:
+        if b.has_grad(name):
+            # The output bias gradient is Σ dlogits, exactly 0 (softmax gradients sum to zero per item):
+            # both sides hold rounding noise there, hence the absolute floor.
+            want, got = b.grad(name), a.grad(name)
+            assert np.linalg.norm(got - want) <= 1e-5 * np.linalg.norm(want) + 1e-6, name

@@ -287,3 +287,54 @@ def test_adamw_and_clip_match_the_oracle(ctx):
     assert rel_l2(pr, pd.numpy()) < 1e-6
     assert rel_l2(mr, md.numpy()) < 1e-6
     assert rel_l2(vr, vd.numpy()) < 1e-6
+
+
+def _device_f64(ctx, a):
+    """A float64 array on the device (DeviceArray holds 4-byte elements: twice as many)."""
+    from laya_amd.device import DeviceArray
+    a = np.ascontiguousarray(a, np.float64)
+    d = DeviceArray(ctx, (2 * max(a.size, 1),), np.float32, zero=False)
+    if a.size:
+        d.upload(a.view(np.float32))
+    return d
+
+
+def _rlcd_on_device(ctx, ks, qtypes, logits, targets, draws, sigma, **kw):
+    offsets = np.concatenate([[0], np.cumsum(ks)]).astype(np.int32)
+    return laya.rlcd_objective(ctx, dev(ctx, logits), dev(ctx, targets), dev(ctx, offsets),
+                               dev(ctx, np.asarray(qtypes, np.int32)), ks, _device_f64(ctx, draws),
+                               len(draws) // len(logits), sigma, **kw)
+
+
+def test_rlcd_objective_matches_the_notebook_fixture(ctx):
+    """The reference's objective golden values (the notebook's loss terms and logit gradient)."""
+    from fixtures import objective_fixture
+    fx = objective_fixture()
+    ks = fx["ks"]
+    logits = np.concatenate(fx["logits"]).astype(np.float32)
+    target = np.concatenate(fx["target"]).astype(np.float32)
+    draws = np.concatenate([np.concatenate(g) for g in fx["draws"]])
+    (loss, policy, ce, reward), grad = _rlcd_on_device(ctx, ks, fx["qtypes"], logits, target, draws, fx["sigma"])
+    assert abs(ce - fx["loss_ce"]) < 1e-5
+    assert abs(policy - fx["loss_rl"]) < 1e-4
+    assert abs(reward - fx["reward_mean"]) < 1e-4
+    assert abs(loss - fx["loss"]) < 1e-4
+    np.testing.assert_allclose(grad.numpy()[:logits.size], np.concatenate(fx["grad"]), atol=1e-4)
+
+
+def test_rlcd_objective_matches_the_oracle_at_batch_size(ctx):
+    """32 items cycling choice K = 8 / score K = 4 / noul K = 2 plus one 64-option item, G = 4, soft targets,
+    σ 0.4, weights off their defaults, gradient scale 1/4 (accumulation)."""
+    rng = np.random.default_rng(8)
+    ks = [8, 4, 2] * 11 + [64]
+    qtypes = [0, 1, 2] * 11 + [1]
+    logits = rng.standard_normal(sum(ks)).astype(np.float32)
+    targets = np.concatenate([rng.dirichlet(np.ones(k)) for k in ks]).astype(np.float32)
+    G = 4
+    draws = rng.standard_normal(G * sum(ks))
+    kw = dict(spherical_weight=0.6, rps_weight=0.8, ce_weight=0.5, scale=0.25)
+    (loss, policy, ce, reward), grad = _rlcd_on_device(ctx, ks, qtypes, logits, targets, draws, 0.4, **kw)
+    out, g = oracle.rlcd(ks, qtypes, logits, targets, draws, 0.4, spherical=0.6, rps=0.8, ce_weight=0.5, scale=0.25)
+    # fp32 softmax on both sides; device and host exp may differ by an ulp.
+    np.testing.assert_allclose([loss, policy, ce, reward], out, rtol=1e-5, atol=1e-6)
+    assert rel_l2(g, grad.numpy()[:logits.size]) < 1e-5
