@@ -163,7 +163,8 @@ int laya_softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets
 /* RlcdObjective.Compute (RlcdObjective.cs:57-155) with supplied draws, all operands on the device:
  * option_offsets [n_items + 1] and qtypes [n_items] (int), logits / targets [total_options], draws
  * [groups][total_options] (double); grad [total_options] = ∂loss/∂logit · scale; losses [4] (double):
- * total, policy, cross-entropy, mean reward. max_options (≤ 64) bounds any item's option count. */
+ * total, policy, cross-entropy, mean reward. max_options (≤ 64) bounds any item's option count.
+ * groups = 0 is the cross-entropy-only objective (no draws read; mean reward NaN, as 0/0 in the reference). */
 int laya_rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets, const int* option_offsets,
                         const int* qtypes, int n_items, int total_options, int max_options, int groups,
                         const double* draws, double sigma, double spherical_weight, double rps_weight,
@@ -238,12 +239,18 @@ int laya_model_train_step(laya_model* model, const laya_batch* batch, const floa
                           float loss_scale, uint64_t seed, double max_norm, double lr_encoder, double lr_head,
                           double beta1, double beta2, double eps, double weight_decay, float* loss_out);
 int laya_model_steps(laya_model* model, int* steps);
+/* Adam moments of parameter i (numel floats each; zeros before the first step) and the step count
+ * that drives bias correction. No counterpart in the reference, whose trainer cannot resume (TODO.md:74):
+ * the moments are what a checkpoint needs beyond the weights (AdamW.cs:24 keeps them per parameter). */
+int laya_model_get_moments(laya_model* model, int i, float* m1_host, float* m2_host);
+int laya_model_set_moments(laya_model* model, int i, const float* m1_host, const float* m2_host);
+int laya_model_set_steps(laya_model* model, int steps);
 
 /* RlcdObjective.Compute on the last forward's logits (RlcdObjective.cs:57-155, as Trainer.cs:134-136 calls it),
  * with the standard-normal draws supplied as in its second overload: targets_host [Σ n_options], draws_host
  * [groups][Σ n_options] (double). The scaled logit gradient stays on the device for
  * laya_model_backward_from_objective; losses_host [4] = total, policy, cross-entropy, mean reward (may be
- * NULL; non-NULL synchronises). At most 64 options per item. */
+ * NULL; non-NULL synchronises). At most 64 options per item; groups = 0 drops the policy term. */
 int laya_model_objective_rlcd(laya_model* model, const float* targets_host, const double* draws_host, int groups,
                               double sigma, double spherical_weight, double rps_weight, double ce_weight,
                               double scale, double* losses_host);

@@ -136,6 +136,9 @@ SIGNATURES = {
     "laya_model_train_step": (c_int, [P, ctypes.POINTER(BatchC), P, c_float, c_float, c_u64, c_double, c_double,
                                       c_double, c_double, c_double, c_double, c_double, ctypes.POINTER(c_float)]),
     "laya_model_steps": (c_int, [P, ctypes.POINTER(c_int)]),
+    "laya_model_get_moments": (c_int, [P, c_int, P, P]),
+    "laya_model_set_moments": (c_int, [P, c_int, P, P]),
+    "laya_model_set_steps": (c_int, [P, c_int]),
     "laya_model_stage_batch": (c_int, [P, ctypes.POINTER(BatchC), P, ctypes.POINTER(c_int)]),
     "laya_model_train_step_staged": (c_int, [P, c_int, c_float, c_float, c_u64, c_double, c_double, c_double, c_double,
                                              c_double, c_double, c_double, ctypes.POINTER(c_float)]),

@@ -1059,8 +1059,8 @@ int laya_model_objective_rlcd(laya_model* m, const float* targets_host, const do
     return guarded([&] {
         checked(m);
         LAYA_REQUIRE(m->has_tape, "objective: run forward first");
-        LAYA_REQUIRE(groups >= 1, "objective: at least one group");
-        LAYA_REQUIRE(m->nmark == 0 || (targets_host && draws_host), "objective: null targets or draws");
+        LAYA_REQUIRE(groups >= 0, "objective: negative group count");
+        LAYA_REQUIRE(m->nmark == 0 || (targets_host && (groups == 0 || draws_host)), "objective: null targets or draws");
         const size_t draws = (size_t)groups * m->nmark;
         if (m->draws_cap < draws) {
             if (m->d_draws) m->ctx->release(m->d_draws);
@@ -1071,8 +1071,9 @@ int laya_model_objective_rlcd(laya_model* m, const float* targets_host, const do
         if (m->nmark) {
             LAYA_HIP(hipMemcpyAsync(m->targets, targets_host, sizeof(float) * m->nmark, hipMemcpyHostToDevice,
                                     m->ctx->stream));
-            LAYA_HIP(hipMemcpyAsync(m->d_draws, draws_host, sizeof(double) * draws, hipMemcpyHostToDevice,
-                                    m->ctx->stream));
+            if (draws)
+                LAYA_HIP(hipMemcpyAsync(m->d_draws, draws_host, sizeof(double) * draws, hipMemcpyHostToDevice,
+                                        m->ctx->stream));
         }
         rlcd_objective(m->ctx, m->scores, m->targets, m->cur.opt_off, m->cur.qtypes, m->nseg, m->nmark, m->max_opts,
                        groups, m->d_draws, sigma, spherical_weight, rps_weight, ce_weight, scale, m->ds_scores,
@@ -1121,6 +1122,47 @@ int laya_model_train_step_staged(laya_model* m, int slot, float ce_weight, float
 
 int laya_model_steps(laya_model* m, int* steps) {
     return guarded([&] { *steps = checked(m)->steps; });
+}
+
+// Optimizer state in and out, one parameter at a time, for checkpoints that resume training.
+int laya_model_get_moments(laya_model* m, int i, float* m1_host, float* m2_host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(i >= 0 && i < (int)m->params.size() && m1_host && m2_host, "get_moments: bad argument");
+        const Param& p = m->params[i];
+        if (!m->M1) {  // no step taken yet: both moments are zero
+            std::fill(m1_host, m1_host + p.numel, 0.0f);
+            std::fill(m2_host, m2_host + p.numel, 0.0f);
+            return;
+        }
+        LAYA_HIP(hipMemcpyAsync(m1_host, m->M1 + p.offset, p.numel * sizeof(float), hipMemcpyDeviceToHost,
+                                m->ctx->stream));
+        LAYA_HIP(hipMemcpyAsync(m2_host, m->M2 + p.offset, p.numel * sizeof(float), hipMemcpyDeviceToHost,
+                                m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+    });
+}
+
+int laya_model_set_moments(laya_model* m, int i, const float* m1_host, const float* m2_host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(i >= 0 && i < (int)m->params.size() && m1_host && m2_host, "set_moments: bad argument");
+        const Param& p = m->params[i];
+        ensure_moments(m);
+        LAYA_HIP(hipMemcpyAsync(m->M1 + p.offset, m1_host, p.numel * sizeof(float), hipMemcpyHostToDevice,
+                                m->ctx->stream));
+        LAYA_HIP(hipMemcpyAsync(m->M2 + p.offset, m2_host, p.numel * sizeof(float), hipMemcpyHostToDevice,
+                                m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+    });
+}
+
+int laya_model_set_steps(laya_model* m, int steps) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(steps >= 0, "set_steps: negative step count");
+        m->steps = steps;
+    });
 }
 
 }  // extern "C"

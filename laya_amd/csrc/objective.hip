@@ -169,12 +169,14 @@ __global__ __launch_bounds__(THREADS) void rlcd_kernel(RlcdArgs a) {
 void rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets, const int* offsets, const int* qtypes,
                     int n_items, int total_options, int max_options, int groups, const double* draws, double sigma,
                     double spherical, double rps, double ce_weight, double scale, float* grad, double* losses) {
-    LAYA_REQUIRE(n_items >= 0 && groups >= 1 && total_options >= 0, "rlcd: bad size");
+    // Zero groups is the cross-entropy-only objective: the policy term vanishes and the mean reward is
+    // 0/0, NaN, as in the reference. Zero items still writes the losses.
+    LAYA_REQUIRE(n_items >= 0 && groups >= 0 && total_options >= 0, "rlcd: bad size");
     LAYA_REQUIRE(max_options <= MAX_OPTIONS, "rlcd: at most 64 options per item");
-    LAYA_REQUIRE(sigma > 0.0, "rlcd: sigma must be positive");
-    if (n_items == 0) return;
+    LAYA_REQUIRE(groups == 0 || sigma > 0.0, "rlcd: sigma must be positive");
+    LAYA_REQUIRE(offsets && losses, "rlcd: null offsets or losses");
     const size_t scratch = sizeof(double) * ((size_t)groups * total_options + (size_t)groups * n_items + 3 * (size_t)n_items);
-    double* base = static_cast<double*>(ctx->workspace(5, scratch));
+    double* base = static_cast<double*>(ctx->workspace(5, std::max<size_t>(scratch, 64)));
     RlcdArgs a{};
     a.logits = logits;
     a.targets = targets;

@@ -8,7 +8,9 @@ marker rows go in, and logits come out (dlogits go back in).
 from __future__ import annotations
 
 import ctypes
+import json
 import os
+import shutil
 from typing import Dict, List, Optional, Sequence
 
 import numpy as np
@@ -18,6 +20,7 @@ from .batch import Batch, TrainingItem
 from .config import ModelConfig
 from .device import Context
 from .safetensors_io import SafetensorsFile
+from .safetensors_io import write as write_safetensors
 
 
 def _config_struct(mc: ModelConfig):
@@ -74,6 +77,11 @@ class TrainableDecisionModel:
             self.index[nm] = i
         self._batch: Optional[Batch] = None
         self._head_dropout = 0.1
+        # What Save writes back (TrainableDecisionModel.cs:649-661): the source's tensors in file order,
+        # each in the dtype it was stored in; tensors the model does not use are kept as read.
+        self.stored_dtypes: Dict[str, str] = {n: "F32" for n in self.names}
+        self.file_order: List[str] = list(self.names)
+        self.extra_tensors: Dict[str, np.ndarray] = {}
 
     def close(self) -> None:
         if getattr(self, "handle", None) and getattr(self.ctx, "handle", None):
@@ -99,7 +107,77 @@ class TrainableDecisionModel:
                     continue
                 raise KeyError(f"the checkpoint has no '{name}' tensor; is it a laya decision model?")
             model.set_param(name, st.read_float32(name))
+        model.file_order = st.names_in_file_order()
+        model.stored_dtypes = {n: st.dtype(n) for n in model.file_order}
+        model.extra_tensors = {n: st.read_float32(n) for n in model.file_order if n not in model.index}
         return model
+
+    def save(self, directory: str, source_directory: str, config: dict) -> None:
+        """TrainableDecisionModel.Save (TrainableDecisionModel.cs:649-661): model.safetensors with every
+        tensor in its stored dtype (BF16 rounds to nearest even), the source's encoder/ and tokenizer/
+        copied, and ``config`` as rl_agent_config.json."""
+        os.makedirs(directory, exist_ok=True)
+        tensors = []
+        for name in self.file_order:
+            values = self.extra_tensors[name] if name in self.extra_tensors else self.param(name)
+            dtype = self.stored_dtypes.get(name, "F32")
+            tensors.append((name, tuple(values.shape), values, dtype if dtype in ("F32", "F16", "BF16") else "F32"))
+        write_safetensors(os.path.join(directory, "model.safetensors"), tensors)
+        for sub, required in (("encoder", True), ("tokenizer", False)):
+            src, dst = os.path.join(source_directory, sub), os.path.join(directory, sub)
+            if not os.path.isdir(src):
+                if required:
+                    raise FileNotFoundError(f"{src}: the source checkpoint has no {sub} directory")
+                continue
+            if os.path.abspath(src) != os.path.abspath(dst):
+                shutil.copytree(src, dst, dirs_exist_ok=True)
+        with open(os.path.join(directory, "rl_agent_config.json"), "w") as f:
+            json.dump(config, f, indent=2)
+
+    # Optimizer state (the reference trainer cannot resume, TODO.md:74; its AdamW keeps these per
+    # parameter, AdamW.cs:24): both moments of every trainable tensor and the step count.
+    def optimizer_state(self) -> Dict[str, tuple]:
+        out = {}
+        for name in self.names:
+            if not self.trainable(name):
+                continue
+            m1 = np.empty(self.shapes[name], np.float32)
+            m2 = np.empty(self.shapes[name], np.float32)
+            check(lib().laya_model_get_moments(self.handle, self.index[name], m1.ctypes.data, m2.ctypes.data))
+            out[name] = (m1, m2)
+        return out
+
+    def save_optimizer_state(self, path: str) -> None:
+        """Writes the moments as F32 tensors 'exp_avg.<name>' / 'exp_avg_sq.<name>', an F32 master copy
+        'master.<name>' of every tensor the checkpoint stores in a narrower dtype (so a resumed run starts
+        from the exact weights, not their rounding), and the step count in a JSON side file."""
+        tensors = []
+        for name, (m1, m2) in self.optimizer_state().items():
+            tensors.append(("exp_avg." + name, m1.shape, m1, "F32"))
+            tensors.append(("exp_avg_sq." + name, m2.shape, m2, "F32"))
+        for name in self.names:
+            if self.stored_dtypes.get(name, "F32") != "F32":
+                values = self.param(name)
+                tensors.append(("master." + name, values.shape, values, "F32"))
+        write_safetensors(path, tensors)
+        with open(path + ".json", "w") as f:
+            json.dump({"steps": self.steps}, f)
+
+    def load_optimizer_state(self, path: str) -> None:
+        """Restores what save_optimizer_state wrote: master weights, moments and the step count."""
+        st = SafetensorsFile(path)
+        with open(path + ".json") as f:
+            steps = int(json.load(f)["steps"])
+        for name in self.names:
+            if ("master." + name) in st.entries:
+                self.set_param(name, st.read_float32("master." + name))
+            if ("exp_avg." + name) in st.entries:
+                m1 = np.ascontiguousarray(st.read_float32("exp_avg." + name), np.float32)
+                m2 = np.ascontiguousarray(st.read_float32("exp_avg_sq." + name), np.float32)
+                if m1.shape != self.shapes[name] or m2.shape != self.shapes[name]:
+                    raise ValueError(f"{path}: optimizer state of '{name}' has shape {m1.shape}")
+                check(lib().laya_model_set_moments(self.handle, self.index[name], m1.ctypes.data, m2.ctypes.data))
+        check(lib().laya_model_set_steps(self.handle, steps))
 
     @classmethod
     def synthetic(cls, config: ModelConfig, seed: int = 0, std: float = 0.02,
@@ -145,6 +223,10 @@ class TrainableDecisionModel:
     def parameter_count(self) -> int:
         return sum(int(np.prod(s)) for n, s in self.shapes.items() if n != "temperature")
 
+    @property
+    def trainable_parameter_count(self) -> int:
+        return sum(int(np.prod(s)) for n, s in self.shapes.items() if self.trainable(n))
+
     # ------------------------------------------------------------------------ training
 
     def set_trainable_encoder_layers(self, n: Optional[int]) -> None:
@@ -179,11 +261,14 @@ class TrainableDecisionModel:
     def objective_rlcd(self, targets, draws, sigma: float, spherical_weight: float = 0.75, rps_weight: float = 1.0,
                        ce_weight: float = 1.0, scale: float = 1.0) -> tuple:
         """RlcdObjective.Compute on the last forward's logits, on the device (RlcdObjective.cs:57-155):
-        targets [Σ n_options], draws [groups][Σ n_options] standard normal. The logit gradient stays on
-        the device for backward_from_objective. Returns (loss, policy, cross-entropy, mean reward)."""
+        targets [Σ n_options], draws [groups][Σ n_options] standard normal (None or zero groups: the
+        cross-entropy term alone). The logit gradient stays on the device for backward_from_objective.
+        Returns (loss, policy, cross-entropy, mean reward)."""
         t = np.ascontiguousarray(targets, np.float32).reshape(-1)
-        z = np.ascontiguousarray(draws, np.float64)
-        groups = z.shape[0] if z.ndim > 1 else max(1, z.size // max(1, t.size))
+        z = np.zeros((0, t.size)) if draws is None else np.ascontiguousarray(draws, np.float64)
+        groups = z.shape[0] if z.ndim > 1 else z.size // max(1, t.size)
+        if z.size != groups * t.size:
+            raise ValueError(f"draws: {z.size} values for {groups} groups of {t.size} options")
         out = np.zeros(4, np.float64)
         check(lib().laya_model_objective_rlcd(self.handle, t.ctypes.data, z.ctypes.data, groups, sigma,
                                               spherical_weight, rps_weight, ce_weight, scale, out.ctypes.data))
