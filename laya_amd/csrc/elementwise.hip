@@ -25,6 +25,14 @@ __global__ void scale_kernel(float* dst, float s, size_t n) {
     GRID_STRIDE(i, n) dst[i] *= s;
 }
 
+__global__ void fill4_kernel(f32x4* dst, float v, size_t n4) {
+    GRID_STRIDE(i, n4) dst[i] = f32x4{v, v, v, v};
+}
+
+__global__ void add4_kernel(f32x4* dst, const f32x4* src, size_t n4) {
+    GRID_STRIDE(i, n4) dst[i] += src[i];
+}
+
 __global__ void gelu_fwd_kernel(const float* x, size_t n, float* y) {
     GRID_STRIDE(i, n) y[i] = gelu_f(x[i]);
 }
@@ -107,6 +115,52 @@ __global__ void relu_dropout_bwd_kernel(const float* wide, float* g, size_t n, f
     }
 }
 
+// Four elements per thread; the mask of element i is still Uniform(seed, i) < p.
+__global__ void dropout4_kernel(f32x4* v, size_t n4, float p, float keep, uint64_t seed) {
+    GRID_STRIDE(i, n4) {
+        f32x4 x = v[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = uniform01(seed, 4 * i + e) < p ? 0.0f : x[e] * keep;
+        v[i] = x;
+    }
+}
+
+__global__ void dropout_copy4_kernel(const f32x4* src, f32x4* dst, size_t n4, float p, float keep, uint64_t seed) {
+    GRID_STRIDE(i, n4) {
+        f32x4 x = src[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = uniform01(seed, 4 * i + e) < p ? 0.0f : x[e] * keep;
+        dst[i] = x;
+    }
+}
+
+__global__ void relu_dropout_fwd4_kernel(const f32x4* wide, size_t n4, float p, float keep, uint64_t seed,
+                                         f32x4* dropped) {
+    GRID_STRIDE(i, n4) {
+        const f32x4 w = wide[i];
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float r = fmaxf(w[e], 0.0f);
+            o[e] = (p > 0.0f && uniform01(seed, 4 * i + e) < p) ? 0.0f : (p > 0.0f ? r * keep : r);
+        }
+        dropped[i] = o;
+    }
+}
+
+// The backward from the forward's output: an element passes its gradient (times 1/(1 − p)) exactly when
+// it was kept and its pre-activation was positive, i.e. when its output is positive. Same product as
+// recomputing the mask from the pre-activation, without the per-element hash.
+__global__ void relu_dropout_bwd_out4_kernel(const f32x4* dropped, f32x4* g, size_t n4, float keep) {
+    GRID_STRIDE(i, n4) {
+        const f32x4 d = dropped[i];
+        f32x4 v = g[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = d[e] > 0.0f ? v[e] * keep : 0.0f;
+        g[i] = v;
+    }
+}
+
 // Rotary.Apply (Ops.cs:489-503) over rows of [rows, head_dim].
 __global__ void rotary_kernel(const float* cos_t, const float* sin_t, int half, float* vec, int rows, const int* pos,
                               int inverse) {
@@ -165,30 +219,75 @@ __global__ void scatter_add_rows_kernel(const float* src, const int* rows, int n
     for (int r = 0; r < n; ++r) dst[(size_t)rows[r] * width + c] += src[(size_t)r * width + c];
 }
 
-// Per-segment column sums, then per-type accumulation in segment order (TrainableDecisionModel.cs:512-521).
-__global__ void segment_sum_kernel(const float* d, const int* seg_start, const int* seg_len, int width,
-                                   float* part) {
-    const int s = blockIdx.y;
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= width) return;
-    const int b = seg_start[s], L = seg_len[s];
-    float acc = 0.0f;
-    for (int t = 0; t < L; ++t) acc += d[(size_t)(b + t) * width + c];
-    part[(size_t)s * width + c] = acc;
+// Column sums in two deterministic stages (bias gradients, the type-embedding gradient, LayerNorm γ/β
+// partials). Stage 1: part[chunk][type][c] = Σ over the chunk's rows r with row_type[r] == type of x[r][c]
+// (one type when row_type is null); a block is 64 float4 columns × 4 row phases, phase k summing rows
+// k, k + 4, … in order, the phases combined in LDS in order.
+template <int TYPES>
+__global__ __launch_bounds__(256) void colsum_partial4_kernel(const f32x4* __restrict__ x, int rows, int n4,
+                                                              int rows_per, const int* __restrict__ row_type,
+                                                              f32x4* __restrict__ part) {
+    __shared__ f32x4 red[TYPES][4][64];
+    const int lc = threadIdx.x & 63, ph = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + lc;
+    const int r0 = blockIdx.y * rows_per, r1 = min(rows, r0 + rows_per);
+    f32x4 acc[TYPES];
+#pragma unroll
+    for (int t = 0; t < TYPES; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < n4) {
+#pragma unroll 4
+        for (int r = r0 + ph; r < r1; r += 4) {
+            const f32x4 v = x[(long)r * n4 + c];
+            if (TYPES == 1) {
+                acc[0] += v;
+            } else {
+                const int ty = row_type[r];
+#pragma unroll
+                for (int t = 0; t < TYPES; ++t)
+                    if (ty == t) acc[t] += v;
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < TYPES; ++t) red[t][ph][lc] = acc[t];
+    __syncthreads();
+    if (ph == 0 && c < n4)
+#pragma unroll
+        for (int t = 0; t < TYPES; ++t)
+            part[((long)blockIdx.y * TYPES + t) * n4 + c] =
+                ((red[t][0][lc] + red[t][1][lc]) + red[t][2][lc]) + red[t][3][lc];
 }
 
-__global__ void type_accumulate_kernel(const float* part, const int* qtypes, int nseg, int width, float* grad) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= width) return;
-    for (int s = 0; s < nseg; ++s) grad[(size_t)qtypes[s] * width + c] += part[(size_t)s * width + c];
+// Stage 2: out[c] += Σ_k part[k][c] over `count` partials; a block is 16 float4 columns × 16 phases,
+// phase q summing partials q, q + 16, … in order, the phases combined in order.
+__global__ __launch_bounds__(256) void colsum_reduce4_kernel(const f32x4* __restrict__ part, int count, int w4,
+                                                             f32x4* __restrict__ out) {
+    __shared__ f32x4 red[16][16];
+    const int lc = threadIdx.x & 15, ph = threadIdx.x >> 4;
+    const int c = blockIdx.x * 16 + lc;
+    f32x4 s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < w4) {
+#pragma unroll 4
+        for (int k = ph; k < count; k += 16) s += part[(long)k * w4 + c];
+    }
+    red[ph][lc] = s;
+    __syncthreads();
+    if (ph == 0 && c < w4) {
+        f32x4 t = red[0][lc];
+#pragma unroll
+        for (int q = 1; q < 16; ++q) t += red[q][lc];
+        out[c] += t;
+    }
 }
 
-// Soft cross-entropy gradient (RlcdObjective.cs:139-150), one thread, items in order.
-__global__ void softmax_ce_kernel(const float* logits, const float* targets, const int* offsets, int n_items,
-                                  float ce_weight, float scale, float* grad, float* loss) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    double ce = 0.0;
-    for (int i = 0; i < n_items; ++i) {
+// Soft cross-entropy gradient (RlcdObjective.cs:139-150): one thread per item computes its options'
+// gradient and its loss term; the terms are then added in item order by one thread (a fixed order).
+constexpr int CE_THREADS = 256;
+__global__ __launch_bounds__(CE_THREADS) void softmax_ce_kernel(const float* logits, const float* targets,
+                                                                const int* offsets, int n_items, float ce_weight,
+                                                                float scale, float* grad, float* loss,
+                                                                double* terms) {
+    for (int i = threadIdx.x; i < n_items; i += CE_THREADS) {
         const int b = offsets[i], k = offsets[i + 1] - offsets[i];
         float mx = -__builtin_huge_valf();
         for (int o = 0; o < k; ++o) mx = fmaxf(mx, logits[b + o]);
@@ -197,14 +296,21 @@ __global__ void softmax_ce_kernel(const float* logits, const float* targets, con
         const float inv = total > 0.0f ? 1.0f / total : 0.0f;
         double mass = 0.0;
         for (int o = 0; o < k; ++o) mass += targets[b + o];
+        double ce = 0.0;
         for (int o = 0; o < k; ++o) {
             const float p = expf(logits[b + o] - mx) * inv;
             ce -= targets[b + o] * log(fmax((double)p, 1e-30)) / n_items;
             const double g = (double)ce_weight * (p * mass - targets[b + o]) / n_items;
             grad[b + o] = (float)(g * scale);
         }
+        terms[i] = ce;
     }
-    if (loss) *loss = (float)ce;
+    if (!loss) return;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    double ce = 0.0;
+    for (int i = 0; i < n_items; ++i) ce += terms[i];
+    *loss = (float)ce;
 }
 
 // N(0, std) by Box–Muller over two counter-RNG draws; kind 0 normal, 1 ones, 2 zeros.
@@ -227,15 +333,29 @@ unsigned grid_for(size_t n) { return blocks_for(n, 256, 8192); }
 
 }  // namespace
 
+bool vec4(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
 void fill(laya_ctx* ctx, float* dst, float v, size_t n) {
     if (!n) return;
     ProfileScope scope(ctx, "fill", 0.0, 4.0 * n);
+    if (n % 4 == 0 && vec4(dst)) {
+        hipLaunchKernelGGL(fill4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<f32x4*>(dst), v, n / 4);
+        check_launch("fill4_kernel");
+        return;
+    }
     hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, v, n);
     check_launch("fill_kernel");
 }
 void add(laya_ctx* ctx, float* dst, const float* src, size_t n) {
     if (!n) return;
     ProfileScope scope(ctx, "add", 0.0, 12.0 * n);
+    if (n % 4 == 0 && vec4(dst) && vec4(src)) {
+        hipLaunchKernelGGL(add4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<f32x4*>(dst), reinterpret_cast<const f32x4*>(src), n / 4);
+        check_launch("add4_kernel");
+        return;
+    }
     hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, src, n);
     check_launch("add_kernel");
 }
@@ -281,14 +401,40 @@ void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, in
 void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed) {
     if (!n || p <= 0.0f) return;
     ProfileScope scope(ctx, "dropout", 0.0, 8.0 * n);
+    if (n % 4 == 0 && vec4(v)) {
+        hipLaunchKernelGGL(dropout4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<f32x4*>(v), n / 4, p, 1.0f / (1.0f - p), seed);
+        check_launch("dropout4_kernel");
+        return;
+    }
     hipLaunchKernelGGL(dropout_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, v, n, p, 1.0f / (1.0f - p),
                        seed);
     check_launch("dropout_kernel");
+}
+void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p, uint64_t seed) {
+    if (!n) return;
+    if (p <= 0.0f || n % 4 != 0 || !vec4(src) || !vec4(dst)) {
+        LAYA_HIP(hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+        dropout(ctx, dst, n, p, seed);
+        return;
+    }
+    ProfileScope scope(ctx, "dropout", 0.0, 8.0 * n);
+    hipLaunchKernelGGL(dropout_copy4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                       reinterpret_cast<const f32x4*>(src), reinterpret_cast<f32x4*>(dst), n / 4, p,
+                       1.0f / (1.0f - p), seed);
+    check_launch("dropout_copy4_kernel");
 }
 void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped) {
     if (!n) return;
     const float keep = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
     ProfileScope scope(ctx, "relu_dropout_fwd", 0.0, 8.0 * n);
+    if (n % 4 == 0 && vec4(wide) && vec4(dropped)) {
+        hipLaunchKernelGGL(relu_dropout_fwd4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const f32x4*>(wide), n / 4, p, keep, seed,
+                           reinterpret_cast<f32x4*>(dropped));
+        check_launch("relu_dropout_fwd4_kernel");
+        return;
+    }
     hipLaunchKernelGGL(relu_dropout_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, wide, n, p, keep, seed,
                        dropped);
     check_launch("relu_dropout_fwd_kernel");
@@ -300,6 +446,44 @@ void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, floa
     hipLaunchKernelGGL(relu_dropout_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, wide, g, n, p, keep,
                        seed);
     check_launch("relu_dropout_bwd_kernel");
+}
+void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g, size_t n, float p) {
+    if (!n) return;
+    LAYA_REQUIRE(n % 4 == 0 && vec4(dropped) && vec4(g), "relu_dropout_bwd: 16-byte aligned multiples of 4");
+    const float keep = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
+    ProfileScope scope(ctx, "relu_dropout_bwd", 0.0, 12.0 * n);
+    hipLaunchKernelGGL(relu_dropout_bwd_out4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                       reinterpret_cast<const f32x4*>(dropped), reinterpret_cast<f32x4*>(g), n / 4, keep);
+    check_launch("relu_dropout_bwd_out4_kernel");
+}
+void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_type, int types, float* out,
+                 int slot) {
+    LAYA_REQUIRE(types == 1 || types == 3, "column_sums: one or three row types");
+    LAYA_REQUIRE(n % 4 == 0 && vec4(x) && vec4(out), "column_sums: 16-byte aligned rows of a multiple of 4");
+    if (rows <= 0 || n <= 0) return;
+    const int n4 = n / 4, cblocks = (n4 + 63) / 64;
+    // About 2048 workgroups in stage 1, at least 16 rows each.
+    const int want = std::max(1, 2048 / cblocks);
+    const int rows_per = std::max(16, ((rows + want - 1) / want + 15) / 16 * 16);
+    const int chunks = (rows + rows_per - 1) / rows_per;
+    f32x4* part = static_cast<f32x4*>(ctx->workspace(slot, sizeof(f32x4) * (size_t)chunks * types * n4));
+    ProfileScope scope(ctx, "column_sums", 0.0, 4.0 * (double)rows * n);
+    if (types == 1)
+        hipLaunchKernelGGL(colsum_partial4_kernel<1>, dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, nullptr, part);
+    else
+        hipLaunchKernelGGL(colsum_partial4_kernel<3>, dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, row_type, part);
+    check_launch("colsum_partial4_kernel");
+    column_reduce(ctx, reinterpret_cast<const float*>(part), chunks, types * n, out);
+}
+void column_reduce(laya_ctx* ctx, const float* part, int count, int n, float* out) {
+    LAYA_REQUIRE(n % 4 == 0 && vec4(part) && vec4(out), "column_reduce: 16-byte aligned rows of a multiple of 4");
+    if (count <= 0 || n <= 0) return;
+    const int w4 = n / 4;
+    hipLaunchKernelGGL(colsum_reduce4_kernel, dim3((w4 + 15) / 16), dim3(256), 0, ctx->stream,
+                       reinterpret_cast<const f32x4*>(part), count, w4, reinterpret_cast<f32x4*>(out));
+    check_launch("colsum_reduce4_kernel");
 }
 void rotary_apply(laya_ctx* ctx, const float* cos_t, const float* sin_t, int head_dim, float* vec, int rows,
                   const int* pos, int inverse) {
@@ -336,22 +520,20 @@ void scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows, int n, i
                        width, dst);
     check_launch("scatter_add_rows_kernel");
 }
-void type_embedding_bwd(laya_ctx* ctx, const float* d, const int* seg_start, const int* seg_len, const int* qtypes,
-                        int nseg, int width, float* grad) {
-    if (nseg <= 0) return;
-    float* part = static_cast<float*>(ctx->workspace(1, sizeof(float) * (size_t)nseg * width));
-    hipLaunchKernelGGL(segment_sum_kernel, dim3((width + 255) / 256, nseg), dim3(256), 0, ctx->stream, d, seg_start,
-                       seg_len, width, part);
-    check_launch("segment_sum_kernel");
-    hipLaunchKernelGGL(type_accumulate_kernel, dim3((width + 255) / 256), dim3(256), 0, ctx->stream, part, qtypes,
-                       nseg, width, grad);
-    check_launch("type_accumulate_kernel");
+void type_embedding_bwd(laya_ctx* ctx, const float* d, const int* row_type, int rows, int width, float* grad) {
+    if (rows <= 0) return;
+    if (width % 4 == 0 && vec4(d) && vec4(grad)) {
+        column_sums(ctx, d, rows, width, row_type, 3, grad, 1);
+        return;
+    }
+    LAYA_REQUIRE(false, "type_embedding_bwd: rows must be 16-byte aligned multiples of 4 floats");
 }
 void softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets, const int* offsets, int n_items,
                     float ce_weight, float s, float* grad, float* loss) {
     if (n_items <= 0) return;
-    hipLaunchKernelGGL(softmax_ce_kernel, dim3(1), dim3(64), 0, ctx->stream, logits, targets, offsets, n_items,
-                       ce_weight, s, grad, loss);
+    double* terms = static_cast<double*>(ctx->workspace(1, sizeof(double) * (size_t)n_items));
+    hipLaunchKernelGGL(softmax_ce_kernel, dim3(1), dim3(CE_THREADS), 0, ctx->stream, logits, targets, offsets, n_items,
+                       ce_weight, s, grad, loss, terms);
     check_launch("softmax_ce_kernel");
 }
 void init_param(laya_ctx* ctx, float* dst, size_t n, int kind, float std, uint64_t seed) {

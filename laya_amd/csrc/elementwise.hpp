@@ -12,6 +12,8 @@ void gelu_bwd(laya_ctx* ctx, const float* u, float* g, size_t n);
 void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act);
 void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide);
 void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed);
+// dst = Dropout(src) out of place (one pass).
+void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p, uint64_t seed);
 void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped);
 void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, float p, uint64_t seed);
 void rotary_apply(laya_ctx* ctx, const float* cos_t, const float* sin_t, int head_dim, float* vec, int rows,
@@ -21,8 +23,15 @@ void embedding_bwd(laya_ctx* ctx, const int* sorted_pos, const int* unique_ids, 
                    const float* d, int hidden, float* grad);
 void gather_rows(laya_ctx* ctx, const float* src, const int* rows, int n, int width, float* dst);
 void scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows, int n, int width, float* dst);
-void type_embedding_bwd(laya_ctx* ctx, const float* d, const int* seg_start, const int* seg_len, const int* qtypes,
-                        int nseg, int width, float* grad);
+// grad[type] += Σ over rows r with row_type[r] == type of d[r] (TrainableDecisionModel.cs:512-521).
+void type_embedding_bwd(laya_ctx* ctx, const float* d, const int* row_type, int rows, int width, float* grad);
+// ReLU + dropout backward from the forward's output (positive exactly where the gradient passes).
+void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g, size_t n, float p);
+// out[type·n + c] += Σ rows of x[r][c] (per row type when row_type is given; types 1 or 3), in a fixed
+// order, through workspace `slot`; n % 4 == 0, 16-byte aligned.
+void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_type, int types, float* out, int slot);
+// out[c] += Σ_k part[k][c] for count partial rows of width n, in a fixed order.
+void column_reduce(laya_ctx* ctx, const float* part, int count, int n, float* out);
 void softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets, const int* offsets, int n_items,
                     float ce_weight, float scale, float* grad, float* loss);
 void init_param(laya_ctx* ctx, float* dst, size_t n, int kind, float std, uint64_t seed);

@@ -24,6 +24,7 @@
 // loop in a kernel that also carries unused boundary code and runtime epilogue branches measured a
 // fifth slower on short-K products.
 #include "common.hpp"
+#include "elementwise.hpp"
 
 namespace laya {
 namespace {
@@ -937,6 +938,10 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
 
 void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out) {
     if (rows <= 0 || n <= 0) return;
+    if (n % 4 == 0 && aligned16(x) && aligned16(out) && rows > 256) {
+        column_sums(ctx, x, rows, n, nullptr, 1, out, 1);
+        return;
+    }
     const int rows_per = 256;
     const int chunks = (rows + rows_per - 1) / rows_per;
     if (chunks <= 1) {

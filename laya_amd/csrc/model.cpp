@@ -518,8 +518,7 @@ void linear_backward(laya_model* m, const float* x, const float* dy, int rows, i
 }
 
 void dropout_copy(laya_model* m, const float* src, float* dst, size_t n, float p, uint64_t seed) {
-    LAYA_HIP(hipMemcpyAsync(dst, src, n * sizeof(float), hipMemcpyDeviceToDevice, m->ctx->stream));
-    dropout(m->ctx, dst, n, p, seed);
+    laya::dropout_copy(m->ctx, src, dst, n, p, seed);
 }
 
 // Forward (TrainableDecisionModel.cs:248-353) with EncoderLayerForward (361-414) and HeadLayerForward (428-468).
@@ -641,7 +640,10 @@ void head_backward(laya_model* m, int j) {
         dy = m->dy;
     }
     linear_backward(m, a.drop, dy, T, ff, d, H.linear2, H.linear2_b, m->dact);
-    relu_dropout_bwd(ctx, a.wide, m->dact, (size_t)T * ff, p, salt(m->seed, j, 2));
+    if (ff % 4 == 0)
+        relu_dropout_bwd_from_output(ctx, a.drop, m->dact, (size_t)T * ff, p);
+    else
+        relu_dropout_bwd(ctx, a.wide, m->dact, (size_t)T * ff, p, salt(m->seed, j, 2));
     linear_backward(m, a.n2, m->dact, T, d, ff, H.linear1, H.linear1_b, m->dn);
     layernorm_bwd(ctx, a.res, T, d, m->W(H.norm2), 1e-5f, m->dn, m->dS, m->Gt(H.norm2), m->Gt(H.norm2_b), a.mean2,
                   a.rstd2);
@@ -673,7 +675,7 @@ void backward(laya_model* m) {
     scatter_add_rows(ctx, m->ds_mark, m->cur.marker_rows, M, d, m->dS);
     for (int j = m->cfg.head_layers - 1; j >= 0; --j) head_backward(m, j);
     if (float* g = m->Gt(m->type_emb))
-        type_embedding_bwd(ctx, m->dS, m->cur.seg_start, m->cur.seg_len, m->cur.qtypes, m->nseg, d, g);
+        type_embedding_bwd(ctx, m->dS, m->cur.row_type, T, d, g);
     if (m->first_trainable >= m->cfg.layers) return;  // the encoder is frozen
     fill(ctx, m->dE, 0.0f, (size_t)T * d);
     layernorm_bwd(ctx, m->x_final, T, d, m->W(m->final_norm), eps, m->dS, m->dE, m->Gt(m->final_norm),

@@ -10,7 +10,7 @@
 // Backward restates Ops.LayerNormBackward (Ops.cs:117-186) in one pass: each wave writes dx for
 // its rows and keeps dγ/dβ partials in registers for a fixed row stride; a second kernel sums the
 // partials in wave order. Bytes per row: x, dy, dx in, dx out = 16·n.
-#include "common.hpp"
+#include "elementwise.hpp"
 
 namespace laya {
 namespace {
@@ -37,14 +37,20 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
         zero = (unsigned)id >= (unsigned)gather_rows;
         src = x + (long)(zero ? 0 : id) * n;
     }
-    f32x4 v[NCH];
-    float s = 0.0f;
+    // Issue every load of the row (x, γ, β, the added table row) before the reductions.
+    const float* add = add_table ? add_table + (long)add_index[row] * n : nullptr;
+    f32x4 v[NCH], gw[NCH], bw[NCH], aw[NCH];
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = (c * 64 + lane) * 4;
         v[c] = (col < n && !zero) ? ld4(src + col) : f32x4{0, 0, 0, 0};
-        s += (v[c][0] + v[c][1]) + (v[c][2] + v[c][3]);
+        gw[c] = col < n ? ld4(w + col) : f32x4{0, 0, 0, 0};
+        bw[c] = (col < n && b) ? ld4(b + col) : f32x4{0, 0, 0, 0};
+        aw[c] = (col < n && add) ? ld4(add + col) : f32x4{0, 0, 0, 0};
     }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) s += (v[c][0] + v[c][1]) + (v[c][2] + v[c][3]);
     const float mean = wave_sum(s) / (float)n;
     float q = 0.0f;
 #pragma unroll
@@ -60,15 +66,13 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
     }
     const float var = wave_sum(q) / (float)n;
     const float rstd = 1.0f / sqrtf(var + eps);
-    const float* add = add_table ? add_table + (long)add_index[row] * n : nullptr;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = (c * 64 + lane) * 4;
         if (col < n) {
-            f32x4 g = ld4(w + col);
-            f32x4 o = (v[c] - mean) * rstd * g;
-            if (b) o += ld4(b + col);
-            if (add) o += ld4(add + col);
+            f32x4 o = (v[c] - mean) * rstd * gw[c];
+            if (b) o += bw[c];
+            if (add) o += aw[c];
             st4(y + (long)row * n + col, o);
         }
     }
@@ -78,6 +82,29 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
     }
 }
 
+// One row's operands for the backward: x (gathered when ids are given), dy, and the dx it adds into.
+template <int NCH>
+__device__ __forceinline__ void ln_bwd_load(const float* __restrict__ x, const float* __restrict__ dy,
+                                            const float* __restrict__ dx, int row, int n, int lane,
+                                            const int* __restrict__ gather_ids, int gather_rows, f32x4 (&xv)[NCH],
+                                            f32x4 (&gv)[NCH], f32x4 (&dv)[NCH]) {
+    const float* src = x + (long)row * n;
+    bool zero = false;
+    if (gather_ids) {
+        const int id = gather_ids[row];
+        zero = (unsigned)id >= (unsigned)gather_rows;
+        src = x + (long)(zero ? 0 : id) * n;
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        const int col = (c * 64 + lane) * 4;
+        xv[c] = (col < n && !zero) ? ld4(src + col) : f32x4{0, 0, 0, 0};
+        gv[c] = col < n ? ld4(dy + (long)row * n + col) : f32x4{0, 0, 0, 0};
+        dv[c] = col < n ? ld4(dx + (long)row * n + col) : f32x4{0, 0, 0, 0};
+    }
+}
+
+// Rows up to 1024 wide (NCH ≤ 4) keep the next row's loads in flight while the current row computes.
 template <int NCH>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x, int rows, int n,
                                                      const float* __restrict__ w, float eps,
@@ -88,6 +115,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x
                                                      int total_waves, float* __restrict__ part_g,
                                                      float* __restrict__ part_b) {
     // total_waves is a multiple of 4 (whole blocks); a wave past the last row only adds zeros.
+    constexpr bool PIPE = NCH <= 4;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     f32x4 gacc[NCH], bacc[NCH], gm[NCH];
@@ -99,28 +127,24 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x
         gm[c] = col < n ? ld4(w + col) : f32x4{0, 0, 0, 0};
     }
     const float inv_n = 1.0f / (float)n;
+    f32x4 xv[NCH], gv[NCH], dv[NCH];
+    if (PIPE && wave < rows) ln_bwd_load<NCH>(x, dy, dx, wave, n, lane, gather_ids, gather_rows, xv, gv, dv);
     for (int row = wave; row < rows; row += total_waves) {
-        const float* src = x + (long)row * n;
-        bool zero = false;
-        if (gather_ids) {
-            const int id = gather_ids[row];
-            zero = (unsigned)id >= (unsigned)gather_rows;
-            src = x + (long)(zero ? 0 : id) * n;
-        }
-        f32x4 xv[NCH], gv[NCH];
-        float s = 0.0f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int col = (c * 64 + lane) * 4;
-            xv[c] = (col < n && !zero) ? ld4(src + col) : f32x4{0, 0, 0, 0};
-            gv[c] = col < n ? ld4(dy + (long)row * n + col) : f32x4{0, 0, 0, 0};
-            s += (xv[c][0] + xv[c][1]) + (xv[c][2] + xv[c][3]);
+        f32x4 xn[NCH], gn[NCH], dn[NCH];
+        const int next = row + total_waves;
+        if (PIPE) {
+            if (next < rows) ln_bwd_load<NCH>(x, dy, dx, next, n, lane, gather_ids, gather_rows, xn, gn, dn);
+        } else {
+            ln_bwd_load<NCH>(x, dy, dx, row, n, lane, gather_ids, gather_rows, xv, gv, dv);
         }
         float mean, rstd;
         if (mean_in) {
             mean = mean_in[row];
             rstd = rstd_in[row];
         } else {
+            float s = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) s += (xv[c][0] + xv[c][1]) + (xv[c][2] + xv[c][3]);
             mean = wave_sum(s) * inv_n;
             float q = 0.0f;
 #pragma unroll
@@ -156,8 +180,15 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x
             const int col = (c * 64 + lane) * 4;
             if (col < n) {
                 const f32x4 xh = (xv[c] - mean) * rstd;
-                float* o = dx + (long)row * n + col;
-                st4(o, ld4(o) + rstd * (gv[c] * gm[c] - mg - xh * mgx));
+                st4(dx + (long)row * n + col, dv[c] + rstd * (gv[c] * gm[c] - mg - xh * mgx));
+            }
+        }
+        if (PIPE) {
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                xv[c] = xn[c];
+                gv[c] = gn[c];
+                dv[c] = dn[c];
             }
         }
     }
@@ -202,6 +233,8 @@ __global__ __launch_bounds__(RED_COLS* RED_GROUPS) void partial_reduce_kernel(co
         out[c] += t;
     }
 }
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 int chunks_for(int n) {
     LAYA_REQUIRE(n > 0 && n % 4 == 0, "layernorm: the row width must be a positive multiple of 4");
@@ -257,6 +290,16 @@ void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
     switch (nch) { LN_BWD(1) LN_BWD(2) LN_BWD(3) LN_BWD(4) LN_BWD(5) LN_BWD(6) LN_BWD(7) LN_BWD(8) }
 #undef LN_BWD
     check_launch("ln_bwd_kernel");
+    if (n % 4 == 0) {  // workspace partials are 256-byte aligned; the parameter gradients 16-byte aligned
+        if (pg && aligned16(dgamma)) {
+            column_reduce(ctx, pg, blocks, n, dgamma);
+            pg = nullptr;
+        }
+        if (pb && aligned16(dbeta)) {
+            column_reduce(ctx, pb, blocks, n, dbeta);
+            pb = nullptr;
+        }
+    }
     const dim3 rgrid((n + RED_COLS - 1) / RED_COLS), rblock(RED_COLS * RED_GROUPS);
     if (pg) {
         hipLaunchKernelGGL(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pg, blocks, n, dgamma);

@@ -32,11 +32,41 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ g,
     if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-__global__ void norm_finish_kernel(const double* __restrict__ partial, int count, double max_norm, double* norm,
-                                   float* coef, int* nonfinite) {
-    if (threadIdx.x != 0) return;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ double sq4(f32x4 v) {
+    const double a = v[0], b = v[1], c = v[2], d = v[3];
+    return (a * a + b * b) + (c * c + d * d);
+}
+
+// The same fixed partition in float4 units: four loads in flight per thread, four accumulators.
+__global__ __launch_bounds__(256) void sumsq4_kernel(const f32x4* __restrict__ g, size_t n4, size_t chunk4,
+                                                     double* __restrict__ partial) {
+    __shared__ double red[4];
+    const size_t b = blockIdx.x * chunk4, e = min(n4, b + chunk4);
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    size_t i = b + threadIdx.x;
+    for (; i + 768 < e; i += 1024) {
+        const f32x4 a = g[i], c = g[i + 256], d = g[i + 512], f = g[i + 768];
+        s0 += sq4(a);
+        s1 += sq4(c);
+        s2 += sq4(d);
+        s3 += sq4(f);
+    }
+    for (; i < e; i += 256) s0 += sq4(g[i]);
+    double s = wave_sum_d((s0 + s1) + (s2 + s3));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// One wave: lane l sums partials l, l + 64, …; the lanes combine in a fixed butterfly.
+__global__ __launch_bounds__(64) void norm_finish_kernel(const double* __restrict__ partial, int count,
+                                                         double max_norm, double* norm, float* coef, int* nonfinite) {
     double s = 0.0;
-    for (int i = 0; i < count; ++i) s += partial[i];
+    for (int i = threadIdx.x; i < count; i += 64) s += partial[i];
+    s = wave_sum_d(s);
+    if (threadIdx.x != 0) return;
     const double nrm = sqrt(s);
     const double c = max_norm / (nrm + 1e-6);
     if (norm) *norm = nrm;
@@ -69,6 +99,43 @@ __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, float
     }
 }
 
+// The same update on float4s: every group bound is a multiple of 4 (in float4 units here).
+__global__ __launch_bounds__(256) void adamw4_kernel(f32x4* __restrict__ p, f32x4* __restrict__ g,
+                                                     f32x4* __restrict__ m, f32x4* __restrict__ v, size_t n4,
+                                                     AdamGroups groups, float b1, float b2, float eps, float sqrt_c2,
+                                                     const float* coef, int zero_grads) {
+    const float cf = coef ? *coef : 1.0f;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        int grp = -1;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (k < groups.n && i >= groups.begin[k] && i < groups.end[k]) grp = k;
+        const f32x4 gi = g[i];
+        if (grp >= 0) {
+            const f32x4 pi = p[i], mi0 = m[i], vi0 = v[i];
+            const float decay = groups.decay[grp], step = groups.step_size[grp];
+            f32x4 wo, mo, vo;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float gs = gi[e] * cf;
+                float w = pi[e] * decay;
+                const float mi = b1 * mi0[e] + (1.0f - b1) * gs;
+                const float vi = b2 * vi0[e] + (1.0f - b2) * gs * gs;
+                w -= step * mi / (sqrtf(vi) / sqrt_c2 + eps);
+                wo[e] = w;
+                mo[e] = mi;
+                vo[e] = vi;
+            }
+            p[i] = wo;
+            m[i] = mo;
+            v[i] = vo;
+        }
+        if (zero_grads) g[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
+bool vec4_ok(const void* a) { return ((uintptr_t)a & 15u) == 0; }
+
 }  // namespace
 
 void grad_norm(laya_ctx* ctx, const float* g, size_t n, double max_norm, double* norm, float* coef, int* nonfinite) {
@@ -77,8 +144,14 @@ void grad_norm(laya_ctx* ctx, const float* g, size_t n, double max_norm, double*
     chunk = (chunk + 1023) / 1024 * 1024;
     if (chunk == 0) chunk = 1024;
     ProfileScope scope(ctx, "grad_norm", 0.0, 4.0 * n);
-    hipLaunchKernelGGL(sumsq_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx->stream, g, n, chunk, partial);
-    check_launch("sumsq_kernel");
+    if (n % 4 == 0 && vec4_ok(g)) {
+        hipLaunchKernelGGL(sumsq4_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const f32x4*>(g), n / 4, chunk / 4, partial);
+        check_launch("sumsq4_kernel");
+    } else {
+        hipLaunchKernelGGL(sumsq_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx->stream, g, n, chunk, partial);
+        check_launch("sumsq_kernel");
+    }
     hipLaunchKernelGGL(norm_finish_kernel, dim3(1), dim3(64), 0, ctx->stream, partial, NORM_BLOCKS, max_norm, norm,
                        coef, nonfinite);
     check_launch("norm_finish_kernel");
@@ -91,6 +164,20 @@ void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n
         LAYA_REQUIRE(groups.begin[k] <= groups.end[k] && groups.end[k] <= n, "adamw: group range outside the arena");
     if (!n) return;
     ProfileScope scope(ctx, "adamw", 0.0, (zero_grads ? 32.0 : 28.0) * n);
+    bool vec = n % 4 == 0 && vec4_ok(p) && vec4_ok(g) && vec4_ok(m) && vec4_ok(v);
+    for (int k = 0; k < groups.n; ++k) vec = vec && groups.begin[k] % 4 == 0 && groups.end[k] % 4 == 0;
+    if (vec) {
+        AdamGroups g4 = groups;
+        for (int k = 0; k < groups.n; ++k) {
+            g4.begin[k] = groups.begin[k] / 4;
+            g4.end[k] = groups.end[k] / 4;
+        }
+        hipLaunchKernelGGL(adamw4_kernel, dim3(blocks_for(n / 4, 256, 8192)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<f32x4*>(p), reinterpret_cast<f32x4*>(g), reinterpret_cast<f32x4*>(m),
+                           reinterpret_cast<f32x4*>(v), n / 4, g4, beta1, beta2, eps, sqrt_c2, coef, zero_grads);
+        check_launch("adamw4_kernel");
+        return;
+    }
     hipLaunchKernelGGL(adamw_kernel, dim3(blocks_for(n, 256, 8192)), dim3(256), 0, ctx->stream, p, g, m, v, n, groups,
                        beta1, beta2, eps, sqrt_c2, coef, zero_grads);
     check_launch("adamw_kernel");
