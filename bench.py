@@ -1,6 +1,6 @@
 """Fine-tuning throughput of the Laya ModernBERT decision model on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload NAME]
 
 A step is one full optimizer step over one synthetic batch: forward, the decision head's soft
 cross-entropy gradient, backward, global-norm clip and AdamW (fwd+bwd+AdamW), all on the device.
@@ -9,6 +9,9 @@ layer global, the rest a 128-token sliding window) plus the two-layer decision h
 32 × seq 512 with a trailing-padding fraction U[0, 0.3] per sequence (padding is never computed:
 sequences are packed), items cycling choice K=8 / score K=4 / noul K=2, summed cross-entropy,
 AdamW lr 3e-5 wd 0.01, clip 1.0, head dropout 0.1. Weights N(0, 0.02) from a fixed seed.
+
+`--workload` selects another shape (batch 4 × 128; batch 32 × 1024 and a packed Zipf batch of 64
+sequences with the backward products in bf16; batch 2 × 8192); the default is the one above.
 
 Prints one JSON line. `value` counts real (unpadded) tokens per second over the timed steps, with
 every input already resident; `roofline` describes the kernel with the largest share of device
@@ -43,14 +46,43 @@ MFMA_KERNELS = ("gemm_nt", "gemm_nn", "gemm_tn", "gemm_bwd_pair", "attention_fwd
 MEASURED_TRAFFIC = {"gemm_bwd_pair": 1.753e9}
 
 
-def make_batch(rng, batch=32, seq=512, vocab=50368, pad_max=0.3):
+PEAK_BF16_MFMA = 2.5e15
+
+# The workloads: batch shape, heads, loss scaling (summed CE multiplies the mean by the item count) and
+# the precision of the matrix products. b32x512 is the headline configuration.
+WORKLOADS = {
+    "b4x128": dict(desc="batch 4 x seq 128, no padding, one choice head K=5, mean CE", batch=4, seq=128, pad=0.0,
+                   heads="choice5", summed=False, matmul="fp32"),
+    "b32x512": dict(desc="batch 32 x seq 512, trailing padding U[0,0.3], heads choice8/score4/noul2, summed CE",
+                    batch=32, seq=512, pad=0.3, heads="mixed", summed=True, matmul="fp32"),
+    "b32x1024-bf16": dict(desc="batch 32 x seq 1024, no padding, heads choice8/score4/noul2, summed CE, backward "
+                               "products in bf16 (fp32 master weights, accumulation, softmax and LayerNorm statistics)",
+                          batch=32, seq=1024, pad=0.0, heads="mixed", summed=True, matmul="bf16-backward"),
+    "b2x8192": dict(desc="batch 2 x seq 8192, no padding, one choice head K=5, mean CE", batch=2, seq=8192, pad=0.0,
+                    heads="choice5", summed=False, matmul="fp32"),
+    "packed64-zipf-bf16": dict(desc="64 sequences of lengths U[16,2048] packed without padding, ids Zipf(1.1), heads "
+                                    "choice8/score4/noul2, summed CE, backward products in bf16",
+                               batch=64, seq=2048, pad=None, heads="mixed", summed=True, matmul="bf16-backward"),
+}
+
+
+def make_batch(rng, w, vocab=50368):
     from laya_amd.batch import Batch
-    fractions = rng.uniform(0.0, pad_max, size=batch)
-    lengths = (seq - np.floor(seq * fractions)).astype(np.int32)
-    kinds = [(0, 8), (1, 4), (2, 2)]  # choice K=8, score K=4, noul K=2
-    qtypes = np.array([kinds[i % 3][0] for i in range(batch)], np.int32)
-    n_options = np.array([kinds[i % 3][1] for i in range(batch)], np.int32)
-    tokens = rng.integers(0, vocab, size=int(lengths.sum()), dtype=np.int64).astype(np.int32)
+    n = w["batch"]
+    if w["pad"] is None:  # packed variable lengths U[16, seq]
+        lengths = rng.integers(16, w["seq"] + 1, size=n).astype(np.int32)
+    else:
+        fractions = rng.uniform(0.0, w["pad"], size=n)
+        lengths = (w["seq"] - np.floor(w["seq"] * fractions)).astype(np.int32)
+    kinds = [(0, 5)] if w["heads"] == "choice5" else [(0, 8), (1, 4), (2, 2)]  # choice / score / noul
+    qtypes = np.array([kinds[i % len(kinds)][0] for i in range(n)], np.int32)
+    n_options = np.array([kinds[i % len(kinds)][1] for i in range(n)], np.int32)
+    total = int(lengths.sum())
+    if w["pad"] is None:  # Zipf(1.1) ranks over the vocabulary, rank r → id r − 1
+        p = np.arange(1, vocab + 1, dtype=np.float64) ** -1.1
+        tokens = rng.choice(vocab, size=total, p=p / p.sum()).astype(np.int32)
+    else:
+        tokens = rng.integers(0, vocab, size=total, dtype=np.int64).astype(np.int32)
     markers = np.concatenate([1 + 2 * np.arange(k) for k in n_options]).astype(np.int32)
     labels = [rng.integers(0, k) for k in n_options]
     targets = np.concatenate([np.eye(k, dtype=np.float32)[lab] for k, lab in zip(n_options, labels)])
@@ -94,7 +126,9 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-baseline leg")
-    ap.add_argument("--cpu-items", type=int, default=16)
+    ap.add_argument("--cpu-items", type=int, default=None,
+                    help="sequences in the CPU sample (default 16 for b32x512, 1 for the long-sequence workloads)")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="b32x512")
     ap.add_argument("--no-profile", action="store_true", help="time without per-launch events")
     ap.add_argument("--by-value", action="store_true",
                     help="pass each batch as host arrays (laya_model_train_step: host planning and uploads inside "
@@ -112,10 +146,13 @@ def main():
     from laya_amd.device import Context
     from laya_amd.model import TrainableDecisionModel
 
+    w = WORKLOADS[args.workload]
     rng = np.random.default_rng(2024)
     mc = modernbert_base()
-    batches = [make_batch(rng) for _ in range(args.warmup + args.steps)]
+    batches = [make_batch(rng, w) for _ in range(args.warmup + args.steps)]
     ctx = Context(0)
+    ctx.set_matmul_precision(w["matmul"])
+    cpu_items = args.cpu_items or (16 if w["seq"] <= 512 else 1)
     model = TrainableDecisionModel.synthetic(mc, seed=42, std=0.02, ctx=ctx)
     model.head_dropout = 0.1
     if args.traffic_probe:
@@ -135,13 +172,16 @@ def main():
 
     by_value = [(b, t, model.batch_args(b)) for b, t in batches] if args.by_value else None
 
+    def scale(b):  # summed CE: the mean gradient times the item count
+        return float(b.n_items) if w["summed"] else 1.0
+
     def step(i):
         if by_value:
             b, t, a = by_value[i]
-            model.train_step(b, t, seed=1000 + i, ce_weight=1.0, loss_scale=float(b.n_items), max_norm=1.0,
+            model.train_step(b, t, seed=1000 + i, ce_weight=1.0, loss_scale=scale(b), max_norm=1.0,
                              lr_encoder=3e-5, lr_head=3e-5, weight_decay=0.01, _args=a)
             return
-        model.train_step_staged(slots[i], seed=1000 + i, ce_weight=1.0, loss_scale=float(batches[i][0].n_items),
+        model.train_step_staged(slots[i], seed=1000 + i, ce_weight=1.0, loss_scale=scale(batches[i][0]),
                                 max_norm=1.0, lr_encoder=3e-5, lr_head=3e-5, weight_decay=0.01)
 
     print(f"warmup {args.warmup} steps", file=sys.stderr, flush=True)
@@ -163,7 +203,7 @@ def main():
             step(i)
         ctx.sync()
         prof = ctx.profile_end()
-    loss = model.train_step_staged(slots[0], seed=7, loss_scale=float(batches[0][0].n_items), want_loss=True)
+    loss = model.train_step_staged(slots[0], seed=7, loss_scale=scale(batches[0][0]), want_loss=True)
     print(f"timed {args.steps} steps in {elapsed:.3f} s, {tokens} real tokens, loss after {loss:.4f}",
           file=sys.stderr, flush=True)
 
@@ -179,8 +219,9 @@ def main():
         per_launch_s = k["ms"] / k["launches"] / 1e3
         if k["flops"]:
             achieved = k["flops"] / k["launches"] / per_launch_s
+            peak = PEAK_BF16_MFMA if name.endswith("_bf16") else PEAK_FP32_MFMA
             roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved / 1e12, 2),
-                        "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA, 4),
+                        "peak": peak / 1e12, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                         "traffic": MEASURED_TRAFFIC.get(name), "avg_launch_ms": round(per_launch_s * 1e3, 4),
                         "launches": k["launches"]}
         else:
@@ -193,6 +234,12 @@ def main():
             f = sum(x["flops"] for x in bwd)
             ms = sum(x["ms"] for x in bwd)
             breakdown["bwd_gemm_mfma_util"] = round(f / (ms / 1e3) / PEAK_FP32_MFMA, 4)
+        bwd16 = [prof[n] for n in ("gemm_nn_bf16", "gemm_tn_bf16") if n in prof]
+        if bwd16:
+            f = sum(x["flops"] for x in bwd16)
+            ms = sum(x["ms"] for x in bwd16)
+            breakdown["bwd_gemm_bf16_mfma_util"] = round(f / (ms / 1e3) / PEAK_BF16_MFMA, 4)
+            breakdown["bwd_gemm_bf16_tflops"] = round(f / (ms / 1e3) / 1e12, 1)
         attn = [prof[n] for n in ("attention_bwd_dkv", "attention_bwd_dq") if n in prof]
         if attn:
             f = sum(x["flops"] for x in attn)
@@ -208,17 +255,19 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        print(f"cpu baseline: oracle on {args.cpu_items} sequences", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(mc, *batches[args.warmup], items=args.cpu_items)
+        print(f"cpu baseline: oracle on {cpu_items} sequences", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(mc, *batches[args.warmup], items=cpu_items)
 
     value = tokens / elapsed
     line = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 3), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
-            "config": {"workload": "ModernBERT-base Laya encoder + decision head fp32 fine-tune step, batch 32 x "
-                                   "seq 512, trailing padding U[0,0.3], heads choice8/score4/noul2, summed CE, "
+            "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp32" if w["matmul"] == "fp32" else "fp32 (bf16 operands in the backward products)",
+            "data": "synthetic",
+            "config": {"workload": f"ModernBERT-base Laya encoder + decision head fine-tune step, {w['desc']}, "
                                    "AdamW lr 3e-5 wd 0.01, clip 1.0",
-                       "global_batch": 32, "seq_len": 512, "parallelism": "none (1 GPU)",
+                       "global_batch": w["batch"], "seq_len": w["seq"], "parallelism": "none (1 GPU)",
+                       "matmul_precision": w["matmul"],
                        "real_tokens_per_step": round(tokens / args.steps, 1),
                        "inputs": ("host arrays passed every step (PCIe-inclusive)" if args.by_value else
                                   "staged in HBM before the timed steps")},

@@ -68,6 +68,7 @@ SIGNATURES = {
     "laya_ctx_destroy": (c_int, [P]),
     "laya_ctx_set_memory_cap": (c_int, [P, c_size]),
     "laya_ctx_memory_in_use": (c_int, [P, ctypes.POINTER(c_size)]),
+    "laya_ctx_set_matmul_precision": (c_int, [P, c_int]),
     "laya_alloc": (c_int, [P, c_size, PP]),
     "laya_free": (c_int, [P, P]),
     "laya_upload": (c_int, [P, P, P, c_size]),

@@ -159,6 +159,15 @@ int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes) {
     });
 }
 
+int laya_ctx_set_matmul_precision(laya_ctx* ctx, int precision) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(precision >= 0 && precision <= LAYA_MATMUL_BF16,
+                     "matmul precision: a combination of LAYA_MATMUL_BF16_FORWARD, _INPUT_GRAD and _WEIGHT_GRAD");
+        ctx->matmul_bf16 = precision;
+    });
+}
+
 int laya_ctx_memory_in_use(laya_ctx* ctx, size_t* bytes) {
     return guarded([&] {
         require_ctx(ctx);

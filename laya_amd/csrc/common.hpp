@@ -84,6 +84,9 @@ struct laya_ctx {
     hipEvent_t timers[16][2] = {};
     int cu_count = 256;
     bool profiling = false;
+    // Products with bf16 operands on the bf16 MFMA (fp32 accumulation) instead of fp32 MFMA, per product
+    // class: bit 0 the forward products (NT), bit 1 the input gradients (NN), bit 2 the weight gradients (TN).
+    int matmul_bf16 = 0;
     std::vector<hipEvent_t> event_pool;
     std::vector<laya::LaunchRecord> launches;
     int next_event = 0;

@@ -388,6 +388,156 @@ __device__ __forceinline__ void tile_mma(const GemmParams& p, const TileCoord& c
     }
 }
 
+// ------------------------------------------------------------------------------ bf16 main loop
+//
+// The same tiles with bf16 operands on v_mfma_f32_32x32x16_bf16 and fp32 accumulation. Operands are read
+// as fp32 (activations, and the fp32 master weights), rounded to bf16 (nearest even, the hardware
+// convert) on their way into LDS, and laid out there as [mn][k] rows of 32 k with an 80-byte stride
+// whatever their global orientation: every MFMA fragment (8 consecutive k of one row) is then one b128
+// read, and 16 consecutive rows fall on distinct bank groups for both the fragment reads and the row
+// writes. The accumulators come out in the fp32 loop's layout for k-contiguous operands, so the same
+// epilogues store them.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+constexpr int KPADH = BK + 8;        // bf16 row stride of an [mn][k] tile
+constexpr int STAGE_H = BM * KPADH;  // bf16 elements per operand tile
+
+// One thread's share of a 128×32 bf16 operand tile, read as fp32, in one of three forms:
+//  KVEC     k-contiguous with float4 access: the fp32 loader's four float4 (rows (tid >> 3) + 32i,
+//           k = 4(tid & 7)), coalesced along k;
+//  KSCALAR  k-contiguous, any extent or alignment: one tile row per thread (tid & 127) and 16
+//           consecutive k (16·(tid >> 7) …), one element at a time;
+//  MNSCALAR mn-contiguous: the same row/k split, one element at a time, coalesced along mn across the
+//           wave.
+// Rows past the edge are clamped; positions at or past a ragged K end read an in-bounds neighbour and
+// become 0.
+enum : int { KVEC = 0, KSCALAR = 1, MNSCALAR = 2 };
+
+template <int KIND>
+struct OperandH;
+
+template <>
+struct OperandH<KVEC> {
+    Loader<true> ld;
+    f32x4 reg[4];
+    __device__ __forceinline__ OperandH(const float* s, long ldl, int mn0, int MN, int tid) : ld(s, ldl, mn0, MN, tid) {}
+    __device__ __forceinline__ void full(int k0) { ld.full(k0, reg); }
+    __device__ __forceinline__ void tail(int k0, int kend) { ld.tail(k0, kend, reg); }
+    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<bf16x4*>(lds + ((tid >> 3) + 32 * i) * KPADH + ((tid & 7) << 2)) =
+                __builtin_convertvector(reg[i], bf16x4);
+    }
+};
+
+// The two one-element-at-a-time forms: element k of this thread's row at src[base + k·kstride].
+template <int KIND>
+struct OperandH {
+    static_assert(KIND == KSCALAR || KIND == MNSCALAR, "operand form");
+    const float* src;
+    unsigned base, kstride;
+    int kq;
+    float v[16];
+    __device__ __forceinline__ OperandH(const float* s, long ldl, int mn0, int MN, int tid) : src(s), kq((tid >> 7) << 4) {
+        const unsigned row = (unsigned)min(mn0 + (tid & 127), MN - 1);
+        base = KIND == KSCALAR ? row * (unsigned)ldl : row;
+        kstride = KIND == KSCALAR ? 1u : (unsigned)ldl;
+    }
+    __device__ __forceinline__ void full(int k0) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = src[base + (unsigned)(k0 + kq + e) * kstride];
+    }
+    __device__ __forceinline__ void tail(int k0, int kend) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int k = k0 + kq + e;
+            const float x = src[base + (unsigned)min(k, kend - 1) * kstride];
+            v[e] = k < kend ? x : 0.0f;
+        }
+    }
+    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+        bf16x8 h0, h1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h0[e] = (__bf16)v[e];
+            h1[e] = (__bf16)v[8 + e];
+        }
+        __bf16* row = lds + (tid & 127) * KPADH + kq;
+        *reinterpret_cast<bf16x8*>(row) = h0;
+        *reinterpret_cast<bf16x8*>(row + 8) = h1;
+    }
+};
+
+// 8 MFMAs of one wave over one LDS stage (K = 32): two steps of 16 k; lane half h holds k = 16s + 8h … + 7
+// of row lane % 32 for both operands.
+__device__ __forceinline__ void mma_stage_h(const __bf16* As, const __bf16* Bs, f32x16 (&acc)[2][2], int wm, int wn,
+                                            int lr, int half) {
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 16) {
+        const int k = ks + 8 * half;
+        bf16x8 a[2], b[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            a[i] = *reinterpret_cast<const bf16x8*>(As + (wm * 64 + 32 * i + lr) * KPADH + k);
+            b[i] = *reinterpret_cast<const bf16x8*>(Bs + (wn * 64 + 32 * i + lr) * KPADH + k);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+}
+
+// tile_mma with bf16 operands: the same K order (rotation, peeled tail), so the result is deterministic.
+template <int AOP, int BOP>
+__device__ __forceinline__ void tile_mma_h(const GemmParams& p, const TileCoord& c, __bf16 (*smem)[2][STAGE_H],
+                                           f32x16 (&acc)[2][2]) {
+    const int len = max(0, c.ke - c.kb);
+    const int nfull = len / BK, ntiles = nfull + (len % BK != 0 ? 1 : 0);
+    const int rot = nfull > 0 ? c.t % nfull : 0;
+
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, half = lane >> 5;
+
+    OperandH<AOP> a(p.A, p.lda, c.m0, p.M, tid);
+    OperandH<BOP> b(p.B, p.ldb, c.n0, p.N, tid);
+    auto fetch = [&](int j) {  // block-uniform branch
+        if (j < nfull) {
+            int q = j + rot;
+            if (q >= nfull) q -= nfull;
+            a.full(c.kb + q * BK);
+            b.full(c.kb + q * BK);
+        } else {
+            a.tail(c.kb + nfull * BK, c.ke);
+            b.tail(c.kb + nfull * BK, c.ke);
+        }
+    };
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+    if (ntiles > 0) {
+        fetch(0);
+        a.store(smem[0][0], tid);
+        b.store(smem[0][1], tid);
+    }
+    __syncthreads();
+    for (int j = 0; j < ntiles; ++j) {
+        const int cur = j & 1;
+        if (j + 1 < ntiles) fetch(j + 1);
+        mma_stage_h(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
+        if (j + 1 < ntiles) {
+            a.store(smem[cur ^ 1][0], tid);
+            b.store(smem[cur ^ 1][1], tid);
+        }
+        __syncthreads();
+    }
+}
+
 // The epilogue of one tile: unguarded when the tile lies inside C.
 template <bool AK, bool BKC, int MODE, bool RES>
 __device__ __forceinline__ void tile_store(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[2][2]) {
@@ -406,6 +556,16 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_kernel(GemmParams p) {
     f32x16 acc[2][2];
     tile_mma<AK, BKC>(p, c, smem, acc);
     tile_store<AK, BKC, MODE, RES>(p, c, acc);
+}
+
+// The bf16 product: the tile's accumulators are in the k-contiguous layout whatever the operands' form.
+template <int AOP, int BOP, int MODE, bool RES>
+__global__ __launch_bounds__(THREADS, 2) void gemm_bf16_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][STAGE_H];
+    const TileCoord c = tile_coord(p, xcd_logical_block());
+    f32x16 acc[2][2];
+    tile_mma_h<AOP, BOP>(p, c, smem, acc);
+    tile_store<true, true, MODE, RES>(p, c, acc);
 }
 
 // dX = dY·W (NN, + residual when RES) and dW += dYᵀ·X (TN, accumulated in place or as split-K
@@ -703,8 +863,62 @@ bool gemm_fast(const GemmParams& p, bool ak, bool bkc) {
            (long)p.M * p.ldc < (1L << 31) && (p.R == nullptr || (long)p.M * p.ldr < (1L << 31)) && pairs_ok;
 }
 
+// The bf16 kernel reads an mn-contiguous operand, or a k-contiguous one without float4 access, one
+// element at a time: it takes every shape whose offsets fit in 32 bits.
+bool gemm_fits_h(const GemmParams& p, bool ak, bool bkc) {
+    auto fits = [](const float* src, long ld, bool kcontig, int mn, int K) {
+        const long last = kcontig ? (long)(mn - 1) * ld + K : (long)(K - 1) * ld + mn;
+        return src != nullptr && K >= 1 && mn >= 1 && ld >= (kcontig ? K : mn) && last < (1L << 31);
+    };
+    return fits(p.A, p.lda, ak, p.M, p.K) && fits(p.B, p.ldb, bkc, p.N, p.K) && (long)p.M * p.ldc < (1L << 31) &&
+           (p.R == nullptr || (long)p.M * p.ldr < (1L << 31));
+}
+
+template <int AOP, int BOP> void launch_h(laya_ctx* ctx, const GemmParams& p, int blocks) {
+    const dim3 g(blocks), b(THREADS);
+    switch (p.mode) {
+        case STORE:
+            if (p.R)
+                hipLaunchKernelGGL((gemm_bf16_kernel<AOP, BOP, STORE, true>), g, b, 0, ctx->stream, p);
+            else
+                hipLaunchKernelGGL((gemm_bf16_kernel<AOP, BOP, STORE, false>), g, b, 0, ctx->stream, p);
+            break;
+        case ACCUMULATE:
+            hipLaunchKernelGGL((gemm_bf16_kernel<AOP, BOP, ACCUMULATE, false>), g, b, 0, ctx->stream, p);
+            break;
+        default: hipLaunchKernelGGL((gemm_bf16_kernel<AOP, BOP, PARTIAL, false>), g, b, 0, ctx->stream, p);
+    }
+    check_launch("gemm_bf16_kernel");
+}
+
+// Picks the operand forms of a bf16 product (float4 access for a k-contiguous operand where it is allowed).
+template <bool AK, bool BKC> void launch_bf16(laya_ctx* ctx, const GemmParams& p, int blocks) {
+    const bool va = AK && operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K);
+    const bool vb = BKC && operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K);
+    if constexpr (AK && BKC) {
+        if (va && vb) launch_h<KVEC, KVEC>(ctx, p, blocks);
+        else if (va) launch_h<KVEC, KSCALAR>(ctx, p, blocks);
+        else if (vb) launch_h<KSCALAR, KVEC>(ctx, p, blocks);
+        else launch_h<KSCALAR, KSCALAR>(ctx, p, blocks);
+    } else if constexpr (AK) {
+        if (va) launch_h<KVEC, MNSCALAR>(ctx, p, blocks);
+        else launch_h<KSCALAR, MNSCALAR>(ctx, p, blocks);
+    } else {
+        static_assert(!BKC, "no TN-with-k-contiguous-B layout");
+        launch_h<MNSCALAR, MNSCALAR>(ctx, p, blocks);
+    }
+}
+
+// The precision class of a layout: NT forward (bit 0), NN input gradient (bit 1), TN weight gradient (bit 2).
+constexpr int layout_bit(bool ak, bool bkc) { return ak && bkc ? 1 : ak ? 2 : 4; }
+
 template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int blocks) {
     const dim3 g(blocks), b(THREADS);
+    if (ctx->matmul_bf16 & layout_bit(AK, BKC)) {
+        LAYA_REQUIRE(gemm_fits_h(p, AK, BKC), "gemm: bf16 operands need offsets below 2^31");
+        launch_bf16<AK, BKC>(ctx, p, blocks);
+        return;
+    }
     if (!gemm_fast(p, AK, BKC)) {
         switch (p.mode) {
             case STORE: hipLaunchKernelGGL((gemm_generic_kernel<AK, BKC, STORE>), g, b, 0, ctx->stream, p); break;
@@ -804,8 +1018,10 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
     }
     const int blocks = tiles * p.splits;
     {
-        static const char* names[3] = {"gemm_nt", "gemm_nn", "gemm_tn"};
-        ProfileScope scope(ctx, names[(int)layout], 2.0 * M * N * (double)K, 0.0);
+        static const char* names[2][3] = {{"gemm_nt", "gemm_nn", "gemm_tn"},
+                                          {"gemm_nt_bf16", "gemm_nn_bf16", "gemm_tn_bf16"}};
+        const int bit = layout == GemmLayout::NT ? 1 : layout == GemmLayout::NN ? 2 : 4;
+        ProfileScope scope(ctx, names[(ctx->matmul_bf16 & bit) ? 1 : 0][(int)layout], 2.0 * M * N * (double)K, 0.0);
         switch (layout) {
             case GemmLayout::NT: launch<true, true>(ctx, p, blocks); break;
             case GemmLayout::NN: launch<true, false>(ctx, p, blocks); break;
@@ -826,6 +1042,13 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
     p.rope_cos = cos_t;
     p.rope_sin = sin_t;
     p.rope_cols = rope_cols;
+    if (ctx->matmul_bf16 & 1) {
+        ProfileScope scope(ctx, "gemm_nt_bf16", 2.0 * M * N * (double)K, 0.0);
+        hipLaunchKernelGGL((gemm_bf16_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
+                           dim3(THREADS), 0, ctx->stream, p);
+        check_launch("gemm_bf16_kernel");
+        return;
+    }
     ProfileScope scope(ctx, "gemm_nt", 2.0 * M * N * (double)K, 0.0);
     hipLaunchKernelGGL((gemm_kernel<true, true, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n), dim3(THREADS), 0,
                        ctx->stream, p);
@@ -840,7 +1063,7 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
     nn.mode = STORE;
     // dW[out, in] += dy[rows, out]ᵀ · x[rows, in]     (TN, K = rows)
     GemmParams tn = make_params(out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr, 0);
-    if (!gemm_fast(nn, true, false) || !gemm_fast(tn, false, false)) {
+    if ((ctx->matmul_bf16 & 6) || !gemm_fast(nn, true, false) || !gemm_fast(tn, false, false)) {
         gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual,
              in);
         gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);

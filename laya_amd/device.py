@@ -18,6 +18,7 @@ class Context:
         check(lib().laya_ctx_create(device, ctypes.byref(h)))
         self.handle = h.value
         self.device = device
+        self.matmul_precision = "fp32"
         self._dependents = weakref.WeakSet()
 
     def register(self, obj) -> None:
@@ -42,6 +43,19 @@ class Context:
 
     def set_memory_cap(self, nbytes: int) -> None:
         check(lib().laya_ctx_set_memory_cap(self.handle, nbytes))
+
+    # Products that take bf16 operands under each policy: forward (y = x·Wᵀ), input gradient (dx = dy·W),
+    # weight gradient (dW += dyᵀ·x).
+    MATMUL_POLICIES = {"fp32": 0, "bf16": 7, "bf16-forward": 1, "bf16-backward": 6, "bf16-weight-grad": 4}
+
+    def set_matmul_precision(self, precision: str) -> None:
+        """The operand precision of the matrix products launched afterwards: 'fp32' (default), 'bf16'
+        (every product), or one class in bf16 ('bf16-forward', 'bf16-backward', 'bf16-weight-grad').
+        bf16 operands are rounded to nearest even; accumulation and outputs stay fp32."""
+        if precision not in self.MATMUL_POLICIES:
+            raise ValueError(f"matmul precision '{precision}': expected one of {sorted(self.MATMUL_POLICIES)}")
+        check(lib().laya_ctx_set_matmul_precision(self.handle, self.MATMUL_POLICIES[precision]))
+        self.matmul_precision = precision
 
     def memory_in_use(self) -> int:
         v = ctypes.c_size_t()

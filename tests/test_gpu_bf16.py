@@ -1,0 +1,226 @@
+"""The bf16 matrix-product path (bf16 operands on the bf16 matrix cores, fp32 accumulation, fp32 master
+weights, gradients and statistics) against the oracle.
+
+Two bars. Exactness: each product equals the fp64 product of the bf16-rounded operands up to fp32
+accumulation order (relative L2 ≤ 2e-5) — this pins the rounding (nearest even), the fragment layouts and
+the epilogues. Tolerance: against the exact fp32-input result, relative L2 ≤ 2e-2 per tensor, the bf16 bar.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from fixtures import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+laya = pytest.importorskip("laya_amd.ops")
+
+
+def bf16(a):
+    """Round to bf16, nearest even (finite inputs)."""
+    bits = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    return ((bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from laya_amd.device import Context
+    print("GPU bf16 tests: creating context on device 0", flush=True)
+    c = Context(0)
+    c.set_matmul_precision("bf16")
+    yield c
+    c.close()
+
+
+def dev(ctx, a):
+    from laya_amd.device import DeviceArray
+    return DeviceArray.from_numpy(ctx, np.asarray(a))
+
+
+@pytest.mark.parametrize("rows,inn,out", [(37, 96, 130), (333, 100, 260), (1000, 768, 2304), (2048, 1152, 768),
+                                          (4100, 64, 96), (9000, 768, 2304)])
+def test_bf16_linear_is_the_product_of_rounded_operands(ctx, rows, inn, out):
+    """Forward with bias and residual (NT), dx (NN) and dW accumulated twice (TN, split-K at 4100 and 9000
+    rows), in bf16."""
+    print(f"bf16 linear rows={rows} in={inn} out={out}", flush=True)
+    rng = np.random.default_rng(rows + 3 * inn + out)
+    x = rng.standard_normal((rows, inn)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+    b = rng.standard_normal(out).astype(np.float32)
+    res = rng.standard_normal((rows, out)).astype(np.float32)
+    dy = rng.standard_normal((rows, out)).astype(np.float32)
+    w, bias = laya.Parameter(ctx, "w", W, True), laya.Parameter(ctx, "b", b, True)
+    y = dev(ctx, np.zeros((rows, out), np.float32))
+    dx = dev(ctx, np.zeros((rows, inn), np.float32))
+    xd, dyd = dev(ctx, x), dev(ctx, dy)
+    laya.linear(w, bias, xd, rows, y, residual=dev(ctx, res))
+    laya.linear_backward(w, bias, xd, dyd, rows, dx)
+    laya.linear_backward(w, bias, xd, dyd, rows, dx)
+    xb, Wb, dyb = (bf16(a).astype(np.float64) for a in (x, W, dy))
+    y_exact = xb @ Wb.T + b + res
+    dx_exact = dyb @ Wb
+    dW_exact = 2 * dyb.T @ xb
+    assert rel_l2(y_exact, y.numpy()) < 2e-5
+    assert rel_l2(dx_exact, dx.numpy()) < 2e-5
+    assert rel_l2(dW_exact, w.gradient.numpy()) < 2e-5
+    assert rel_l2(2 * dy.sum(0, dtype=np.float64), bias.gradient.numpy()) < 1e-6  # the bias sum stays fp32
+    x64, W64, dy64 = (a.astype(np.float64) for a in (x, W, dy))
+    assert rel_l2(x64 @ W64.T + b + res, y.numpy()) < 2e-2
+    assert rel_l2(dy64 @ W64, dx.numpy()) < 2e-2
+    assert rel_l2(2 * dy64.T @ x64, w.gradient.numpy()) < 2e-2
+
+
+def test_bf16_precision_switch_is_per_context():
+    """fp32 stays the default: a second context multiplies in fp32 while another is in bf16."""
+    from laya_amd.device import Context
+    a, b = Context(0), Context(0)
+    try:
+        b.set_matmul_precision("bf16")
+        rng = np.random.default_rng(0)
+        x = rng.standard_normal((300, 256)).astype(np.float32)
+        W = (0.05 * rng.standard_normal((128, 256))).astype(np.float32)
+        outs = []
+        for c in (a, b):
+            w = laya.Parameter(c, "w", W, False)
+            y = dev(c, np.zeros((300, 128), np.float32))
+            laya.linear(w, None, dev(c, x), 300, y)
+            outs.append(y.numpy())
+        exact = x.astype(np.float64) @ W.astype(np.float64).T
+        rounded = bf16(x).astype(np.float64) @ bf16(W).astype(np.float64).T
+        assert rel_l2(exact, outs[0]) < 1e-6
+        assert rel_l2(rounded, outs[1]) < 2e-5 and rel_l2(exact, outs[1]) > 1e-4
+        with pytest.raises(ValueError):
+            a.set_matmul_precision("fp16")
+    finally:
+        a.close()
+        b.close()
+
+
+def _heads(n):
+    """choice K = 8, score K = 4, noul K = 2, cycling."""
+    return [(8, 4, 2)[i % 3] for i in range(n)], [i % 3 for i in range(n)]
+
+
+def _grads_match(names, want, got, bar, skip=("scorer.3.bias",)):
+    """Per-tensor relative L2 against the fp32 result; the output bias's gradient is Σ of a softmax-CE
+    gradient, zero up to rounding in any implementation, so it has no relative error to measure."""
+    errors = {n: rel_l2(want[n], got[n]) for n in names if n not in skip and n in want}
+    top = sorted(errors.items(), key=lambda kv: -kv[1])[:8]
+    print("largest gradient rel-L2: " + ", ".join(f"{n} {e:.2e}" for n, e in top), flush=True)
+    bad = {n: e for n, e in errors.items() if e >= bar}
+    assert not bad, bad
+    return max(errors.values())
+
+
+def _bf16_vs_oracle(ctx, batch, seed):
+    """The backward products in bf16 (forward in fp32) against the fp32 oracle."""
+    from laya_amd.config import modernbert_base
+    from laya_amd.model import TrainableDecisionModel
+    import helpers
+    mc = modernbert_base()
+    o = oracle.OracleModel(mc)
+    params = helpers.random_params(o.shapes, seed, std=0.02)
+    rng = np.random.default_rng(seed + 1)
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+    o.set_params(params)
+    o.set_head_dropout(0.1)
+    logits_o = o.forward(batch, training=True, keep_tape=True, seed=seed).astype(np.float32)
+    _, g = oracle.cross_entropy(batch.n_options, logits_o, targets, 1.0, float(batch.n_items))
+    o.backward(g)
+    ctx.set_matmul_precision("bf16-backward")
+    try:
+        m = TrainableDecisionModel(mc, ctx)
+        m.set_params(params)
+        m.head_dropout = 0.1
+        logits_m = m.forward(batch, training=True, seed=seed)
+        m.backward(g)
+    finally:
+        ctx.set_matmul_precision("bf16")
+    assert rel_l2(logits_o, logits_m) < 1e-4  # the forward is fp32
+    names = [n for n in m.names if m.has_grad(n)]
+    worst = _grads_match(names, {n: o.grad(n) for n in names}, {n: m.grad(n) for n in names}, 2e-2)
+    print(f"bf16 backward vs fp32 oracle: worst gradient rel-L2 {worst:.2e} over {len(names)} tensors", flush=True)
+    m.close()
+
+
+def test_bf16_modernbert_base_gradients_match_the_fp32_oracle(ctx):
+    """Batch 32 × 1024 in bf16 at reduced size: ModernBERT-base (22 layers, 164M parameters), 4 × 256 tokens
+    without padding, heads choice 8 / score 4 / noul 2, summed CE, head dropout 0.1: every gradient of the
+    bf16 backward products within the bf16 bar of the fp32 oracle."""
+    from laya_amd.batch import synthetic_batch
+    print("bf16 model: ModernBERT-base 22 layers, 4 x 256", flush=True)
+    rng = np.random.default_rng(31)
+    opts, qt = _heads(4)
+    _bf16_vs_oracle(ctx, synthetic_batch(rng, [256] * 4, opts, qt, 50368), 31)
+
+
+def test_bf16_packed_zipf_batch_gradients_match_the_fp32_oracle(ctx):
+    """The variable-length packed batch in bf16 at reduced size: 6 sequences of lengths U[16, 400]
+    concatenated with per-sequence RoPE positions, ids Zipf(1.1) over the 50368 vocabulary (repeated ids
+    in the embedding-gradient scatter)."""
+    from laya_amd.batch import synthetic_batch
+    print("bf16 model: ModernBERT-base 22 layers, 6 packed sequences, Zipf ids", flush=True)
+    rng = np.random.default_rng(41)
+    lengths = rng.integers(16, 401, 6)
+    opts, qt = _heads(6)
+    _bf16_vs_oracle(ctx, synthetic_batch(rng, lengths, opts, qt, 50368, zipf=1.1), 41)
+
+
+def _grads(m, c, batch, targets, seed, forward_policy, backward_policy):
+    c.set_matmul_precision(forward_policy)
+    m.zero_gradients()
+    logits = m.forward(batch, training=True, seed=seed)
+    _, g = oracle.cross_entropy(batch.n_options, logits, targets, 1.0, float(batch.n_items))
+    c.set_matmul_precision(backward_policy)
+    m.backward(g)
+    return logits, {n: m.grad(n) for n in m.names if m.has_grad(n)}
+
+
+def _bf16_at_full_size(batch, seed):
+    """At full size, on the GPU (the fp32 path is held to the oracle at 1e-4 on smaller inputs):
+    - the bf16 backward products on an fp32 forward against the fp32 backward: every gradient within 2e-2;
+    - with the forward in bf16 too (every product in bf16), the bf16 backward against an fp32 backward of
+      the same bf16 forward: every gradient within 2e-2, and the bf16 forward's logits within 2e-2 of fp32.
+    (A bf16 forward evaluates a slightly different function — activations move by ~1e-2 and near-zero
+    ReLU inputs flip — so its gradients are compared with the backward of that same forward.)"""
+    from laya_amd.config import modernbert_base
+    from laya_amd.device import Context
+    from laya_amd.model import TrainableDecisionModel
+    c = Context(0)
+    try:
+        m = TrainableDecisionModel.synthetic(modernbert_base(), seed=seed, std=0.02, ctx=c)
+        m.head_dropout = 0.1
+        rng = np.random.default_rng(seed)
+        targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+        l32, g32 = _grads(m, c, batch, targets, seed, "fp32", "fp32")
+        _, gbwd = _grads(m, c, batch, targets, seed, "fp32", "bf16-backward")
+        worst = _grads_match(g32.keys(), g32, gbwd, 2e-2)
+        print(f"bf16 backward products vs fp32: worst gradient rel-L2 {worst:.2e}", flush=True)
+        l16, gf = _grads(m, c, batch, targets, seed, "bf16-forward", "bf16-forward")  # bf16 forward, fp32 backward
+        _, gall = _grads(m, c, batch, targets, seed, "bf16", "bf16")
+        assert rel_l2(l32, l16) < 2e-2
+        worst = _grads_match(gf.keys(), gf, gall, 2e-2)
+        print(f"every product in bf16: logits rel-L2 {rel_l2(l32, l16):.2e}; bf16 vs fp32 backward of the bf16 "
+              f"forward: worst gradient rel-L2 {worst:.2e}", flush=True)
+        m.close()
+    finally:
+        c.close()
+
+
+def test_bf16_at_batch_32x1024(ctx):
+    """Batch 32 × 1024, no padding, bf16 products (32,768 tokens)."""
+    from laya_amd.batch import synthetic_batch
+    print("bf16 model: 32 x 1024 full size", flush=True)
+    rng = np.random.default_rng(51)
+    opts, qt = _heads(32)
+    _bf16_at_full_size(synthetic_batch(rng, [1024] * 32, opts, qt, 50368), 51)
+
+
+def test_bf16_at_64_packed_zipf_sequences(ctx):
+    """64 sequences of lengths U[16, 2048] packed without padding, Zipf(1.1) ids, bf16 products."""
+    from laya_amd.batch import synthetic_batch
+    print("bf16 model: 64 packed sequences U[16, 2048], Zipf ids, full size", flush=True)
+    rng = np.random.default_rng(61)
+    lengths = rng.integers(16, 2049, 64)
+    opts, qt = _heads(64)
+    _bf16_at_full_size(synthetic_batch(rng, lengths, opts, qt, 50368, zipf=1.1), 61)
