@@ -151,3 +151,22 @@ def modernbert_base(layers: Optional[int] = None) -> ModelConfig:
                         num_hidden_layers=22 if layers is None else layers, num_attention_heads=12,
                         local_attention=128, global_attn_every_n_layers=3)
     return ModelConfig(encoder=enc, head_layers=2, n_act=2)
+
+
+def modernbert_large(layers: Optional[int] = None) -> ModelConfig:
+    """ModernBERT-large shape (the reference's English and TypedDecisions checkpoints, 421M parameters with
+    the head): 28 layers, d 1024, 16 heads × 64, GeGLU intermediate 2624, vocab 50368, every third layer
+    global (θ 160000), the rest sliding window 128 (θ 10000)."""
+    enc = EncoderConfig(vocab_size=50368, hidden_size=1024, intermediate_size=2624,
+                        num_hidden_layers=28 if layers is None else layers, num_attention_heads=16,
+                        local_attention=128, global_attn_every_n_layers=3)
+    return ModelConfig(encoder=enc, head_layers=2, n_act=2)
+
+
+def mmbert_base(layers: Optional[int] = None) -> ModelConfig:
+    """mmBERT-base shape (the reference's Multilingual checkpoint): ModernBERT-base widths with a
+    256,000-token vocabulary."""
+    enc = EncoderConfig(vocab_size=256000, hidden_size=768, intermediate_size=1152,
+                        num_hidden_layers=22 if layers is None else layers, num_attention_heads=12,
+                        local_attention=128, global_attn_every_n_layers=3)
+    return ModelConfig(encoder=enc, head_layers=2, n_act=2)

@@ -291,3 +291,76 @@ def test_rlcd_step_on_the_device_matches_the_host_objective(ctx):
             # both sides hold rounding noise there, hence the absolute floor.
             want, got = b.grad(name), a.grad(name)
             assert np.linalg.norm(got - want) <= 1e-5 * np.linalg.norm(want) + 1e-6, name
+
+
+def _large_shape_case(ctx, mc, trainable, lengths, seed, zipf=0.0):
+    """One training-mode forward/backward (head dropout 0.1) of a checkpoint-sized shape on the GPU and on
+    the oracle, weights N(0, 0.02) with non-trivial norms. Each gradient is held to the exact (fp64 oracle)
+    result by the reference test's metric and by rel-L2 at max(bar, 4 × the error of the fp32 oracle on the
+    same tensor): the head's ReLU can flip a pre-activation within fp32 rounding of zero in any two fp32
+    implementations, which moves single elements."""
+    from laya_amd.batch import synthetic_batch
+    from laya_amd.model import TrainableDecisionModel
+    o = oracle.OracleModel(mc)
+    params = random_params(o.shapes, seed, std=0.02)
+    rng = np.random.default_rng(seed + 1)
+    opts = [(8, 4, 2)[i % 3] for i in range(len(lengths))]
+    batch = synthetic_batch(rng, lengths, opts, [i % 3 for i in range(len(lengths))], mc.encoder.vocab_size, zipf)
+    dlogits = rng.standard_normal(batch.n_markers).astype(np.float32)
+    refs = []
+    for double in (False, True):
+        r = oracle.OracleModel(mc, double=double) if double else o
+        r.set_params(params)
+        r.set_head_dropout(0.1)
+        r.set_trainable_encoder_layers(trainable)
+        logits_r = r.forward(batch, training=True, keep_tape=True, seed=seed)
+        r.backward(dlogits)
+        refs.append((r, logits_r))
+    (o32, _), (o64, logits_o) = refs
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    m.head_dropout = 0.1
+    m.set_trainable_encoder_layers(trainable)
+    logits_m = m.forward(batch, training=True, seed=seed)
+    m.backward(dlogits)
+    assert np.abs(logits_o - logits_m).max() < 1e-3
+    checked = 0
+    for name in m.names:
+        assert m.has_grad(name) == o64.has_grad(name), name
+        if not m.has_grad(name) or name == "scorer.3.bias":
+            continue
+        exact, ref32, got = o64.grad(name), o32.grad(name), m.grad(name)
+        cos = float(np.dot(exact.ravel(), got.ravel().astype(np.float64)) /
+                    max(np.linalg.norm(exact) * np.linalg.norm(got), 1e-300))
+        assert cos > 0.99999, (name, cos)  # TrainingGradientTests.cs:213
+        assert max_rel(exact, got) < max(1e-3, 4 * max_rel(exact, ref32)), (name, max_rel(exact, got))
+        assert rel_l2(exact, got) < max(1e-4, 4 * rel_l2(exact, ref32)), (name, rel_l2(exact, got))
+        checked += 1
+    m.close()
+    return checked
+
+
+def test_modernbert_large_gradients_match_the_oracle(ctx):
+    """The English / TypedDecisions checkpoint shape (ModernBERT-large: 28 layers, d 1024, 16 heads,
+    GeGLU 2624, 421M parameters with the head), all layers trainable, 2 sequences of 160 and 96 tokens."""
+    from laya_amd.config import modernbert_large
+    print("model: ModernBERT-large 28 layers, 2 sequences", flush=True)
+    n = _large_shape_case(ctx, modernbert_large(), None, [160, 96], 71)
+    assert n >= 195  # 28 layers × 6 tensors (layer 0: 5), embeddings, final norm, head, scorer
+
+
+def test_partial_training_of_the_top_layers_at_large_shape(ctx):
+    """SetTrainableEncoderLayers(4) (TrainableDecisionModel.cs:206-231) on the large shape: only the top
+    four layers, the final norm and the head get gradients, and those match the oracle."""
+    from laya_amd.config import modernbert_large
+    print("model: ModernBERT-large, top 4 layers trainable", flush=True)
+    n = _large_shape_case(ctx, modernbert_large(), 4, [140, 70, 33], 72)
+    assert 30 < n < 100
+
+
+def test_mmbert_base_gradients_match_the_oracle(ctx):
+    """The Multilingual checkpoint shape (mmBERT-base: ModernBERT-base widths, 256,000-token vocabulary),
+    Zipf(1.1) ids so embedding rows repeat."""
+    from laya_amd.config import mmbert_base
+    print("model: mmBERT-base 22 layers, vocab 256000", flush=True)
+    _large_shape_case(ctx, mmbert_base(), None, [120, 64, 40], 73, zipf=1.1)
