@@ -14,7 +14,7 @@
 // (its column) and 16 keys (its rows). Those registers are exactly the B operand of Oᵀ = Vᵀ·Pᵀ, so
 // P never leaves registers, and each query's running max / sum live in one lane pair.
 // The backward runs two kernels, both without atomics (deterministic):
-//   dkv: each wave owns 32 keys (K, V in registers) and sweeps the query tiles: S = Q·Kᵀ,
+//   dkv: each wave owns 32 keys (K in LDS, V in registers) and sweeps the query tiles: S = Q·Kᵀ,
 //        dVᵀ += dOᵀ·P, dP = dO·Vᵀ, dS, dKᵀ += Qᵀ·dS;
 //   dq:  each wave owns 32 queries (Q, dO in registers) and sweeps the key tiles: Sᵀ, dPᵀ, dSᵀ,
 //        dQᵀ += Kᵀ·dSᵀ.
@@ -276,12 +276,16 @@ __global__ __launch_bounds__(THREADS) void attn_dot_kernel(const float* __restri
     }
 }
 
+// Two waves per SIMD: the block's keys sit in LDS (read back as b128 fragments by the wave that owns them)
+// and each query tile is loaded straight into LDS, which keeps the kernel under 256 registers without
+// spills; the other resident block hides the tile loads.
 template <int D>
-__global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
+__global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_kernel(Params p) {
     using S = Shape<D>;
     __shared__ __attribute__((aligned(16))) float Qs[TILE * S::KS];
     __shared__ __attribute__((aligned(16))) float Os[TILE * S::VS];  // dO rows
     __shared__ float lse_s[TILE], dot_s[TILE];
+    __shared__ __attribute__((aligned(16))) float Ks[BLOCK_ROWS * S::KS];  // the block's keys
 
     const int seg = blockIdx.y, head = blockIdx.z;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
@@ -296,10 +300,16 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
     const long stride = 3L * p.hidden;
     const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
 
-    f32x4 kv[S::G], vv[S::G];
+    f32x4 vv[S::G];
     const long krow = (long)(start + (kvalid ? key : 0)) * stride;
-    load_lane_row<D>(p.qkv + krow + kcol, kvalid, h, kv);
     load_lane_row<D>(p.qkv + krow + vcol, kvalid, h, vv);
+    {
+        f32x4 kv[S::G];
+        load_lane_row<D>(p.qkv + krow + kcol, kvalid, h, kv);
+#pragma unroll
+        for (int g = 0; g < S::G; ++g) st4(Ks + (wave * WAVE_ROWS + lr) * S::KS + 8 * g + 4 * h, kv[g]);
+    }
+    const float* krow_s = Ks + (wave * WAVE_ROWS + lr) * S::KS + 4 * h;
 
     int qbeg = 0, qend = L, wbeg = 0, wend = L;
     if (hw >= 0) {
@@ -320,28 +330,21 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
     // of the products.
     const float* qbase = p.qkv + (long)start * stride + qcol;
     const float* obase = p.dcontext + (long)start * p.hidden + qcol;
-    PlainStage<D> qst, ost;
-    float lse_r = 0.0f, dot_r = 0.0f;
-    auto fetch = [&](int t0) {
-        fetch_plain<D>(qst, qbase, stride, L, t0);
-        fetch_plain<D>(ost, obase, p.hidden, L, t0);
-        const int t = t0 + (int)threadIdx.x;
-        if (threadIdx.x < TILE) {
-            lse_r = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
-            dot_r = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
-        }
-    };
-    fetch(qbeg);
     for (int qt0 = qbeg; qt0 < qend; qt0 += TILE) {
         __syncthreads();
-        commit_plain<D, S::KS>(qst, Qs);
-        commit_plain<D, S::VS>(ost, Os);
-        if (threadIdx.x < TILE) {
-            lse_s[threadIdx.x] = lse_r;
-            dot_s[threadIdx.x] = dot_r;
+        {
+            PlainStage<D> qst, ost;
+            fetch_plain<D>(qst, qbase, stride, L, qt0);
+            fetch_plain<D>(ost, obase, p.hidden, L, qt0);
+            const int t = qt0 + (int)threadIdx.x;
+            if (threadIdx.x < TILE) {
+                lse_s[threadIdx.x] = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
+                dot_s[threadIdx.x] = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
+            }
+            commit_plain<D, S::KS>(qst, Qs);
+            commit_plain<D, S::VS>(ost, Os);
         }
         __syncthreads();
-        if (qt0 + TILE < qend) fetch(qt0 + TILE);  // block-uniform
 #pragma unroll
         for (int st = 0; st < TILE / 32; ++st) {
             const int qbs = qt0 + 32 * st;
@@ -354,9 +357,10 @@ __global__ __launch_bounds__(THREADS) void attn_bwd_dkv_kernel(Params p) {
             for (int g = 0; g < S::G; ++g) {
                 const f32x4 qf = ld4(qrow + 8 * g);
                 const f32x4 of = ld4(orow + 8 * g);
+                const f32x4 kf = ld4(krow_s + 8 * g);
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
-                    s = mfma(qf[c], kv[g][c], s);
+                    s = mfma(qf[c], kf[c], s);
                     dp = mfma(of[c], vv[g][c], dp);
                 }
             }
