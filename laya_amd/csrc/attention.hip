@@ -194,7 +194,8 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
 #pragma unroll
         for (int st = 0; st < TILE / 32; ++st) {
             const int kbs = kt0 + 32 * st;
-            if (kbs >= wend || kbs + 32 <= wbeg || kbs >= kend) continue;  // wave-uniform
+            // Wave-uniform: outside this wave's window, or a wave whose rows all lie past the segment end.
+            if (kbs >= wend || kbs + 32 <= wbeg || kbs >= kend || q0w >= L) continue;
             f32x16 s = f32x16{};
             const float* krow = Ks + (32 * st + lr) * S::KS + 4 * h;
 #pragma unroll
@@ -348,7 +349,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_kernel(Params p) {
 #pragma unroll
         for (int st = 0; st < TILE / 32; ++st) {
             const int qbs = qt0 + 32 * st;
-            if (qbs >= wend || qbs + 32 <= wbeg || qbs >= qend) continue;  // wave-uniform
+            // Wave-uniform: outside this wave's window, or a wave whose keys all lie past the segment end.
+            if (qbs >= wend || qbs + 32 <= wbeg || qbs >= qend || k0w >= L) continue;
             // S[q][key] = Q·Kᵀ: lane column = its key, rows = 16 queries.
             f32x16 s = f32x16{}, dp = f32x16{};
             const float* qrow = Qs + (32 * st + lr) * S::KS + 4 * h;
@@ -465,7 +467,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
 #pragma unroll
         for (int st = 0; st < TILE / 32; ++st) {
             const int kbs = kt0 + 32 * st;
-            if (kbs >= wend || kbs + 32 <= wbeg || kbs >= kend) continue;  // wave-uniform
+            // Wave-uniform: outside this wave's window, or a wave whose rows all lie past the segment end.
+            if (kbs >= wend || kbs + 32 <= wbeg || kbs >= kend || q0w >= L) continue;
             f32x16 s = f32x16{}, dp = f32x16{};
             const float* krow = Ks + (32 * st + lr) * S::KS + 4 * h;
             const float* vrow = Vs + (32 * st + lr) * S::KS + 4 * h;
