@@ -50,18 +50,24 @@ int laya_ctx_destroy(laya_ctx* ctx);
 /* Caps the bytes laya_alloc may hold (0 = no cap); an allocation over it fails with LAYA_ERR_MEMORY. */
 int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes);
 /* Precision of the matrix products launched on the context afterwards (linear layers and the model's
- * projections; attention and the elementwise kernels stay fp32), per product class. A bf16 class rounds both operands
+ * projections; attention and the elementwise kernels stay fp32), per product class. An fp32 class (the
+ * default) is computed from an exact three-piece bf16 split of each operand: six bf16 matrix-core products
+ * per fp32 product, accumulated in fp32, so the result carries fp32 rounding only (within 1e-6 relative
+ * L2 of the fp64 product on every tested shape, as the fp32 matrix-core path); LAYA_MATMUL_FP32_MFMA
+ * selects the fp32 matrix cores instead. A bf16 class rounds both operands
  * to bf16 (nearest even) as they are staged and multiplies on the bf16 matrix cores with fp32
  * accumulation and fp32 outputs: the mixed-precision mode (bf16 weights and activations in the
  * products, fp32 master weights, gradients and statistics). No counterpart in the reference, whose
  * products are all fp32 (PackedMatrixBf16, PackedMatrixBf16.cs:7-21, only stores weights in bf16 and
  * widens them to fp32 before multiplying). */
 enum {
-    LAYA_MATMUL_FP32 = 0,
+    LAYA_MATMUL_FP32 = 0,             /* fp32-accurate products (the default), from bf16 pieces (below) */
     LAYA_MATMUL_BF16_FORWARD = 1,     /* y = x·Wᵀ (and the fused RoPE projection) */
     LAYA_MATMUL_BF16_INPUT_GRAD = 2,  /* dx = dy·W */
     LAYA_MATMUL_BF16_WEIGHT_GRAD = 4, /* dW += dyᵀ·x */
-    LAYA_MATMUL_BF16 = 7              /* every product */
+    LAYA_MATMUL_BF16 = 7,             /* every product */
+    LAYA_MATMUL_FP32_MFMA = 8,        /* the fp32 classes on v_mfma_f32_32x32x2_f32 instead */
+    LAYA_MATMUL_SPLIT_ALL = 7
 };
 int laya_ctx_set_matmul_precision(laya_ctx* ctx, int precision);
 int laya_ctx_memory_in_use(laya_ctx* ctx, size_t* bytes);

@@ -162,9 +162,11 @@ int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes) {
 int laya_ctx_set_matmul_precision(laya_ctx* ctx, int precision) {
     return guarded([&] {
         require_ctx(ctx);
-        LAYA_REQUIRE(precision >= 0 && precision <= LAYA_MATMUL_BF16,
-                     "matmul precision: a combination of LAYA_MATMUL_BF16_FORWARD, _INPUT_GRAD and _WEIGHT_GRAD");
-        ctx->matmul_bf16 = precision;
+        LAYA_REQUIRE(precision >= 0 && precision <= (LAYA_MATMUL_BF16 | LAYA_MATMUL_FP32_MFMA),
+                     "matmul precision: LAYA_MATMUL_FP32, LAYA_MATMUL_FP32_MFMA, or bf16 classes");
+        ctx->matmul_bf16 = precision & LAYA_MATMUL_BF16;
+        // fp32 classes use split products unless LAYA_MATMUL_FP32_MFMA asks for the fp32 matrix cores.
+        ctx->matmul_split = (precision & LAYA_MATMUL_FP32_MFMA) ? 0 : (LAYA_MATMUL_SPLIT_ALL & ~ctx->matmul_bf16);
     });
 }
 

@@ -87,6 +87,8 @@ struct laya_ctx {
     // Products with bf16 operands on the bf16 MFMA (fp32 accumulation) instead of fp32 MFMA, per product
     // class: bit 0 the forward products (NT), bit 1 the input gradients (NN), bit 2 the weight gradients (TN).
     int matmul_bf16 = 0;
+    // fp32 products from three-piece bf16 splits (fp32-accurate, on the bf16 MFMA), same class bits.
+    int matmul_split = LAYA_MATMUL_SPLIT_ALL;
     std::vector<hipEvent_t> event_pool;
     std::vector<laya::LaunchRecord> launches;
     int next_event = 0;

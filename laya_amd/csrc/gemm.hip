@@ -339,7 +339,7 @@ __device__ __forceinline__ int opaque_tid() {
 // that all fetched the same K columns at once would hit the same few memory channels; staggered
 // starts spread them. The sum order is fixed per tile, so results stay deterministic. Ends with a
 // barrier, so the caller may start another tile on the same LDS.
-template <bool AK, bool BKC>
+template <bool AK, bool BKC, int NSTAGE = 2>
 __device__ __forceinline__ void tile_mma(const GemmParams& p, const TileCoord& c, float (*smem)[2][STAGE],
                                          f32x16 (&acc)[2][2]) {
     const int len = max(0, c.ke - c.kb);
@@ -370,6 +370,21 @@ __device__ __forceinline__ void tile_mma(const GemmParams& p, const TileCoord& c
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
+    if constexpr (NSTAGE == 1) {
+        // One LDS stage (half the LDS, so three workgroups fit on a CU): the next K tile waits in registers
+        // while this one is multiplied, and is stored once every wave has finished reading the stage.
+        if (ntiles > 0) fetch(0);
+        for (int j = 0; j < ntiles; ++j) {
+            __syncthreads();
+            store_tile<AK>(smem[0][0], ra, tid);
+            store_tile<BKC>(smem[0][1], rb, tid);
+            __syncthreads();
+            if (j + 1 < ntiles) fetch(j + 1);
+            mma_stage<AK, BKC>(smem[0][0], smem[0][1], acc, wm, wn, lr, kh);
+        }
+        __syncthreads();
+        return;
+    }
     if (ntiles > 0) {
         fetch(0);
         store_tile<AK>(smem[0][0], ra, tid);
@@ -556,6 +571,137 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_kernel(GemmParams p) {
     f32x16 acc[2][2];
     tile_mma<AK, BKC>(p, c, smem, acc);
     tile_store<AK, BKC, MODE, RES>(p, c, acc);
+}
+
+// The same product with one LDS stage, three workgroups per CU: for tile counts that would leave the
+// last round of two-per-CU workgroups mostly empty (e.g. 654 tiles on 512 slots: one round instead of two).
+template <bool AK, bool BKC, int MODE, bool RES>
+__global__ __launch_bounds__(THREADS, 3) void gemm3_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) float smem[1][2][STAGE];
+    const TileCoord c = tile_coord(p, xcd_logical_block());
+    f32x16 acc[2][2];
+    tile_mma<AK, BKC, 1>(p, c, smem, acc);
+    tile_store<AK, BKC, MODE, RES>(p, c, acc);
+}
+
+// ------------------------------------------------------------------------------ fp32 from bf16 pieces
+//
+// fp32 products on the bf16 matrix cores. Every fp32 operand x is split exactly into three bf16 pieces,
+// x = x1 + x2 + x3 (x1 = bf16(x) to nearest, x2 = bf16(x − x1), x3 = x − x1 − x2: 8 + 8 + 8 significand
+// bits, each remainder exact in fp32), and a·b is accumulated in fp32 from the six piece products whose
+// combined order is at most 2⁻¹⁶ of the product — a1b1, a1b2, a2b1, a1b3, a3b1, a2b2 (the three dropped
+// ones are below 2⁻²⁴, under fp32 rounding). Each piece product is exact in the fp32 accumulator, so the
+// result carries fp32 rounding only, like an fp32 product; the smallest terms are added first. Six
+// v_mfma_f32_32x32x16_bf16 do the work of 32 fp32 v_mfma_f32_32x32x2_f32 in 192 against 512 cycles.
+// The pieces are staged in LDS as three bf16 planes ([mn][k], the bf16 loop's layout) in one stage.
+__device__ __forceinline__ void split3_4(f32x4 x, bf16x4& h1, bf16x4& h2, bf16x4& h3) {
+    h1 = __builtin_convertvector(x, bf16x4);
+    const f32x4 r = x - __builtin_convertvector(h1, f32x4);
+    h2 = __builtin_convertvector(r, bf16x4);
+    const f32x4 r2 = r - __builtin_convertvector(h2, f32x4);
+    h3 = __builtin_convertvector(r2, bf16x4);
+}
+
+template <int KIND>
+__device__ __forceinline__ void store_x3(const OperandH<KIND>& op, __bf16* lds0, __bf16* lds1, __bf16* lds2, int tid) {
+    if constexpr (KIND == KVEC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            bf16x4 h1, h2, h3;
+            split3_4(op.reg[i], h1, h2, h3);
+            const int o = ((tid >> 3) + 32 * i) * KPADH + ((tid & 7) << 2);
+            *reinterpret_cast<bf16x4*>(lds0 + o) = h1;
+            *reinterpret_cast<bf16x4*>(lds1 + o) = h2;
+            *reinterpret_cast<bf16x4*>(lds2 + o) = h3;
+        }
+    } else {
+        const int o = (tid & 127) * KPADH + op.kq;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            bf16x4 h1, h2, h3;
+            split3_4(f32x4{op.v[4 * q], op.v[4 * q + 1], op.v[4 * q + 2], op.v[4 * q + 3]}, h1, h2, h3);
+            *reinterpret_cast<bf16x4*>(lds0 + o + 4 * q) = h1;
+            *reinterpret_cast<bf16x4*>(lds1 + o + 4 * q) = h2;
+            *reinterpret_cast<bf16x4*>(lds2 + o + 4 * q) = h3;
+        }
+    }
+}
+
+__device__ __forceinline__ void mma_stage_x6(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2], int wm, int wn,
+                                             int lr, int half) {
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 16) {
+        const int k = ks + 8 * half;
+        bf16x8 a[2][3], b[2][3];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                a[i][pl] = *reinterpret_cast<const bf16x8*>(A + pl * STAGE_H + (wm * 64 + 32 * i + lr) * KPADH + k);
+                b[i][pl] = *reinterpret_cast<const bf16x8*>(B + pl * STAGE_H + (wn * 64 + 32 * i + lr) * KPADH + k);
+            }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                f32x16 c = acc[i][j];
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][2], b[j][0], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][2], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][1], b[j][1], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][1], b[j][0], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][1], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][0], c, 0, 0, 0);
+                acc[i][j] = c;
+            }
+    }
+}
+
+template <int AOP, int BOP>
+__device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord& c, __bf16 (*smem)[3 * STAGE_H],
+                                            f32x16 (&acc)[2][2]) {
+    const int len = max(0, c.ke - c.kb);
+    const int nfull = len / BK, ntiles = nfull + (len % BK != 0 ? 1 : 0);
+    const int rot = nfull > 0 ? c.t % nfull : 0;
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, half = lane >> 5;
+    OperandH<AOP> a(p.A, p.lda, c.m0, p.M, tid);
+    OperandH<BOP> b(p.B, p.ldb, c.n0, p.N, tid);
+    auto fetch = [&](int j) {
+        if (j < nfull) {
+            int q = j + rot;
+            if (q >= nfull) q -= nfull;
+            a.full(c.kb + q * BK);
+            b.full(c.kb + q * BK);
+        } else {
+            a.tail(c.kb + nfull * BK, c.ke);
+            b.tail(c.kb + nfull * BK, c.ke);
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    if (ntiles > 0) fetch(0);
+    for (int j = 0; j < ntiles; ++j) {
+        __syncthreads();
+        store_x3<AOP>(a, smem[0], smem[0] + STAGE_H, smem[0] + 2 * STAGE_H, tid);
+        store_x3<BOP>(b, smem[1], smem[1] + STAGE_H, smem[1] + 2 * STAGE_H, tid);
+        __syncthreads();
+        if (j + 1 < ntiles) fetch(j + 1);
+        mma_stage_x6(smem[0], smem[1], acc, wm, wn, lr, half);
+    }
+    __syncthreads();
+}
+
+// The fp32 product from bf16 pieces; accumulators in the k-contiguous layout whatever the operands' form.
+template <int AOP, int BOP, int MODE, bool RES>
+__global__ __launch_bounds__(THREADS, 2) void gemm_x6_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * STAGE_H];
+    const TileCoord c = tile_coord(p, xcd_logical_block());
+    f32x16 acc[2][2];
+    tile_mma_x6<AOP, BOP>(p, c, smem, acc);
+    tile_store<true, true, MODE, RES>(p, c, acc);
 }
 
 // The bf16 product: the tile's accumulators are in the k-contiguous layout whatever the operands' form.
@@ -912,11 +1058,57 @@ template <bool AK, bool BKC> void launch_bf16(laya_ctx* ctx, const GemmParams& p
 // The precision class of a layout: NT forward (bit 0), NN input gradient (bit 1), TN weight gradient (bit 2).
 constexpr int layout_bit(bool ak, bool bkc) { return ak && bkc ? 1 : ak ? 2 : 4; }
 
+// Three single-stage workgroups per CU when the tile count makes that fewer rounds of work: a round of
+// three shares each CU's matrix cores three ways, so it is worth 1.5 rounds of two.
+bool three_per_cu(const laya_ctx* ctx, int blocks) {
+    const long two = (blocks + 2L * ctx->cu_count - 1) / (2L * ctx->cu_count);
+    const long three = (blocks + 3L * ctx->cu_count - 1) / (3L * ctx->cu_count);
+    return 3 * three < 2 * two;
+}
+
+template <int AOP, int BOP> void launch_x(laya_ctx* ctx, const GemmParams& p, int blocks) {
+    const dim3 g(blocks), b(THREADS);
+    switch (p.mode) {
+        case STORE:
+            if (p.R)
+                hipLaunchKernelGGL((gemm_x6_kernel<AOP, BOP, STORE, true>), g, b, 0, ctx->stream, p);
+            else
+                hipLaunchKernelGGL((gemm_x6_kernel<AOP, BOP, STORE, false>), g, b, 0, ctx->stream, p);
+            break;
+        case ACCUMULATE:
+            hipLaunchKernelGGL((gemm_x6_kernel<AOP, BOP, ACCUMULATE, false>), g, b, 0, ctx->stream, p);
+            break;
+        default: hipLaunchKernelGGL((gemm_x6_kernel<AOP, BOP, PARTIAL, false>), g, b, 0, ctx->stream, p);
+    }
+    check_launch("gemm_x6_kernel");
+}
+
+// The operand forms of a split product, as for a bf16 one.
+template <bool AK, bool BKC> void launch_x6(laya_ctx* ctx, const GemmParams& p, int blocks) {
+    const bool va = AK && operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K);
+    const bool vb = BKC && operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K);
+    if constexpr (AK && BKC) {
+        if (va && vb) launch_x<KVEC, KVEC>(ctx, p, blocks);
+        else if (va) launch_x<KVEC, KSCALAR>(ctx, p, blocks);
+        else if (vb) launch_x<KSCALAR, KVEC>(ctx, p, blocks);
+        else launch_x<KSCALAR, KSCALAR>(ctx, p, blocks);
+    } else if constexpr (AK) {
+        if (va) launch_x<KVEC, MNSCALAR>(ctx, p, blocks);
+        else launch_x<KSCALAR, MNSCALAR>(ctx, p, blocks);
+    } else {
+        launch_x<MNSCALAR, MNSCALAR>(ctx, p, blocks);
+    }
+}
+
 template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int blocks) {
     const dim3 g(blocks), b(THREADS);
     if (ctx->matmul_bf16 & layout_bit(AK, BKC)) {
         LAYA_REQUIRE(gemm_fits_h(p, AK, BKC), "gemm: bf16 operands need offsets below 2^31");
         launch_bf16<AK, BKC>(ctx, p, blocks);
+        return;
+    }
+    if ((ctx->matmul_split & layout_bit(AK, BKC)) && gemm_fits_h(p, AK, BKC)) {
+        launch_x6<AK, BKC>(ctx, p, blocks);
         return;
     }
     if (!gemm_fast(p, AK, BKC)) {
@@ -932,6 +1124,13 @@ template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int
     }
     switch (p.mode) {
         case STORE:
+            if (AK && BKC && three_per_cu(ctx, blocks)) {
+                if (p.R)
+                    hipLaunchKernelGGL((gemm3_kernel<AK, BKC, STORE, true>), g, b, 0, ctx->stream, p);
+                else
+                    hipLaunchKernelGGL((gemm3_kernel<AK, BKC, STORE, false>), g, b, 0, ctx->stream, p);
+                break;
+            }
             if (p.R)
                 hipLaunchKernelGGL((gemm_kernel<AK, BKC, STORE, true>), g, b, 0, ctx->stream, p);
             else
@@ -1018,10 +1217,12 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
     }
     const int blocks = tiles * p.splits;
     {
-        static const char* names[2][3] = {{"gemm_nt", "gemm_nn", "gemm_tn"},
-                                          {"gemm_nt_bf16", "gemm_nn_bf16", "gemm_tn_bf16"}};
+        static const char* names[3][3] = {{"gemm_nt", "gemm_nn", "gemm_tn"},
+                                          {"gemm_nt_bf16", "gemm_nn_bf16", "gemm_tn_bf16"},
+                                          {"gemm_nt_x6", "gemm_nn_x6", "gemm_tn_x6"}};
         const int bit = layout == GemmLayout::NT ? 1 : layout == GemmLayout::NN ? 2 : 4;
-        ProfileScope scope(ctx, names[(ctx->matmul_bf16 & bit) ? 1 : 0][(int)layout], 2.0 * M * N * (double)K, 0.0);
+        const int kind = (ctx->matmul_bf16 & bit) ? 1 : (ctx->matmul_split & bit) ? 2 : 0;
+        ProfileScope scope(ctx, names[kind][(int)layout], 2.0 * M * N * (double)K, 0.0);
         switch (layout) {
             case GemmLayout::NT: launch<true, true>(ctx, p, blocks); break;
             case GemmLayout::NN: launch<true, false>(ctx, p, blocks); break;
@@ -1049,6 +1250,13 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
         check_launch("gemm_bf16_kernel");
         return;
     }
+    if (ctx->matmul_split & 1) {
+        ProfileScope scope(ctx, "gemm_nt_x6", 2.0 * M * N * (double)K, 0.0);
+        hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
+                           dim3(THREADS), 0, ctx->stream, p);
+        check_launch("gemm_x6_kernel");
+        return;
+    }
     ProfileScope scope(ctx, "gemm_nt", 2.0 * M * N * (double)K, 0.0);
     hipLaunchKernelGGL((gemm_kernel<true, true, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n), dim3(THREADS), 0,
                        ctx->stream, p);
@@ -1063,7 +1271,7 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
     nn.mode = STORE;
     // dW[out, in] += dy[rows, out]ᵀ · x[rows, in]     (TN, K = rows)
     GemmParams tn = make_params(out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr, 0);
-    if ((ctx->matmul_bf16 & 6) || !gemm_fast(nn, true, false) || !gemm_fast(tn, false, false)) {
+    if (((ctx->matmul_bf16 | ctx->matmul_split) & 6) || !gemm_fast(nn, true, false) || !gemm_fast(tn, false, false)) {
         gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual,
              in);
         gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);

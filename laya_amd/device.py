@@ -46,12 +46,15 @@ class Context:
 
     # Products that take bf16 operands under each policy: forward (y = x·Wᵀ), input gradient (dx = dy·W),
     # weight gradient (dW += dyᵀ·x).
-    MATMUL_POLICIES = {"fp32": 0, "bf16": 7, "bf16-forward": 1, "bf16-backward": 6, "bf16-weight-grad": 4}
+    MATMUL_POLICIES = {"fp32": 0, "fp32-mfma": 8, "bf16": 7, "bf16-forward": 1, "bf16-backward": 6,
+                       "bf16-weight-grad": 4}
 
     def set_matmul_precision(self, precision: str) -> None:
-        """The operand precision of the matrix products launched afterwards: 'fp32' (default), 'bf16'
-        (every product), or one class in bf16 ('bf16-forward', 'bf16-backward', 'bf16-weight-grad').
-        bf16 operands are rounded to nearest even; accumulation and outputs stay fp32."""
+        """The operand precision of the matrix products launched afterwards: 'fp32' (default: fp32-accurate
+        products from exact three-piece bf16 splits on the bf16 matrix cores), 'fp32-mfma' (the fp32 matrix
+        cores), 'bf16' (every product), or one class in bf16 ('bf16-forward', 'bf16-backward',
+        'bf16-weight-grad', the other classes fp32). bf16 operands are rounded to nearest even;
+        accumulation and outputs stay fp32."""
         if precision not in self.MATMUL_POLICIES:
             raise ValueError(f"matmul precision '{precision}': expected one of {sorted(self.MATMUL_POLICIES)}")
         check(lib().laya_ctx_set_matmul_precision(self.handle, self.MATMUL_POLICIES[precision]))

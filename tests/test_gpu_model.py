@@ -293,30 +293,43 @@ def test_rlcd_step_on_the_device_matches_the_host_objective(ctx):
             assert np.linalg.norm(got - want) <= 1e-5 * np.linalg.norm(want) + 1e-6, name
 
 
+def _clear_of_the_relu(params, mc, seed):
+    """Moves every head linear1 bias to ±5 × the RMS of its product (random sign per unit): no ReLU input
+    then lies anywhere near zero, while the ReLU still masks about half the units.
+
+    The head's ReLU is the model's one discontinuity. With ~10⁶ ReLU inputs drawn around zero, a few lie
+    within fp32 rounding of it, and any two fp32 implementations (the reference-faithful fp32 oracle
+    included) land some on different sides now and then, which moves every gradient below by up to ~1e-3
+    (measured: 1–3 of 8 seeds for each implementation). Away from zero the step is a smooth function of the
+    inputs and fp32 implementations agree to their rounding."""
+    rng = np.random.default_rng(seed + 100)
+    scale = 5.0 * 0.02 * np.sqrt(mc.encoder.hidden_size)  # weights N(0, 0.02) on unit-scale normed inputs
+    for j in range(mc.head_layers):
+        name = f"head.layers.{j}.linear1.bias"
+        params[name] = (scale * rng.choice([-1.0, 1.0], params[name].shape)).astype(np.float32)
+    return params
+
+
 def _large_shape_case(ctx, mc, trainable, lengths, seed, zipf=0.0):
-    """One training-mode forward/backward (head dropout 0.1) of a checkpoint-sized shape on the GPU and on
-    the oracle, weights N(0, 0.02) with non-trivial norms. Each gradient is held to the exact (fp64 oracle)
-    result by the reference test's metric and by rel-L2 at max(bar, 4 × the error of the fp32 oracle on the
-    same tensor): the head's ReLU can flip a pre-activation within fp32 rounding of zero in any two fp32
-    implementations, which moves single elements."""
+    """One training-mode forward/backward (head dropout 0.1) of a checkpoint-sized shape on the GPU and on the
+    oracle (fp64 = exact, and fp32), weights N(0, 0.02) with non-trivial norms and the head ReLU's inputs
+    clear of zero. Each gradient is held to the reference test's tolerance (TrainingGradientTests.cs:205-214:
+    max|Δ|/max|g| < 1e-3, cosine > 0.99999) and to the fp32 bar, rel-L2 ≤ max(1e-4, 4 × the fp32 oracle's)."""
     from laya_amd.batch import synthetic_batch
     from laya_amd.model import TrainableDecisionModel
-    o = oracle.OracleModel(mc)
-    params = random_params(o.shapes, seed, std=0.02)
+    o32 = oracle.OracleModel(mc)
+    params = _clear_of_the_relu(random_params(o32.shapes, seed, std=0.02), mc, seed)
     rng = np.random.default_rng(seed + 1)
     opts = [(8, 4, 2)[i % 3] for i in range(len(lengths))]
     batch = synthetic_batch(rng, lengths, opts, [i % 3 for i in range(len(lengths))], mc.encoder.vocab_size, zipf)
     dlogits = rng.standard_normal(batch.n_markers).astype(np.float32)
-    refs = []
-    for double in (False, True):
-        r = oracle.OracleModel(mc, double=double) if double else o
+    o64 = oracle.OracleModel(mc, double=True)
+    for r in (o32, o64):
         r.set_params(params)
         r.set_head_dropout(0.1)
         r.set_trainable_encoder_layers(trainable)
-        logits_r = r.forward(batch, training=True, keep_tape=True, seed=seed)
+        logits_o = r.forward(batch, training=True, keep_tape=True, seed=seed)
         r.backward(dlogits)
-        refs.append((r, logits_r))
-    (o32, _), (o64, logits_o) = refs
     m = TrainableDecisionModel(mc, ctx)
     m.set_params(params)
     m.head_dropout = 0.1
@@ -324,7 +337,7 @@ def _large_shape_case(ctx, mc, trainable, lengths, seed, zipf=0.0):
     logits_m = m.forward(batch, training=True, seed=seed)
     m.backward(dlogits)
     assert np.abs(logits_o - logits_m).max() < 1e-3
-    checked = 0
+    checked, worst = 0, (0.0, "")
     for name in m.names:
         assert m.has_grad(name) == o64.has_grad(name), name
         if not m.has_grad(name) or name == "scorer.3.bias":
@@ -332,10 +345,13 @@ def _large_shape_case(ctx, mc, trainable, lengths, seed, zipf=0.0):
         exact, ref32, got = o64.grad(name), o32.grad(name), m.grad(name)
         cos = float(np.dot(exact.ravel(), got.ravel().astype(np.float64)) /
                     max(np.linalg.norm(exact) * np.linalg.norm(got), 1e-300))
-        assert cos > 0.99999, (name, cos)  # TrainingGradientTests.cs:213
-        assert max_rel(exact, got) < max(1e-3, 4 * max_rel(exact, ref32)), (name, max_rel(exact, got))
-        assert rel_l2(exact, got) < max(1e-4, 4 * rel_l2(exact, ref32)), (name, rel_l2(exact, got))
+        assert cos > 0.99999, (name, cos)
+        assert max_rel(exact, got) < 1e-3, (name, max_rel(exact, got))
+        e = rel_l2(exact, got)
+        assert e < max(1e-4, 4 * rel_l2(exact, ref32)), (name, e)
+        worst = max(worst, (e, name))
         checked += 1
+    print(f"worst gradient rel-L2 {worst[0]:.1e} ({worst[1]})", flush=True)
     m.close()
     return checked
 

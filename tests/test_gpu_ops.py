@@ -32,12 +32,16 @@ def param(ctx, name, a, trainable=True):
     return laya.Parameter(ctx, name, np.asarray(a, np.float32), trainable)
 
 
+@pytest.mark.parametrize("policy", ["fp32", "fp32-mfma"])
 @pytest.mark.parametrize("rows,inn,out", [(37, 96, 130), (300, 128, 384), (1000, 768, 2304), (5, 768, 1),
                                           (2048, 1152, 768), (333, 100, 260),
                                           # large enough for the balanced static schedule of dX + dW
                                           (8000, 768, 768), (9000, 768, 2304)])
-def test_linear_forward_and_backward(ctx, rows, inn, out):
-    print(f"linear rows={rows} in={inn} out={out}", flush=True)
+def test_linear_forward_and_backward(ctx, rows, inn, out, policy):
+    """Both fp32 implementations (exact bf16 splits, the default; the fp32 matrix cores) at the fp64
+    oracle's result to 1e-6."""
+    print(f"linear rows={rows} in={inn} out={out} {policy}", flush=True)
+    ctx.set_matmul_precision(policy)
     rng = np.random.default_rng(rows + inn + out)
     x = rng.standard_normal((rows, inn)).astype(np.float32)
     W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
@@ -58,6 +62,7 @@ def test_linear_forward_and_backward(ctx, rows, inn, out):
     assert rel_l2(dx_ref, dx_.numpy()) < 1e-6
     assert rel_l2(2 * dW, w.gradient.numpy()) < 1e-6
     assert rel_l2(2 * db, bias.gradient.numpy()) < 1e-6
+    ctx.set_matmul_precision("fp32")
 
 
 @pytest.mark.parametrize("rows,inn,out", [(4100, 64, 96), (1500, 256, 132)])
