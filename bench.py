@@ -38,12 +38,12 @@ PEAK_FP32_MFMA = 157.3e12
 PEAK_HBM = 8.0e12
 MFMA_KERNELS = ("gemm_nt", "gemm_nn", "gemm_tn", "gemm_bwd_pair", "attention_fwd", "attention_bwd_dkv",
                 "attention_bwd_dq")
-# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on this workload and
-# calibrated against a copy-like kernel of known size (the commands and the calibration sit in
-# profiles/gemm_bwd_pair_hbm_traffic.md). Counters cannot be read from inside the process, so the
-# figure is carried here for the kernel it was measured on and is reported only when that kernel is
-# the dominant one; any other dominant kernel reports null.
-MEASURED_TRAFFIC = {"gemm_bwd_pair": 1.753e9}
+# HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and calibrated against a
+# copy-like kernel of known size (the commands and the calibration sit in
+# profiles/gemm_tn_x6_hbm_traffic_b32x512.md). Counters cannot be read from inside the process, so the
+# figure is carried here per (workload, kernel) it was measured on and is reported only when that kernel
+# is the dominant one of that workload; any other case reports null.
+MEASURED_TRAFFIC = {("b32x512", "gemm_tn_x6"): 0.713e9}
 
 
 PEAK_BF16_MFMA = 2.5e15
@@ -220,6 +220,7 @@ def main():
                      f"{k['bytes'] / k['ms'] / 1e6:8.1f} GB/s"), file=sys.stderr)
         name, k = max(prof.items(), key=lambda kv: kv[1]["ms"])
         per_launch_s = k["ms"] / k["launches"] / 1e3
+        traffic = MEASURED_TRAFFIC.get((args.workload, name)) if matmul == w["matmul"] else None
         if k["flops"]:
             achieved = k["flops"] / k["launches"] / per_launch_s
             # A split-product kernel issues six bf16 MFMA products per fp32 product: its fp32-equivalent peak
@@ -228,12 +229,12 @@ def main():
                     else PEAK_FP32_MFMA)
             roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved / 1e12, 2),
                         "peak": round(peak / 1e12, 1), "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
-                        "traffic": MEASURED_TRAFFIC.get(name), "avg_launch_ms": round(per_launch_s * 1e3, 4),
+                        "traffic": traffic, "avg_launch_ms": round(per_launch_s * 1e3, 4),
                         "launches": k["launches"]}
         else:
             achieved = k["bytes"] / k["launches"] / per_launch_s
             roofline = {"bound": "hbm", "kernel": name, "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
-                        "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": MEASURED_TRAFFIC.get(name),
+                        "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
                         "avg_launch_ms": round(per_launch_s * 1e3, 4), "launches": k["launches"]}
         bwd = [prof[n] for n in ("gemm_nn", "gemm_tn", "gemm_bwd_pair") if n in prof]
         if bwd:
