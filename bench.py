@@ -241,7 +241,7 @@ def main():
             f = sum(x["flops"] for x in bwd)
             ms = sum(x["ms"] for x in bwd)
             breakdown["bwd_gemm_mfma_util"] = round(f / (ms / 1e3) / PEAK_FP32_MFMA, 4)
-        bwdx = [prof[n] for n in ("gemm_nn_x6", "gemm_tn_x6") if n in prof]
+        bwdx = [prof[n] for n in ("gemm_bwd_pair_x6", "gemm_nn_x6", "gemm_tn_x6") if n in prof]
         if bwdx:
             f = sum(x["flops"] for x in bwdx)
             ms = sum(x["ms"] for x in bwdx)

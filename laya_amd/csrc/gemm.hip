@@ -805,9 +805,36 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_pair_planned_kernel(GemmParam
     }
 }
 
+// The planned pair with split products: the same schedule and partial slots; dX tiles read dY as a
+// k-contiguous operand (AOP) and W as an mn-contiguous one, dW slices read dY and x mn-contiguous.
+template <int AOP, bool RES>
+__global__ __launch_bounds__(THREADS, 2) void gemm_pair_planned_x6_kernel(GemmParams nn, GemmParams tn, PairPlan s) {
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * STAGE_H];
+    const int g = xcd_logical_block();
+    const int count = s.q + (g < s.r ? 1 : 0);
+    for (int n = 0; n < count; ++n) {
+        const TileCoord c = unit_coord(nn, g + n * s.G, 0, s.nn_units);
+        f32x16 acc[2][2];
+        tile_mma_x6<AOP, MNSCALAR>(nn, c, smem, acc);
+        tile_store<true, true, STORE, RES>(nn, c, acc);
+    }
+    const int lo = plan_tn_lo(s, g), hi = plan_tn_lo(s, g + 1);
+    for (int u = lo; u < hi;) {
+        const int t = u / s.tn_units;
+        const int a = u - t * s.tn_units;
+        const int b = min(s.tn_units, a + (hi - u));
+        const TileCoord c = unit_coord(tn, t, a, b);
+        f32x16 acc[2][2];
+        tile_mma_x6<MNSCALAR, MNSCALAR>(tn, c, smem, acc);
+        write_partial(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (BM * BN), acc);
+        u += b - a;
+    }
+}
+
 // Adds the partials of the workers that shared a dW tile, in worker order, into dW. Eight workgroups
 // per tile (blockIdx.y = 4i + r/4): each thread sums the two float4 groups (j = 0, 1) of its lanes'
 // accumulator rows and adds them to dW as four column pairs, in the layout `store_acc` uses.
+template <bool KLAYOUT>
 __global__ __launch_bounds__(THREADS) void pair_fixup_kernel(GemmParams tn, PairPlan s) {
     const int t = blockIdx.x, i = blockIdx.y >> 2, r4 = blockIdx.y & 3;
     const int a = t * s.tn_units, b = a + s.tn_units;
@@ -858,6 +885,30 @@ __global__ __launch_bounds__(THREADS) void pair_fixup_kernel(GemmParams tn, Pair
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, kh = (lane >> 5) << 2;
     const TileCoord c = unit_coord(tn, t, 0, s.tn_units);
+    if constexpr (KLAYOUT) {
+        // Split-product accumulators: element e of group (i, j, r4) is row 32i + 8·r4 + kh + e, column
+        // 32j + lr of the wave's 64×64 block.
+        float cur[2][4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {  // all reads before the first write (see store_acc)
+            const int row = c.m0 + wm * 64 + 32 * i + 8 * r4 + kh + e;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = c.n0 + wn * 64 + 32 * j + lr;
+                cur[j][e] = row < tn.M && col < tn.N ? tn.C[(long)row * tn.ldc + col] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = c.m0 + wm * 64 + 32 * i + 8 * r4 + kh + e;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int col = c.n0 + wn * 64 + 32 * j + lr;
+                if (row < tn.M && col < tn.N) tn.C[(long)row * tn.ldc + col] = cur[j][e] + sum[j][e];
+            }
+        }
+        return;
+    }
     const int col = c.n0 + wn * 64 + 2 * lr;
     f32x2 cur[4];
 #pragma unroll
@@ -1263,6 +1314,25 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
     check_launch("gemm_kernel");
 }
 
+// The balanced static schedule of a backward pair, when every worker's whole dX tiles fit in its share of
+// the work and every worker's dW run is shorter than one dW tile (so every dW tile is shared by two or
+// more workers, whose partials the fixup adds, and no worker holds more than its two partial slots).
+bool make_pair_plan(const laya_ctx* ctx, int n0, int out, int n1, int rows, PairPlan& s) {
+    s = PairPlan{};
+    s.G = 2 * ctx->cu_count;
+    s.nn_tiles = n0;
+    s.nn_units = (out + BK - 1) / BK;
+    s.tn_tiles = n1;
+    s.tn_units = (rows + BK - 1) / BK;
+    s.q = n0 / s.G;
+    s.r = n0 % s.G;
+    const long W = (long)n0 * s.nn_units + (long)n1 * s.tn_units;
+    s.W = (int)std::min<long>(W, 1L << 30);
+    const long need_min = W / s.G - (long)(s.q + (s.r > 0 ? 1 : 0)) * s.nn_units;
+    const long max_run = (W + s.G - 1) / s.G - (long)s.q * s.nn_units;
+    return need_min >= 0 && s.nn_units > 0 && W * s.G < (1L << 31) && max_run < s.tn_units;
+}
+
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
                         float* dx, const float* dx_residual, float* dW) {
     if (rows == 0) return;
@@ -1271,59 +1341,72 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
     nn.mode = STORE;
     // dW[out, in] += dy[rows, out]ᵀ · x[rows, in]     (TN, K = rows)
     GemmParams tn = make_params(out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr, 0);
-    if (((ctx->matmul_bf16 | ctx->matmul_split) & 6) || !gemm_fast(nn, true, false) || !gemm_fast(tn, false, false)) {
-        gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual,
-             in);
-        gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
-        return;
-    }
+    const bool split = !(ctx->matmul_bf16 & 6) && (ctx->matmul_split & 6) == 6 && gemm_fits_h(nn, true, false) &&
+                       gemm_fits_h(tn, false, false);
+    const bool fp32 = !((ctx->matmul_bf16 | ctx->matmul_split) & 6) && gemm_fast(nn, true, false) &&
+                      gemm_fast(tn, false, false);
     const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
-    {
-        // The balanced static schedule, when every worker's whole dX tiles fit in its share of the work.
-        PairPlan s{};
-        s.G = 2 * ctx->cu_count;
-        s.nn_tiles = n0;
-        s.nn_units = (out + BK - 1) / BK;
-        s.tn_tiles = n1;
-        s.tn_units = (rows + BK - 1) / BK;
-        s.q = n0 / s.G;
-        s.r = n0 % s.G;
-        const long W = (long)n0 * s.nn_units + (long)n1 * s.tn_units;
-        s.W = (int)std::min<long>(W, 1L << 30);
-        const long need_min = W / s.G - (long)(s.q + (s.r > 0 ? 1 : 0)) * s.nn_units;
-        if (need_min >= 0 && s.nn_units > 0 && W * s.G < (1L << 31)) {
-            s.partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)s.G * 2 * BM * BN));
-            tn.mode = ACCUMULATE;
-            {
-                ProfileScope scope(ctx, "gemm_bwd_pair", 2.0 * 2.0 * rows * (double)in * out, 0.0);
-                const dim3 g(s.G), b(THREADS);
+    PairPlan s{};
+    if ((split || fp32) && make_pair_plan(ctx, n0, out, n1, rows, s)) {
+        s.partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)s.G * 2 * BM * BN));
+        tn.mode = ACCUMULATE;
+        {
+            ProfileScope scope(ctx, split ? "gemm_bwd_pair_x6" : "gemm_bwd_pair", 2.0 * 2.0 * rows * (double)in * out,
+                               0.0);
+            const dim3 g(s.G), b(THREADS);
+            if (split) {
+                if (operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) {
+                    if (dx_residual)
+                        hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KVEC, true>), g, b, 0, ctx->stream, nn, tn, s);
+                    else
+                        hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KVEC, false>), g, b, 0, ctx->stream, nn, tn, s);
+                } else {
+                    if (dx_residual)
+                        hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KSCALAR, true>), g, b, 0, ctx->stream, nn, tn,
+                                           s);
+                    else
+                        hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KSCALAR, false>), g, b, 0, ctx->stream, nn, tn,
+                                           s);
+                }
+                check_launch("gemm_pair_planned_x6_kernel");
+            } else {
                 if (dx_residual)
                     hipLaunchKernelGGL((gemm_pair_planned_kernel<true>), g, b, 0, ctx->stream, nn, tn, s);
                 else
                     hipLaunchKernelGGL((gemm_pair_planned_kernel<false>), g, b, 0, ctx->stream, nn, tn, s);
                 check_launch("gemm_pair_planned_kernel");
             }
-            // Compulsory bytes of the fixup: every partial tile read once, every shared dW tile read and
-            // written once (the same walk over the workers' runs the kernels make).
-            long partials = 0, shared = 0;
-            auto tn_lo = [&](long g) { return g * W / s.G - (long)s.nn_units * (g * s.q + std::min<long>(g, s.r)); };
-            for (int g = 0; ctx->profiling && g < s.G; ++g) {
-                const long lo = tn_lo(g), hi = tn_lo(g + 1);
-                for (long u = lo; u < hi;) {
-                    const long t = u / s.tn_units, a = u - t * s.tn_units;
-                    const long b = std::min<long>(s.tn_units, a + (hi - u));
-                    if (!(a == 0 && b == s.tn_units)) {
-                        ++partials;
-                        if (a == 0) ++shared;  // count each shared tile at its first piece
-                    }
-                    u += b - a;
-                }
-            }
-            ProfileScope scope(ctx, "gemm_pair_fixup", 0.0, 4.0 * BM * BN * (double)(partials + 2 * shared));
-            hipLaunchKernelGGL(pair_fixup_kernel, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
-            check_launch("pair_fixup_kernel");
-            return;
         }
+        // Compulsory bytes of the fixup: every partial tile read once, every shared dW tile read and
+        // written once (the same walk over the workers' runs the kernels make).
+        long partials = 0, shared = 0;
+        const long Wt = (long)n0 * s.nn_units + (long)n1 * s.tn_units;
+        auto tn_lo = [&](long g) { return g * Wt / s.G - (long)s.nn_units * (g * s.q + std::min<long>(g, s.r)); };
+        for (int g = 0; ctx->profiling && g < s.G; ++g) {
+            const long lo = tn_lo(g), hi = tn_lo(g + 1);
+            for (long u = lo; u < hi;) {
+                const long t = u / s.tn_units, a = u - t * s.tn_units;
+                const long b = std::min<long>(s.tn_units, a + (hi - u));
+                if (!(a == 0 && b == s.tn_units)) {
+                    ++partials;
+                    if (a == 0) ++shared;  // count each shared tile at its first piece
+                }
+                u += b - a;
+            }
+        }
+        ProfileScope scope(ctx, "gemm_pair_fixup", 0.0, 4.0 * BM * BN * (double)(partials + 2 * shared));
+        if (split)
+            hipLaunchKernelGGL(pair_fixup_kernel<true>, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
+        else
+            hipLaunchKernelGGL(pair_fixup_kernel<false>, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
+        check_launch("pair_fixup_kernel");
+        return;
+    }
+    if (!fp32) {
+        gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual,
+             in);
+        gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
+        return;
     }
     // Choose the dW split so its slices are as long as a dX tile's K loop, then minimise the rounds of
     // 2-blocks-per-CU the combined grid needs times the longest block.

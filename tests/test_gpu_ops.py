@@ -36,10 +36,14 @@ def param(ctx, name, a, trainable=True):
 @pytest.mark.parametrize("rows,inn,out", [(37, 96, 130), (300, 128, 384), (1000, 768, 2304), (5, 768, 1),
                                           (2048, 1152, 768), (333, 100, 260),
                                           # large enough for the balanced static schedule of dX + dW
-                                          (8000, 768, 768), (9000, 768, 2304)])
+                                          (8000, 768, 768), (9000, 768, 2304),
+                                          # dW tiles outnumber the workers: a worker's dW run would cover a
+                                          # whole tile, which the schedule must not take
+                                          (4096, 2944, 2944)])
 def test_linear_forward_and_backward(ctx, rows, inn, out, policy):
     """Both fp32 implementations (exact bf16 splits, the default; the fp32 matrix cores) at the fp64
-    oracle's result to 1e-6."""
+    oracle's result to 1e-6, widened as √K for reductions longer than 2048 terms (fp32 rounding of a
+    K-term sum grows as √K)."""
     print(f"linear rows={rows} in={inn} out={out} {policy}", flush=True)
     ctx.set_matmul_precision(policy)
     rng = np.random.default_rng(rows + inn + out)
@@ -59,9 +63,10 @@ def test_linear_forward_and_backward(ctx, rows, inn, out, policy):
     laya.linear_backward(w, bias, xd, dyd, rows, dx_)
     dW = np.zeros((out, inn)); db = np.zeros(out)
     dx_ref = oracle.linear_backward(x, dy, W, True, dW, db, double=True)
-    assert rel_l2(dx_ref, dx_.numpy()) < 1e-6
-    assert rel_l2(2 * dW, w.gradient.numpy()) < 1e-6
-    assert rel_l2(2 * db, bias.gradient.numpy()) < 1e-6
+    tol = 1e-6 * max(1.0, (max(rows, out) / 2048) ** 0.5)
+    assert rel_l2(dx_ref, dx_.numpy()) < tol
+    assert rel_l2(2 * dW, w.gradient.numpy()) < tol
+    assert rel_l2(2 * db, bias.gradient.numpy()) < tol
     ctx.set_matmul_precision("fp32")
 
 
