@@ -19,6 +19,7 @@
 //   dq:  each wave owns 32 queries (Q, dO in registers) and sweeps the key tiles: Sᵀ, dPᵀ, dSᵀ,
 //        dQᵀ += Kᵀ·dSᵀ.
 #include "common.hpp"
+#include "split.hpp"
 
 namespace laya {
 namespace {
@@ -247,6 +248,241 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
                 const float* vcolp = Vs + (32 * st + 4 * h) * S::VS + dt * 32 + lr;
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[dt] = mfma(vcolp[(8 * (r >> 2) + (r & 3)) * S::VS], pr[r], o[dt]);
+            }
+        }
+    }
+
+    const float lt = l + __shfl_xor(l, 32, 64);
+    if (qvalid) {
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        store_acc<D>(o, p.context + (long)(start + q) * p.hidden + qcol, h, inv);
+        if (h == 0) p.lse[(long)(start + q) * p.heads + head] = lt > 0.0f ? m + log2f(lt) : __builtin_huge_valf();
+    }
+}
+
+// ------------------------------------------------------------------------------------ split products
+//
+// The products on the bf16 matrix cores (v_mfma_f32_32x32x16_bf16) from exact three-piece splits of every
+// fp32 operand (split.hpp): six piece products per fp32 product with fp32 accumulation, so the results
+// carry fp32 rounding only. A tile streamed through LDS is split once, as it is committed, into three bf16
+// planes; a wave's own rows are split once into registers; P (and dS) are split in registers.
+// In a 32×32×16 product a lane supplies 8 consecutive k of its row or column. The scores' accumulator
+// gives a lane the keys 8(r/4) + 4h + r%4 of its column, so a product over keys takes, per 16 keys, the
+// key order {4h … 4h+3, 8+4h … 8+4h+3} for both operands: P stays in the registers it was computed in and
+// the other operand is read from a transposed ([d][key]) plane as two runs of 4 keys.
+
+constexpr int KSH = 64 + 8;    // bf16 stride of [row][d] planes: b128 fragment reads without bank conflicts
+constexpr int TSH = TILE + 4;  // bf16 stride of [d][row] planes: b64 reads of 4 rows without bank conflicts
+
+__device__ __forceinline__ f32x16 mfma16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// c += a·b over one 16-k step from the pieces, the smallest products first.
+__device__ __forceinline__ f32x16 mma6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f32x16 c) {
+    c = mfma16(a[2], b[0], c);
+    c = mfma16(a[0], b[2], c);
+    c = mfma16(a[1], b[1], c);
+    c = mfma16(a[1], b[0], c);
+    c = mfma16(a[0], b[1], c);
+    return mfma16(a[0], b[0], c);
+}
+
+__device__ __forceinline__ bf16x8 cat8(bf16x4 lo, bf16x4 hi) {
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// The three pieces of 8 values (two float4).
+__device__ __forceinline__ void split8(f32x4 lo, f32x4 hi, bf16x8 (&out)[3]) {
+    bf16x4 a1, a2, a3, b1, b2, b3;
+    split3_4(lo, a1, a2, a3);
+    split3_4(hi, b1, b2, b3);
+    out[0] = cat8(a1, b1);
+    out[1] = cat8(a2, b2);
+    out[2] = cat8(a3, b3);
+}
+
+// A TILE × 64 slice of one head in registers between its global fetch and its LDS commit: thread t holds
+// rows 4·(t/16) + i (i < 4) at d = 4·(t%16) … +3, so it can write both a [row][d] and a [d][row] plane.
+struct RowStage4 {
+    f32x4 v[4];
+};
+
+__device__ __forceinline__ void fetch_rows4(RowStage4& st, const float* base, long stride, int L, int row0) {
+    const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = row0 + 4 * q + i;
+        st.v[i] = (t >= 0 && t < L) ? ld4(base + (long)t * stride + j) : f32x4{0, 0, 0, 0};
+    }
+}
+
+// Three [row][d] planes (stride KSH, plane stride TILE·KSH).
+__device__ __forceinline__ void commit_rows(const RowStage4& st, __bf16* planes) {
+    const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        bf16x4 h1, h2, h3;
+        split3_4(st.v[i], h1, h2, h3);
+        __bf16* o = planes + (4 * q + i) * KSH + j;
+        *reinterpret_cast<bf16x4*>(o) = h1;
+        *reinterpret_cast<bf16x4*>(o + TILE * KSH) = h2;
+        *reinterpret_cast<bf16x4*>(o + 2 * TILE * KSH) = h3;
+    }
+}
+
+// Three [d][row] planes (stride TSH, plane stride 64·TSH).
+__device__ __forceinline__ void commit_cols(const RowStage4& st, __bf16* planes) {
+    const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        bf16x4 h1, h2, h3;
+        split3_4(f32x4{st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]}, h1, h2, h3);
+        __bf16* o = planes + (j + e) * TSH + 4 * q;
+        *reinterpret_cast<bf16x4*>(o) = h1;
+        *reinterpret_cast<bf16x4*>(o + 64 * TSH) = h2;
+        *reinterpret_cast<bf16x4*>(o + 2 * 64 * TSH) = h3;
+    }
+}
+
+// The lane's own row (d = 16s + 8h … +7 for s < 4), split.
+__device__ __forceinline__ void split_lane_row(const float* src, bool valid, int h, bf16x8 (&out)[4][3]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const f32x4 lo = valid ? ld4(src + 16 * s + 8 * h) : f32x4{0, 0, 0, 0};
+        const f32x4 hi = valid ? ld4(src + 16 * s + 8 * h + 4) : f32x4{0, 0, 0, 0};
+        split8(lo, hi, out[s]);
+    }
+}
+
+// The 16-k fragments of row `row` of three [row][d] planes at k-step s.
+__device__ __forceinline__ void row_frag(const __bf16* planes, int row, int s, int h, bf16x8 (&f)[3]) {
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl)
+        f[pl] = *reinterpret_cast<const bf16x8*>(planes + pl * TILE * KSH + row * KSH + 16 * s + 8 * h);
+}
+
+// The fragments of d-row `d` of three [d][row] planes over the 16 rows from r0, in the key order above.
+__device__ __forceinline__ void col_frag(const __bf16* planes, int d, int r0, int h, bf16x8 (&f)[3]) {
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+        const __bf16* row = planes + pl * 64 * TSH + d * TSH + r0 + 4 * h;
+        f[pl] = cat8(*reinterpret_cast<const bf16x4*>(row), *reinterpret_cast<const bf16x4*>(row + 8));
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
+    static_assert(D == 64, "split-product attention is written for head_dim 64");
+    __shared__ __attribute__((aligned(16))) __bf16 Kh[3 * TILE * KSH];  // K tile, [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Vt[3 * D * TSH];     // V tile, [d][key]
+
+    const int seg = blockIdx.y, head = blockIdx.z;
+    const int start = p.seg_start[seg], L = p.seg_len[seg];
+    const int qb0 = blockIdx.x * BLOCK_ROWS;
+    if (qb0 >= L) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
+    const int q0w = qb0 + wave * WAVE_ROWS;
+    const int q = q0w + lr;
+    const bool qvalid = q < L;
+    const int hw = p.half_window;
+    const long stride = 3L * p.hidden;
+    const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
+
+    bf16x8 qh[4][3];
+    split_lane_row(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, qvalid, h, qh);
+
+    int kbeg = 0, kend = L;
+    int wbeg = 0, wend = L;
+    if (hw >= 0) {
+        kbeg = max(0, qb0 - hw);
+        kend = min(L, qb0 + BLOCK_ROWS + hw);
+        wbeg = max(0, q0w - hw);
+        wend = min(L, q0w + WAVE_ROWS + hw);
+    }
+
+    f32x16 o[2];
+    o[0] = f32x16{};
+    o[1] = f32x16{};
+    float m = -1e30f, l = 0.0f;
+
+    const float* kbase = p.qkv + (long)start * stride + kcol;
+    const float* vbase = p.qkv + (long)start * stride + vcol;
+    RowStage4 kst, vst;
+    fetch_rows4(kst, kbase, stride, L, kbeg);
+    fetch_rows4(vst, vbase, stride, L, kbeg);
+    for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
+        __syncthreads();
+        commit_rows(kst, Kh);
+        commit_cols(vst, Vt);
+        __syncthreads();
+        if (kt0 + TILE < kend) {  // block-uniform: the next tile's loads overlap this tile's products
+            fetch_rows4(kst, kbase, stride, L, kt0 + TILE);
+            fetch_rows4(vst, vbase, stride, L, kt0 + TILE);
+        }
+#pragma unroll
+        for (int st = 0; st < TILE / 32; ++st) {
+            const int kbs = kt0 + 32 * st;
+            // Wave-uniform: outside this wave's window, or a wave whose rows all lie past the segment end.
+            if (kbs >= wend || kbs + 32 <= wbeg || kbs >= kend || q0w >= L) continue;
+            // Sᵀ = K·Qᵀ: lane column = its query, rows = 16 keys.
+            f32x16 s = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                bf16x8 kf[3];
+                row_frag(Kh, 32 * st + lr, ks, h, kf);
+                s = mma6(kf, qh[ks], s);
+            }
+            float t[16];
+            float mx = -1e30f;
+            if (subtile_inside(q0w, kbs, L, hw)) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    t[r] = s[r] * p.scale_log2;
+                    mx = fmaxf(mx, t[r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
+                    t[r] = in_window(q, key, L, hw) ? s[r] * p.scale_log2 : NEG_INF;
+                    mx = fmaxf(mx, t[r]);
+                }
+            }
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mnew = fmaxf(m, mx);
+            const float alpha = fast_exp2(m - mnew);
+            float pr[16];
+            float sum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                pr[r] = fast_exp2(t[r] - mnew);
+                sum += pr[r];
+            }
+            l = l * alpha + sum;
+            m = mnew;
+            o[0] *= alpha;
+            o[1] *= alpha;
+            if (p.p_drop > 0.0f) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
+                    const float u = uniform01(p.seed, attn_dropout_index(head, start + q, key));
+                    pr[r] = u < p.p_drop ? 0.0f : pr[r] * p.keep;
+                }
+            }
+            // Oᵀ += Vᵀ·Pᵀ over the subtile's 32 keys in two 16-key steps.
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                bf16x8 ph[3];
+                split8(f32x4{pr[8 * u], pr[8 * u + 1], pr[8 * u + 2], pr[8 * u + 3]},
+                       f32x4{pr[8 * u + 4], pr[8 * u + 5], pr[8 * u + 6], pr[8 * u + 7]}, ph);
+#pragma unroll
+                for (int dt = 0; dt < 2; ++dt) {
+                    bf16x8 vf[3];
+                    col_frag(Vt, 32 * dt + lr, 32 * st + 16 * u, h, vf);
+                    o[dt] = mma6(vf, ph, o[dt]);
+                }
             }
         }
     }
@@ -586,6 +822,10 @@ void check_args(const AttentionArgs& a) {
     LAYA_REQUIRE(a.cos_table == nullptr || a.positions >= a.max_len, "attention: rotary table shorter than max_len");
 }
 
+// Attention takes split products under the fp32 policy that splits every product class; the fp32 matrix
+// cores otherwise (the fp32-MFMA policy, and the bf16 policies, whose attention stays fp32).
+bool split_attention(const laya_ctx* ctx) { return (ctx->matmul_split & 7) == 7; }
+
 }  // namespace
 
 void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse) {
@@ -597,7 +837,9 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
     p.lse = lse;
     dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
     ProfileScope scope(ctx, "attention_fwd", 4.0 * a.hidden * a.keys, 0.0);
-    if (a.head_dim == 64)
+    if (a.head_dim == 64 && split_attention(ctx))
+        hipLaunchKernelGGL(attn_fwd_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+    else if (a.head_dim == 64)
         hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
     else
         hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);

@@ -25,6 +25,7 @@
 // fifth slower on short-K products.
 #include "common.hpp"
 #include "elementwise.hpp"
+#include "split.hpp"
 
 namespace laya {
 namespace {
@@ -412,8 +413,6 @@ __device__ __forceinline__ void tile_mma(const GemmParams& p, const TileCoord& c
 // read, and 16 consecutive rows fall on distinct bank groups for both the fragment reads and the row
 // writes. The accumulators come out in the fp32 loop's layout for k-contiguous operands, so the same
 // epilogues store them.
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int KPADH = BK + 8;        // bf16 row stride of an [mn][k] tile
 constexpr int STAGE_H = BM * KPADH;  // bf16 elements per operand tile
 
@@ -594,14 +593,6 @@ __global__ __launch_bounds__(THREADS, 3) void gemm3_kernel(GemmParams p) {
 // result carries fp32 rounding only, like an fp32 product; the smallest terms are added first. Six
 // v_mfma_f32_32x32x16_bf16 do the work of 32 fp32 v_mfma_f32_32x32x2_f32 in 192 against 512 cycles.
 // The pieces are staged in LDS as three bf16 planes ([mn][k], the bf16 loop's layout) in one stage.
-__device__ __forceinline__ void split3_4(f32x4 x, bf16x4& h1, bf16x4& h2, bf16x4& h3) {
-    h1 = __builtin_convertvector(x, bf16x4);
-    const f32x4 r = x - __builtin_convertvector(h1, f32x4);
-    h2 = __builtin_convertvector(r, bf16x4);
-    const f32x4 r2 = r - __builtin_convertvector(h2, f32x4);
-    h3 = __builtin_convertvector(r2, bf16x4);
-}
-
 template <int KIND>
 __device__ __forceinline__ void store_x3(const OperandH<KIND>& op, __bf16* lds0, __bf16* lds1, __bf16* lds2, int tid) {
     if constexpr (KIND == KVEC) {

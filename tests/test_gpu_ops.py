@@ -169,9 +169,13 @@ ATTENTION_CASES = [
 ]
 
 
+@pytest.mark.parametrize("policy", ["fp32", "fp32-mfma"])
 @pytest.mark.parametrize("hd,heads,lengths,hw,theta,p", ATTENTION_CASES)
-def test_attention_forward_and_backward(ctx, hd, heads, lengths, hw, theta, p):
-    print(f"attention hd={hd} heads={heads} lengths={lengths} hw={hw} theta={theta} p={p}", flush=True)
+def test_attention_forward_and_backward(ctx, hd, heads, lengths, hw, theta, p, policy):
+    """Both fp32 implementations (split products on the bf16 matrix cores for head_dim 64, the default;
+    the fp32 matrix cores) at the fp64 oracle's result to 1e-5."""
+    print(f"attention hd={hd} heads={heads} lengths={lengths} hw={hw} theta={theta} p={p} {policy}", flush=True)
+    ctx.set_matmul_precision(policy)
     rng = np.random.default_rng(hd * 1000 + sum(lengths))
     hidden = hd * heads
     T = sum(lengths)
@@ -194,6 +198,7 @@ def test_attention_forward_and_backward(ctx, hd, heads, lengths, hw, theta, p):
     got = dq.numpy()
     for part, sl in (("q", slice(0, hidden)), ("k", slice(hidden, 2 * hidden)), ("v", slice(2 * hidden, None))):
         assert rel_l2(dref[:, sl], got[:, sl]) < 1e-5, part
+    ctx.set_matmul_precision("fp32")
 
 
 def test_attention_is_deterministic(ctx):
