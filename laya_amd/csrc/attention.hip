@@ -272,7 +272,6 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
 // the other operand is read from a transposed ([d][key]) plane as two runs of 4 keys.
 
 constexpr int KSH = 64 + 8;    // bf16 stride of [row][d] planes: b128 fragment reads without bank conflicts
-constexpr int TSH = TILE + 4;  // bf16 stride of [d][row] planes: b64 reads of 4 rows without bank conflicts
 
 __device__ __forceinline__ f32x16 mfma16(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -302,46 +301,68 @@ __device__ __forceinline__ void split8(f32x4 lo, f32x4 hi, bf16x8 (&out)[3]) {
     out[2] = cat8(a3, b3);
 }
 
-// A TILE × 64 slice of one head in registers between its global fetch and its LDS commit: thread t holds
-// rows 4·(t/16) + i (i < 4) at d = 4·(t%16) … +3, so it can write both a [row][d] and a [d][row] plane.
-struct RowStage4 {
-    f32x4 v[4];
+// An R × 64 slice of one head (R = 64 or 32 rows) in registers between its global fetch and its LDS commit:
+// thread t holds rows (R/16)·(t/16) + i (i < R/16) at d = 4·(t%16) … +3, so it can write both a [row][d]
+// and a [d][row] plane.
+template <int R>
+struct RowStage {
+    static constexpr int N = R / 16;
+    f32x4 v[N];
 };
 
-__device__ __forceinline__ void fetch_rows4(RowStage4& st, const float* base, long stride, int L, int row0) {
+template <int R>
+constexpr int tsh() { return R + 4; }  // bf16 stride of [d][row] planes: b64 reads of 4 rows without conflicts
+
+template <int R>
+__device__ __forceinline__ void fetch_rows(RowStage<R>& st, const float* base, long stride, int L, int row0) {
+    constexpr int N = RowStage<R>::N;
     const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int t = row0 + 4 * q + i;
+    for (int i = 0; i < N; ++i) {
+        const int t = row0 + N * q + i;
         st.v[i] = (t >= 0 && t < L) ? ld4(base + (long)t * stride + j) : f32x4{0, 0, 0, 0};
     }
 }
 
-// Three [row][d] planes (stride KSH, plane stride TILE·KSH).
-__device__ __forceinline__ void commit_rows(const RowStage4& st, __bf16* planes) {
+// Three [row][d] planes (stride KSH, plane stride R·KSH).
+template <int R>
+__device__ __forceinline__ void commit_rows(const RowStage<R>& st, __bf16* planes) {
+    constexpr int N = RowStage<R>::N;
     const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < N; ++i) {
         bf16x4 h1, h2, h3;
         split3_4(st.v[i], h1, h2, h3);
-        __bf16* o = planes + (4 * q + i) * KSH + j;
+        __bf16* o = planes + (N * q + i) * KSH + j;
         *reinterpret_cast<bf16x4*>(o) = h1;
-        *reinterpret_cast<bf16x4*>(o + TILE * KSH) = h2;
-        *reinterpret_cast<bf16x4*>(o + 2 * TILE * KSH) = h3;
+        *reinterpret_cast<bf16x4*>(o + R * KSH) = h2;
+        *reinterpret_cast<bf16x4*>(o + 2 * R * KSH) = h3;
     }
 }
 
-// Three [d][row] planes (stride TSH, plane stride 64·TSH).
-__device__ __forceinline__ void commit_cols(const RowStage4& st, __bf16* planes) {
+// Three [d][row] planes (stride tsh<R>(), plane stride 64·tsh<R>()).
+template <int R>
+__device__ __forceinline__ void commit_cols(const RowStage<R>& st, __bf16* planes) {
+    constexpr int N = RowStage<R>::N, TS = tsh<R>();
     const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        bf16x4 h1, h2, h3;
-        split3_4(f32x4{st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]}, h1, h2, h3);
-        __bf16* o = planes + (j + e) * TSH + 4 * q;
-        *reinterpret_cast<bf16x4*>(o) = h1;
-        *reinterpret_cast<bf16x4*>(o + 64 * TSH) = h2;
-        *reinterpret_cast<bf16x4*>(o + 2 * 64 * TSH) = h3;
+        __bf16* o = planes + (j + e) * TS + N * q;
+        if constexpr (N == 4) {
+            bf16x4 h1, h2, h3;
+            split3_4(f32x4{st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]}, h1, h2, h3);
+            *reinterpret_cast<bf16x4*>(o) = h1;
+            *reinterpret_cast<bf16x4*>(o + 64 * TS) = h2;
+            *reinterpret_cast<bf16x4*>(o + 2 * 64 * TS) = h3;
+        } else {
+            static_assert(N == 2, "tiles of 64 or 32 rows");
+            bf16x4 h1, h2, h3;
+            split3_4(f32x4{st.v[0][e], st.v[1][e], 0.0f, 0.0f}, h1, h2, h3);
+            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<bf16x2*>(o) = __builtin_shufflevector(h1, h1, 0, 1);
+            *reinterpret_cast<bf16x2*>(o + 64 * TS) = __builtin_shufflevector(h2, h2, 0, 1);
+            *reinterpret_cast<bf16x2*>(o + 2 * 64 * TS) = __builtin_shufflevector(h3, h3, 0, 1);
+        }
     }
 }
 
@@ -356,26 +377,35 @@ __device__ __forceinline__ void split_lane_row(const float* src, bool valid, int
 }
 
 // The 16-k fragments of row `row` of three [row][d] planes at k-step s.
+template <int R>
 __device__ __forceinline__ void row_frag(const __bf16* planes, int row, int s, int h, bf16x8 (&f)[3]) {
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl)
-        f[pl] = *reinterpret_cast<const bf16x8*>(planes + pl * TILE * KSH + row * KSH + 16 * s + 8 * h);
+        f[pl] = *reinterpret_cast<const bf16x8*>(planes + pl * R * KSH + row * KSH + 16 * s + 8 * h);
 }
 
 // The fragments of d-row `d` of three [d][row] planes over the 16 rows from r0, in the key order above.
+template <int R>
 __device__ __forceinline__ void col_frag(const __bf16* planes, int d, int r0, int h, bf16x8 (&f)[3]) {
+    constexpr int TS = tsh<R>();
 #pragma unroll
     for (int pl = 0; pl < 3; ++pl) {
-        const __bf16* row = planes + pl * 64 * TSH + d * TSH + r0 + 4 * h;
+        const __bf16* row = planes + pl * 64 * TS + d * TS + r0 + 4 * h;
         f[pl] = cat8(*reinterpret_cast<const bf16x4*>(row), *reinterpret_cast<const bf16x4*>(row + 8));
     }
+}
+
+// 16 values of a lane's accumulator column as the pieces of two 16-row k-steps (in the key order above).
+__device__ __forceinline__ void split_col16(const float (&v)[16], int u, bf16x8 (&out)[3]) {
+    split8(f32x4{v[8 * u], v[8 * u + 1], v[8 * u + 2], v[8 * u + 3]},
+           f32x4{v[8 * u + 4], v[8 * u + 5], v[8 * u + 6], v[8 * u + 7]}, out);
 }
 
 template <int D>
 __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
     __shared__ __attribute__((aligned(16))) __bf16 Kh[3 * TILE * KSH];  // K tile, [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 Vt[3 * D * TSH];     // V tile, [d][key]
+    __shared__ __attribute__((aligned(16))) __bf16 Vt[3 * D * tsh<TILE>()];  // V tile, [d][key]
 
     const int seg = blockIdx.y, head = blockIdx.z;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
@@ -408,17 +438,17 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
 
     const float* kbase = p.qkv + (long)start * stride + kcol;
     const float* vbase = p.qkv + (long)start * stride + vcol;
-    RowStage4 kst, vst;
-    fetch_rows4(kst, kbase, stride, L, kbeg);
-    fetch_rows4(vst, vbase, stride, L, kbeg);
+    RowStage<TILE> kst, vst;
+    fetch_rows<TILE>(kst, kbase, stride, L, kbeg);
+    fetch_rows<TILE>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
         __syncthreads();
-        commit_rows(kst, Kh);
-        commit_cols(vst, Vt);
+        commit_rows<TILE>(kst, Kh);
+        commit_cols<TILE>(vst, Vt);
         __syncthreads();
         if (kt0 + TILE < kend) {  // block-uniform: the next tile's loads overlap this tile's products
-            fetch_rows4(kst, kbase, stride, L, kt0 + TILE);
-            fetch_rows4(vst, vbase, stride, L, kt0 + TILE);
+            fetch_rows<TILE>(kst, kbase, stride, L, kt0 + TILE);
+            fetch_rows<TILE>(vst, vbase, stride, L, kt0 + TILE);
         }
 #pragma unroll
         for (int st = 0; st < TILE / 32; ++st) {
@@ -430,7 +460,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 bf16x8 kf[3];
-                row_frag(Kh, 32 * st + lr, ks, h, kf);
+                row_frag<TILE>(Kh, 32 * st + lr, ks, h, kf);
                 s = mma6(kf, qh[ks], s);
             }
             float t[16];
@@ -475,12 +505,11 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 bf16x8 ph[3];
-                split8(f32x4{pr[8 * u], pr[8 * u + 1], pr[8 * u + 2], pr[8 * u + 3]},
-                       f32x4{pr[8 * u + 4], pr[8 * u + 5], pr[8 * u + 6], pr[8 * u + 7]}, ph);
+                split_col16(pr, u, ph);
 #pragma unroll
                 for (int dt = 0; dt < 2; ++dt) {
                     bf16x8 vf[3];
-                    col_frag(Vt, 32 * dt + lr, 32 * st + 16 * u, h, vf);
+                    col_frag<TILE>(Vt, 32 * dt + lr, 32 * st + 16 * u, h, vf);
                     o[dt] = mma6(vf, ph, o[dt]);
                 }
             }
@@ -749,6 +778,244 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
     }
 }
 
+// The backward on split products, tiles of 32 rows (the transposed planes would not leave room for two
+// blocks per CU at 64).
+constexpr int BT = 32;
+
+template <int D>
+__global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
+    static_assert(D == 64, "split-product attention is written for head_dim 64");
+    __shared__ __attribute__((aligned(16))) __bf16 Qh[3 * BT * KSH];      // Q tile, [q][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Qt[3 * D * tsh<BT>()];  // Q tile, [d][q]
+    __shared__ __attribute__((aligned(16))) __bf16 Oh[3 * BT * KSH];      // dO tile, [q][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Ot[3 * D * tsh<BT>()];  // dO tile, [d][q]
+    __shared__ float lse_s[BT], dot_s[BT];
+
+    const int seg = blockIdx.y, head = blockIdx.z;
+    const int start = p.seg_start[seg], L = p.seg_len[seg];
+    const int kb0 = blockIdx.x * BLOCK_ROWS;
+    if (kb0 >= L) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
+    const int k0w = kb0 + wave * WAVE_ROWS;
+    const int key = k0w + lr;
+    const bool kvalid = key < L;
+    const bool rope = p.cos_t != nullptr;
+    const int hw = p.half_window;
+    const long stride = 3L * p.hidden;
+    const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
+
+    // The own K row split once; the own V row kept in fp32 (d = 16s + 8h … +7) and split per use, which
+    // keeps the kernel within two waves' registers.
+    bf16x8 kh[4][3];
+    f32x4 vlo[4], vhi[4];
+    const long krow = (long)(start + (kvalid ? key : 0)) * stride;
+    split_lane_row(p.qkv + krow + kcol, kvalid, h, kh);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        vlo[ks] = kvalid ? ld4(p.qkv + krow + vcol + 16 * ks + 8 * h) : f32x4{0, 0, 0, 0};
+        vhi[ks] = kvalid ? ld4(p.qkv + krow + vcol + 16 * ks + 8 * h + 4) : f32x4{0, 0, 0, 0};
+    }
+
+    int qbeg = 0, qend = L, wbeg = 0, wend = L;
+    if (hw >= 0) {
+        qbeg = max(0, kb0 - hw);
+        qend = min(L, kb0 + BLOCK_ROWS + hw);
+        wbeg = max(0, k0w - hw);
+        wend = min(L, k0w + WAVE_ROWS + hw);
+    }
+
+    f32x16 dk[2], dv[2];
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+        dk[dt] = f32x16{};
+        dv[dt] = f32x16{};
+    }
+
+    const float* qbase = p.qkv + (long)start * stride + qcol;
+    const float* obase = p.dcontext + (long)start * p.hidden + qcol;
+    for (int qt0 = qbeg; qt0 < qend; qt0 += BT) {
+        __syncthreads();
+        {
+            RowStage<BT> qst, ost;
+            fetch_rows<BT>(qst, qbase, stride, L, qt0);
+            fetch_rows<BT>(ost, obase, p.hidden, L, qt0);
+            const int t = qt0 + (int)threadIdx.x;
+            if (threadIdx.x < BT) {
+                lse_s[threadIdx.x] = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
+                dot_s[threadIdx.x] = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
+            }
+            commit_rows<BT>(qst, Qh);
+            commit_cols<BT>(qst, Qt);
+            commit_rows<BT>(ost, Oh);
+            commit_cols<BT>(ost, Ot);
+        }
+        __syncthreads();
+        // Wave-uniform: outside this wave's window, or a wave whose keys all lie past the segment end.
+        if (qt0 >= wend || qt0 + BT <= wbeg || k0w >= L) continue;
+        // S[q][key] = Q·Kᵀ and dP = dO·Vᵀ: lane column = its key, rows = 16 queries.
+        f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8 f[3];
+            row_frag<BT>(Qh, lr, ks, h, f);
+            s = mma6(f, kh[ks], s);
+            row_frag<BT>(Oh, lr, ks, h, f);
+            // The asm marks the row as changed, so its split is not hoisted out of the query loop.
+            asm volatile("" : "+v"(vlo[ks]), "+v"(vhi[ks]));
+            bf16x8 vh[3];
+            split8(vlo[ks], vhi[ks], vh);
+            dp = mma6(f, vh, dp);
+        }
+        float pm[16], ds[16];
+        if (p.p_drop == 0.0f && subtile_inside(qt0, k0w, L, hw)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
+                const float pr = fast_exp2(s[r] * p.scale_log2 - lse_s[ql]);
+                pm[r] = pr;
+                ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
+                const int qq = qt0 + ql;
+                const bool ok = in_window(qq, key, L, hw) && kvalid;
+                const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse_s[ql]) : 0.0f;
+                float mask = 1.0f;
+                if (p.p_drop > 0.0f && ok)
+                    mask = uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
+                pm[r] = pr * mask;
+                ds[r] = pr * (dp[r] * mask - dot_s[ql]) * p.scale;
+            }
+        }
+        // dVᵀ += dOᵀ·(P∘M) and dKᵀ += Qᵀ·dS over the tile's 32 queries in two 16-query steps.
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            bf16x8 ph[3], dh[3];
+            split_col16(pm, u, ph);
+            split_col16(ds, u, dh);
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) {
+                bf16x8 f[3];
+                col_frag<BT>(Ot, 32 * dt + lr, 16 * u, h, f);
+                dv[dt] = mma6(f, ph, dv[dt]);
+                col_frag<BT>(Qt, 32 * dt + lr, 16 * u, h, f);
+                dk[dt] = mma6(f, dh, dk[dt]);
+            }
+        }
+    }
+
+    if (kvalid) {
+        if (rope) inverse_rope_acc<D>(dk, p, key, h);
+        float* dst = p.dqkv + (long)(start + key) * stride;
+        store_acc<D>(dk, dst + kcol, h, 1.0f);
+        store_acc<D>(dv, dst + vcol, h, 1.0f);
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
+    static_assert(D == 64, "split-product attention is written for head_dim 64");
+    __shared__ __attribute__((aligned(16))) __bf16 Kh[3 * BT * KSH];      // K tile, [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Kt[3 * D * tsh<BT>()];  // K tile, [d][key]
+    __shared__ __attribute__((aligned(16))) __bf16 Vh[3 * BT * KSH];      // V tile, [key][d]
+
+    const int seg = blockIdx.y, head = blockIdx.z;
+    const int start = p.seg_start[seg], L = p.seg_len[seg];
+    const int qb0 = blockIdx.x * BLOCK_ROWS;
+    if (qb0 >= L) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
+    const int q0w = qb0 + wave * WAVE_ROWS;
+    const int q = q0w + lr;
+    const bool qvalid = q < L;
+    const bool rope = p.cos_t != nullptr;
+    const int hw = p.half_window;
+    const long stride = 3L * p.hidden;
+    const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
+
+    bf16x8 qh[4][3], oh[4][3];
+    const int qs = start + (qvalid ? q : 0);
+    split_lane_row(p.qkv + (long)qs * stride + qcol, qvalid, h, qh);
+    split_lane_row(p.dcontext + (long)qs * p.hidden + qcol, qvalid, h, oh);
+    const float lse = qvalid ? p.lse[(long)qs * p.heads + head] : __builtin_huge_valf();
+    const float dot = qvalid ? p.dots[(long)qs * p.heads + head] : 0.0f;
+
+    int kbeg = 0, kend = L, wbeg = 0, wend = L;
+    if (hw >= 0) {
+        kbeg = max(0, qb0 - hw);
+        kend = min(L, qb0 + BLOCK_ROWS + hw);
+        wbeg = max(0, q0w - hw);
+        wend = min(L, q0w + WAVE_ROWS + hw);
+    }
+
+    f32x16 dq[2];
+    dq[0] = f32x16{};
+    dq[1] = f32x16{};
+
+    const float* kbase = p.qkv + (long)start * stride + kcol;
+    const float* vbase = p.qkv + (long)start * stride + vcol;
+    RowStage<BT> kst, vst;
+    fetch_rows<BT>(kst, kbase, stride, L, kbeg);
+    fetch_rows<BT>(vst, vbase, stride, L, kbeg);
+    for (int kt0 = kbeg; kt0 < kend; kt0 += BT) {
+        __syncthreads();
+        commit_rows<BT>(kst, Kh);
+        commit_cols<BT>(kst, Kt);
+        commit_rows<BT>(vst, Vh);
+        __syncthreads();
+        if (kt0 + BT < kend) {  // block-uniform
+            fetch_rows<BT>(kst, kbase, stride, L, kt0 + BT);
+            fetch_rows<BT>(vst, vbase, stride, L, kt0 + BT);
+        }
+        // Wave-uniform: outside this wave's window, or a wave whose rows all lie past the segment end.
+        if (kt0 >= wend || kt0 + BT <= wbeg || q0w >= L) continue;
+        // Sᵀ = K·Qᵀ and dPᵀ = V·dOᵀ: lane column = its query, rows = 16 keys.
+        f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8 f[3];
+            row_frag<BT>(Kh, lr, ks, h, f);
+            s = mma6(f, qh[ks], s);
+            row_frag<BT>(Vh, lr, ks, h, f);
+            dp = mma6(f, oh[ks], dp);
+        }
+        float ds[16];
+        if (p.p_drop == 0.0f && subtile_inside(q0w, kt0, L, hw)) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * p.scale_log2 - lse) * (dp[r] - dot) * p.scale;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = kt0 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const bool ok = in_window(q, key, L, hw);
+                const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse) : 0.0f;
+                float mask = 1.0f;
+                if (p.p_drop > 0.0f && ok)
+                    mask = uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
+                ds[r] = pr * (dp[r] * mask - dot) * p.scale;
+            }
+        }
+        // dQᵀ += Kᵀ·dSᵀ over the tile's 32 keys in two 16-key steps.
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            bf16x8 dh[3];
+            split_col16(ds, u, dh);
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt) {
+                bf16x8 f[3];
+                col_frag<BT>(Kt, 32 * dt + lr, 16 * u, h, f);
+                dq[dt] = mma6(f, dh, dq[dt]);
+            }
+        }
+    }
+
+    if (qvalid) {
+        if (rope) inverse_rope_acc<D>(dq, p, q, h);
+        store_acc<D>(dq, p.dqkv + (long)(start + q) * stride + qcol, h, 1.0f);
+    }
+}
+
 // RoPE at segment-local positions on the q and k columns of one segment's qkv rows, written to `out`
 // together with an unchanged copy of v (Gather, Ops.cs:297-313). One thread per float4 unit of a row:
 // the first hidden/4 units are (d, d + D/2) pairs of q and then k, the next hidden/4 copy v.
@@ -877,7 +1144,9 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     }
     {
         ProfileScope scope(ctx, "attention_bwd_dkv", 2.0 * fb, 0.0);
-        if (a.head_dim == 64)
+        if (a.head_dim == 64 && split_attention(ctx))
+            hipLaunchKernelGGL(attn_bwd_dkv_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        else if (a.head_dim == 64)
             hipLaunchKernelGGL(attn_bwd_dkv_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         else
             hipLaunchKernelGGL(attn_bwd_dkv_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
@@ -885,7 +1154,9 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     }
     {
         ProfileScope scope(ctx, "attention_bwd_dq", 2.0 * fb, 0.0);
-        if (a.head_dim == 64)
+        if (a.head_dim == 64 && split_attention(ctx))
+            hipLaunchKernelGGL(attn_bwd_dq_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        else if (a.head_dim == 64)
             hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         else
             hipLaunchKernelGGL(attn_bwd_dq_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
