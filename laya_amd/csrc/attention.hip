@@ -1089,9 +1089,9 @@ void check_args(const AttentionArgs& a) {
     LAYA_REQUIRE(a.cos_table == nullptr || a.positions >= a.max_len, "attention: rotary table shorter than max_len");
 }
 
-// Attention takes split products under the fp32 policy that splits every product class; the fp32 matrix
-// cores otherwise (the fp32-MFMA policy, and the bf16 policies, whose attention stays fp32).
-bool split_attention(const laya_ctx* ctx) { return (ctx->matmul_split & 7) == 7; }
+// Attention takes split products (fp32 results) unless the context asked for the fp32 matrix cores; the
+// bf16 product policies leave attention in fp32 arithmetic too.
+bool split_attention(const laya_ctx* ctx) { return (ctx->matmul_split | ctx->matmul_bf16) != 0; }
 
 }  // namespace
 
