@@ -736,6 +736,8 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_pair_kernel(GemmParams nn, Ge
 // (a worker holds at most two: its first and its last dW tile) and `pair_fixup_kernel` adds them in
 // worker order. No workgroup ever waits on another, and the sums do not depend on timing.
 
+constexpr int FIXUP_MAX_WORKERS = 2048;  // workers a pair plan may have (2 per CU)
+
 struct PairPlan {
     int G;                   // workers = grid size
     int nn_tiles, nn_units;  // dX tiles and K units per dX tile
@@ -829,15 +831,19 @@ template <bool KLAYOUT>
 __global__ __launch_bounds__(THREADS) void pair_fixup_kernel(GemmParams tn, PairPlan s) {
     const int t = blockIdx.x, i = blockIdx.y >> 2, r4 = blockIdx.y & 3;
     const int a = t * s.tn_units, b = a + s.tn_units;
+    // Every worker's dW run start, computed once per block in parallel (G ≤ FIXUP_MAX_WORKERS).
+    __shared__ int run_lo[FIXUP_MAX_WORKERS + 1];
+    for (int g = threadIdx.x; g <= s.G; g += THREADS) run_lo[g] = plan_tn_lo(s, g);
+    __syncthreads();
     // First worker whose dW run ends after a (runs are ordered and contiguous).
     int lo = 0, hi = s.G - 1;
     while (lo < hi) {
         const int mid = (lo + hi) >> 1;
-        if (plan_tn_lo(s, mid + 1) > a) hi = mid; else lo = mid + 1;
+        if (run_lo[mid + 1] > a) hi = mid; else lo = mid + 1;
     }
     int covering = 0;
-    for (int g = lo; g < s.G && plan_tn_lo(s, g) < b; ++g)
-        if (plan_tn_lo(s, g + 1) > plan_tn_lo(s, g)) ++covering;
+    for (int g = lo; g < s.G && run_lo[g] < b; ++g)
+        if (run_lo[g + 1] > run_lo[g]) ++covering;
     if (covering <= 1) return;  // one worker held the whole tile and accumulated it in place
 
     // The covering workers' partial slots in worker order, in batches of 8 so the loads of a batch are
@@ -850,7 +856,7 @@ __global__ __launch_bounds__(THREADS) void pair_fixup_kernel(GemmParams tn, Pair
         int slots[8];
         int n = 0;
         for (; g < s.G && n < 8; ++g) {
-            const int glo = plan_tn_lo(s, g), ghi = plan_tn_lo(s, g + 1);
+            const int glo = run_lo[g], ghi = run_lo[g + 1];
             if (glo >= b) {
                 g = s.G;
                 break;
@@ -1321,7 +1327,8 @@ bool make_pair_plan(const laya_ctx* ctx, int n0, int out, int n1, int rows, Pair
     s.W = (int)std::min<long>(W, 1L << 30);
     const long need_min = W / s.G - (long)(s.q + (s.r > 0 ? 1 : 0)) * s.nn_units;
     const long max_run = (W + s.G - 1) / s.G - (long)s.q * s.nn_units;
-    return need_min >= 0 && s.nn_units > 0 && W * s.G < (1L << 31) && max_run < s.tn_units;
+    return need_min >= 0 && s.nn_units > 0 && W * s.G < (1L << 31) && max_run < s.tn_units &&
+           s.G <= FIXUP_MAX_WORKERS;
 }
 
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
