@@ -685,6 +685,114 @@ __device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord
     __syncthreads();
 }
 
+// Split products with 16-deep K stages, three workgroups per CU: half the LDS (36 KB) and half the staging
+// registers of the 32-deep form, for grids that fill the chip in one round at three per CU but not at two
+// (e.g. 654 tiles: one round on 768 slots instead of two on 512). k-contiguous float4 operands only.
+constexpr int BKQ = 16;
+constexpr int KPADQ = BKQ + 8;       // 48-byte rows: b128 fragment reads of 16 consecutive rows hit distinct banks
+constexpr int STAGE_Q = BM * KPADQ;  // bf16 elements per operand plane
+
+struct OperandQ {
+    const float* src;
+    unsigned off[2];
+    int kq;
+    f32x4 reg[2];
+    __device__ __forceinline__ OperandQ(const float* s, long ldl, int mn0, int MN, int tid) : src(s) {
+        kq = (tid & 3) << 2;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) off[i] = (unsigned)min(mn0 + (tid >> 2) + 64 * i, MN - 1) * (unsigned)ldl + kq;
+    }
+    __device__ __forceinline__ void full(int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) reg[i] = *reinterpret_cast<const f32x4*>(src + off[i] + (unsigned)k0);
+    }
+    // The ragged last K stage: positions at or past kend (a multiple of 4) become 0.
+    __device__ __forceinline__ void tail(int k0, int kend) {
+        const int k = k0 + kq;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const f32x4 v = *reinterpret_cast<const f32x4*>(src + off[i] - kq + (unsigned)min(k, kend - 4));
+            reg[i] = k < kend ? v : f32x4{0, 0, 0, 0};
+        }
+    }
+    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            bf16x4 h1, h2, h3;
+            split3_4(reg[i], h1, h2, h3);
+            const int o = ((tid >> 2) + 64 * i) * KPADQ + ((tid & 3) << 2);
+            *reinterpret_cast<bf16x4*>(lds + o) = h1;
+            *reinterpret_cast<bf16x4*>(lds + STAGE_Q + o) = h2;
+            *reinterpret_cast<bf16x4*>(lds + 2 * STAGE_Q + o) = h3;
+        }
+    }
+};
+
+__device__ __forceinline__ void mma_stage_q(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2], int wm, int wn,
+                                            int lr, int half) {
+    bf16x8 a[2][3], b[2][3];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+            a[i][pl] = *reinterpret_cast<const bf16x8*>(A + pl * STAGE_Q + (wm * 64 + 32 * i + lr) * KPADQ + 8 * half);
+            b[i][pl] = *reinterpret_cast<const bf16x8*>(B + pl * STAGE_Q + (wn * 64 + 32 * i + lr) * KPADQ + 8 * half);
+        }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f32x16 c = acc[i][j];
+            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][2], b[j][0], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][2], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][1], b[j][1], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][1], b[j][0], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][1], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i][0], b[j][0], c, 0, 0, 0);
+            acc[i][j] = c;
+        }
+}
+
+template <int MODE, bool RES>
+__global__ __launch_bounds__(THREADS, 3) void gemm_x6q_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * STAGE_Q];
+    const TileCoord c = tile_coord(p, xcd_logical_block());
+    const int len = max(0, c.ke - c.kb);
+    const int nfull = len / BKQ, ntiles = nfull + (len % BKQ != 0 ? 1 : 0);
+    const int rot = nfull > 0 ? c.t % nfull : 0;
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, half = lane >> 5;
+    OperandQ a(p.A, p.lda, c.m0, p.M, tid);
+    OperandQ b(p.B, p.ldb, c.n0, p.N, tid);
+    auto fetch = [&](int j) {
+        if (j < nfull) {
+            int q = j + rot;
+            if (q >= nfull) q -= nfull;
+            a.full(c.kb + q * BKQ);
+            b.full(c.kb + q * BKQ);
+        } else {
+            a.tail(c.kb + nfull * BKQ, c.ke);
+            b.tail(c.kb + nfull * BKQ, c.ke);
+        }
+    };
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    if (ntiles > 0) fetch(0);
+    for (int j = 0; j < ntiles; ++j) {
+        __syncthreads();
+        a.store(smem[0], tid);
+        b.store(smem[1], tid);
+        __syncthreads();
+        if (j + 1 < ntiles) fetch(j + 1);
+        mma_stage_q(smem[0], smem[1], acc, wm, wn, lr, half);
+    }
+    tile_store<true, true, MODE, RES>(p, c, acc);
+}
+
 // The fp32 product from bf16 pieces; accumulators in the k-contiguous layout whatever the operands' form.
 template <int AOP, int BOP, int MODE, bool RES>
 __global__ __launch_bounds__(THREADS, 2) void gemm_x6_kernel(GemmParams p) {
@@ -1136,7 +1244,14 @@ template <bool AK, bool BKC> void launch_x6(laya_ctx* ctx, const GemmParams& p, 
     const bool va = AK && operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K);
     const bool vb = BKC && operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K);
     if constexpr (AK && BKC) {
-        if (va && vb) launch_x<KVEC, KVEC>(ctx, p, blocks);
+        if (va && vb && p.mode == STORE && three_per_cu(ctx, blocks)) {
+            const dim3 g(blocks), b(THREADS);
+            if (p.R)
+                hipLaunchKernelGGL((gemm_x6q_kernel<STORE, true>), g, b, 0, ctx->stream, p);
+            else
+                hipLaunchKernelGGL((gemm_x6q_kernel<STORE, false>), g, b, 0, ctx->stream, p);
+            check_launch("gemm_x6q_kernel");
+        } else if (va && vb) launch_x<KVEC, KVEC>(ctx, p, blocks);
         else if (va) launch_x<KVEC, KSCALAR>(ctx, p, blocks);
         else if (vb) launch_x<KSCALAR, KVEC>(ctx, p, blocks);
         else launch_x<KSCALAR, KSCALAR>(ctx, p, blocks);

@@ -39,7 +39,10 @@ def param(ctx, name, a, trainable=True):
                                           (8000, 768, 768), (9000, 768, 2304),
                                           # dW tiles outnumber the workers: a worker's dW run would cover a
                                           # whole tile, which the schedule must not take
-                                          (4096, 2944, 2944)])
+                                          (4096, 2944, 2944),
+                                          # 516 forward tiles: three workgroups per CU with 16-deep K
+                                          # stages (the second with a ragged last stage)
+                                          (11000, 768, 768), (11000, 1148, 768)])
 def test_linear_forward_and_backward(ctx, rows, inn, out, policy):
     """Both fp32 implementations (exact bf16 splits, the default; the fp32 matrix cores) at the fp64
     oracle's result to 1e-6, widened as √K for reductions longer than 2048 terms (fp32 rounding of a
