@@ -1106,6 +1106,22 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_generic_kernel(GemmParams p) 
 
 // ------------------------------------------------------------------------------ reductions
 
+// C[m, n] = (Σ_s P[s][m][n] + bias[n]) + R[m, n], s in order: the epilogue of a stored product whose K
+// was split, in the order the unsplit epilogue adds (R may be C itself: one thread reads and writes each
+// element).
+__global__ void splitk_store_kernel(const float* __restrict__ P, int splits, int M, int N, float* C, long ldc,
+                                    const float* __restrict__ bias, const float* R, long ldr) {
+    const long total = (long)M * N;
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+        float s = 0.0f;
+        for (int k = 0; k < splits; ++k) s += P[(long)k * total + i];
+        const long m = i / N, n = i - m * N;
+        if (bias) s += bias[n];
+        if (R) s += R[m * ldr + n];
+        C[m * ldc + n] = s;
+    }
+}
+
 // C[m, n] += Σ_s P[s][m][n], s in order.
 __global__ void splitk_reduce_kernel(const float* __restrict__ P, int splits, int M, int N, float* C, long ldc) {
     const long total = (long)M * N;
@@ -1362,6 +1378,15 @@ void finish_accumulate(laya_ctx* ctx, const GemmParams& p, float* out, long ldc)
     check_launch("splitk_reduce_kernel");
 }
 
+// K splits for a grid of `tiles` that would not fill one round of two workgroups per CU: as many as fit in
+// that round, keeping at least min_k of K per split. A lone workgroup's K loop is latency-bound (about a
+// microsecond per 32-deep stage), so splitting K across idle CUs is what shortens such products.
+int fill_splits(const laya_ctx* ctx, int tiles, int K, int min_k) {
+    const int slots = 2 * ctx->cu_count;
+    if (tiles <= 0 || tiles * 2 > slots) return 1;
+    return std::max(1, std::min({slots / tiles, K / min_k, 32}));
+}
+
 }  // namespace
 
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
@@ -1370,13 +1395,17 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
     GemmParams p = make_params(M, N, K, A, lda, B, ldb, C, ldc, bias, R, ldr);
     const int tiles = p.tiles_m * p.tiles_n;
     float* out = C;
+    bool split_store = false;
     if (ep == GemmEpilogue::Accumulate) {
-        // Fill the chip: aim for ≥ 2 workgroups per CU, but keep ≥ 512 of K per split.
-        const int want = (2 * ctx->cu_count + tiles - 1) / tiles;
-        set_splits(p, std::max(1, std::min(want, std::max(1, K / 512))));
+        set_splits(p, fill_splits(ctx, tiles, K, 128));
         out = prepare_accumulate(ctx, p);
     } else {
         p.mode = STORE;
+        if (set_splits(p, fill_splits(ctx, tiles, K, 128)) > 1) {
+            p.mode = PARTIAL;
+            p.C = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)p.splits * M * N));
+            split_store = true;
+        }
     }
     const int blocks = tiles * p.splits;
     {
@@ -1391,6 +1420,14 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
             case GemmLayout::NN: launch<true, false>(ctx, p, blocks); break;
             case GemmLayout::TN: launch<false, false>(ctx, p, blocks); break;
         }
+    }
+    if (split_store) {
+        const long total = (long)M * N;
+        ProfileScope scope(ctx, "gemm_splitk_store", 0.0, 4.0 * total * (p.splits + 1 + (R ? 1 : 0)));
+        hipLaunchKernelGGL(splitk_store_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
+                           p.splits, M, N, C, ldc, bias, R, ldr);
+        check_launch("splitk_store_kernel");
+        return;
     }
     finish_accumulate(ctx, p, out, ldc);
 }
