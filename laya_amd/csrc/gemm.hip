@@ -932,6 +932,33 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_pair_planned_x6_kernel(GemmPa
     }
 }
 
+// The planned pair with bf16 products (the bf16 policies for both backward product classes).
+template <int AOP, bool RES>
+__global__ __launch_bounds__(THREADS, 2) void gemm_pair_planned_h_kernel(GemmParams nn, GemmParams tn, PairPlan s) {
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][STAGE_H];
+    const int g = xcd_logical_block();
+    const int count = s.q + (g < s.r ? 1 : 0);
+    for (int n = 0; n < count; ++n) {
+        const TileCoord c = unit_coord(nn, g + n * s.G, 0, s.nn_units);
+        f32x16 acc[2][2];
+        tile_mma_h<AOP, MNSCALAR>(nn, c, smem, acc);
+        tile_store<true, true, STORE, RES>(nn, c, acc);
+        __syncthreads();
+    }
+    const int lo = plan_tn_lo(s, g), hi = plan_tn_lo(s, g + 1);
+    for (int u = lo; u < hi;) {
+        const int t = u / s.tn_units;
+        const int a = u - t * s.tn_units;
+        const int b = min(s.tn_units, a + (hi - u));
+        const TileCoord c = unit_coord(tn, t, a, b);
+        f32x16 acc[2][2];
+        tile_mma_h<MNSCALAR, MNSCALAR>(tn, c, smem, acc);
+        write_partial(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (BM * BN), acc);
+        __syncthreads();
+        u += b - a;
+    }
+}
+
 // Adds the partials of the workers that shared a dW tile, in worker order, into dW. Eight workgroups
 // per tile (blockIdx.y = 4i + r/4): each thread sums the two float4 groups (j = 0, 1) of its lanes'
 // accumulator rows and adds them to dW as four column pairs, in the layout `store_acc` uses.
@@ -1495,16 +1522,28 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
                        gemm_fits_h(tn, false, false);
     const bool fp32 = !((ctx->matmul_bf16 | ctx->matmul_split) & 6) && gemm_fast(nn, true, false) &&
                       gemm_fast(tn, false, false);
+    const bool half = (ctx->matmul_bf16 & 6) == 6 && gemm_fits_h(nn, true, false) && gemm_fits_h(tn, false, false);
     const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
     PairPlan s{};
-    if ((split || fp32) && make_pair_plan(ctx, n0, out, n1, rows, s)) {
+    if ((split || fp32 || half) && make_pair_plan(ctx, n0, out, n1, rows, s)) {
         s.partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)s.G * 2 * BM * BN));
         tn.mode = ACCUMULATE;
         {
-            ProfileScope scope(ctx, split ? "gemm_bwd_pair_x6" : "gemm_bwd_pair", 2.0 * 2.0 * rows * (double)in * out,
-                               0.0);
+            ProfileScope scope(ctx, split ? "gemm_bwd_pair_x6" : half ? "gemm_bwd_pair_bf16" : "gemm_bwd_pair",
+                               2.0 * 2.0 * rows * (double)in * out, 0.0);
             const dim3 g(s.G), b(THREADS);
-            if (split) {
+            if (half) {
+                const bool va = operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K);
+                if (va && dx_residual)
+                    hipLaunchKernelGGL((gemm_pair_planned_h_kernel<KVEC, true>), g, b, 0, ctx->stream, nn, tn, s);
+                else if (va)
+                    hipLaunchKernelGGL((gemm_pair_planned_h_kernel<KVEC, false>), g, b, 0, ctx->stream, nn, tn, s);
+                else if (dx_residual)
+                    hipLaunchKernelGGL((gemm_pair_planned_h_kernel<KSCALAR, true>), g, b, 0, ctx->stream, nn, tn, s);
+                else
+                    hipLaunchKernelGGL((gemm_pair_planned_h_kernel<KSCALAR, false>), g, b, 0, ctx->stream, nn, tn, s);
+                check_launch("gemm_pair_planned_h_kernel");
+            } else if (split) {
                 if (operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) {
                     if (dx_residual)
                         hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KVEC, true>), g, b, 0, ctx->stream, nn, tn, s);
@@ -1545,7 +1584,7 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
             }
         }
         ProfileScope scope(ctx, "gemm_pair_fixup", 0.0, 4.0 * BM * BN * (double)(partials + 2 * shared));
-        if (split)
+        if (split || half)
             hipLaunchKernelGGL(pair_fixup_kernel<true>, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
         else
             hipLaunchKernelGGL(pair_fixup_kernel<false>, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
