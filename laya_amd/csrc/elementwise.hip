@@ -204,6 +204,30 @@ __global__ void embedding_bwd_kernel(const int* __restrict__ sorted_pos, const i
     }
 }
 
+// The same sums four columns per thread with the loads of 16 token rows in flight before they are added
+// (in token order, so each column's sum is the serial one): a frequent id's long run of tokens is no longer
+// one load latency per token.
+__global__ void embedding_bwd4_kernel(const int* __restrict__ sorted_pos, const int* __restrict__ unique_ids,
+                                      const int* __restrict__ offsets, const f32x4* __restrict__ d, int hidden4,
+                                      f32x4* __restrict__ grad) {
+    const int u = blockIdx.x;
+    const int b = offsets[u], e = offsets[u + 1];
+    f32x4* g = grad + (size_t)unique_ids[u] * hidden4;
+    for (int c = threadIdx.x; c < hidden4; c += blockDim.x) {
+        f32x4 s = g[c];
+        int k = b;
+        for (; k + 16 <= e; k += 16) {
+            f32x4 v[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) v[j] = d[(size_t)sorted_pos[k + j] * hidden4 + c];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s += v[j];
+        }
+        for (; k < e; ++k) s += d[(size_t)sorted_pos[k] * hidden4 + c];
+        g[c] = s;
+    }
+}
+
 __global__ void gather_rows_kernel(const float* src, const int* rows, int n, int width, float* dst) {
     const size_t total = (size_t)n * width;
     GRID_STRIDE(i, total) {
@@ -504,6 +528,14 @@ void embedding_bwd(laya_ctx* ctx, const int* sorted_pos, const int* unique_ids, 
                    const float* d, int hidden, float* grad) {
     if (n_unique <= 0) return;
     ProfileScope scope(ctx, "embedding_bwd", 0.0, 0.0);
+    if (hidden % 4 == 0 && vec4(d) && vec4(grad)) {
+        const int h4 = hidden / 4;
+        hipLaunchKernelGGL(embedding_bwd4_kernel, dim3(n_unique), dim3(std::min(256, (h4 + 63) / 64 * 64)), 0,
+                           ctx->stream, sorted_pos, unique_ids, offsets, reinterpret_cast<const f32x4*>(d), h4,
+                           reinterpret_cast<f32x4*>(grad));
+        check_launch("embedding_bwd4_kernel");
+        return;
+    }
     hipLaunchKernelGGL(embedding_bwd_kernel, dim3(n_unique), dim3(256), 0, ctx->stream, sorted_pos, unique_ids,
                        offsets, d, hidden, grad);
     check_launch("embedding_bwd_kernel");
