@@ -50,16 +50,18 @@ int laya_ctx_destroy(laya_ctx* ctx);
 /* Caps the bytes laya_alloc may hold (0 = no cap); an allocation over it fails with LAYA_ERR_MEMORY. */
 int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes);
 /* Precision of the matrix products launched on the context afterwards (linear layers and the model's
- * projections; attention and the elementwise kernels stay fp32), per product class. An fp32 class (the
+ * projections; the elementwise kernels stay fp32), per product class. An fp32 class (the
  * default) is computed from an exact three-piece bf16 split of each operand: six bf16 matrix-core products
  * per fp32 product, accumulated in fp32, so the result carries fp32 rounding only (within 1e-6 relative
  * L2 of the fp64 product on every tested shape, as the fp32 matrix-core path); LAYA_MATMUL_FP32_MFMA
  * selects the fp32 matrix cores instead. A bf16 class rounds both operands
  * to bf16 (nearest even) as they are staged and multiplies on the bf16 matrix cores with fp32
  * accumulation and fp32 outputs: the mixed-precision mode (bf16 weights and activations in the
- * products, fp32 master weights, gradients and statistics). No counterpart in the reference, whose
- * products are all fp32 (PackedMatrixBf16, PackedMatrixBf16.cs:7-21, only stores weights in bf16 and
- * widens them to fp32 before multiplying). */
+ * products, fp32 master weights, gradients and statistics). Attention's products (head_dim 64) use the
+ * same fp32-accurate split products under every policy except LAYA_MATMUL_FP32_MFMA, which keeps them on
+ * the fp32 matrix cores; attention never drops to bf16. No counterpart in the reference, whose products are
+ * all fp32 (PackedMatrixBf16, PackedMatrixBf16.cs:7-21, only stores weights in bf16 and widens them to fp32
+ * before multiplying). */
 enum {
     LAYA_MATMUL_FP32 = 0,             /* fp32-accurate products (the default), from bf16 pieces (below) */
     LAYA_MATMUL_BF16_FORWARD = 1,     /* y = x·Wᵀ (and the fused RoPE projection) */
