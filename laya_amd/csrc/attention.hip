@@ -45,7 +45,7 @@ struct Params {
     float* context;
     float* lse;
     const float* dcontext;
-    const float* dots;  // Σ_d dO·O per (row, head)
+    float* dots;  // Σ_d dO·O per (row, head)
     float* dqkv;
 };
 
@@ -939,7 +939,21 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     split_lane_row(p.qkv + (long)qs * stride + qcol, qvalid, h, qh);
     split_lane_row(p.dcontext + (long)qs * p.hidden + qcol, qvalid, h, oh);
     const float lse = qvalid ? p.lse[(long)qs * p.heads + head] : __builtin_huge_valf();
-    const float dot = qvalid ? p.dots[(long)qs * p.heads + head] : 0.0f;
+    // The row constant Σ_d dO·O (Ops.cs:408-409) from the lane's half of the row and its partner's, written
+    // for the dK/dV kernel, which runs after this one.
+    float dot = 0.0f;
+    if (qvalid) {
+        const float* dor = p.dcontext + (long)qs * p.hidden + qcol;
+        const float* cr = p.context + (long)qs * p.hidden + qcol;
+#pragma unroll
+        for (int s4 = 0; s4 < 8; ++s4) {
+            const int d0 = 16 * (s4 >> 1) + 8 * h + 4 * (s4 & 1);
+            const f32x4 a = ld4(dor + d0), b = ld4(cr + d0);
+            dot += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+        }
+    }
+    dot += __shfl_xor(dot, 32, 64);
+    if (qvalid && h == 0) p.dots[(long)qs * p.heads + head] = dot;
 
     int kbeg = 0, kend = L, wbeg = 0, wend = L;
     if (hw >= 0) {
@@ -1132,6 +1146,19 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     // Model flops of the backward, 8·d·Σkeys, split as the kernels do the work: dK/dV (4 products of
     // which 2 recompute the forward's) and dQ (3 products, 2 recomputed).
     const double fb = 2.0 * a.hidden * a.keys;
+    if (a.head_dim == 64 && split_attention(ctx)) {
+        p.context = const_cast<float*>(context);
+        {
+            // dQ first: it forms each row's Σ dO·O and writes it for dK/dV.
+            ProfileScope scope(ctx, "attention_bwd_dq", 2.0 * fb, 0.0);
+            hipLaunchKernelGGL(attn_bwd_dq_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+            check_launch("attn_bwd_dq_x6_kernel");
+        }
+        ProfileScope scope(ctx, "attention_bwd_dkv", 2.0 * fb, 0.0);
+        hipLaunchKernelGGL(attn_bwd_dkv_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        check_launch("attn_bwd_dkv_x6_kernel");
+        return;
+    }
     {
         ProfileScope scope(ctx, "attention_bwd_dots", 0.0, 8.0 * total);
         if (a.head_dim == 64)
@@ -1144,9 +1171,7 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     }
     {
         ProfileScope scope(ctx, "attention_bwd_dkv", 2.0 * fb, 0.0);
-        if (a.head_dim == 64 && split_attention(ctx))
-            hipLaunchKernelGGL(attn_bwd_dkv_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
-        else if (a.head_dim == 64)
+        if (a.head_dim == 64)
             hipLaunchKernelGGL(attn_bwd_dkv_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         else
             hipLaunchKernelGGL(attn_bwd_dkv_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
@@ -1154,9 +1179,7 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     }
     {
         ProfileScope scope(ctx, "attention_bwd_dq", 2.0 * fb, 0.0);
-        if (a.head_dim == 64 && split_attention(ctx))
-            hipLaunchKernelGGL(attn_bwd_dq_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
-        else if (a.head_dim == 64)
+        if (a.head_dim == 64)
             hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         else
             hipLaunchKernelGGL(attn_bwd_dq_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
