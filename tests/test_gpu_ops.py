@@ -73,6 +73,23 @@ def test_linear_forward_and_backward(ctx, rows, inn, out, policy):
     ctx.set_matmul_precision("fp32")
 
 
+@pytest.mark.parametrize("rows,inn,out,with_bias", [(512, 768, 768, True), (200, 2304, 768, False)])
+def test_linear_in_place_residual_with_split_k(ctx, rows, inn, out, with_bias):
+    """y = x·Wᵀ + b + y with the residual being the output itself, on grids small enough (24 and 12 tiles)
+    that the product splits K and a reduce applies bias and residual."""
+    print(f"linear in-place residual rows={rows} in={inn} out={out}", flush=True)
+    rng = np.random.default_rng(rows + inn)
+    x = rng.standard_normal((rows, inn)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+    b = rng.standard_normal(out).astype(np.float32)
+    y0 = rng.standard_normal((rows, out)).astype(np.float32)
+    w, bias = param(ctx, "w", W), (param(ctx, "b", b) if with_bias else None)
+    yd = dev(ctx, y0)
+    laya.linear(w, bias, dev(ctx, x), rows, yd, residual=yd)
+    ref = oracle.linear(x, W, b if with_bias else None, double=True) + y0
+    assert rel_l2(ref, yd.numpy()) < 1e-6
+
+
 @pytest.mark.parametrize("rows,inn,out", [(4100, 64, 96), (1500, 256, 132)])
 def test_linear_backward_one_product(ctx, rows, inn, out):
     """dW alone (split-K partials over a ragged last slice) and dx alone (frozen weight)."""
