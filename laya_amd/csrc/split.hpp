@@ -9,15 +9,30 @@
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 namespace laya {
 
+// Two values to nearest-even bf16 with one convert; the pair's fp32 values are the low half shifted up
+// and the high half masked, so each level costs one convert, two bit operations and two subtractions.
+__device__ __forceinline__ unsigned bf16_pair(float a, float b, float& ra, float& rb) {
+    const unsigned u = __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2{a, b}), bf16x2));
+    ra = a - __builtin_bit_cast(float, u << 16);
+    rb = b - __builtin_bit_cast(float, u & 0xffff0000u);
+    return u;
+}
+
 __device__ __forceinline__ void split3_4(f32x4 x, bf16x4& h1, bf16x4& h2, bf16x4& h3) {
-    h1 = __builtin_convertvector(x, bf16x4);
-    const f32x4 r = x - __builtin_convertvector(h1, f32x4);
-    h2 = __builtin_convertvector(r, bf16x4);
-    const f32x4 r2 = r - __builtin_convertvector(h2, f32x4);
-    h3 = __builtin_convertvector(r2, bf16x4);
+    float r0, r1, r2, r3, q0, q1, q2, q3;
+    const unsigned a01 = bf16_pair(x[0], x[1], r0, r1), a23 = bf16_pair(x[2], x[3], r2, r3);
+    const unsigned b01 = bf16_pair(r0, r1, q0, q1), b23 = bf16_pair(r2, r3, q2, q3);
+    const unsigned c01 = __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2{q0, q1}), bf16x2));
+    const unsigned c23 = __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2{q2, q3}), bf16x2));
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    h1 = __builtin_bit_cast(bf16x4, (u32x2{a01, a23}));
+    h2 = __builtin_bit_cast(bf16x4, (u32x2{b01, b23}));
+    h3 = __builtin_bit_cast(bf16x4, (u32x2{c01, c23}));
 }
 
 }  // namespace laya
