@@ -125,6 +125,20 @@ def test_modernbert_base_width_gradients_match_the_oracle(ctx):
     print(f"worst relative L2 vs fp64 over {len(m.names)} tensors: {worst:.2e}", flush=True)
 
 
+def test_wide_tile_forward_matches_the_oracle(ctx):
+    """4448 tokens at d = 768: the QKV projection (RoPE in its epilogue) and the GeGLU input projection
+    run on 256 × 256 tiles; the logits match the fp64 oracle to 1e-5."""
+    from laya_amd.model import TrainableDecisionModel
+    print("model: d=768, 1 global layer, 4448 tokens", flush=True)
+    mc, o, params, batch = _mid_case(layers=1, lengths=(2048, 1500, 900))
+    o64 = oracle.OracleModel(mc, double=True)
+    o64.set_params(params)
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    lg = m.forward(batch, training=False)
+    assert rel_l2(o64.forward(batch, training=False, keep_tape=False), lg) < 1e-5
+
+
 def _assert_step_matches(o, m, params, lr):
     """The weights after one optimizer step on the GPU against the oracle's step."""
     for name in m.names:

@@ -73,6 +73,24 @@ def test_linear_forward_and_backward(ctx, rows, inn, out, policy):
     ctx.set_matmul_precision("fp32")
 
 
+@pytest.mark.parametrize("rows,inn,out,with_bias", [(6000, 768, 2304, True), (6000, 1152, 2100, False),
+                                                    (13871, 768, 2304, True)])
+def test_linear_forward_on_wide_tiles(ctx, rows, inn, out, with_bias):
+    """Grids whose rounds are shorter on 256 × 256 tiles (no residual): ragged rows and columns, with
+    and without bias, at the fp64 oracle's result to 1e-6."""
+    print(f"linear (wide tiles) rows={rows} in={inn} out={out} bias={with_bias}", flush=True)
+    rng = np.random.default_rng(rows + inn + out)
+    x = rng.standard_normal((rows, inn)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+    b = rng.standard_normal(out).astype(np.float32) if with_bias else None
+    w = param(ctx, "w", W)
+    bias = param(ctx, "b", b) if with_bias else None
+    y_ = dev(ctx, np.zeros((rows, out), np.float32))
+    laya.linear(w, bias, dev(ctx, x), rows, y_)
+    y_ref = oracle.linear(x, W, b if with_bias else np.zeros(out, np.float32), double=True)
+    assert rel_l2(y_ref, y_.numpy()) < 1e-6
+
+
 @pytest.mark.parametrize("rows,inn,out,with_bias", [(512, 768, 768, True), (200, 2304, 768, False)])
 def test_linear_in_place_residual_with_split_k(ctx, rows, inn, out, with_bias):
     """y = x·Wᵀ + b + y with the residual being the output itself, on grids small enough (24 and 12 tiles)
