@@ -1099,6 +1099,184 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_pair_planned_h_kernel(GemmPar
     }
 }
 
+// ------------------------------------------------------------- the backward pair on 256 x 256 tiles
+//
+// The planned pair with the wide tiles' loop: one worker per CU (eight waves, two 16-deep LDS stages),
+// whole dX tiles, then a contiguous run of 16-deep dW units whose partial tiles the wide fixup adds.
+
+// A 256-wide mn-contiguous operand's 16-deep stage (element (mn, k) at src[k·ld + mn]): thread t holds
+// mn = t mod 256 at 8 consecutive k. Positions at or past a ragged K end read an in-bounds row and become 0.
+struct OperandWS {
+    const float* src;
+    unsigned base, ld;
+    int kq;
+    float v[8];
+    __device__ __forceinline__ OperandWS(const float* s, long ldl, int mn0, int MN, int tid)
+        : src(s), base((unsigned)min(mn0 + (tid & 255), MN - 1)), ld((unsigned)ldl), kq((tid >> 8) << 3) {}
+    __device__ __forceinline__ void full(int k0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = src[base + (unsigned)(k0 + kq + e) * ld];
+    }
+    __device__ __forceinline__ void tail(int k0, int kend) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = k0 + kq + e;
+            const float x = src[base + (unsigned)min(k, kend - 1) * ld];
+            v[e] = k < kend ? x : 0.0f;
+        }
+    }
+    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+        bf16x4 a1, a2, a3, b1, b2, b3;
+        split3_4(f32x4{v[0], v[1], v[2], v[3]}, a1, a2, a3);
+        split3_4(f32x4{v[4], v[5], v[6], v[7]}, b1, b2, b3);
+        const int o = (tid & 255) * KPADQ + kq;
+        *reinterpret_cast<bf16x8*>(lds + o) = __builtin_shufflevector(a1, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+        *reinterpret_cast<bf16x8*>(lds + STAGE_W + o) = __builtin_shufflevector(a2, b2, 0, 1, 2, 3, 4, 5, 6, 7);
+        *reinterpret_cast<bf16x8*>(lds + 2 * STAGE_W + o) = __builtin_shufflevector(a3, b3, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+};
+
+// The k-contiguous operand of the wide loop with the ragged-stage form the pair's loop calls (never
+// taken: the plan requires the dX product's K to be a multiple of 16).
+struct OperandWK : OperandW {
+    using OperandW::OperandW;
+    __device__ __forceinline__ void tail(int k0, int) { full(k0); }
+};
+
+// acc += A·Bᵀ over K positions [kb, ke) in 16-deep stages (the last one ragged when ke − kb is not a
+// multiple of 16), full stages in rotated order starting at `rot`.
+template <class OA, class OB>
+__device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, __bf16 (*smem)[2][3 * STAGE_W],
+                                         f32x16 (&acc)[2][2][2], int tid, int wm, int wn, int lr, int half) {
+    const int len = ke - kb, nfull = len / BKQ, nt = nfull + (len % BKQ != 0 ? 1 : 0);
+    rot = nfull > 0 ? rot % nfull : 0;
+    auto fetch = [&](int j) {
+        if (j < nfull) {
+            const int q = j + rot;
+            const int k0 = kb + (q >= nfull ? q - nfull : q) * BKQ;
+            a.full(k0);
+            b.full(k0);
+        } else {
+            a.tail(kb + nfull * BKQ, ke);
+            b.tail(kb + nfull * BKQ, ke);
+        }
+    };
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[s][i][j] = f32x16{};
+    fetch(0);
+    a.store(smem[0][0], tid);
+    b.store(smem[0][1], tid);
+    fetch(min(1, nt - 1));
+    lds_barrier();
+    for (int j = 0; j < nt; ++j) {
+        const int cur = j & 1;
+        mma_stage_w(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
+        a.store(smem[cur ^ 1][0], tid);
+        b.store(smem[cur ^ 1][1], tid);
+        fetch(min(j + 2, nt - 1));
+        lds_barrier();
+    }
+}
+
+// A wide partial tile in lane order: group q = 16s + 8i + 4j + r4 holds elements 4·r4 … 4·r4 + 3 of
+// acc[s][i][j], [q][thread][4].
+__device__ __forceinline__ void write_partial_w(float* slot, const f32x16 (&acc)[2][2][2]) {
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+        const int s = q >> 4, i = (q >> 3) & 1, j = (q >> 2) & 1, r = (q & 3) * 4;
+        *reinterpret_cast<f32x4*>(slot + (q * WT_THREADS + threadIdx.x) * 4) =
+            f32x4{acc[s][i][j][r], acc[s][i][j][r + 1], acc[s][i][j][r + 2], acc[s][i][j][r + 3]};
+    }
+}
+
+// nn and tn carry wide tile counts (tiles_m, tiles_n of 256 x 256 tiles); s counts 16-deep units.
+__global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParams nn, GemmParams tn, PairPlan s) {
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];
+    const int g = xcd_logical_block();
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, half = lane >> 5, kh = (lane >> 5) << 2;
+    const int count = s.q + (g < s.r ? 1 : 0);
+    for (int n = 0; n < count; ++n) {
+        const int t = g + n * s.G, tm = t / nn.tiles_n;
+        TileCoord c;
+        c.split = 0;
+        c.t = t;
+        c.m0 = tm * WT;
+        c.n0 = (t - tm * nn.tiles_n) * WT;
+        c.kb = 0;
+        c.ke = nn.K;
+        OperandWK a(nn.A, nn.lda, c.m0, nn.M, tid);
+        OperandWS b(nn.B, nn.ldb, c.n0, nn.N, tid);
+        f32x16 acc[2][2][2];
+        wide_mma(a, b, 0, nn.K, t, smem, acc, tid, wm, wn, lr, half);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            TileCoord cs = c;
+            cs.m0 = c.m0 + 128 * h;
+            if (cs.m0 >= nn.M) break;
+            if (cs.m0 + 128 <= nn.M && c.n0 + WT <= nn.N)
+                store_acc<true, true, STORE, false, false, true>(nn, cs, acc[h], wm, wn, lr, kh);
+            else
+                store_acc<true, true, STORE, false, true, true>(nn, cs, acc[h], wm, wn, lr, kh);
+        }
+    }
+    const int lo = plan_tn_lo(s, g), hi = plan_tn_lo(s, g + 1);
+    for (int u = lo; u < hi;) {
+        const int t = u / s.tn_units;
+        const int a0 = u - t * s.tn_units;
+        const int b0 = min(s.tn_units, a0 + (hi - u));
+        const int tm = t / tn.tiles_n;
+        const int m0 = tm * WT, n0 = (t - tm * tn.tiles_n) * WT;
+        OperandWS a(tn.A, tn.lda, m0, tn.M, tid);
+        OperandWS b(tn.B, tn.ldb, n0, tn.N, tid);
+        f32x16 acc[2][2][2];
+        wide_mma(a, b, a0 * BKQ, min(tn.K, b0 * BKQ), g, smem, acc, tid, wm, wn, lr, half);
+        write_partial_w(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (WT * WT), acc);
+        u += b0 - a0;
+    }
+}
+
+// dW += the partials of the workers that shared each wide dW tile, summed in worker order. Block (t, q)
+// takes group q of tile t: each thread sums its float4 of that group over the covering workers.
+__global__ __launch_bounds__(WT_THREADS) void pair_fixup_w_kernel(GemmParams tn, PairPlan s) {
+    const int t = blockIdx.x, q = blockIdx.y;
+    const int a = t * s.tn_units, b = a + s.tn_units;
+    __shared__ int run_lo[FIXUP_MAX_WORKERS + 1];
+    for (int g = threadIdx.x; g <= s.G; g += WT_THREADS) run_lo[g] = plan_tn_lo(s, g);
+    __syncthreads();
+    int lo = 0, hi = s.G - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (run_lo[mid + 1] > a) hi = mid; else lo = mid + 1;
+    }
+    const int tid = threadIdx.x;
+    const long off = (long)q * WT_THREADS + tid;
+    f32x4 sum = f32x4{0, 0, 0, 0};
+    for (int g = lo; g < s.G && run_lo[g] < b; ++g) {
+        const int glo = run_lo[g], ghi = run_lo[g + 1];
+        if (ghi <= glo || ghi <= a) continue;
+        const int slot = g * 2 + (glo / s.tn_units == t ? 0 : 1);
+        sum += reinterpret_cast<const f32x4*>(s.partial + (long)slot * (WT * WT))[off];
+    }
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, kh = (lane >> 5) << 2;
+    const int sq = q >> 4, i = (q >> 3) & 1, j = (q >> 2) & 1, r4 = q & 3;
+    const int tm = t / tn.tiles_n;
+    const int row0 = tm * WT + 128 * sq + wm * 64 + 32 * i + 8 * r4 + kh;
+    const int col = (t - tm * tn.tiles_n) * WT + wn * 64 + 32 * j + lr;
+    if (col >= tn.N) return;
+    float cur[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) cur[e] = row0 + e < tn.M ? tn.C[(long)(row0 + e) * tn.ldc + col] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        if (row0 + e < tn.M) tn.C[(long)(row0 + e) * tn.ldc + col] = cur[e] + sum[e];
+}
+
 // Adds the partials of the workers that shared a dW tile, in worker order, into dW. Eight workgroups
 // per tile (blockIdx.y = 4i + r/4): each thread sums the two float4 groups (j = 0, 1) of its lanes'
 // accumulator rows and adds them to dW as four column pairs, in the layout `store_acc` uses.
@@ -1682,6 +1860,60 @@ bool make_pair_plan(const laya_ctx* ctx, int n0, int out, int n1, int rows, Pair
            s.G <= FIXUP_MAX_WORKERS;
 }
 
+// The same schedule over one worker per CU, 256 x 256 tiles and 16-deep units (the wide pair).
+bool make_pair_plan_wide(const laya_ctx* ctx, int n0, int out, int n1, int rows, PairPlan& s) {
+    s = PairPlan{};
+    s.G = ctx->cu_count;
+    s.nn_tiles = n0;
+    s.nn_units = (out + BKQ - 1) / BKQ;
+    s.tn_tiles = n1;
+    s.tn_units = (rows + BKQ - 1) / BKQ;
+    s.q = n0 / s.G;
+    s.r = n0 % s.G;
+    const long W = (long)n0 * s.nn_units + (long)n1 * s.tn_units;
+    s.W = (int)std::min<long>(W, 1L << 30);
+    const long need_min = W / s.G - (long)(s.q + (s.r > 0 ? 1 : 0)) * s.nn_units;
+    const long max_run = (W + s.G - 1) / s.G - (long)s.q * s.nn_units;
+    return need_min >= 0 && s.nn_units > 0 && W * s.G < (1L << 31) && max_run < s.tn_units &&
+           s.G <= FIXUP_MAX_WORKERS;
+}
+
+// The wide pair for split products: dX without residual, dX's K a multiple of 16, dY k-contiguous in
+// float4s. Returns false (nothing launched) when the wide plan does not apply.
+bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out) {
+    if (nn.R || out % BKQ != 0 || !operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) return false;
+    nn.tiles_m = (rows + WT - 1) / WT;
+    nn.tiles_n = (in + WT - 1) / WT;
+    tn.tiles_m = (out + WT - 1) / WT;
+    tn.tiles_n = (in + WT - 1) / WT;
+    const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
+    PairPlan s{};
+    if (!make_pair_plan_wide(ctx, n0, out, n1, rows, s)) return false;
+    s.partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)s.G * 2 * WT * WT));
+    {
+        ProfileScope scope(ctx, "gemm_bwd_pair_x6", 2.0 * 2.0 * rows * (double)in * out, 0.0);
+        hipLaunchKernelGGL(gemm_pair_wide_kernel, dim3(s.G), dim3(WT_THREADS), 0, ctx->stream, nn, tn, s);
+        check_launch("gemm_pair_wide_kernel");
+    }
+    long partials = 0, shared = 0;
+    const long Wt = (long)n0 * s.nn_units + (long)n1 * s.tn_units;
+    auto tn_lo = [&](long g) { return g * Wt / s.G - (long)s.nn_units * (g * s.q + std::min<long>(g, s.r)); };
+    for (int g = 0; ctx->profiling && g < s.G; ++g) {
+        const long lo = tn_lo(g), hi = tn_lo(g + 1);
+        for (long u = lo; u < hi;) {
+            const long t = u / s.tn_units, a = u - t * s.tn_units;
+            const long b = std::min<long>(s.tn_units, a + (hi - u));
+            ++partials;
+            if (a == 0) ++shared;
+            u += b - a;
+        }
+    }
+    ProfileScope scope(ctx, "gemm_pair_fixup", 0.0, 4.0 * WT * WT * (double)(partials + 2 * shared));
+    hipLaunchKernelGGL(pair_fixup_w_kernel, dim3(n1, 32), dim3(WT_THREADS), 0, ctx->stream, tn, s);
+    check_launch("pair_fixup_w_kernel");
+    return true;
+}
+
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
                         float* dx, const float* dx_residual, float* dW) {
     if (rows == 0) return;
@@ -1695,6 +1927,9 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
     const bool fp32 = !((ctx->matmul_bf16 | ctx->matmul_split) & 6) && gemm_fast(nn, true, false) &&
                       gemm_fast(tn, false, false);
     const bool half = (ctx->matmul_bf16 & 6) == 6 && gemm_fits_h(nn, true, false) && gemm_fits_h(tn, false, false);
+    tn.mode = ACCUMULATE;
+    if (split && backward_pair_wide(ctx, nn, tn, rows, in, out)) return;
+    tn.mode = STORE;
     const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
     PairPlan s{};
     if ((split || fp32 || half) && make_pair_plan(ctx, n0, out, n1, rows, s)) {
