@@ -809,19 +809,27 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// A 256-row operand's 16-deep stage: thread t holds 4 consecutive k of rows t/4 and t/4 + 128.
+// Raw buffer descriptor over `bytes` bytes of p (offsets are 32-bit; the host keeps operands under 2³¹ B).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* p, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, (int)bytes, 0x00020000);
+}
+
+// A 256-row k-contiguous operand's 16-deep stage: thread t holds 4 consecutive k of rows t/4 and t/4 + 128.
+// Buffer loads: the per-thread row offset in a VGPR, the stage's k offset in the wave-uniform SGPR offset.
 struct OperandW {
-    const float* src;
+    __amdgpu_buffer_rsrc_t rsrc;
     unsigned off[2];
     f32x4 reg[2];
-    __device__ __forceinline__ OperandW(const float* s, long ldl, int mn0, int MN, int tid) : src(s) {
+    __device__ __forceinline__ OperandW(const float* s, long ldl, int mn0, int MN, int tid, unsigned bytes)
+        : rsrc(buffer_of(s, bytes)) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            off[i] = (unsigned)min(mn0 + (tid >> 2) + 128 * i, MN - 1) * (unsigned)ldl + ((tid & 3) << 2);
+            off[i] = ((unsigned)min(mn0 + (tid >> 2) + 128 * i, MN - 1) * (unsigned)ldl + ((tid & 3) << 2)) * 4u;
     }
     __device__ __forceinline__ void full(int k0) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) reg[i] = *reinterpret_cast<const f32x4*>(src + off[i] + (unsigned)k0);
+        for (int i = 0; i < 2; ++i)
+            reg[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[i], k0 * 4, 0));
     }
     __device__ __forceinline__ void store(__bf16* lds, int tid) const {
 #pragma unroll
@@ -889,8 +897,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3;
     const int lr = lane & 31, half = lane >> 5;
-    OperandW a(p.A, p.lda, c.m0, p.M, tid);
-    OperandW b(p.B, p.ldb, c.n0, p.N, tid);
+    OperandW a(p.A, p.lda, c.m0, p.M, tid, (unsigned)(p.M * p.lda * 4));
+    OperandW b(p.B, p.ldb, c.n0, p.N, tid, (unsigned)(p.N * p.ldb * 4));
     auto kof = [&](int j) {
         const int q = j + rot;
         return (q >= nt ? q - nt : q) * BKQ;
@@ -1105,23 +1113,28 @@ __global__ __launch_bounds__(THREADS, 2) void gemm_pair_planned_h_kernel(GemmPar
 // whole dX tiles, then a contiguous run of 16-deep dW units whose partial tiles the wide fixup adds.
 
 // A 256-wide mn-contiguous operand's 16-deep stage (element (mn, k) at src[k·ld + mn]): thread t holds
-// mn = t mod 256 at 8 consecutive k. Positions at or past a ragged K end read an in-bounds row and become 0.
+// mn = t mod 256 at 8 consecutive k. Full stages are buffer loads whose k row offsets are wave-uniform
+// SGPR offsets; in the ragged last stage positions at or past kend read an in-bounds row and become 0.
 struct OperandWS {
-    const float* src;
-    unsigned base, ld;
+    __amdgpu_buffer_rsrc_t rsrc;
+    unsigned base, ld4;
     int kq;
     float v[8];
-    __device__ __forceinline__ OperandWS(const float* s, long ldl, int mn0, int MN, int tid)
-        : src(s), base((unsigned)min(mn0 + (tid & 255), MN - 1)), ld((unsigned)ldl), kq((tid >> 8) << 3) {}
+    __device__ __forceinline__ OperandWS(const float* s, long ldl, int mn0, int MN, int tid, unsigned bytes)
+        : rsrc(buffer_of(s, bytes)), base((unsigned)min(mn0 + (tid & 255), MN - 1) * 4u),
+          ld4((unsigned)ldl * 4u), kq((tid >> 8) << 3) {}
     __device__ __forceinline__ void full(int k0) {
+        const unsigned o = base + (unsigned)(k0 + kq) * ld4;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = src[base + (unsigned)(k0 + kq + e) * ld];
+        for (int e = 0; e < 8; ++e)
+            v[e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, o, (int)(e * ld4), 0));
     }
     __device__ __forceinline__ void tail(int k0, int kend) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int k = k0 + kq + e;
-            const float x = src[base + (unsigned)min(k, kend - 1) * ld];
+            const float x = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, base + (unsigned)min(k, kend - 1) * ld4, 0, 0));
             v[e] = k < kend ? x : 0.0f;
         }
     }
@@ -1143,23 +1156,19 @@ struct OperandWK : OperandW {
     __device__ __forceinline__ void tail(int k0, int) { full(k0); }
 };
 
-// acc += A·Bᵀ over K positions [kb, ke) in 16-deep stages (the last one ragged when ke − kb is not a
-// multiple of 16), full stages in rotated order starting at `rot`.
+// acc += A·Bᵀ over K positions [kb, ke) in 16-deep stages: the full stages in rotated order starting at
+// `rot`, then the ragged last one (when ke − kb is not a multiple of 16) on its own, so the loop body
+// carries no per-element selects.
 template <class OA, class OB>
 __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, __bf16 (*smem)[2][3 * STAGE_W],
                                          f32x16 (&acc)[2][2][2], int tid, int wm, int wn, int lr, int half) {
-    const int len = ke - kb, nfull = len / BKQ, nt = nfull + (len % BKQ != 0 ? 1 : 0);
+    const int len = ke - kb, nfull = len / BKQ;
     rot = nfull > 0 ? rot % nfull : 0;
     auto fetch = [&](int j) {
-        if (j < nfull) {
-            const int q = j + rot;
-            const int k0 = kb + (q >= nfull ? q - nfull : q) * BKQ;
-            a.full(k0);
-            b.full(k0);
-        } else {
-            a.tail(kb + nfull * BKQ, ke);
-            b.tail(kb + nfull * BKQ, ke);
-        }
+        const int q = j + rot;
+        const int k0 = kb + (q >= nfull ? q - nfull : q) * BKQ;
+        a.full(k0);
+        b.full(k0);
     };
 #pragma unroll
     for (int s = 0; s < 2; ++s)
@@ -1167,17 +1176,28 @@ __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, 
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) acc[s][i][j] = f32x16{};
-    fetch(0);
-    a.store(smem[0][0], tid);
-    b.store(smem[0][1], tid);
-    fetch(min(1, nt - 1));
-    lds_barrier();
-    for (int j = 0; j < nt; ++j) {
-        const int cur = j & 1;
-        mma_stage_w(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
-        a.store(smem[cur ^ 1][0], tid);
-        b.store(smem[cur ^ 1][1], tid);
-        fetch(min(j + 2, nt - 1));
+    if (nfull > 0) {
+        fetch(0);
+        a.store(smem[0][0], tid);
+        b.store(smem[0][1], tid);
+        fetch(min(1, nfull - 1));
+        lds_barrier();
+        for (int j = 0; j < nfull; ++j) {
+            const int cur = j & 1;
+            mma_stage_w(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
+            a.store(smem[cur ^ 1][0], tid);
+            b.store(smem[cur ^ 1][1], tid);
+            fetch(min(j + 2, nfull - 1));
+            lds_barrier();
+        }
+    }
+    if (len % BKQ != 0) {
+        a.tail(kb + nfull * BKQ, ke);
+        b.tail(kb + nfull * BKQ, ke);
+        a.store(smem[0][0], tid);
+        b.store(smem[0][1], tid);
+        lds_barrier();
+        mma_stage_w(smem[0][0], smem[0][1], acc, wm, wn, lr, half);
         lds_barrier();
     }
 }
@@ -1209,8 +1229,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         c.n0 = (t - tm * nn.tiles_n) * WT;
         c.kb = 0;
         c.ke = nn.K;
-        OperandWK a(nn.A, nn.lda, c.m0, nn.M, tid);
-        OperandWS b(nn.B, nn.ldb, c.n0, nn.N, tid);
+        OperandWK a(nn.A, nn.lda, c.m0, nn.M, tid, (unsigned)(nn.M * nn.lda * 4));
+        OperandWS b(nn.B, nn.ldb, c.n0, nn.N, tid, (unsigned)(nn.K * nn.ldb * 4));
         f32x16 acc[2][2][2];
         wide_mma(a, b, 0, nn.K, t, smem, acc, tid, wm, wn, lr, half);
 #pragma unroll
@@ -1231,8 +1251,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         const int b0 = min(s.tn_units, a0 + (hi - u));
         const int tm = t / tn.tiles_n;
         const int m0 = tm * WT, n0 = (t - tm * tn.tiles_n) * WT;
-        OperandWS a(tn.A, tn.lda, m0, tn.M, tid);
-        OperandWS b(tn.B, tn.ldb, n0, tn.N, tid);
+        OperandWS a(tn.A, tn.lda, m0, tn.M, tid, (unsigned)(tn.K * tn.lda * 4));
+        OperandWS b(tn.B, tn.ldb, n0, tn.N, tid, (unsigned)(tn.K * tn.ldb * 4));
         f32x16 acc[2][2][2];
         wide_mma(a, b, a0 * BKQ, min(tn.K, b0 * BKQ), g, smem, acc, tid, wm, wn, lr, half);
         write_partial_w(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (WT * WT), acc);
@@ -1590,6 +1610,7 @@ bool three_per_cu(const laya_ctx* ctx, int blocks) {
 bool wide_tiles_pay(const laya_ctx* ctx, const GemmParams& p, bool three) {
     if (p.mode != STORE && p.mode != STORE_ROPE) return false;
     if (p.R || p.K <= 0 || p.K % BKQ != 0 || p.splits != 1) return false;
+    if ((long)p.M * p.lda * 4 >= (1L << 31) || (long)p.N * p.ldb * 4 >= (1L << 31)) return false;  // buffer offsets
     const long cu = ctx->cu_count;
     const long wide = (long)((p.M + WT - 1) / WT) * ((p.N + WT - 1) / WT);
     const long tiles = (long)p.tiles_m * p.tiles_n;
@@ -1882,6 +1903,8 @@ bool make_pair_plan_wide(const laya_ctx* ctx, int n0, int out, int n1, int rows,
 // float4s. Returns false (nothing launched) when the wide plan does not apply.
 bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out) {
     if (nn.R || out % BKQ != 0 || !operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) return false;
+    const long lim = 1L << 31;  // buffer offsets of dY, W and x
+    if ((long)rows * out * 4 >= lim || (long)out * in * 4 >= lim || (long)rows * in * 4 >= lim) return false;
     nn.tiles_m = (rows + WT - 1) / WT;
     nn.tiles_n = (in + WT - 1) / WT;
     tn.tiles_m = (out + WT - 1) / WT;
