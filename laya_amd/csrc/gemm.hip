@@ -1275,12 +1275,24 @@ __global__ __launch_bounds__(WT_THREADS) void pair_fixup_w_kernel(GemmParams tn,
     }
     const int tid = threadIdx.x;
     const long off = (long)q * WT_THREADS + tid;
+    // Up to eight partials in flight at a time; the sum order stays the worker order.
     f32x4 sum = f32x4{0, 0, 0, 0};
-    for (int g = lo; g < s.G && run_lo[g] < b; ++g) {
-        const int glo = run_lo[g], ghi = run_lo[g + 1];
-        if (ghi <= glo || ghi <= a) continue;
-        const int slot = g * 2 + (glo / s.tn_units == t ? 0 : 1);
-        sum += reinterpret_cast<const f32x4*>(s.partial + (long)slot * (WT * WT))[off];
+    int g = lo;
+    while (g < s.G && run_lo[g] < b) {
+        int slots[8];
+        int n = 0;
+        for (; g < s.G && run_lo[g] < b && n < 8; ++g) {
+            const int glo = run_lo[g], ghi = run_lo[g + 1];
+            if (ghi <= glo || ghi <= a) continue;
+            slots[n++] = g * 2 + (glo / s.tn_units == t ? 0 : 1);
+        }
+        f32x4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k < n) v[k] = reinterpret_cast<const f32x4*>(s.partial + (long)slots[k] * (WT * WT))[off];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (k < n) sum += v[k];
     }
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, kh = (lane >> 5) << 2;
