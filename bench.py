@@ -43,7 +43,7 @@ MFMA_KERNELS = ("gemm_nt", "gemm_nn", "gemm_tn", "gemm_bwd_pair", "attention_fwd
 # profiles/gemm_bwd_pair_x6_hbm_traffic_b32x512.md). Counters cannot be read from inside the process, so the
 # figure is carried here per (workload, kernel) it was measured on and is reported only when that kernel
 # is the dominant one of that workload; any other case reports null.
-MEASURED_TRAFFIC = {("b32x512", "gemm_bwd_pair_x6"): 1.756e9}
+MEASURED_TRAFFIC = {("b32x512", "gemm_bwd_pair_x6"): 0.967e9}
 
 
 PEAK_BF16_MFMA = 2.5e15
