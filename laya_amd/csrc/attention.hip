@@ -366,6 +366,37 @@ __device__ __forceinline__ void commit_cols(const RowStage<R>& st, __bf16* plane
     }
 }
 
+// Both layouts of one staged tile (as commit_rows then commit_cols) from one split of each value: the
+// [d][row] pieces are the [row][d] pieces regrouped, since the split is elementwise.
+template <int R>
+__device__ __forceinline__ void commit_both(const RowStage<R>& st, __bf16* rows, __bf16* cols) {
+    constexpr int N = RowStage<R>::N, TS = tsh<R>();
+    const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
+    bf16x4 h[N][3];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        split3_4(st.v[i], h[i][0], h[i][1], h[i][2]);
+        __bf16* o = rows + (N * q + i) * KSH + j;
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) *reinterpret_cast<bf16x4*>(o + pl * R * KSH) = h[i][pl];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        __bf16* o = cols + (j + e) * TS + N * q;
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl) {
+            if constexpr (N == 4) {
+                *reinterpret_cast<bf16x4*>(o + pl * 64 * TS) =
+                    bf16x4{h[0][pl][e], h[1][pl][e], h[2][pl][e], h[3][pl][e]};
+            } else {
+                static_assert(N == 2, "tiles of 64 or 32 rows");
+                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+                *reinterpret_cast<bf16x2*>(o + pl * 64 * TS) = bf16x2{h[0][pl][e], h[1][pl][e]};
+            }
+        }
+    }
+}
+
 // The lane's own row (d = 16s + 8h … +7 for s < 4), split.
 __device__ __forceinline__ void split_lane_row(const float* src, bool valid, int h, bf16x8 (&out)[4][3]) {
 #pragma unroll
@@ -844,10 +875,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                 lse_s[threadIdx.x] = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
                 dot_s[threadIdx.x] = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
             }
-            commit_rows<BT>(qst, Qh);
-            commit_cols<BT>(qst, Qt);
-            commit_rows<BT>(ost, Oh);
-            commit_cols<BT>(ost, Ot);
+            commit_both<BT>(qst, Qh, Qt);
+            commit_both<BT>(ost, Oh, Ot);
         }
         __syncthreads();
         // Wave-uniform: outside this wave's window, or a wave whose keys all lie past the segment end.
@@ -974,8 +1003,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     fetch_rows<BT>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += BT) {
         __syncthreads();
-        commit_rows<BT>(kst, Kh);
-        commit_cols<BT>(kst, Kt);
+        commit_both<BT>(kst, Kh, Kt);
         commit_rows<BT>(vst, Vh);
         __syncthreads();
         if (kt0 + BT < kend) {  // block-uniform
