@@ -94,6 +94,27 @@ def test_linear_forward_on_wide_tiles(ctx, rows, inn, out, with_bias):
     assert rel_l2(y_ref, y_.numpy()) < 1e-6
 
 
+def test_wide_tile_products_are_bitwise_deterministic(ctx):
+    """The 256 x 256 forward tiles and the wide backward pair (whose dW tiles several workers share, summed
+    by the fixup in worker order) give the same bits on every call."""
+    rows, inn, out = 13871, 768, 2304
+    print(f"wide tiles twice: rows={rows} in={inn} out={out}", flush=True)
+    rng = np.random.default_rng(5)
+    x = dev(ctx, rng.standard_normal((rows, inn)).astype(np.float32))
+    dy = dev(ctx, rng.standard_normal((rows, out)).astype(np.float32))
+    W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+    results = []
+    for _ in range(2):
+        w = param(ctx, "w", W)
+        y = dev(ctx, np.zeros((rows, out), np.float32))
+        dx = dev(ctx, np.zeros((rows, inn), np.float32))
+        laya.linear(w, None, x, rows, y)
+        laya.linear_backward(w, None, x, dy, rows, dx)
+        results.append((y.numpy(), dx.numpy(), w.gradient.numpy()))
+    for a, b in zip(*results):
+        assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("rows,inn,out,with_bias", [(512, 768, 768, True), (200, 2304, 768, False)])
 def test_linear_in_place_residual_with_split_k(ctx, rows, inn, out, with_bias):
     """y = x·Wᵀ + b + y with the residual being the output itself, on grids small enough (24 and 12 tiles)
