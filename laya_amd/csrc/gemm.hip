@@ -1261,40 +1261,50 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
 }
 
 // dW += the partials of the workers that shared each wide dW tile, summed in worker order. Block (t, q)
-// takes group q of tile t: each thread sums its float4 of that group over the covering workers.
+// takes group q of tile t. The block first lists the covering workers' slots in worker order (one thread
+// per worker, an ordered compaction by wave ballots), then each thread sums its float4 of that group over
+// the list, sixteen loads in flight at a time.
 __global__ __launch_bounds__(WT_THREADS) void pair_fixup_w_kernel(GemmParams tn, PairPlan s) {
     const int t = blockIdx.x, q = blockIdx.y;
     const int a = t * s.tn_units, b = a + s.tn_units;
     __shared__ int run_lo[FIXUP_MAX_WORKERS + 1];
-    for (int g = threadIdx.x; g <= s.G; g += WT_THREADS) run_lo[g] = plan_tn_lo(s, g);
+    __shared__ int slots[FIXUP_MAX_WORKERS];
+    __shared__ int wave_count[WT_THREADS / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int g = tid; g <= s.G; g += WT_THREADS) run_lo[g] = plan_tn_lo(s, g);
     __syncthreads();
-    int lo = 0, hi = s.G - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (run_lo[mid + 1] > a) hi = mid; else lo = mid + 1;
-    }
-    const int tid = threadIdx.x;
-    const long off = (long)q * WT_THREADS + tid;
-    // Up to eight partials in flight at a time; the sum order stays the worker order.
-    f32x4 sum = f32x4{0, 0, 0, 0};
-    int g = lo;
-    while (g < s.G && run_lo[g] < b) {
-        int slots[8];
-        int n = 0;
-        for (; g < s.G && run_lo[g] < b && n < 8; ++g) {
+    int base = 0;
+    for (int g0 = 0; g0 < s.G; g0 += WT_THREADS) {
+        const int g = g0 + tid;
+        bool covers = false;
+        int slot = 0;
+        if (g < s.G) {
             const int glo = run_lo[g], ghi = run_lo[g + 1];
-            if (ghi <= glo || ghi <= a) continue;
-            slots[n++] = g * 2 + (glo / s.tn_units == t ? 0 : 1);
+            covers = ghi > glo && glo < b && ghi > a;
+            slot = g * 2 + (glo / s.tn_units == t ? 0 : 1);
         }
-        f32x4 v[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (k < n) v[k] = reinterpret_cast<const f32x4*>(s.partial + (long)slots[k] * (WT * WT))[off];
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-            if (k < n) sum += v[k];
+        const unsigned long long mask = __ballot(covers);
+        const int before = __popcll(mask & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_count[wave] = __popcll(mask);
+        __syncthreads();
+        int offset = base;
+        for (int w = 0; w < wave; ++w) offset += wave_count[w];
+        if (covers) slots[offset + before] = slot;
+        for (int w = 0; w < WT_THREADS / 64; ++w) base += wave_count[w];
+        __syncthreads();
     }
-    const int lane = tid & 63, wave = tid >> 6;
+    const int n = base;
+    const long off = (long)q * WT_THREADS + tid;
+    f32x4 sum = f32x4{0, 0, 0, 0};
+    for (int k0 = 0; k0 < n; k0 += 16) {
+        f32x4 v[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (k0 + k < n) v[k] = reinterpret_cast<const f32x4*>(s.partial + (long)slots[k0 + k] * (WT * WT))[off];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (k0 + k < n) sum += v[k];
+    }
     const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, kh = (lane >> 5) << 2;
     const int sq = q >> 4, i = (q >> 3) & 1, j = (q >> 2) & 1, r4 = q & 3;
     const int tm = t / tn.tiles_n;
