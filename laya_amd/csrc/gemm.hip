@@ -831,15 +831,21 @@ struct OperandW {
         for (int i = 0; i < 2; ++i)
             reg[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[i], k0 * 4, 0));
     }
+    // NP = 3: the three split planes; NP = 1: one plane of the values rounded to bf16.
+    template <int NP = 3>
     __device__ __forceinline__ void store(__bf16* lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            bf16x4 h1, h2, h3;
-            split3_4(reg[i], h1, h2, h3);
             const int o = ((tid >> 2) + 128 * i) * KPADQ + ((tid & 3) << 2);
-            *reinterpret_cast<bf16x4*>(lds + o) = h1;
-            *reinterpret_cast<bf16x4*>(lds + STAGE_W + o) = h2;
-            *reinterpret_cast<bf16x4*>(lds + 2 * STAGE_W + o) = h3;
+            if constexpr (NP == 3) {
+                bf16x4 h1, h2, h3;
+                split3_4(reg[i], h1, h2, h3);
+                *reinterpret_cast<bf16x4*>(lds + o) = h1;
+                *reinterpret_cast<bf16x4*>(lds + STAGE_W + o) = h2;
+                *reinterpret_cast<bf16x4*>(lds + 2 * STAGE_W + o) = h3;
+            } else {
+                *reinterpret_cast<bf16x4*>(lds + o) = __builtin_convertvector(reg[i], bf16x4);
+            }
         }
     }
 };
@@ -856,26 +862,34 @@ __device__ __forceinline__ void mma6(const bf16x8 (&a)[3], const bf16x8 (&b)[3],
 }
 
 // One 16-deep stage of a wave's two subtiles: B fragments once, A fragments one 32-row group ahead.
+// NP = 3: six piece products per block (split products); NP = 1: one bf16 product.
+template <int NP = 3>
 __device__ __forceinline__ void mma_stage_w(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2][2], int wm, int wn,
                                             int lr, int half) {
     bf16x8 b[2][3], a[2][3];
     auto rd_a = [&](int g, bf16x8 (&dst)[3]) {
         const int row = 128 * (g >> 1) + wm * 64 + 32 * (g & 1) + lr;
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
+        for (int pl = 0; pl < NP; ++pl)
             dst[pl] = *reinterpret_cast<const bf16x8*>(A + pl * STAGE_W + row * KPADQ + 8 * half);
     };
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int pl = 0; pl < 3; ++pl)
+        for (int pl = 0; pl < NP; ++pl)
             b[j][pl] = *reinterpret_cast<const bf16x8*>(B + pl * STAGE_W + (wn * 64 + 32 * j + lr) * KPADQ + 8 * half);
     rd_a(0, a[0]);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         if (g + 1 < 4) rd_a(g + 1, a[(g + 1) & 1]);
-        mma6(a[g & 1], b[0], acc[g >> 1][g & 1][0]);
-        mma6(a[g & 1], b[1], acc[g >> 1][g & 1][1]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if constexpr (NP == 3)
+                mma6(a[g & 1], b[j], acc[g >> 1][g & 1][j]);
+            else
+                acc[g >> 1][g & 1][j] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[g & 1][0], b[j][0], acc[g >> 1][g & 1][j], 0, 0, 0);
+        }
     }
 }
 
@@ -1138,14 +1152,21 @@ struct OperandWS {
             v[e] = k < kend ? x : 0.0f;
         }
     }
+    template <int NP = 3>
     __device__ __forceinline__ void store(__bf16* lds, int tid) const {
-        bf16x4 a1, a2, a3, b1, b2, b3;
-        split3_4(f32x4{v[0], v[1], v[2], v[3]}, a1, a2, a3);
-        split3_4(f32x4{v[4], v[5], v[6], v[7]}, b1, b2, b3);
         const int o = (tid & 255) * KPADQ + kq;
-        *reinterpret_cast<bf16x8*>(lds + o) = __builtin_shufflevector(a1, b1, 0, 1, 2, 3, 4, 5, 6, 7);
-        *reinterpret_cast<bf16x8*>(lds + STAGE_W + o) = __builtin_shufflevector(a2, b2, 0, 1, 2, 3, 4, 5, 6, 7);
-        *reinterpret_cast<bf16x8*>(lds + 2 * STAGE_W + o) = __builtin_shufflevector(a3, b3, 0, 1, 2, 3, 4, 5, 6, 7);
+        if constexpr (NP == 3) {
+            bf16x4 a1, a2, a3, b1, b2, b3;
+            split3_4(f32x4{v[0], v[1], v[2], v[3]}, a1, a2, a3);
+            split3_4(f32x4{v[4], v[5], v[6], v[7]}, b1, b2, b3);
+            *reinterpret_cast<bf16x8*>(lds + o) = __builtin_shufflevector(a1, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+            *reinterpret_cast<bf16x8*>(lds + STAGE_W + o) = __builtin_shufflevector(a2, b2, 0, 1, 2, 3, 4, 5, 6, 7);
+            *reinterpret_cast<bf16x8*>(lds + 2 * STAGE_W + o) = __builtin_shufflevector(a3, b3, 0, 1, 2, 3, 4, 5, 6, 7);
+        } else {
+            const bf16x4 lo = __builtin_convertvector((f32x4{v[0], v[1], v[2], v[3]}), bf16x4);
+            const bf16x4 hi = __builtin_convertvector((f32x4{v[4], v[5], v[6], v[7]}), bf16x4);
+            *reinterpret_cast<bf16x8*>(lds + o) = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
     }
 };
 
@@ -1159,7 +1180,7 @@ struct OperandWK : OperandW {
 // acc += A·Bᵀ over K positions [kb, ke) in 16-deep stages: the full stages in rotated order starting at
 // `rot`, then the ragged last one (when ke − kb is not a multiple of 16) on its own, so the loop body
 // carries no per-element selects.
-template <class OA, class OB>
+template <int NP, class OA, class OB>
 __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, __bf16 (*smem)[2][3 * STAGE_W],
                                          f32x16 (&acc)[2][2][2], int tid, int wm, int wn, int lr, int half) {
     const int len = ke - kb, nfull = len / BKQ;
@@ -1178,15 +1199,15 @@ __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, 
             for (int j = 0; j < 2; ++j) acc[s][i][j] = f32x16{};
     if (nfull > 0) {
         fetch(0);
-        a.store(smem[0][0], tid);
-        b.store(smem[0][1], tid);
+        a.template store<NP>(smem[0][0], tid);
+        b.template store<NP>(smem[0][1], tid);
         fetch(min(1, nfull - 1));
         lds_barrier();
         for (int j = 0; j < nfull; ++j) {
             const int cur = j & 1;
-            mma_stage_w(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
-            a.store(smem[cur ^ 1][0], tid);
-            b.store(smem[cur ^ 1][1], tid);
+            mma_stage_w<NP>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
+            a.template store<NP>(smem[cur ^ 1][0], tid);
+            b.template store<NP>(smem[cur ^ 1][1], tid);
             fetch(min(j + 2, nfull - 1));
             lds_barrier();
         }
@@ -1194,10 +1215,10 @@ __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, 
     if (len % BKQ != 0) {
         a.tail(kb + nfull * BKQ, ke);
         b.tail(kb + nfull * BKQ, ke);
-        a.store(smem[0][0], tid);
-        b.store(smem[0][1], tid);
+        a.template store<NP>(smem[0][0], tid);
+        b.template store<NP>(smem[0][1], tid);
         lds_barrier();
-        mma_stage_w(smem[0][0], smem[0][1], acc, wm, wn, lr, half);
+        mma_stage_w<NP>(smem[0][0], smem[0][1], acc, wm, wn, lr, half);
         lds_barrier();
     }
 }
@@ -1214,6 +1235,8 @@ __device__ __forceinline__ void write_partial_w(float* slot, const f32x16 (&acc)
 }
 
 // nn and tn carry wide tile counts (tiles_m, tiles_n of 256 x 256 tiles); s counts 16-deep units.
+// NP = 3: split products (fp32); NP = 1: bf16 products (the bf16 policies of both backward classes).
+template <int NP>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParams nn, GemmParams tn, PairPlan s) {
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];
     const int g = xcd_logical_block();
@@ -1232,7 +1255,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         OperandWK a(nn.A, nn.lda, c.m0, nn.M, tid, (unsigned)(nn.M * nn.lda * 4));
         OperandWS b(nn.B, nn.ldb, c.n0, nn.N, tid, (unsigned)(nn.K * nn.ldb * 4));
         f32x16 acc[2][2][2];
-        wide_mma(a, b, 0, nn.K, t, smem, acc, tid, wm, wn, lr, half);
+        wide_mma<NP>(a, b, 0, nn.K, t, smem, acc, tid, wm, wn, lr, half);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             TileCoord cs = c;
@@ -1254,7 +1277,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         OperandWS a(tn.A, tn.lda, m0, tn.M, tid, (unsigned)(tn.K * tn.lda * 4));
         OperandWS b(tn.B, tn.ldb, n0, tn.N, tid, (unsigned)(tn.K * tn.ldb * 4));
         f32x16 acc[2][2][2];
-        wide_mma(a, b, a0 * BKQ, min(tn.K, b0 * BKQ), g, smem, acc, tid, wm, wn, lr, half);
+        wide_mma<NP>(a, b, a0 * BKQ, min(tn.K, b0 * BKQ), g, smem, acc, tid, wm, wn, lr, half);
         write_partial_w(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (WT * WT), acc);
         u += b0 - a0;
     }
@@ -1923,7 +1946,7 @@ bool make_pair_plan_wide(const laya_ctx* ctx, int n0, int out, int n1, int rows,
 
 // The wide pair for split products: dX without residual, dX's K a multiple of 16, dY k-contiguous in
 // float4s. Returns false (nothing launched) when the wide plan does not apply.
-bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out) {
+bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out, bool half) {
     if (nn.R || out % BKQ != 0 || !operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) return false;
     const long lim = 1L << 31;  // buffer offsets of dY, W and x
     if ((long)rows * out * 4 >= lim || (long)out * in * 4 >= lim || (long)rows * in * 4 >= lim) return false;
@@ -1936,8 +1959,12 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
     if (!make_pair_plan_wide(ctx, n0, out, n1, rows, s)) return false;
     s.partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)s.G * 2 * WT * WT));
     {
-        ProfileScope scope(ctx, "gemm_bwd_pair_x6", 2.0 * 2.0 * rows * (double)in * out, 0.0);
-        hipLaunchKernelGGL(gemm_pair_wide_kernel, dim3(s.G), dim3(WT_THREADS), 0, ctx->stream, nn, tn, s);
+        ProfileScope scope(ctx, half ? "gemm_bwd_pair_bf16" : "gemm_bwd_pair_x6", 2.0 * 2.0 * rows * (double)in * out,
+                           0.0);
+        if (half)
+            hipLaunchKernelGGL(gemm_pair_wide_kernel<1>, dim3(s.G), dim3(WT_THREADS), 0, ctx->stream, nn, tn, s);
+        else
+            hipLaunchKernelGGL(gemm_pair_wide_kernel<3>, dim3(s.G), dim3(WT_THREADS), 0, ctx->stream, nn, tn, s);
         check_launch("gemm_pair_wide_kernel");
     }
     long partials = 0, shared = 0;
@@ -1973,7 +2000,7 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
                       gemm_fast(tn, false, false);
     const bool half = (ctx->matmul_bf16 & 6) == 6 && gemm_fits_h(nn, true, false) && gemm_fits_h(tn, false, false);
     tn.mode = ACCUMULATE;
-    if (split && backward_pair_wide(ctx, nn, tn, rows, in, out)) return;
+    if ((split || half) && backward_pair_wide(ctx, nn, tn, rows, in, out, half)) return;
     tn.mode = STORE;
     const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
     PairPlan s{};

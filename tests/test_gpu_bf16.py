@@ -38,7 +38,10 @@ def dev(ctx, a):
 
 
 @pytest.mark.parametrize("rows,inn,out", [(37, 96, 130), (333, 100, 260), (1000, 768, 2304), (2048, 1152, 768),
-                                          (4100, 64, 96), (9000, 768, 2304)])
+                                          (4100, 64, 96), (9000, 768, 2304),
+                                          # the backward pair on 256 x 256 tiles (ragged columns, ragged last
+                                          # dW unit; the model's shapes)
+                                          (11000, 1148, 768), (13871, 768, 2304)])
 def test_bf16_linear_is_the_product_of_rounded_operands(ctx, rows, inn, out):
     """Forward with bias and residual (NT), dx (NN) and dW accumulated twice (TN, split-K at 4100 and 9000
     rows), in bf16."""
