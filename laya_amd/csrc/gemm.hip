@@ -943,11 +943,20 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
         lds_barrier();
     }
     const int kh = (lane >> 5) << 2;
+    // The stages are done (the loop ended on a barrier): park the second subtile's accumulators in LDS,
+    // each thread in its own slots, so the first subtile's epilogue has their registers.
+    f32x16* park = reinterpret_cast<f32x16*>(&smem[0][0][0]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) park[q * WT_THREADS + tid] = acc[1][q >> 1][q & 1];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         TileCoord cs = c;
         cs.m0 = c.m0 + 128 * s;
         if (cs.m0 >= p.M) break;
+        if (s == 1) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[1][q >> 1][q & 1] = park[q * WT_THREADS + tid];
+        }
         if (cs.m0 + 128 <= p.M && c.n0 + WT <= p.N)
             store_acc<true, true, MODE, false, false, true>(p, cs, acc[s], wm, wn, lr, kh);
         else
