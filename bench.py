@@ -36,17 +36,46 @@ sys.path.insert(0, ROOT)
 METRIC = "fine-tune tokens/sec (fwd+bwd+AdamW), 1 MI355X; bwd MFMA util % & HBM GB/s"
 PEAK_FP32_MFMA = 157.3e12
 PEAK_HBM = 8.0e12
-MFMA_KERNELS = ("gemm_nt", "gemm_nn", "gemm_tn", "gemm_bwd_pair", "attention_fwd", "attention_bwd_dkv",
-                "attention_bwd_dq")
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and calibrated against a
 # copy-like kernel of known size (the commands and the calibration sit in
-# profiles/gemm_bwd_pair_x6_hbm_traffic_b32x512.md). Counters cannot be read from inside the process, so the
+# profiles/gemm_bwd_pair_x6w_hbm_traffic_b32x512.md). Counters cannot be read from inside the process, so the
 # figure is carried here per (workload, kernel) it was measured on and is reported only when that kernel
 # is the dominant one of that workload; any other case reports null.
-MEASURED_TRAFFIC = {("b32x512", "gemm_bwd_pair_x6"): 0.967e9}
+MEASURED_TRAFFIC = {("b32x512", "gemm_bwd_pair_x6w"): 0.967e9}
 
 
 PEAK_BF16_MFMA = 2.5e15
+
+
+def mfma_peaks(name: str):
+    """(peak in algorithmic fp32 flops/s, bf16-MFMA issues per algorithmic flop) of a matrix-core kernel.
+
+    Kernels named *_x6 / *_x6w compute fp32 products from exact three-piece bf16 splits: six bf16 MFMA
+    products per fp32 one, so their fp32-equivalent peak is the bf16 peak over six. *_bf16 / *_bf16w run
+    bf16 operands (one product each). The rest run the fp32 matrix cores."""
+    base = name[:-1] if name.endswith(("_x6w", "_bf16w")) else name
+    if base.endswith("_x6"):
+        return PEAK_BF16_MFMA / 6, 6.0
+    if base.endswith("_bf16"):
+        return PEAK_BF16_MFMA, 1.0
+    return PEAK_FP32_MFMA, 0.0
+
+
+def mfma_summary(prof: dict, names) -> dict:
+    """Algorithmic TFLOP/s of a group of kernels, its fraction of the group's fp32-equivalent peak, and
+    the fraction of the bf16 matrix-core pipe the hardware products keep busy (the same denominator for
+    GEMMs and attention)."""
+    ks = [(n, prof[n]) for n in names if n in prof and prof[n]["flops"]]
+    if not ks:
+        return {}
+    flops = sum(k["flops"] for _, k in ks)
+    sec = sum(k["ms"] for _, k in ks) / 1e3
+    peak_time = sum(k["flops"] / mfma_peaks(n)[0] for n, k in ks)
+    out = {"tflops": round(flops / sec / 1e12, 1), "frac_of_peak": round(peak_time / sec, 4)}
+    bf16_ops = sum(k["flops"] * mfma_peaks(n)[1] for n, k in ks)
+    if bf16_ops:
+        out["bf16_pipe_frac"] = round(bf16_ops / sec / PEAK_BF16_MFMA, 4)
+    return out
 
 # The workloads: batch shape, heads, loss scaling (summed CE multiplies the mean by the item count) and
 # the precision of the matrix products. b32x512 is the headline configuration.
@@ -223,46 +252,35 @@ def main():
         traffic = MEASURED_TRAFFIC.get((args.workload, name)) if matmul == w["matmul"] else None
         if k["flops"]:
             achieved = k["flops"] / k["launches"] / per_launch_s
-            # A split-product kernel issues six bf16 MFMA products per fp32 product: its fp32-equivalent peak
-            # is the bf16 peak over six.
-            peak = (PEAK_BF16_MFMA if name.endswith("_bf16") else PEAK_BF16_MFMA / 6 if name.endswith("_x6")
-                    else PEAK_FP32_MFMA)
+            peak, issue = mfma_peaks(name)
             roofline = {"bound": "mfma", "kernel": name, "achieved": round(achieved / 1e12, 2),
                         "peak": round(peak / 1e12, 1), "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                         "traffic": traffic, "avg_launch_ms": round(per_launch_s * 1e3, 4),
                         "launches": k["launches"]}
+            if issue:
+                roofline["bf16_pipe_frac"] = round(achieved * issue / PEAK_BF16_MFMA, 4)
         else:
             achieved = k["bytes"] / k["launches"] / per_launch_s
             roofline = {"bound": "hbm", "kernel": name, "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
                         "unit": "GB/s", "frac": round(achieved / PEAK_HBM, 4), "traffic": traffic,
                         "avg_launch_ms": round(per_launch_s * 1e3, 4), "launches": k["launches"]}
-        bwd = [prof[n] for n in ("gemm_nn", "gemm_tn", "gemm_bwd_pair") if n in prof]
-        if bwd:
-            f = sum(x["flops"] for x in bwd)
-            ms = sum(x["ms"] for x in bwd)
-            breakdown["bwd_gemm_mfma_util"] = round(f / (ms / 1e3) / PEAK_FP32_MFMA, 4)
-        bwdx = [prof[n] for n in ("gemm_bwd_pair_x6", "gemm_nn_x6", "gemm_tn_x6") if n in prof]
-        if bwdx:
-            f = sum(x["flops"] for x in bwdx)
-            ms = sum(x["ms"] for x in bwdx)
-            breakdown["bwd_gemm_tflops"] = round(f / (ms / 1e3) / 1e12, 1)
-            breakdown["bwd_gemm_bf16_mfma_util"] = round(6 * f / (ms / 1e3) / PEAK_BF16_MFMA, 4)
-        bwd16 = [prof[n] for n in ("gemm_nn_bf16", "gemm_tn_bf16") if n in prof]
-        if bwd16:
-            f = sum(x["flops"] for x in bwd16)
-            ms = sum(x["ms"] for x in bwd16)
-            breakdown["bwd_gemm_bf16_mfma_util"] = round(f / (ms / 1e3) / PEAK_BF16_MFMA, 4)
-            breakdown["bwd_gemm_bf16_tflops"] = round(f / (ms / 1e3) / 1e12, 1)
-        attn = [prof[n] for n in ("attention_bwd_dkv", "attention_bwd_dq") if n in prof]
-        if attn:
-            f = sum(x["flops"] for x in attn)
-            ms = sum(x["ms"] for x in attn)
-            breakdown["attention_bwd_mfma_util"] = round(f / (ms / 1e3) / PEAK_FP32_MFMA, 4)
+        groups = {
+            "bwd_gemm": [n for n in prof if n.startswith(("gemm_bwd_pair", "gemm_nn", "gemm_tn"))],
+            "fwd_gemm": [n for n in prof if n.startswith("gemm_nt")],
+            "attention_bwd": [n for n in prof if n.startswith(("attention_bwd_dkv", "attention_bwd_dq"))],
+            "attention_fwd": [n for n in prof if n.startswith("attention_fwd")],
+        }
+        for g, names in groups.items():
+            summ = mfma_summary(prof, names)
+            if summ:
+                breakdown[g] = summ
         ew = [prof[n] for n in ("layernorm_bwd", "geglu_bwd", "relu_dropout_bwd") if n in prof]
         if ew:
             b = sum(x["bytes"] for x in ew)
             ms = sum(x["ms"] for x in ew)
             breakdown["elementwise_bwd_hbm_gbs"] = round(b / (ms / 1e3) / 1e9, 1)
+        hbm = {n: round(x["bytes"] / (x["ms"] / 1e3) / 1e9, 1) for n, x in prof.items() if x["bytes"] and x["ms"]}
+        breakdown["hbm_gbs"] = dict(sorted(hbm.items(), key=lambda kv: -prof[kv[0]]["ms"])[:10])
         breakdown["kernel_share"] = {n: round(k["ms"] / total_ms, 4) for n, k in
                                      sorted(prof.items(), key=lambda kv: -kv[1]["ms"])[:8]}
 

@@ -12,7 +12,8 @@
  *  - Every function returns an int status (LAYA_OK = 0); laya_last_error() gives a thread-local
  *    message for the last failure on the calling thread.
  *  - Tensor arguments are DEVICE pointers (from laya_alloc) to row-major fp32 data unless noted;
- *    sizes are element counts. Segment tables are device int32 arrays.
+ *    sizes are element counts. Index tables (ids, rows, positions) are device int32 arrays; a segment
+ *    list is a laya_segments handle made from host arrays.
  *  - Calls are ordered on the context's single HIP stream and asynchronous until laya_sync().
  *    A context is not re-entrant; separate contexts are independent.
  *  - Results do not depend on launch configuration: no floating-point atomics; every reduction
@@ -39,6 +40,7 @@ extern "C" {
 
 typedef struct laya_ctx laya_ctx;
 typedef struct laya_rotary laya_rotary;
+typedef struct laya_segments laya_segments;
 typedef struct laya_model laya_model;
 
 const char* laya_last_error(void);
@@ -144,21 +146,28 @@ int laya_rotary_destroy(laya_ctx* ctx, laya_rotary* rot);
 /* Rotary.Apply (Ops.cs:489-503) on rows of [rows, head_dim] at positions pos[rows] (device int32). */
 int laya_rotary_apply(laya_ctx* ctx, const laya_rotary* rot, float* vec, int rows, const int* pos, int inverse);
 
+/* The segment list a batch's attention calls share (ModernBertEncoder.cs:30-33: Segment(Start, Length);
+ * TrainableDecisionModel.cs:254-264 builds it once per batch and passes it to every AttentionForward and
+ * AttentionBackward). start/length are HOST arrays [nseg]: they are validated, copied to the device once,
+ * and kept on the host so attention calls size their launches without reading the device back. */
+int laya_segments_create(laya_ctx* ctx, const int* start, const int* length, int nseg, laya_segments** out);
+int laya_segments_destroy(laya_ctx* ctx, laya_segments* segs);
+
 /* Ops.AttentionForward (Ops.cs:275-277, 329-366): multi-head attention per segment over qkv rows
  * [q | k | v] (head slice at head·d_h), RoPE with segment-local positions (rot NULL: none), window
  * [t − w, t + w] clipped to the segment (half_window < 0: none), softmax(scale·qkᵀ), prob-dropout p
- * with the counter RNG at index head<<42 | row<<21 | key (Ops.cs:318).
- * seg_start/seg_len: device int32 [nseg]; max_len ≥ every seg_len. lse [rows·heads] receives the
- * row log-sum-exp (base 2, of the scaled scores) the backward reuses. */
-int laya_attention_fwd(laya_ctx* ctx, const float* qkv, const int* seg_start, const int* seg_len, int nseg,
-                       int max_len, int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
-                       float p_drop, uint64_t seed, float* context, float* lse);
+ * with the counter RNG at index head<<42 | row<<21 | key (Ops.cs:318). lse [rows·heads] receives the
+ * row log-sum-exp (base 2, of the scaled scores) the backward can reuse. Asynchronous. */
+int laya_attention_fwd(laya_ctx* ctx, const float* qkv, const laya_segments* segs, int hidden, int heads, float scale,
+                       int half_window, const laya_rotary* rot, float p_drop, uint64_t seed, float* context,
+                       float* lse);
 /* Ops.AttentionBackward (Ops.cs:280-282, 368-438): dq, dk, dv WRITTEN (not added) into dqkv, with
- * inverse RoPE on dq and dk. Needs the forward's context and lse. */
-int laya_attention_bwd(laya_ctx* ctx, const float* qkv, const int* seg_start, const int* seg_len, int nseg,
-                       int max_len, int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
-                       float p_drop, uint64_t seed, const float* context, const float* lse, const float* dcontext,
-                       float* dqkv);
+ * inverse RoPE on dq and dk. context and lse from laya_attention_fwd, or both NULL (the reference's
+ * signature carries neither): the row statistics are then recomputed, as Ops.AttentionBackward
+ * recomputes each row's softmax (Ops.cs:390-394). Asynchronous. */
+int laya_attention_bwd(laya_ctx* ctx, const float* qkv, const laya_segments* segs, int hidden, int heads, float scale,
+                       int half_window, const laya_rotary* rot, float p_drop, uint64_t seed, const float* context,
+                       const float* lse, const float* dcontext, float* dqkv);
 
 /* Embedding gather (TrainableDecisionModel.cs:277-283): out[t] = E[ids[t]]; ids are checked on the
  * device: an id outside [0, vocab) writes zeros and sets *bad_count (device int32, may be NULL). */
@@ -195,8 +204,13 @@ int laya_rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets
 
 /* Gradients.ClipByGlobalNorm (AdamW.cs:103-130) over a flat arena: Σg² in double, in a fixed order.
  * Writes the norm (double) and the clip coefficient (float, 1 when not clipping) to device memory.
- * Sets LAYA_ERR_NOT_FINITE only through laya_grad_norm_status. */
+ * A NaN or infinite norm leaves the coefficient at 1, as the reference does (its `coefficient < 1`
+ * test is false for NaN), and raises the context's non-finite flag, which laya_grad_norm_status reads. */
 int laya_grad_norm(laya_ctx* ctx, const float* grads, size_t n, double max_norm, double* norm_out, float* coef_out);
+/* Synchronises and returns LAYA_ERR_NOT_FINITE when the last laya_grad_norm on the context met a NaN or
+ * infinite gradient, LAYA_OK otherwise (LAYA_ERR_STATE before any laya_grad_norm). The reference has no such
+ * check (AdamW.cs:122-128 lets a NaN norm through); this is the detection its callers lack. */
+int laya_grad_norm_status(laya_ctx* ctx);
 /* Multi-tensor AdamW (AdamW.cs:29-73) over a flat arena split into parameter groups:
  * element i of group g (ranges [begin[g], end[g])) uses lr[g]; g_i is scaled by *coef (device, may be
  * NULL = 1) as the clip does; zero_grads clears the gradient after it is read. */
@@ -248,8 +262,14 @@ int laya_model_set_head_dropout(laya_model* model, float p);
 int laya_model_forward(laya_model* model, const laya_batch* batch, int training, uint64_t seed, float* logits_host);
 /* Backward (TrainableDecisionModel.cs:479-549): dlogits_host has Σ n_options floats. */
 int laya_model_backward(laya_model* model, const float* dlogits_host);
-/* Gradients.ClipByGlobalNorm (AdamW.cs:103-130); norm_out (may be NULL) synchronises. */
+/* Gradients.ClipByGlobalNorm (AdamW.cs:103-130); norm_out (may be NULL) synchronises, and then a NaN or
+ * infinite norm returns LAYA_ERR_NOT_FINITE (norm_out still written, gradients left unscaled as the
+ * reference leaves them). */
 int laya_model_clip_grad_norm(laya_model* model, double max_norm, double* norm_out);
+/* Synchronises and returns LAYA_ERR_NOT_FINITE when the model's last gradient norm (its clip, or the clip
+ * inside laya_model_train_step[_staged]) was not finite; LAYA_ERR_STATE before any. No counterpart in the
+ * reference, which does not detect non-finite gradients (AdamW.cs:122-128). */
+int laya_model_grad_norm_status(laya_model* model);
 /* AdamW.Step (AdamW.cs:29-73) with the trainer's groups (Trainer.cs:96-100): "encoder." parameters at
  * lr_encoder, the rest at lr_head. Applies the clip coefficient of the last clip, if any. */
 int laya_model_adamw_step(laya_model* model, double lr_encoder, double lr_head, double beta1, double beta2,

@@ -40,8 +40,16 @@ class LayaMissingError(LayaError, KeyError):
     pass
 
 
+class LayaNotFiniteError(LayaError, ArithmeticError):
+    pass
+
+
+class LayaStateError(LayaError):
+    pass
+
+
 _ERRORS = {ERR_ARGUMENT: LayaArgumentError, ERR_OUT_OF_RANGE: LayaOutOfRangeError, ERR_MEMORY: LayaMemoryError,
-           ERR_MISSING: LayaMissingError}
+           ERR_MISSING: LayaMissingError, ERR_NOT_FINITE: LayaNotFiniteError, ERR_STATE: LayaStateError}
 
 c_int, c_float, c_double, c_size, c_u64 = ctypes.c_int, ctypes.c_float, ctypes.c_double, ctypes.c_size_t, ctypes.c_uint64
 P = ctypes.c_void_p
@@ -100,9 +108,10 @@ SIGNATURES = {
     "laya_rotary_create": (c_int, [P, c_int, c_double, c_int, PP]),
     "laya_rotary_destroy": (c_int, [P, P]),
     "laya_rotary_apply": (c_int, [P, P, P, c_int, P, c_int]),
-    "laya_attention_fwd": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_float, c_int, P, c_float, c_u64, P, P]),
-    "laya_attention_bwd": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_float, c_int, P, c_float, c_u64, P, P, P,
-                                   P]),
+    "laya_segments_create": (c_int, [P, P, P, c_int, PP]),
+    "laya_segments_destroy": (c_int, [P, P]),
+    "laya_attention_fwd": (c_int, [P, P, P, c_int, c_int, c_float, c_int, P, c_float, c_u64, P, P]),
+    "laya_attention_bwd": (c_int, [P, P, P, c_int, c_int, c_float, c_int, P, c_float, c_u64, P, P, P, P]),
     "laya_embedding_fwd": (c_int, [P, P, c_int, P, c_int, c_int, P, P]),
     "laya_embedding_plan": (c_int, [P, c_int, c_int, P, P, P, ctypes.POINTER(c_int)]),
     "laya_embedding_bwd": (c_int, [P, P, P, P, c_int, P, c_int, P]),
@@ -112,6 +121,7 @@ SIGNATURES = {
     "laya_rlcd_objective": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_double, c_double, c_double,
                                     c_double, c_double, P, P]),
     "laya_grad_norm": (c_int, [P, P, c_size, c_double, P, P]),
+    "laya_grad_norm_status": (c_int, [P]),
     "laya_adamw": (c_int, [P, P, P, P, P, c_int, P, P, P, c_double, c_double, c_double, c_double, c_int, P, c_int]),
     "laya_model_create": (c_int, [P, ctypes.POINTER(ModelConfigC), PP]),
     "laya_model_destroy": (c_int, [P]),
@@ -132,6 +142,7 @@ SIGNATURES = {
     "laya_model_objective_rlcd": (c_int, [P, P, P, c_int, c_double, c_double, c_double, c_double, c_double, P]),
     "laya_model_backward_from_objective": (c_int, [P]),
     "laya_model_clip_grad_norm": (c_int, [P, c_double, ctypes.POINTER(c_double)]),
+    "laya_model_grad_norm_status": (c_int, [P]),
     "laya_model_adamw_step": (c_int, [P, c_double, c_double, c_double, c_double, c_double, c_double]),
     "laya_model_zero_grad": (c_int, [P]),
     "laya_model_train_step": (c_int, [P, ctypes.POINTER(BatchC), P, c_float, c_float, c_u64, c_double, c_double,

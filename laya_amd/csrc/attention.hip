@@ -1145,8 +1145,9 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
     p.context = context;
     p.lse = lse;
     dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
-    ProfileScope scope(ctx, "attention_fwd", 4.0 * a.hidden * a.keys, 0.0);
-    if (a.head_dim == 64 && split_attention(ctx))
+    const bool split = a.head_dim == 64 && split_attention(ctx);
+    ProfileScope scope(ctx, split ? "attention_fwd_x6" : "attention_fwd", 4.0 * a.hidden * a.keys, 0.0);
+    if (split)
         hipLaunchKernelGGL(attn_fwd_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
     else if (a.head_dim == 64)
         hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
@@ -1178,11 +1179,11 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
         p.context = const_cast<float*>(context);
         {
             // dQ first: it forms each row's Σ dO·O and writes it for dK/dV.
-            ProfileScope scope(ctx, "attention_bwd_dq", 2.0 * fb, 0.0);
+            ProfileScope scope(ctx, "attention_bwd_dq_x6", 2.0 * fb, 0.0);
             hipLaunchKernelGGL(attn_bwd_dq_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
             check_launch("attn_bwd_dq_x6_kernel");
         }
-        ProfileScope scope(ctx, "attention_bwd_dkv", 2.0 * fb, 0.0);
+        ProfileScope scope(ctx, "attention_bwd_dkv_x6", 2.0 * fb, 0.0);
         hipLaunchKernelGGL(attn_bwd_dkv_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         check_launch("attn_bwd_dkv_x6_kernel");
         return;

@@ -64,13 +64,22 @@ static int take_event(laya_ctx* ctx) {
     return ctx->next_event++;
 }
 
-ProfileScope::ProfileScope(laya_ctx* c, const char* n, double f, double b) : ctx(c), name(n), flops(f), bytes(b) {
+static thread_local ProfileScope* g_scope = nullptr;
+
+void profile_rename(const char* name) {
+    if (g_scope) g_scope->name = name;
+}
+
+ProfileScope::ProfileScope(laya_ctx* c, const char* n, double f, double b)
+    : ctx(c), name(n), flops(f), bytes(b), outer(g_scope) {
+    g_scope = this;
     if (!ctx->profiling) return;
     start = take_event(ctx);
     LAYA_HIP(hipEventRecord(ctx->event_pool[start], ctx->stream));
 }
 
 ProfileScope::~ProfileScope() {
+    g_scope = outer;
     if (start < 0 || !ctx->profiling) return;
     try {
         const int stop = take_event(ctx);
@@ -462,17 +471,60 @@ int laya_rotary_apply(laya_ctx* ctx, const laya_rotary* rot, float* vec, int row
     });
 }
 
-static AttentionArgs attention_args(const float* qkv, const int* seg_start, const int* seg_len, int nseg, int max_len,
-                                    int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
-                                    float p_drop, uint64_t seed) {
-    LAYA_REQUIRE(qkv && seg_start && seg_len, "attention: null tensor");
+int laya_segments_create(laya_ctx* ctx, const int* start, const int* length, int nseg, laya_segments** out) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(out && nseg >= 0 && (nseg == 0 || (start && length)), "segments: bad arguments");
+        auto* s = new laya_segments();
+        try {
+            s->nseg = nseg;
+            s->start.assign(start, start + nseg);
+            s->length.assign(length, length + nseg);
+            for (int i = 0; i < nseg; ++i) {
+                LAYA_REQUIRE(s->start[i] >= 0 && s->length[i] >= 0 && (long)s->start[i] + s->length[i] <= INT32_MAX,
+                             "segments: a segment with a negative start or length");
+                s->max_len = std::max(s->max_len, s->length[i]);
+                s->rows = std::max(s->rows, s->start[i] + s->length[i]);
+            }
+            const size_t bytes = sizeof(int) * (size_t)std::max(nseg, 1);
+            s->d_start = static_cast<int*>(ctx->alloc(bytes));
+            s->d_len = static_cast<int*>(ctx->alloc(bytes));
+            // The host vectors live as long as the handle, which outlives the copies (destroy synchronises).
+            if (nseg) {
+                LAYA_HIP(hipMemcpyAsync(s->d_start, s->start.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
+                LAYA_HIP(hipMemcpyAsync(s->d_len, s->length.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
+            }
+        } catch (...) {
+            if (s->d_start) ctx->release(s->d_start);
+            if (s->d_len) ctx->release(s->d_len);
+            delete s;
+            throw;
+        }
+        *out = s;
+    });
+}
+
+int laya_segments_destroy(laya_ctx* ctx, laya_segments* segs) {
+    return guarded([&] {
+        require_ctx(ctx);
+        if (!segs) return;
+        ctx->release(segs->d_start);  // release synchronises the stream first
+        ctx->release(segs->d_len);
+        delete segs;
+    });
+}
+
+static AttentionArgs attention_args(const float* qkv, const laya_segments* segs, int hidden, int heads, float scale,
+                                    int half_window, const laya_rotary* rot, float p_drop, uint64_t seed) {
+    LAYA_REQUIRE(qkv && segs, "attention: null tensor or segment list");
     LAYA_REQUIRE(heads > 0 && hidden % heads == 0, "attention: hidden must be a multiple of heads");
     AttentionArgs a{};
     a.qkv = qkv;
-    a.seg_start = seg_start;
-    a.seg_len = seg_len;
-    a.nseg = nseg;
-    a.max_len = max_len;
+    a.seg_start = segs->d_start;
+    a.seg_len = segs->d_len;
+    a.nseg = segs->nseg;
+    a.max_len = segs->max_len;
+    a.rows = segs->rows;
     a.hidden = hidden;
     a.heads = heads;
     a.head_dim = hidden / heads;
@@ -486,57 +538,41 @@ static AttentionArgs attention_args(const float* qkv, const int* seg_start, cons
         a.sin_table = rot->sin_t;
         a.positions = rot->positions;
     }
+    for (int L : segs->length) a.keys += window_keys(L, half_window);
     return a;
 }
 
-int laya_attention_fwd(laya_ctx* ctx, const float* qkv, const int* seg_start, const int* seg_len, int nseg,
-                       int max_len, int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
-                       float p_drop, uint64_t seed, float* context, float* lse) {
+int laya_attention_fwd(laya_ctx* ctx, const float* qkv, const laya_segments* segs, int hidden, int heads, float scale,
+                       int half_window, const laya_rotary* rot, float p_drop, uint64_t seed, float* context,
+                       float* lse) {
     return guarded([&] {
         require_ctx(ctx);
         LAYA_REQUIRE(context && lse, "attention: null output");
-        AttentionArgs a = attention_args(qkv, seg_start, seg_len, nseg, max_len, hidden, heads, scale, half_window,
-                                         rot, p_drop, seed);
-        if ((ctx->profiling || rot) && nseg > 0) {
-            // The segment table (small) sizes the profile's flop count and the rotated copy of q and k.
-            std::vector<int> st(nseg), ln(nseg);
-            LAYA_HIP(hipMemcpyAsync(st.data(), seg_start, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
-            LAYA_HIP(hipMemcpyAsync(ln.data(), seg_len, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
-            LAYA_HIP(hipStreamSynchronize(ctx->stream));
-            a.rows = 0;
-            for (int i = 0; i < nseg; ++i) {
-                LAYA_REQUIRE(ln[i] >= 0 && ln[i] <= max_len && st[i] >= 0, "attention: bad segment table");
-                a.rows = std::max(a.rows, st[i] + ln[i]);
-                a.keys += window_keys(ln[i], half_window);
-            }
-        }
+        const AttentionArgs a =
+            attention_args(qkv, segs, hidden, heads, scale, half_window, rot, p_drop, seed);
         attention_fwd(ctx, a, context, lse);
     });
 }
 
-int laya_attention_bwd(laya_ctx* ctx, const float* qkv, const int* seg_start, const int* seg_len, int nseg,
-                       int max_len, int hidden, int heads, float scale, int half_window, const laya_rotary* rot,
-                       float p_drop, uint64_t seed, const float* context, const float* lse, const float* dcontext,
-                       float* dqkv) {
+int laya_attention_bwd(laya_ctx* ctx, const float* qkv, const laya_segments* segs, int hidden, int heads, float scale,
+                       int half_window, const laya_rotary* rot, float p_drop, uint64_t seed, const float* context,
+                       const float* lse, const float* dcontext, float* dqkv) {
     return guarded([&] {
         require_ctx(ctx);
-        LAYA_REQUIRE(context && lse && dcontext && dqkv, "attention_bwd: null tensor");
-        // The rows the segment table covers: read it back (small) to size the row-constant pass.
-        std::vector<int> st(nseg), ln(nseg);
-        if (nseg > 0) {
-            LAYA_HIP(hipMemcpyAsync(st.data(), seg_start, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
-            LAYA_HIP(hipMemcpyAsync(ln.data(), seg_len, sizeof(int) * nseg, hipMemcpyDeviceToHost, ctx->stream));
-            LAYA_HIP(hipStreamSynchronize(ctx->stream));
+        LAYA_REQUIRE(dcontext && dqkv, "attention_bwd: null tensor");
+        const AttentionArgs a =
+            attention_args(qkv, segs, hidden, heads, scale, half_window, rot, p_drop, seed);
+        if (!context || !lse) {
+            // Ops.AttentionBackward recomputes each row's softmax from q and k (Ops.cs:390-394); here the
+            // forward runs once more into scratch for the context and the row log-sum-exp.
+            const size_t rows = (size_t)std::max(a.rows, 1);
+            float* c = static_cast<float*>(ctx->workspace(6, sizeof(float) * rows * hidden));
+            float* l = static_cast<float*>(ctx->workspace(7, sizeof(float) * rows * heads));
+            attention_fwd(ctx, a, c, l);
+            context = c;
+            lse = l;
         }
-        int rows = 0;
-        for (int i = 0; i < nseg; ++i) {
-            LAYA_REQUIRE(ln[i] >= 0 && ln[i] <= max_len && st[i] >= 0, "attention_bwd: bad segment table");
-            rows = std::max(rows, st[i] + ln[i]);
-        }
-        AttentionArgs a = attention_args(qkv, seg_start, seg_len, nseg, max_len, hidden, heads, scale, half_window,
-                                         rot, p_drop, seed);
-        for (int L : ln) a.keys += window_keys(L, half_window);
-        attention_bwd(ctx, a, rows, context, lse, dcontext, dqkv);
+        attention_bwd(ctx, a, a.rows, context, lse, dcontext, dqkv);
     });
 }
 
@@ -624,7 +660,23 @@ int laya_rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets
 int laya_grad_norm(laya_ctx* ctx, const float* grads, size_t n, double max_norm, double* norm_out, float* coef_out) {
     return guarded([&] {
         require_ctx(ctx);
-        grad_norm(ctx, grads, n, max_norm, norm_out, coef_out, nullptr);
+        LAYA_REQUIRE(n == 0 || grads, "grad_norm: null gradients");
+        if (!ctx->nonfinite) ctx->nonfinite = static_cast<int*>(ctx->alloc(64));
+        grad_norm(ctx, grads, n, max_norm, norm_out, coef_out, ctx->nonfinite);
+    });
+}
+
+int laya_grad_norm_status(laya_ctx* ctx) {
+    return guarded([&] {
+        require_ctx(ctx);
+        if (!ctx->nonfinite) throw Error(LAYA_ERR_STATE, "grad_norm_status: no gradient norm was computed on this context");
+        int flag = 0;
+        LAYA_HIP(hipMemcpyAsync(&flag, ctx->nonfinite, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(ctx->stream));
+        if (flag)
+            throw Error(LAYA_ERR_NOT_FINITE, "the gradient norm is not finite (a NaN or infinite gradient): the clip "
+                                             "coefficient stayed 1, as Gradients.ClipByGlobalNorm leaves such "
+                                             "gradients unscaled");
     });
 }
 

@@ -80,7 +80,7 @@ struct laya_ctx {
     hipStream_t stream = nullptr;
     size_t cap = 0, in_use = 0;
     std::unordered_map<void*, size_t> allocations;
-    laya::Workspace scratch[6];
+    laya::Workspace scratch[8];
     hipEvent_t timers[16][2] = {};
     int cu_count = 256;
     bool profiling = false;
@@ -92,11 +92,22 @@ struct laya_ctx {
     std::vector<hipEvent_t> event_pool;
     std::vector<laya::LaunchRecord> launches;
     int next_event = 0;
+    // Non-finite flag of the last laya_grad_norm on this context (device int, allocated on first use).
+    int* nonfinite = nullptr;
 
     // Device scratch slot `slot` of at least `bytes`, reallocated (not preserved) when it grows.
     void* workspace(int slot, size_t bytes);
     void* alloc(size_t bytes);
     void release(void* p);
+};
+
+// A segment list (ModernBertEncoder.cs:30-33: Segment(Start, Length)) uploaded once: device tables the
+// attention kernels read, and the host copy that sizes launches without reading the device back.
+struct laya_segments {
+    int nseg = 0, max_len = 0, rows = 0;
+    std::vector<int> start, length;
+    int* d_start = nullptr;
+    int* d_len = nullptr;
 };
 
 // Rotary tables on the device (Ops.cs:446-504).
@@ -164,9 +175,14 @@ struct ProfileScope {
     int start = -1;
     const char* name;
     double flops, bytes;
+    ProfileScope* outer;
     ProfileScope(laya_ctx* c, const char* n, double f, double b);
     ~ProfileScope();
 };
+
+// Renames the innermost open profile scope of this thread: a launcher that picks a kernel variant
+// below the scope's opener (the 256 × 256 tiles) tags the launch with that variant's name.
+void profile_rename(const char* name);
 
 // ------------------------------------------------------------------------ internal launchers
 

@@ -1675,6 +1675,7 @@ bool wide_tiles_pay(const laya_ctx* ctx, const GemmParams& p, bool three) {
 }
 
 void launch_wide(laya_ctx* ctx, GemmParams p) {
+    profile_rename("gemm_nt_x6w");
     p.tiles_n = (p.N + WT - 1) / WT;
     const dim3 g(((p.M + WT - 1) / WT) * p.tiles_n), b(WT_THREADS);
     if (p.mode == STORE_ROPE)
@@ -1968,8 +1969,8 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
     if (!make_pair_plan_wide(ctx, n0, out, n1, rows, s)) return false;
     s.partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)s.G * 2 * WT * WT));
     {
-        ProfileScope scope(ctx, half ? "gemm_bwd_pair_bf16" : "gemm_bwd_pair_x6", 2.0 * 2.0 * rows * (double)in * out,
-                           0.0);
+        ProfileScope scope(ctx, half ? "gemm_bwd_pair_bf16w" : "gemm_bwd_pair_x6w",
+                           2.0 * 2.0 * rows * (double)in * out, 0.0);
         if (half)
             hipLaunchKernelGGL(gemm_pair_wide_kernel<1>, dim3(s.G), dim3(WT_THREADS), 0, ctx->stream, nn, tn, s);
         else

@@ -158,6 +158,7 @@ struct laya_model {
     float* d_loss = nullptr;
     int* d_nonfinite = nullptr;
     bool coef_valid = false;
+    bool norm_done = false;  // a gradient norm has been computed (d_nonfinite holds its flag)
 
     // ----- the batch of the last forward
     bool has_tape = false, training = false;
@@ -947,11 +948,28 @@ int laya_model_clip_grad_norm(laya_model* m, double max_norm, double* norm_out) 
     return guarded([&] {
         checked(m);
         grad_norm(m->ctx, m->G, m->total, max_norm, m->d_norm, m->d_coef, m->d_nonfinite);
-        m->coef_valid = true;
+        m->coef_valid = m->norm_done = true;
         if (norm_out) {
             LAYA_HIP(hipMemcpyAsync(norm_out, m->d_norm, sizeof(double), hipMemcpyDeviceToHost, m->ctx->stream));
             LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+            if (!std::isfinite(*norm_out))
+                throw Error(LAYA_ERR_NOT_FINITE, "clip: the gradient norm is not finite; the gradients stay "
+                                                 "unscaled (Gradients.ClipByGlobalNorm)");
         }
+    });
+}
+
+int laya_model_grad_norm_status(laya_model* m) {
+    return guarded([&] {
+        checked(m);
+        if (!m->norm_done) throw Error(LAYA_ERR_STATE, "grad_norm_status: no gradient norm since the model was built");
+        int flag = 0;
+        LAYA_HIP(hipMemcpyAsync(&flag, m->d_nonfinite, sizeof(int), hipMemcpyDeviceToHost, m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+        if (flag)
+            throw Error(LAYA_ERR_NOT_FINITE, "the last step's gradient norm is not finite (a NaN or infinite "
+                                             "gradient): its clip left the gradients unscaled and AdamW applied them, "
+                                             "as the reference does");
     });
 }
 
@@ -984,7 +1002,7 @@ void train_step_current(laya_model* m, const float* targets, float ce_weight, fl
                    m->d_loss);
     backward(m);
     grad_norm(m->ctx, m->G, m->total, max_norm, m->d_norm, m->d_coef, m->d_nonfinite);
-    m->coef_valid = true;
+    m->coef_valid = m->norm_done = true;
     adamw_step(m, lr_encoder, lr_head, beta1, beta2, eps, weight_decay, true);
     if (loss_out) {
         LAYA_HIP(hipMemcpyAsync(loss_out, m->d_loss, sizeof(float), hipMemcpyDeviceToHost, m->ctx->stream));

@@ -10,7 +10,12 @@
 // adamw restates AdamW.Step (AdamW.cs:29-73) for several parameter groups in one launch:
 // decoupled decay, both moments, bias-corrected update, optional clearing of the gradient
 // (ZeroGradients, TrainableDecisionModel.cs:237-240) in the same pass. 32 bytes per parameter.
+// Every float operation of the update is rounded on its own, as C# evaluates it (no multiply-add
+// contraction, correctly rounded division and square root), so a step is bit-identical to
+// AdamW.cs:61-68 on the same inputs.
 #include "elementwise.hpp"
+
+#pragma clang fp contract(off)
 
 namespace laya {
 namespace {

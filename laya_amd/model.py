@@ -15,7 +15,7 @@ from typing import Dict, List, Optional, Sequence
 
 import numpy as np
 
-from ._native import BatchC, ModelConfigC, check, lib
+from ._native import ERR_MISSING, ERR_NOT_FINITE, BatchC, LayaMissingError, ModelConfigC, check, lib
 from .batch import Batch, TrainingItem
 from .config import ModelConfig
 from .device import Context
@@ -105,7 +105,10 @@ class TrainableDecisionModel:
             if name not in st.entries:
                 if name == "temperature":
                     continue
-                raise KeyError(f"the checkpoint has no '{name}' tensor; is it a laya decision model?")
+                # InvalidDataException of TrainableDecisionModel.cs:184-186: the same status the C-ABI
+                # gives a lookup of a tensor the model does not have.
+                raise LayaMissingError(ERR_MISSING, f"the checkpoint has no '{name}' tensor; is it a laya "
+                                                    "decision model?")
             model.set_param(name, st.read_float32(name))
         model.file_order = st.names_in_file_order()
         model.stored_dtypes = {n: st.dtype(n) for n in model.file_order}
@@ -282,10 +285,19 @@ class TrainableDecisionModel:
         check(lib().laya_model_zero_grad(self.handle))
 
     def clip_grad_norm(self, max_norm: float) -> float:
-        """Gradients.ClipByGlobalNorm (AdamW.cs:103-130); the scaling is applied by the next AdamW step."""
+        """Gradients.ClipByGlobalNorm (AdamW.cs:103-130); the scaling is applied by the next AdamW step.
+        Like the reference it returns a NaN or infinite norm and leaves such gradients unscaled;
+        ``check_gradients_finite`` turns that case into an exception."""
         v = ctypes.c_double()
-        check(lib().laya_model_clip_grad_norm(self.handle, float(max_norm), ctypes.byref(v)))
+        rc = lib().laya_model_clip_grad_norm(self.handle, float(max_norm), ctypes.byref(v))
+        if rc != ERR_NOT_FINITE:
+            check(rc)
         return v.value
+
+    def check_gradients_finite(self) -> None:
+        """Raises LayaNotFiniteError when the last gradient norm (an explicit clip, or the one inside
+        train_step) met a NaN or infinite gradient."""
+        check(lib().laya_model_grad_norm_status(self.handle))
 
     def adamw_step(self, lr_encoder: float, lr_head: float, beta1: float = 0.9, beta2: float = 0.999,
                    eps: float = 1e-8, weight_decay: float = 0.01) -> None:

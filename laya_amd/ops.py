@@ -105,6 +105,13 @@ def geglu_backward(ctx: Context, wide: DeviceArray, dact: DeviceArray, rows: int
     check(lib().laya_geglu_bwd(_h(ctx), wide.ptr, dact.ptr, rows, intermediate, dwide.ptr))
 
 
+def add(ctx: Context, dst: DeviceArray, src: DeviceArray) -> None:
+    """SimdOps.Add (SimdOps.cs:84-93): dst += src (the residual adds of TrainableDecisionModel.cs:385, 402)."""
+    if dst.size != src.size:
+        raise ValueError(f"add: {dst.size} and {src.size} elements")
+    check(lib().laya_add(_h(ctx), dst.ptr, src.ptr, dst.size))
+
+
 # ---------------------------------------------------------------------------------- dropout
 
 def uniform(seed: int, index: int) -> float:
@@ -177,18 +184,36 @@ class AttentionShape:
 
 
 class Segments:
-    """The concatenated items of a batch (ModernBertEncoder.Segment), as device tables."""
+    """The concatenated items of a batch (ModernBertEncoder.Segment), uploaded once as a laya_segments
+    handle that every attention call of the batch shares."""
 
-    def __init__(self, ctx: Context, lengths: Sequence[int]):
-        lengths = np.asarray(lengths, np.int32)
+    def __init__(self, ctx: Context, lengths: Sequence[int], starts: Optional[Sequence[int]] = None):
+        import ctypes
+        lengths = np.ascontiguousarray(lengths, np.int32)
+        self.ctx = ctx
         self.lengths = lengths
-        self.starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]).astype(np.int32) if len(lengths) else \
-            np.zeros(0, np.int32)
-        self.d_start = DeviceArray.from_numpy(ctx, self.starts if len(lengths) else np.zeros(1, np.int32))
-        self.d_len = DeviceArray.from_numpy(ctx, lengths if len(lengths) else np.zeros(1, np.int32))
+        if starts is None:
+            starts = np.concatenate([[0], np.cumsum(lengths)[:-1]]) if len(lengths) else np.zeros(0)
+        self.starts = np.ascontiguousarray(starts, np.int32)
         self.count = len(lengths)
         self.max_len = int(lengths.max()) if len(lengths) else 0
-        self.rows = int(lengths.sum())
+        self.rows = int((self.starts + lengths).max()) if len(lengths) else 0
+        h = ctypes.c_void_p()
+        check(lib().laya_segments_create(_h(ctx), self.starts.ctypes.data, lengths.ctypes.data, self.count,
+                                         ctypes.byref(h)))
+        self.handle = h.value
+        ctx.register(self)
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) and getattr(self.ctx, "handle", None):
+            lib().laya_segments_destroy(self.ctx.handle, self.handle)
+        self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def _hw(shape: AttentionShape) -> int:
@@ -197,24 +222,25 @@ def _hw(shape: AttentionShape) -> int:
 
 def attention_forward(qkv: DeviceArray, segments: Segments, shape: AttentionShape, context: DeviceArray,
                       lse: DeviceArray) -> None:
-    """Ops.AttentionForward (Ops.cs:275-277); also writes the row log-sum-exp the backward reuses."""
+    """Ops.AttentionForward (Ops.cs:275-277); also writes the row log-sum-exp the backward may reuse."""
     if shape.rotary is not None:
         shape.rotary.ensure(segments.max_len)
-    check(lib().laya_attention_fwd(_h(qkv.ctx), qkv.ptr, segments.d_start.ptr, segments.d_len.ptr, segments.count,
-                                   segments.max_len, shape.hidden, shape.heads, shape.scale, _hw(shape),
-                                   None if shape.rotary is None else shape.rotary.handle, shape.dropout,
+    check(lib().laya_attention_fwd(_h(qkv.ctx), qkv.ptr, segments.handle, shape.hidden, shape.heads, shape.scale,
+                                   _hw(shape), None if shape.rotary is None else shape.rotary.handle, shape.dropout,
                                    shape.seed & (2 ** 64 - 1), context.ptr, lse.ptr))
 
 
-def attention_backward(qkv: DeviceArray, segments: Segments, shape: AttentionShape, context: DeviceArray,
-                       lse: DeviceArray, dcontext: DeviceArray, dqkv: DeviceArray) -> None:
-    """Ops.AttentionBackward (Ops.cs:280-282): dq, dk, dv written (not added) into dqkv."""
+def attention_backward(qkv: DeviceArray, segments: Segments, shape: AttentionShape, dcontext: DeviceArray,
+                       dqkv: DeviceArray, context: Optional[DeviceArray] = None,
+                       lse: Optional[DeviceArray] = None) -> None:
+    """Ops.AttentionBackward (Ops.cs:280-282): dq, dk, dv written (not added) into dqkv. The forward's
+    context and lse are reused when given; without them the row statistics are recomputed, as the
+    reference recomputes each row's softmax."""
     if shape.rotary is not None:
         shape.rotary.ensure(segments.max_len)
-    check(lib().laya_attention_bwd(_h(qkv.ctx), qkv.ptr, segments.d_start.ptr, segments.d_len.ptr, segments.count,
-                                   segments.max_len, shape.hidden, shape.heads, shape.scale, _hw(shape),
-                                   None if shape.rotary is None else shape.rotary.handle, shape.dropout,
-                                   shape.seed & (2 ** 64 - 1), context.ptr, lse.ptr, dcontext.ptr, dqkv.ptr))
+    check(lib().laya_attention_bwd(_h(qkv.ctx), qkv.ptr, segments.handle, shape.hidden, shape.heads, shape.scale,
+                                   _hw(shape), None if shape.rotary is None else shape.rotary.handle, shape.dropout,
+                                   shape.seed & (2 ** 64 - 1), ptr(context), ptr(lse), dcontext.ptr, dqkv.ptr))
 
 
 def default_scale(head_dim: int) -> float:

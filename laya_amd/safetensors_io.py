@@ -9,6 +9,7 @@ memory-mapped, nothing in it is executed.
 from __future__ import annotations
 
 import json
+import os
 import struct
 from typing import Dict, Iterable, List, Tuple
 
@@ -91,8 +92,14 @@ def write(path: str, tensors: Iterable[Tuple[str, Tuple[int, ...], np.ndarray, s
         offset += len(blob)
     text = json.dumps(header, separators=(",", ":")).encode("utf-8")
     text += b" " * ((8 - len(text) % 8) % 8)
-    with open(path, "wb") as f:
+    # Written beside the target and moved over it once complete (as SafetensorsWriter does with its .tmp
+    # file, SafetensorsWriter.cs:46-58): a crash mid-write never leaves a truncated file under `path`.
+    tmp = path + ".tmp"
+    with open(tmp, "wb") as f:
         f.write(struct.pack("<Q", len(text)))
         f.write(text)
         for b in blobs:
             f.write(b)
+        f.flush()
+        os.fsync(f.fileno())
+    os.replace(tmp, path)

@@ -24,6 +24,7 @@ from __future__ import annotations
 import json
 import math
 import os
+import shutil
 import time
 from dataclasses import dataclass, field
 from typing import Callable, List, Optional, Sequence
@@ -201,6 +202,31 @@ class _LoopState:
     elapsed: float = 0.0
 
 
+_STAGING, _RETIRED = ".new", ".old"
+
+
+def _swap_in(staging: str, rolling: str) -> None:
+    """Replaces `rolling` by the complete checkpoint in `staging` with two renames."""
+    retired = rolling + _RETIRED
+    shutil.rmtree(retired, ignore_errors=True)
+    if os.path.exists(rolling):
+        os.rename(rolling, retired)
+    os.rename(staging, rolling)
+    shutil.rmtree(retired, ignore_errors=True)
+
+
+def _recover_rolling(rolling: str) -> None:
+    """Finishes a swap an interruption cut short: a staged checkpoint whose loop state was written is
+    complete and wins; otherwise the retired one is restored."""
+    if os.path.exists(rolling):
+        return
+    staging, retired = rolling + _STAGING, rolling + _RETIRED
+    if os.path.exists(os.path.join(staging, STATE_FILE)):
+        os.rename(staging, rolling)
+    elif os.path.exists(retired):
+        os.rename(retired, rolling)
+
+
 class Trainer:
     """Trainer (Trainer.cs:73-180) on one GPU."""
 
@@ -230,6 +256,8 @@ class Trainer:
         rolling = os.path.join(output_directory, ROLLING)
         state = _LoopState()
         load_from = source_directory
+        if resume:
+            _recover_rolling(rolling)
         if resume and os.path.exists(os.path.join(rolling, STATE_FILE)):
             with open(os.path.join(rolling, STATE_FILE)) as f:
                 saved = json.load(f)
@@ -310,14 +338,20 @@ class Trainer:
                                           sigma, elapsed(), f"epoch {epoch + 1}/{o.epochs} done, average loss "
                                           f"{average:.4f}"))
             if o.rolling_checkpoint and not stop and epoch + 1 < o.epochs:
-                model.save(rolling, source_directory, build_config(source_directory, o, None, max_length,
+                # The whole checkpoint is written into a sibling directory, the loop state last, and only
+                # then swapped in: an interruption never leaves weights of one epoch beside the loop state
+                # and moments of another.
+                staging = rolling + _STAGING
+                shutil.rmtree(staging, ignore_errors=True)
+                model.save(staging, source_directory, build_config(source_directory, o, None, max_length,
                                                                    head_max_length, model.steps, epoch + 1, elapsed()))
-                with open(os.path.join(rolling, "checkpoint_meta.json"), "w") as f:
+                with open(os.path.join(staging, "checkpoint_meta.json"), "w") as f:
                     json.dump({"epoch": epoch + 1, "total_epochs": o.epochs, "avg_loss": average}, f, indent=2)
-                model.save_optimizer_state(os.path.join(rolling, STATE_TENSORS))
-                with open(os.path.join(rolling, STATE_FILE), "w") as f:
+                model.save_optimizer_state(os.path.join(staging, STATE_TENSORS))
+                with open(os.path.join(staging, STATE_FILE), "w") as f:
                     json.dump({"next_epoch": epoch + 1, "micro_step": micro_step, "epoch_loss": epoch_loss,
                                "elapsed": elapsed(), "optimizer_steps": model.steps}, f, indent=2)
+                _swap_in(staging, rolling)
 
         calibration = list(calibration_items) if calibration_items is not None else calibration_sample(items, o)
         fit = calibrate(model, calibration, o.minimum_bucket_samples)

@@ -33,3 +33,20 @@ def mixed_batch(rng, lengths, vocab, options=(8, 4, 2)):
     opts = [min(options[i % len(options)], max(1, (lengths[i] - 1) // 2)) for i in range(n)]
     qtypes = [i % 3 for i in range(n)]
     return synthetic_batch(rng, lengths, opts, qtypes, vocab)
+
+
+def fixture_params(shapes: dict, seed: int, std: float = 0.02) -> dict:
+    """Parameters of the full-size parity fixtures: each tensor from its own generator keyed by (seed, name),
+    so the draw does not depend on the order the shapes are listed in. Norm weights and the scorer's norm
+    1 + 0.2·N(0,1) (so γ errors show), biases and the rest std·N(0,1), temperature 1."""
+    import zlib
+    out = {}
+    for name, shape in shapes.items():
+        rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+        if name == "temperature":
+            out[name] = np.ones(shape, np.float32)
+        elif len(shape) == 1 and "norm" in name and name.endswith("weight") or name.startswith("scorer.0.weight"):
+            out[name] = (1.0 + 0.2 * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+        else:
+            out[name] = (std * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+    return out

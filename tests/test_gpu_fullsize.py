@@ -1,0 +1,124 @@
+"""Full-size parity of the benchmark workloads: the whole ModernBERT-base model (22 layers, 164M
+parameters, the decision head) on the exact first batch bench.py draws, every gradient against the fp64
+oracle.
+
+* batch 32 × seq 512 with trailing padding U[0, 0.3], heads choice-8 / score-4 / noul-2, summed CE
+  (14,344 real tokens): the headline workload, where the linears run the 256 × 256 backward pair and
+  forward products;
+* batch 2 × seq 8192, one choice head K = 5, mean CE (16,384 tokens): long-context attention, eight
+  global layers over 8192 keys and the head's full attention.
+
+The fp64 oracle needs minutes to hours for these, so it ran once, offline
+(tests/golden/make_fullsize_fixtures.py), and the fixture holds count sketches of its gradients
+(tests/sketch.py): a linear summary from which the relative L2 distance of any tensor to the exact one
+is estimated to a few per cent. Bar per tensor, as at the smaller sizes: rel-L2 ≤ max(1e-4, 4 × the fp32
+oracle's own distance from fp64), the fp32 oracle being the reference's arithmetic; plus the reference's
+max|Δ|/max|g| (TrainingGradientTests.cs:58-85) over each tensor's 64 largest exact entries."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "golden"))
+
+from helpers import fixture_params  # noqa: E402
+from make_fullsize_fixtures import HEAD_DROPOUT, PARAM_SEED, STEP_SEED, fixture_path, workload_batch  # noqa: E402
+from sketch import rel_l2 as sketch_rel_l2  # noqa: E402
+from sketch import sketch  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from laya_amd.device import Context
+    print("full-size tests: creating context on device 0", flush=True)
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def _step(ctx, workload):
+    from laya_amd.config import modernbert_base
+    from laya_amd.model import TrainableDecisionModel
+    fx = np.load(fixture_path(workload))
+    batch, _, _ = workload_batch(workload)
+    assert int(fx["meta"][2]) == batch.n_tokens, "the fixture was made from another batch"
+    m = TrainableDecisionModel(modernbert_base(), ctx)
+    m.set_params(fixture_params(m.shapes, PARAM_SEED))
+    m.head_dropout = HEAD_DROPOUT
+    ctx.profile_begin()
+    logits = m.forward(batch, training=True, seed=STEP_SEED)
+    m.backward(fx["dlogits"])
+    prof = ctx.profile_end()
+    return m, fx, batch, logits, prof
+
+
+def _check_gradients(m, fx):
+    names = [str(n) for n in fx["names"]]
+    with_grad = [n for n in m.names if m.has_grad(n)]
+    assert sorted(with_grad) == sorted(names)
+    worst, worst_top, bar_hits = (0.0, ""), (0.0, ""), 0
+    for i, n in enumerate(names):
+        g = m.grad(n)
+        r = sketch_rel_l2(fx["sk/" + n], sketch(n, g))
+        bar = max(1e-4, 4 * float(fx["fp32_err"][i]))
+        assert r < bar, (n, r, bar)
+        if r >= 1e-4:
+            bar_hits += 1
+        top = float(np.abs(g.reshape(-1)[fx["top_i/" + n]] - fx["top_v/" + n]).max() / fx["max_abs"][i])
+        if bar == 1e-4:  # a tensor whose exact gradient is rounding noise in fp32 is held by rel-L2 alone
+            assert top < 1e-4, (n, top)
+        if bar == 1e-4:
+            worst = max(worst, (r, n))
+            worst_top = max(worst_top, (top, n))
+    print(f"{len(names)} gradients; among those whose fp32-oracle error is below 2.5e-5: worst rel-L2 "
+          f"{worst[0]:.2e} ({worst[1]}), worst max|Δ|/max|g| over the top "
+          f"entries {worst_top[0]:.2e} ({worst_top[1]}); fp32 oracle worst {fx['fp32_err'].max():.2e}; "
+          f"{bar_hits} tensors above 1e-4 under the fp32-oracle bar", flush=True)
+
+
+def test_headline_batch_32x512_every_gradient_matches_fp64(ctx):
+    print("full size: ModernBERT-base 22 layers, batch 32 x 512 padded (14344 tokens)", flush=True)
+    m, fx, batch, logits, prof = _step(ctx, "b32x512")
+    assert np.abs(logits - fx["logits"]).max() < 1e-4
+    # The wide kernels this workload's timing rests on are the ones under test.
+    assert prof.get("gemm_bwd_pair_x6w", {}).get("launches", 0) >= 90, sorted(prof)
+    # At 14,344 rows the 2304-wide products would need a third round of 256 × 256 tiles and stay on
+    # 128 × 128 tiles; the head's 3072-wide products take the wide forward kernel.
+    assert prof.get("gemm_nt_x6w", {}).get("launches", 0) >= 2, sorted(prof)
+    _check_gradients(m, fx)
+    m.close()
+
+
+def test_long_context_batch_2x8192_every_gradient_matches_fp64(ctx):
+    print("full size: ModernBERT-base 22 layers, batch 2 x 8192 (16384 tokens)", flush=True)
+    m, fx, batch, logits, prof = _step(ctx, "b2x8192")
+    assert np.abs(logits - fx["logits"]).max() < 1e-4
+    assert prof.get("attention_bwd_dkv_x6", {}).get("launches", 0) == 24, sorted(prof)
+    _check_gradients(m, fx)
+    m.close()
+
+
+@pytest.mark.parametrize("workload", ["b32x512", "b2x8192"])
+def test_full_size_gradients_are_bitwise_repeatable(ctx, workload):
+    """No float atomics and fixed reduction orders: the same step twice gives identical bits."""
+    from laya_amd.config import modernbert_base
+    from laya_amd.model import TrainableDecisionModel
+    print(f"full size: repeatability on {workload}", flush=True)
+    batch, _, _ = workload_batch(workload)
+    m = TrainableDecisionModel(modernbert_base(), ctx)
+    m.set_params(fixture_params(m.shapes, PARAM_SEED))
+    d = np.random.default_rng(5).standard_normal(batch.n_markers).astype(np.float32)
+    names = [n for n in m.names if not n.startswith(("act_head", "temperature"))]
+    runs = []
+    for _ in range(2):
+        m.zero_gradients()
+        m.forward(batch, training=True, seed=3)
+        m.backward(d)
+        runs.append({n: m.grad(n) for n in names})
+    for n in names:
+        np.testing.assert_array_equal(runs[0][n], runs[1][n], err_msg=n)
+    m.close()

@@ -256,11 +256,17 @@ def test_attention_forward_and_backward(ctx, hd, heads, lengths, hw, theta, p, p
     ref = oracle.attention_forward(qkv, lengths, heads, scale, hw, theta, p, seed, double=True)
     assert rel_l2(ref, cd.numpy()) < 1e-5
     dq = dev(ctx, np.zeros_like(qkv))
-    laya.attention_backward(qd, segs, shape, cd, lse, dev(ctx, dctx), dq)
+    dcd = dev(ctx, dctx)
+    laya.attention_backward(qd, segs, shape, dcd, dq, context=cd, lse=lse)
     dref = oracle.attention_backward(qkv, dctx, lengths, heads, scale, hw, theta, p, seed, double=True)
     got = dq.numpy()
     for part, sl in (("q", slice(0, hidden)), ("k", slice(hidden, 2 * hidden)), ("v", slice(2 * hidden, None))):
         assert rel_l2(dref[:, sl], got[:, sl]) < 1e-5, part
+    # The reference's signature (Ops.AttentionBackward carries no forward outputs): the row statistics are
+    # recomputed by the same kernels, so the result is the same to the bit.
+    dq2 = dev(ctx, np.zeros_like(qkv))
+    laya.attention_backward(qd, segs, shape, dcd, dq2)
+    np.testing.assert_array_equal(got, dq2.numpy())
     ctx.set_matmul_precision("fp32")
 
 
@@ -278,7 +284,7 @@ def test_attention_is_deterministic(ctx):
         qd, cd = dev(ctx, qkv), dev(ctx, np.zeros((T, hidden), np.float32))
         lse, dq = dev(ctx, np.zeros(T * heads, np.float32)), dev(ctx, np.zeros_like(qkv))
         laya.attention_forward(qd, segs, shape, cd, lse)
-        laya.attention_backward(qd, segs, shape, cd, lse, dev(ctx, dctx), dq)
+        laya.attention_backward(qd, segs, shape, dev(ctx, dctx), dq, context=cd, lse=lse)
         outs.append((cd.numpy(), dq.numpy()))
     np.testing.assert_array_equal(outs[0][0], outs[1][0])
     np.testing.assert_array_equal(outs[0][1], outs[1][1])

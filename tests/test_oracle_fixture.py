@@ -67,6 +67,18 @@ def test_objective_matches_the_notebook_loss_and_gradient():
     # The CE-only path (no groups) is the same soft cross-entropy term.
     ce2, g2 = oracle.cross_entropy(ks, logits, target)
     assert abs(ce2 - fx["loss_ce"]) < 1e-5
+    # Its gradient is pinned two ways. (1) The objective is linear in its term weights, so the fixture's full
+    # gradient minus the policy-only gradient (ce_weight 0) is the CE gradient.
+    _, g_policy = oracle.rlcd(ks, fx["qtypes"], logits, target, draws, fx["sigma"], ce_weight=0.0)
+    np.testing.assert_allclose(g2, np.concatenate(fx["grad"]) - g_policy, atol=1e-4)
+    # (2) Central differences of the CE value, itself pinned to the fixture above.
+    h = 1e-2
+    for i in range(len(logits)):
+        up, dn = logits.copy(), logits.copy()
+        up[i] += h
+        dn[i] -= h
+        fd = (oracle.cross_entropy(ks, up, target)[0] - oracle.cross_entropy(ks, dn, target)[0]) / (2 * h)
+        assert abs(fd - g2[i]) < 2e-4, (i, fd, g2[i])
 
 
 def test_adamw_and_cosine_match_pytorch_closed_values():

@@ -3,6 +3,7 @@ fitting, the calibration sample and the written config (no GPU)."""
 import json
 import math
 import os
+import shutil
 
 import numpy as np
 import pytest
@@ -148,3 +149,53 @@ def test_build_config_keeps_unknown_keys(tmp_path):
     c2 = {}
     write_temperatures(c2, fitted)
     assert c2["temperature"][2] == float(np.float32(1.2))
+
+
+def test_rolling_checkpoint_swap_survives_an_interruption(tmp_path):
+    """The rolling checkpoint is written whole into a sibling directory and swapped in by renames; an
+    interruption at any point leaves one complete checkpoint that resume picks up."""
+    from laya_amd.trainer import STATE_FILE, _recover_rolling, _swap_in
+
+    def make(d, epoch):
+        os.makedirs(d, exist_ok=True)
+        with open(os.path.join(d, "model.safetensors"), "w") as f:
+            f.write(f"weights {epoch}")
+        with open(os.path.join(d, STATE_FILE), "w") as f:
+            f.write(f"state {epoch}")
+
+    def epoch_of(d):
+        a = open(os.path.join(d, "model.safetensors")).read().split()[1]
+        b = open(os.path.join(d, STATE_FILE)).read().split()[1]
+        assert a == b
+        return int(a)
+
+    rolling = str(tmp_path / "checkpoint_latest")
+    make(rolling + ".new", 1)
+    _swap_in(rolling + ".new", rolling)
+    assert epoch_of(rolling) == 1 and not os.path.exists(rolling + ".new")
+    # Interrupted after the old checkpoint was retired, before the new one moved in: the staged one is whole.
+    make(rolling + ".new", 2)
+    os.rename(rolling, rolling + ".old")
+    _recover_rolling(rolling)
+    assert epoch_of(rolling) == 2
+    # Interrupted while staging (no loop state yet): the retired checkpoint comes back.
+    shutil.rmtree(rolling + ".old", ignore_errors=True)
+    os.rename(rolling, rolling + ".old")
+    os.makedirs(rolling + ".new")
+    with open(os.path.join(rolling + ".new", "model.safetensors"), "w") as f:
+        f.write("weights 3")
+    _recover_rolling(rolling)
+    assert epoch_of(rolling) == 2
+
+
+def test_safetensors_write_replaces_the_file_whole(tmp_path):
+    """Written beside the target and moved over it (SafetensorsWriter.cs:46-58): no .tmp remains and the
+    file reads back."""
+    from laya_amd.safetensors_io import SafetensorsFile, write
+    path = str(tmp_path / "t.safetensors")
+    write(path, [("a", (2, 3), np.arange(6, dtype=np.float32), "F32")])
+    write(path, [("b", (4,), np.ones(4, np.float32), "BF16")])
+    assert not os.path.exists(path + ".tmp")
+    st = SafetensorsFile(path)
+    assert list(st.entries) == ["b"]
+    np.testing.assert_array_equal(st.read_float32("b"), np.ones(4, np.float32))
