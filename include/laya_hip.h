@@ -118,6 +118,16 @@ int laya_layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const flo
 int laya_layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
                        float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd);
 
+/* laya_layernorm_bwd with no allocation. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, results bit-identical to laya_layernorm_bwd; its dγ/dβ partials live in a
+ * static device array of 8 MiB (512 blocks × 2048 columns × 2 floats) that each GPU holds until the
+ * process ends, so n is limited to a multiple of 4 of at most 2048 (rows unlimited). Calls that overlap
+ * on one GPU (two contexts or streams at once) race on that array. */
+int laya_layernorm_bwd_noalloc(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
+                               const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
+                               const float* rstd);
+
 /* SimdOps.Gelu (SimdOps.cs:305-323), exact erf GELU: y = gelu(x). y may alias x. */
 int laya_gelu_fwd(laya_ctx* ctx, const float* x, size_t n, float* y);
 /* Ops.GeluBackward (Ops.cs:194-218): grad *= Φ(u) + u·φ(u) (in place). */

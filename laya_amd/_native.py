@@ -95,6 +95,7 @@ SIGNATURES = {
     "laya_linear_bwd": (c_int, [P, P, P, c_int, c_int, c_int, P, P, P, P]),
     "laya_layernorm_fwd": (c_int, [P, P, c_int, c_int, P, P, c_float, P, P, P]),
     "laya_layernorm_bwd": (c_int, [P, P, c_int, c_int, P, c_float, P, P, P, P, P, P]),
+    "laya_layernorm_bwd_noalloc": (c_int, [P, P, c_int, c_int, P, c_float, P, P, P, P, P, P]),
     "laya_gelu_fwd": (c_int, [P, P, c_size, P]),
     "laya_gelu_bwd": (c_int, [P, P, P, c_size]),
     "laya_geglu_fwd": (c_int, [P, P, c_int, c_int, P]),

@@ -73,7 +73,7 @@ void profile_rename(const char* name) {
 ProfileScope::ProfileScope(laya_ctx* c, const char* n, double f, double b)
     : ctx(c), name(n), flops(f), bytes(b), outer(g_scope) {
     g_scope = this;
-    if (!ctx->profiling) return;
+    if (!ctx->profiling || !name) return;
     start = take_event(ctx);
     LAYA_HIP(hipEventRecord(ctx->event_pool[start], ctx->stream));
 }
@@ -137,6 +137,7 @@ int laya_ctx_create(int device, laya_ctx** out) {
         LAYA_HIP(hipGetDeviceCount(&count));
         LAYA_REQUIRE(device >= 0 && device < count, "device index out of range");
         LAYA_HIP(hipSetDevice(device));
+        noalloc_scratch_init(device);
         auto* c = new laya_ctx();
         c->device = device;
         LAYA_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
@@ -372,6 +373,18 @@ int laya_layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const flo
         LAYA_REQUIRE(rows >= 0 && x && w && dy && dx, "layernorm_bwd: bad arguments");
         LAYA_REQUIRE((mean == nullptr) == (rstd == nullptr), "layernorm_bwd: pass both mean and rstd, or neither");
         layernorm_bwd(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd);
+    });
+}
+
+int laya_layernorm_bwd_noalloc(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
+                               const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
+                               const float* rstd) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && x && w && dy && dx, "layernorm_bwd_noalloc: bad arguments");
+        LAYA_REQUIRE((mean == nullptr) == (rstd == nullptr),
+                     "layernorm_bwd_noalloc: pass both mean and rstd, or neither");
+        layernorm_bwd_noalloc(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd);
     });
 }
 

@@ -222,6 +222,13 @@ void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
                    float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
                    const int* gather_ids = nullptr);
 
+// The allocation-free LayerNorm backward: partials in a static device array whose per-device address
+// noalloc_scratch_init resolves once (laya_ctx_create calls it with the device current).
+void noalloc_scratch_init(int device);
+void layernorm_bwd_noalloc(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
+                           const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
+                           const float* rstd);
+
 struct AttentionArgs {
     const float* qkv;
     const int* seg_start;

@@ -12,6 +12,8 @@
 // partials in wave order. Bytes per row: x, dy, dx in, dx out = 16·n.
 #include "elementwise.hpp"
 
+#include <mutex>
+
 namespace laya {
 namespace {
 
@@ -236,6 +238,9 @@ __global__ __launch_bounds__(RED_COLS* RED_GROUPS) void partial_reduce_kernel(co
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Blocks of four waves for a backward over `rows` rows: at most 2048 waves, rows dealt round-robin.
+int ln_bwd_blocks(int rows) { return (std::min(rows, 2048) + 3) / 4; }
+
 int chunks_for(int n) {
     LAYA_REQUIRE(n > 0 && n % 4 == 0, "layernorm: the row width must be a positive multiple of 4");
     const int nch = (n + 255) / 256;
@@ -263,34 +268,39 @@ void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
     check_launch("ln_fwd_kernel");
 }
 
-void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
-                   float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
-                   const int* gather_ids) {
+// The backward with its dγ/dβ partials in `ws` (2·blocks·n floats, or null for the context's workspace).
+// `profile`: bracket the launch for the live profile (events may be created on first use).
+static void layernorm_bwd_impl(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
+                               const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
+                               const float* rstd, const int* gather_ids, float* ws, bool profile) {
     if (rows <= 0) return;
     const int nch = chunks_for(n);
     const int gather_rows = gather_ids ? INT32_MAX : 0;
     // A fixed row → wave assignment (wave w takes rows w, w + W, …) keeps dγ/dβ independent of timing.
-    const int waves = (std::min(rows, 2048) + 3) / 4 * 4;
-    const int blocks = waves / 4;
+    const int blocks = ln_bwd_blocks(rows);
+    const int waves = 4 * blocks;
     float* pg = nullptr;
     float* pb = nullptr;
     if (dgamma || dbeta) {
-        float* ws = static_cast<float*>(ctx->workspace(2, sizeof(float) * 2 * (size_t)blocks * n));
+        if (!ws) ws = static_cast<float*>(ctx->workspace(2, sizeof(float) * 2 * (size_t)blocks * n));
         if (dgamma) pg = ws;
         if (dbeta) pb = ws + (size_t)blocks * n;
     }
     const size_t lds = (pg || pb) ? sizeof(float) * 8 * (size_t)n : 0;
     dim3 grid(blocks), block(256);
-    ProfileScope scope(ctx, "layernorm_bwd", 0.0, (16.0 * n + (mean ? 8.0 : 0.0)) * rows + 4.0 * n);
+    {
+        ProfileScope scope(ctx, profile ? "layernorm_bwd" : nullptr, 0.0,
+                           (16.0 * n + (mean ? 8.0 : 0.0)) * rows + 4.0 * n);
 #define LN_BWD(C)                                                                                                \
     case C:                                                                                                      \
         hipLaunchKernelGGL(ln_bwd_kernel<C>, grid, block, lds, ctx->stream, x, rows, n, w, eps, dy, dx, mean,  \
                            rstd, gather_ids, gather_rows, waves, pg, pb);                                        \
         break;
-    switch (nch) { LN_BWD(1) LN_BWD(2) LN_BWD(3) LN_BWD(4) LN_BWD(5) LN_BWD(6) LN_BWD(7) LN_BWD(8) }
+        switch (nch) { LN_BWD(1) LN_BWD(2) LN_BWD(3) LN_BWD(4) LN_BWD(5) LN_BWD(6) LN_BWD(7) LN_BWD(8) }
 #undef LN_BWD
-    check_launch("ln_bwd_kernel");
-    if (n % 4 == 0) {  // workspace partials are 256-byte aligned; the parameter gradients 16-byte aligned
+        check_launch("ln_bwd_kernel");
+    }
+    if (n % 4 == 0) {  // the partials are 16-byte aligned (workspace and scratch); the parameter gradients may not be
         if (pg && aligned16(dgamma)) {
             column_reduce(ctx, pg, blocks, n, dgamma);
             pg = nullptr;
@@ -309,6 +319,54 @@ void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
         hipLaunchKernelGGL(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pb, blocks, n, dbeta);
         check_launch("partial_reduce_kernel");
     }
+}
+
+void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
+                   float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
+                   const int* gather_ids) {
+    layernorm_bwd_impl(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, gather_ids, nullptr, true);
+}
+
+// ------------------------------------------------------------------ the allocation-free variant
+//
+// laya_layernorm_bwd_noalloc keeps its dγ/dβ partials in this file-scope device array instead of the
+// context's workspace: at most 512 blocks × 2048 columns × (γ, β) floats, 8 MiB, which every GPU the
+// library runs on holds until the process ends. The kernel writes every partial it later reads, so
+// nothing in it needs clearing between calls; calls that overlap on one GPU (two streams) race on it.
+constexpr size_t NOALLOC_SCRATCH_FLOATS = 2u * 512u * 2048u;
+static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_FLOATS];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[NOALLOC_MAX_DEVICES] = {};
+}  // namespace
+
+void noalloc_scratch_init(int device) {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    LAYA_REQUIRE(device >= 0 && device < NOALLOC_MAX_DEVICES, "noalloc scratch: device index out of range");
+    if (g_scratch_ptr[device]) return;
+    void* p = nullptr;
+    // The array's name is a host-side stand-in; its device address on the current device comes from here.
+    LAYA_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[device] = static_cast<float*>(p);
+}
+
+void layernorm_bwd_noalloc(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
+                           const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
+                           const float* rstd) {
+    LAYA_REQUIRE(n > 0 && n <= 2048 && n % 4 == 0,
+                 "layernorm_bwd_noalloc: the row width must be a multiple of 4 of at most 2048 (the partials of "
+                 "its static scratch are sized for 512 blocks of 2048 columns)");
+    float* ws = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        ws = ctx->device >= 0 && ctx->device < NOALLOC_MAX_DEVICES ? g_scratch_ptr[ctx->device] : nullptr;
+    }
+    if (!ws) throw Error(LAYA_ERR_STATE, "layernorm_bwd_noalloc: the scratch address of this device is not set up");
+    LAYA_REQUIRE(2 * (size_t)ln_bwd_blocks(rows) * n <= NOALLOC_SCRATCH_FLOATS,
+                 "layernorm_bwd_noalloc: partials exceed the static scratch");
+    layernorm_bwd_impl(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, nullptr, ws, false);
 }
 
 }  // namespace laya
