@@ -270,6 +270,12 @@ int laya_model_set_head_dropout(laya_model* model, float p);
 /* Forward (TrainableDecisionModel.cs:248-353). Keeps every activation the backward needs resident
  * in HBM (no recompute). logits_host (may be NULL) receives Σ n_options floats and synchronises. */
 int laya_model_forward(laya_model* model, const laya_batch* batch, int training, uint64_t seed, float* logits_host);
+/* DecisionModel.ReadOut (src/StructuredDecisions.Laya/Models/DecisionModel.cs:170-226) for every item of
+ * the last forward, on the device: the option logits (logits_host, Σ n_options floats, may be NULL), the
+ * action probabilities act_probs_host [n_items][n_act] from the act head on [h[start], top1, top1 − top2,
+ * normalised entropy, K/255], and those four calibration features (features_host [n_items][4], may be
+ * NULL). DecisionModel.Forward's outputs for a batch = laya_model_forward (training 0) + this. Synchronises. */
+int laya_model_readout(laya_model* model, float* logits_host, float* act_probs_host, float* features_host);
 /* Backward (TrainableDecisionModel.cs:479-549): dlogits_host has Σ n_options floats. */
 int laya_model_backward(laya_model* model, const float* dlogits_host);
 /* Gradients.ClipByGlobalNorm (AdamW.cs:103-130); norm_out (may be NULL) synchronises, and then a NaN or

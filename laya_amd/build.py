@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "liblaya_hip.so")
-SOURCES = ["gemm.hip", "norm.hip", "attention.hip", "elementwise.hip", "optim.hip", "objective.hip", "capi.cpp", "model.cpp"]
+SOURCES = ["gemm.hip", "norm.hip", "attention.hip", "elementwise.hip", "optim.hip", "objective.hip", "readout.hip", "capi.cpp", "model.cpp"]
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
          "-packed-fp32-ops", "-Wall", "-Wno-unused-function", "-Wno-unused-result"]

@@ -80,7 +80,7 @@ struct laya_ctx {
     hipStream_t stream = nullptr;
     size_t cap = 0, in_use = 0;
     std::unordered_map<void*, size_t> allocations;
-    laya::Workspace scratch[8];
+    laya::Workspace scratch[9];
     hipEvent_t timers[16][2] = {};
     int cu_count = 256;
     bool profiling = false;
@@ -218,6 +218,25 @@ void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out);
 void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps, float* y,
                    float* mean, float* rstd, const int* gather_ids = nullptr, const float* add_table = nullptr,
                    const int* add_index = nullptr);
+// Column sums whose reduction is deferred: `count` partial rows of `n` floats in `part`, added into `out`.
+struct ColumnSumJob {
+    const float* part;
+    float* out;
+    int count, n;
+};
+constexpr int MAX_COLUMN_JOBS = 96;  // 2.3 KB of kernel arguments
+struct ColumnSumJobs {
+    int n = 0;
+    ColumnSumJob job[MAX_COLUMN_JOBS];
+};
+
+// LayerNorm backward whose dγ/dβ partials go to `ws` (2 · ln_bwd_partial_rows(rows) · n floats) and whose
+// reduction is appended to `jobs` instead of launched (the caller runs column_reduce_batch later; a full
+// list is flushed first). Falls back to the immediate reduction when a gradient is not 16-byte aligned.
+int ln_bwd_partial_rows(int rows);
+void layernorm_bwd_deferred(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
+                            const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
+                            const float* rstd, const int* gather_ids, float* ws, ColumnSumJobs& jobs);
 void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
                    float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
                    const int* gather_ids = nullptr);
@@ -258,6 +277,11 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
 void rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets, const int* offsets, const int* qtypes,
                     int n_items, int total_options, int max_options, int groups, const double* draws, double sigma,
                     double spherical, double rps, double ce_weight, double scale, float* grad, double* losses);
+// DecisionModel.ReadOut (DecisionModel.cs:170-226) per item: probs [n_items][na], features [n_items][4]
+// (may be null); states are the head output rows, opt_off [n_items + 1] the items' option offsets.
+void decision_readout(laya_ctx* ctx, const float* scores, const int* opt_off, const int* seg_start, int n_items,
+                      const float* states, int d, const float* w1, const float* b1, int a1, const float* w2,
+                      const float* b2, int na, float* probs, float* features);
 // rows: the number of rows of qkv / context / dcontext (the dO·O row constants span all of them).
 void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,
                    const float* dcontext, float* dqkv);

@@ -304,6 +304,30 @@ __global__ __launch_bounds__(256) void colsum_reduce4_kernel(const f32x4* __rest
     }
 }
 
+// The same reduction for a batch of independent column sums in one launch: blockIdx.y picks the job.
+__global__ __launch_bounds__(256) void colsum_reduce4_multi_kernel(ColumnSumJobs jobs) {
+    const ColumnSumJob j = jobs.job[blockIdx.y];
+    const int w4 = j.n / 4;
+    if ((int)blockIdx.x * 16 >= w4) return;  // block-uniform
+    __shared__ f32x4 red[16][16];
+    const f32x4* part = reinterpret_cast<const f32x4*>(j.part);
+    const int lc = threadIdx.x & 15, ph = threadIdx.x >> 4;
+    const int c = blockIdx.x * 16 + lc;
+    f32x4 s = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (c < w4) {
+#pragma unroll 4
+        for (int k = ph; k < j.count; k += 16) s += part[(long)k * w4 + c];
+    }
+    red[ph][lc] = s;
+    __syncthreads();
+    if (ph == 0 && c < w4) {
+        f32x4 t = red[0][lc];
+#pragma unroll
+        for (int q = 1; q < 16; ++q) t += red[q][lc];
+        reinterpret_cast<f32x4*>(j.out)[c] += t;
+    }
+}
+
 // Soft cross-entropy gradient (RlcdObjective.cs:139-150): one thread per item computes its options'
 // gradient and its loss term; the terms are then added in item order by one thread (a fixed order).
 constexpr int CE_THREADS = 256;
@@ -508,6 +532,21 @@ void column_reduce(laya_ctx* ctx, const float* part, int count, int n, float* ou
     hipLaunchKernelGGL(colsum_reduce4_kernel, dim3((w4 + 15) / 16), dim3(256), 0, ctx->stream,
                        reinterpret_cast<const f32x4*>(part), count, w4, reinterpret_cast<f32x4*>(out));
     check_launch("colsum_reduce4_kernel");
+}
+void column_reduce_batch(laya_ctx* ctx, const ColumnSumJobs& jobs) {
+    if (jobs.n <= 0) return;
+    int max_w4 = 0;
+    for (int i = 0; i < jobs.n; ++i) {
+        const ColumnSumJob& j = jobs.job[i];
+        LAYA_REQUIRE(j.n % 4 == 0 && vec4(j.part) && vec4(j.out) && j.count > 0,
+                     "column_reduce_batch: 16-byte aligned rows of a multiple of 4");
+        max_w4 = std::max(max_w4, j.n / 4);
+    }
+    double bytes = 0;
+    for (int i = 0; i < jobs.n; ++i) bytes += 4.0 * jobs.job[i].n * (jobs.job[i].count + 2);
+    ProfileScope scope(ctx, "column_sums_deferred", 0.0, bytes);
+    hipLaunchKernelGGL(colsum_reduce4_multi_kernel, dim3((max_w4 + 15) / 16, jobs.n), dim3(256), 0, ctx->stream, jobs);
+    check_launch("colsum_reduce4_multi_kernel");
 }
 void rotary_apply(laya_ctx* ctx, const float* cos_t, const float* sin_t, int head_dim, float* vec, int rows,
                   const int* pos, int inverse) {

@@ -32,6 +32,8 @@ void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g,
 void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_type, int types, float* out, int slot);
 // out[c] += Σ_k part[k][c] for count partial rows of width n, in a fixed order.
 void column_reduce(laya_ctx* ctx, const float* part, int count, int n, float* out);
+// Several column reductions out[c] += Σ_k part[k][c] in one launch (each in column_reduce's order).
+void column_reduce_batch(laya_ctx* ctx, const ColumnSumJobs& jobs);
 void softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets, const int* offsets, int n_items,
                     float ce_weight, float scale, float* grad, float* loss);
 void init_param(laya_ctx* ctx, float* dst, size_t n, int kind, float std, uint64_t seed);

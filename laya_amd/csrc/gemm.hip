@@ -1245,7 +1245,8 @@ __device__ __forceinline__ void write_partial_w(float* slot, const f32x16 (&acc)
 
 // nn and tn carry wide tile counts (tiles_m, tiles_n of 256 x 256 tiles); s counts 16-deep units.
 // NP = 3: split products (fp32); NP = 1: bf16 products (the bf16 policies of both backward classes).
-template <int NP>
+// RES: dX = dY·W + nn.R (the residual may be dX itself: each element is read and written by one lane).
+template <int NP, bool RES>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParams nn, GemmParams tn, PairPlan s) {
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];
     const int g = xcd_logical_block();
@@ -1271,9 +1272,9 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
             cs.m0 = c.m0 + 128 * h;
             if (cs.m0 >= nn.M) break;
             if (cs.m0 + 128 <= nn.M && c.n0 + WT <= nn.N)
-                store_acc<true, true, STORE, false, false, true>(nn, cs, acc[h], wm, wn, lr, kh);
+                store_acc<true, true, STORE, RES, false, true>(nn, cs, acc[h], wm, wn, lr, kh);
             else
-                store_acc<true, true, STORE, false, true, true>(nn, cs, acc[h], wm, wn, lr, kh);
+                store_acc<true, true, STORE, RES, true, true>(nn, cs, acc[h], wm, wn, lr, kh);
         }
     }
     const int lo = plan_tn_lo(s, g), hi = plan_tn_lo(s, g + 1);
@@ -1957,7 +1958,7 @@ bool make_pair_plan_wide(const laya_ctx* ctx, int n0, int out, int n1, int rows,
 // The wide pair for split products: dX without residual, dX's K a multiple of 16, dY k-contiguous in
 // float4s. Returns false (nothing launched) when the wide plan does not apply.
 bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out, bool half) {
-    if (nn.R || out % BKQ != 0 || !operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) return false;
+    if (out % BKQ != 0 || !operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) return false;
     const long lim = 1L << 31;  // buffer offsets of dY, W and x
     if ((long)rows * out * 4 >= lim || (long)out * in * 4 >= lim || (long)rows * in * 4 >= lim) return false;
     nn.tiles_m = (rows + WT - 1) / WT;
@@ -1971,10 +1972,15 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
     {
         ProfileScope scope(ctx, half ? "gemm_bwd_pair_bf16w" : "gemm_bwd_pair_x6w",
                            2.0 * 2.0 * rows * (double)in * out, 0.0);
-        if (half)
-            hipLaunchKernelGGL(gemm_pair_wide_kernel<1>, dim3(s.G), dim3(WT_THREADS), 0, ctx->stream, nn, tn, s);
+        const dim3 g(s.G), b(WT_THREADS);
+        if (half && nn.R)
+            hipLaunchKernelGGL((gemm_pair_wide_kernel<1, true>), g, b, 0, ctx->stream, nn, tn, s);
+        else if (half)
+            hipLaunchKernelGGL((gemm_pair_wide_kernel<1, false>), g, b, 0, ctx->stream, nn, tn, s);
+        else if (nn.R)
+            hipLaunchKernelGGL((gemm_pair_wide_kernel<3, true>), g, b, 0, ctx->stream, nn, tn, s);
         else
-            hipLaunchKernelGGL(gemm_pair_wide_kernel<3>, dim3(s.G), dim3(WT_THREADS), 0, ctx->stream, nn, tn, s);
+            hipLaunchKernelGGL((gemm_pair_wide_kernel<3, false>), g, b, 0, ctx->stream, nn, tn, s);
         check_launch("gemm_pair_wide_kernel");
     }
     long partials = 0, shared = 0;

@@ -152,6 +152,11 @@ struct laya_model {
     // passed by value; `cur` is what the kernels read (own, or a staged batch's tables)
     BatchTables own{}, cur{};
     std::vector<StagedBatch> staged;  // laya_model_stage_batch slots; a null block marks a free slot
+    // LayerNorm dγ/dβ partials of one backward (a slice per LayerNorm) and their deferred reductions, run
+    // as one launch at the end of the backward
+    float* ln_part = nullptr;
+    size_t ln_part_cap = 0, ln_part_used = 0;
+    ColumnSumJobs ln_jobs;
     // optimizer scalars
     double* d_norm = nullptr;
     float* d_coef = nullptr;
@@ -188,6 +193,11 @@ struct laya_model {
     }
 
     float* W(int i) const { return i >= 0 ? P + params[i].offset : nullptr; }
+    int find(const std::string& name) const {
+        auto it = by_name.find(name);
+        if (it == by_name.end()) throw laya::Error(LAYA_ERR_MISSING, "the model has no '" + name + "' tensor");
+        return it->second;
+    }
     // Parameter.GradientBuffer (Parameter.cs:177): the gradient of a trainable parameter, else null.
     float* Gt(int i) {
         if (i < 0 || !params[i].trainable) return nullptr;
@@ -598,6 +608,22 @@ void forward(laya_model* m, bool train, uint64_t seed) {
     m->has_tape = true;
 }
 
+// Ops.LayerNormBackward with its dγ/dβ reduction deferred to the end of the backward.
+void ln_backward(laya_model* m, const float* x, int rows, int n, int w, int b, float eps, const float* dy, float* dx,
+                 const float* mean, const float* rstd, const int* gather_ids = nullptr) {
+    float* dg = m->Gt(w);
+    float* db = m->Gt(b);
+    float* ws = nullptr;
+    if (dg || db) {
+        const size_t need = 2 * (size_t)ln_bwd_partial_rows(rows) * n;
+        LAYA_REQUIRE(m->ln_part_used + need <= m->ln_part_cap, "layernorm partials: buffer too small");
+        ws = m->ln_part + m->ln_part_used;
+        m->ln_part_used += (need + 63) / 64 * 64;
+    }
+    layernorm_bwd_deferred(m->ctx, x, rows, n, m->W(w), eps, dy, dx, dg, db, mean, rstd, gather_ids,
+                           ws ? ws : m->ln_part, m->ln_jobs);
+}
+
 // EncoderLayerBackward (TrainableDecisionModel.cs:551-603); dS holds dOutput and becomes dx.
 void encoder_backward(laya_model* m, int l, bool need_input) {
     laya_ctx* ctx = m->ctx;
@@ -608,8 +634,7 @@ void encoder_backward(laya_model* m, int l, bool need_input) {
     linear_backward(m, a.act, m->dS, T, I, d, L.mlp_wo, L.mlp_wo_b, m->dact);
     geglu_bwd(ctx, a.wide, m->dact, T, I, m->dwide);
     linear_backward(m, a.mlpn, m->dwide, T, d, 2 * I, L.wi, L.wi_b, m->dn);
-    layernorm_bwd(ctx, a.res, T, d, m->W(L.mlp_norm), eps, m->dn, m->dS, m->Gt(L.mlp_norm), m->Gt(L.mlp_norm_b),
-                  a.mean2, a.rstd2);
+    ln_backward(m, a.res, T, d, L.mlp_norm, L.mlp_norm_b, eps, m->dn, m->dS, a.mean2, a.rstd2);
     linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx);
     attention_bwd(ctx, enc_attention(m, a.qkv, L.kind), T, a.ctx, a.lse, m->dctx, m->dqkv);
     const float* normed = L.attn_norm >= 0 ? a.normed : a.x;
@@ -622,8 +647,7 @@ void encoder_backward(laya_model* m, int l, bool need_input) {
         linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dS, m->dS);
     } else {
         linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dn);
-        layernorm_bwd(ctx, a.x, T, d, m->W(L.attn_norm), eps, m->dn, m->dS, m->Gt(L.attn_norm), m->Gt(L.attn_norm_b),
-                      a.mean1, a.rstd1);
+        ln_backward(m, a.x, T, d, L.attn_norm, L.attn_norm_b, eps, m->dn, m->dS, a.mean1, a.rstd1);
     }
 }
 
@@ -646,8 +670,7 @@ void head_backward(laya_model* m, int j) {
     else
         relu_dropout_bwd(ctx, a.wide, m->dact, (size_t)T * ff, p, salt(m->seed, j, 2));
     linear_backward(m, a.n2, m->dact, T, d, ff, H.linear1, H.linear1_b, m->dn);
-    layernorm_bwd(ctx, a.res, T, d, m->W(H.norm2), 1e-5f, m->dn, m->dS, m->Gt(H.norm2), m->Gt(H.norm2_b), a.mean2,
-                  a.rstd2);
+    ln_backward(m, a.res, T, d, H.norm2, H.norm2_b, 1e-5f, m->dn, m->dS, a.mean2, a.rstd2);
     const float* datt = m->dS;
     if (p > 0.0f) {
         dropout_copy(m, m->dS, m->dy, nd, p, salt(m->seed, j, 1));
@@ -656,13 +679,34 @@ void head_backward(laya_model* m, int j) {
     linear_backward(m, a.ctx, datt, T, d, d, H.out_proj, H.out_proj_b, m->dctx);
     attention_bwd(ctx, head_attention(m, a.qkv, j, p, m->seed), T, a.ctx, a.lse, m->dctx, m->dqkv);
     linear_backward(m, a.n1, m->dqkv, T, d, 3 * d, H.in_proj, H.in_proj_b, m->dn);
-    layernorm_bwd(ctx, a.x, T, d, m->W(H.norm1), 1e-5f, m->dn, m->dS, m->Gt(H.norm1), m->Gt(H.norm1_b), a.mean1,
-                  a.rstd1);
+    ln_backward(m, a.x, T, d, H.norm1, H.norm1_b, 1e-5f, m->dn, m->dS, a.mean1, a.rstd1);
 }
 
-// Backward (TrainableDecisionModel.cs:479-549), from dscores already on the device.
+void backward_body(laya_model* m);
+
+// Backward (TrainableDecisionModel.cs:479-549), from dscores already on the device. The LayerNorm dγ/dβ
+// partials of every site are reduced in one launch at the end (each in its fixed order).
 void backward(laya_model* m) {
     LAYA_REQUIRE(m->has_tape, "backward: run forward first");
+    const int d = m->d();
+    const size_t sites = 2 * (size_t)m->cfg.layers + 2 * (size_t)m->cfg.head_layers + 3;
+    const size_t need = sites * ((2 * (size_t)ln_bwd_partial_rows(std::max(m->T, m->nmark)) * d + 63) / 64 * 64);
+    if (need > m->ln_part_cap) {
+        if (m->ln_part) m->ctx->release(m->ln_part);
+        m->ln_part = nullptr;
+        m->ln_part_cap = 0;
+        const size_t cap = sites * ((2 * (size_t)ln_bwd_partial_rows(1 << 30) * d + 63) / 64 * 64);
+        m->ln_part = static_cast<float*>(m->ctx->alloc(sizeof(float) * cap));
+        m->ln_part_cap = cap;
+    }
+    m->ln_part_used = 0;
+    m->ln_jobs.n = 0;
+    backward_body(m);
+    column_reduce_batch(m->ctx, m->ln_jobs);
+    m->ln_jobs.n = 0;
+}
+
+void backward_body(laya_model* m) {
     laya_ctx* ctx = m->ctx;
     const int T = m->T, d = m->d(), M = m->nmark;
     const float eps = m->cfg.norm_eps;
@@ -670,8 +714,7 @@ void backward(laya_model* m) {
     gelu_bwd(ctx, m->s_pre, m->ds_act, (size_t)M * d);
     linear_backward(m, m->s_norm, m->ds_act, M, d, d, m->sc1, m->sc1_b, m->ds_norm);
     fill(ctx, m->ds_mark, 0.0f, (size_t)M * d);
-    layernorm_bwd(ctx, m->s_in, M, d, m->W(m->sc_norm), 1e-5f, m->ds_norm, m->ds_mark, m->Gt(m->sc_norm),
-                  m->Gt(m->sc_norm_b), m->s_mean, m->s_rstd);
+    ln_backward(m, m->s_in, M, d, m->sc_norm, m->sc_norm_b, 1e-5f, m->ds_norm, m->ds_mark, m->s_mean, m->s_rstd);
     fill(ctx, m->dS, 0.0f, (size_t)T * d);
     scatter_add_rows(ctx, m->ds_mark, m->cur.marker_rows, M, d, m->dS);
     for (int j = m->cfg.head_layers - 1; j >= 0; --j) head_backward(m, j);
@@ -679,15 +722,14 @@ void backward(laya_model* m) {
         type_embedding_bwd(ctx, m->dS, m->cur.row_type, T, d, g);
     if (m->first_trainable >= m->cfg.layers) return;  // the encoder is frozen
     fill(ctx, m->dE, 0.0f, (size_t)T * d);
-    layernorm_bwd(ctx, m->x_final, T, d, m->W(m->final_norm), eps, m->dS, m->dE, m->Gt(m->final_norm),
-                  m->Gt(m->final_norm_b), m->fin_mean, m->fin_rstd);
+    ln_backward(m, m->x_final, T, d, m->final_norm, m->final_norm_b, eps, m->dS, m->dE, m->fin_mean, m->fin_rstd);
     std::swap(m->dS, m->dE);
     for (int l = m->cfg.layers - 1; l >= m->first_trainable; --l)
         encoder_backward(m, l, l > m->first_trainable || m->embeddings_trainable);
     if (m->embeddings_trainable && m->first_trainable == 0) {
         fill(ctx, m->dE, 0.0f, (size_t)T * d);
-        layernorm_bwd(ctx, m->W(m->tok_emb), T, d, m->W(m->emb_norm), eps, m->dS, m->dE, m->Gt(m->emb_norm),
-                      m->Gt(m->emb_norm_b), m->emb_mean, m->emb_rstd, m->cur.tokens);
+        ln_backward(m, m->W(m->tok_emb), T, d, m->emb_norm, m->emb_norm_b, eps, m->dS, m->dE, m->emb_mean, m->emb_rstd,
+                    m->cur.tokens);
         if (float* g = m->Gt(m->tok_emb))
             embedding_bwd(ctx, m->cur.sorted, m->cur.unique, m->cur.uoff, m->n_unique, m->dE, d, g);
     }
@@ -797,7 +839,7 @@ int laya_model_destroy(laya_model* m) {
             if (p) ctx->release(p);
         for (auto& s : m->staged)
             if (s.block) ctx->release(s.block);
-        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses})
+        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part})
             if (p) ctx->release(p);
         free_rotary(ctx, &m->rot_global);
         free_rotary(ctx, &m->rot_local);
@@ -928,6 +970,29 @@ int laya_model_forward(laya_model* m, const laya_batch* batch, int training, uin
                                     m->ctx->stream));
             LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
         }
+    });
+}
+
+int laya_model_readout(laya_model* m, float* logits_host, float* act_probs_host, float* features_host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(m->has_tape, "readout: run forward first");
+        LAYA_REQUIRE(act_probs_host, "readout: null output");
+        const int a1 = m->find("act_head.0.bias"), na_i = m->find("act_head.2.bias");
+        const int w1 = m->find("act_head.0.weight"), w2 = m->find("act_head.2.weight");
+        const int A1 = (int)m->params[a1].numel, NA = (int)m->params[na_i].numel, n = m->nseg;
+        float* out = static_cast<float*>(m->ctx->workspace(8, sizeof(float) * (size_t)std::max(1, n) * (NA + 4)));
+        decision_readout(m->ctx, m->scores, m->cur.opt_off, m->cur.seg_start, n, m->head_out, m->d(), m->W(w1),
+                         m->W(a1), A1, m->W(w2), m->W(na_i), NA, out, out + (size_t)n * NA);
+        LAYA_HIP(hipMemcpyAsync(act_probs_host, out, sizeof(float) * (size_t)n * NA, hipMemcpyDeviceToHost,
+                                m->ctx->stream));
+        if (features_host)
+            LAYA_HIP(hipMemcpyAsync(features_host, out + (size_t)n * NA, sizeof(float) * (size_t)n * 4,
+                                    hipMemcpyDeviceToHost, m->ctx->stream));
+        if (logits_host)
+            LAYA_HIP(hipMemcpyAsync(logits_host, m->scores, sizeof(float) * m->nmark, hipMemcpyDeviceToHost,
+                                    m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
     });
 }
 

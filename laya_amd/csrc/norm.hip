@@ -272,7 +272,8 @@ void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
 // `profile`: bracket the launch for the live profile (events may be created on first use).
 static void layernorm_bwd_impl(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
                                const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
-                               const float* rstd, const int* gather_ids, float* ws, bool profile) {
+                               const float* rstd, const int* gather_ids, float* ws, bool profile,
+                               ColumnSumJobs* defer = nullptr) {
     if (rows <= 0) return;
     const int nch = chunks_for(n);
     const int gather_rows = gather_ids ? INT32_MAX : 0;
@@ -301,16 +302,26 @@ static void layernorm_bwd_impl(laya_ctx* ctx, const float* x, int rows, int n, c
         check_launch("ln_bwd_kernel");
     }
     if (n % 4 == 0) {  // the partials are 16-byte aligned (workspace and scratch); the parameter gradients may not be
-        if (pg && aligned16(dgamma)) {
-            column_reduce(ctx, pg, blocks, n, dgamma);
-            pg = nullptr;
-        }
-        if (pb && aligned16(dbeta)) {
-            column_reduce(ctx, pb, blocks, n, dbeta);
-            pb = nullptr;
-        }
+        auto reduce = [&](float*& part, float* out) {
+            if (!part || !aligned16(out)) return;
+            if (defer) {
+                if (defer->n == MAX_COLUMN_JOBS) {
+                    column_reduce_batch(ctx, *defer);
+                    defer->n = 0;
+                }
+                defer->job[defer->n++] = ColumnSumJob{part, out, blocks, n};
+            } else {
+                ProfileScope scope(ctx, profile ? "layernorm_bwd_reduce" : nullptr, 0.0, 4.0 * n * (blocks + 2.0));
+                column_reduce(ctx, part, blocks, n, out);
+            }
+            part = nullptr;
+        };
+        reduce(pg, dgamma);
+        reduce(pb, dbeta);
     }
     const dim3 rgrid((n + RED_COLS - 1) / RED_COLS), rblock(RED_COLS * RED_GROUPS);
+    ProfileScope scope(ctx, (pg || pb) && profile ? "layernorm_bwd_reduce" : nullptr, 0.0,
+                       4.0 * n * (blocks + 2.0) * ((pg ? 1 : 0) + (pb ? 1 : 0)));
     if (pg) {
         hipLaunchKernelGGL(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pg, blocks, n, dgamma);
         check_launch("partial_reduce_kernel");
@@ -325,6 +336,15 @@ void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
                    float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
                    const int* gather_ids) {
     layernorm_bwd_impl(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, gather_ids, nullptr, true);
+}
+
+int ln_bwd_partial_rows(int rows) { return ln_bwd_blocks(std::max(rows, 1)); }
+
+void layernorm_bwd_deferred(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
+                            const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
+                            const float* rstd, const int* gather_ids, float* ws, ColumnSumJobs& jobs) {
+    LAYA_REQUIRE(ws != nullptr, "layernorm_bwd_deferred: no partial buffer");
+    layernorm_bwd_impl(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, gather_ids, ws, true, &jobs);
 }
 
 // ------------------------------------------------------------------ the allocation-free variant

@@ -104,38 +104,52 @@ __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, float
     }
 }
 
-// The same update on float4s: every group bound is a multiple of 4 (in float4 units here).
+// The same update on float4s: every group bound is a multiple of 4 (in float4 units here). The arena is
+// streamed once: non-temporal loads and stores (no cache allocation) and one float4 of each stream per
+// thread, the grid covering the arena (measured on 164M parameters: 5.98 TB/s against 4.7 for a
+// grid-stride loop over 8192 workgroups with cached accesses).
+__device__ __forceinline__ void adam4(f32x4& wo, f32x4& mo, f32x4& vo, f32x4 pi, f32x4 gi, f32x4 mi0, f32x4 vi0,
+                                      float cf, float decay, float step, float b1, float b2, float eps,
+                                      float sqrt_c2) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float gs = gi[e] * cf;
+        float w = pi[e] * decay;
+        const float mi = b1 * mi0[e] + (1.0f - b1) * gs;
+        const float vi = b2 * vi0[e] + (1.0f - b2) * gs * gs;
+        w -= step * mi / (sqrtf(vi) / sqrt_c2 + eps);
+        wo[e] = w;
+        mo[e] = mi;
+        vo[e] = vi;
+    }
+}
+
+__device__ __forceinline__ int adam_group(const AdamGroups& groups, size_t i) {
+    int grp = -1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (k < groups.n && i >= groups.begin[k] && i < groups.end[k]) grp = k;
+    return grp;
+}
+
 __global__ __launch_bounds__(256) void adamw4_kernel(f32x4* __restrict__ p, f32x4* __restrict__ g,
                                                      f32x4* __restrict__ m, f32x4* __restrict__ v, size_t n4,
                                                      AdamGroups groups, float b1, float b2, float eps, float sqrt_c2,
                                                      const float* coef, int zero_grads) {
     const float cf = coef ? *coef : 1.0f;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
-        int grp = -1;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (k < groups.n && i >= groups.begin[k] && i < groups.end[k]) grp = k;
-        const f32x4 gi = g[i];
+        const int grp = adam_group(groups, i);
+        const f32x4 gi = __builtin_nontemporal_load(g + i);
         if (grp >= 0) {
-            const f32x4 pi = p[i], mi0 = m[i], vi0 = v[i];
-            const float decay = groups.decay[grp], step = groups.step_size[grp];
             f32x4 wo, mo, vo;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float gs = gi[e] * cf;
-                float w = pi[e] * decay;
-                const float mi = b1 * mi0[e] + (1.0f - b1) * gs;
-                const float vi = b2 * vi0[e] + (1.0f - b2) * gs * gs;
-                w -= step * mi / (sqrtf(vi) / sqrt_c2 + eps);
-                wo[e] = w;
-                mo[e] = mi;
-                vo[e] = vi;
-            }
-            p[i] = wo;
-            m[i] = mo;
-            v[i] = vo;
+            adam4(wo, mo, vo, __builtin_nontemporal_load(p + i), gi, __builtin_nontemporal_load(m + i),
+                  __builtin_nontemporal_load(v + i), cf, groups.decay[grp], groups.step_size[grp], b1, b2, eps,
+                  sqrt_c2);
+            __builtin_nontemporal_store(wo, p + i);
+            __builtin_nontemporal_store(mo, m + i);
+            __builtin_nontemporal_store(vo, v + i);
         }
-        if (zero_grads) g[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (zero_grads) __builtin_nontemporal_store(f32x4{0.0f, 0.0f, 0.0f, 0.0f}, g + i);
     }
 }
 
@@ -177,7 +191,7 @@ void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n
             g4.begin[k] = groups.begin[k] / 4;
             g4.end[k] = groups.end[k] / 4;
         }
-        hipLaunchKernelGGL(adamw4_kernel, dim3(blocks_for(n / 4, 256, 8192)), dim3(256), 0, ctx->stream,
+        hipLaunchKernelGGL(adamw4_kernel, dim3(blocks_for(n / 4, 256, 1u << 22)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<f32x4*>(p), reinterpret_cast<f32x4*>(g), reinterpret_cast<f32x4*>(m),
                            reinterpret_cast<f32x4*>(v), n / 4, g4, beta1, beta2, eps, sqrt_c2, coef, zero_grads);
         check_launch("adamw4_kernel");

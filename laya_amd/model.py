@@ -254,6 +254,28 @@ class TrainableDecisionModel:
         self._batch = batch
         return None if logits is None else logits[:batch.n_markers]
 
+    def readout(self):
+        """DecisionModel.ReadOut (DecisionModel.cs:170-226) for every item of the last forward, on the device:
+        (per-item option logits, action probabilities [items, n_act], calibration features [items, 4] =
+        top1, top1 − top2, normalised entropy, K/255)."""
+        if self._batch is None:
+            raise RuntimeError("readout: run forward first")
+        b = self._batch
+        na = self.shapes["act_head.2.bias"][0]
+        logits = np.zeros(max(1, b.n_markers), np.float32)
+        probs = np.zeros((b.n_items, na), np.float32)
+        feats = np.zeros((b.n_items, 4), np.float32)
+        check(lib().laya_model_readout(self.handle, logits.ctypes.data, probs.ctypes.data, feats.ctypes.data))
+        offs = np.concatenate([[0], np.cumsum(b.n_options)])
+        return [logits[offs[i]:offs[i + 1]] for i in range(b.n_items)], probs, feats
+
+    def decide(self, items):
+        """DecisionModel.Forward (DecisionModel.cs:128-169) for a batch: the eval-mode forward and the read-out;
+        returns (option logits, action probabilities) per item, as DecisionOutput holds them."""
+        self.forward(items, training=False, want_logits=False)
+        logits, probs, _ = self.readout()
+        return [(lg, probs[i]) for i, lg in enumerate(logits)]
+
     def backward(self, logit_gradients) -> None:
         """Backward (TrainableDecisionModel.cs:479-549): per-option dL/dlogit, concatenated or per item."""
         if isinstance(logit_gradients, (list, tuple)):

@@ -61,6 +61,7 @@ def lib():
         L.orc_model_set_head_dropout.argtypes = [P, c_float]
         L.orc_model_forward.argtypes = [P, c_int, P, P, P, P, P, c_int, c_int, c_u64, P]
         L.orc_model_backward.argtypes = [P, P]
+        L.orc_model_readout.argtypes = [P, P, P, P]
         L.orc_model_clip.argtypes = [P, c_double]
         L.orc_model_clip.restype = c_double
         L.orc_model_adamw.argtypes = [P, c_double, c_double, c_double, c_double, c_double, c_double]
@@ -193,12 +194,25 @@ class OracleModel:
                                      ctypes.c_uint64(seed & (2**64 - 1)), ptr(logits))
         if rc != 0:
             raise RuntimeError(lib().orc_last_error().decode())
+        self._last_opts = np.asarray(batch.n_options)
         return logits
 
     def backward(self, dlogits: np.ndarray) -> None:
         d = np.ascontiguousarray(dlogits, dtype=np.float32)
         if lib().orc_model_backward(self._h, ptr(d)) != 0:
             raise RuntimeError(lib().orc_last_error().decode())
+
+    def readout(self):
+        """DecisionModel.ReadOut on the last forward: (action probabilities [items, n_act], features
+        [items, 4] = top1, top1 − top2, normalised entropy, K/255, pooled rows [items, d])."""
+        n = len(self._last_opts)
+        na = self.shapes["act_head.2.bias"][0]
+        probs = np.zeros((n, na), np.float32)
+        feats = np.zeros((n, 4), np.float32)
+        pooled = np.zeros((n, self.shapes["type_emb.weight"][1]), np.float64)
+        if lib().orc_model_readout(self._h, ptr(probs), ptr(feats), ptr(pooled)) != 0:
+            raise RuntimeError(lib().orc_last_error().decode())
+        return probs, feats, pooled
 
     def zero_grad(self) -> None:
         lib().orc_model_zero_grad(self._h)

@@ -513,6 +513,7 @@ struct ModelBase {
     virtual void forward(int n_items, const int* lengths, const int* tokens, const int* n_options, const int* markers,
                          const int* qtypes, bool training, bool keep_tape, u64 seed, double* logits) = 0;
     virtual void backward(const float* dlogits) = 0;
+    virtual void readout(float* act_probs, float* features, double* pooled) = 0;
     virtual void zero_grad() = 0;
     virtual double clip(double max_norm) = 0;
     virtual void adamw(double lr_enc, double lr_head, double b1, double b2, double eps, double wd) = 0;
@@ -598,6 +599,10 @@ template <typename R> struct Model : ModelBase {
         bool has_final = false, has_embedding = false;
         std::vector<R> scorer_input, scorer_normed, scorer_pre, scorer_act;
     } tape;
+    // What the read-out needs from the last forward: each item's first head-output row and option logits.
+    std::vector<R> last_pooled, last_scores;
+    std::vector<int> last_opts;
+    int act1 = -1, act1_b = -1, act2 = -1, act2_b = -1;
 
     explicit Model(const orc_config& c) {
         cfg = c;
@@ -658,10 +663,10 @@ template <typename R> struct Model : ModelBase {
         sc1_b = add_param("scorer.1.bias", {d}, total);
         sc2 = add_param("scorer.3.weight", {1, d}, total);
         sc2_b = add_param("scorer.3.bias", {1}, total);
-        add_param("act_head.0.weight", {256, d + 4}, total);
-        add_param("act_head.0.bias", {256}, total);
-        add_param("act_head.2.weight", {c.n_act, 256}, total);
-        add_param("act_head.2.bias", {c.n_act}, total);
+        act1 = add_param("act_head.0.weight", {256, d + 4}, total);
+        act1_b = add_param("act_head.0.bias", {256}, total);
+        act2 = add_param("act_head.2.weight", {c.n_act, 256}, total);
+        act2_b = add_param("act_head.2.bias", {c.n_act}, total);
         int temp = add_param("temperature", {3}, total);
         params[temp].trainable = false;
         data.assign(total, R(0));
@@ -851,6 +856,11 @@ template <typename R> struct Model : ModelBase {
         std::vector<R> scores(nmark);
         linear(act.data(), nmark, d, P(sc2), 1, P(sc2_b), scores.data());
         for (int r = 0; r < nmark; ++r) logits[r] = (double)scores[r];
+        last_scores = scores;
+        last_opts.assign(n_options, n_options + n_items);
+        last_pooled.resize((size_t)n_items * d);
+        for (int i = 0; i < n_items; ++i)
+            std::memcpy(last_pooled.data() + (size_t)i * d, states.data() + (size_t)segs[i].start * d, sizeof(R) * d);
 
         tape = Tape{};
         if (keep_tape) {
@@ -872,6 +882,48 @@ template <typename R> struct Model : ModelBase {
             tape.scorer_normed = std::move(snormed);
             tape.scorer_pre = std::move(pre);
             tape.scorer_act = std::move(act);
+        }
+    }
+
+    // DecisionModel.ReadOut (src/StructuredDecisions.Laya/Models/DecisionModel.cs:170-226) for every item of
+    // the last forward: the untempered softmax of the option logits (SimdOps.Softmax), its entropy over
+    // log(max(2, K)) with p clamped to ≥ 1e-9 inside the log, the top probability and its margin over the
+    // second (strict comparisons, in option order), then the act head on [h[start], top1, top1 − top2,
+    // entropy, k/255]: Linear → GELU → Linear (SimdOps.Linear: a Dot per output plus the bias) → softmax.
+    // act_probs [n_items][n_act]; features [n_items][4]; pooled (may be null) [n_items][d] as doubles.
+    void readout(float* act_probs, float* features, double* pooled) override {
+        const int d = hidden, n_items = (int)last_opts.size();
+        const int a1 = (int)params[act1_b].numel, na = (int)params[act2_b].numel;
+        std::vector<R> x(d + 4), hid(a1), out(na);
+        for (int i = 0, off = 0; i < n_items; off += last_opts[i], ++i) {
+            const int K = last_opts[i];
+            std::vector<R> p(last_scores.begin() + off, last_scores.begin() + off + K);
+            softmax(p.data(), K);
+            const R k = (R)std::max(2, K);
+            R entropy = 0;
+            for (R v : p) entropy -= v * std::log(std::max(v, (R)1e-9f));
+            entropy /= std::log(k);
+            R top1 = 0, top2 = 0;
+            for (R v : p) {
+                if (v > top1) {
+                    top2 = top1;
+                    top1 = v;
+                } else if (v > top2) {
+                    top2 = v;
+                }
+            }
+            std::memcpy(x.data(), last_pooled.data() + (size_t)i * d, sizeof(R) * d);
+            x[d] = top1;
+            x[d + 1] = top1 - top2;
+            x[d + 2] = entropy;
+            x[d + 3] = k / (R)255;
+            for (int o = 0; o < a1; ++o) hid[o] = gelu<R>(dot(x.data(), P(act1) + (size_t)o * (d + 4), d + 4) + P(act1_b)[o]);
+            for (int o = 0; o < na; ++o) out[o] = dot(hid.data(), P(act2) + (size_t)o * a1, a1) + P(act2_b)[o];
+            softmax(out.data(), na);
+            for (int o = 0; o < na; ++o) act_probs[(size_t)i * na + o] = (float)out[o];
+            for (int f = 0; f < 4; ++f) features[(size_t)i * 4 + f] = (float)x[d + f];
+            if (pooled)
+                for (int c = 0; c < d; ++c) pooled[(size_t)i * d + c] = (double)x[c];
         }
     }
 
@@ -1107,6 +1159,15 @@ int orc_model_forward(void* m, int n_items, const int* lengths, const int* token
     try {
         M_(m)->forward(n_items, lengths, tokens, n_options, markers, qtypes, training != 0, keep_tape != 0, seed,
                        logits);
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return 1;
+    }
+}
+int orc_model_readout(void* m, float* act_probs, float* features, double* pooled) {
+    try {
+        M_(m)->readout(act_probs, features, pooled);
         return 0;
     } catch (const std::exception& e) {
         g_error = e.what();

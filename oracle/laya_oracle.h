@@ -46,6 +46,9 @@ int orc_model_forward(void* model, int n_items, const int* lengths, const int* t
                       const int* markers, const int* qtypes, int training, int keep_tape, uint64_t seed,
                       double* logits_out);
 int orc_model_backward(void* model, const float* dlogits);
+/* DecisionModel.ReadOut on the last forward: act_probs [n_items][n_act], features [n_items][4]
+ * (top1, top1 − top2, normalised entropy, K/255), pooled [n_items][d] (may be NULL). */
+int orc_model_readout(void* model, float* act_probs, float* features, double* pooled);
 void orc_model_zero_grad(void* model);
 double orc_model_clip(void* model, double max_norm);
 void orc_model_adamw(void* model, double lr_encoder, double lr_head, double beta1, double beta2, double eps,

@@ -432,3 +432,62 @@ def test_mmbert_base_gradients_match_the_oracle(ctx):
     from laya_amd.config import mmbert_base
     print("model: mmBERT-base 22 layers, vocab 256000", flush=True)
     _large_shape_case(ctx, mmbert_base(), None, [120, 64, 40], 73, zipf=1.1)
+
+
+def test_readout_matches_the_oracle_on_the_fixture(ctx):
+    """DecisionModel.ReadOut on the device (DecisionModel.cs:170-226): with the fixture's trained scorer and act
+    head, the option logits, the four calibration features and the action probabilities of every item match
+    the oracle's read-out (fp64) to fp32 rounding; decide() = eval forward + read-out."""
+    from laya_amd.model import TrainableDecisionModel
+    m = TrainableDecisionModel.from_directory(TINY, ctx)
+    batch, _, torch_logits = tiny_batch()
+    o = oracle.OracleModel(tiny_config(), double=True)
+    o.set_params(tiny_params())
+    o.forward(batch, training=False)
+    probs_o, feats_o, _ = o.readout()
+    m.forward(batch, training=False)
+    logits, probs, feats = m.readout()
+    np.testing.assert_allclose(np.concatenate(logits), torch_logits, atol=1e-4)
+    np.testing.assert_allclose(feats, feats_o, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(probs, probs_o, rtol=1e-5, atol=1e-6)
+    out = m.decide(batch)
+    assert len(out) == batch.n_items
+    for i, (lg, p) in enumerate(out):
+        np.testing.assert_array_equal(lg, logits[i])
+        np.testing.assert_array_equal(p, probs[i])
+    m.close()
+
+
+def test_readout_at_modernbert_base_width(ctx):
+    """d = 768 (act-head input 772, hidden 256), items with K = 8, 4, 2 and 1 option, random weights, after a
+    training-mode forward (the read-out takes whatever the last forward left)."""
+    from laya_amd.batch import synthetic_batch
+    from laya_amd.model import TrainableDecisionModel
+    mc = mid_config(layers=2)
+    o = oracle.OracleModel(mc)
+    params = random_params(o.shapes, 31, std=0.05)
+    rng = np.random.default_rng(32)
+    batch = synthetic_batch(rng, [120, 77, 40, 9, 33], [8, 4, 2, 1, 3], [0, 1, 2, 0, 1], mc.encoder.vocab_size)
+    o64 = oracle.OracleModel(mc, double=True)
+    o64.set_params(params)
+    o64.forward(batch, training=True, seed=5)
+    probs_o, feats_o, _ = o64.readout()
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    m.forward(batch, training=True, seed=5)
+    logits, probs, feats = m.readout()
+    # Against fp64 the forward's own fp32 error (≈ 1e-6 of the logits) carries through; the margin top1 − top2
+    # is a difference of two probabilities, hence the absolute bar.
+    np.testing.assert_allclose(feats, feats_o, atol=1e-5)
+    np.testing.assert_allclose(probs, probs_o, atol=1e-5)
+    # The feature arithmetic itself, on the device's own logits, to fp32 rounding.
+    for i, lg in enumerate(logits):
+        p = np.exp(lg.astype(np.float64) - lg.max())
+        p /= p.sum()
+        k = max(2, len(lg))
+        srt = np.sort(p)[::-1]
+        want = [srt[0], srt[0] - (srt[1] if len(lg) > 1 else 0.0),
+                -np.sum(p * np.log(np.maximum(p, 1e-9))) / np.log(k), k / 255.0]
+        np.testing.assert_allclose(feats[i], want, atol=2e-7)
+    assert feats[3, 2] == 0.0 and abs(feats[3, 0] - 1.0) < 1e-7  # K = 1: p = 1, entropy 0
+    m.close()
