@@ -118,14 +118,10 @@ def make_batch(rng, w, vocab=50368):
     return Batch(lengths=lengths, tokens=tokens, n_options=n_options, markers=markers, qtypes=qtypes), targets
 
 
-def cpu_baseline(mc, batch, targets, items: int):
-    """The oracle (reference algorithm, fp32, OpenMP over the host cores) on the first `items`
-    sequences of the batch: one full step (forward, CE, backward with per-layer recompute, clip, AdamW)."""
+def _oracle_step(mc, sub, t_sub, summed: bool) -> float:
+    """One full fp32 step of the oracle (forward, CE, backward with per-layer recompute, clip, AdamW) on `sub`;
+    returns its wall time. The Adam moments are allocated first, as the reference's first step does."""
     import oracle
-    from laya_amd.batch import Batch
-    sub = Batch(lengths=batch.lengths[:items], tokens=batch.tokens[:int(batch.lengths[:items].sum())],
-                n_options=batch.n_options[:items], markers=batch.markers[:int(batch.n_options[:items].sum())],
-                qtypes=batch.qtypes[:items])
     o = oracle.OracleModel(mc)
     prng = np.random.default_rng(1)
     o.set_params({n: (np.ones(s, np.float32) if ("norm" in n and n.endswith("weight")) or n == "scorer.0.weight"
@@ -133,20 +129,52 @@ def cpu_baseline(mc, batch, targets, items: int):
                       np.zeros(s, np.float32) if n.endswith("bias") else
                       (0.02 * prng.standard_normal(s)).astype(np.float32)) for n, s in o.shapes.items()})
     o.set_head_dropout(0.1)
-    o.adamw(0.0, 0.0)  # allocates the moments, as the reference's first step does, outside the timed step
-    t_sub = targets[:sub.n_markers]
+    o.adamw(0.0, 0.0)
     t0 = time.perf_counter()
     logits = o.forward(sub, training=True, keep_tape=True, seed=1).astype(np.float32)
-    _, g = oracle.cross_entropy(sub.n_options, logits, t_sub, 1.0, float(sub.n_items))
+    _, g = oracle.cross_entropy(sub.n_options, logits, t_sub, 1.0, float(sub.n_items) if summed else 1.0)
     o.backward(g)
     o.clip(1.0)
     o.adamw(3e-5, 3e-5)
-    dt = time.perf_counter() - t0
+    return time.perf_counter() - t0
+
+
+def cpu_baseline(mc, batch, targets, items: int, summed: bool, extrapolate: bool, one_thread: bool):
+    """The oracle (the reference algorithm restated, fp32, OpenMP over the host cores) on the first `items`
+    sequences of the batch. With `extrapolate`, the step is timed on 3- and 6-layer encoders and extrapolated
+    linearly in layers to the model's depth (the long-sequence workloads, whose 22-layer CPU step would take
+    minutes). With `one_thread`, the same sample is also timed on one thread."""
+    import oracle
+    from laya_amd.batch import Batch
+    from laya_amd.config import modernbert_base
+    sub = Batch(lengths=batch.lengths[:items], tokens=batch.tokens[:int(batch.lengths[:items].sum())],
+                n_options=batch.n_options[:items], markers=batch.markers[:int(batch.n_options[:items].sum())],
+                qtypes=batch.qtypes[:items])
+    t_sub = targets[:sub.n_markers]
+    layers = mc.encoder.num_hidden_layers
+
+    def timed():
+        if not extrapolate:
+            return _oracle_step(mc, sub, t_sub, summed), "one full fp32 step"
+        t3 = _oracle_step(modernbert_base(3), sub, t_sub, summed)
+        t6 = _oracle_step(modernbert_base(6), sub, t_sub, summed)
+        return (t3 + (t6 - t3) * (layers - 3) / 3.0,
+                f"one fp32 step extrapolated linearly in layers to {layers} from 3- and 6-layer encoders "
+                f"({t3:.1f} s and {t6:.1f} s)")
+
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": sub.n_tokens / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"one full fp32 step (fwd+CE+bwd with per-layer recompute+clip+AdamW over all 164M params) "
-                      f"of the first {items} sequences ({sub.n_tokens} real tokens) of the same batch, "
-                      f"{dt:.1f} s"}
+    oracle.set_threads(cores)
+    dt, how = timed()
+    out = {"value": sub.n_tokens / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+           "sample": f"{how} (fwd+CE+bwd with per-layer recompute+clip+AdamW over all parameters) of the first "
+                     f"{items} sequences ({sub.n_tokens} real tokens) of the same batch, {dt:.1f} s"}
+    if one_thread:
+        oracle.set_threads(1)
+        dt1, how1 = timed()
+        oracle.set_threads(cores)
+        out["one_thread"] = {"value": sub.n_tokens / dt1, "unit": "tokens/s", "cores": 1,
+                             "sample": f"{how1} on one thread, same sample, {dt1:.1f} s"}
+    return out
 
 
 def main():
@@ -158,6 +186,10 @@ def main():
     ap.add_argument("--cpu-items", type=int, default=None,
                     help="sequences in the CPU sample (default 16 for b32x512, 1 for the long-sequence workloads)")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="b32x512")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="time the CPU baseline at full depth even for the long-sequence workloads")
+    ap.add_argument("--cpu-one-thread", action="store_true",
+                    help="also time the CPU baseline's sample on one thread (always done for the headline)")
     ap.add_argument("--fp32-mfma", action="store_true",
                     help="fp32 products on the fp32 matrix cores instead of exact bf16 splits (for comparison)")
     ap.add_argument("--no-profile", action="store_true", help="time without per-launch events")
@@ -185,6 +217,7 @@ def main():
     matmul = "fp32-mfma" if args.fp32_mfma and w["matmul"] == "fp32" else w["matmul"]
     ctx.set_matmul_precision(matmul)
     cpu_items = args.cpu_items or (16 if w["seq"] <= 512 else 1)
+    long_workload = w["seq"] > 512
     model = TrainableDecisionModel.synthetic(mc, seed=42, std=0.02, ctx=ctx)
     model.head_dropout = 0.1
     if args.traffic_probe:
@@ -287,7 +320,16 @@ def main():
     cpu = None
     if not args.no_cpu:
         print(f"cpu baseline: oracle on {cpu_items} sequences", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(mc, *batches[args.warmup], items=cpu_items)
+        b0, t0_ = batches[args.warmup]
+        if args.workload == "b32x512":
+            # All cores on 16 sequences; one thread on the first of them (≈ 10 s each).
+            cpu = cpu_baseline(mc, b0, t0_, cpu_items, w["summed"], False, False)
+            print("cpu baseline: one thread on 1 sequence", file=sys.stderr, flush=True)
+            one = cpu_baseline(mc, b0, t0_, 1, w["summed"], False, True)
+            cpu["one_thread"] = one["one_thread"]
+        else:
+            cpu = cpu_baseline(mc, b0, t0_, cpu_items, w["summed"], long_workload and not args.cpu_full,
+                               args.cpu_one_thread)
 
     value = tokens / elapsed
     line = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,

@@ -67,6 +67,8 @@ def lib():
         L.orc_model_adamw.argtypes = [P, c_double, c_double, c_double, c_double, c_double, c_double]
         L.orc_model_adamw.restype = None
         L.orc_model_steps.argtypes = [P]
+        L.orc_set_threads.argtypes = [c_int]
+        L.orc_set_threads.restype = c_int
         L.orc_uniform.argtypes = [c_u64, c_u64]
         L.orc_uniform.restype = c_float
         L.orc_mix.argtypes = [c_u64, c_u64]
@@ -225,6 +227,11 @@ class OracleModel:
 
 
 # ------------------------------------------------------------------------------------ op wrappers
+
+def set_threads(n: int) -> int:
+    """OpenMP threads of the oracle's later calls; returns the previous count."""
+    return lib().orc_set_threads(int(n))
+
 
 def uniform(seed: int, index: int) -> float:
     return lib().orc_uniform(seed & (2**64 - 1), index & (2**64 - 1))

@@ -1191,6 +1191,12 @@ void orc_model_adamw(void* m, double lr_enc, double lr_head, double b1, double b
 }
 int orc_model_steps(void* m) { return M_(m)->steps; }
 
+// The OpenMP thread count of the calls that follow (the CPU baseline's one-thread figure); returns the old one.
+int orc_set_threads(int n) {
+    const int old = omp_get_max_threads();
+    if (n > 0) omp_set_num_threads(n);
+    return old;
+}
 float orc_uniform(uint64_t seed, uint64_t index) { return uniform(seed, index); }
 uint64_t orc_mix(uint64_t seed, uint64_t salt) { return mix(seed, salt); }
 float orc_exp_f32(float x) { return exp_ref(x); }

@@ -49,6 +49,8 @@ int orc_model_backward(void* model, const float* dlogits);
 /* DecisionModel.ReadOut on the last forward: act_probs [n_items][n_act], features [n_items][4]
  * (top1, top1 − top2, normalised entropy, K/255), pooled [n_items][d] (may be NULL). */
 int orc_model_readout(void* model, float* act_probs, float* features, double* pooled);
+/* OpenMP threads for the calls that follow (n > 0); returns the previous maximum. */
+int orc_set_threads(int n);
 void orc_model_zero_grad(void* model);
 double orc_model_clip(void* model, double max_norm);
 void orc_model_adamw(void* model, double lr_encoder, double lr_head, double beta1, double beta2, double eps,
