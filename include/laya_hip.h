@@ -267,8 +267,18 @@ int laya_model_init_random(laya_model* model, uint64_t seed, float std);
 /* SetTrainableEncoderLayers (TrainableDecisionModel.cs:206-231); n < 0 trains everything. */
 int laya_model_set_trainable_encoder_layers(laya_model* model, int n);
 int laya_model_set_head_dropout(laya_model* model, float p);
-/* Forward (TrainableDecisionModel.cs:248-353). Keeps every activation the backward needs resident
- * in HBM (no recompute). logits_host (may be NULL) receives Σ n_options floats and synchronises. */
+/* Layer checkpointing (TrainableDecisionModel.cs:61-64: the reference checkpoints every layer, always):
+ * mode 0 keeps every encoder layer's activations resident from forward to backward; 1 keeps only each
+ * layer's input and recomputes the layer's internals just before its backward, as the reference does
+ * (the two head layers stay resident); 2 (the default) keeps everything when the activation arena fits
+ * under the context's memory cap and the device's free memory, and recomputes otherwise. Gradients are
+ * bitwise the same in every mode. A change takes effect at the next forward. */
+int laya_model_set_layer_checkpointing(laya_model* model, int mode);
+/* The mode, and whether the current arena recomputes (0 before the first forward). Either may be NULL. */
+int laya_model_layer_checkpointing(laya_model* model, int* mode, int* recomputing);
+/* Forward (TrainableDecisionModel.cs:248-353). Keeps what the backward needs resident in HBM (all of it,
+ * or the encoder layers' inputs under layer checkpointing). logits_host (may be NULL) receives
+ * Σ n_options floats and synchronises. */
 int laya_model_forward(laya_model* model, const laya_batch* batch, int training, uint64_t seed, float* logits_host);
 /* DecisionModel.ReadOut (src/StructuredDecisions.Laya/Models/DecisionModel.cs:170-226) for every item of
  * the last forward, on the device: the option logits (logits_host, Σ n_options floats, may be NULL), the

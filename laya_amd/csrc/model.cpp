@@ -131,6 +131,11 @@ struct laya_model {
 
     // ----- activations (capacity-sized, reused across steps)
     int cap_tokens = 0, cap_markers = 0, cap_segs = 0;
+    // Layer checkpointing (TrainableDecisionModel.cs:61-64): 0 keeps every encoder layer's activations,
+    // 1 keeps only each layer's input and recomputes the layer before its backward, 2 (the default) does
+    // that only when keeping everything would not fit (the context's cap, or the device's memory).
+    int checkpoint_mode = 2;
+    bool recompute = false;  // the arena's current layout
     void* act_block = nullptr;
     struct EncAct {
         float *x, *normed, *mean1, *rstd1, *qkv, *ctx, *lse, *res, *mlpn, *mean2, *rstd2, *wide, *act;
@@ -277,21 +282,17 @@ void ensure_rotary(laya_model* m, int positions) {
     build_rotary(m->ctx, &m->rot_local, hd, m->cfg.theta_local, p);
 }
 
-void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
-    if (T <= m->cap_tokens && nmark <= m->cap_markers && nseg <= m->cap_segs && m->act_block) return;
-    m->has_tape = false;  // the activations of the last forward go with the old block
-    if (m->act_block) {
-        m->ctx->release(m->act_block);
-        m->act_block = nullptr;
-    }
-    const int Tc = std::max(T, m->cap_tokens), Mc = std::max(std::max(nmark, m->cap_markers), 1),
-              Sc = std::max(std::max(nseg, m->cap_segs), 1);
-    const size_t d = m->d(), I = m->I(), ff = m->cfg.head_ff, Tz = Tc;
+// The activation arena's layout for Tc tokens; with `recompute`, the encoder layers share one set of
+// internal buffers and keep only their inputs.
+Carver carve_activations(laya_model* m, size_t Tz, size_t Mc, bool recompute) {
+    const size_t d = m->d(), I = m->I(), ff = m->cfg.head_ff;
     const size_t H = m->cfg.heads, HH = m->head_heads;
     Carver cv;
     m->ea.assign(m->cfg.layers, {});
-    for (auto& a : m->ea) {
+    for (size_t l = 0; l < m->ea.size(); ++l) {
+        auto& a = m->ea[l];
         cv.add(a.x, Tz * d);
+        if (recompute && l > 0) continue;  // internals shared with layer 0's (assigned after binding)
         cv.add(a.normed, Tz * d);
         cv.add(a.mean1, Tz);
         cv.add(a.rstd1, Tz);
@@ -347,11 +348,48 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     cv.add(m->ds_norm, (size_t)Mc * d);
     cv.add(m->ds_mark, (size_t)Mc * d);
     cv.add(m->targets, Mc);
-    // int tables share the carve (4-byte elements)
+    return cv;
+}
+
+void share_layer_internals(laya_model* m) {
+    for (size_t l = 1; l < m->ea.size(); ++l) {
+        float* x = m->ea[l].x;
+        m->ea[l] = m->ea[0];
+        m->ea[l].x = x;
+    }
+}
+
+void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
+    const bool want_full = m->checkpoint_mode != 1;
+    const bool layout_ok = m->checkpoint_mode == 2 || m->recompute == (m->checkpoint_mode == 1);
+    if (T <= m->cap_tokens && nmark <= m->cap_markers && nseg <= m->cap_segs && m->act_block && layout_ok) return;
+    m->has_tape = false;  // the activations of the last forward go with the old block
+    if (m->act_block) {
+        m->ctx->release(m->act_block);
+        m->act_block = nullptr;
+    }
+    const int Tc = std::max(T, m->cap_tokens), Mc = std::max(std::max(nmark, m->cap_markers), 1),
+              Sc = std::max(std::max(nseg, m->cap_segs), 1);
+    bool recompute = !want_full;
+    Carver cv = carve_activations(m, Tc, Mc, recompute);
     TableCarve tc;
-    tc.add(cv, Tz, Mc, Sc);
+    tc.add(cv, Tc, Mc, Sc);
+    if (m->checkpoint_mode == 2) {
+        // Keep everything when it fits under the context's cap and the device's free memory, else recompute.
+        size_t free_b = 0, total_b = 0;
+        if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) free_b = SIZE_MAX;
+        const bool over_cap = m->ctx->cap && m->ctx->in_use + cv.bytes > m->ctx->cap;
+        if (over_cap || cv.bytes + (64u << 20) > free_b) {
+            recompute = true;
+            cv = carve_activations(m, Tc, Mc, true);
+            tc = TableCarve{};
+            tc.add(cv, Tc, Mc, Sc);
+        }
+    }
     m->act_block = m->ctx->alloc(cv.bytes);
     cv.bind(static_cast<char*>(m->act_block));
+    if (recompute) share_layer_internals(m);
+    m->recompute = recompute;
     m->own = tc.bind();
     m->cur = m->own;
     m->cap_tokens = Tc;
@@ -534,6 +572,36 @@ void dropout_copy(laya_model* m, const float* src, float* dst, size_t n, float p
 
 // Forward (TrainableDecisionModel.cs:248-353) with EncoderLayerForward (361-414) and HeadLayerForward (428-468).
 // Forward over the current batch (prepare_batch or a staged batch made it current).
+// EncoderLayerForward (TrainableDecisionModel.cs:361-414) of layer l from its input ea[l].x: its internals
+// into ea[l] and, with `output`, its output into the next layer's input (or x_final). A recompute before the
+// layer's backward needs only the internals: the output is still held as the next layer's input.
+void encoder_forward(laya_model* m, int l, bool output = true) {
+    laya_ctx* ctx = m->ctx;
+    const int T = m->T, d = m->d(), I = m->I();
+    const float eps = m->cfg.norm_eps;
+    auto& L = m->enc[l];
+    auto& a = m->ea[l];
+    float* out = l + 1 < m->cfg.layers ? m->ea[l + 1].x : m->x_final;
+    const float* normed = a.x;
+    if (L.attn_norm >= 0) {
+        layernorm_fwd(ctx, a.x, T, d, m->W(L.attn_norm), m->W(L.attn_norm_b), eps, a.normed, a.mean1, a.rstd1);
+        normed = a.normed;
+    }
+    if (fused_rope(m)) {
+        const laya_rotary& r = L.kind == 0 ? m->rot_global : m->rot_local;
+        gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->cur.pos, r.cos_t, r.sin_t,
+                  2 * d);
+    } else {
+        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv);
+    }
+    attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse);
+    linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res);  // x1 = x + attn
+    layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2);
+    linear(m, a.mlpn, T, d, L.wi, L.wi_b, 2 * I, nullptr, a.wide);
+    geglu_fwd(ctx, a.wide, T, I, a.act);
+    if (output) linear(m, a.act, T, I, L.mlp_wo, L.mlp_wo_b, d, a.res, out);  // x2 = x1 + mlp
+}
+
 void forward(laya_model* m, bool train, uint64_t seed) {
     laya_ctx* ctx = m->ctx;
     const int T = m->T, d = m->d(), I = m->I(), ff = m->cfg.head_ff;
@@ -545,29 +613,7 @@ void forward(laya_model* m, bool train, uint64_t seed) {
     float* x0 = m->cfg.layers > 0 ? m->ea[0].x : m->x_final;
     layernorm_fwd(ctx, m->W(m->tok_emb), T, d, m->W(m->emb_norm), m->W(m->emb_norm_b), eps, x0, m->emb_mean,
                   m->emb_rstd, m->cur.tokens);
-    for (int l = 0; l < m->cfg.layers; ++l) {
-        auto& L = m->enc[l];
-        auto& a = m->ea[l];
-        float* out = l + 1 < m->cfg.layers ? m->ea[l + 1].x : m->x_final;
-        const float* normed = a.x;
-        if (L.attn_norm >= 0) {
-            layernorm_fwd(ctx, a.x, T, d, m->W(L.attn_norm), m->W(L.attn_norm_b), eps, a.normed, a.mean1, a.rstd1);
-            normed = a.normed;
-        }
-        if (fused_rope(m)) {
-            const laya_rotary& r = L.kind == 0 ? m->rot_global : m->rot_local;
-            gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->cur.pos, r.cos_t, r.sin_t,
-                      2 * d);
-        } else {
-            linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv);
-        }
-        attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse);
-        linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res);  // x1 = x + attn
-        layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2);
-        linear(m, a.mlpn, T, d, L.wi, L.wi_b, 2 * I, nullptr, a.wide);
-        geglu_fwd(ctx, a.wide, T, I, a.act);
-        linear(m, a.act, T, I, L.mlp_wo, L.mlp_wo_b, d, a.res, out);  // x2 = x1 + mlp
-    }
+    for (int l = 0; l < m->cfg.layers; ++l) encoder_forward(m, l);
     // Final norm, then each question's type vector on its rows (TrainableDecisionModel.cs:294-304).
     float* h0 = m->cfg.head_layers > 0 ? m->ha[0].x : m->head_out;
     layernorm_fwd(ctx, m->x_final, T, d, m->W(m->final_norm), m->W(m->final_norm_b), eps, h0, m->fin_mean, m->fin_rstd,
@@ -724,8 +770,12 @@ void backward_body(laya_model* m) {
     fill(ctx, m->dE, 0.0f, (size_t)T * d);
     ln_backward(m, m->x_final, T, d, m->final_norm, m->final_norm_b, eps, m->dS, m->dE, m->fin_mean, m->fin_rstd);
     std::swap(m->dS, m->dE);
-    for (int l = m->cfg.layers - 1; l >= m->first_trainable; --l)
+    for (int l = m->cfg.layers - 1; l >= m->first_trainable; --l) {
+        // Layer checkpointing: the layer's internals are recomputed from its kept input (the same kernels on
+        // the same inputs give the same values) just before its backward, as the reference always does.
+        if (m->recompute) encoder_forward(m, l, false);
         encoder_backward(m, l, l > m->first_trainable || m->embeddings_trainable);
+    }
     if (m->embeddings_trainable && m->first_trainable == 0) {
         fill(ctx, m->dE, 0.0f, (size_t)T * d);
         ln_backward(m, m->W(m->tok_emb), T, d, m->emb_norm, m->emb_norm_b, eps, m->dS, m->dE, m->emb_mean, m->emb_rstd,
@@ -950,6 +1000,28 @@ int laya_model_set_trainable_encoder_layers(laya_model* m, int n) {
             if (!train) p.touched = false;
         }
         m->embeddings_trainable = m->params[m->tok_emb].trainable;
+    });
+}
+
+int laya_model_set_layer_checkpointing(laya_model* m, int mode) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(mode >= 0 && mode <= 2, "layer checkpointing: 0 (keep), 1 (recompute) or 2 (when needed)");
+        if (mode == m->checkpoint_mode) return;
+        m->checkpoint_mode = mode;
+        // The next forward lays the activation arena out for the new mode.
+        m->has_tape = false;
+        if (m->act_block) m->ctx->release(m->act_block);
+        m->act_block = nullptr;
+        m->cap_tokens = m->cap_markers = m->cap_segs = 0;
+    });
+}
+
+int laya_model_layer_checkpointing(laya_model* m, int* mode, int* recomputing) {
+    return guarded([&] {
+        checked(m);
+        if (mode) *mode = m->checkpoint_mode;
+        if (recomputing) *recomputing = m->act_block && m->recompute ? 1 : 0;
     });
 }
 

@@ -244,6 +244,30 @@ class TrainableDecisionModel:
         check(lib().laya_model_set_head_dropout(self.handle, float(p)))
         self._head_dropout = float(p)
 
+    CHECKPOINT_KEEP, CHECKPOINT_RECOMPUTE, CHECKPOINT_AUTO = 0, 1, 2
+
+    @property
+    def layer_checkpointing(self) -> int:
+        """Layer checkpointing (TrainableDecisionModel.cs:61-64, where every layer is always checkpointed):
+        0 keeps every encoder activation, 1 recomputes each encoder layer before its backward, 2 (default)
+        recomputes only when keeping everything would not fit. Gradients are bitwise the same."""
+        mode = ctypes.c_int()
+        check(lib().laya_model_layer_checkpointing(self.handle, ctypes.byref(mode), None))
+        return mode.value
+
+    @layer_checkpointing.setter
+    def layer_checkpointing(self, mode) -> None:
+        if isinstance(mode, bool):
+            mode = self.CHECKPOINT_RECOMPUTE if mode else self.CHECKPOINT_KEEP
+        check(lib().laya_model_set_layer_checkpointing(self.handle, int(mode)))
+
+    @property
+    def recomputing(self) -> bool:
+        """Whether the current activation arena recomputes encoder layers in backward."""
+        r = ctypes.c_int()
+        check(lib().laya_model_layer_checkpointing(self.handle, None, ctypes.byref(r)))
+        return bool(r.value)
+
     def forward(self, items, training: bool = False, seed: int = 0, want_logits: bool = True):
         """Forward (TrainableDecisionModel.cs:248-353): returns the per-option logits, concatenated."""
         batch = _as_batch(items)
