@@ -14,7 +14,7 @@
 // (its column) and 16 keys (its rows). Those registers are exactly the B operand of Oᵀ = Vᵀ·Pᵀ, so
 // P never leaves registers, and each query's running max / sum live in one lane pair.
 // The backward runs two kernels, both without atomics (deterministic):
-//   dkv: each wave owns 32 keys (K in LDS, V in registers) and sweeps the query tiles: S = Q·Kᵀ,
+//   dkv: each wave owns 32 keys and sweeps the query tiles: S = Q·Kᵀ,
 //        dVᵀ += dOᵀ·P, dP = dO·Vᵀ, dS, dKᵀ += Qᵀ·dS;
 //   dq:  each wave owns 32 queries (Q, dO in registers) and sweeps the key tiles: Sᵀ, dPᵀ, dSᵀ,
 //        dQᵀ += Kᵀ·dSᵀ.
@@ -269,9 +269,7 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
 // In a 32×32×16 product a lane supplies 8 consecutive k of its row or column. The scores' accumulator
 // gives a lane the keys 8(r/4) + 4h + r%4 of its column, so a product over keys takes, per 16 keys, the
 // key order {4h … 4h+3, 8+4h … 8+4h+3} for both operands: P stays in the registers it was computed in and
-// the other operand is read from a transposed ([d][key]) plane as two runs of 4 keys.
-
-constexpr int KSH = 64 + 8;    // bf16 stride of [row][d] planes: b128 fragment reads without bank conflicts
+// the other operand is read from its [key][d] plane as two runs of 4 keys by transposing LDS reads.
 
 __device__ __forceinline__ f32x16 mfma16(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -301,17 +299,13 @@ __device__ __forceinline__ void split8(f32x4 lo, f32x4 hi, bf16x8 (&out)[3]) {
     out[2] = cat8(a3, b3);
 }
 
-// An R × 64 slice of one head (R = 64 or 32 rows) in registers between its global fetch and its LDS commit:
-// thread t holds rows (R/16)·(t/16) + i (i < R/16) at d = 4·(t%16) … +3, so it can write both a [row][d]
-// and a [d][row] plane.
+// An R × 64 slice of one head (R = 32, 64 or 128 rows) in registers between its global fetch and its LDS
+// commit: thread t holds rows (R/16)·(t/16) + i (i < R/16) at d = 4·(t%16) … +3.
 template <int R>
 struct RowStage {
     static constexpr int N = R / 16;
     f32x4 v[N];
 };
-
-template <int R>
-constexpr int tsh() { return R + 4; }  // bf16 stride of [d][row] planes: b64 reads of 4 rows without conflicts
 
 template <int R>
 __device__ __forceinline__ void fetch_rows(RowStage<R>& st, const float* base, long stride, int L, int row0) {
@@ -321,79 +315,6 @@ __device__ __forceinline__ void fetch_rows(RowStage<R>& st, const float* base, l
     for (int i = 0; i < N; ++i) {
         const int t = row0 + N * q + i;
         st.v[i] = (t >= 0 && t < L) ? ld4(base + (long)t * stride + j) : f32x4{0, 0, 0, 0};
-    }
-}
-
-// Three [row][d] planes (stride KSH, plane stride R·KSH).
-template <int R>
-__device__ __forceinline__ void commit_rows(const RowStage<R>& st, __bf16* planes) {
-    constexpr int N = RowStage<R>::N;
-    const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        bf16x4 h1, h2, h3;
-        split3_4(st.v[i], h1, h2, h3);
-        __bf16* o = planes + (N * q + i) * KSH + j;
-        *reinterpret_cast<bf16x4*>(o) = h1;
-        *reinterpret_cast<bf16x4*>(o + R * KSH) = h2;
-        *reinterpret_cast<bf16x4*>(o + 2 * R * KSH) = h3;
-    }
-}
-
-// Three [d][row] planes (stride tsh<R>(), plane stride 64·tsh<R>()).
-template <int R>
-__device__ __forceinline__ void commit_cols(const RowStage<R>& st, __bf16* planes) {
-    constexpr int N = RowStage<R>::N, TS = tsh<R>();
-    const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        __bf16* o = planes + (j + e) * TS + N * q;
-        if constexpr (N == 4) {
-            bf16x4 h1, h2, h3;
-            split3_4(f32x4{st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]}, h1, h2, h3);
-            *reinterpret_cast<bf16x4*>(o) = h1;
-            *reinterpret_cast<bf16x4*>(o + 64 * TS) = h2;
-            *reinterpret_cast<bf16x4*>(o + 2 * 64 * TS) = h3;
-        } else {
-            static_assert(N == 2, "tiles of 64 or 32 rows");
-            bf16x4 h1, h2, h3;
-            split3_4(f32x4{st.v[0][e], st.v[1][e], 0.0f, 0.0f}, h1, h2, h3);
-            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-            *reinterpret_cast<bf16x2*>(o) = __builtin_shufflevector(h1, h1, 0, 1);
-            *reinterpret_cast<bf16x2*>(o + 64 * TS) = __builtin_shufflevector(h2, h2, 0, 1);
-            *reinterpret_cast<bf16x2*>(o + 2 * 64 * TS) = __builtin_shufflevector(h3, h3, 0, 1);
-        }
-    }
-}
-
-// Both layouts of one staged tile (as commit_rows then commit_cols) from one split of each value: the
-// [d][row] pieces are the [row][d] pieces regrouped, since the split is elementwise.
-template <int R>
-__device__ __forceinline__ void commit_both(const RowStage<R>& st, __bf16* rows, __bf16* cols) {
-    constexpr int N = RowStage<R>::N, TS = tsh<R>();
-    const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
-    bf16x4 h[N][3];
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-        split3_4(st.v[i], h[i][0], h[i][1], h[i][2]);
-        __bf16* o = rows + (N * q + i) * KSH + j;
-#pragma unroll
-        for (int pl = 0; pl < 3; ++pl) *reinterpret_cast<bf16x4*>(o + pl * R * KSH) = h[i][pl];
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        __bf16* o = cols + (j + e) * TS + N * q;
-#pragma unroll
-        for (int pl = 0; pl < 3; ++pl) {
-            if constexpr (N == 4) {
-                *reinterpret_cast<bf16x4*>(o + pl * 64 * TS) =
-                    bf16x4{h[0][pl][e], h[1][pl][e], h[2][pl][e], h[3][pl][e]};
-            } else {
-                static_assert(N == 2, "tiles of 64 or 32 rows");
-                typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-                *reinterpret_cast<bf16x2*>(o + pl * 64 * TS) = bf16x2{h[0][pl][e], h[1][pl][e]};
-            }
-        }
     }
 }
 
@@ -407,36 +328,72 @@ __device__ __forceinline__ void split_lane_row(const float* src, bool valid, int
     }
 }
 
-// The 16-k fragments of row `row` of three [row][d] planes at k-step s.
-template <int R>
-__device__ __forceinline__ void row_frag(const __bf16* planes, int row, int s, int h, bf16x8 (&f)[3]) {
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
-        f[pl] = *reinterpret_cast<const bf16x8*>(planes + pl * R * KSH + row * KSH + 16 * s + 8 * h);
-}
-
-// The fragments of d-row `d` of three [d][row] planes over the 16 rows from r0, in the key order above.
-template <int R>
-__device__ __forceinline__ void col_frag(const __bf16* planes, int d, int r0, int h, bf16x8 (&f)[3]) {
-    constexpr int TS = tsh<R>();
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl) {
-        const __bf16* row = planes + pl * 64 * TS + d * TS + r0 + 4 * h;
-        f[pl] = cat8(*reinterpret_cast<const bf16x4*>(row), *reinterpret_cast<const bf16x4*>(row + 8));
-    }
-}
-
 // 16 values of a lane's accumulator column as the pieces of two 16-row k-steps (in the key order above).
 __device__ __forceinline__ void split_col16(const float (&v)[16], int u, bf16x8 (&out)[3]) {
     split8(f32x4{v[8 * u], v[8 * u + 1], v[8 * u + 2], v[8 * u + 3]},
            f32x4{v[8 * u + 4], v[8 * u + 5], v[8 * u + 6], v[8 * u + 7]}, out);
 }
 
+// One LDS layout for every staged tile.
+//
+// Planes of 64 bf16 per row (128 bytes) with the 16-byte chunks of row r XOR-swizzled by
+// g(r) = 4·(r/2 mod 2) + (r/4 mod 4). The LDS serves a b128 read 16 lanes (256 bytes, 64 banks) at a time:
+// 16 consecutive rows at one chunk then take 16 distinct (row parity, chunk) bank groups. A transposing
+// read is served 32 lanes at a time, four consecutive rows at four adjacent chunks: rows r and r + 2 differ
+// in bit 2 of g, so their aligned groups of four chunks do not meet. A product over rows (queries)
+// reads its operand from the [row][d] plane with ds_read_b64_tr_b16: in each 16-lane group, lane j names
+// the 4-element chunk (row r0 + j/4, columns c0 + 4(j mod 4)) and lane i receives element i mod 4 of the
+// chunks named by lanes i/4, 4 + i/4, 8 + i/4, 12 + i/4 — i.e. 4 consecutive rows of its column.
+__device__ __forceinline__ int swz(int row, int col) {
+    return row * 64 + ((((col >> 3) ^ ((((row >> 1) & 1) << 2) | ((row >> 2) & 3)))) << 3) + (col & 7);
+}
+
+__device__ __forceinline__ bf16x4 ds_read_tr(const __bf16* p) {
+    typedef short i16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) i16x4* lds_i16x4;
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(p)));
+}
+
+// Three swizzled [row][d] planes of R rows (plane stride R·64) from a staged tile.
+template <int R>
+__device__ __forceinline__ void commit_swz(const RowStage<R>& st, __bf16* planes) {
+    constexpr int N = RowStage<R>::N;
+    const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        bf16x4 h1, h2, h3;
+        split3_4(st.v[i], h1, h2, h3);
+        const int o = swz(N * q + i, j);
+        *reinterpret_cast<bf16x4*>(planes + o) = h1;
+        *reinterpret_cast<bf16x4*>(planes + R * 64 + o) = h2;
+        *reinterpret_cast<bf16x4*>(planes + 2 * R * 64 + o) = h3;
+    }
+}
+
+// Row fragments (8 consecutive d of row `row` at k-step s) of three swizzled planes of R rows.
+template <int R>
+__device__ __forceinline__ void swz_row_frag(const __bf16* planes, int row, int s, int h, bf16x8 (&f)[3]) {
+    const int o = swz(row, 16 * s + 8 * h);
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) f[pl] = *reinterpret_cast<const bf16x8*>(planes + pl * R * 64 + o);
+}
+
+// The A fragments of d-rows 32·dt + lane mod 32 over the 16 rows from r0, in the key order of the score
+// accumulators (rows r0 + 4h … +3, then r0 + 8 + 4h … +3), from three swizzled planes of R rows.
+template <int R>
+__device__ __forceinline__ void swz_col_frag(const __bf16* planes, int r0, int dt, int lane, bf16x8 (&f)[3]) {
+    const int G = lane >> 4, j = lane & 15;
+    const int row = r0 + 4 * (G >> 1) + (j >> 2), col = 32 * dt + 16 * (G & 1) + 4 * (j & 3);
+    const int o0 = swz(row, col), o1 = swz(row + 8, col);
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) f[pl] = cat8(ds_read_tr(planes + pl * R * 64 + o0), ds_read_tr(planes + pl * R * 64 + o1));
+}
+
 template <int D>
 __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
-    __shared__ __attribute__((aligned(16))) __bf16 Kh[3 * TILE * KSH];  // K tile, [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 Vt[3 * D * tsh<TILE>()];  // V tile, [d][key]
+    __shared__ __attribute__((aligned(16))) __bf16 Ks[3 * TILE * 64];  // K tile, swizzled [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Vs[3 * TILE * 64];  // V tile, swizzled [key][d]
 
     const int seg = blockIdx.y, head = blockIdx.z;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
@@ -474,8 +431,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     fetch_rows<TILE>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
         __syncthreads();
-        commit_rows<TILE>(kst, Kh);
-        commit_cols<TILE>(vst, Vt);
+        commit_swz<TILE>(kst, Ks);
+        commit_swz<TILE>(vst, Vs);
         __syncthreads();
         if (kt0 + TILE < kend) {  // block-uniform: the next tile's loads overlap this tile's products
             fetch_rows<TILE>(kst, kbase, stride, L, kt0 + TILE);
@@ -491,7 +448,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 bf16x8 kf[3];
-                row_frag<TILE>(Kh, 32 * st + lr, ks, h, kf);
+                swz_row_frag<TILE>(Ks, 32 * st + lr, ks, h, kf);
                 s = mma6(kf, qh[ks], s);
             }
             float t[16];
@@ -540,7 +497,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
 #pragma unroll
                 for (int dt = 0; dt < 2; ++dt) {
                     bf16x8 vf[3];
-                    col_frag<TILE>(Vt, 32 * dt + lr, 32 * st + 16 * u, h, vf);
+                    swz_col_frag<TILE>(Vs, 32 * st + 16 * u, dt, lane, vf);
                     o[dt] = mma6(vf, ph, o[dt]);
                 }
             }
@@ -809,17 +766,19 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
     }
 }
 
-// The backward on split products, tiles of 32 rows (the transposed planes would not leave room for two
-// blocks per CU at 64).
+// The backward on split products, tiles of 32 query or key rows: with the dK/dV kernel's V planes (the
+// block's 128 keys), 64-row tiles would not leave room for two blocks per CU.
 constexpr int BT = 32;
 
+// Each wave owns 32 keys: K split once into registers, V split once into the block's LDS planes. The
+// query tiles are committed to one swizzled layout each (Q and dO), the next tile's rows load while the
+// current one is multiplied, and the products over queries read Qᵀ and dOᵀ with the transposing reads.
 template <int D>
 __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
-    __shared__ __attribute__((aligned(16))) __bf16 Qh[3 * BT * KSH];      // Q tile, [q][d]
-    __shared__ __attribute__((aligned(16))) __bf16 Qt[3 * D * tsh<BT>()];  // Q tile, [d][q]
-    __shared__ __attribute__((aligned(16))) __bf16 Oh[3 * BT * KSH];      // dO tile, [q][d]
-    __shared__ __attribute__((aligned(16))) __bf16 Ot[3 * D * tsh<BT>()];  // dO tile, [d][q]
+    __shared__ __attribute__((aligned(16))) __bf16 Qs[3 * BT * 64];
+    __shared__ __attribute__((aligned(16))) __bf16 Os[3 * BT * 64];
+    __shared__ __attribute__((aligned(16))) __bf16 Vs[3 * BLOCK_ROWS * 64];
     __shared__ float lse_s[BT], dot_s[BT];
 
     const int seg = blockIdx.y, head = blockIdx.z;
@@ -835,16 +794,13 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     const long stride = 3L * p.hidden;
     const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
 
-    // The own K row split once; the own V row kept in fp32 (d = 16s + 8h … +7) and split per use, which
-    // keeps the kernel within two waves' registers.
     bf16x8 kh[4][3];
-    f32x4 vlo[4], vhi[4];
     const long krow = (long)(start + (kvalid ? key : 0)) * stride;
     split_lane_row(p.qkv + krow + kcol, kvalid, h, kh);
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        vlo[ks] = kvalid ? ld4(p.qkv + krow + vcol + 16 * ks + 8 * h) : f32x4{0, 0, 0, 0};
-        vhi[ks] = kvalid ? ld4(p.qkv + krow + vcol + 16 * ks + 8 * h + 4) : f32x4{0, 0, 0, 0};
+    {
+        RowStage<BLOCK_ROWS> vst;
+        fetch_rows<BLOCK_ROWS>(vst, p.qkv + (long)start * stride + vcol, stride, L, kb0);
+        commit_swz<BLOCK_ROWS>(vst, Vs);
     }
 
     int qbeg = 0, qend = L, wbeg = 0, wend = L;
@@ -864,35 +820,39 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
 
     const float* qbase = p.qkv + (long)start * stride + qcol;
     const float* obase = p.dcontext + (long)start * p.hidden + qcol;
+    RowStage<BT> qst, ost;
+    float lse_n = __builtin_huge_valf(), dot_n = 0.0f;
+    auto fetch = [&](int t0) {
+        fetch_rows<BT>(qst, qbase, stride, L, t0);
+        fetch_rows<BT>(ost, obase, p.hidden, L, t0);
+        const int t = t0 + (int)threadIdx.x;
+        if (threadIdx.x < BT) {
+            lse_n = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
+            dot_n = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
+        }
+    };
+    if (qbeg < qend) fetch(qbeg);
     for (int qt0 = qbeg; qt0 < qend; qt0 += BT) {
-        __syncthreads();
-        {
-            RowStage<BT> qst, ost;
-            fetch_rows<BT>(qst, qbase, stride, L, qt0);
-            fetch_rows<BT>(ost, obase, p.hidden, L, qt0);
-            const int t = qt0 + (int)threadIdx.x;
-            if (threadIdx.x < BT) {
-                lse_s[threadIdx.x] = t < L ? p.lse[(long)(start + t) * p.heads + head] : __builtin_huge_valf();
-                dot_s[threadIdx.x] = t < L ? p.dots[(long)(start + t) * p.heads + head] : 0.0f;
-            }
-            commit_both<BT>(qst, Qh, Qt);
-            commit_both<BT>(ost, Oh, Ot);
+        __syncthreads();  // the previous tile's fragments (and, first time round, V's commit) are read
+        commit_swz<BT>(qst, Qs);
+        commit_swz<BT>(ost, Os);
+        if (threadIdx.x < BT) {
+            lse_s[threadIdx.x] = lse_n;
+            dot_s[threadIdx.x] = dot_n;
         }
         __syncthreads();
+        if (qt0 + BT < qend) fetch(qt0 + BT);  // block-uniform
         // Wave-uniform: outside this wave's window, or a wave whose keys all lie past the segment end.
         if (qt0 >= wend || qt0 + BT <= wbeg || k0w >= L) continue;
         // S[q][key] = Q·Kᵀ and dP = dO·Vᵀ: lane column = its key, rows = 16 queries.
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            bf16x8 f[3];
-            row_frag<BT>(Qh, lr, ks, h, f);
+            bf16x8 f[3], vh[3];
+            swz_row_frag<BT>(Qs, lr, ks, h, f);
             s = mma6(f, kh[ks], s);
-            row_frag<BT>(Oh, lr, ks, h, f);
-            // The asm marks the row as changed, so its split is not hoisted out of the query loop.
-            asm volatile("" : "+v"(vlo[ks]), "+v"(vhi[ks]));
-            bf16x8 vh[3];
-            split8(vlo[ks], vhi[ks], vh);
+            swz_row_frag<BT>(Os, lr, ks, h, f);
+            swz_row_frag<BLOCK_ROWS>(Vs, wave * WAVE_ROWS + lr, ks, h, vh);
             dp = mma6(f, vh, dp);
         }
         float pm[16], ds[16];
@@ -927,9 +887,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
                 bf16x8 f[3];
-                col_frag<BT>(Ot, 32 * dt + lr, 16 * u, h, f);
+                swz_col_frag<BT>(Os, 16 * u, dt, lane, f);
                 dv[dt] = mma6(f, ph, dv[dt]);
-                col_frag<BT>(Qt, 32 * dt + lr, 16 * u, h, f);
+                swz_col_frag<BT>(Qs, 16 * u, dt, lane, f);
                 dk[dt] = mma6(f, dh, dk[dt]);
             }
         }
@@ -946,9 +906,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
 template <int D>
 __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
-    __shared__ __attribute__((aligned(16))) __bf16 Kh[3 * BT * KSH];      // K tile, [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 Kt[3 * D * tsh<BT>()];  // K tile, [d][key]
-    __shared__ __attribute__((aligned(16))) __bf16 Vh[3 * BT * KSH];      // V tile, [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Ks[3 * BT * 64];  // K tile, swizzled [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Vs[3 * BT * 64];  // V tile, swizzled [key][d]
 
     const int seg = blockIdx.y, head = blockIdx.z;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
@@ -1003,8 +962,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     fetch_rows<BT>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += BT) {
         __syncthreads();
-        commit_both<BT>(kst, Kh, Kt);
-        commit_rows<BT>(vst, Vh);
+        commit_swz<BT>(kst, Ks);
+        commit_swz<BT>(vst, Vs);
         __syncthreads();
         if (kt0 + BT < kend) {  // block-uniform
             fetch_rows<BT>(kst, kbase, stride, L, kt0 + BT);
@@ -1017,9 +976,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             bf16x8 f[3];
-            row_frag<BT>(Kh, lr, ks, h, f);
+            swz_row_frag<BT>(Ks, lr, ks, h, f);
             s = mma6(f, qh[ks], s);
-            row_frag<BT>(Vh, lr, ks, h, f);
+            swz_row_frag<BT>(Vs, lr, ks, h, f);
             dp = mma6(f, oh[ks], dp);
         }
         float ds[16];
@@ -1046,7 +1005,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
                 bf16x8 f[3];
-                col_frag<BT>(Kt, 32 * dt + lr, 16 * u, h, f);
+                swz_col_frag<BT>(Ks, 16 * u, dt, lane, f);
                 dq[dt] = mma6(f, dh, dq[dt]);
             }
         }
