@@ -197,20 +197,24 @@ enum class GemmEpilogue {
     Accumulate,  // C += acc, deterministically (split-K partials reduced in a fixed order)
 };
 
+// A16 / B16: optional bf16 copies of A / B (rounded to nearest even, same leading dimensions) that a bf16
+// product reads instead of rounding A / B itself; the result is the same.
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
           const float* B, long ldb, float* C, long ldc, const float* bias = nullptr, const float* R = nullptr,
-          long ldr = 0);
+          long ldr = 0, const __bf16* A16 = nullptr, const __bf16* B16 = nullptr);
 
 // y = x·Wᵀ + b for x [M, K], W [N, K] with RoPE applied in the epilogue to output columns [0, rope_cols)
 // taken as heads of 64 (d and d + 32 rotated at position pos[row]; tables [positions][32]). The fused
 // QKV projection: q and k leave the GEMM already rotated (Ops.cs:297-313).
 void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* B, float* C, const float* bias,
-               const int* pos, const float* cos_t, const float* sin_t, int rope_cols);
+               const int* pos, const float* cos_t, const float* sin_t, int rope_cols, const __bf16* A16 = nullptr,
+               const __bf16* B16 = nullptr);
 
 // The two products of Ops.LinearBackward in one launch: dx = dy·W (+ dx_residual) and dW += dyᵀ·x,
 // for dy [rows, out], W [out, in], x [rows, in]; split-K partials of dW reduced in a fixed order.
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
-                        float* dx, const float* dx_residual, float* dW);
+                        float* dx, const float* dx_residual, float* dW, const __bf16* W16 = nullptr,
+                        const __bf16* x16 = nullptr);
 
 // Σ over rows of a [rows, n] matrix added into out[n], deterministic (bias gradients).
 void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out);

@@ -58,6 +58,11 @@ struct GemmParams {
     const float* rope_cos;
     const float* rope_sin;
     int rope_cols;
+    // Optional bf16 copies of A and B (same leading dimensions), rounded to nearest even as the kernels
+    // would round A and B: a bf16 product whose kernel can read them streams half the bytes and skips the
+    // conversion; the result is the same.
+    const __bf16* A16;
+    const __bf16* B16;
 };
 
 // ------------------------------------------------------------------------------ shared pieces
@@ -810,8 +815,8 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Raw buffer descriptor over `bytes` bytes of p (offsets are 32-bit; the host keeps operands under 2³¹ B).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* p, unsigned bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), 0, (int)bytes, 0x00020000);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
 }
 
 // A 256-row k-contiguous operand's 16-deep stage: thread t holds 4 consecutive k of rows t/4 and t/4 + 128.
@@ -847,6 +852,33 @@ struct OperandW {
                 *reinterpret_cast<bf16x4*>(lds + o) = __builtin_convertvector(reg[i], bf16x4);
             }
         }
+    }
+};
+
+// OperandW over a bf16 copy (one plane, the bf16 products): thread t loads its 4 k of each row as 8 bytes
+// and stores them as loaded.
+struct OperandW16 {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    __amdgpu_buffer_rsrc_t rsrc;
+    unsigned off[2];
+    u32x2 reg[2];
+    __device__ __forceinline__ OperandW16(const __bf16* s, long ldl, int mn0, int MN, int tid, unsigned bytes)
+        : rsrc(buffer_of(s, bytes)) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            off[i] = ((unsigned)min(mn0 + (tid >> 2) + 128 * i, MN - 1) * (unsigned)ldl + ((tid & 3) << 2)) * 2u;
+    }
+    __device__ __forceinline__ void full(int k0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) reg[i] = __builtin_amdgcn_raw_buffer_load_b64(rsrc, off[i], k0 * 2, 0);
+    }
+    __device__ __forceinline__ void tail(int k0, int) { full(k0); }
+    template <int NP = 1>
+    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+        static_assert(NP == 1, "a bf16 copy feeds bf16 products");
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            *reinterpret_cast<u32x2*>(lds + ((tid >> 2) + 128 * i) * KPADQ + ((tid & 3) << 2)) = reg[i];
     }
 };
 
@@ -893,9 +925,28 @@ __device__ __forceinline__ void mma_stage_w(const __bf16* A, const __bf16* B, f3
     }
 }
 
-template <int MODE>
+// The k-contiguous operand of the wide NT kernel: fp32 (split or rounded as it is staged) or its bf16 copy.
+template <bool H>
+struct WideK {
+    typedef OperandW T;
+    static __device__ __forceinline__ T make(const float* s, const __bf16*, long ld, int mn0, int MN, int tid) {
+        return T(s, ld, mn0, MN, tid, (unsigned)(MN * ld * 4));
+    }
+};
+template <>
+struct WideK<true> {
+    typedef OperandW16 T;
+    static __device__ __forceinline__ T make(const float*, const __bf16* h, long ld, int mn0, int MN, int tid) {
+        return T(h, ld, mn0, MN, tid, (unsigned)(MN * ld * 2));
+    }
+};
+
+// NP = 3: the split (fp32) product; NP = 1: the bf16 product, with AH / BH reading A / B from their bf16
+// copies.
+template <int MODE, int NP = 3, bool AH = false, bool BH = false>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     static_assert(MODE == STORE || MODE == STORE_ROPE, "whole-K NT epilogues");
+    static_assert(NP == 1 || !(AH || BH), "bf16 copies feed bf16 products");
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];  // [stage][operand]
     const int t = xcd_logical_block();
     const int tm = t / p.tiles_n;
@@ -911,8 +962,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3;
     const int lr = lane & 31, half = lane >> 5;
-    OperandW a(p.A, p.lda, c.m0, p.M, tid, (unsigned)(p.M * p.lda * 4));
-    OperandW b(p.B, p.ldb, c.n0, p.N, tid, (unsigned)(p.N * p.ldb * 4));
+    typename WideK<AH>::T a = WideK<AH>::make(p.A, p.A16, p.lda, c.m0, p.M, tid);
+    typename WideK<BH>::T b = WideK<BH>::make(p.B, p.B16, p.ldb, c.n0, p.N, tid);
     auto kof = [&](int j) {
         const int q = j + rot;
         return (q >= nt ? q - nt : q) * BKQ;
@@ -926,8 +977,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
             for (int j = 0; j < 2; ++j) acc[s][i][j] = f32x16{};
     a.full(kof(0));
     b.full(kof(0));
-    a.store(smem[0][0], tid);
-    b.store(smem[0][1], tid);
+    a.template store<NP>(smem[0][0], tid);
+    b.template store<NP>(smem[0][1], tid);
     a.full(kof(min(1, nt - 1)));
     b.full(kof(min(1, nt - 1)));
     lds_barrier();
@@ -935,19 +986,21 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     for (int j = 0; j < nt; ++j) {
         const int cur = j & 1;
         const int kn = kof(min(j + 2, nt - 1));
-        mma_stage_w(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
-        a.store(smem[cur ^ 1][0], tid);
-        b.store(smem[cur ^ 1][1], tid);
+        mma_stage_w<NP>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
+        a.template store<NP>(smem[cur ^ 1][0], tid);
+        b.template store<NP>(smem[cur ^ 1][1], tid);
         a.full(kn);
         b.full(kn);
         lds_barrier();
     }
-    const int kh = (lane >> 5) << 2;
+    // The epilogue's lane coordinates are taken again after the K loop, so its store offsets are computed
+    // here rather than held across the loop (the RoPE epilogue measured fewer spills the other way).
+    const int te = MODE == STORE_ROPE ? tid : opaque_tid(), le = te & 63, we = te >> 6;
     // The stages are done (the loop ended on a barrier): park the second subtile's accumulators in LDS,
     // each thread in its own slots, so the first subtile's epilogue has their registers.
     f32x16* park = reinterpret_cast<f32x16*>(&smem[0][0][0]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) park[q * WT_THREADS + tid] = acc[1][q >> 1][q & 1];
+    for (int q = 0; q < 4; ++q) park[q * WT_THREADS + te] = acc[1][q >> 1][q & 1];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         TileCoord cs = c;
@@ -955,12 +1008,12 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
         if (cs.m0 >= p.M) break;
         if (s == 1) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) acc[1][q >> 1][q & 1] = park[q * WT_THREADS + tid];
+            for (int q = 0; q < 4; ++q) acc[1][q >> 1][q & 1] = park[q * WT_THREADS + te];
         }
         if (cs.m0 + 128 <= p.M && c.n0 + WT <= p.N)
-            store_acc<true, true, MODE, false, false, true>(p, cs, acc[s], wm, wn, lr, kh);
+            store_acc<true, true, MODE, false, false, true>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2);
         else
-            store_acc<true, true, MODE, false, true, true>(p, cs, acc[s], wm, wn, lr, kh);
+            store_acc<true, true, MODE, false, true, true>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2);
     }
 }
 
@@ -1186,6 +1239,59 @@ struct OperandWK : OperandW {
     __device__ __forceinline__ void tail(int k0, int) { full(k0); }
 };
 
+// OperandWS over a bf16 copy (element (mn, k) at src[k·ld + mn]): the same 8 k per thread as 2-byte loads,
+// stored as loaded (one plane, the bf16 products).
+struct OperandWS16 {
+    __amdgpu_buffer_rsrc_t rsrc;
+    unsigned base, ld2;
+    int kq;
+    unsigned short v[8];
+    __device__ __forceinline__ OperandWS16(const __bf16* s, long ldl, int mn0, int MN, int tid, unsigned bytes)
+        : rsrc(buffer_of(s, bytes)), base((unsigned)min(mn0 + (tid & 255), MN - 1) * 2u),
+          ld2((unsigned)ldl * 2u), kq((tid >> 8) << 3) {}
+    __device__ __forceinline__ void full(int k0) {
+        const unsigned o = base + (unsigned)(k0 + kq) * ld2;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, o, (int)(e * ld2), 0);
+    }
+    __device__ __forceinline__ void tail(int k0, int kend) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = k0 + kq + e;
+            const unsigned short x =
+                __builtin_amdgcn_raw_buffer_load_b16(rsrc, base + (unsigned)min(k, kend - 1) * ld2, 0, 0);
+            v[e] = k < kend ? x : (unsigned short)0;
+        }
+    }
+    template <int NP = 1>
+    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+        static_assert(NP == 1, "a bf16 copy feeds bf16 products");
+        typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (unsigned)v[2 * i] | ((unsigned)v[2 * i + 1] << 16);
+        *reinterpret_cast<u32x4*>(lds + (tid & 255) * KPADQ + kq) = w;
+    }
+};
+
+// The mn-contiguous B operand of the wide pair: fp32 or its bf16 copy.
+template <bool H>
+struct WideS {
+    typedef OperandWS T;
+    static __device__ __forceinline__ T make(const float* s, const __bf16*, long ld, int mn0, int MN, int tid,
+                                             long rows) {
+        return T(s, ld, mn0, MN, tid, (unsigned)(rows * ld * 4));
+    }
+};
+template <>
+struct WideS<true> {
+    typedef OperandWS16 T;
+    static __device__ __forceinline__ T make(const float*, const __bf16* h, long ld, int mn0, int MN, int tid,
+                                             long rows) {
+        return T(h, ld, mn0, MN, tid, (unsigned)(rows * ld * 2));
+    }
+};
+
 // acc += A·Bᵀ over K positions [kb, ke) in 16-deep stages: the full stages in rotated order starting at
 // `rot`, then the ragged last one (when ke − kb is not a multiple of 16) on its own, so the loop body
 // carries no per-element selects.
@@ -1246,14 +1352,18 @@ __device__ __forceinline__ void write_partial_w(float* slot, const f32x16 (&acc)
 // nn and tn carry wide tile counts (tiles_m, tiles_n of 256 x 256 tiles); s counts 16-deep units.
 // NP = 3: split products (fp32); NP = 1: bf16 products (the bf16 policies of both backward classes).
 // RES: dX = dY·W + nn.R (the residual may be dX itself: each element is read and written by one lane).
-template <int NP, bool RES>
+// BH (NP = 1): W and x are read from their bf16 copies (nn.B16, tn.B16).
+template <int NP, bool RES, bool BH = false>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParams nn, GemmParams tn, PairPlan s) {
+    static_assert(NP == 1 || !BH, "bf16 copies feed bf16 products");
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];
     const int g = xcd_logical_block();
-    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, half = lane >> 5, kh = (lane >> 5) << 2;
     const int count = s.q + (g < s.r ? 1 : 0);
     for (int n = 0; n < count; ++n) {
+        // The lane's coordinates are taken afresh for each tile: derived from a value the compiler cannot
+        // see through, the epilogue's per-lane store offsets are not hoisted out of the loop and spilled.
+        const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+        const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, half = lane >> 5;
         const int t = g + n * s.G, tm = t / nn.tiles_n;
         TileCoord c;
         c.split = 0;
@@ -1263,29 +1373,48 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         c.kb = 0;
         c.ke = nn.K;
         OperandWK a(nn.A, nn.lda, c.m0, nn.M, tid, (unsigned)(nn.M * nn.lda * 4));
-        OperandWS b(nn.B, nn.ldb, c.n0, nn.N, tid, (unsigned)(nn.K * nn.ldb * 4));
+        typename WideS<BH>::T b = WideS<BH>::make(nn.B, nn.B16, nn.ldb, c.n0, nn.N, tid, nn.K);
         f32x16 acc[2][2][2];
         wide_mma<NP>(a, b, 0, nn.K, t, smem, acc, tid, wm, wn, lr, half);
+        // The epilogue's lane coordinates are taken again after the K loop, so its store offsets are
+        // computed here rather than before the loop (where they would be held, spilled, across it).
+        const int te = opaque_tid(), le = te & 63, we = te >> 6;
+        // With a residual to read, the second subtile's accumulators wait in LDS (the stages are done:
+        // wide_mma ends on a barrier), each thread in its own slots, during the first subtile's epilogue.
+        f32x16* park = reinterpret_cast<f32x16*>(&smem[0][0][0]);
+        if constexpr (RES) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) park[q * WT_THREADS + te] = acc[1][q >> 1][q & 1];
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             TileCoord cs = c;
             cs.m0 = c.m0 + 128 * h;
             if (cs.m0 >= nn.M) break;
+            if (RES && h == 1) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[1][q >> 1][q & 1] = park[q * WT_THREADS + te];
+            }
             if (cs.m0 + 128 <= nn.M && c.n0 + WT <= nn.N)
-                store_acc<true, true, STORE, RES, false, true>(nn, cs, acc[h], wm, wn, lr, kh);
+                store_acc<true, true, STORE, RES, false, true>(nn, cs, acc[h], we >> 2, we & 3, le & 31,
+                                                               (le >> 5) << 2);
             else
-                store_acc<true, true, STORE, RES, true, true>(nn, cs, acc[h], wm, wn, lr, kh);
+                store_acc<true, true, STORE, RES, true, true>(nn, cs, acc[h], we >> 2, we & 3, le & 31,
+                                                              (le >> 5) << 2);
         }
+        if constexpr (RES) lds_barrier();  // every park slot is read before the next stages overwrite them
     }
     const int lo = plan_tn_lo(s, g), hi = plan_tn_lo(s, g + 1);
     for (int u = lo; u < hi;) {
+        const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+        const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, half = lane >> 5;
         const int t = u / s.tn_units;
         const int a0 = u - t * s.tn_units;
         const int b0 = min(s.tn_units, a0 + (hi - u));
         const int tm = t / tn.tiles_n;
         const int m0 = tm * WT, n0 = (t - tm * tn.tiles_n) * WT;
         OperandWS a(tn.A, tn.lda, m0, tn.M, tid, (unsigned)(tn.K * tn.lda * 4));
-        OperandWS b(tn.B, tn.ldb, n0, tn.N, tid, (unsigned)(tn.K * tn.ldb * 4));
+        typename WideS<BH>::T b = WideS<BH>::make(tn.B, tn.B16, tn.ldb, n0, tn.N, tid, tn.K);
         f32x16 acc[2][2][2];
         wide_mma<NP>(a, b, a0 * BKQ, min(tn.K, b0 * BKQ), g, smem, acc, tid, wm, wn, lr, half);
         write_partial_w(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (WT * WT), acc);
@@ -1630,11 +1759,15 @@ template <int AOP, int BOP> void launch_h(laya_ctx* ctx, const GemmParams& p, in
 }
 
 // Picks the operand forms of a bf16 product (float4 access for a k-contiguous operand where it is allowed).
+bool wide_tiles_pay(const laya_ctx* ctx, const GemmParams& p, bool three);
+void launch_wide_h(laya_ctx* ctx, GemmParams p);
+
 template <bool AK, bool BKC> void launch_bf16(laya_ctx* ctx, const GemmParams& p, int blocks) {
     const bool va = AK && operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K);
     const bool vb = BKC && operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K);
     if constexpr (AK && BKC) {
-        if (va && vb) launch_h<KVEC, KVEC>(ctx, p, blocks);
+        if (va && vb && wide_tiles_pay(ctx, p, false)) launch_wide_h(ctx, p);
+        else if (va && vb) launch_h<KVEC, KVEC>(ctx, p, blocks);
         else if (va) launch_h<KVEC, KSCALAR>(ctx, p, blocks);
         else if (vb) launch_h<KSCALAR, KVEC>(ctx, p, blocks);
         else launch_h<KSCALAR, KSCALAR>(ctx, p, blocks);
@@ -1683,6 +1816,30 @@ void launch_wide(laya_ctx* ctx, GemmParams p) {
         hipLaunchKernelGGL((gemm_x6w_kernel<STORE_ROPE>), g, b, 0, ctx->stream, p);
     else
         hipLaunchKernelGGL((gemm_x6w_kernel<STORE>), g, b, 0, ctx->stream, p);
+    check_launch("gemm_x6w_kernel");
+}
+
+// The bf16 NT product on 256 x 256 tiles, reading whichever operands have bf16 copies.
+void launch_wide_h(laya_ctx* ctx, GemmParams p) {
+    profile_rename("gemm_nt_bf16w");
+    p.tiles_n = (p.N + WT - 1) / WT;
+    const dim3 g(((p.M + WT - 1) / WT) * p.tiles_n), b(WT_THREADS);
+    const bool ah = p.A16 != nullptr, bh = p.B16 != nullptr;
+#define WIDE_H(MODE)                                                                                         \
+    if (ah && bh)                                                                                            \
+        hipLaunchKernelGGL((gemm_x6w_kernel<MODE, 1, true, true>), g, b, 0, ctx->stream, p);                 \
+    else if (ah)                                                                                             \
+        hipLaunchKernelGGL((gemm_x6w_kernel<MODE, 1, true, false>), g, b, 0, ctx->stream, p);                \
+    else if (bh)                                                                                             \
+        hipLaunchKernelGGL((gemm_x6w_kernel<MODE, 1, false, true>), g, b, 0, ctx->stream, p);                \
+    else                                                                                                     \
+        hipLaunchKernelGGL((gemm_x6w_kernel<MODE, 1, false, false>), g, b, 0, ctx->stream, p);
+    if (p.mode == STORE_ROPE) {
+        WIDE_H(STORE_ROPE)
+    } else {
+        WIDE_H(STORE)
+    }
+#undef WIDE_H
     check_launch("gemm_x6w_kernel");
 }
 
@@ -1840,9 +1997,12 @@ int fill_splits(const laya_ctx* ctx, int tiles, int K, int min_k) {
 }  // namespace
 
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
-          const float* B, long ldb, float* C, long ldc, const float* bias, const float* R, long ldr) {
+          const float* B, long ldb, float* C, long ldc, const float* bias, const float* R, long ldr,
+          const __bf16* A16, const __bf16* B16) {
     if (M == 0 || N == 0) return;
     GemmParams p = make_params(M, N, K, A, lda, B, ldb, C, ldc, bias, R, ldr);
+    p.A16 = A16;
+    p.B16 = B16;
     const int tiles = p.tiles_m * p.tiles_n;
     float* out = C;
     bool split_store = false;
@@ -1883,9 +2043,12 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
 }
 
 void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* B, float* C, const float* bias,
-               const int* pos, const float* cos_t, const float* sin_t, int rope_cols) {
+               const int* pos, const float* cos_t, const float* sin_t, int rope_cols, const __bf16* A16,
+               const __bf16* B16) {
     if (M == 0 || N == 0) return;
     GemmParams p = make_params(M, N, K, A, K, B, K, C, N, bias, nullptr, 0);
+    p.A16 = A16;
+    p.B16 = B16;
     LAYA_REQUIRE(gemm_fast(p, true, true), "gemm_rope: operands must allow the vectorised kernel");
     LAYA_REQUIRE(rope_cols % 64 == 0 && rope_cols <= N && pos && cos_t && sin_t, "gemm_rope: bad rotary layout");
     p.mode = STORE_ROPE;
@@ -1895,6 +2058,10 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
     p.rope_cols = rope_cols;
     if (ctx->matmul_bf16 & 1) {
         ProfileScope scope(ctx, "gemm_nt_bf16", 2.0 * M * N * (double)K, 0.0);
+        if (wide_tiles_pay(ctx, p, false)) {
+            launch_wide_h(ctx, p);
+            return;
+        }
         hipLaunchKernelGGL((gemm_bf16_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
                            dim3(THREADS), 0, ctx->stream, p);
         check_launch("gemm_bf16_kernel");
@@ -1958,6 +2125,7 @@ bool make_pair_plan_wide(const laya_ctx* ctx, int n0, int out, int n1, int rows,
 // The wide pair for split products: dX without residual, dX's K a multiple of 16, dY k-contiguous in
 // float4s. Returns false (nothing launched) when the wide plan does not apply.
 bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out, bool half) {
+    const bool bh = half && nn.B16 && tn.B16;  // W and x from their bf16 copies
     if (out % BKQ != 0 || !operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) return false;
     const long lim = 1L << 31;  // buffer offsets of dY, W and x
     if ((long)rows * out * 4 >= lim || (long)out * in * 4 >= lim || (long)rows * in * 4 >= lim) return false;
@@ -1973,7 +2141,11 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
         ProfileScope scope(ctx, half ? "gemm_bwd_pair_bf16w" : "gemm_bwd_pair_x6w",
                            2.0 * 2.0 * rows * (double)in * out, 0.0);
         const dim3 g(s.G), b(WT_THREADS);
-        if (half && nn.R)
+        if (bh && nn.R)
+            hipLaunchKernelGGL((gemm_pair_wide_kernel<1, true, true>), g, b, 0, ctx->stream, nn, tn, s);
+        else if (bh)
+            hipLaunchKernelGGL((gemm_pair_wide_kernel<1, false, true>), g, b, 0, ctx->stream, nn, tn, s);
+        else if (half && nn.R)
             hipLaunchKernelGGL((gemm_pair_wide_kernel<1, true>), g, b, 0, ctx->stream, nn, tn, s);
         else if (half)
             hipLaunchKernelGGL((gemm_pair_wide_kernel<1, false>), g, b, 0, ctx->stream, nn, tn, s);
@@ -2003,13 +2175,15 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
 }
 
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
-                        float* dx, const float* dx_residual, float* dW) {
+                        float* dx, const float* dx_residual, float* dW, const __bf16* W16, const __bf16* x16) {
     if (rows == 0) return;
     // dx[rows, in] = dy[rows, out] · W[out, in]       (NN, K = out)
     GemmParams nn = make_params(rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual, in);
     nn.mode = STORE;
+    nn.B16 = W16;
     // dW[out, in] += dy[rows, out]ᵀ · x[rows, in]     (TN, K = rows)
     GemmParams tn = make_params(out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr, 0);
+    tn.B16 = x16;
     const bool split = !(ctx->matmul_bf16 & 6) && (ctx->matmul_split & 6) == 6 && gemm_fits_h(nn, true, false) &&
                        gemm_fits_h(tn, false, false);
     const bool fp32 = !((ctx->matmul_bf16 | ctx->matmul_split) & 6) && gemm_fast(nn, true, false) &&
