@@ -193,6 +193,9 @@ def main():
     ap.add_argument("--fp32-mfma", action="store_true",
                     help="fp32 products on the fp32 matrix cores instead of exact bf16 splits (for comparison)")
     ap.add_argument("--no-profile", action="store_true", help="time without per-launch events")
+    ap.add_argument("--no-bf16-copies", action="store_true",
+                    help="bf16 workloads: round the fp32 weights and activations inside the products instead of "
+                         "keeping bf16 copies (same results, less memory)")
     ap.add_argument("--by-value", action="store_true",
                     help="pass each batch as host arrays (laya_model_train_step: host planning and uploads inside "
                          "every step), to measure the PCIe-inclusive rate; the default stages batches first")
@@ -220,6 +223,8 @@ def main():
     long_workload = w["seq"] > 512
     model = TrainableDecisionModel.synthetic(mc, seed=42, std=0.02, ctx=ctx)
     model.head_dropout = 0.1
+    if args.no_bf16_copies:
+        model.set_bf16_copies(False)
     if args.traffic_probe:
         import ctypes
         from laya_amd._native import check, lib

@@ -276,6 +276,16 @@ int laya_model_set_head_dropout(laya_model* model, float p);
 int laya_model_set_layer_checkpointing(laya_model* model, int mode);
 /* The mode, and whether the current arena recomputes (0 before the first forward). Either may be NULL. */
 int laya_model_layer_checkpointing(laya_model* model, int* mode, int* recomputing);
+/* bf16 copies for the bf16 products (PackedMatrixBf16, src/StructuredDecisions.Base/Numerics/
+ * PackedMatrixBf16.cs:7-21, keeps weights as bf16 for its products; here the fp32 arenas stay the masters).
+ * While the context's precision policy has bf16 products (laya_ctx_set_matmul_precision), the model keeps
+ * bf16(weights), updated by the AdamW step with each update, and bf16 copies of the saved activations the
+ * products read (written by the kernels that produce them); the products read those copies instead of
+ * rounding fp32 operands on their way into LDS — the same values, half the bytes. on = 1 (default) keeps
+ * them, 0 drops them (less memory). Results are the same either way. Takes effect at the next forward. */
+int laya_model_set_bf16_copies(laya_model* model, int on);
+/* Parameter i's bf16 copy (numel uint16, the bf16 bit patterns); LAYA_ERR_STATE when no current copy exists. */
+int laya_model_get_param_bf16(laya_model* model, int i, uint16_t* host);
 /* Forward (TrainableDecisionModel.cs:248-353). Keeps what the backward needs resident in HBM (all of it,
  * or the encoder layers' inputs under layer checkpointing). logits_host (may be NULL) receives
  * Σ n_options floats and synchronises. */

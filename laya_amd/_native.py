@@ -140,6 +140,8 @@ SIGNATURES = {
     "laya_model_set_head_dropout": (c_int, [P, c_float]),
     "laya_model_set_layer_checkpointing": (c_int, [P, c_int]),
     "laya_model_layer_checkpointing": (c_int, [P, P, P]),
+    "laya_model_set_bf16_copies": (c_int, [P, c_int]),
+    "laya_model_get_param_bf16": (c_int, [P, c_int, P]),
     "laya_model_forward": (c_int, [P, ctypes.POINTER(BatchC), c_int, c_u64, P]),
     "laya_model_backward": (c_int, [P, P]),
     "laya_model_readout": (c_int, [P, P, P, P]),

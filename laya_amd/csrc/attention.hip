@@ -19,6 +19,7 @@
 //   dq:  each wave owns 32 queries (Q, dO in registers) and sweeps the key tiles: Sᵀ, dPᵀ, dSᵀ,
 //        dQᵀ += Kᵀ·dSᵀ.
 #include "common.hpp"
+#include "elementwise.hpp"
 #include "split.hpp"
 
 namespace laya {
@@ -43,6 +44,7 @@ struct Params {
     const float* cos_t;
     const float* sin_t;
     float* context;
+    __bf16* context16;  // optional bf16 copy of the context (nearest even)
     float* lse;
     const float* dcontext;
     float* dots;  // Σ_d dO·O per (row, head)
@@ -138,6 +140,20 @@ __device__ __forceinline__ void store_acc(const f32x16 (&acc)[Shape<D>::ND], flo
             const f32x4 v = {acc[dt][4 * r4] * scale, acc[dt][4 * r4 + 1] * scale, acc[dt][4 * r4 + 2] * scale,
                              acc[dt][4 * r4 + 3] * scale};
             st4(dst_row + dt * 32 + 8 * r4 + 4 * h, v);
+        }
+}
+
+// store_acc's values, also as bf16 (nearest even) into row `row` of a bf16 copy.
+template <int D>
+__device__ __forceinline__ void store_acc16(const f32x16 (&acc)[Shape<D>::ND], __bf16* dst_row, int h, float scale) {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int dt = 0; dt < Shape<D>::ND; ++dt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+            const f32x4 v = {acc[dt][4 * r4] * scale, acc[dt][4 * r4 + 1] * scale, acc[dt][4 * r4 + 2] * scale,
+                             acc[dt][4 * r4 + 3] * scale};
+            *reinterpret_cast<bf16x4*>(dst_row + dt * 32 + 8 * r4 + 4 * h) = __builtin_convertvector(v, bf16x4);
         }
 }
 
@@ -508,6 +524,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     if (qvalid) {
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
         store_acc<D>(o, p.context + (long)(start + q) * p.hidden + qcol, h, inv);
+        if (p.context16) store_acc16<D>(o, p.context16 + (long)(start + q) * p.hidden + qcol, h, inv);
         if (h == 0) p.lse[(long)(start + q) * p.heads + head] = lt > 0.0f ? m + log2f(lt) : __builtin_huge_valf();
     }
 }
@@ -895,11 +912,15 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
         }
     }
 
-    if (kvalid) {
-        if (rope) inverse_rope_acc<D>(dk, p, key, h);
-        float* dst = p.dqkv + (long)(start + key) * stride;
-        store_acc<D>(dk, dst + kcol, h, 1.0f);
-        store_acc<D>(dv, dst + vcol, h, 1.0f);
+    // The epilogue's lane values are taken again after the loop rather than held across it.
+    int te = threadIdx.x;
+    asm volatile("" : "+v"(te));
+    const int he = (te & 63) >> 5, keye = kb0 + (te >> 6) * WAVE_ROWS + (te & 31);
+    if (keye < L) {
+        if (rope) inverse_rope_acc<D>(dk, p, keye, he);
+        float* dst = p.dqkv + (long)(start + keye) * stride;
+        store_acc<D>(dk, dst + kcol, he, 1.0f);
+        store_acc<D>(dv, dst + vcol, he, 1.0f);
     }
 }
 
@@ -1096,7 +1117,7 @@ bool split_attention(const laya_ctx* ctx) { return (ctx->matmul_split | ctx->mat
 
 }  // namespace
 
-void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse) {
+void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse, __bf16* context16) {
     check_args(a);
     if (a.nseg == 0 || a.max_len == 0) return;
     Params p = make_params(a);
@@ -1105,14 +1126,21 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
     p.lse = lse;
     dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
     const bool split = a.head_dim == 64 && split_attention(ctx);
-    ProfileScope scope(ctx, split ? "attention_fwd_x6" : "attention_fwd", 4.0 * a.hidden * a.keys, 0.0);
-    if (split)
-        hipLaunchKernelGGL(attn_fwd_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
-    else if (a.head_dim == 64)
-        hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
-    else
-        hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
-    check_launch("attn_fwd_kernel");
+    p.context16 = split ? context16 : nullptr;
+    {
+        ProfileScope scope(ctx, split ? "attention_fwd_x6" : "attention_fwd", 4.0 * a.hidden * a.keys, 0.0);
+        if (split)
+            hipLaunchKernelGGL(attn_fwd_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        else if (a.head_dim == 64)
+            hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        else
+            hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
+        check_launch("attn_fwd_kernel");
+    }
+    if (context16 && !split) {
+        LAYA_REQUIRE(a.rows >= 0, "attention: row count needed for the bf16 copy of the context");
+        to_bf16(ctx, context, (size_t)a.rows * a.hidden, context16);
+    }
 }
 
 void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,

@@ -219,9 +219,10 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
 // Σ over rows of a [rows, n] matrix added into out[n], deterministic (bias gradients).
 void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out);
 
+// y16 (optional): a bf16 copy of y (nearest even), for the bf16 products that read it.
 void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps, float* y,
                    float* mean, float* rstd, const int* gather_ids = nullptr, const float* add_table = nullptr,
-                   const int* add_index = nullptr);
+                   const int* add_index = nullptr, __bf16* y16 = nullptr);
 // Column sums whose reduction is deferred: `count` partial rows of `n` floats in `part`, added into `out`.
 struct ColumnSumJob {
     const float* part;
@@ -274,7 +275,8 @@ inline double window_keys(int L, int hw) {
     for (int q = 0; q < L; ++q) s += std::min(L - 1, q + hw) - std::max(0, q - hw) + 1;
     return s;
 }
-void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse);
+// context16 (optional): a bf16 copy of the context (nearest even), for the bf16 products that read it.
+void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse, __bf16* context16 = nullptr);
 
 // RlcdObjective.Compute (RlcdObjective.cs:57-155) with supplied standard-normal draws [groups][Σ K], all
 // operands on the device; grad [Σ K]; losses [4] = total, policy, cross-entropy, mean reward.

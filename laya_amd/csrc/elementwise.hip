@@ -8,6 +8,7 @@ namespace laya {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 
@@ -42,7 +43,8 @@ __global__ void gelu_bwd_kernel(const float* u, float* g, size_t n) {
 }
 
 // GeGLU, 4 columns per thread: act[t, i] = gelu(wide[t, i]) · wide[t, I + i].
-__global__ void geglu_fwd_kernel(const float* __restrict__ wide, int rows, int inter, float* __restrict__ act) {
+__global__ void geglu_fwd_kernel(const float* __restrict__ wide, int rows, int inter, float* __restrict__ act,
+                                 __bf16* __restrict__ act16) {
     const int q = inter >> 2;
     const size_t n = (size_t)rows * q;
     GRID_STRIDE(i, n) {
@@ -50,8 +52,9 @@ __global__ void geglu_fwd_kernel(const float* __restrict__ wide, int rows, int i
         const int c = (int)(i - t * q) * 4;
         const float* w = wide + t * 2 * inter;
         const f32x4 x = ld4(w + c), g = ld4(w + inter + c);
-        st4(act + t * inter + c, f32x4{gelu_f(x[0]) * g[0], gelu_f(x[1]) * g[1], gelu_f(x[2]) * g[2],
-                                       gelu_f(x[3]) * g[3]});
+        const f32x4 o = {gelu_f(x[0]) * g[0], gelu_f(x[1]) * g[1], gelu_f(x[2]) * g[2], gelu_f(x[3]) * g[3]};
+        st4(act + t * inter + c, o);
+        if (act16) *reinterpret_cast<bf16x4*>(act16 + t * inter + c) = __builtin_convertvector(o, bf16x4);
     }
 }
 
@@ -135,7 +138,7 @@ __global__ void dropout_copy4_kernel(const f32x4* src, f32x4* dst, size_t n4, fl
 }
 
 __global__ void relu_dropout_fwd4_kernel(const f32x4* wide, size_t n4, float p, float keep, uint64_t seed,
-                                         f32x4* dropped) {
+                                         f32x4* dropped, bf16x4* dropped16) {
     GRID_STRIDE(i, n4) {
         const f32x4 w = wide[i];
         f32x4 o;
@@ -145,7 +148,16 @@ __global__ void relu_dropout_fwd4_kernel(const f32x4* wide, size_t n4, float p, 
             o[e] = (p > 0.0f && uniform01(seed, 4 * i + e) < p) ? 0.0f : (p > 0.0f ? r * keep : r);
         }
         dropped[i] = o;
+        if (dropped16) dropped16[i] = __builtin_convertvector(o, bf16x4);
     }
+}
+
+// dst = bf16(src), nearest even: the bf16 copies of weights and activations the bf16 products read.
+__global__ void to_bf16_kernel(const f32x4* __restrict__ src, bf16x4* __restrict__ dst, size_t n4) {
+    GRID_STRIDE(i, n4) dst[i] = __builtin_convertvector(src[i], bf16x4);
+}
+__global__ void to_bf16_scalar_kernel(const float* __restrict__ src, __bf16* __restrict__ dst, size_t n) {
+    GRID_STRIDE(i, n) dst[i] = (__bf16)src[i];
 }
 
 // The backward from the forward's output: an element passes its gradient (times 1/(1 − p)) exactly when
@@ -422,17 +434,31 @@ void gelu_bwd(laya_ctx* ctx, const float* u, float* g, size_t n) {
     hipLaunchKernelGGL(gelu_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, u, g, n);
     check_launch("gelu_bwd_kernel");
 }
-void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act) {
+void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, __bf16* act16) {
     if (rows <= 0 || inter <= 0) return;
-    ProfileScope scope(ctx, "geglu_fwd", 0.0, 12.0 * rows * (double)inter);
+    ProfileScope scope(ctx, "geglu_fwd", 0.0, (12.0 + (act16 ? 2.0 : 0.0)) * rows * (double)inter);
     if (inter % 4 == 0) {
         hipLaunchKernelGGL(geglu_fwd_kernel, dim3(grid_for((size_t)rows * inter / 4)), dim3(256), 0, ctx->stream,
-                           wide, rows, inter, act);
+                           wide, rows, inter, act, act16);
     } else {
         hipLaunchKernelGGL(geglu_fwd_scalar_kernel, dim3(grid_for((size_t)rows * inter)), dim3(256), 0, ctx->stream,
                            wide, rows, inter, act);
+        if (act16) to_bf16(ctx, act, (size_t)rows * inter, act16);
     }
     check_launch("geglu_fwd_kernel");
+}
+
+void to_bf16(laya_ctx* ctx, const float* src, size_t n, __bf16* dst) {
+    if (!n) return;
+    ProfileScope scope(ctx, "to_bf16", 0.0, 6.0 * n);
+    if (n % 4 == 0 && vec4(src) && ((uintptr_t)dst & 7u) == 0) {
+        hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const f32x4*>(src), reinterpret_cast<bf16x4*>(dst), n / 4);
+        check_launch("to_bf16_kernel");
+        return;
+    }
+    hipLaunchKernelGGL(to_bf16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, src, dst, n);
+    check_launch("to_bf16_scalar_kernel");
 }
 void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide) {
     if (rows <= 0 || inter <= 0) return;
@@ -472,20 +498,22 @@ void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p
                        1.0f / (1.0f - p), seed);
     check_launch("dropout_copy4_kernel");
 }
-void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped) {
+void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped,
+                      __bf16* dropped16) {
     if (!n) return;
     const float keep = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
-    ProfileScope scope(ctx, "relu_dropout_fwd", 0.0, 8.0 * n);
-    if (n % 4 == 0 && vec4(wide) && vec4(dropped)) {
+    ProfileScope scope(ctx, "relu_dropout_fwd", 0.0, (8.0 + (dropped16 ? 2.0 : 0.0)) * n);
+    if (n % 4 == 0 && vec4(wide) && vec4(dropped) && ((uintptr_t)dropped16 & 7u) == 0) {
         hipLaunchKernelGGL(relu_dropout_fwd4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<const f32x4*>(wide), n / 4, p, keep, seed,
-                           reinterpret_cast<f32x4*>(dropped));
+                           reinterpret_cast<f32x4*>(dropped), reinterpret_cast<bf16x4*>(dropped16));
         check_launch("relu_dropout_fwd4_kernel");
         return;
     }
     hipLaunchKernelGGL(relu_dropout_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, wide, n, p, keep, seed,
                        dropped);
     check_launch("relu_dropout_fwd_kernel");
+    if (dropped16) to_bf16(ctx, dropped, n, dropped16);
 }
 void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, float p, uint64_t seed) {
     if (!n) return;

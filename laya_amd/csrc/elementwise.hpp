@@ -9,12 +9,15 @@ void add(laya_ctx* ctx, float* dst, const float* src, size_t n);
 void scale(laya_ctx* ctx, float* dst, float s, size_t n);
 void gelu_fwd(laya_ctx* ctx, const float* x, size_t n, float* y);
 void gelu_bwd(laya_ctx* ctx, const float* u, float* g, size_t n);
-void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act);
+// The optional __bf16* outputs are copies rounded to nearest even, for the bf16 products that read them.
+void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, __bf16* act16 = nullptr);
+void to_bf16(laya_ctx* ctx, const float* src, size_t n, __bf16* dst);
 void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide);
 void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed);
 // dst = Dropout(src) out of place (one pass).
 void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p, uint64_t seed);
-void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped);
+void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped,
+                      __bf16* dropped16 = nullptr);
 void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, float p, uint64_t seed);
 void rotary_apply(laya_ctx* ctx, const float* cos_t, const float* sin_t, int head_dim, float* vec, int rows,
                   const int* pos, int inverse);
@@ -47,8 +50,10 @@ struct AdamGroups {
     size_t begin[4], end[4];
     float decay[4], step_size[4];
 };
-// Elements outside every group are left alone (frozen parameters); zero_grads clears all n gradients.
+// Elements outside every group are left alone (frozen parameters); zero_grads clears all n gradients;
+// mirror (optional, n bf16) receives bf16(p) of every updated element.
 void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n, const AdamGroups& groups,
-                 float beta1, float beta2, float eps, float sqrt_c2, const float* coef, int zero_grads);
+                 float beta1, float beta2, float eps, float sqrt_c2, const float* coef, int zero_grads,
+                 __bf16* mirror = nullptr);
 
 }  // namespace laya

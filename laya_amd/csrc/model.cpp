@@ -43,13 +43,15 @@ struct Param {
 // Carves one device allocation into 256-byte aligned tensors.
 struct Carver {
     size_t bytes = 0;
-    std::vector<std::pair<float**, size_t>> slots;
-    void add(float*& p, size_t floats) {
-        slots.push_back({&p, bytes});
-        bytes += (floats * sizeof(float) + 255) / 256 * 256;
+    std::vector<std::pair<void**, size_t>> slots;
+    void add(float*& p, size_t floats) { add_bytes(reinterpret_cast<void**>(&p), floats * sizeof(float)); }
+    void add(__bf16*& p, size_t n) { add_bytes(reinterpret_cast<void**>(&p), n * sizeof(__bf16)); }
+    void add_bytes(void** p, size_t b) {
+        slots.push_back({p, bytes});
+        bytes += (b + 255) / 256 * 256;
     }
     void bind(char* base) {
-        for (auto& s : slots) *s.first = reinterpret_cast<float*>(base + s.second);
+        for (auto& s : slots) *s.first = base + s.second;
     }
 };
 
@@ -136,12 +138,22 @@ struct laya_model {
     // that only when keeping everything would not fit (the context's cap, or the device's memory).
     int checkpoint_mode = 2;
     bool recompute = false;  // the arena's current layout
+    // bf16 copies for the bf16 products (a bf16 precision policy): the fp32 arenas stay the masters; WB is
+    // bf16(P), refreshed from P when stale and written by AdamW with each update; the activation arena then
+    // also holds bf16 copies of the saved activations the products read (written by their producers). A
+    // product reads a copy instead of rounding its fp32 operand on the way into LDS: the same values.
+    bool bf16_copies = true;   // the option (laya_model_set_bf16_copies)
+    bool copies = false;       // the activation arena's current layout has the copies
+    __bf16* WB = nullptr;
+    bool wb_fresh = false;
     void* act_block = nullptr;
     struct EncAct {
         float *x, *normed, *mean1, *rstd1, *qkv, *ctx, *lse, *res, *mlpn, *mean2, *rstd2, *wide, *act;
+        __bf16 *normed16, *ctx16, *mlpn16, *act16;  // layer 0: normed16 = bf16(x), its QKV input
     };
     struct HeadAct {
         float *x, *n1, *mean1, *rstd1, *qkv, *ctx, *lse, *res, *n2, *mean2, *rstd2, *wide, *drop;
+        __bf16 *n1_16, *ctx16, *n2_16, *drop16;
     };
     std::vector<EncAct> ea;
     std::vector<HeadAct> ha;
@@ -198,6 +210,8 @@ struct laya_model {
     }
 
     float* W(int i) const { return i >= 0 ? P + params[i].offset : nullptr; }
+    // The bf16 copy of parameter i when the products read copies (else null: they round W themselves).
+    const __bf16* W16(int i) const { return i >= 0 && copies && WB && wb_fresh ? WB + params[i].offset : nullptr; }
     int find(const std::string& name) const {
         auto it = by_name.find(name);
         if (it == by_name.end()) throw laya::Error(LAYA_ERR_MISSING, "the model has no '" + name + "' tensor");
@@ -284,7 +298,7 @@ void ensure_rotary(laya_model* m, int positions) {
 
 // The activation arena's layout for Tc tokens; with `recompute`, the encoder layers share one set of
 // internal buffers and keep only their inputs.
-Carver carve_activations(laya_model* m, size_t Tz, size_t Mc, bool recompute) {
+Carver carve_activations(laya_model* m, size_t Tz, size_t Mc, bool recompute, bool copies) {
     const size_t d = m->d(), I = m->I(), ff = m->cfg.head_ff;
     const size_t H = m->cfg.heads, HH = m->head_heads;
     Carver cv;
@@ -305,6 +319,12 @@ Carver carve_activations(laya_model* m, size_t Tz, size_t Mc, bool recompute) {
         cv.add(a.rstd2, Tz);
         cv.add(a.wide, Tz * 2 * I);
         cv.add(a.act, Tz * I);
+        if (copies) {
+            cv.add(a.normed16, Tz * d);
+            cv.add(a.ctx16, Tz * d);
+            cv.add(a.mlpn16, Tz * d);
+            cv.add(a.act16, Tz * I);
+        }
     }
     m->ha.assign(m->cfg.head_layers, {});
     for (auto& a : m->ha) {
@@ -321,6 +341,12 @@ Carver carve_activations(laya_model* m, size_t Tz, size_t Mc, bool recompute) {
         cv.add(a.rstd2, Tz);
         cv.add(a.wide, Tz * ff);
         cv.add(a.drop, Tz * ff);
+        if (copies) {
+            cv.add(a.n1_16, Tz * d);
+            cv.add(a.ctx16, Tz * d);
+            cv.add(a.n2_16, Tz * d);
+            cv.add(a.drop16, Tz * ff);
+        }
     }
     cv.add(m->x_final, Tz * d);
     cv.add(m->emb_mean, Tz);
@@ -361,7 +387,8 @@ void share_layer_internals(laya_model* m) {
 
 void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     const bool want_full = m->checkpoint_mode != 1;
-    const bool layout_ok = m->checkpoint_mode == 2 || m->recompute == (m->checkpoint_mode == 1);
+    const bool copies = m->bf16_copies && m->ctx->matmul_bf16 != 0;
+    const bool layout_ok = (m->checkpoint_mode == 2 || m->recompute == (m->checkpoint_mode == 1)) && m->copies == copies;
     if (T <= m->cap_tokens && nmark <= m->cap_markers && nseg <= m->cap_segs && m->act_block && layout_ok) return;
     m->has_tape = false;  // the activations of the last forward go with the old block
     if (m->act_block) {
@@ -371,7 +398,7 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     const int Tc = std::max(T, m->cap_tokens), Mc = std::max(std::max(nmark, m->cap_markers), 1),
               Sc = std::max(std::max(nseg, m->cap_segs), 1);
     bool recompute = !want_full;
-    Carver cv = carve_activations(m, Tc, Mc, recompute);
+    Carver cv = carve_activations(m, Tc, Mc, recompute, copies);
     TableCarve tc;
     tc.add(cv, Tc, Mc, Sc);
     if (m->checkpoint_mode == 2) {
@@ -381,7 +408,7 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
         const bool over_cap = m->ctx->cap && m->ctx->in_use + cv.bytes > m->ctx->cap;
         if (over_cap || cv.bytes + (64u << 20) > free_b) {
             recompute = true;
-            cv = carve_activations(m, Tc, Mc, true);
+            cv = carve_activations(m, Tc, Mc, true, copies);
             tc = TableCarve{};
             tc.add(cv, Tc, Mc, Sc);
         }
@@ -390,11 +417,26 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     cv.bind(static_cast<char*>(m->act_block));
     if (recompute) share_layer_internals(m);
     m->recompute = recompute;
+    m->copies = copies;
     m->own = tc.bind();
     m->cur = m->own;
     m->cap_tokens = Tc;
     m->cap_markers = Mc;
     m->cap_segs = Sc;
+}
+
+// The weights' bf16 copy, when the products read copies: allocated on first use, refreshed from the fp32
+// masters when a host write or an update without it left it stale.
+void ensure_mirror(laya_model* m) {
+    if (!m->copies) return;
+    if (!m->WB) {
+        m->WB = static_cast<__bf16*>(m->ctx->alloc(m->total * sizeof(__bf16)));
+        m->wb_fresh = false;
+    }
+    if (!m->wb_fresh) {
+        to_bf16(m->ctx, m->P, m->total, m->WB);
+        m->wb_fresh = true;
+    }
 }
 
 void upload_ints(laya_model* m, int* dst, const std::vector<int>& src) {
@@ -546,22 +588,25 @@ AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p
     return a;
 }
 
-void linear(laya_model* m, const float* x, int rows, int in, int wi, int bi, int out, const float* residual, float* y) {
+// x16: x's bf16 copy, or null.
+void linear(laya_model* m, const float* x, int rows, int in, int wi, int bi, int out, const float* residual, float* y,
+            const __bf16* x16 = nullptr) {
     gemm(m->ctx, GemmLayout::NT, GemmEpilogue::Store, rows, out, in, x, in, m->W(wi), in, y, out, m->W(bi), residual,
-         out);
+         out, x16, m->W16(wi));
 }
 
 // Ops.LinearBackward (Ops.cs:33-69): dx = dy·W (overwrite; + residual when given), dW += dyᵀ·x, db += Σ dy.
 void linear_backward(laya_model* m, const float* x, const float* dy, int rows, int in, int out, int wi, int bi,
-                     float* dx, const float* dx_residual = nullptr) {
+                     float* dx, const float* dx_residual = nullptr, const __bf16* x16 = nullptr) {
     float* dW = m->Gt(wi);
     if (dx && dW) {
-        gemm_backward_pair(m->ctx, rows, in, out, dy, m->W(wi), x, dx, dx_residual, dW);
+        gemm_backward_pair(m->ctx, rows, in, out, dy, m->W(wi), x, dx, dx_residual, dW, m->W16(wi), x16);
     } else if (dx) {
         gemm(m->ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, m->W(wi), in, dx, in, nullptr,
-             dx_residual, in);
+             dx_residual, in, nullptr, m->W16(wi));
     } else if (dW) {
-        gemm(m->ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
+        gemm(m->ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr,
+             0, nullptr, x16);
     }
     if (float* db = m->Gt(bi)) column_sum_add(m->ctx, dy, rows, out, db);
 }
@@ -584,22 +629,26 @@ void encoder_forward(laya_model* m, int l, bool output = true) {
     float* out = l + 1 < m->cfg.layers ? m->ea[l + 1].x : m->x_final;
     const float* normed = a.x;
     if (L.attn_norm >= 0) {
-        layernorm_fwd(ctx, a.x, T, d, m->W(L.attn_norm), m->W(L.attn_norm_b), eps, a.normed, a.mean1, a.rstd1);
+        layernorm_fwd(ctx, a.x, T, d, m->W(L.attn_norm), m->W(L.attn_norm_b), eps, a.normed, a.mean1, a.rstd1,
+                      nullptr, nullptr, nullptr, a.normed16);
         normed = a.normed;
+    } else if (a.normed16) {
+        to_bf16(ctx, a.x, (size_t)T * d, a.normed16);  // nn.Identity: the QKV input is x itself
     }
     if (fused_rope(m)) {
         const laya_rotary& r = L.kind == 0 ? m->rot_global : m->rot_local;
         gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->cur.pos, r.cos_t, r.sin_t,
-                  2 * d);
+                  2 * d, a.normed16, m->W16(L.wqkv));
     } else {
-        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv);
+        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv, a.normed16);
     }
-    attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse);
-    linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res);  // x1 = x + attn
-    layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2);
-    linear(m, a.mlpn, T, d, L.wi, L.wi_b, 2 * I, nullptr, a.wide);
-    geglu_fwd(ctx, a.wide, T, I, a.act);
-    if (output) linear(m, a.act, T, I, L.mlp_wo, L.mlp_wo_b, d, a.res, out);  // x2 = x1 + mlp
+    attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse, a.ctx16);
+    linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res, a.ctx16);  // x1 = x + attn
+    layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2, nullptr,
+                  nullptr, nullptr, a.mlpn16);
+    linear(m, a.mlpn, T, d, L.wi, L.wi_b, 2 * I, nullptr, a.wide, a.mlpn16);
+    geglu_fwd(ctx, a.wide, T, I, a.act, a.act16);
+    if (output) linear(m, a.act, T, I, L.mlp_wo, L.mlp_wo_b, d, a.res, out, a.act16);  // x2 = x1 + mlp
 }
 
 void forward(laya_model* m, bool train, uint64_t seed) {
@@ -608,6 +657,7 @@ void forward(laya_model* m, bool train, uint64_t seed) {
     const float eps = m->cfg.norm_eps;
     m->training = train;
     m->seed = seed;
+    ensure_mirror(m);
 
     // Embedding gather fused into the embedding LayerNorm.
     float* x0 = m->cfg.layers > 0 ? m->ea[0].x : m->x_final;
@@ -623,25 +673,27 @@ void forward(laya_model* m, bool train, uint64_t seed) {
         auto& H = m->head[j];
         auto& a = m->ha[j];
         float* out = j + 1 < m->cfg.head_layers ? m->ha[j + 1].x : m->head_out;
-        layernorm_fwd(ctx, a.x, T, d, m->W(H.norm1), m->W(H.norm1_b), 1e-5f, a.n1, a.mean1, a.rstd1);
-        linear(m, a.n1, T, d, H.in_proj, H.in_proj_b, 3 * d, nullptr, a.qkv);
-        attention_fwd(ctx, head_attention(m, a.qkv, j, p, seed), a.ctx, a.lse);
+        layernorm_fwd(ctx, a.x, T, d, m->W(H.norm1), m->W(H.norm1_b), 1e-5f, a.n1, a.mean1, a.rstd1, nullptr,
+                      nullptr, nullptr, a.n1_16);
+        linear(m, a.n1, T, d, H.in_proj, H.in_proj_b, 3 * d, nullptr, a.qkv, a.n1_16);
+        attention_fwd(ctx, head_attention(m, a.qkv, j, p, seed), a.ctx, a.lse, a.ctx16);
         if (p > 0.0f) {
-            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, nullptr, a.res);
+            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, nullptr, a.res, a.ctx16);
             dropout(ctx, a.res, (size_t)T * d, p, salt(seed, j, 1));
             add(ctx, a.res, a.x, (size_t)T * d);
         } else {
-            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, a.x, a.res);
+            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, a.x, a.res, a.ctx16);
         }
-        layernorm_fwd(ctx, a.res, T, d, m->W(H.norm2), m->W(H.norm2_b), 1e-5f, a.n2, a.mean2, a.rstd2);
-        linear(m, a.n2, T, d, H.linear1, H.linear1_b, ff, nullptr, a.wide);
-        relu_dropout_fwd(ctx, a.wide, (size_t)T * ff, p, salt(seed, j, 2), a.drop);
+        layernorm_fwd(ctx, a.res, T, d, m->W(H.norm2), m->W(H.norm2_b), 1e-5f, a.n2, a.mean2, a.rstd2, nullptr,
+                      nullptr, nullptr, a.n2_16);
+        linear(m, a.n2, T, d, H.linear1, H.linear1_b, ff, nullptr, a.wide, a.n2_16);
+        relu_dropout_fwd(ctx, a.wide, (size_t)T * ff, p, salt(seed, j, 2), a.drop, a.drop16);
         if (p > 0.0f) {
-            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, nullptr, out);
+            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, nullptr, out, a.drop16);
             dropout(ctx, out, (size_t)T * d, p, salt(seed, j, 3));
             add(ctx, out, a.res, (size_t)T * d);
         } else {
-            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, a.res, out);
+            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, a.res, out, a.drop16);
         }
     }
     // Scorer at the option markers (TrainableDecisionModel.cs:313-323).
@@ -677,22 +729,22 @@ void encoder_backward(laya_model* m, int l, bool need_input) {
     auto& a = m->ea[l];
     const int T = m->T, d = m->d(), I = m->I();
     const float eps = m->cfg.norm_eps;
-    linear_backward(m, a.act, m->dS, T, I, d, L.mlp_wo, L.mlp_wo_b, m->dact);
+    linear_backward(m, a.act, m->dS, T, I, d, L.mlp_wo, L.mlp_wo_b, m->dact, nullptr, a.act16);
     geglu_bwd(ctx, a.wide, m->dact, T, I, m->dwide);
-    linear_backward(m, a.mlpn, m->dwide, T, d, 2 * I, L.wi, L.wi_b, m->dn);
+    linear_backward(m, a.mlpn, m->dwide, T, d, 2 * I, L.wi, L.wi_b, m->dn, nullptr, a.mlpn16);
     ln_backward(m, a.res, T, d, L.mlp_norm, L.mlp_norm_b, eps, m->dn, m->dS, a.mean2, a.rstd2);
-    linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx);
+    linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx, nullptr, a.ctx16);
     attention_bwd(ctx, enc_attention(m, a.qkv, L.kind), T, a.ctx, a.lse, m->dctx, m->dqkv);
     const float* normed = L.attn_norm >= 0 ? a.normed : a.x;
     if (!need_input) {
-        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, nullptr);
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, nullptr, nullptr, a.normed16);
         return;
     }
     if (L.attn_norm < 0) {
         // Layer 0: nn.Identity, so dx = dResidual + dNormed, fused as the GEMM's residual.
-        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dS, m->dS);
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dS, m->dS, a.normed16);
     } else {
-        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dn);
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dn, nullptr, a.normed16);
         ln_backward(m, a.x, T, d, L.attn_norm, L.attn_norm_b, eps, m->dn, m->dS, a.mean1, a.rstd1);
     }
 }
@@ -710,21 +762,21 @@ void head_backward(laya_model* m, int j) {
         dropout_copy(m, m->dS, m->dy, nd, p, salt(m->seed, j, 3));
         dy = m->dy;
     }
-    linear_backward(m, a.drop, dy, T, ff, d, H.linear2, H.linear2_b, m->dact);
+    linear_backward(m, a.drop, dy, T, ff, d, H.linear2, H.linear2_b, m->dact, nullptr, a.drop16);
     if (ff % 4 == 0)
         relu_dropout_bwd_from_output(ctx, a.drop, m->dact, (size_t)T * ff, p);
     else
         relu_dropout_bwd(ctx, a.wide, m->dact, (size_t)T * ff, p, salt(m->seed, j, 2));
-    linear_backward(m, a.n2, m->dact, T, d, ff, H.linear1, H.linear1_b, m->dn);
+    linear_backward(m, a.n2, m->dact, T, d, ff, H.linear1, H.linear1_b, m->dn, nullptr, a.n2_16);
     ln_backward(m, a.res, T, d, H.norm2, H.norm2_b, 1e-5f, m->dn, m->dS, a.mean2, a.rstd2);
     const float* datt = m->dS;
     if (p > 0.0f) {
         dropout_copy(m, m->dS, m->dy, nd, p, salt(m->seed, j, 1));
         datt = m->dy;
     }
-    linear_backward(m, a.ctx, datt, T, d, d, H.out_proj, H.out_proj_b, m->dctx);
+    linear_backward(m, a.ctx, datt, T, d, d, H.out_proj, H.out_proj_b, m->dctx, nullptr, a.ctx16);
     attention_bwd(ctx, head_attention(m, a.qkv, j, p, m->seed), T, a.ctx, a.lse, m->dctx, m->dqkv);
-    linear_backward(m, a.n1, m->dqkv, T, d, 3 * d, H.in_proj, H.in_proj_b, m->dn);
+    linear_backward(m, a.n1, m->dqkv, T, d, 3 * d, H.in_proj, H.in_proj_b, m->dn, nullptr, a.n1_16);
     ln_backward(m, a.x, T, d, H.norm1, H.norm1_b, 1e-5f, m->dn, m->dS, a.mean1, a.rstd1);
 }
 
@@ -734,6 +786,7 @@ void backward_body(laya_model* m);
 // partials of every site are reduced in one launch at the end (each in its fixed order).
 void backward(laya_model* m) {
     LAYA_REQUIRE(m->has_tape, "backward: run forward first");
+    ensure_mirror(m);
     const int d = m->d();
     const size_t sites = 2 * (size_t)m->cfg.layers + 2 * (size_t)m->cfg.head_layers + 3;
     const size_t need = sites * ((2 * (size_t)ln_bwd_partial_rows(std::max(m->T, m->nmark)) * d + 63) / 64 * 64);
@@ -829,8 +882,11 @@ void adamw_step(laya_model* m, double lr_enc, double lr_head, double b1, double 
     const double c1 = 1.0 - std::pow(b1, m->steps), c2 = 1.0 - std::pow(b2, m->steps);
     size_t n = 0;
     AdamGroups g = adam_groups(m, lr_enc, lr_head, wd, c1, &n);
+    // The weights' bf16 copy is updated with them when the products read it; otherwise it goes stale.
+    __bf16* mirror = m->copies && m->WB && m->wb_fresh ? m->WB : nullptr;
     adamw_arena(m->ctx, m->P, m->G, m->M1, m->M2, n, g, (float)b1, (float)b2, (float)eps, (float)std::sqrt(c2),
-                m->coef_valid ? m->d_coef : nullptr, zero_grads ? 1 : 0);
+                m->coef_valid ? m->d_coef : nullptr, zero_grads ? 1 : 0, mirror);
+    if (!mirror) m->wb_fresh = false;
     m->coef_valid = false;
 }
 
@@ -889,7 +945,7 @@ int laya_model_destroy(laya_model* m) {
             if (p) ctx->release(p);
         for (auto& s : m->staged)
             if (s.block) ctx->release(s.block);
-        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part})
+        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part, (void*)m->WB})
             if (p) ctx->release(p);
         free_rotary(ctx, &m->rot_global);
         free_rotary(ctx, &m->rot_local);
@@ -933,6 +989,7 @@ int laya_model_set_param(laya_model* m, int i, const float* host) {
         const Param& p = m->params[i];
         LAYA_HIP(hipMemcpyAsync(m->P + p.offset, host, p.numel * sizeof(float), hipMemcpyHostToDevice, m->ctx->stream));
         LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+        m->wb_fresh = false;
     });
 }
 
@@ -971,6 +1028,7 @@ int laya_model_init_random(laya_model* m, uint64_t seed, float std) {
             init_param(m->ctx, m->P + p.offset, p.numel, p.init, std, mix64(seed, (uint64_t)i + 1));
         }
         LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
+        m->wb_fresh = false;
     });
 }
 
@@ -1014,6 +1072,34 @@ int laya_model_set_layer_checkpointing(laya_model* m, int mode) {
         if (m->act_block) m->ctx->release(m->act_block);
         m->act_block = nullptr;
         m->cap_tokens = m->cap_markers = m->cap_segs = 0;
+    });
+}
+
+int laya_model_set_bf16_copies(laya_model* m, int on) {
+    return guarded([&] {
+        checked(m);
+        if ((on != 0) == m->bf16_copies) return;
+        m->bf16_copies = on != 0;
+        // The next forward lays the activation arena out with or without the copies.
+        m->has_tape = false;
+        if (m->act_block) m->ctx->release(m->act_block);
+        m->act_block = nullptr;
+        m->cap_tokens = m->cap_markers = m->cap_segs = 0;
+        m->copies = false;
+    });
+}
+
+int laya_model_get_param_bf16(laya_model* m, int i, uint16_t* host) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(i >= 0 && i < (int)m->params.size() && host, "get_param_bf16: bad argument");
+        if (!m->WB || !m->wb_fresh)
+            throw Error(LAYA_ERR_STATE, "get_param_bf16: no current bf16 copy (it is kept while a bf16 precision "
+                                        "policy's products read it, from the first forward on)");
+        const Param& p = m->params[i];
+        LAYA_HIP(hipMemcpyAsync(host, m->WB + p.offset, p.numel * sizeof(uint16_t), hipMemcpyDeviceToHost,
+                                m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
     });
 }
 

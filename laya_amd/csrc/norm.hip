@@ -18,6 +18,7 @@ namespace laya {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
@@ -28,7 +29,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
                                                      float eps, float* __restrict__ y, float* __restrict__ mean_out,
                                                      float* __restrict__ rstd_out, const int* __restrict__ gather_ids,
                                                      int gather_rows, const float* __restrict__ add_table,
-                                                     const int* __restrict__ add_index) {
+                                                     const int* __restrict__ add_index, __bf16* __restrict__ y16) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
@@ -76,6 +77,7 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
             if (b) o += bw[c];
             if (add) o += aw[c];
             st4(y + (long)row * n + col, o);
+            if (y16) *reinterpret_cast<bf16x4*>(y16 + (long)row * n + col) = __builtin_convertvector(o, bf16x4);
         }
     }
     if (lane == 0) {
@@ -251,17 +253,18 @@ int chunks_for(int n) {
 }  // namespace
 
 void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps, float* y,
-                   float* mean, float* rstd, const int* gather_ids, const float* add_table, const int* add_index) {
+                   float* mean, float* rstd, const int* gather_ids, const float* add_table, const int* add_index,
+                   __bf16* y16) {
     if (rows <= 0) return;
     const int nch = chunks_for(n);
     // With gather_ids, x is a table of `gather_rows` rows; the caller validates ids on the host.
     const int gather_rows = gather_ids ? INT32_MAX : 0;
     dim3 grid((rows + 3) / 4), block(256);
-    ProfileScope scope(ctx, "layernorm_fwd", 0.0, (8.0 * n + 8.0) * rows + 4.0 * n * (b ? 2 : 1));
+    ProfileScope scope(ctx, "layernorm_fwd", 0.0, (8.0 * n + (y16 ? 2.0 * n : 0.0) + 8.0) * rows + 4.0 * n * (b ? 2 : 1));
 #define LN_FWD(C)                                                                                                 \
     case C:                                                                                                       \
         hipLaunchKernelGGL(ln_fwd_kernel<C>, grid, block, 0, ctx->stream, x, rows, n, w, b, eps, y, mean, rstd, \
-                           gather_ids, gather_rows, add_table, add_index);                                       \
+                           gather_ids, gather_rows, add_table, add_index, y16);                                  \
         break;
     switch (nch) { LN_FWD(1) LN_FWD(2) LN_FWD(3) LN_FWD(4) LN_FWD(5) LN_FWD(6) LN_FWD(7) LN_FWD(8) }
 #undef LN_FWD

@@ -38,6 +38,7 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ g,
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ double sq4(f32x4 v) {
     const double a = v[0], b = v[1], c = v[2], d = v[3];
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(64) void norm_finish_kernel(const double* __restric
 __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, float* __restrict__ g, float* __restrict__ m,
                                                     float* __restrict__ v, size_t n, AdamGroups groups, float b1,
                                                     float b2, float eps, float sqrt_c2, const float* coef,
-                                                    int zero_grads) {
+                                                    int zero_grads, __bf16* __restrict__ mirror) {
     const float cf = coef ? *coef : 1.0f;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
         int grp = -1;
@@ -99,6 +100,7 @@ __global__ __launch_bounds__(256) void adamw_kernel(float* __restrict__ p, float
             p[i] = w;
             m[i] = mi;
             v[i] = vi;
+            if (mirror) mirror[i] = (__bf16)w;
         }
         if (zero_grads) g[i] = 0.0f;
     }
@@ -135,7 +137,7 @@ __device__ __forceinline__ int adam_group(const AdamGroups& groups, size_t i) {
 __global__ __launch_bounds__(256) void adamw4_kernel(f32x4* __restrict__ p, f32x4* __restrict__ g,
                                                      f32x4* __restrict__ m, f32x4* __restrict__ v, size_t n4,
                                                      AdamGroups groups, float b1, float b2, float eps, float sqrt_c2,
-                                                     const float* coef, int zero_grads) {
+                                                     const float* coef, int zero_grads, bf16x4* __restrict__ mirror) {
     const float cf = coef ? *coef : 1.0f;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
         const int grp = adam_group(groups, i);
@@ -148,6 +150,8 @@ __global__ __launch_bounds__(256) void adamw4_kernel(f32x4* __restrict__ p, f32x
             __builtin_nontemporal_store(wo, p + i);
             __builtin_nontemporal_store(mo, m + i);
             __builtin_nontemporal_store(vo, v + i);
+            // The bf16 copy of the updated weights (nearest even) that the bf16 products read.
+            if (mirror) mirror[i] = __builtin_convertvector(wo, bf16x4);
         }
         if (zero_grads) __builtin_nontemporal_store(f32x4{0.0f, 0.0f, 0.0f, 0.0f}, g + i);
     }
@@ -177,13 +181,14 @@ void grad_norm(laya_ctx* ctx, const float* g, size_t n, double max_norm, double*
 }
 
 void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n, const AdamGroups& groups,
-                 float beta1, float beta2, float eps, float sqrt_c2, const float* coef, int zero_grads) {
+                 float beta1, float beta2, float eps, float sqrt_c2, const float* coef, int zero_grads,
+                 __bf16* mirror) {
     LAYA_REQUIRE(groups.n >= 0 && groups.n <= 4, "adamw: at most 4 parameter groups");
     for (int k = 0; k < groups.n; ++k)
         LAYA_REQUIRE(groups.begin[k] <= groups.end[k] && groups.end[k] <= n, "adamw: group range outside the arena");
     if (!n) return;
-    ProfileScope scope(ctx, "adamw", 0.0, (zero_grads ? 32.0 : 28.0) * n);
-    bool vec = n % 4 == 0 && vec4_ok(p) && vec4_ok(g) && vec4_ok(m) && vec4_ok(v);
+    ProfileScope scope(ctx, "adamw", 0.0, (zero_grads ? 32.0 : 28.0) * n + (mirror ? 2.0 * n : 0.0));
+    bool vec = n % 4 == 0 && vec4_ok(p) && vec4_ok(g) && vec4_ok(m) && vec4_ok(v) && ((uintptr_t)mirror & 7u) == 0;
     for (int k = 0; k < groups.n; ++k) vec = vec && groups.begin[k] % 4 == 0 && groups.end[k] % 4 == 0;
     if (vec) {
         AdamGroups g4 = groups;
@@ -193,12 +198,13 @@ void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n
         }
         hipLaunchKernelGGL(adamw4_kernel, dim3(blocks_for(n / 4, 256, 1u << 22)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<f32x4*>(p), reinterpret_cast<f32x4*>(g), reinterpret_cast<f32x4*>(m),
-                           reinterpret_cast<f32x4*>(v), n / 4, g4, beta1, beta2, eps, sqrt_c2, coef, zero_grads);
+                           reinterpret_cast<f32x4*>(v), n / 4, g4, beta1, beta2, eps, sqrt_c2, coef, zero_grads,
+                           reinterpret_cast<bf16x4*>(mirror));
         check_launch("adamw4_kernel");
         return;
     }
     hipLaunchKernelGGL(adamw_kernel, dim3(blocks_for(n, 256, 8192)), dim3(256), 0, ctx->stream, p, g, m, v, n, groups,
-                       beta1, beta2, eps, sqrt_c2, coef, zero_grads);
+                       beta1, beta2, eps, sqrt_c2, coef, zero_grads, mirror);
     check_launch("adamw_kernel");
 }
 

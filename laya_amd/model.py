@@ -261,6 +261,17 @@ class TrainableDecisionModel:
             mode = self.CHECKPOINT_RECOMPUTE if mode else self.CHECKPOINT_KEEP
         check(lib().laya_model_set_layer_checkpointing(self.handle, int(mode)))
 
+    def set_bf16_copies(self, on: bool) -> None:
+        """Keep bf16 copies of the weights (updated by AdamW) and of the saved activations for the bf16
+        products while the context's precision policy has any (the default), or drop them; same results."""
+        check(lib().laya_model_set_bf16_copies(self.handle, 1 if on else 0))
+
+    def param_bf16(self, name: str) -> np.ndarray:
+        """The bf16 copy of a parameter, as float32 values (exactly representable)."""
+        bits = np.zeros(int(np.prod(self.shapes[name])), np.uint16)
+        check(lib().laya_model_get_param_bf16(self.handle, self.index[name], bits.ctypes.data))
+        return (bits.astype(np.uint32) << 16).view(np.float32).reshape(self.shapes[name])
+
     @property
     def recomputing(self) -> bool:
         """Whether the current activation arena recomputes encoder layers in backward."""

@@ -227,3 +227,78 @@ def test_bf16_at_64_packed_zipf_sequences(ctx):
     lengths = rng.integers(16, 2049, 64)
     opts, qt = _heads(64)
     _bf16_at_full_size(synthetic_batch(rng, lengths, opts, qt, 50368, zipf=1.1), 61)
+
+
+def _copies_step(m, batch, d, seed=5):
+    m.zero_gradients()
+    logits = m.forward(batch, training=True, seed=seed)
+    m.backward(d)
+    return logits, {n: m.grad(n) for n in m.names if m.has_grad(n)}
+
+
+@pytest.mark.parametrize("policy", ["bf16-backward", "bf16"])
+def test_bf16_copies_give_bitwise_the_same_step(policy):
+    """The bf16 copies (weights, and the saved activations the products read) hold exactly the values the
+    products would round their fp32 operands to (nearest even), so a step reading them equals a step
+    rounding in-kernel bit for bit — with head dropout, and with the encoder layers recomputed."""
+    from laya_amd.device import Context
+    from laya_amd.model import TrainableDecisionModel
+    import helpers
+    print(f"bf16 copies: on vs off, policy {policy}", flush=True)
+    c = Context(0)
+    try:
+        c.set_matmul_precision(policy)
+        cfg = helpers.mid_config(layers=4)
+        m = TrainableDecisionModel(cfg, c)
+        m.set_params(helpers.random_params(m.shapes, 71, std=0.03))
+        m.head_dropout = 0.1
+        batch = helpers.mixed_batch(np.random.default_rng(72), [300, 129, 64, 17, 211, 1200], cfg.encoder.vocab_size)
+        d = np.random.default_rng(73).standard_normal(batch.n_markers).astype(np.float32)
+        m.set_bf16_copies(False)
+        l0, g0 = _copies_step(m, batch, d)
+        with pytest.raises(Exception):
+            m.param_bf16("encoder.layers.1.attn.Wqkv.weight")  # no copy is kept with the option off
+        m.set_bf16_copies(True)
+        l1, g1 = _copies_step(m, batch, d)
+        np.testing.assert_array_equal(l0, l1)
+        for n in g0:
+            np.testing.assert_array_equal(g0[n], g1[n], err_msg=n)
+        m.layer_checkpointing = m.CHECKPOINT_RECOMPUTE
+        l2, g2 = _copies_step(m, batch, d)
+        assert m.recomputing
+        np.testing.assert_array_equal(l0, l2)
+        for n in g0:
+            np.testing.assert_array_equal(g0[n], g2[n], err_msg=n)
+        m.close()
+    finally:
+        c.close()
+
+
+def test_adamw_keeps_the_bf16_weight_copy_current():
+    """Through optimizer steps the weights' bf16 copy is bf16(master) to the bit: refreshed from the masters
+    after host writes, and written by the AdamW kernel with each update."""
+    from laya_amd.device import Context
+    from laya_amd.model import TrainableDecisionModel
+    import helpers
+    print("bf16 copies: the weight copy through AdamW steps", flush=True)
+    c = Context(0)
+    try:
+        c.set_matmul_precision("bf16-backward")
+        cfg = helpers.mid_config(layers=2)
+        m = TrainableDecisionModel(cfg, c)
+        m.set_params(helpers.random_params(m.shapes, 81, std=0.03))
+        rng = np.random.default_rng(82)
+        batch = helpers.mixed_batch(rng, [200, 90, 33], cfg.encoder.vocab_size)
+        targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+        m.set_trainable_encoder_layers(1)  # frozen layers keep their copy as refreshed
+        for step in range(3):
+            m.train_step(batch, targets, seed=step, ce_weight=1.0, loss_scale=1.0, max_norm=1.0, lr_encoder=1e-3,
+                         lr_head=1e-3, weight_decay=0.01)
+            if step == 1:
+                m.set_param("scorer.0.weight", np.full(m.shapes["scorer.0.weight"], 1.0 + 2 ** -9, np.float32))
+        m.forward(batch)  # refreshes the copy after the host write
+        for n in m.names:
+            np.testing.assert_array_equal(m.param_bf16(n), bf16(m.param(n)), err_msg=n)
+        m.close()
+    finally:
+        c.close()
