@@ -157,7 +157,9 @@ def cpu_baseline(mc, batch, targets, items: int, summed: bool, extrapolate: bool
         if not extrapolate:
             return _oracle_step(mc, sub, t_sub, summed), "one full fp32 step"
         t3 = _oracle_step(modernbert_base(3), sub, t_sub, summed)
+        print(f"cpu baseline: 3-layer step {t3:.1f} s", file=sys.stderr, flush=True)
         t6 = _oracle_step(modernbert_base(6), sub, t_sub, summed)
+        print(f"cpu baseline: 6-layer step {t6:.1f} s", file=sys.stderr, flush=True)
         return (t3 + (t6 - t3) * (layers - 3) / 3.0,
                 f"one fp32 step extrapolated linearly in layers to {layers} from 3- and 6-layer encoders "
                 f"({t3:.1f} s and {t6:.1f} s)")
