@@ -76,6 +76,22 @@ __device__ __forceinline__ bool subtile_inside(int q0, int k0, int L, int hw) {
     return q0 + 32 <= L && k0 >= 0 && k0 + 32 <= L && (hw < 0 || (k0 + 31 - q0 <= hw && q0 + 31 - k0 <= hw));
 }
 
+// The partners (keys of a query, or queries of a key) that row t may pair with under in_window, as
+// one unsigned range test: partner i qualifies iff (unsigned)(i − lo) ≤ span. A row past the segment
+// end gets a range nothing falls in. Lets a partial subtile mask its 16 elements with an add, a compare
+// and a select each, instead of a branch per element.
+struct WindowRange {
+    int lo;
+    unsigned span;
+};
+__device__ __forceinline__ WindowRange window_range(int t, int L, int hw) {
+    if (t >= L) return {1 << 30, 0u};
+    const int lo = hw < 0 ? 0 : max(0, t - hw);
+    const int hi = hw < 0 ? L - 1 : min(L - 1, t + hw);
+    return {lo, (unsigned)(hi - lo)};
+}
+__device__ __forceinline__ bool in_range(const WindowRange& w, int rel) { return (unsigned)rel <= w.span; }
+
 // 2^x on the hardware exponential (v_exp_f32): arguments here are finite or −inf (→ 0), and results
 // below the normal range only arise for probabilities far under the fp32 parity tolerance.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -405,7 +421,7 @@ __device__ __forceinline__ void swz_col_frag(const __bf16* planes, int r0, int d
     for (int pl = 0; pl < 3; ++pl) f[pl] = cat8(ds_read_tr(planes + pl * R * 64 + o0), ds_read_tr(planes + pl * R * 64 + o1));
 }
 
-template <int D>
+template <int D, bool DROP>
 __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
     __shared__ __attribute__((aligned(16))) __bf16 Ks[3 * TILE * 64];  // K tile, swizzled [key][d]
@@ -435,6 +451,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
         wend = min(L, q0w + WAVE_ROWS + hw);
     }
 
+    const WindowRange win = window_range(q, L, hw);
     f32x16 o[2];
     o[0] = f32x16{};
     o[1] = f32x16{};
@@ -476,10 +493,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
                     mx = fmaxf(mx, t[r]);
                 }
             } else {
+                const int rel0 = kbs + 4 * h - win.lo;  // key − lo of the lane's row r = 0
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
-                    t[r] = in_window(q, key, L, hw) ? s[r] * p.scale_log2 : NEG_INF;
+                    t[r] = in_range(win, rel0 + 8 * (r >> 2) + (r & 3)) ? s[r] * p.scale_log2 : NEG_INF;
                     mx = fmaxf(mx, t[r]);
                 }
             }
@@ -497,7 +514,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
             m = mnew;
             o[0] *= alpha;
             o[1] *= alpha;
-            if (p.p_drop > 0.0f) {
+            if (DROP) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int key = kbs + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -790,7 +807,7 @@ constexpr int BT = 32;
 // Each wave owns 32 keys: K split once into registers, V split once into the block's LDS planes. The
 // query tiles are committed to one swizzled layout each (Q and dO), the next tile's rows load while the
 // current one is multiplied, and the products over queries read Qᵀ and dOᵀ with the transposing reads.
-template <int D>
+template <int D, bool DROP>
 __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
     __shared__ __attribute__((aligned(16))) __bf16 Qs[3 * BT * 64];
@@ -828,6 +845,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
         wend = min(L, k0w + WAVE_ROWS + hw);
     }
 
+    const WindowRange win = window_range(key, L, hw);
     f32x16 dk[2], dv[2];
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
@@ -873,24 +891,36 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
             dp = mma6(f, vh, dp);
         }
         float pm[16], ds[16];
-        if (p.p_drop == 0.0f && subtile_inside(qt0, k0w, L, hw)) {
+        const int rel0 = qt0 + 4 * h - win.lo;  // query − lo of the lane's row r = 0
+        if (!DROP) {
+            if (subtile_inside(qt0, k0w, L, hw)) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
-                const float pr = fast_exp2(s[r] * p.scale_log2 - lse_s[ql]);
-                pm[r] = pr;
-                ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
+                for (int r = 0; r < 16; ++r) {
+                    const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
+                    const float pr = fast_exp2(s[r] * p.scale_log2 - lse_s[ql]);
+                    pm[r] = pr;
+                    ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
+                    const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
+                    const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse_s[ql]) : 0.0f;
+                    pm[r] = pr;
+                    ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
+                }
             }
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
                 const int qq = qt0 + ql;
-                const bool ok = in_window(qq, key, L, hw) && kvalid;
+                const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
                 const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse_s[ql]) : 0.0f;
-                float mask = 1.0f;
-                if (p.p_drop > 0.0f && ok)
-                    mask = uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
+                const float drop =
+                    uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
+                const float mask = ok ? drop : 1.0f;
                 pm[r] = pr * mask;
                 ds[r] = pr * (dp[r] * mask - dot_s[ql]) * p.scale;
             }
@@ -924,7 +954,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     }
 }
 
-template <int D>
+template <int D, bool DROP>
 __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
     __shared__ __attribute__((aligned(16))) __bf16 Ks[3 * BT * 64];  // K tile, swizzled [key][d]
@@ -972,6 +1002,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
         wend = min(L, q0w + WAVE_ROWS + hw);
     }
 
+    const WindowRange win = window_range(q, L, hw);
     f32x16 dq[2];
     dq[0] = f32x16{};
     dq[1] = f32x16{};
@@ -1003,18 +1034,28 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
             dp = mma6(f, oh[ks], dp);
         }
         float ds[16];
-        if (p.p_drop == 0.0f && subtile_inside(q0w, kt0, L, hw)) {
+        const int rel0 = kt0 + 4 * h - win.lo;  // key − lo of the lane's row r = 0
+        if (!DROP) {
+            if (subtile_inside(q0w, kt0, L, hw)) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * p.scale_log2 - lse) * (dp[r] - dot) * p.scale;
+                for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * p.scale_log2 - lse) * (dp[r] - dot) * p.scale;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
+                    const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse) : 0.0f;
+                    ds[r] = pr * (dp[r] - dot) * p.scale;
+                }
+            }
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = kt0 + 8 * (r >> 2) + 4 * h + (r & 3);
-                const bool ok = in_window(q, key, L, hw);
+                const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
                 const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse) : 0.0f;
-                float mask = 1.0f;
-                if (p.p_drop > 0.0f && ok)
-                    mask = uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
+                const float drop =
+                    uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
+                const float mask = ok ? drop : 1.0f;
                 ds[r] = pr * (dp[r] * mask - dot) * p.scale;
             }
         }
@@ -1129,8 +1170,10 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
     p.context16 = split ? context16 : nullptr;
     {
         ProfileScope scope(ctx, split ? "attention_fwd_x6" : "attention_fwd", 4.0 * a.hidden * a.keys, 0.0);
-        if (split)
-            hipLaunchKernelGGL(attn_fwd_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        if (split && p.p_drop > 0.0f)
+            hipLaunchKernelGGL((attn_fwd_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
+        else if (split)
+            hipLaunchKernelGGL((attn_fwd_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
         else if (a.head_dim == 64)
             hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         else
@@ -1167,11 +1210,17 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
         {
             // dQ first: it forms each row's Σ dO·O and writes it for dK/dV.
             ProfileScope scope(ctx, "attention_bwd_dq_x6", 2.0 * fb, 0.0);
-            hipLaunchKernelGGL(attn_bwd_dq_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+            if (p.p_drop > 0.0f)
+                hipLaunchKernelGGL((attn_bwd_dq_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
+            else
+                hipLaunchKernelGGL((attn_bwd_dq_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
             check_launch("attn_bwd_dq_x6_kernel");
         }
         ProfileScope scope(ctx, "attention_bwd_dkv_x6", 2.0 * fb, 0.0);
-        hipLaunchKernelGGL(attn_bwd_dkv_x6_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+        if (p.p_drop > 0.0f)
+            hipLaunchKernelGGL((attn_bwd_dkv_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
+        else
+            hipLaunchKernelGGL((attn_bwd_dkv_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
         check_launch("attn_bwd_dkv_x6_kernel");
         return;
     }
