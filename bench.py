@@ -50,10 +50,10 @@ PEAK_BF16_MFMA = 2.5e15
 def mfma_peaks(name: str):
     """(peak in algorithmic fp32 flops/s, bf16-MFMA issues per algorithmic flop) of a matrix-core kernel.
 
-    Kernels named *_x6 / *_x6w compute fp32 products from exact three-piece bf16 splits: six bf16 MFMA
-    products per fp32 one, so their fp32-equivalent peak is the bf16 peak over six. *_bf16 / *_bf16w run
-    bf16 operands (one product each). The rest run the fp32 matrix cores."""
-    base = name[:-1] if name.endswith(("_x6w", "_bf16w")) else name
+    Kernels named *_x6 / *_x6w / *_x6t compute fp32 products from exact three-piece bf16 splits: six bf16
+    MFMA products per fp32 one, so their fp32-equivalent peak is the bf16 peak over six. *_bf16 / *_bf16w
+    run bf16 operands (one product each). The rest run the fp32 matrix cores."""
+    base = name[:-1] if name.endswith(("_x6w", "_x6t", "_bf16w")) else name
     if base.endswith("_x6"):
         return PEAK_BF16_MFMA / 6, 6.0
     if base.endswith("_bf16"):

@@ -13,7 +13,8 @@ from typing import Optional
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liblaya_hip.so")
+# The in-tree build; LAYA_HIP_LIBRARY names another build of the same library (e.g. to compare two).
+LIB_PATH = os.environ.get("LAYA_HIP_LIBRARY") or os.path.join(HERE, "liblaya_hip.so")
 
 OK, ERR_ARGUMENT, ERR_OUT_OF_RANGE, ERR_MEMORY, ERR_HIP, ERR_NOT_FINITE, ERR_STATE, ERR_MISSING = range(8)
 

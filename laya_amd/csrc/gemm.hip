@@ -173,9 +173,10 @@ __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, f32x
 // stores, so a load issued after stores waits for all of them, and interleaving load-add-store per
 // element would serialise the epilogue. Each element is read and written by its own lane only, so
 // this order is also right when R is C.
-template <bool AK, bool BKC, int MODE, bool RES, bool GUARD, bool VEC2>
-__device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[2][2], int wm,
+template <bool AK, bool BKC, int MODE, bool RES, bool GUARD, bool VEC2, int NI>
+__device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[NI][2], int wm,
                                           int wn, int lr, int kh) {
+    static_assert(AK || NI == 2, "three row groups are a k-contiguous layout");
     auto rowoff = [&](int i, int r) {
         const int q = 8 * (r >> 2) + kh + (r & 3);
         return AK ? wm * 64 + 32 * i + q : wm * 64 + 2 * q + i;
@@ -200,7 +201,7 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
         static_assert(AK && BKC, "STORE_ROPE is an NT epilogue");
         const bool rot = c.n0 + wn * 64 < p.rope_cols;  // wave-uniform
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NI; ++i) {
             float cs[16], sn[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -233,7 +234,7 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
         const int col = coloff(0);
         auto inside = [&](int i, int r) { return !GUARD || (c.m0 + rowoff(i, r) < p.M && c.n0 + col < p.N); };
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {  // two halves bound the registers the reads hold
+        for (int i = 0; i < NI; ++i) {  // two halves bound the registers the reads hold
             f32x2 add[16];
             if (READS) {
 #pragma unroll
@@ -255,7 +256,7 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
         return !GUARD || (c.m0 + rowoff(i, r) < p.M && c.n0 + coloff(j) < p.N);
     };
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NI; ++i) {
         float add[2][16];
         if (READS) {
 #pragma unroll
@@ -1015,6 +1016,128 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
         else
             store_acc<true, true, MODE, false, true, true>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2);
     }
+}
+
+// ------------------------------------------------------------- split products on 192 x 256 tiles
+//
+// The wide kernel's loop on 192-row tiles, for outputs 256-wide products leave under-filled: an output
+// 768 columns wide and ≈ 14 k rows is 165 tiles of 256 x 256 (65 % of 256 CUs) but 219 of 192 x 256
+// (one round at 86 %), the same work per CU as three 128 x 128 tiles with the wide tile's operand reuse.
+// Eight waves (2 x 4), each owning 96 x 64 (three 32-row groups by two 32-column groups). NT, whole K,
+// K a multiple of 16; STORE with optional residual.
+constexpr int TM = 192, STAGE_T = TM * KPADQ;
+constexpr double TALL_GAIN = 1.25;  // 192 x 256 over three 128 x 128 per CU, per unit of work
+
+// The 192-row k-contiguous operand's 16-deep stage: thread t holds 4 consecutive k of row t/4 and, for
+// t < 256 (waves 0-3, wave-uniform), of row 128 + t/4.
+struct OperandT {
+    __amdgpu_buffer_rsrc_t rsrc;
+    unsigned off[2];
+    f32x4 reg[2];
+    bool two;
+    __device__ __forceinline__ OperandT(const float* s, long ldl, int mn0, int MN, int tid, unsigned bytes)
+        : rsrc(buffer_of(s, bytes)), two(tid < 256) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            off[i] = ((unsigned)min(mn0 + (tid >> 2) + 128 * i, MN - 1) * (unsigned)ldl + ((tid & 3) << 2)) * 4u;
+    }
+    __device__ __forceinline__ void full(int k0) {
+        reg[0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[0], k0 * 4, 0));
+        if (two) reg[1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[1], k0 * 4, 0));
+    }
+    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (i == 1 && !two) break;
+            const int o = ((tid >> 2) + 128 * i) * KPADQ + ((tid & 3) << 2);
+            bf16x4 h1, h2, h3;
+            split3_4(reg[i], h1, h2, h3);
+            *reinterpret_cast<bf16x4*>(lds + o) = h1;
+            *reinterpret_cast<bf16x4*>(lds + STAGE_T + o) = h2;
+            *reinterpret_cast<bf16x4*>(lds + 2 * STAGE_T + o) = h3;
+        }
+    }
+};
+
+// One 16-deep stage of a wave's 96 x 64: B fragments once, A fragments one 32-row group ahead.
+__device__ __forceinline__ void mma_stage_t(const __bf16* A, const __bf16* B, f32x16 (&acc)[3][2], int wm, int wn,
+                                            int lr, int half) {
+    bf16x8 b[2][3], a[2][3];
+    auto rd_a = [&](int g, bf16x8 (&dst)[3]) {
+        const int row = 96 * wm + 32 * g + lr;
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+            dst[pl] = *reinterpret_cast<const bf16x8*>(A + pl * STAGE_T + row * KPADQ + 8 * half);
+    };
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int pl = 0; pl < 3; ++pl)
+            b[j][pl] = *reinterpret_cast<const bf16x8*>(B + pl * STAGE_W + (wn * 64 + 32 * j + lr) * KPADQ + 8 * half);
+    rd_a(0, a[0]);
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+        if (g + 1 < 3) rd_a(g + 1, a[(g + 1) & 1]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) mma6(a[g & 1], b[j], acc[g][j]);
+    }
+}
+
+template <bool RES>
+__global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * (STAGE_T + STAGE_W)];  // [stage][A planes, B planes]
+    const int t = xcd_logical_block();
+    const int tm = t / p.tiles_n;
+    TileCoord c;
+    c.split = 0;
+    c.t = t;
+    c.m0 = tm * TM;
+    c.n0 = (t - tm * p.tiles_n) * WT;
+    c.kb = 0;
+    c.ke = p.K;
+    const int nt = p.K / BKQ;
+    const int rot = t % nt;
+    const int tid = opaque_tid(), lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3;
+    const int lr = lane & 31, half = lane >> 5;
+    OperandT a(p.A, p.lda, c.m0, p.M, tid, (unsigned)(p.M * p.lda * 4));
+    OperandW b(p.B, p.ldb, c.n0, p.N, tid, (unsigned)(p.N * p.ldb * 4));
+    auto kof = [&](int j) {
+        const int q = j + rot;
+        return (q >= nt ? q - nt : q) * BKQ;
+    };
+    f32x16 acc[3][2];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    a.full(kof(0));
+    b.full(kof(0));
+    a.store(smem[0], tid);
+    b.store<3>(smem[0] + 3 * STAGE_T, tid);
+    a.full(kof(min(1, nt - 1)));
+    b.full(kof(min(1, nt - 1)));
+    lds_barrier();
+    // Branch-free body: the last two iterations reload the last stage and fill a stage no one reads.
+    for (int j = 0; j < nt; ++j) {
+        const int cur = j & 1;
+        const int kn = kof(min(j + 2, nt - 1));
+        mma_stage_t(smem[cur], smem[cur] + 3 * STAGE_T, acc, wm, wn, lr, half);
+        a.store(smem[cur ^ 1], tid);
+        b.store<3>(smem[cur ^ 1] + 3 * STAGE_T, tid);
+        a.full(kn);
+        b.full(kn);
+        lds_barrier();
+    }
+    const int te = opaque_tid(), le = te & 63, we = te >> 6, wme = we >> 2;
+    // store_acc places row group i of wave row wm at 64·wm + 32·i: a base 32·wm further down puts the
+    // wave's three groups at 96·wm + 32·i.
+    TileCoord cs = c;
+    cs.m0 = c.m0 + 32 * wme;
+    if (c.m0 + TM <= p.M && c.n0 + WT <= p.N)
+        store_acc<true, true, STORE, RES, false, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
+    else
+        store_acc<true, true, STORE, RES, true, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
 }
 
 // The fp32 product from bf16 pieces; accumulators in the k-contiguous layout whatever the operands' form.
@@ -1808,6 +1931,33 @@ bool wide_tiles_pay(const laya_ctx* ctx, const GemmParams& p, bool three) {
     return t_wide < (three ? std::min(t_two, t_three) : t_two);
 }
 
+// 192 x 256 tiles when their rounds take less time than the 128 x 128 grid's at three per CU (the same
+// work per CU per round, done faster by the larger tile: the factor is measured on 13871 x 768 x 768).
+// A whole-K NT STORE (residual allowed), K a multiple of 16.
+bool tall_tiles_pay(const laya_ctx* ctx, const GemmParams& p) {
+    if (p.mode != STORE || p.K <= 0 || p.K % BKQ != 0 || p.splits != 1) return false;
+    if ((long)p.M * p.lda * 4 >= (1L << 31) || (long)p.N * p.ldb * 4 >= (1L << 31)) return false;  // buffer offsets
+    const long cu = ctx->cu_count;
+    const long tall = (long)((p.M + TM - 1) / TM) * ((p.N + WT - 1) / WT);
+    const long tiles = (long)p.tiles_m * p.tiles_n;
+    const double t_tall = (double)((tall + cu - 1) / cu) * 3.0 / TALL_GAIN;
+    const double t_two = (double)((tiles + 2 * cu - 1) / (2 * cu)) * 2.0;
+    const double t_three = (double)((tiles + 3 * cu - 1) / (3 * cu)) * 3.0 / 1.08;
+    return t_tall < std::min(t_two, t_three);
+}
+
+void launch_tall(laya_ctx* ctx, GemmParams p) {
+    profile_rename("gemm_nt_x6t");
+    p.tiles_m = (p.M + TM - 1) / TM;
+    p.tiles_n = (p.N + WT - 1) / WT;
+    const dim3 g(p.tiles_m * p.tiles_n), b(WT_THREADS);
+    if (p.R)
+        hipLaunchKernelGGL(gemm_x6t_kernel<true>, g, b, 0, ctx->stream, p);
+    else
+        hipLaunchKernelGGL(gemm_x6t_kernel<false>, g, b, 0, ctx->stream, p);
+    check_launch("gemm_x6t_kernel");
+}
+
 void launch_wide(laya_ctx* ctx, GemmParams p) {
     profile_rename("gemm_nt_x6w");
     p.tiles_n = (p.N + WT - 1) / WT;
@@ -1867,6 +2017,8 @@ template <bool AK, bool BKC> void launch_x6(laya_ctx* ctx, const GemmParams& p, 
     if constexpr (AK && BKC) {
         if (va && vb && wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks))) {
             launch_wide(ctx, p);
+        } else if (va && vb && tall_tiles_pay(ctx, p)) {
+            launch_tall(ctx, p);
         } else if (va && vb && p.mode == STORE && three_per_cu(ctx, blocks)) {
             const dim3 g(blocks), b(THREADS);
             if (p.R)
