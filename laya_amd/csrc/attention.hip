@@ -33,6 +33,7 @@ constexpr int WAVE_ROWS = 32;   // queries (or keys) owned by one wave
 constexpr int BLOCK_ROWS = 128; // 4 waves
 constexpr int TILE = 64;        // rows of the streamed operand per LDS tile
 constexpr float NEG_INF = -__builtin_huge_valf();
+constexpr float LAZY_RESCALE = 8.0f;  // log2 headroom of the split-product forward's running max
 
 struct Params {
     const float* qkv;
@@ -501,19 +502,25 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
                 }
             }
             mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(m, mx);
-            const float alpha = fast_exp2(m - mnew);
+            // The running max moves only when a score passes it by more than 2^LAZY_RESCALE (the
+            // probabilities then stay below 2^LAZY_RESCALE): most subtiles rescale nothing.
+            const bool grow = mx > m + LAZY_RESCALE;
+            if (__any(grow)) {  // wave-uniform
+                const float mnew = grow ? mx : m;
+                const float alpha = fast_exp2(m - mnew);  // exactly 1 where the max stays
+                l *= alpha;
+                o[0] *= alpha;
+                o[1] *= alpha;
+                m = mnew;
+            }
             float pr[16];
             float sum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                pr[r] = fast_exp2(t[r] - mnew);
+                pr[r] = fast_exp2(t[r] - m);
                 sum += pr[r];
             }
-            l = l * alpha + sum;
-            m = mnew;
-            o[0] *= alpha;
-            o[1] *= alpha;
+            l += sum;
             if (DROP) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
