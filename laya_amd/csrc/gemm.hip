@@ -1024,7 +1024,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
 // 768 columns wide and ≈ 14 k rows is 165 tiles of 256 x 256 (65 % of 256 CUs) but 219 of 192 x 256
 // (one round at 86 %), the same work per CU as three 128 x 128 tiles with the wide tile's operand reuse.
 // Eight waves (2 x 4), each owning 96 x 64 (three 32-row groups by two 32-column groups). NT, whole K,
-// K a multiple of 16; STORE with optional residual.
+// K a multiple of 16; STORE with optional residual, or STORE_ROPE.
 constexpr int TM = 192, STAGE_T = TM * KPADQ;
 constexpr double TALL_GAIN = 1.25;  // 192 x 256 over three 128 x 128 per CU, per unit of work
 
@@ -1083,8 +1083,9 @@ __device__ __forceinline__ void mma_stage_t(const __bf16* A, const __bf16* B, f3
     }
 }
 
-template <bool RES>
+template <int MODE, bool RES>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
+    static_assert(MODE == STORE || (MODE == STORE_ROPE && !RES), "whole-K NT epilogues");
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * (STAGE_T + STAGE_W)];  // [stage][A planes, B planes]
     const int t = xcd_logical_block();
     const int tm = t / p.tiles_n;
@@ -1135,9 +1136,9 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     TileCoord cs = c;
     cs.m0 = c.m0 + 32 * wme;
     if (c.m0 + TM <= p.M && c.n0 + WT <= p.N)
-        store_acc<true, true, STORE, RES, false, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
+        store_acc<true, true, MODE, RES, false, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
     else
-        store_acc<true, true, STORE, RES, true, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
+        store_acc<true, true, MODE, RES, true, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
 }
 
 // The fp32 product from bf16 pieces; accumulators in the k-contiguous layout whatever the operands' form.
@@ -1931,18 +1932,19 @@ bool wide_tiles_pay(const laya_ctx* ctx, const GemmParams& p, bool three) {
     return t_wide < (three ? std::min(t_two, t_three) : t_two);
 }
 
-// 192 x 256 tiles when their rounds take less time than the 128 x 128 grid's at three per CU (the same
-// work per CU per round, done faster by the larger tile: the factor is measured on 13871 x 768 x 768).
-// A whole-K NT STORE (residual allowed), K a multiple of 16.
+// 192 x 256 tiles when their rounds take less time than the 128 x 128 grid's at two or (STORE only)
+// three per CU (the same work per CU per round, done faster by the larger tile: the factor is measured
+// on 13871 x 768 x 768). A whole-K NT STORE (residual allowed) or STORE_ROPE, K a multiple of 16.
 bool tall_tiles_pay(const laya_ctx* ctx, const GemmParams& p) {
-    if (p.mode != STORE || p.K <= 0 || p.K % BKQ != 0 || p.splits != 1) return false;
+    if ((p.mode != STORE && p.mode != STORE_ROPE) || p.K <= 0 || p.K % BKQ != 0 || p.splits != 1) return false;
+    if (p.mode == STORE_ROPE && p.R) return false;
     if ((long)p.M * p.lda * 4 >= (1L << 31) || (long)p.N * p.ldb * 4 >= (1L << 31)) return false;  // buffer offsets
     const long cu = ctx->cu_count;
     const long tall = (long)((p.M + TM - 1) / TM) * ((p.N + WT - 1) / WT);
     const long tiles = (long)p.tiles_m * p.tiles_n;
     const double t_tall = (double)((tall + cu - 1) / cu) * 3.0 / TALL_GAIN;
     const double t_two = (double)((tiles + 2 * cu - 1) / (2 * cu)) * 2.0;
-    const double t_three = (double)((tiles + 3 * cu - 1) / (3 * cu)) * 3.0 / 1.08;
+    const double t_three = p.mode == STORE ? (double)((tiles + 3 * cu - 1) / (3 * cu)) * 3.0 / 1.08 : 1e30;
     return t_tall < std::min(t_two, t_three);
 }
 
@@ -1951,10 +1953,12 @@ void launch_tall(laya_ctx* ctx, GemmParams p) {
     p.tiles_m = (p.M + TM - 1) / TM;
     p.tiles_n = (p.N + WT - 1) / WT;
     const dim3 g(p.tiles_m * p.tiles_n), b(WT_THREADS);
-    if (p.R)
-        hipLaunchKernelGGL(gemm_x6t_kernel<true>, g, b, 0, ctx->stream, p);
+    if (p.mode == STORE_ROPE)
+        hipLaunchKernelGGL((gemm_x6t_kernel<STORE_ROPE, false>), g, b, 0, ctx->stream, p);
+    else if (p.R)
+        hipLaunchKernelGGL((gemm_x6t_kernel<STORE, true>), g, b, 0, ctx->stream, p);
     else
-        hipLaunchKernelGGL(gemm_x6t_kernel<false>, g, b, 0, ctx->stream, p);
+        hipLaunchKernelGGL((gemm_x6t_kernel<STORE, false>), g, b, 0, ctx->stream, p);
     check_launch("gemm_x6t_kernel");
 }
 
@@ -2223,6 +2227,10 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
         ProfileScope scope(ctx, "gemm_nt_x6", 2.0 * M * N * (double)K, 0.0);
         if (wide_tiles_pay(ctx, p, false)) {
             launch_wide(ctx, p);
+            return;
+        }
+        if (tall_tiles_pay(ctx, p)) {
+            launch_tall(ctx, p);
             return;
         }
         hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),

@@ -86,9 +86,11 @@ def test_headline_batch_32x512_every_gradient_matches_fp64(ctx):
     assert np.abs(logits - fx["logits"]).max() < 1e-4
     # The wide kernels this workload's timing rests on are the ones under test.
     assert prof.get("gemm_bwd_pair_x6w", {}).get("launches", 0) >= 90, sorted(prof)
-    # At 14,344 rows the 2304-wide products would need a third round of 256 × 256 tiles and stay on
-    # 128 × 128 tiles; the head's 3072-wide products take the wide forward kernel.
+    # At 14,344 rows the 2304-wide products would need a third round of 256 × 256 tiles, so they and the
+    # 768-wide ones (RoPE and residual epilogues included) run on 192 × 256 tiles; the head's 3072-wide
+    # products take the wide forward kernel.
     assert prof.get("gemm_nt_x6w", {}).get("launches", 0) >= 2, sorted(prof)
+    assert prof.get("gemm_nt_x6t", {}).get("launches", 0) >= 88, sorted(prof)
     _check_gradients(m, fx)
     m.close()
 
@@ -98,6 +100,9 @@ def test_long_context_batch_2x8192_every_gradient_matches_fp64(ctx):
     m, fx, batch, logits, prof = _step(ctx, "b2x8192")
     assert np.abs(logits - fx["logits"]).max() < 1e-4
     assert prof.get("attention_bwd_dkv_x6", {}).get("launches", 0) == 24, sorted(prof)
+    # 16,384 rows: the RoPE-fused QKV products run on 192 × 256 tiles (three rounds of 256 × 256 tiles
+    # or five of 128 × 128 would take longer).
+    assert prof.get("gemm_nt_x6t", {}).get("launches", 0) >= 22, sorted(prof)
     _check_gradients(m, fx)
     m.close()
 
