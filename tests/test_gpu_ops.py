@@ -47,9 +47,11 @@ def param(ctx, name, a, trainable=True):
                                           # the backward pair on 256 x 256 tiles at the model's shapes,
                                           # and with rows of x and dX that are not float4-aligned
                                           (13871, 768, 2304), (13871, 1152, 768), (11000, 1150, 768),
-                                          # the forward on 192 x 256 tiles with a ragged last row and
-                                          # column tile (the model's 768-wide outputs use full ones)
-                                          (12345, 768, 700)])
+                                          # the forward on 192 x 256 tiles (with the residual, the
+                                          # 2304-wide cases above run two and three rounds of them): a
+                                          # ragged last row and column tile, and whole tiles with a
+                                          # 4-stage K loop
+                                          (12345, 768, 700), (13824, 64, 768)])
 def test_linear_forward_and_backward(ctx, rows, inn, out, policy):
     """Both fp32 implementations (exact bf16 splits, the default; the fp32 matrix cores) at the fp64
     oracle's result to 1e-6, widened as √K for reductions longer than 2048 terms (fp32 rounding of a
