@@ -48,14 +48,18 @@ PEAK_BF16_MFMA = 2.5e15
 
 
 def mfma_peaks(name: str):
-    """(peak in algorithmic fp32 flops/s, bf16-MFMA issues per algorithmic flop) of a matrix-core kernel.
+    """(peak in algorithmic fp32 flops/s, 16-bit MFMA issues per algorithmic flop) of a matrix-core kernel.
 
     Kernels named *_x6 / *_x6w / *_x6t compute fp32 products from exact three-piece bf16 splits: six bf16
-    MFMA products per fp32 one, so their fp32-equivalent peak is the bf16 peak over six. *_bf16 / *_bf16w
-    run bf16 operands (one product each). The rest run the fp32 matrix cores."""
-    base = name[:-1] if name.endswith(("_x6w", "_x6t", "_bf16w")) else name
+    MFMA products per fp32 one, so their fp32-equivalent peak is the bf16 peak over six. *_h2w / *_h2t
+    compute them from two-piece fp16 splits of power-of-two-scaled operands: three fp16 MFMA products per
+    fp32 one (fp16 and bf16 share the 2.5 PFLOP/s dense peak), peak over three. *_bf16 / *_bf16w run bf16
+    operands (one product each). The rest run the fp32 matrix cores."""
+    base = name[:-1] if name.endswith(("_x6w", "_x6t", "_bf16w", "_h2w", "_h2t")) else name
     if base.endswith("_x6"):
         return PEAK_BF16_MFMA / 6, 6.0
+    if base.endswith("_h2"):
+        return PEAK_BF16_MFMA / 3, 3.0
     if base.endswith("_bf16"):
         return PEAK_BF16_MFMA, 1.0
     return PEAK_FP32_MFMA, 0.0
@@ -194,6 +198,9 @@ def main():
                     help="also time the CPU baseline's sample on one thread (always done for the headline)")
     ap.add_argument("--fp32-mfma", action="store_true",
                     help="fp32 products on the fp32 matrix cores instead of exact bf16 splits (for comparison)")
+    ap.add_argument("--split3", action="store_true",
+                    help="fp32 products from three-piece bf16 splits in every kernel instead of two-piece fp16 "
+                         "products in the 256-wide ones (for comparison)")
     ap.add_argument("--no-profile", action="store_true", help="time without per-launch events")
     ap.add_argument("--no-bf16-copies", action="store_true",
                     help="bf16 workloads: round the fp32 weights and activations inside the products instead of "
@@ -219,7 +226,11 @@ def main():
     mc = modernbert_base()
     batches = [make_batch(rng, w) for _ in range(args.warmup + args.steps)]
     ctx = Context(0)
-    matmul = "fp32-mfma" if args.fp32_mfma and w["matmul"] == "fp32" else w["matmul"]
+    matmul = w["matmul"]
+    if matmul == "fp32" and args.fp32_mfma:
+        matmul = "fp32-mfma"
+    elif matmul == "fp32" and args.split3:
+        matmul = "fp32-split3"
     ctx.set_matmul_precision(matmul)
     cpu_items = args.cpu_items or (16 if w["seq"] <= 512 else 1)
     long_workload = w["seq"] > 512
@@ -347,8 +358,12 @@ def main():
             "config": {"workload": f"ModernBERT-base Laya encoder + decision head fine-tune step, {w['desc']}, "
                                    "AdamW lr 3e-5 wd 0.01, clip 1.0",
                        "global_batch": w["batch"], "seq_len": w["seq"], "parallelism": "none (1 GPU)",
-                       "matmul_precision": {"fp32": "fp32 products from exact three-piece bf16 splits (six bf16 "
-                                                     "MFMA products each, fp32 accumulation)",
+                       "matmul_precision": {"fp32": "fp32-accurate products: two-piece fp16 splits of power-of-two-"
+                                                     "scaled operands on 256-wide tiles (three fp16 MFMA products "
+                                                     "each), exact three-piece bf16 splits elsewhere (six bf16 "
+                                                     "MFMA products each); fp32 accumulation",
+                                            "fp32-split3": "fp32 products from exact three-piece bf16 splits (six "
+                                                           "bf16 MFMA products each, fp32 accumulation)",
                                             "fp32-mfma": "fp32 products on the fp32 MFMA"}.get(matmul, matmul),
                        "real_tokens_per_step": round(tokens / args.steps, 1),
                        "inputs": ("host arrays passed every step (PCIe-inclusive)" if args.by_value else

@@ -53,10 +53,13 @@ int laya_ctx_destroy(laya_ctx* ctx);
 int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes);
 /* Precision of the matrix products launched on the context afterwards (linear layers and the model's
  * projections; the elementwise kernels stay fp32), per product class. An fp32 class (the
- * default) is computed from an exact three-piece bf16 split of each operand: six bf16 matrix-core products
- * per fp32 product, accumulated in fp32, so the result carries fp32 rounding only (within 1e-6 relative
- * L2 of the fp64 product on every tested shape, as the fp32 matrix-core path); LAYA_MATMUL_FP32_MFMA
- * selects the fp32 matrix cores instead. A bf16 class rounds both operands
+ * default) is computed on the 16-bit matrix cores with fp32 accumulation and fp32 results as accurate as
+ * the fp32 matrix-core path (within 1e-6 relative L2 of the fp64 product on every tested shape): the
+ * 256-wide kernels (the large products) split each operand, scaled by a power of two taken from its
+ * largest finite magnitude, into two fp16 pieces and add three piece products per fp32 product; the
+ * other kernels split each operand exactly into three bf16 pieces and add six piece products.
+ * LAYA_MATMUL_SPLIT3_* keeps a class on the three-piece splits everywhere; LAYA_MATMUL_FP32_MFMA selects
+ * the fp32 matrix cores instead. A bf16 class rounds both operands
  * to bf16 (nearest even) as they are staged and multiplies on the bf16 matrix cores with fp32
  * accumulation and fp32 outputs: the mixed-precision mode (bf16 weights and activations in the
  * products, fp32 master weights, gradients and statistics). Attention's products (head_dim 64) use the
@@ -71,6 +74,10 @@ enum {
     LAYA_MATMUL_BF16_WEIGHT_GRAD = 4, /* dW += dyᵀ·x */
     LAYA_MATMUL_BF16 = 7,             /* every product */
     LAYA_MATMUL_FP32_MFMA = 8,        /* the fp32 classes on v_mfma_f32_32x32x2_f32 instead */
+    LAYA_MATMUL_SPLIT3_FORWARD = 16,  /* per class: an fp32 class on three-piece bf16 splits in every */
+    LAYA_MATMUL_SPLIT3_INPUT_GRAD = 32,  /*   kernel (no two-piece fp16 products); the backward pair */
+    LAYA_MATMUL_SPLIT3_WEIGHT_GRAD = 64, /*   takes them unless both of its classes allow them */
+    LAYA_MATMUL_FP32_SPLIT3 = 112,    /* every fp32 class on three-piece bf16 splits */
     LAYA_MATMUL_SPLIT_ALL = 7
 };
 int laya_ctx_set_matmul_precision(laya_ctx* ctx, int precision);

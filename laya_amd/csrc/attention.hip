@@ -50,6 +50,7 @@ struct Params {
     const float* dcontext;
     float* dots;  // Σ_d dO·O per (row, head)
     float* dqkv;
+    unsigned* amax;  // optional magnitude word group of the output (context, or dqkv), folded per block
 };
 
 template <int D> struct Shape {
@@ -149,7 +150,9 @@ __device__ __forceinline__ void inverse_rope_acc(f32x16 (&acc)[Shape<D>::ND], co
 
 // Writes an accumulator (rows d, column = the lane's row) into row `row` of dst at column `col`.
 template <int D>
-__device__ __forceinline__ void store_acc(const f32x16 (&acc)[Shape<D>::ND], float* dst_row, int h, float scale) {
+// Returns max|stored value| (amax_bits) for the output's magnitude word.
+__device__ __forceinline__ unsigned store_acc(const f32x16 (&acc)[Shape<D>::ND], float* dst_row, int h, float scale) {
+    unsigned m = 0;
 #pragma unroll
     for (int dt = 0; dt < Shape<D>::ND; ++dt)
 #pragma unroll
@@ -157,7 +160,9 @@ __device__ __forceinline__ void store_acc(const f32x16 (&acc)[Shape<D>::ND], flo
             const f32x4 v = {acc[dt][4 * r4] * scale, acc[dt][4 * r4 + 1] * scale, acc[dt][4 * r4 + 2] * scale,
                              acc[dt][4 * r4 + 3] * scale};
             st4(dst_row + dt * 32 + 8 * r4 + 4 * h, v);
+            m = max(m, amax_bits4(v));
         }
+    return m;
 }
 
 // store_acc's values, also as bf16 (nearest even) into row `row` of a bf16 copy.
@@ -286,11 +291,13 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
     }
 
     const float lt = l + __shfl_xor(l, 32, 64);
+    unsigned am = 0;
     if (qvalid) {
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        store_acc<D>(o, p.context + (long)(start + q) * p.hidden + qcol, h, inv);
+        am = store_acc<D>(o, p.context + (long)(start + q) * p.hidden + qcol, h, inv);
         if (h == 0) p.lse[(long)(start + q) * p.heads + head] = lt > 0.0f ? m + log2f(lt) : __builtin_huge_valf();
     }
+    block_amax_fold(am, p.amax);
 }
 
 // ------------------------------------------------------------------------------------ split products
@@ -545,12 +552,14 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     }
 
     const float lt = l + __shfl_xor(l, 32, 64);
+    unsigned am = 0;
     if (qvalid) {
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        store_acc<D>(o, p.context + (long)(start + q) * p.hidden + qcol, h, inv);
+        am = store_acc<D>(o, p.context + (long)(start + q) * p.hidden + qcol, h, inv);
         if (p.context16) store_acc16<D>(o, p.context16 + (long)(start + q) * p.hidden + qcol, h, inv);
         if (h == 0) p.lse[(long)(start + q) * p.heads + head] = lt > 0.0f ? m + log2f(lt) : __builtin_huge_valf();
     }
+    block_amax_fold(am, p.amax);
 }
 
 // ------------------------------------------------------------------------------------ backward
@@ -698,12 +707,13 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_kernel(Params p) {
         }
     }
 
+    unsigned am = 0;
     if (kvalid) {
         if (rope) inverse_rope_acc<D>(dk, p, key, h);
         float* dst = p.dqkv + (long)(start + key) * stride;
-        store_acc<D>(dk, dst + kcol, h, 1.0f);
-        store_acc<D>(dv, dst + vcol, h, 1.0f);
+        am = max(store_acc<D>(dk, dst + kcol, h, 1.0f), store_acc<D>(dv, dst + vcol, h, 1.0f));
     }
+    block_amax_fold(am, p.amax);
 }
 
 template <int D>
@@ -801,10 +811,12 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
         }
     }
 
+    unsigned am = 0;
     if (qvalid) {
         if (rope) inverse_rope_acc<D>(dq, p, q, h);
-        store_acc<D>(dq, p.dqkv + (long)(start + q) * stride + qcol, h, 1.0f);
+        am = store_acc<D>(dq, p.dqkv + (long)(start + q) * stride + qcol, h, 1.0f);
     }
+    block_amax_fold(am, p.amax);
 }
 
 // The backward on split products, tiles of 32 query or key rows: with the dK/dV kernel's V planes (the
@@ -953,12 +965,13 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     int te = threadIdx.x;
     asm volatile("" : "+v"(te));
     const int he = (te & 63) >> 5, keye = kb0 + (te >> 6) * WAVE_ROWS + (te & 31);
+    unsigned am = 0;
     if (keye < L) {
         if (rope) inverse_rope_acc<D>(dk, p, keye, he);
         float* dst = p.dqkv + (long)(start + keye) * stride;
-        store_acc<D>(dk, dst + kcol, he, 1.0f);
-        store_acc<D>(dv, dst + vcol, he, 1.0f);
+        am = max(store_acc<D>(dk, dst + kcol, he, 1.0f), store_acc<D>(dv, dst + vcol, he, 1.0f));
     }
+    block_amax_fold(am, p.amax);
 }
 
 template <int D, bool DROP>
@@ -1080,10 +1093,12 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
         }
     }
 
+    unsigned am = 0;
     if (qvalid) {
         if (rope) inverse_rope_acc<D>(dq, p, q, h);
-        store_acc<D>(dq, p.dqkv + (long)(start + q) * stride + qcol, h, 1.0f);
+        am = store_acc<D>(dq, p.dqkv + (long)(start + q) * stride + qcol, h, 1.0f);
     }
+    block_amax_fold(am, p.amax);
 }
 
 // RoPE at segment-local positions on the q and k columns of one segment's qkv rows, written to `out`
@@ -1165,13 +1180,15 @@ bool split_attention(const laya_ctx* ctx) { return (ctx->matmul_split | ctx->mat
 
 }  // namespace
 
-void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse, __bf16* context16) {
+void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse, __bf16* context16,
+                   unsigned* amax) {
     check_args(a);
     if (a.nseg == 0 || a.max_len == 0) return;
     Params p = make_params(a);
     p.qkv = rotated_qkv(ctx, a);
     p.context = context;
     p.lse = lse;
+    p.amax = amax;
     dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
     const bool split = a.head_dim == 64 && split_attention(ctx);
     p.context16 = split ? context16 : nullptr;
@@ -1194,10 +1211,11 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
 }
 
 void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,
-                        const float* dcontext, float* dqkv) {
+                        const float* dcontext, float* dqkv, unsigned* amax) {
     check_args(a);
     if (a.nseg == 0 || a.max_len == 0 || rows == 0) return;
     Params p = make_params(a);
+    p.amax = amax;
     AttentionArgs ar = a;
     if (ar.rows < 0) ar.rows = rows;
     p.qkv = rotated_qkv(ctx, ar);

@@ -172,11 +172,17 @@ int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes) {
 int laya_ctx_set_matmul_precision(laya_ctx* ctx, int precision) {
     return guarded([&] {
         require_ctx(ctx);
-        LAYA_REQUIRE(precision >= 0 && precision <= (LAYA_MATMUL_BF16 | LAYA_MATMUL_FP32_MFMA),
-                     "matmul precision: LAYA_MATMUL_FP32, LAYA_MATMUL_FP32_MFMA, or bf16 classes");
+        LAYA_REQUIRE(precision >= 0 && precision <= (LAYA_MATMUL_BF16 | LAYA_MATMUL_FP32_MFMA | LAYA_MATMUL_FP32_SPLIT3),
+                     "matmul precision: LAYA_MATMUL_FP32, LAYA_MATMUL_FP32_MFMA, LAYA_MATMUL_FP32_SPLIT3, or bf16 "
+                     "classes");
+        LAYA_REQUIRE(!((precision & LAYA_MATMUL_FP32_MFMA) && (precision & LAYA_MATMUL_FP32_SPLIT3)),
+                     "matmul precision: LAYA_MATMUL_FP32_MFMA and LAYA_MATMUL_FP32_SPLIT3 exclude each other");
         ctx->matmul_bf16 = precision & LAYA_MATMUL_BF16;
-        // fp32 classes use split products unless LAYA_MATMUL_FP32_MFMA asks for the fp32 matrix cores.
+        // fp32 classes use split products unless LAYA_MATMUL_FP32_MFMA asks for the fp32 matrix cores; the
+        // 256-wide kernels of those take two-piece fp16 products unless LAYA_MATMUL_FP32_SPLIT3 asks for the
+        // three-piece bf16 splits.
         ctx->matmul_split = (precision & LAYA_MATMUL_FP32_MFMA) ? 0 : (LAYA_MATMUL_SPLIT_ALL & ~ctx->matmul_bf16);
+        ctx->matmul_pair = ctx->matmul_split & ~((precision & LAYA_MATMUL_FP32_SPLIT3) >> 4);
     });
 }
 

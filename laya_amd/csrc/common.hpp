@@ -89,6 +89,11 @@ struct laya_ctx {
     int matmul_bf16 = 0;
     // fp32 products from three-piece bf16 splits (fp32-accurate, on the bf16 MFMA), same class bits.
     int matmul_split = LAYA_MATMUL_SPLIT_ALL;
+    // Of those, the classes whose 256-wide kernels take two-piece fp16 products instead (fp32-accurate,
+    // three fp16 MFMA products per fp32 one, operands scaled by powers of two), same class bits.
+    int matmul_pair = LAYA_MATMUL_SPLIT_ALL;
+    // max|operand| words of the two-piece products that no caller keeps (one per operand of a product).
+    unsigned* amax = nullptr;
     std::vector<hipEvent_t> event_pool;
     std::vector<laya::LaunchRecord> launches;
     int next_event = 0;
@@ -163,6 +168,35 @@ __device__ inline double wave_sum_d(double v) {
     return v;
 }
 
+// The two-piece fp16 products take each operand's scale from max|x| over its finite elements, kept as
+// fp32 bit patterns (non-negative patterns order as their values) in a group of AMAX_SPREAD device words
+// that the kernels producing the operand fold their outputs into: amax_bits of each value, then one
+// atomicMax per block into word blockIdx mod AMAX_SPREAD (spread so that thousands of blocks do not
+// meet on one address); the maximum is the largest word of the group.
+constexpr int AMAX_SPREAD = 16;
+__device__ inline unsigned amax_bits(float x) {
+    const unsigned a = __builtin_bit_cast(unsigned, x) & 0x7fffffffu;
+    return a < 0x7f800000u ? a : 0u;  // infinities and NaNs left out
+}
+template <class V>
+__device__ inline unsigned amax_bits4(V v) {
+    return max(max(amax_bits(v[0]), amax_bits(v[1])), max(amax_bits(v[2]), amax_bits(v[3])));
+}
+// Every thread of the block calls it (it synchronises the block); out may be null.
+__device__ inline void block_amax_fold(unsigned m, unsigned* out) {
+    if (!out) return;
+    __shared__ unsigned red[16];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = max(m, (unsigned)__shfl_xor((int)m, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned t = red[0];
+        for (int w = 1; w < (int)((blockDim.x + 63) >> 6); ++w) t = max(t, red[w]);
+        atomicMax(out + (blockIdx.x & (AMAX_SPREAD - 1)), t);
+    }
+}
+
 inline unsigned blocks_for(size_t n, unsigned per_block, unsigned cap = 65535u * 16u) {
     size_t b = (n + per_block - 1) / per_block;
     if (b == 0) b = 1;
@@ -199,30 +233,46 @@ enum class GemmEpilogue {
 
 // A16 / B16: optional bf16 copies of A / B (rounded to nearest even, same leading dimensions) that a bf16
 // product reads instead of rounding A / B itself; the result is the same.
+// A max|operand| word group (AMAX_SPREAD words) kept by a caller for the two-piece fp16 products: `word`
+// on the device, `*known` on the host says whether it holds the operand's current value. A product that
+// needs it and finds it unknown measures the operand into it (and sets *known): an unknown group must
+// hold zeros. A null word makes the product measure into the context's own words on every call.
+struct AmaxRef {
+    unsigned* word = nullptr;
+    unsigned char* known = nullptr;
+};
+
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
           const float* B, long ldb, float* C, long ldc, const float* bias = nullptr, const float* R = nullptr,
-          long ldr = 0, const __bf16* A16 = nullptr, const __bf16* B16 = nullptr);
+          long ldr = 0, const __bf16* A16 = nullptr, const __bf16* B16 = nullptr, AmaxRef amax_a = {},
+          AmaxRef amax_b = {});
 
 // y = x·Wᵀ + b for x [M, K], W [N, K] with RoPE applied in the epilogue to output columns [0, rope_cols)
 // taken as heads of 64 (d and d + 32 rotated at position pos[row]; tables [positions][32]). The fused
 // QKV projection: q and k leave the GEMM already rotated (Ops.cs:297-313).
 void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* B, float* C, const float* bias,
                const int* pos, const float* cos_t, const float* sin_t, int rope_cols, const __bf16* A16 = nullptr,
-               const __bf16* B16 = nullptr);
+               const __bf16* B16 = nullptr, AmaxRef amax_a = {}, AmaxRef amax_b = {});
 
 // The two products of Ops.LinearBackward in one launch: dx = dy·W (+ dx_residual) and dW += dyᵀ·x,
 // for dy [rows, out], W [out, in], x [rows, in]; split-K partials of dW reduced in a fixed order.
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
                         float* dx, const float* dx_residual, float* dW, const __bf16* W16 = nullptr,
-                        const __bf16* x16 = nullptr);
+                        const __bf16* x16 = nullptr, AmaxRef amax_dy = {}, AmaxRef amax_W = {},
+                        AmaxRef amax_x = {});
+
+// max|x| over the finite elements of a rows x cols operand (row stride ld), folded into the word group
+// at out by atomicMax as fp32 bit patterns (the two-piece products' operand scales).
+void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, unsigned* out);
 
 // Σ over rows of a [rows, n] matrix added into out[n], deterministic (bias gradients).
 void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out);
 
-// y16 (optional): a bf16 copy of y (nearest even), for the bf16 products that read it.
+// y16 (optional): a bf16 copy of y (nearest even), for the bf16 products that read it; amax (optional):
+// max|y| folded into a magnitude word group (absmax_into).
 void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps, float* y,
                    float* mean, float* rstd, const int* gather_ids = nullptr, const float* add_table = nullptr,
-                   const int* add_index = nullptr, __bf16* y16 = nullptr);
+                   const int* add_index = nullptr, __bf16* y16 = nullptr, unsigned* amax = nullptr);
 // Column sums whose reduction is deferred: `count` partial rows of `n` floats in `part`, added into `out`.
 struct ColumnSumJob {
     const float* part;
@@ -239,9 +289,11 @@ struct ColumnSumJobs {
 // reduction is appended to `jobs` instead of launched (the caller runs column_reduce_batch later; a full
 // list is flushed first). Falls back to the immediate reduction when a gradient is not 16-byte aligned.
 int ln_bwd_partial_rows(int rows);
+// amax (optional): max|dx| (after the addition) folded into a magnitude word group.
 void layernorm_bwd_deferred(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
                             const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
-                            const float* rstd, const int* gather_ids, float* ws, ColumnSumJobs& jobs);
+                            const float* rstd, const int* gather_ids, float* ws, ColumnSumJobs& jobs,
+                            unsigned* amax = nullptr);
 void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
                    float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
                    const int* gather_ids = nullptr);
@@ -275,8 +327,10 @@ inline double window_keys(int L, int hw) {
     for (int q = 0; q < L; ++q) s += std::min(L - 1, q + hw) - std::max(0, q - hw) + 1;
     return s;
 }
-// context16 (optional): a bf16 copy of the context (nearest even), for the bf16 products that read it.
-void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse, __bf16* context16 = nullptr);
+// context16 (optional): a bf16 copy of the context (nearest even), for the bf16 products that read it;
+// amax (optional): max|context| folded into a magnitude word group.
+void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse, __bf16* context16 = nullptr,
+                   unsigned* amax = nullptr);
 
 // RlcdObjective.Compute (RlcdObjective.cs:57-155) with supplied standard-normal draws [groups][Σ K], all
 // operands on the device; grad [Σ K]; losses [4] = total, policy, cross-entropy, mean reward.
@@ -288,8 +342,9 @@ void rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets, co
 void decision_readout(laya_ctx* ctx, const float* scores, const int* opt_off, const int* seg_start, int n_items,
                       const float* states, int d, const float* w1, const float* b1, int a1, const float* w2,
                       const float* b2, int na, float* probs, float* features);
-// rows: the number of rows of qkv / context / dcontext (the dO·O row constants span all of them).
+// rows: the number of rows of qkv / context / dcontext (the dO·O row constants span all of them); amax
+// (optional): max|dqkv| folded into a magnitude word group.
 void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,
-                   const float* dcontext, float* dqkv);
+                   const float* dcontext, float* dqkv, unsigned* amax = nullptr);
 
 }  // namespace laya

@@ -43,10 +43,12 @@ __global__ void gelu_bwd_kernel(const float* u, float* g, size_t n) {
 }
 
 // GeGLU, 4 columns per thread: act[t, i] = gelu(wide[t, i]) · wide[t, I + i].
+// amax (optional): max|act| folded in (the output's magnitude word).
 __global__ void geglu_fwd_kernel(const float* __restrict__ wide, int rows, int inter, float* __restrict__ act,
-                                 __bf16* __restrict__ act16) {
+                                 __bf16* __restrict__ act16, unsigned* amax) {
     const int q = inter >> 2;
     const size_t n = (size_t)rows * q;
+    unsigned m = 0;
     GRID_STRIDE(i, n) {
         const size_t t = i / q;
         const int c = (int)(i - t * q) * 4;
@@ -55,14 +57,18 @@ __global__ void geglu_fwd_kernel(const float* __restrict__ wide, int rows, int i
         const f32x4 o = {gelu_f(x[0]) * g[0], gelu_f(x[1]) * g[1], gelu_f(x[2]) * g[2], gelu_f(x[3]) * g[3]};
         st4(act + t * inter + c, o);
         if (act16) *reinterpret_cast<bf16x4*>(act16 + t * inter + c) = __builtin_convertvector(o, bf16x4);
+        m = max(m, amax_bits4(o));
     }
+    block_amax_fold(m, amax);
 }
 
 // dwide[t] = [dact·gate·gelu'(input) | dact·gelu(input)] (TrainableDecisionModel.cs:573-578).
+// amax (optional): max|dwide| folded in.
 __global__ void geglu_bwd_kernel(const float* __restrict__ wide, const float* __restrict__ dact, int rows, int inter,
-                                 float* __restrict__ dwide) {
+                                 float* __restrict__ dwide, unsigned* amax) {
     const int q = inter >> 2;
     const size_t n = (size_t)rows * q;
+    unsigned m = 0;
     GRID_STRIDE(i, n) {
         const size_t t = i / q;
         const int c = (int)(i - t * q) * 4;
@@ -76,7 +82,9 @@ __global__ void geglu_bwd_kernel(const float* __restrict__ wide, const float* __
         }
         st4(dwide + t * 2 * inter + c, di);
         st4(dwide + t * 2 * inter + inter + c, dg);
+        m = max(m, max(amax_bits4(di), amax_bits4(dg)));
     }
+    block_amax_fold(m, amax);
 }
 
 __global__ void geglu_fwd_scalar_kernel(const float* wide, int rows, int inter, float* act) {
@@ -434,16 +442,17 @@ void gelu_bwd(laya_ctx* ctx, const float* u, float* g, size_t n) {
     hipLaunchKernelGGL(gelu_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, u, g, n);
     check_launch("gelu_bwd_kernel");
 }
-void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, __bf16* act16) {
+void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, __bf16* act16, unsigned* amax) {
     if (rows <= 0 || inter <= 0) return;
     ProfileScope scope(ctx, "geglu_fwd", 0.0, (12.0 + (act16 ? 2.0 : 0.0)) * rows * (double)inter);
     if (inter % 4 == 0) {
         hipLaunchKernelGGL(geglu_fwd_kernel, dim3(grid_for((size_t)rows * inter / 4)), dim3(256), 0, ctx->stream,
-                           wide, rows, inter, act, act16);
+                           wide, rows, inter, act, act16, amax);
     } else {
         hipLaunchKernelGGL(geglu_fwd_scalar_kernel, dim3(grid_for((size_t)rows * inter)), dim3(256), 0, ctx->stream,
                            wide, rows, inter, act);
         if (act16) to_bf16(ctx, act, (size_t)rows * inter, act16);
+        if (amax) absmax_into(ctx, act, rows, inter, inter, amax);
     }
     check_launch("geglu_fwd_kernel");
 }
@@ -460,15 +469,17 @@ void to_bf16(laya_ctx* ctx, const float* src, size_t n, __bf16* dst) {
     hipLaunchKernelGGL(to_bf16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, src, dst, n);
     check_launch("to_bf16_scalar_kernel");
 }
-void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide) {
+void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide,
+               unsigned* amax) {
     if (rows <= 0 || inter <= 0) return;
     ProfileScope scope(ctx, "geglu_bwd", 0.0, 20.0 * rows * (double)inter);
     if (inter % 4 == 0) {
         hipLaunchKernelGGL(geglu_bwd_kernel, dim3(grid_for((size_t)rows * inter / 4)), dim3(256), 0, ctx->stream,
-                           wide, dact, rows, inter, dwide);
+                           wide, dact, rows, inter, dwide, amax);
     } else {
         hipLaunchKernelGGL(geglu_bwd_scalar_kernel, dim3(grid_for((size_t)rows * inter)), dim3(256), 0, ctx->stream,
                            wide, dact, rows, inter, dwide);
+        if (amax) absmax_into(ctx, dwide, rows, 2 * inter, 2 * inter, amax);
     }
     check_launch("geglu_bwd_kernel");
 }

@@ -9,10 +9,13 @@ void add(laya_ctx* ctx, float* dst, const float* src, size_t n);
 void scale(laya_ctx* ctx, float* dst, float s, size_t n);
 void gelu_fwd(laya_ctx* ctx, const float* x, size_t n, float* y);
 void gelu_bwd(laya_ctx* ctx, const float* u, float* g, size_t n);
-// The optional __bf16* outputs are copies rounded to nearest even, for the bf16 products that read them.
-void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, __bf16* act16 = nullptr);
+// The optional __bf16* outputs are copies rounded to nearest even, for the bf16 products that read them;
+// the optional unsigned* amax outputs fold max|output| into a magnitude word (absmax_into).
+void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, __bf16* act16 = nullptr,
+               unsigned* amax = nullptr);
 void to_bf16(laya_ctx* ctx, const float* src, size_t n, __bf16* dst);
-void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide);
+void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide,
+               unsigned* amax = nullptr);
 void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed);
 // dst = Dropout(src) out of place (one pass).
 void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p, uint64_t seed);

@@ -63,6 +63,10 @@ struct GemmParams {
     // conversion; the result is the same.
     const __bf16* A16;
     const __bf16* B16;
+    // Two-piece fp16 products: the bit patterns of max|A| and max|B| (device words, written by
+    // absmax_kernel before the product), from which each kernel takes its operands' power-of-two scales.
+    const unsigned* amax_a;
+    const unsigned* amax_b;
 };
 
 // ------------------------------------------------------------------------------ shared pieces
@@ -837,13 +841,19 @@ struct OperandW {
         for (int i = 0; i < 2; ++i)
             reg[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[i], k0 * 4, 0));
     }
-    // NP = 3: the three split planes; NP = 1: one plane of the values rounded to bf16.
+    // NP = 3: the three split planes; NP = 2: the two fp16 planes of s·x; NP = 1: one plane of the values
+    // rounded to bf16.
     template <int NP = 3>
-    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+    __device__ __forceinline__ void store(__bf16* lds, int tid, float sc = 1.0f) const {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int o = ((tid >> 2) + 128 * i) * KPADQ + ((tid & 3) << 2);
-            if constexpr (NP == 3) {
+            if constexpr (NP == 2) {
+                f16x4 hi, lo;
+                split2h_4(reg[i], sc, hi, lo);
+                *reinterpret_cast<f16x4*>(lds + o) = hi;
+                *reinterpret_cast<f16x4*>(lds + STAGE_W + o) = lo;
+            } else if constexpr (NP == 3) {
                 bf16x4 h1, h2, h3;
                 split3_4(reg[i], h1, h2, h3);
                 *reinterpret_cast<bf16x4*>(lds + o) = h1;
@@ -875,7 +885,7 @@ struct OperandW16 {
     }
     __device__ __forceinline__ void tail(int k0, int) { full(k0); }
     template <int NP = 1>
-    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+    __device__ __forceinline__ void store(__bf16* lds, int tid, float = 1.0f) const {
         static_assert(NP == 1, "a bf16 copy feeds bf16 products");
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -894,11 +904,51 @@ __device__ __forceinline__ void mma6(const bf16x8 (&a)[3], const bf16x8 (&b)[3],
     acc = c;
 }
 
+// The three fp16 piece products of a two-piece product block, smallest first.
+__device__ __forceinline__ void mma3h(const f16x8 (&a)[2], const f16x8 (&b)[2], f32x16& acc) {
+    f32x16 c = acc;
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b[0], c, 0, 0, 0);
+    acc = c;
+}
+
+// Two-piece fp16 stage: the same fragment walk as mma_stage_w over two fp16 planes, three products each.
+__device__ __forceinline__ void mma_stage_w2(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2][2], int wm, int wn,
+                                             int lr, int half) {
+    const _Float16* Ah = reinterpret_cast<const _Float16*>(A);
+    const _Float16* Bh = reinterpret_cast<const _Float16*>(B);
+    f16x8 b[2][2], a[2][2];
+    auto rd_a = [&](int g, f16x8 (&dst)[2]) {
+        const int row = 128 * (g >> 1) + wm * 64 + 32 * (g & 1) + lr;
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+            dst[pl] = *reinterpret_cast<const f16x8*>(Ah + pl * STAGE_W + row * KPADQ + 8 * half);
+    };
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+            b[j][pl] = *reinterpret_cast<const f16x8*>(Bh + pl * STAGE_W + (wn * 64 + 32 * j + lr) * KPADQ + 8 * half);
+    rd_a(0, a[0]);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        if (g + 1 < 4) rd_a(g + 1, a[(g + 1) & 1]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) mma3h(a[g & 1], b[j], acc[g >> 1][g & 1][j]);
+    }
+}
+
 // One 16-deep stage of a wave's two subtiles: B fragments once, A fragments one 32-row group ahead.
-// NP = 3: six piece products per block (split products); NP = 1: one bf16 product.
+// NP = 3: six piece products per block (split products); NP = 2: three fp16 piece products (two-piece
+// products); NP = 1: one bf16 product.
 template <int NP = 3>
 __device__ __forceinline__ void mma_stage_w(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2][2], int wm, int wn,
                                             int lr, int half) {
+    if constexpr (NP == 2) {
+        mma_stage_w2(A, B, acc, wm, wn, lr, half);
+        return;
+    }
     bf16x8 b[2][3], a[2][3];
     auto rd_a = [&](int g, bf16x8 (&dst)[3]) {
         const int row = 128 * (g >> 1) + wm * 64 + 32 * (g & 1) + lr;
@@ -942,12 +992,50 @@ struct WideK<true> {
     }
 };
 
-// NP = 3: the split (fp32) product; NP = 1: the bf16 product, with AH / BH reading A / B from their bf16
-// copies.
+// The power-of-two operand scales 2^ea, 2^eb of a two-piece fp16 product; the accumulators are scaled
+// back by 2^-(ea+eb) with one exact ldexp each.
+struct PairScales {
+    float sa = 1.0f, sb = 1.0f;
+    int ex = 0;
+    __device__ __forceinline__ PairScales() = default;
+    static __device__ __forceinline__ unsigned group_max(const unsigned* w) {
+        unsigned m = w[0];
+#pragma unroll
+        for (int i = 1; i < AMAX_SPREAD; ++i) m = max(m, w[i]);
+        return m;
+    }
+    __device__ __forceinline__ PairScales(const unsigned* amax_a, const unsigned* amax_b) {
+        const int ea = pair_scale_exp(group_max(amax_a)), eb = pair_scale_exp(group_max(amax_b));
+        sa = exp2_int(ea);
+        sb = exp2_int(eb);
+        ex = -(ea + eb);
+    }
+    __device__ __forceinline__ void unscale(f32x16& a) const {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a[i] = __builtin_amdgcn_ldexpf(a[i], ex);
+    }
+    template <int A, int B>
+    __device__ __forceinline__ void unscale(f32x16 (&acc)[A][B]) const {
+#pragma unroll
+        for (int i = 0; i < A; ++i)
+#pragma unroll
+            for (int j = 0; j < B; ++j) unscale(acc[i][j]);
+    }
+    template <int A, int B, int C>
+    __device__ __forceinline__ void unscale(f32x16 (&acc)[A][B][C]) const {
+#pragma unroll
+        for (int i = 0; i < A; ++i) unscale(acc[i]);
+    }
+};
+
+// NP = 3: the split (fp32) product; NP = 2: the two-piece fp16 product (fp32-accurate, scaled operands);
+// NP = 1: the bf16 product, with AH / BH reading A / B from their bf16 copies.
 template <int MODE, int NP = 3, bool AH = false, bool BH = false>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     static_assert(MODE == STORE || MODE == STORE_ROPE, "whole-K NT epilogues");
     static_assert(NP == 1 || !(AH || BH), "bf16 copies feed bf16 products");
+    PairScales ps;
+    if constexpr (NP == 2) ps = PairScales(p.amax_a, p.amax_b);
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];  // [stage][operand]
     const int t = xcd_logical_block();
     const int tm = t / p.tiles_n;
@@ -978,8 +1066,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
             for (int j = 0; j < 2; ++j) acc[s][i][j] = f32x16{};
     a.full(kof(0));
     b.full(kof(0));
-    a.template store<NP>(smem[0][0], tid);
-    b.template store<NP>(smem[0][1], tid);
+    a.template store<NP>(smem[0][0], tid, ps.sa);
+    b.template store<NP>(smem[0][1], tid, ps.sb);
     a.full(kof(min(1, nt - 1)));
     b.full(kof(min(1, nt - 1)));
     lds_barrier();
@@ -988,12 +1076,13 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
         const int cur = j & 1;
         const int kn = kof(min(j + 2, nt - 1));
         mma_stage_w<NP>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
-        a.template store<NP>(smem[cur ^ 1][0], tid);
-        b.template store<NP>(smem[cur ^ 1][1], tid);
+        a.template store<NP>(smem[cur ^ 1][0], tid, ps.sa);
+        b.template store<NP>(smem[cur ^ 1][1], tid, ps.sb);
         a.full(kn);
         b.full(kn);
         lds_barrier();
     }
+    if constexpr (NP == 2) ps.unscale(acc);
     // The epilogue's lane coordinates are taken again after the K loop, so its store offsets are computed
     // here rather than held across the loop (the RoPE epilogue measured fewer spills the other way).
     const int te = MODE == STORE_ROPE ? tid : opaque_tid(), le = te & 63, we = te >> 6;
@@ -1016,6 +1105,45 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
         else
             store_acc<true, true, MODE, false, true, true>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2);
     }
+}
+
+// ------------------------------------------------------------- operand magnitudes for two-piece products
+//
+// max|x| over the finite elements of a rows x cols operand (row stride ld) as an fp32 bit pattern,
+// folded into *out (which holds 0 or a smaller pattern beforehand) by one atomicMax per block: the
+// maximum is the same whatever the order, and the product that reads it is a later launch. Infinities
+// and NaNs are left out, so the scale fits the finite values and the non-finite ones still reach the
+// products (an infinity's low piece is a NaN: outputs that an infinity reaches are non-finite, as in
+// fp32, though possibly NaN where fp32 gives an infinity).
+constexpr int AMAX_BLOCKS = 1024, AMAX_SLOTS = 4;
+
+__global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, int rows, int cols, long ld,
+                                                     int vec, unsigned* out) {
+    unsigned m = 0;
+    const int tid = threadIdx.x;
+    if (vec && ld == cols) {
+        const long n4 = (long)rows * cols / 4;
+        const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+        const long stride = (long)gridDim.x * 256;
+        long i = (long)blockIdx.x * 256 + tid;
+        for (; i + 3 * stride < n4; i += 4 * stride) {
+            f32x4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(x4 + i + u * stride);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) m = max(m, amax_bits4(v[u]));
+        }
+        for (; i < n4; i += stride) m = max(m, amax_bits4(x4[i]));
+    } else if (vec) {
+        for (int r = blockIdx.x; r < rows; r += gridDim.x) {
+            const f32x4* row = reinterpret_cast<const f32x4*>(x + (long)r * ld);
+            for (int c = tid; c < cols / 4; c += 256) m = max(m, amax_bits4(row[c]));
+        }
+    } else {
+        for (int r = blockIdx.x; r < rows; r += gridDim.x)
+            for (int c = tid; c < cols; c += 256) m = max(m, amax_bits(x[(long)r * ld + c]));
+    }
+    block_amax_fold(m, out);
 }
 
 // ------------------------------------------------------------- split products on 192 x 256 tiles
@@ -1045,11 +1173,19 @@ struct OperandT {
         reg[0] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[0], k0 * 4, 0));
         if (two) reg[1] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[1], k0 * 4, 0));
     }
-    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+    template <int NP = 3>
+    __device__ __forceinline__ void store(__bf16* lds, int tid, float sc = 1.0f) const {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             if (i == 1 && !two) break;
             const int o = ((tid >> 2) + 128 * i) * KPADQ + ((tid & 3) << 2);
+            if constexpr (NP == 2) {
+                f16x4 hi, lo;
+                split2h_4(reg[i], sc, hi, lo);
+                *reinterpret_cast<f16x4*>(lds + o) = hi;
+                *reinterpret_cast<f16x4*>(lds + STAGE_T + o) = lo;
+                continue;
+            }
             bf16x4 h1, h2, h3;
             split3_4(reg[i], h1, h2, h3);
             *reinterpret_cast<bf16x4*>(lds + o) = h1;
@@ -1059,9 +1195,40 @@ struct OperandT {
     }
 };
 
+// The two-piece fp16 form of mma_stage_t: two fp16 planes, three products per block.
+__device__ __forceinline__ void mma_stage_t2(const __bf16* A, const __bf16* B, f32x16 (&acc)[3][2], int wm, int wn,
+                                             int lr, int half) {
+    const _Float16* Ah = reinterpret_cast<const _Float16*>(A);
+    const _Float16* Bh = reinterpret_cast<const _Float16*>(B);
+    f16x8 b[2][2], a[2][2];
+    auto rd_a = [&](int g, f16x8 (&dst)[2]) {
+        const int row = 96 * wm + 32 * g + lr;
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+            dst[pl] = *reinterpret_cast<const f16x8*>(Ah + pl * STAGE_T + row * KPADQ + 8 * half);
+    };
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+            b[j][pl] = *reinterpret_cast<const f16x8*>(Bh + pl * STAGE_W + (wn * 64 + 32 * j + lr) * KPADQ + 8 * half);
+    rd_a(0, a[0]);
+#pragma unroll
+    for (int g = 0; g < 3; ++g) {
+        if (g + 1 < 3) rd_a(g + 1, a[(g + 1) & 1]);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) mma3h(a[g & 1], b[j], acc[g][j]);
+    }
+}
+
 // One 16-deep stage of a wave's 96 x 64: B fragments once, A fragments one 32-row group ahead.
+template <int NP = 3>
 __device__ __forceinline__ void mma_stage_t(const __bf16* A, const __bf16* B, f32x16 (&acc)[3][2], int wm, int wn,
                                             int lr, int half) {
+    if constexpr (NP == 2) {
+        mma_stage_t2(A, B, acc, wm, wn, lr, half);
+        return;
+    }
     bf16x8 b[2][3], a[2][3];
     auto rd_a = [&](int g, bf16x8 (&dst)[3]) {
         const int row = 96 * wm + 32 * g + lr;
@@ -1083,9 +1250,12 @@ __device__ __forceinline__ void mma_stage_t(const __bf16* A, const __bf16* B, f3
     }
 }
 
-template <int MODE, bool RES>
+// NP = 3: split products; NP = 2: two-piece fp16 products.
+template <int MODE, bool RES, int NP = 3>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     static_assert(MODE == STORE || (MODE == STORE_ROPE && !RES), "whole-K NT epilogues");
+    PairScales ps;
+    if constexpr (NP == 2) ps = PairScales(p.amax_a, p.amax_b);
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * (STAGE_T + STAGE_W)];  // [stage][A planes, B planes]
     const int t = xcd_logical_block();
     const int tm = t / p.tiles_n;
@@ -1114,8 +1284,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
     a.full(kof(0));
     b.full(kof(0));
-    a.store(smem[0], tid);
-    b.store<3>(smem[0] + 3 * STAGE_T, tid);
+    a.template store<NP>(smem[0], tid, ps.sa);
+    b.template store<NP>(smem[0] + 3 * STAGE_T, tid, ps.sb);
     a.full(kof(min(1, nt - 1)));
     b.full(kof(min(1, nt - 1)));
     lds_barrier();
@@ -1123,13 +1293,14 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     for (int j = 0; j < nt; ++j) {
         const int cur = j & 1;
         const int kn = kof(min(j + 2, nt - 1));
-        mma_stage_t(smem[cur], smem[cur] + 3 * STAGE_T, acc, wm, wn, lr, half);
-        a.store(smem[cur ^ 1], tid);
-        b.store<3>(smem[cur ^ 1] + 3 * STAGE_T, tid);
+        mma_stage_t<NP>(smem[cur], smem[cur] + 3 * STAGE_T, acc, wm, wn, lr, half);
+        a.template store<NP>(smem[cur ^ 1], tid, ps.sa);
+        b.template store<NP>(smem[cur ^ 1] + 3 * STAGE_T, tid, ps.sb);
         a.full(kn);
         b.full(kn);
         lds_barrier();
     }
+    if constexpr (NP == 2) ps.unscale(acc);
     const int te = opaque_tid(), le = te & 63, we = te >> 6, wme = we >> 2;
     // store_acc places row group i of wave row wm at 64·wm + 32·i: a base 32·wm further down puts the
     // wave's three groups at 96·wm + 32·i.
@@ -1339,9 +1510,15 @@ struct OperandWS {
         }
     }
     template <int NP = 3>
-    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+    __device__ __forceinline__ void store(__bf16* lds, int tid, float sc = 1.0f) const {
         const int o = (tid & 255) * KPADQ + kq;
-        if constexpr (NP == 3) {
+        if constexpr (NP == 2) {
+            f16x4 a1, a2, b1, b2;
+            split2h_4(f32x4{v[0], v[1], v[2], v[3]}, sc, a1, a2);
+            split2h_4(f32x4{v[4], v[5], v[6], v[7]}, sc, b1, b2);
+            *reinterpret_cast<f16x8*>(lds + o) = __builtin_shufflevector(a1, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+            *reinterpret_cast<f16x8*>(lds + STAGE_W + o) = __builtin_shufflevector(a2, b2, 0, 1, 2, 3, 4, 5, 6, 7);
+        } else if constexpr (NP == 3) {
             bf16x4 a1, a2, a3, b1, b2, b3;
             split3_4(f32x4{v[0], v[1], v[2], v[3]}, a1, a2, a3);
             split3_4(f32x4{v[4], v[5], v[6], v[7]}, b1, b2, b3);
@@ -1388,7 +1565,7 @@ struct OperandWS16 {
         }
     }
     template <int NP = 1>
-    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+    __device__ __forceinline__ void store(__bf16* lds, int tid, float = 1.0f) const {
         static_assert(NP == 1, "a bf16 copy feeds bf16 products");
         typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
         u32x4 w;
@@ -1419,9 +1596,11 @@ struct WideS<true> {
 // acc += A·Bᵀ over K positions [kb, ke) in 16-deep stages: the full stages in rotated order starting at
 // `rot`, then the ragged last one (when ke − kb is not a multiple of 16) on its own, so the loop body
 // carries no per-element selects.
+// sa, sb: the operands' scales (two-piece fp16 products; 1 otherwise).
 template <int NP, class OA, class OB>
 __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, __bf16 (*smem)[2][3 * STAGE_W],
-                                         f32x16 (&acc)[2][2][2], int tid, int wm, int wn, int lr, int half) {
+                                         f32x16 (&acc)[2][2][2], int tid, int wm, int wn, int lr, int half,
+                                         float sa = 1.0f, float sb = 1.0f) {
     const int len = ke - kb, nfull = len / BKQ;
     rot = nfull > 0 ? rot % nfull : 0;
     auto fetch = [&](int j) {
@@ -1438,15 +1617,15 @@ __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, 
             for (int j = 0; j < 2; ++j) acc[s][i][j] = f32x16{};
     if (nfull > 0) {
         fetch(0);
-        a.template store<NP>(smem[0][0], tid);
-        b.template store<NP>(smem[0][1], tid);
+        a.template store<NP>(smem[0][0], tid, sa);
+        b.template store<NP>(smem[0][1], tid, sb);
         fetch(min(1, nfull - 1));
         lds_barrier();
         for (int j = 0; j < nfull; ++j) {
             const int cur = j & 1;
             mma_stage_w<NP>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
-            a.template store<NP>(smem[cur ^ 1][0], tid);
-            b.template store<NP>(smem[cur ^ 1][1], tid);
+            a.template store<NP>(smem[cur ^ 1][0], tid, sa);
+            b.template store<NP>(smem[cur ^ 1][1], tid, sb);
             fetch(min(j + 2, nfull - 1));
             lds_barrier();
         }
@@ -1454,8 +1633,8 @@ __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, 
     if (len % BKQ != 0) {
         a.tail(kb + nfull * BKQ, ke);
         b.tail(kb + nfull * BKQ, ke);
-        a.template store<NP>(smem[0][0], tid);
-        b.template store<NP>(smem[0][1], tid);
+        a.template store<NP>(smem[0][0], tid, sa);
+        b.template store<NP>(smem[0][1], tid, sb);
         lds_barrier();
         mma_stage_w<NP>(smem[0][0], smem[0][1], acc, wm, wn, lr, half);
         lds_barrier();
@@ -1474,12 +1653,19 @@ __device__ __forceinline__ void write_partial_w(float* slot, const f32x16 (&acc)
 }
 
 // nn and tn carry wide tile counts (tiles_m, tiles_n of 256 x 256 tiles); s counts 16-deep units.
-// NP = 3: split products (fp32); NP = 1: bf16 products (the bf16 policies of both backward classes).
+// NP = 3: split products (fp32); NP = 2: two-piece fp16 products (fp32-accurate; nn.amax_a = max|dY|,
+// nn.amax_b = max|W|, tn.amax_b = max|x|); NP = 1: bf16 products (the bf16 policies of both backward
+// classes).
 // RES: dX = dY·W + nn.R (the residual may be dX itself: each element is read and written by one lane).
 // BH (NP = 1): W and x are read from their bf16 copies (nn.B16, tn.B16).
 template <int NP, bool RES, bool BH = false>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParams nn, GemmParams tn, PairPlan s) {
     static_assert(NP == 1 || !BH, "bf16 copies feed bf16 products");
+    PairScales px, pw;  // dX = dY·W, dW = dYᵀ·x
+    if constexpr (NP == 2) {
+        px = PairScales(nn.amax_a, nn.amax_b);
+        pw = PairScales(nn.amax_a, tn.amax_b);
+    }
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];
     const int g = xcd_logical_block();
     const int count = s.q + (g < s.r ? 1 : 0);
@@ -1499,7 +1685,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         OperandWK a(nn.A, nn.lda, c.m0, nn.M, tid, (unsigned)(nn.M * nn.lda * 4));
         typename WideS<BH>::T b = WideS<BH>::make(nn.B, nn.B16, nn.ldb, c.n0, nn.N, tid, nn.K);
         f32x16 acc[2][2][2];
-        wide_mma<NP>(a, b, 0, nn.K, t, smem, acc, tid, wm, wn, lr, half);
+        wide_mma<NP>(a, b, 0, nn.K, t, smem, acc, tid, wm, wn, lr, half, px.sa, px.sb);
+        if constexpr (NP == 2) px.unscale(acc);
         // The epilogue's lane coordinates are taken again after the K loop, so its store offsets are
         // computed here rather than before the loop (where they would be held, spilled, across it).
         const int te = opaque_tid(), le = te & 63, we = te >> 6;
@@ -1540,7 +1727,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         OperandWS a(tn.A, tn.lda, m0, tn.M, tid, (unsigned)(tn.K * tn.lda * 4));
         typename WideS<BH>::T b = WideS<BH>::make(tn.B, tn.B16, tn.ldb, n0, tn.N, tid, tn.K);
         f32x16 acc[2][2][2];
-        wide_mma<NP>(a, b, a0 * BKQ, min(tn.K, b0 * BKQ), g, smem, acc, tid, wm, wn, lr, half);
+        wide_mma<NP>(a, b, a0 * BKQ, min(tn.K, b0 * BKQ), g, smem, acc, tid, wm, wn, lr, half, pw.sa, pw.sb);
+        if constexpr (NP == 2) pw.unscale(acc);
         write_partial_w(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (WT * WT), acc);
         u += b0 - a0;
     }
@@ -1948,11 +2136,66 @@ bool tall_tiles_pay(const laya_ctx* ctx, const GemmParams& p) {
     return t_tall < std::min(t_two, t_three);
 }
 
+}  // namespace
+
+// max|x| of a rows x cols operand folded into *out (0 beforehand for the operand's own maximum).
+void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, unsigned* out) {
+    const long n = (long)rows * cols;
+    if (n <= 0) return;
+    ProfileScope scope(ctx, "absmax", 0.0, 4.0 * n);
+    const int vec = cols % 4 == 0 && ld % 4 == 0 && aligned16(x);
+    const long per_block = 256L * 4 * 8;  // eight float4 per thread
+    const int blocks = (int)std::max(1L, std::min<long>(AMAX_BLOCKS, (n + per_block - 1) / per_block));
+    hipLaunchKernelGGL(absmax_kernel, dim3(vec && ld == cols ? blocks : std::min(blocks, std::max(rows, 1))),
+                       dim3(256), 0, ctx->stream, x, rows, cols, ld, vec, out);
+    check_launch("absmax_kernel");
+}
+
+namespace {
+
+// max|x| of a rows x cols operand into the context's word group `slot` (cleared first); returns it.
+const unsigned* operand_absmax(laya_ctx* ctx, int slot, const float* x, int rows, int cols, long ld) {
+    if (!ctx->amax) ctx->amax = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_SLOTS * AMAX_SPREAD));
+    unsigned* out = ctx->amax + slot * AMAX_SPREAD;
+    fill(ctx, reinterpret_cast<float*>(out), 0.0f, AMAX_SPREAD);  // +0.0f is the all-zero word
+    absmax_into(ctx, x, rows, cols, ld, out);
+    return out;
+}
+
+// The magnitude word of an operand: the caller's (measured now if it is not known yet: an unknown word
+// holds zero) or the context's slot `slot`, measured now.
+const unsigned* operand_amax(laya_ctx* ctx, AmaxRef r, int slot, const float* x, int rows, int cols, long ld) {
+    if (!r.word) return operand_absmax(ctx, slot, x, rows, cols, ld);
+    if (!*r.known) {
+        absmax_into(ctx, x, rows, cols, ld, r.word);
+        *r.known = 1;
+    }
+    return r.word;
+}
+
+// An NT product on 256-wide tiles (wide or tall) as two-piece fp16 products: both operands' magnitudes
+// are taken first (outside the product's profile scope) and the launchers below see amax_a set.
+void prepare_pair_nt(laya_ctx* ctx, GemmParams& p, AmaxRef ra, AmaxRef rb) {
+    p.amax_a = operand_amax(ctx, ra, 0, p.A, p.M, p.K, p.lda);
+    p.amax_b = operand_amax(ctx, rb, 1, p.B, p.N, p.K, p.ldb);
+}
+
 void launch_tall(laya_ctx* ctx, GemmParams p) {
-    profile_rename("gemm_nt_x6t");
     p.tiles_m = (p.M + TM - 1) / TM;
     p.tiles_n = (p.N + WT - 1) / WT;
     const dim3 g(p.tiles_m * p.tiles_n), b(WT_THREADS);
+    if (p.amax_a) {
+        profile_rename("gemm_nt_h2t");
+        if (p.mode == STORE_ROPE)
+            hipLaunchKernelGGL((gemm_x6t_kernel<STORE_ROPE, false, 2>), g, b, 0, ctx->stream, p);
+        else if (p.R)
+            hipLaunchKernelGGL((gemm_x6t_kernel<STORE, true, 2>), g, b, 0, ctx->stream, p);
+        else
+            hipLaunchKernelGGL((gemm_x6t_kernel<STORE, false, 2>), g, b, 0, ctx->stream, p);
+        check_launch("gemm_x6t_kernel");
+        return;
+    }
+    profile_rename("gemm_nt_x6t");
     if (p.mode == STORE_ROPE)
         hipLaunchKernelGGL((gemm_x6t_kernel<STORE_ROPE, false>), g, b, 0, ctx->stream, p);
     else if (p.R)
@@ -1963,9 +2206,18 @@ void launch_tall(laya_ctx* ctx, GemmParams p) {
 }
 
 void launch_wide(laya_ctx* ctx, GemmParams p) {
-    profile_rename("gemm_nt_x6w");
     p.tiles_n = (p.N + WT - 1) / WT;
     const dim3 g(((p.M + WT - 1) / WT) * p.tiles_n), b(WT_THREADS);
+    if (p.amax_a) {
+        profile_rename("gemm_nt_h2w");
+        if (p.mode == STORE_ROPE)
+            hipLaunchKernelGGL((gemm_x6w_kernel<STORE_ROPE, 2>), g, b, 0, ctx->stream, p);
+        else
+            hipLaunchKernelGGL((gemm_x6w_kernel<STORE, 2>), g, b, 0, ctx->stream, p);
+        check_launch("gemm_x6w_kernel");
+        return;
+    }
+    profile_rename("gemm_nt_x6w");
     if (p.mode == STORE_ROPE)
         hipLaunchKernelGGL((gemm_x6w_kernel<STORE_ROPE>), g, b, 0, ctx->stream, p);
     else
@@ -2154,7 +2406,7 @@ int fill_splits(const laya_ctx* ctx, int tiles, int K, int min_k) {
 
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
           const float* B, long ldb, float* C, long ldc, const float* bias, const float* R, long ldr,
-          const __bf16* A16, const __bf16* B16) {
+          const __bf16* A16, const __bf16* B16, AmaxRef amax_a, AmaxRef amax_b) {
     if (M == 0 || N == 0) return;
     GemmParams p = make_params(M, N, K, A, lda, B, ldb, C, ldc, bias, R, ldr);
     p.A16 = A16;
@@ -2174,6 +2426,11 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
         }
     }
     const int blocks = tiles * p.splits;
+    if (layout == GemmLayout::NT && (ctx->matmul_pair & 1) && !(ctx->matmul_bf16 & 1) && (ctx->matmul_split & 1) &&
+        gemm_fits_h(p, true, true) && operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K) &&
+        operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K) &&
+        (wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks)) || tall_tiles_pay(ctx, p)))
+        prepare_pair_nt(ctx, p, amax_a, amax_b);
     {
         static const char* names[3][3] = {{"gemm_nt", "gemm_nn", "gemm_tn"},
                                           {"gemm_nt_bf16", "gemm_nn_bf16", "gemm_tn_bf16"},
@@ -2200,7 +2457,7 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
 
 void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* B, float* C, const float* bias,
                const int* pos, const float* cos_t, const float* sin_t, int rope_cols, const __bf16* A16,
-               const __bf16* B16) {
+               const __bf16* B16, AmaxRef amax_a, AmaxRef amax_b) {
     if (M == 0 || N == 0) return;
     GemmParams p = make_params(M, N, K, A, K, B, K, C, N, bias, nullptr, 0);
     p.A16 = A16;
@@ -2224,6 +2481,8 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
         return;
     }
     if (ctx->matmul_split & 1) {
+        if ((ctx->matmul_pair & 1) && (wide_tiles_pay(ctx, p, false) || tall_tiles_pay(ctx, p)))
+            prepare_pair_nt(ctx, p, amax_a, amax_b);
         ProfileScope scope(ctx, "gemm_nt_x6", 2.0 * M * N * (double)K, 0.0);
         if (wide_tiles_pay(ctx, p, false)) {
             launch_wide(ctx, p);
@@ -2284,7 +2543,8 @@ bool make_pair_plan_wide(const laya_ctx* ctx, int n0, int out, int n1, int rows,
 
 // The wide pair for split products: dX without residual, dX's K a multiple of 16, dY k-contiguous in
 // float4s. Returns false (nothing launched) when the wide plan does not apply.
-bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out, bool half) {
+bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out, bool half,
+                        AmaxRef amax_dy, AmaxRef amax_W, AmaxRef amax_x) {
     const bool bh = half && nn.B16 && tn.B16;  // W and x from their bf16 copies
     if (out % BKQ != 0 || !operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) return false;
     const long lim = 1L << 31;  // buffer offsets of dY, W and x
@@ -2297,11 +2557,21 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
     PairPlan s{};
     if (!make_pair_plan_wide(ctx, n0, out, n1, rows, s)) return false;
     s.partial = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)s.G * 2 * WT * WT));
+    const bool pair = !half && (ctx->matmul_pair & 6) == 6;
+    if (pair) {
+        nn.amax_a = tn.amax_a = operand_amax(ctx, amax_dy, 0, nn.A, rows, out, nn.lda);
+        nn.amax_b = operand_amax(ctx, amax_W, 1, nn.B, out, in, nn.ldb);
+        tn.amax_b = operand_amax(ctx, amax_x, 2, tn.B, rows, in, tn.ldb);
+    }
     {
-        ProfileScope scope(ctx, half ? "gemm_bwd_pair_bf16w" : "gemm_bwd_pair_x6w",
+        ProfileScope scope(ctx, half ? "gemm_bwd_pair_bf16w" : pair ? "gemm_bwd_pair_h2w" : "gemm_bwd_pair_x6w",
                            2.0 * 2.0 * rows * (double)in * out, 0.0);
         const dim3 g(s.G), b(WT_THREADS);
-        if (bh && nn.R)
+        if (pair && nn.R)
+            hipLaunchKernelGGL((gemm_pair_wide_kernel<2, true>), g, b, 0, ctx->stream, nn, tn, s);
+        else if (pair)
+            hipLaunchKernelGGL((gemm_pair_wide_kernel<2, false>), g, b, 0, ctx->stream, nn, tn, s);
+        else if (bh && nn.R)
             hipLaunchKernelGGL((gemm_pair_wide_kernel<1, true, true>), g, b, 0, ctx->stream, nn, tn, s);
         else if (bh)
             hipLaunchKernelGGL((gemm_pair_wide_kernel<1, false, true>), g, b, 0, ctx->stream, nn, tn, s);
@@ -2335,7 +2605,8 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
 }
 
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
-                        float* dx, const float* dx_residual, float* dW, const __bf16* W16, const __bf16* x16) {
+                        float* dx, const float* dx_residual, float* dW, const __bf16* W16, const __bf16* x16,
+                        AmaxRef amax_dy, AmaxRef amax_W, AmaxRef amax_x) {
     if (rows == 0) return;
     // dx[rows, in] = dy[rows, out] · W[out, in]       (NN, K = out)
     GemmParams nn = make_params(rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual, in);
@@ -2350,7 +2621,7 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
                       gemm_fast(tn, false, false);
     const bool half = (ctx->matmul_bf16 & 6) == 6 && gemm_fits_h(nn, true, false) && gemm_fits_h(tn, false, false);
     tn.mode = ACCUMULATE;
-    if ((split || half) && backward_pair_wide(ctx, nn, tn, rows, in, out, half)) return;
+    if ((split || half) && backward_pair_wide(ctx, nn, tn, rows, in, out, half, amax_dy, amax_W, amax_x)) return;
     tn.mode = STORE;
     const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
     PairPlan s{};

@@ -182,6 +182,31 @@ struct laya_model {
     bool coef_valid = false;
     bool norm_done = false;  // a gradient norm has been computed (d_nonfinite holds its flag)
 
+    // max|operand| words of the two-piece fp16 products: one per parameter, one per product site for its
+    // input (four per encoder layer: the QKV, Wo, Wi and MLP-output inputs; four per head layer; two for
+    // the scorer), and one per site for its output gradient; the host flags say which hold the current
+    // values. The weight and input words are cleared at each forward (a weight is measured once per step,
+    // an input once per forward and reused by its backward product), the gradient words at each backward.
+    unsigned* amax_words = nullptr;
+    std::vector<unsigned char> amax_known;
+    size_t amax_sites() const { return (size_t)scorer_site(2); }
+    laya::AmaxRef word(size_t k) {
+        return amax_words ? laya::AmaxRef{amax_words + k * laya::AMAX_SPREAD, &amax_known[k]} : laya::AmaxRef{};
+    }
+    laya::AmaxRef wref(int i) { return i < 0 ? laya::AmaxRef{} : word(i); }
+    laya::AmaxRef aref(int site) { return word(params.size() + site); }
+    laya::AmaxRef dref(int site) { return word(params.size() + amax_sites() + site); }
+    // The word a producing kernel folds its output into, when a product of the classes `bits` will read it
+    // as two-piece products (else null: no fold); the word counts as measured from then on.
+    unsigned* produce(laya::AmaxRef r, int bits) {
+        if (!r.word || !(ctx->matmul_pair & bits)) return nullptr;
+        *r.known = 1;
+        return r.word;
+    }
+    int enc_site(int l, int k) const { return 4 * l + k; }
+    int head_site(int j, int k) const { return 4 * cfg.layers + 4 * j + k; }
+    int scorer_site(int k) const { return 4 * cfg.layers + 4 * cfg.head_layers + k; }
+
     // ----- the batch of the last forward
     bool has_tape = false, training = false;
     uint64_t seed = 0;
@@ -425,6 +450,16 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     m->cap_segs = Sc;
 }
 
+// After a host write of the weights: the bf16 copy is stale, and so are the weights' magnitude words
+// (cleared, to be measured again by the next product that reads them).
+void weights_changed(laya_model* m) {
+    m->wb_fresh = false;
+    if (m->amax_words) {
+        fill(m->ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_SPREAD * m->params.size());
+        std::fill(m->amax_known.begin(), m->amax_known.begin() + m->params.size(), 0);
+    }
+}
+
 // The weights' bf16 copy, when the products read copies: allocated on first use, refreshed from the fp32
 // masters when a host write or an update without it left it stale.
 void ensure_mirror(laya_model* m) {
@@ -588,19 +623,22 @@ AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p
     return a;
 }
 
-// x16: x's bf16 copy, or null.
+// x16: x's bf16 copy, or null; ax: x's magnitude word.
 void linear(laya_model* m, const float* x, int rows, int in, int wi, int bi, int out, const float* residual, float* y,
-            const __bf16* x16 = nullptr) {
+            const __bf16* x16 = nullptr, AmaxRef ax = {}) {
     gemm(m->ctx, GemmLayout::NT, GemmEpilogue::Store, rows, out, in, x, in, m->W(wi), in, y, out, m->W(bi), residual,
-         out, x16, m->W16(wi));
+         out, x16, m->W16(wi), ax, m->wref(wi));
 }
 
 // Ops.LinearBackward (Ops.cs:33-69): dx = dy·W (overwrite; + residual when given), dW += dyᵀ·x, db += Σ dy.
+// site: the product's magnitude-word site (its input's word and its output gradient's), or -1.
 void linear_backward(laya_model* m, const float* x, const float* dy, int rows, int in, int out, int wi, int bi,
-                     float* dx, const float* dx_residual = nullptr, const __bf16* x16 = nullptr) {
+                     float* dx, const float* dx_residual = nullptr, const __bf16* x16 = nullptr, int site = -1) {
     float* dW = m->Gt(wi);
     if (dx && dW) {
-        gemm_backward_pair(m->ctx, rows, in, out, dy, m->W(wi), x, dx, dx_residual, dW, m->W16(wi), x16);
+        gemm_backward_pair(m->ctx, rows, in, out, dy, m->W(wi), x, dx, dx_residual, dW, m->W16(wi), x16,
+                           site >= 0 ? m->dref(site) : AmaxRef{}, m->wref(wi),
+                           site >= 0 ? m->aref(site) : AmaxRef{});
     } else if (dx) {
         gemm(m->ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, m->W(wi), in, dx, in, nullptr,
              dx_residual, in, nullptr, m->W16(wi));
@@ -628,9 +666,10 @@ void encoder_forward(laya_model* m, int l, bool output = true) {
     auto& a = m->ea[l];
     float* out = l + 1 < m->cfg.layers ? m->ea[l + 1].x : m->x_final;
     const float* normed = a.x;
+    // The products' inputs fold their magnitudes in as they are written (forward NT and backward pair).
     if (L.attn_norm >= 0) {
         layernorm_fwd(ctx, a.x, T, d, m->W(L.attn_norm), m->W(L.attn_norm_b), eps, a.normed, a.mean1, a.rstd1,
-                      nullptr, nullptr, nullptr, a.normed16);
+                      nullptr, nullptr, nullptr, a.normed16, m->produce(m->aref(m->enc_site(l, 0)), 7));
         normed = a.normed;
     } else if (a.normed16) {
         to_bf16(ctx, a.x, (size_t)T * d, a.normed16);  // nn.Identity: the QKV input is x itself
@@ -638,17 +677,19 @@ void encoder_forward(laya_model* m, int l, bool output = true) {
     if (fused_rope(m)) {
         const laya_rotary& r = L.kind == 0 ? m->rot_global : m->rot_local;
         gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->cur.pos, r.cos_t, r.sin_t,
-                  2 * d, a.normed16, m->W16(L.wqkv));
+                  2 * d, a.normed16, m->W16(L.wqkv), m->aref(m->enc_site(l, 0)), m->wref(L.wqkv));
     } else {
-        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv, a.normed16);
+        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv, a.normed16, m->aref(m->enc_site(l, 0)));
     }
-    attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse, a.ctx16);
-    linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res, a.ctx16);  // x1 = x + attn
+    attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse, a.ctx16,
+                  m->produce(m->aref(m->enc_site(l, 1)), 7));
+    linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res, a.ctx16, m->aref(m->enc_site(l, 1)));  // x1 = x + attn
     layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2, nullptr,
-                  nullptr, nullptr, a.mlpn16);
-    linear(m, a.mlpn, T, d, L.wi, L.wi_b, 2 * I, nullptr, a.wide, a.mlpn16);
-    geglu_fwd(ctx, a.wide, T, I, a.act, a.act16);
-    if (output) linear(m, a.act, T, I, L.mlp_wo, L.mlp_wo_b, d, a.res, out, a.act16);  // x2 = x1 + mlp
+                  nullptr, nullptr, a.mlpn16, m->produce(m->aref(m->enc_site(l, 2)), 7));
+    linear(m, a.mlpn, T, d, L.wi, L.wi_b, 2 * I, nullptr, a.wide, a.mlpn16, m->aref(m->enc_site(l, 2)));
+    geglu_fwd(ctx, a.wide, T, I, a.act, a.act16, m->produce(m->aref(m->enc_site(l, 3)), 7));
+    if (output)  // x2 = x1 + mlp
+        linear(m, a.act, T, I, L.mlp_wo, L.mlp_wo_b, d, a.res, out, a.act16, m->aref(m->enc_site(l, 3)));
 }
 
 void forward(laya_model* m, bool train, uint64_t seed) {
@@ -658,11 +699,22 @@ void forward(laya_model* m, bool train, uint64_t seed) {
     m->training = train;
     m->seed = seed;
     ensure_mirror(m);
+    if (!m->amax_words) {
+        const size_t n = m->params.size() + 2 * m->amax_sites();
+        m->amax_words = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_SPREAD * n));
+        m->amax_known.assign(n, 0);
+    }
+    const size_t nw = m->params.size() + m->amax_sites();  // weight and input words (+0.0f: all-zero bits)
+    fill(ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_SPREAD * nw);
+    std::fill(m->amax_known.begin(), m->amax_known.begin() + nw, 0);
 
     // Embedding gather fused into the embedding LayerNorm.
     float* x0 = m->cfg.layers > 0 ? m->ea[0].x : m->x_final;
+    // Layer 0's QKV input is x itself when it has no attention norm.
+    unsigned* x0_amax =
+        m->cfg.layers > 0 && m->enc[0].attn_norm < 0 ? m->produce(m->aref(m->enc_site(0, 0)), 7) : nullptr;
     layernorm_fwd(ctx, m->W(m->tok_emb), T, d, m->W(m->emb_norm), m->W(m->emb_norm_b), eps, x0, m->emb_mean,
-                  m->emb_rstd, m->cur.tokens);
+                  m->emb_rstd, m->cur.tokens, nullptr, nullptr, nullptr, x0_amax);
     for (int l = 0; l < m->cfg.layers; ++l) encoder_forward(m, l);
     // Final norm, then each question's type vector on its rows (TrainableDecisionModel.cs:294-304).
     float* h0 = m->cfg.head_layers > 0 ? m->ha[0].x : m->head_out;
@@ -674,41 +726,42 @@ void forward(laya_model* m, bool train, uint64_t seed) {
         auto& a = m->ha[j];
         float* out = j + 1 < m->cfg.head_layers ? m->ha[j + 1].x : m->head_out;
         layernorm_fwd(ctx, a.x, T, d, m->W(H.norm1), m->W(H.norm1_b), 1e-5f, a.n1, a.mean1, a.rstd1, nullptr,
-                      nullptr, nullptr, a.n1_16);
-        linear(m, a.n1, T, d, H.in_proj, H.in_proj_b, 3 * d, nullptr, a.qkv, a.n1_16);
-        attention_fwd(ctx, head_attention(m, a.qkv, j, p, seed), a.ctx, a.lse, a.ctx16);
+                      nullptr, nullptr, a.n1_16, m->produce(m->aref(m->head_site(j, 0)), 7));
+        linear(m, a.n1, T, d, H.in_proj, H.in_proj_b, 3 * d, nullptr, a.qkv, a.n1_16, m->aref(m->head_site(j, 0)));
+        attention_fwd(ctx, head_attention(m, a.qkv, j, p, seed), a.ctx, a.lse, a.ctx16,
+                      m->produce(m->aref(m->head_site(j, 1)), 7));
         if (p > 0.0f) {
-            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, nullptr, a.res, a.ctx16);
+            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, nullptr, a.res, a.ctx16, m->aref(m->head_site(j, 1)));
             dropout(ctx, a.res, (size_t)T * d, p, salt(seed, j, 1));
             add(ctx, a.res, a.x, (size_t)T * d);
         } else {
-            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, a.x, a.res, a.ctx16);
+            linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, a.x, a.res, a.ctx16, m->aref(m->head_site(j, 1)));
         }
         layernorm_fwd(ctx, a.res, T, d, m->W(H.norm2), m->W(H.norm2_b), 1e-5f, a.n2, a.mean2, a.rstd2, nullptr,
-                      nullptr, nullptr, a.n2_16);
-        linear(m, a.n2, T, d, H.linear1, H.linear1_b, ff, nullptr, a.wide, a.n2_16);
+                      nullptr, nullptr, a.n2_16, m->produce(m->aref(m->head_site(j, 2)), 7));
+        linear(m, a.n2, T, d, H.linear1, H.linear1_b, ff, nullptr, a.wide, a.n2_16, m->aref(m->head_site(j, 2)));
         relu_dropout_fwd(ctx, a.wide, (size_t)T * ff, p, salt(seed, j, 2), a.drop, a.drop16);
         if (p > 0.0f) {
-            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, nullptr, out, a.drop16);
+            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, nullptr, out, a.drop16, m->aref(m->head_site(j, 3)));
             dropout(ctx, out, (size_t)T * d, p, salt(seed, j, 3));
             add(ctx, out, a.res, (size_t)T * d);
         } else {
-            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, a.res, out, a.drop16);
+            linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, a.res, out, a.drop16, m->aref(m->head_site(j, 3)));
         }
     }
     // Scorer at the option markers (TrainableDecisionModel.cs:313-323).
     const int M = m->nmark;
     gather_rows(ctx, m->head_out, m->cur.marker_rows, M, d, m->s_in);
     layernorm_fwd(ctx, m->s_in, M, d, m->W(m->sc_norm), m->W(m->sc_norm_b), 1e-5f, m->s_norm, m->s_mean, m->s_rstd);
-    linear(m, m->s_norm, M, d, m->sc1, m->sc1_b, d, nullptr, m->s_pre);
+    linear(m, m->s_norm, M, d, m->sc1, m->sc1_b, d, nullptr, m->s_pre, nullptr, m->aref(m->scorer_site(0)));
     gelu_fwd(ctx, m->s_pre, (size_t)M * d, m->s_act);
-    linear(m, m->s_act, M, d, m->sc2, m->sc2_b, 1, nullptr, m->scores);
+    linear(m, m->s_act, M, d, m->sc2, m->sc2_b, 1, nullptr, m->scores, nullptr, m->aref(m->scorer_site(1)));
     m->has_tape = true;
 }
 
 // Ops.LayerNormBackward with its dγ/dβ reduction deferred to the end of the backward.
 void ln_backward(laya_model* m, const float* x, int rows, int n, int w, int b, float eps, const float* dy, float* dx,
-                 const float* mean, const float* rstd, const int* gather_ids = nullptr) {
+                 const float* mean, const float* rstd, const int* gather_ids = nullptr, unsigned* amax = nullptr) {
     float* dg = m->Gt(w);
     float* db = m->Gt(b);
     float* ws = nullptr;
@@ -719,7 +772,7 @@ void ln_backward(laya_model* m, const float* x, int rows, int n, int w, int b, f
         m->ln_part_used += (need + 63) / 64 * 64;
     }
     layernorm_bwd_deferred(m->ctx, x, rows, n, m->W(w), eps, dy, dx, dg, db, mean, rstd, gather_ids,
-                           ws ? ws : m->ln_part, m->ln_jobs);
+                           ws ? ws : m->ln_part, m->ln_jobs, amax);
 }
 
 // EncoderLayerBackward (TrainableDecisionModel.cs:551-603); dS holds dOutput and becomes dx.
@@ -729,23 +782,29 @@ void encoder_backward(laya_model* m, int l, bool need_input) {
     auto& a = m->ea[l];
     const int T = m->T, d = m->d(), I = m->I();
     const float eps = m->cfg.norm_eps;
-    linear_backward(m, a.act, m->dS, T, I, d, L.mlp_wo, L.mlp_wo_b, m->dact, nullptr, a.act16);
-    geglu_bwd(ctx, a.wide, m->dact, T, I, m->dwide);
-    linear_backward(m, a.mlpn, m->dwide, T, d, 2 * I, L.wi, L.wi_b, m->dn, nullptr, a.mlpn16);
-    ln_backward(m, a.res, T, d, L.mlp_norm, L.mlp_norm_b, eps, m->dn, m->dS, a.mean2, a.rstd2);
-    linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx, nullptr, a.ctx16);
-    attention_bwd(ctx, enc_attention(m, a.qkv, L.kind), T, a.ctx, a.lse, m->dctx, m->dqkv);
+    linear_backward(m, a.act, m->dS, T, I, d, L.mlp_wo, L.mlp_wo_b, m->dact, nullptr, a.act16, m->enc_site(l, 3));
+    // The products' output gradients fold their magnitudes in as they are written (backward pairs).
+    geglu_bwd(ctx, a.wide, m->dact, T, I, m->dwide, m->produce(m->dref(m->enc_site(l, 2)), 6));
+    linear_backward(m, a.mlpn, m->dwide, T, d, 2 * I, L.wi, L.wi_b, m->dn, nullptr, a.mlpn16, m->enc_site(l, 2));
+    ln_backward(m, a.res, T, d, L.mlp_norm, L.mlp_norm_b, eps, m->dn, m->dS, a.mean2, a.rstd2, nullptr,
+                m->produce(m->dref(m->enc_site(l, 1)), 6));
+    linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx, nullptr, a.ctx16, m->enc_site(l, 1));
+    attention_bwd(ctx, enc_attention(m, a.qkv, L.kind), T, a.ctx, a.lse, m->dctx, m->dqkv,
+                  m->produce(m->dref(m->enc_site(l, 0)), 6));
     const float* normed = L.attn_norm >= 0 ? a.normed : a.x;
+    const int an = m->enc_site(l, 0);
     if (!need_input) {
-        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, nullptr, nullptr, a.normed16);
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, nullptr, nullptr, a.normed16, an);
         return;
     }
     if (L.attn_norm < 0) {
         // Layer 0: nn.Identity, so dx = dResidual + dNormed, fused as the GEMM's residual.
-        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dS, m->dS, a.normed16);
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dS, m->dS, a.normed16, an);
     } else {
-        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dn, nullptr, a.normed16);
-        ln_backward(m, a.x, T, d, L.attn_norm, L.attn_norm_b, eps, m->dn, m->dS, a.mean1, a.rstd1);
+        linear_backward(m, normed, m->dqkv, T, d, 3 * d, L.wqkv, L.wqkv_b, m->dn, nullptr, a.normed16, an);
+        // dS is now the output gradient of layer l − 1, the input of its MLP output product's backward.
+        ln_backward(m, a.x, T, d, L.attn_norm, L.attn_norm_b, eps, m->dn, m->dS, a.mean1, a.rstd1, nullptr,
+                    l > 0 ? m->produce(m->dref(m->enc_site(l - 1, 3)), 6) : nullptr);
     }
 }
 
@@ -762,21 +821,25 @@ void head_backward(laya_model* m, int j) {
         dropout_copy(m, m->dS, m->dy, nd, p, salt(m->seed, j, 3));
         dy = m->dy;
     }
-    linear_backward(m, a.drop, dy, T, ff, d, H.linear2, H.linear2_b, m->dact, nullptr, a.drop16);
+    linear_backward(m, a.drop, dy, T, ff, d, H.linear2, H.linear2_b, m->dact, nullptr, a.drop16,
+                    m->head_site(j, 3));
     if (ff % 4 == 0)
         relu_dropout_bwd_from_output(ctx, a.drop, m->dact, (size_t)T * ff, p);
     else
         relu_dropout_bwd(ctx, a.wide, m->dact, (size_t)T * ff, p, salt(m->seed, j, 2));
-    linear_backward(m, a.n2, m->dact, T, d, ff, H.linear1, H.linear1_b, m->dn, nullptr, a.n2_16);
+    linear_backward(m, a.n2, m->dact, T, d, ff, H.linear1, H.linear1_b, m->dn, nullptr, a.n2_16,
+                    m->head_site(j, 2));
     ln_backward(m, a.res, T, d, H.norm2, H.norm2_b, 1e-5f, m->dn, m->dS, a.mean2, a.rstd2);
     const float* datt = m->dS;
     if (p > 0.0f) {
         dropout_copy(m, m->dS, m->dy, nd, p, salt(m->seed, j, 1));
         datt = m->dy;
     }
-    linear_backward(m, a.ctx, datt, T, d, d, H.out_proj, H.out_proj_b, m->dctx, nullptr, a.ctx16);
+    linear_backward(m, a.ctx, datt, T, d, d, H.out_proj, H.out_proj_b, m->dctx, nullptr, a.ctx16,
+                    m->head_site(j, 1));
     attention_bwd(ctx, head_attention(m, a.qkv, j, p, m->seed), T, a.ctx, a.lse, m->dctx, m->dqkv);
-    linear_backward(m, a.n1, m->dqkv, T, d, 3 * d, H.in_proj, H.in_proj_b, m->dn, nullptr, a.n1_16);
+    linear_backward(m, a.n1, m->dqkv, T, d, 3 * d, H.in_proj, H.in_proj_b, m->dn, nullptr, a.n1_16,
+                    m->head_site(j, 0));
     ln_backward(m, a.x, T, d, H.norm1, H.norm1_b, 1e-5f, m->dn, m->dS, a.mean1, a.rstd1);
 }
 
@@ -800,6 +863,11 @@ void backward(laya_model* m) {
     }
     m->ln_part_used = 0;
     m->ln_jobs.n = 0;
+    if (m->amax_words) {
+        const size_t k = m->params.size() + m->amax_sites();
+        fill(m->ctx, reinterpret_cast<float*>(m->amax_words + AMAX_SPREAD * k), 0.0f, AMAX_SPREAD * m->amax_sites());
+        std::fill(m->amax_known.begin() + k, m->amax_known.end(), 0);
+    }
     backward_body(m);
     column_reduce_batch(m->ctx, m->ln_jobs);
     m->ln_jobs.n = 0;
@@ -809,9 +877,11 @@ void backward_body(laya_model* m) {
     laya_ctx* ctx = m->ctx;
     const int T = m->T, d = m->d(), M = m->nmark;
     const float eps = m->cfg.norm_eps;
-    linear_backward(m, m->s_act, m->ds_scores, M, d, 1, m->sc2, m->sc2_b, m->ds_act);
+    linear_backward(m, m->s_act, m->ds_scores, M, d, 1, m->sc2, m->sc2_b, m->ds_act, nullptr, nullptr,
+                    m->scorer_site(1));
     gelu_bwd(ctx, m->s_pre, m->ds_act, (size_t)M * d);
-    linear_backward(m, m->s_norm, m->ds_act, M, d, d, m->sc1, m->sc1_b, m->ds_norm);
+    linear_backward(m, m->s_norm, m->ds_act, M, d, d, m->sc1, m->sc1_b, m->ds_norm, nullptr, nullptr,
+                    m->scorer_site(0));
     fill(ctx, m->ds_mark, 0.0f, (size_t)M * d);
     ln_backward(m, m->s_in, M, d, m->sc_norm, m->sc_norm_b, 1e-5f, m->ds_norm, m->ds_mark, m->s_mean, m->s_rstd);
     fill(ctx, m->dS, 0.0f, (size_t)T * d);
@@ -821,7 +891,8 @@ void backward_body(laya_model* m) {
         type_embedding_bwd(ctx, m->dS, m->cur.row_type, T, d, g);
     if (m->first_trainable >= m->cfg.layers) return;  // the encoder is frozen
     fill(ctx, m->dE, 0.0f, (size_t)T * d);
-    ln_backward(m, m->x_final, T, d, m->final_norm, m->final_norm_b, eps, m->dS, m->dE, m->fin_mean, m->fin_rstd);
+    ln_backward(m, m->x_final, T, d, m->final_norm, m->final_norm_b, eps, m->dS, m->dE, m->fin_mean, m->fin_rstd,
+                nullptr, m->cfg.layers > 0 ? m->produce(m->dref(m->enc_site(m->cfg.layers - 1, 3)), 6) : nullptr);
     std::swap(m->dS, m->dE);
     for (int l = m->cfg.layers - 1; l >= m->first_trainable; --l) {
         // Layer checkpointing: the layer's internals are recomputed from its kept input (the same kernels on
@@ -945,7 +1016,8 @@ int laya_model_destroy(laya_model* m) {
             if (p) ctx->release(p);
         for (auto& s : m->staged)
             if (s.block) ctx->release(s.block);
-        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part, (void*)m->WB})
+        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part, (void*)m->WB,
+                        (void*)m->amax_words})
             if (p) ctx->release(p);
         free_rotary(ctx, &m->rot_global);
         free_rotary(ctx, &m->rot_local);
@@ -988,8 +1060,8 @@ int laya_model_set_param(laya_model* m, int i, const float* host) {
         LAYA_REQUIRE(i >= 0 && i < (int)m->params.size() && host, "set_param: bad argument");
         const Param& p = m->params[i];
         LAYA_HIP(hipMemcpyAsync(m->P + p.offset, host, p.numel * sizeof(float), hipMemcpyHostToDevice, m->ctx->stream));
+        weights_changed(m);
         LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
-        m->wb_fresh = false;
     });
 }
 
@@ -1027,8 +1099,8 @@ int laya_model_init_random(laya_model* m, uint64_t seed, float std) {
             const Param& p = m->params[i];
             init_param(m->ctx, m->P + p.offset, p.numel, p.init, std, mix64(seed, (uint64_t)i + 1));
         }
+        weights_changed(m);
         LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
-        m->wb_fresh = false;
     });
 }
 

@@ -23,16 +23,15 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 __device__ __forceinline__ void st4(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 
+// One wave's row of the forward; returns max|y| over the lane's elements (amax_bits).
 template <int NCH>
-__global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x, int rows, int n,
-                                                     const float* __restrict__ w, const float* __restrict__ b,
-                                                     float eps, float* __restrict__ y, float* __restrict__ mean_out,
-                                                     float* __restrict__ rstd_out, const int* __restrict__ gather_ids,
-                                                     int gather_rows, const float* __restrict__ add_table,
-                                                     const int* __restrict__ add_index, __bf16* __restrict__ y16) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
+__device__ __forceinline__ unsigned ln_fwd_row(const float* __restrict__ x, int row, int lane, int n,
+                                               const float* __restrict__ w, const float* __restrict__ b, float eps,
+                                               float* __restrict__ y, float* __restrict__ mean_out,
+                                               float* __restrict__ rstd_out, const int* __restrict__ gather_ids,
+                                               int gather_rows, const float* __restrict__ add_table,
+                                               const int* __restrict__ add_index, __bf16* __restrict__ y16) {
+    unsigned m = 0;
     const float* src = x + (long)row * n;
     bool zero = false;
     if (gather_ids) {
@@ -78,12 +77,31 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
             if (add) o += aw[c];
             st4(y + (long)row * n + col, o);
             if (y16) *reinterpret_cast<bf16x4*>(y16 + (long)row * n + col) = __builtin_convertvector(o, bf16x4);
+            m = max(m, amax_bits4(o));
         }
     }
     if (lane == 0) {
         if (mean_out) mean_out[row] = mean;
         if (rstd_out) rstd_out[row] = rstd;
     }
+    return m;
+}
+
+// Four rows per block, one wave each; amax (optional): max|y| folded in (the output's magnitude word).
+template <int NCH>
+__global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x, int rows, int n,
+                                                     const float* __restrict__ w, const float* __restrict__ b,
+                                                     float eps, float* __restrict__ y, float* __restrict__ mean_out,
+                                                     float* __restrict__ rstd_out, const int* __restrict__ gather_ids,
+                                                     int gather_rows, const float* __restrict__ add_table,
+                                                     const int* __restrict__ add_index, __bf16* __restrict__ y16,
+                                                     unsigned* amax) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const unsigned m = row < rows ? ln_fwd_row<NCH>(x, row, lane, n, w, b, eps, y, mean_out, rstd_out, gather_ids,
+                                                    gather_rows, add_table, add_index, y16)
+                                  : 0u;
+    block_amax_fold(m, amax);
 }
 
 // One row's operands for the backward: x (gathered when ids are given), dy, and the dx it adds into.
@@ -117,7 +135,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x
                                                      const float* __restrict__ rstd_in,
                                                      const int* __restrict__ gather_ids, int gather_rows,
                                                      int total_waves, float* __restrict__ part_g,
-                                                     float* __restrict__ part_b) {
+                                                     float* __restrict__ part_b, unsigned* amax) {
     // total_waves is a multiple of 4 (whole blocks); a wave past the last row only adds zeros.
     constexpr bool PIPE = NCH <= 4;
     const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -131,6 +149,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x
         gm[c] = col < n ? ld4(w + col) : f32x4{0, 0, 0, 0};
     }
     const float inv_n = 1.0f / (float)n;
+    unsigned am = 0;  // max|dx| (amax_bits) of the lane's elements
     f32x4 xv[NCH], gv[NCH], dv[NCH];
     if (PIPE && wave < rows) ln_bwd_load<NCH>(x, dy, dx, wave, n, lane, gather_ids, gather_rows, xv, gv, dv);
     for (int row = wave; row < rows; row += total_waves) {
@@ -184,7 +203,9 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x
             const int col = (c * 64 + lane) * 4;
             if (col < n) {
                 const f32x4 xh = (xv[c] - mean) * rstd;
-                st4(dx + (long)row * n + col, dv[c] + rstd * (gv[c] * gm[c] - mg - xh * mgx));
+                const f32x4 o = dv[c] + rstd * (gv[c] * gm[c] - mg - xh * mgx);
+                st4(dx + (long)row * n + col, o);
+                am = max(am, amax_bits4(o));
             }
         }
         if (PIPE) {
@@ -196,6 +217,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ x
             }
         }
     }
+    block_amax_fold(am, amax);
     // The block's 4 waves combine their dγ/dβ partials in LDS (in wave order): one partial per block.
     if (!part_g && !part_b) return;
     extern __shared__ __attribute__((aligned(16))) float red[];  // [2][4][n]
@@ -254,7 +276,7 @@ int chunks_for(int n) {
 
 void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps, float* y,
                    float* mean, float* rstd, const int* gather_ids, const float* add_table, const int* add_index,
-                   __bf16* y16) {
+                   __bf16* y16, unsigned* amax) {
     if (rows <= 0) return;
     const int nch = chunks_for(n);
     // With gather_ids, x is a table of `gather_rows` rows; the caller validates ids on the host.
@@ -264,7 +286,7 @@ void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
 #define LN_FWD(C)                                                                                                 \
     case C:                                                                                                       \
         hipLaunchKernelGGL(ln_fwd_kernel<C>, grid, block, 0, ctx->stream, x, rows, n, w, b, eps, y, mean, rstd, \
-                           gather_ids, gather_rows, add_table, add_index, y16);                                  \
+                           gather_ids, gather_rows, add_table, add_index, y16, amax);                            \
         break;
     switch (nch) { LN_FWD(1) LN_FWD(2) LN_FWD(3) LN_FWD(4) LN_FWD(5) LN_FWD(6) LN_FWD(7) LN_FWD(8) }
 #undef LN_FWD
@@ -276,7 +298,7 @@ void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
 static void layernorm_bwd_impl(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
                                const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
                                const float* rstd, const int* gather_ids, float* ws, bool profile,
-                               ColumnSumJobs* defer = nullptr) {
+                               ColumnSumJobs* defer = nullptr, unsigned* amax = nullptr) {
     if (rows <= 0) return;
     const int nch = chunks_for(n);
     const int gather_rows = gather_ids ? INT32_MAX : 0;
@@ -298,7 +320,7 @@ static void layernorm_bwd_impl(laya_ctx* ctx, const float* x, int rows, int n, c
 #define LN_BWD(C)                                                                                                \
     case C:                                                                                                      \
         hipLaunchKernelGGL(ln_bwd_kernel<C>, grid, block, lds, ctx->stream, x, rows, n, w, eps, dy, dx, mean,  \
-                           rstd, gather_ids, gather_rows, waves, pg, pb);                                        \
+                           rstd, gather_ids, gather_rows, waves, pg, pb, amax);                                  \
         break;
         switch (nch) { LN_BWD(1) LN_BWD(2) LN_BWD(3) LN_BWD(4) LN_BWD(5) LN_BWD(6) LN_BWD(7) LN_BWD(8) }
 #undef LN_BWD
@@ -345,9 +367,11 @@ int ln_bwd_partial_rows(int rows) { return ln_bwd_blocks(std::max(rows, 1)); }
 
 void layernorm_bwd_deferred(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps,
                             const float* dy, float* dx, float* dgamma, float* dbeta, const float* mean,
-                            const float* rstd, const int* gather_ids, float* ws, ColumnSumJobs& jobs) {
+                            const float* rstd, const int* gather_ids, float* ws, ColumnSumJobs& jobs,
+                            unsigned* amax) {
     LAYA_REQUIRE(ws != nullptr, "layernorm_bwd_deferred: no partial buffer");
-    layernorm_bwd_impl(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, gather_ids, ws, true, &jobs);
+    layernorm_bwd_impl(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, gather_ids, ws, true, &jobs,
+                       amax);
 }
 
 // ------------------------------------------------------------------ the allocation-free variant

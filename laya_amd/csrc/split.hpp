@@ -11,6 +11,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 namespace laya {
 
@@ -34,5 +36,25 @@ __device__ __forceinline__ void split3_4(f32x4 x, bf16x4& h1, bf16x4& h2, bf16x4
     h2 = __builtin_bit_cast(bf16x4, (u32x2{b01, b23}));
     h3 = __builtin_bit_cast(bf16x4, (u32x2{c01, c23}));
 }
+
+// Two-piece fp16 split of s·x, s a power of two that brings the operand's largest magnitude into
+// [2¹⁴, 2¹⁵): hi = f16(s·x) to nearest even, lo = f16(s·x − hi) (the remainder is exact in fp32, one
+// fused mix-precision subtract). hi + lo holds s·x to 2⁻²² of its magnitude for every element above
+// 2⁻¹⁸ of the operand's largest, and to 2⁻⁴⁰ of the largest below that. A product a·b accumulated in
+// fp32 from the three piece products alo·bhi, ahi·blo, ahi·bhi (the dropped alo·blo is below 2⁻²² of
+// the product) is within a few 2⁻²⁴ of the exact product, under the fp32 accumulation's own rounding.
+__device__ __forceinline__ void split2h_4(f32x4 x, float s, f16x4& hi, f16x4& lo) {
+    const f32x4 v = x * s;
+    hi = __builtin_convertvector(v, f16x4);
+    lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x4), f16x4);
+}
+
+// The scale exponent of an operand whose largest finite magnitude has the fp32 bit pattern `amax`:
+// s = 2^e with e = 14 − exponent(amax), clamped to [−126, 126] (an all-zero operand takes 2¹²⁶).
+__device__ __forceinline__ int pair_scale_exp(unsigned amax) {
+    const int e = 14 - ((int)(amax >> 23) - 127);
+    return e < -126 ? -126 : e > 126 ? 126 : e;
+}
+__device__ __forceinline__ float exp2_int(int e) { return __builtin_bit_cast(float, (unsigned)(e + 127) << 23); }
 
 }  // namespace laya

@@ -38,13 +38,23 @@ def mixed_batch(rng, lengths, vocab, options=(8, 4, 2)):
 def fixture_params(shapes: dict, seed: int, std: float = 0.02) -> dict:
     """Parameters of the full-size parity fixtures: each tensor from its own generator keyed by (seed, name),
     so the draw does not depend on the order the shapes are listed in. Norm weights and the scorer's norm
-    1 + 0.2·N(0,1) (so γ errors show), biases and the rest std·N(0,1), temperature 1."""
+    1 + 0.2·N(0,1) (so γ errors show), biases and the rest std·N(0,1), temperature 1.
+
+    The head's linear1 biases are ±5 × the RMS of their product (random sign per unit) instead: the
+    head's ReLU is the model's one discontinuity, and with ~10⁸ of its inputs drawn around zero a few lie
+    within fp32 rounding of it, so any two fp32 implementations may put one on different sides and move
+    every gradient below it by ~1e-4 (measured: one such unit moved head layer 1's gradients by 3e-4
+    between two fp32 GPU paths that agree to 1e-5 on other dropout seeds and to 3e-6 with the biases
+    moved). Away from zero the step is smooth, and the ReLU still masks about half the units."""
     import zlib
     out = {}
     for name, shape in shapes.items():
         rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
         if name == "temperature":
             out[name] = np.ones(shape, np.float32)
+        elif name.startswith("head.layers.") and name.endswith(".linear1.bias"):
+            fan_in = shapes[name[:-len("bias")] + "weight"][1]
+            out[name] = (5.0 * std * np.sqrt(fan_in) * rng.choice([-1.0, 1.0], shape)).astype(np.float32)
         elif len(shape) == 1 and "norm" in name and name.endswith("weight") or name.startswith("scorer.0.weight"):
             out[name] = (1.0 + 0.2 * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
         else:

@@ -40,9 +40,16 @@ def ctx():
     c.close()
 
 
-def _step(ctx, workload):
+# The 256-wide kernels each fp32 policy runs: two-piece fp16 products (the default) or three-piece bf16
+# splits everywhere.
+KERNELS = {"fp32": ("gemm_bwd_pair_h2w", "gemm_nt_h2w", "gemm_nt_h2t"),
+           "fp32-split3": ("gemm_bwd_pair_x6w", "gemm_nt_x6w", "gemm_nt_x6t")}
+
+
+def _step(ctx, workload, policy="fp32"):
     from laya_amd.config import modernbert_base
     from laya_amd.model import TrainableDecisionModel
+    ctx.set_matmul_precision(policy)
     fx = np.load(fixture_path(workload))
     batch, _, _ = workload_batch(workload)
     assert int(fx["meta"][2]) == batch.n_tokens, "the fixture was made from another batch"
@@ -53,6 +60,7 @@ def _step(ctx, workload):
     logits = m.forward(batch, training=True, seed=STEP_SEED)
     m.backward(fx["dlogits"])
     prof = ctx.profile_end()
+    ctx.set_matmul_precision("fp32")
     return m, fx, batch, logits, prof
 
 
@@ -80,29 +88,32 @@ def _check_gradients(m, fx):
           f"{bar_hits} tensors above 1e-4 under the fp32-oracle bar", flush=True)
 
 
-def test_headline_batch_32x512_every_gradient_matches_fp64(ctx):
-    print("full size: ModernBERT-base 22 layers, batch 32 x 512 padded (14344 tokens)", flush=True)
-    m, fx, batch, logits, prof = _step(ctx, "b32x512")
+@pytest.mark.parametrize("policy", ["fp32", "fp32-split3"])
+def test_headline_batch_32x512_every_gradient_matches_fp64(ctx, policy):
+    print(f"full size: ModernBERT-base 22 layers, batch 32 x 512 padded (14344 tokens), {policy}", flush=True)
+    m, fx, batch, logits, prof = _step(ctx, "b32x512", policy)
     assert np.abs(logits - fx["logits"]).max() < 1e-4
+    pair, wide, tall = KERNELS[policy]
     # The wide kernels this workload's timing rests on are the ones under test.
-    assert prof.get("gemm_bwd_pair_x6w", {}).get("launches", 0) >= 90, sorted(prof)
+    assert prof.get(pair, {}).get("launches", 0) >= 90, sorted(prof)
     # At 14,344 rows the 2304-wide products would need a third round of 256 × 256 tiles, so they and the
     # 768-wide ones (RoPE and residual epilogues included) run on 192 × 256 tiles; the head's 3072-wide
     # products take the wide forward kernel.
-    assert prof.get("gemm_nt_x6w", {}).get("launches", 0) >= 2, sorted(prof)
-    assert prof.get("gemm_nt_x6t", {}).get("launches", 0) >= 88, sorted(prof)
+    assert prof.get(wide, {}).get("launches", 0) >= 2, sorted(prof)
+    assert prof.get(tall, {}).get("launches", 0) >= 88, sorted(prof)
     _check_gradients(m, fx)
     m.close()
 
 
-def test_long_context_batch_2x8192_every_gradient_matches_fp64(ctx):
-    print("full size: ModernBERT-base 22 layers, batch 2 x 8192 (16384 tokens)", flush=True)
-    m, fx, batch, logits, prof = _step(ctx, "b2x8192")
+@pytest.mark.parametrize("policy", ["fp32", "fp32-split3"])
+def test_long_context_batch_2x8192_every_gradient_matches_fp64(ctx, policy):
+    print(f"full size: ModernBERT-base 22 layers, batch 2 x 8192 (16384 tokens), {policy}", flush=True)
+    m, fx, batch, logits, prof = _step(ctx, "b2x8192", policy)
     assert np.abs(logits - fx["logits"]).max() < 1e-4
     assert prof.get("attention_bwd_dkv_x6", {}).get("launches", 0) == 24, sorted(prof)
     # 16,384 rows: the RoPE-fused QKV products run on 192 × 256 tiles (three rounds of 256 × 256 tiles
     # or five of 128 × 128 would take longer).
-    assert prof.get("gemm_nt_x6t", {}).get("launches", 0) >= 22, sorted(prof)
+    assert prof.get(KERNELS[policy][2], {}).get("launches", 0) >= 22, sorted(prof)
     _check_gradients(m, fx)
     m.close()
 

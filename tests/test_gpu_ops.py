@@ -32,7 +32,7 @@ def param(ctx, name, a, trainable=True):
     return laya.Parameter(ctx, name, np.asarray(a, np.float32), trainable)
 
 
-@pytest.mark.parametrize("policy", ["fp32", "fp32-mfma"])
+@pytest.mark.parametrize("policy", ["fp32", "fp32-split3", "fp32-mfma"])
 @pytest.mark.parametrize("rows,inn,out", [(37, 96, 130), (300, 128, 384), (1000, 768, 2304), (5, 768, 1),
                                           (2048, 1152, 768), (333, 100, 260),
                                           # large enough for the balanced static schedule of dX + dW
@@ -53,9 +53,9 @@ def param(ctx, name, a, trainable=True):
                                           # 4-stage K loop
                                           (12345, 768, 700), (13824, 64, 768)])
 def test_linear_forward_and_backward(ctx, rows, inn, out, policy):
-    """Both fp32 implementations (exact bf16 splits, the default; the fp32 matrix cores) at the fp64
-    oracle's result to 1e-6, widened as √K for reductions longer than 2048 terms (fp32 rounding of a
-    K-term sum grows as √K)."""
+    """Every fp32 implementation (the default: two-piece fp16 products on 256-wide tiles, exact bf16
+    splits elsewhere; exact bf16 splits everywhere; the fp32 matrix cores) at the fp64 oracle's result to
+    1e-6, widened as √K for reductions longer than 2048 terms (fp32 rounding of a K-term sum grows as √K)."""
     print(f"linear rows={rows} in={inn} out={out} {policy}", flush=True)
     ctx.set_matmul_precision(policy)
     rng = np.random.default_rng(rows + inn + out)
@@ -119,6 +119,77 @@ def test_wide_tile_products_are_bitwise_deterministic(ctx):
         results.append((y.numpy(), dx.numpy(), w.gradient.numpy()))
     for a, b in zip(*results):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("sx,sw,sdy", [(1e-20, 1.0, 1.0), (1e20, 1e-3, 1.0), (1.0, 1e15, 1e-25),
+                                        (1e-30, 1e-7, 1e30), (0.0, 1.0, 1.0)])
+def test_two_piece_products_across_magnitudes(ctx, sx, sw, sdy):
+    """The two-piece fp16 products scale each operand by a power of two taken from its largest magnitude,
+    so operands far from 1 (and all-zero ones) keep fp32 accuracy: forward, dX and dW on the 256-wide
+    kernels (13871 x 768 -> 2304 and 768 wide) at the fp64 oracle's result to 1e-6, with rows whose
+    magnitudes spread over six decades."""
+    rows, inn = 13871, 768
+    rng = np.random.default_rng(11)
+    spread = np.exp(rng.uniform(-7, 7, (rows, 1))).astype(np.float32)  # e^±7: six decades across rows
+    x = (sx * spread * rng.standard_normal((rows, inn))).astype(np.float32)
+    for out in (2304, 768):
+        print(f"two-piece magnitudes sx={sx} sw={sw} sdy={sdy} out={out}", flush=True)
+        W = (sw * 0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+        dy = (sdy * spread * rng.standard_normal((rows, out))).astype(np.float32)
+        w = param(ctx, "w", W)
+        y_, dx_ = dev(ctx, np.zeros((rows, out), np.float32)), dev(ctx, np.zeros((rows, inn), np.float32))
+        xd, dyd = dev(ctx, x), dev(ctx, dy)
+        laya.linear(w, None, xd, rows, y_)
+        laya.linear_backward(w, None, xd, dyd, rows, dx_)
+        dW = np.zeros((out, inn)); db = np.zeros(out)
+        dx_ref = oracle.linear_backward(x, dy, W, True, dW, db, double=True)
+        y_ref = oracle.linear(x, W, None, double=True)
+        tol = 1e-6 * (rows / 2048) ** 0.5
+        for ref, got in ((y_ref, y_.numpy()), (dx_ref, dx_.numpy()), (dW, w.gradient.numpy())):
+            if not np.any(ref):
+                assert not np.any(got)
+            else:
+                assert rel_l2(ref, got) < tol
+
+
+def test_two_piece_products_propagate_non_finite_values(ctx):
+    """An infinity or NaN in an operand reaches the outputs it reaches in fp32 arithmetic: the rows (dX,
+    y) and columns (dW) that touch it are non-finite, every other output is finite and accurate (the
+    operand scales come from the finite magnitudes only)."""
+    rows, inn, out = 13871, 768, 2304
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((rows, inn)).astype(np.float32)
+    W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+    dy = rng.standard_normal((rows, out)).astype(np.float32)
+    x[100, 5] = np.inf
+    dy[200, 7] = np.nan
+    w = param(ctx, "w", W)
+    y_, dx_ = dev(ctx, np.zeros((rows, out), np.float32)), dev(ctx, np.zeros((rows, inn), np.float32))
+    xd, dyd = dev(ctx, x), dev(ctx, dy)
+    laya.linear(w, None, xd, rows, y_)
+    laya.linear_backward(w, None, xd, dyd, rows, dx_)
+    y, dx, g = y_.numpy(), dx_.numpy(), w.gradient.numpy()
+    bad_y = ~np.isfinite(y).all(axis=1)
+    assert bad_y[100] and bad_y.sum() == 1
+    bad_dx = ~np.isfinite(dx).all(axis=1)
+    assert bad_dx[200] and bad_dx.sum() == 1
+    assert not np.isfinite(g[7]).any() and not np.isfinite(g[:, 5]).any()
+    ok = np.ones(rows, bool); ok[100] = False
+    assert rel_l2(oracle.linear(x[ok], W, None, double=True), y[ok]) < 1e-6
+    okd = np.ones(rows, bool); okd[200] = False
+    x0, dy0 = x.copy(), dy.copy()
+    x0[100] = 0; dy0[200] = 0
+    dW = np.zeros((out, inn)); db = np.zeros(out)
+    dx_ref = oracle.linear_backward(x0, dy0, W, True, dW, db, double=True)
+    assert rel_l2(dx_ref[okd], dx[okd]) < 1e-6
+    # dW off row 7 and column 5 sums finite terms only (the poisoned tokens' other entries are finite):
+    # the fp64 reference with just the two poisoned entries cleared.
+    xc, dyc = x.copy(), dy.copy()
+    xc[100, 5] = 0; dyc[200, 7] = 0
+    dWc = np.zeros((out, inn)); dbc = np.zeros(out)
+    oracle.linear_backward(xc, dyc, W, False, dWc, dbc, double=True)
+    keep = np.ones((out, inn), bool); keep[7] = False; keep[:, 5] = False
+    assert rel_l2(dWc[keep], g[keep]) < 1e-6 * (rows / 2048) ** 0.5
 
 
 @pytest.mark.parametrize("rows,inn,out,with_bias", [(512, 768, 768, True), (200, 2304, 768, False)])
