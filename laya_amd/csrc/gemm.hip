@@ -1001,7 +1001,7 @@ struct PairScales {
     static __device__ __forceinline__ unsigned group_max(const unsigned* w) {
         unsigned m = w[0];
 #pragma unroll
-        for (int i = 1; i < AMAX_SPREAD; ++i) m = max(m, w[i]);
+        for (int i = 1; i < AMAX_SPREAD; ++i) m = max(m, w[i * AMAX_STRIDE]);
         return m;
     }
     __device__ __forceinline__ PairScales(const unsigned* amax_a, const unsigned* amax_b) {
@@ -2155,9 +2155,9 @@ namespace {
 
 // max|x| of a rows x cols operand into the context's word group `slot` (cleared first); returns it.
 const unsigned* operand_absmax(laya_ctx* ctx, int slot, const float* x, int rows, int cols, long ld) {
-    if (!ctx->amax) ctx->amax = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_SLOTS * AMAX_SPREAD));
-    unsigned* out = ctx->amax + slot * AMAX_SPREAD;
-    fill(ctx, reinterpret_cast<float*>(out), 0.0f, AMAX_SPREAD);  // +0.0f is the all-zero word
+    if (!ctx->amax) ctx->amax = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_SLOTS * AMAX_GROUP));
+    unsigned* out = ctx->amax + slot * AMAX_GROUP;
+    fill(ctx, reinterpret_cast<float*>(out), 0.0f, AMAX_GROUP);  // +0.0f is the all-zero word
     absmax_into(ctx, x, rows, cols, ld, out);
     return out;
 }

@@ -191,7 +191,7 @@ struct laya_model {
     std::vector<unsigned char> amax_known;
     size_t amax_sites() const { return (size_t)scorer_site(2); }
     laya::AmaxRef word(size_t k) {
-        return amax_words ? laya::AmaxRef{amax_words + k * laya::AMAX_SPREAD, &amax_known[k]} : laya::AmaxRef{};
+        return amax_words ? laya::AmaxRef{amax_words + k * laya::AMAX_GROUP, &amax_known[k]} : laya::AmaxRef{};
     }
     laya::AmaxRef wref(int i) { return i < 0 ? laya::AmaxRef{} : word(i); }
     laya::AmaxRef aref(int site) { return word(params.size() + site); }
@@ -455,7 +455,7 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
 void weights_changed(laya_model* m) {
     m->wb_fresh = false;
     if (m->amax_words) {
-        fill(m->ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_SPREAD * m->params.size());
+        fill(m->ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_GROUP * m->params.size());
         std::fill(m->amax_known.begin(), m->amax_known.begin() + m->params.size(), 0);
     }
 }
@@ -701,11 +701,11 @@ void forward(laya_model* m, bool train, uint64_t seed) {
     ensure_mirror(m);
     if (!m->amax_words) {
         const size_t n = m->params.size() + 2 * m->amax_sites();
-        m->amax_words = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_SPREAD * n));
+        m->amax_words = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_GROUP * n));
         m->amax_known.assign(n, 0);
     }
     const size_t nw = m->params.size() + m->amax_sites();  // weight and input words (+0.0f: all-zero bits)
-    fill(ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_SPREAD * nw);
+    fill(ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_GROUP * nw);
     std::fill(m->amax_known.begin(), m->amax_known.begin() + nw, 0);
 
     // Embedding gather fused into the embedding LayerNorm.
@@ -865,7 +865,7 @@ void backward(laya_model* m) {
     m->ln_jobs.n = 0;
     if (m->amax_words) {
         const size_t k = m->params.size() + m->amax_sites();
-        fill(m->ctx, reinterpret_cast<float*>(m->amax_words + AMAX_SPREAD * k), 0.0f, AMAX_SPREAD * m->amax_sites());
+        fill(m->ctx, reinterpret_cast<float*>(m->amax_words + AMAX_GROUP * k), 0.0f, AMAX_GROUP * m->amax_sites());
         std::fill(m->amax_known.begin() + k, m->amax_known.end(), 0);
     }
     backward_body(m);
