@@ -77,7 +77,8 @@ enum {
     LAYA_MATMUL_SPLIT3_FORWARD = 16,  /* per class: an fp32 class on three-piece bf16 splits in every */
     LAYA_MATMUL_SPLIT3_INPUT_GRAD = 32,  /*   kernel (no two-piece fp16 products); the backward pair */
     LAYA_MATMUL_SPLIT3_WEIGHT_GRAD = 64, /*   takes them unless both of its classes allow them */
-    LAYA_MATMUL_FP32_SPLIT3 = 112,    /* every fp32 class on three-piece bf16 splits */
+    LAYA_MATMUL_SPLIT3_ATTENTION = 128, /* attention's products on three-piece bf16 splits */
+    LAYA_MATMUL_FP32_SPLIT3 = 240,    /* every fp32 product (attention's too) on three-piece bf16 splits */
     LAYA_MATMUL_SPLIT_ALL = 7
 };
 int laya_ctx_set_matmul_precision(laya_ctx* ctx, int precision);

@@ -51,6 +51,10 @@ struct Params {
     float* dots;  // Σ_d dO·O per (row, head)
     float* dqkv;
     unsigned* amax;  // optional magnitude word group of the output (context, or dqkv), folded per block
+    // Two-piece products: the magnitude word groups of qkv and (backward) dO, from which q, k, v and dO
+    // take their power-of-two scales.
+    const unsigned* amax_qkv;
+    const unsigned* amax_do;
 };
 
 template <int D> struct Shape {
@@ -325,18 +329,62 @@ __device__ __forceinline__ f32x16 mma6(const bf16x8 (&a)[3], const bf16x8 (&b)[3
     return mfma16(a[0], b[0], c);
 }
 
-__device__ __forceinline__ bf16x8 cat8(bf16x4 lo, bf16x4 hi) {
+template <class V4>
+__device__ __forceinline__ auto cat8(V4 lo, V4 hi) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// The three pieces of 8 values (two float4).
-__device__ __forceinline__ void split8(f32x4 lo, f32x4 hi, bf16x8 (&out)[3]) {
-    bf16x4 a1, a2, a3, b1, b2, b3;
-    split3_4(lo, a1, a2, a3);
-    split3_4(hi, b1, b2, b3);
-    out[0] = cat8(a1, b1);
-    out[1] = cat8(a2, b2);
-    out[2] = cat8(a3, b3);
+// The pieces an operand is split into: NP = 3, exact three-piece bf16 splits and six products per block
+// (split.hpp); NP = 2, two fp16 pieces of the operand scaled by a power of two (split2h_4) and three
+// products per block, the smallest first. Both feed the same 32×32×16 fragment layouts.
+template <int NP> struct Pieces;
+template <> struct Pieces<3> {
+    typedef bf16x8 V8;
+    typedef bf16x4 V4;
+    static __device__ __forceinline__ void split4(f32x4 x, float, V4 (&o)[3]) { split3_4(x, o[0], o[1], o[2]); }
+    static __device__ __forceinline__ f32x16 mma(const V8 (&a)[3], const V8 (&b)[3], f32x16 c) { return mma6(a, b, c); }
+};
+template <> struct Pieces<2> {
+    typedef f16x8 V8;
+    typedef f16x4 V4;
+    static __device__ __forceinline__ void split4(f32x4 x, float sc, V4 (&o)[2]) { split2h_4(x, sc, o[0], o[1]); }
+    static __device__ __forceinline__ f32x16 mma(const V8 (&a)[2], const V8 (&b)[2], f32x16 c) {
+        c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], b[0], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b[1], c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b[0], c, 0, 0, 0);
+    }
+};
+
+// The operands computed in registers (P, dS) take a per-lane power-of-two scale for the two-piece
+// products: a lane's 16 values, with its partner lane's (lanes l and l + 32 feed the same output column),
+// set the exponent 14 − ⌊log₂ max⌋; it only decreases over the tiles, and when it does the column's
+// accumulators are rescaled by the same exact power of two, so they always carry one factor 2^e.
+// Returns the new exponent (e0 = 126 before the first tile).
+// (A NaN is passed over by the maximum; an infinity gives a tiny scale that keeps it infinite.)
+template <int N>
+__device__ __forceinline__ int lane_scale_update(const float (&v)[16], int e, f32x16 (&acc)[N]) {
+    float m = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(v[r]));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    const int et = pair_scale_exp(__builtin_bit_cast(unsigned, m));
+    if (et < e) {
+        const float f = ldexpf(1.0f, et - e);
+#pragma unroll
+        for (int i = 0; i < N; ++i) acc[i] *= f;
+        e = et;
+    }
+    return e;
+}
+
+// The pieces of 8 values (two float4), scaled by sc (two-piece products).
+template <int NP>
+__device__ __forceinline__ void split8(f32x4 lo, f32x4 hi, typename Pieces<NP>::V8 (&out)[NP], float sc = 1.0f) {
+    typename Pieces<NP>::V4 a[NP], b[NP];
+    Pieces<NP>::split4(lo, sc, a);
+    Pieces<NP>::split4(hi, sc, b);
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) out[pl] = cat8(a[pl], b[pl]);
 }
 
 // An R × 64 slice of one head (R = 32, 64 or 128 rows) in registers between its global fetch and its LDS
@@ -359,19 +407,23 @@ __device__ __forceinline__ void fetch_rows(RowStage<R>& st, const float* base, l
 }
 
 // The lane's own row (d = 16s + 8h … +7 for s < 4), split.
-__device__ __forceinline__ void split_lane_row(const float* src, bool valid, int h, bf16x8 (&out)[4][3]) {
+template <int NP>
+__device__ __forceinline__ void split_lane_row(const float* src, bool valid, int h,
+                                               typename Pieces<NP>::V8 (&out)[4][NP], float sc = 1.0f) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
         const f32x4 lo = valid ? ld4(src + 16 * s + 8 * h) : f32x4{0, 0, 0, 0};
         const f32x4 hi = valid ? ld4(src + 16 * s + 8 * h + 4) : f32x4{0, 0, 0, 0};
-        split8(lo, hi, out[s]);
+        split8<NP>(lo, hi, out[s], sc);
     }
 }
 
 // 16 values of a lane's accumulator column as the pieces of two 16-row k-steps (in the key order above).
-__device__ __forceinline__ void split_col16(const float (&v)[16], int u, bf16x8 (&out)[3]) {
-    split8(f32x4{v[8 * u], v[8 * u + 1], v[8 * u + 2], v[8 * u + 3]},
-           f32x4{v[8 * u + 4], v[8 * u + 5], v[8 * u + 6], v[8 * u + 7]}, out);
+template <int NP>
+__device__ __forceinline__ void split_col16(const float (&v)[16], int u, typename Pieces<NP>::V8 (&out)[NP],
+                                            float sc = 1.0f) {
+    split8<NP>(f32x4{v[8 * u], v[8 * u + 1], v[8 * u + 2], v[8 * u + 3]},
+               f32x4{v[8 * u + 4], v[8 * u + 5], v[8 * u + 6], v[8 * u + 7]}, out, sc);
 }
 
 // One LDS layout for every staged tile.
@@ -394,46 +446,53 @@ __device__ __forceinline__ bf16x4 ds_read_tr(const __bf16* p) {
     return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4)(p)));
 }
 
-// Three swizzled [row][d] planes of R rows (plane stride R·64) from a staged tile.
-template <int R>
-__device__ __forceinline__ void commit_swz(const RowStage<R>& st, __bf16* planes) {
+// NP swizzled [row][d] planes of R rows (plane stride R·64, 16-bit pieces) from a staged tile.
+template <int R, int NP = 3>
+__device__ __forceinline__ void commit_swz(const RowStage<R>& st, __bf16* planes, float sc = 1.0f) {
+    typedef typename Pieces<NP>::V4 V4;
     constexpr int N = RowStage<R>::N;
     const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        bf16x4 h1, h2, h3;
-        split3_4(st.v[i], h1, h2, h3);
+        V4 h[NP];
+        Pieces<NP>::split4(st.v[i], sc, h);
         const int o = swz(N * q + i, j);
-        *reinterpret_cast<bf16x4*>(planes + o) = h1;
-        *reinterpret_cast<bf16x4*>(planes + R * 64 + o) = h2;
-        *reinterpret_cast<bf16x4*>(planes + 2 * R * 64 + o) = h3;
+#pragma unroll
+        for (int pl = 0; pl < NP; ++pl) *reinterpret_cast<V4*>(planes + pl * R * 64 + o) = h[pl];
     }
 }
 
-// Row fragments (8 consecutive d of row `row` at k-step s) of three swizzled planes of R rows.
-template <int R>
-__device__ __forceinline__ void swz_row_frag(const __bf16* planes, int row, int s, int h, bf16x8 (&f)[3]) {
+// Row fragments (8 consecutive d of row `row` at k-step s) of NP swizzled planes of R rows.
+template <int R, int NP = 3>
+__device__ __forceinline__ void swz_row_frag(const __bf16* planes, int row, int s, int h,
+                                             typename Pieces<NP>::V8 (&f)[NP]) {
+    typedef typename Pieces<NP>::V8 V8;
     const int o = swz(row, 16 * s + 8 * h);
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl) f[pl] = *reinterpret_cast<const bf16x8*>(planes + pl * R * 64 + o);
+    for (int pl = 0; pl < NP; ++pl) f[pl] = *reinterpret_cast<const V8*>(planes + pl * R * 64 + o);
 }
 
 // The A fragments of d-rows 32·dt + lane mod 32 over the 16 rows from r0, in the key order of the score
-// accumulators (rows r0 + 4h … +3, then r0 + 8 + 4h … +3), from three swizzled planes of R rows.
-template <int R>
-__device__ __forceinline__ void swz_col_frag(const __bf16* planes, int r0, int dt, int lane, bf16x8 (&f)[3]) {
+// accumulators (rows r0 + 4h … +3, then r0 + 8 + 4h … +3), from NP swizzled planes of R rows.
+template <int R, int NP = 3>
+__device__ __forceinline__ void swz_col_frag(const __bf16* planes, int r0, int dt, int lane,
+                                             typename Pieces<NP>::V8 (&f)[NP]) {
+    typedef typename Pieces<NP>::V4 V4;
     const int G = lane >> 4, j = lane & 15;
     const int row = r0 + 4 * (G >> 1) + (j >> 2), col = 32 * dt + 16 * (G & 1) + 4 * (j & 3);
     const int o0 = swz(row, col), o1 = swz(row + 8, col);
 #pragma unroll
-    for (int pl = 0; pl < 3; ++pl) f[pl] = cat8(ds_read_tr(planes + pl * R * 64 + o0), ds_read_tr(planes + pl * R * 64 + o1));
+    for (int pl = 0; pl < NP; ++pl)
+        f[pl] = cat8(__builtin_bit_cast(V4, ds_read_tr(planes + pl * R * 64 + o0)),
+                     __builtin_bit_cast(V4, ds_read_tr(planes + pl * R * 64 + o1)));
 }
 
-template <int D, bool DROP>
+// NP = 3: three-piece bf16 split products; NP = 2: two-piece fp16 products of scaled operands.
+template <int D, bool DROP, int NP = 3>
 __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
-    __shared__ __attribute__((aligned(16))) __bf16 Ks[3 * TILE * 64];  // K tile, swizzled [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 Vs[3 * TILE * 64];  // V tile, swizzled [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Ks[NP * TILE * 64];  // K tile, swizzled [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Vs[NP * TILE * 64];  // V tile, swizzled [key][d]
 
     const int seg = blockIdx.y, head = blockIdx.z;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
@@ -447,8 +506,23 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     const long stride = 3L * p.hidden;
     const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
 
-    bf16x8 qh[4][3];
-    split_lane_row(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, qvalid, h, qh);
+    typedef typename Pieces<NP>::V8 V8;
+    // Two-piece products: q, k and v scaled by 2^eq (from the qkv magnitude), P by the lane's running 2^ep:
+    // a subtile's largest probability is 2^(mx − m) (times keep), so ep = 14 − ⌊mx − m⌋ − ⌈log₂ keep⌉ goes
+    // into the exponential's argument, and the row sum l is kept in the same units as the output's
+    // accumulator (both rescaled when ep drops), so the final o/l needs only q's factor out.
+    int eq = 0, ep = 126, ek = 0;
+    if constexpr (NP == 2) {
+        eq = pair_scale_exp(amax_group_max(p.amax_qkv));
+        if (DROP) {
+            const unsigned kb = __builtin_bit_cast(unsigned, p.keep);
+            ek = (int)(kb >> 23) - 127 + ((kb & 0x7fffffu) != 0u);
+        }
+    }
+    const float sq = exp2_int(eq);
+    const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
+    V8 qh[4][NP];
+    split_lane_row<NP>(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, qvalid, h, qh, sq);
 
     int kbeg = 0, kend = L;
     int wbeg = 0, wend = L;
@@ -472,8 +546,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     fetch_rows<TILE>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
         __syncthreads();
-        commit_swz<TILE>(kst, Ks);
-        commit_swz<TILE>(vst, Vs);
+        commit_swz<TILE, NP>(kst, Ks, sq);
+        commit_swz<TILE, NP>(vst, Vs, sq);
         __syncthreads();
         if (kt0 + TILE < kend) {  // block-uniform: the next tile's loads overlap this tile's products
             fetch_rows<TILE>(kst, kbase, stride, L, kt0 + TILE);
@@ -488,23 +562,23 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
             f32x16 s = f32x16{};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                bf16x8 kf[3];
-                swz_row_frag<TILE>(Ks, 32 * st + lr, ks, h, kf);
-                s = mma6(kf, qh[ks], s);
+                V8 kf[NP];
+                swz_row_frag<TILE, NP>(Ks, 32 * st + lr, ks, h, kf);
+                s = Pieces<NP>::mma(kf, qh[ks], s);
             }
             float t[16];
             float mx = -1e30f;
             if (subtile_inside(q0w, kbs, L, hw)) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    t[r] = s[r] * p.scale_log2;
+                    t[r] = s[r] * scale_log2;
                     mx = fmaxf(mx, t[r]);
                 }
             } else {
                 const int rel0 = kbs + 4 * h - win.lo;  // key − lo of the lane's row r = 0
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    t[r] = in_range(win, rel0 + 8 * (r >> 2) + (r & 3)) ? s[r] * p.scale_log2 : NEG_INF;
+                    t[r] = in_range(win, rel0 + 8 * (r >> 2) + (r & 3)) ? s[r] * scale_log2 : NEG_INF;
                     mx = fmaxf(mx, t[r]);
                 }
             }
@@ -520,11 +594,24 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
                 o[1] *= alpha;
                 m = mnew;
             }
+            float mm = m;  // pr = 2^(t − mm): the probabilities, times 2^ep for two-piece products
+            if constexpr (NP == 2) {
+                const float d = mx - m;
+                const int et = d > -200.0f ? min(126, 14 - (int)floorf(d) - ek) : 126;
+                if (et < ep) {
+                    const float f = ldexpf(1.0f, et - ep);
+                    l *= f;
+                    o[0] *= f;
+                    o[1] *= f;
+                    ep = et;
+                }
+                mm = m - (float)ep;
+            }
             float pr[16];
             float sum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                pr[r] = fast_exp2(t[r] - m);
+                pr[r] = fast_exp2(t[r] - mm);
                 sum += pr[r];
             }
             l += sum;
@@ -539,13 +626,13 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
             // Oᵀ += Vᵀ·Pᵀ over the subtile's 32 keys in two 16-key steps.
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                bf16x8 ph[3];
-                split_col16(pr, u, ph);
+                V8 ph[NP];
+                split_col16<NP>(pr, u, ph);
 #pragma unroll
                 for (int dt = 0; dt < 2; ++dt) {
-                    bf16x8 vf[3];
-                    swz_col_frag<TILE>(Vs, 32 * st + 16 * u, dt, lane, vf);
-                    o[dt] = mma6(vf, ph, o[dt]);
+                    V8 vf[NP];
+                    swz_col_frag<TILE, NP>(Vs, 32 * st + 16 * u, dt, lane, vf);
+                    o[dt] = Pieces<NP>::mma(vf, ph, o[dt]);
                 }
             }
         }
@@ -554,10 +641,11 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     const float lt = l + __shfl_xor(l, 32, 64);
     unsigned am = 0;
     if (qvalid) {
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const float inv = lt > 0.0f ? (NP == 2 ? ldexpf(1.0f / lt, -eq) : 1.0f / lt) : 0.0f;
         am = store_acc<D>(o, p.context + (long)(start + q) * p.hidden + qcol, h, inv);
         if (p.context16) store_acc16<D>(o, p.context16 + (long)(start + q) * p.hidden + qcol, h, inv);
-        if (h == 0) p.lse[(long)(start + q) * p.heads + head] = lt > 0.0f ? m + log2f(lt) : __builtin_huge_valf();
+        if (h == 0) p.lse[(long)(start + q) * p.heads + head] = lt > 0.0f ? (m + log2f(lt)) - (NP == 2 ? (float)ep : 0.0f)
+                                                                     : __builtin_huge_valf();
     }
     block_amax_fold(am, p.amax);
 }
@@ -826,12 +914,12 @@ constexpr int BT = 32;
 // Each wave owns 32 keys: K split once into registers, V split once into the block's LDS planes. The
 // query tiles are committed to one swizzled layout each (Q and dO), the next tile's rows load while the
 // current one is multiplied, and the products over queries read Qᵀ and dOᵀ with the transposing reads.
-template <int D, bool DROP>
+template <int D, bool DROP, int NP = 3>
 __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
-    __shared__ __attribute__((aligned(16))) __bf16 Qs[3 * BT * 64];
-    __shared__ __attribute__((aligned(16))) __bf16 Os[3 * BT * 64];
-    __shared__ __attribute__((aligned(16))) __bf16 Vs[3 * BLOCK_ROWS * 64];
+    __shared__ __attribute__((aligned(16))) __bf16 Qs[NP * BT * 64];
+    __shared__ __attribute__((aligned(16))) __bf16 Os[NP * BT * 64];
+    __shared__ __attribute__((aligned(16))) __bf16 Vs[NP * BLOCK_ROWS * 64];
     __shared__ float lse_s[BT], dot_s[BT];
 
     const int seg = blockIdx.y, head = blockIdx.z;
@@ -847,13 +935,26 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     const long stride = 3L * p.hidden;
     const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
 
-    bf16x8 kh[4][3];
+    typedef typename Pieces<NP>::V8 V8;
+    // Two-piece products: q, k and v scaled by 2^eq (from the qkv magnitude), dO by 2^eo, P and dS by the
+    // lane's running 2^ep and 2^eds (lane_scale_update). The scores' and dP's accumulators carry the
+    // operand factors, taken out with the softmax scale and as dP is used; the gradients' accumulators
+    // at their store.
+    int eq = 0, eo = 0, ep = 126, eds = 126;
+    if constexpr (NP == 2) {
+        eq = pair_scale_exp(amax_group_max(p.amax_qkv));
+        eo = pair_scale_exp(amax_group_max(p.amax_do));
+    }
+    const float sq = exp2_int(eq), so = exp2_int(eo);
+    const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
+    const float udp = NP == 2 ? ldexpf(1.0f, -(eo + eq)) : 1.0f;
+    V8 kh[4][NP];
     const long krow = (long)(start + (kvalid ? key : 0)) * stride;
-    split_lane_row(p.qkv + krow + kcol, kvalid, h, kh);
+    split_lane_row<NP>(p.qkv + krow + kcol, kvalid, h, kh, sq);
     {
         RowStage<BLOCK_ROWS> vst;
         fetch_rows<BLOCK_ROWS>(vst, p.qkv + (long)start * stride + vcol, stride, L, kb0);
-        commit_swz<BLOCK_ROWS>(vst, Vs);
+        commit_swz<BLOCK_ROWS, NP>(vst, Vs, sq);
     }
 
     int qbeg = 0, qend = L, wbeg = 0, wend = L;
@@ -888,8 +989,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     if (qbeg < qend) fetch(qbeg);
     for (int qt0 = qbeg; qt0 < qend; qt0 += BT) {
         __syncthreads();  // the previous tile's fragments (and, first time round, V's commit) are read
-        commit_swz<BT>(qst, Qs);
-        commit_swz<BT>(ost, Os);
+        commit_swz<BT, NP>(qst, Qs, sq);
+        commit_swz<BT, NP>(ost, Os, so);
         if (threadIdx.x < BT) {
             lse_s[threadIdx.x] = lse_n;
             dot_s[threadIdx.x] = dot_n;
@@ -902,12 +1003,16 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            bf16x8 f[3], vh[3];
-            swz_row_frag<BT>(Qs, lr, ks, h, f);
-            s = mma6(f, kh[ks], s);
-            swz_row_frag<BT>(Os, lr, ks, h, f);
-            swz_row_frag<BLOCK_ROWS>(Vs, wave * WAVE_ROWS + lr, ks, h, vh);
-            dp = mma6(f, vh, dp);
+            V8 f[NP], vh[NP];
+            swz_row_frag<BT, NP>(Qs, lr, ks, h, f);
+            s = Pieces<NP>::mma(f, kh[ks], s);
+            swz_row_frag<BT, NP>(Os, lr, ks, h, f);
+            swz_row_frag<BLOCK_ROWS, NP>(Vs, wave * WAVE_ROWS + lr, ks, h, vh);
+            dp = Pieces<NP>::mma(f, vh, dp);
+        }
+        if constexpr (NP == 2) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dp[r] *= udp;
         }
         float pm[16], ds[16];
         const int rel0 = qt0 + 4 * h - win.lo;  // query − lo of the lane's row r = 0
@@ -916,7 +1021,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
-                    const float pr = fast_exp2(s[r] * p.scale_log2 - lse_s[ql]);
+                    const float pr = fast_exp2(s[r] * scale_log2 - lse_s[ql]);
                     pm[r] = pr;
                     ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
                 }
@@ -925,7 +1030,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                 for (int r = 0; r < 16; ++r) {
                     const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
                     const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
-                    const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse_s[ql]) : 0.0f;
+                    const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse_s[ql]) : 0.0f;
                     pm[r] = pr;
                     ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
                 }
@@ -936,7 +1041,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                 const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
                 const int qq = qt0 + ql;
                 const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
-                const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse_s[ql]) : 0.0f;
+                const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse_s[ql]) : 0.0f;
                 const float drop =
                     uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
                 const float mask = ok ? drop : 1.0f;
@@ -945,18 +1050,22 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
             }
         }
         // dVᵀ += dOᵀ·(P∘M) and dKᵀ += Qᵀ·dS over the tile's 32 queries in two 16-query steps.
+        if constexpr (NP == 2) {
+            ep = lane_scale_update(pm, ep, dv);
+            eds = lane_scale_update(ds, eds, dk);
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            bf16x8 ph[3], dh[3];
-            split_col16(pm, u, ph);
-            split_col16(ds, u, dh);
+            V8 ph[NP], dh[NP];
+            split_col16<NP>(pm, u, ph, exp2_int(NP == 2 ? ep : 0));
+            split_col16<NP>(ds, u, dh, exp2_int(NP == 2 ? eds : 0));
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
-                bf16x8 f[3];
-                swz_col_frag<BT>(Os, 16 * u, dt, lane, f);
-                dv[dt] = mma6(f, ph, dv[dt]);
-                swz_col_frag<BT>(Qs, 16 * u, dt, lane, f);
-                dk[dt] = mma6(f, dh, dk[dt]);
+                V8 f[NP];
+                swz_col_frag<BT, NP>(Os, 16 * u, dt, lane, f);
+                dv[dt] = Pieces<NP>::mma(f, ph, dv[dt]);
+                swz_col_frag<BT, NP>(Qs, 16 * u, dt, lane, f);
+                dk[dt] = Pieces<NP>::mma(f, dh, dk[dt]);
             }
         }
     }
@@ -969,16 +1078,17 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     if (keye < L) {
         if (rope) inverse_rope_acc<D>(dk, p, keye, he);
         float* dst = p.dqkv + (long)(start + keye) * stride;
-        am = max(store_acc<D>(dk, dst + kcol, he, 1.0f), store_acc<D>(dv, dst + vcol, he, 1.0f));
+        const float uk = NP == 2 ? ldexpf(1.0f, -(eds + eq)) : 1.0f, uv = NP == 2 ? ldexpf(1.0f, -(ep + eo)) : 1.0f;
+        am = max(store_acc<D>(dk, dst + kcol, he, uk), store_acc<D>(dv, dst + vcol, he, uv));
     }
     block_amax_fold(am, p.amax);
 }
 
-template <int D, bool DROP>
+template <int D, bool DROP, int NP = 3>
 __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
-    __shared__ __attribute__((aligned(16))) __bf16 Ks[3 * BT * 64];  // K tile, swizzled [key][d]
-    __shared__ __attribute__((aligned(16))) __bf16 Vs[3 * BT * 64];  // V tile, swizzled [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Ks[NP * BT * 64];  // K tile, swizzled [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Vs[NP * BT * 64];  // V tile, swizzled [key][d]
 
     const int seg = blockIdx.y, head = blockIdx.z;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
@@ -993,10 +1103,23 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     const long stride = 3L * p.hidden;
     const int qcol = head * D, kcol = p.hidden + head * D, vcol = 2 * p.hidden + head * D;
 
-    bf16x8 qh[4][3], oh[4][3];
+    typedef typename Pieces<NP>::V8 V8;
+    // Two-piece products: q, k and v scaled by 2^eq (from the qkv magnitude), dO by 2^eo, P and dS by the
+    // lane's running 2^ep and 2^eds (lane_scale_update). The scores' and dP's accumulators carry the
+    // operand factors, taken out with the softmax scale and as dP is used; the gradients' accumulators
+    // at their store.
+    int eq = 0, eo = 0, ep = 126, eds = 126;
+    if constexpr (NP == 2) {
+        eq = pair_scale_exp(amax_group_max(p.amax_qkv));
+        eo = pair_scale_exp(amax_group_max(p.amax_do));
+    }
+    const float sq = exp2_int(eq), so = exp2_int(eo);
+    const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
+    const float udp = NP == 2 ? ldexpf(1.0f, -(eo + eq)) : 1.0f;
+    V8 qh[4][NP], oh[4][NP];
     const int qs = start + (qvalid ? q : 0);
-    split_lane_row(p.qkv + (long)qs * stride + qcol, qvalid, h, qh);
-    split_lane_row(p.dcontext + (long)qs * p.hidden + qcol, qvalid, h, oh);
+    split_lane_row<NP>(p.qkv + (long)qs * stride + qcol, qvalid, h, qh, sq);
+    split_lane_row<NP>(p.dcontext + (long)qs * p.hidden + qcol, qvalid, h, oh, so);
     const float lse = qvalid ? p.lse[(long)qs * p.heads + head] : __builtin_huge_valf();
     // The row constant Σ_d dO·O (Ops.cs:408-409) from the lane's half of the row and its partner's, written
     // for the dK/dV kernel, which runs after this one.
@@ -1034,8 +1157,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     fetch_rows<BT>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += BT) {
         __syncthreads();
-        commit_swz<BT>(kst, Ks);
-        commit_swz<BT>(vst, Vs);
+        commit_swz<BT, NP>(kst, Ks, sq);
+        commit_swz<BT, NP>(vst, Vs, sq);
         __syncthreads();
         if (kt0 + BT < kend) {  // block-uniform
             fetch_rows<BT>(kst, kbase, stride, L, kt0 + BT);
@@ -1047,23 +1170,27 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            bf16x8 f[3];
-            swz_row_frag<BT>(Ks, lr, ks, h, f);
-            s = mma6(f, qh[ks], s);
-            swz_row_frag<BT>(Vs, lr, ks, h, f);
-            dp = mma6(f, oh[ks], dp);
+            V8 f[NP];
+            swz_row_frag<BT, NP>(Ks, lr, ks, h, f);
+            s = Pieces<NP>::mma(f, qh[ks], s);
+            swz_row_frag<BT, NP>(Vs, lr, ks, h, f);
+            dp = Pieces<NP>::mma(f, oh[ks], dp);
+        }
+        if constexpr (NP == 2) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) dp[r] *= udp;
         }
         float ds[16];
         const int rel0 = kt0 + 4 * h - win.lo;  // key − lo of the lane's row r = 0
         if (!DROP) {
             if (subtile_inside(q0w, kt0, L, hw)) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * p.scale_log2 - lse) * (dp[r] - dot) * p.scale;
+                for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * scale_log2 - lse) * (dp[r] - dot) * p.scale;
             } else {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
-                    const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse) : 0.0f;
+                    const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse) : 0.0f;
                     ds[r] = pr * (dp[r] - dot) * p.scale;
                 }
             }
@@ -1072,7 +1199,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
             for (int r = 0; r < 16; ++r) {
                 const int key = kt0 + 8 * (r >> 2) + 4 * h + (r & 3);
                 const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
-                const float pr = ok ? fast_exp2(s[r] * p.scale_log2 - lse) : 0.0f;
+                const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse) : 0.0f;
                 const float drop =
                     uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
                 const float mask = ok ? drop : 1.0f;
@@ -1080,15 +1207,16 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
             }
         }
         // dQᵀ += Kᵀ·dSᵀ over the tile's 32 keys in two 16-key steps.
+        if constexpr (NP == 2) eds = lane_scale_update(ds, eds, dq);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            bf16x8 dh[3];
-            split_col16(ds, u, dh);
+            V8 dh[NP];
+            split_col16<NP>(ds, u, dh, exp2_int(NP == 2 ? eds : 0));
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
-                bf16x8 f[3];
-                swz_col_frag<BT>(Ks, 16 * u, dt, lane, f);
-                dq[dt] = mma6(f, dh, dq[dt]);
+                V8 f[NP];
+                swz_col_frag<BT, NP>(Ks, 16 * u, dt, lane, f);
+                dq[dt] = Pieces<NP>::mma(f, dh, dq[dt]);
             }
         }
     }
@@ -1096,7 +1224,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     unsigned am = 0;
     if (qvalid) {
         if (rope) inverse_rope_acc<D>(dq, p, q, h);
-        am = store_acc<D>(dq, p.dqkv + (long)(start + q) * stride + qcol, h, 1.0f);
+        am = store_acc<D>(dq, p.dqkv + (long)(start + q) * stride + qcol, h, NP == 2 ? ldexpf(1.0f, -(eds + eq)) : 1.0f);
     }
     block_amax_fold(am, p.amax);
 }
@@ -1178,10 +1306,17 @@ void check_args(const AttentionArgs& a) {
 // bf16 product policies leave attention in fp32 arithmetic too.
 bool split_attention(const laya_ctx* ctx) { return (ctx->matmul_split | ctx->matmul_bf16) != 0; }
 
+// The two-piece form's scale input: qkv's magnitude (measured into the context's words unless the caller
+// keeps it).
+void pair_inputs(laya_ctx* ctx, const AttentionArgs& a, const float* qkv, AmaxRef r_qkv, Params& p) {
+    LAYA_REQUIRE(a.rows >= 0, "attention: row count needed to measure qkv");
+    p.amax_qkv = operand_amax_ref(ctx, qkv == a.qkv ? r_qkv : AmaxRef{}, 3, qkv, a.rows, 3 * a.hidden, 3L * a.hidden);
+}
+
 }  // namespace
 
 void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse, __bf16* context16,
-                   unsigned* amax) {
+                   unsigned* amax, AmaxRef amax_qkv) {
     check_args(a);
     if (a.nseg == 0 || a.max_len == 0) return;
     Params p = make_params(a);
@@ -1191,10 +1326,17 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
     p.amax = amax;
     dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
     const bool split = a.head_dim == 64 && split_attention(ctx);
+    const bool pair = split && ctx->attention_pair;
     p.context16 = split ? context16 : nullptr;
+    if (pair) pair_inputs(ctx, a, p.qkv, amax_qkv, p);
     {
-        ProfileScope scope(ctx, split ? "attention_fwd_x6" : "attention_fwd", 4.0 * a.hidden * a.keys, 0.0);
-        if (split && p.p_drop > 0.0f)
+        ProfileScope scope(ctx, pair ? "attention_fwd_h2" : split ? "attention_fwd_x6" : "attention_fwd",
+                           4.0 * a.hidden * a.keys, 0.0);
+        if (pair && p.p_drop > 0.0f)
+            hipLaunchKernelGGL((attn_fwd_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+        else if (pair)
+            hipLaunchKernelGGL((attn_fwd_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+        else if (split && p.p_drop > 0.0f)
             hipLaunchKernelGGL((attn_fwd_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
         else if (split)
             hipLaunchKernelGGL((attn_fwd_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
@@ -1211,7 +1353,7 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
 }
 
 void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,
-                        const float* dcontext, float* dqkv, unsigned* amax) {
+                   const float* dcontext, float* dqkv, unsigned* amax, AmaxRef amax_qkv, AmaxRef amax_do) {
     check_args(a);
     if (a.nseg == 0 || a.max_len == 0 || rows == 0) return;
     Params p = make_params(a);
@@ -1230,6 +1372,27 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     // Model flops of the backward, 8·d·Σkeys, split as the kernels do the work: dK/dV (4 products of
     // which 2 recompute the forward's) and dQ (3 products, 2 recomputed).
     const double fb = 2.0 * a.hidden * a.keys;
+    if (a.head_dim == 64 && split_attention(ctx) && ctx->attention_pair) {
+        p.context = const_cast<float*>(context);
+        pair_inputs(ctx, ar, p.qkv, amax_qkv, p);
+        p.amax_do = operand_amax_ref(ctx, amax_do, 4, dcontext, rows, a.hidden, a.hidden);
+        {
+            // dQ first: it forms each row's Σ dO·O and writes it for dK/dV.
+            ProfileScope scope(ctx, "attention_bwd_dq_h2", 2.0 * fb, 0.0);
+            if (p.p_drop > 0.0f)
+                hipLaunchKernelGGL((attn_bwd_dq_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+            else
+                hipLaunchKernelGGL((attn_bwd_dq_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+            check_launch("attn_bwd_dq_x6_kernel");
+        }
+        ProfileScope scope(ctx, "attention_bwd_dkv_h2", 2.0 * fb, 0.0);
+        if (p.p_drop > 0.0f)
+            hipLaunchKernelGGL((attn_bwd_dkv_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+        else
+            hipLaunchKernelGGL((attn_bwd_dkv_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+        check_launch("attn_bwd_dkv_x6_kernel");
+        return;
+    }
     if (a.head_dim == 64 && split_attention(ctx)) {
         p.context = const_cast<float*>(context);
         {

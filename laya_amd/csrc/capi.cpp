@@ -183,6 +183,7 @@ int laya_ctx_set_matmul_precision(laya_ctx* ctx, int precision) {
         // three-piece bf16 splits.
         ctx->matmul_split = (precision & LAYA_MATMUL_FP32_MFMA) ? 0 : (LAYA_MATMUL_SPLIT_ALL & ~ctx->matmul_bf16);
         ctx->matmul_pair = ctx->matmul_split & ~((precision & LAYA_MATMUL_FP32_SPLIT3) >> 4);
+        ctx->attention_pair = !(precision & LAYA_MATMUL_SPLIT3_ATTENTION);
     });
 }
 

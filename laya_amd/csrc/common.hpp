@@ -92,6 +92,8 @@ struct laya_ctx {
     // Of those, the classes whose 256-wide kernels take two-piece fp16 products instead (fp32-accurate,
     // three fp16 MFMA products per fp32 one, operands scaled by powers of two), same class bits.
     int matmul_pair = LAYA_MATMUL_SPLIT_ALL;
+    // Attention's split products as two-piece fp16 products too (the default).
+    bool attention_pair = true;
     // max|operand| words of the two-piece products that no caller keeps (one per operand of a product).
     unsigned* amax = nullptr;
     std::vector<hipEvent_t> event_pool;
@@ -199,6 +201,14 @@ __device__ inline void block_amax_fold(unsigned m, unsigned* out) {
     }
 }
 
+// The largest word of a magnitude word group.
+__device__ inline unsigned amax_group_max(const unsigned* w) {
+    unsigned m = w[0];
+#pragma unroll
+    for (int i = 1; i < AMAX_SPREAD; ++i) m = max(m, w[i * AMAX_STRIDE]);
+    return m;
+}
+
 inline unsigned blocks_for(size_t n, unsigned per_block, unsigned cap = 65535u * 16u) {
     size_t b = (n + per_block - 1) / per_block;
     if (b == 0) b = 1;
@@ -266,6 +276,9 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
 // max|x| over the finite elements of a rows x cols operand (row stride ld), folded into the word group
 // at out by atomicMax as fp32 bit patterns (the two-piece products' operand scales).
 void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, unsigned* out);
+// An operand's magnitude word group: the caller's r (measured now if not known yet), or the context's
+// group `slot` (0 … 5), measured now.
+const unsigned* operand_amax_ref(laya_ctx* ctx, AmaxRef r, int slot, const float* x, int rows, int cols, long ld);
 
 // Σ over rows of a [rows, n] matrix added into out[n], deterministic (bias gradients).
 void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out);
@@ -332,7 +345,7 @@ inline double window_keys(int L, int hw) {
 // context16 (optional): a bf16 copy of the context (nearest even), for the bf16 products that read it;
 // amax (optional): max|context| folded into a magnitude word group.
 void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float* lse, __bf16* context16 = nullptr,
-                   unsigned* amax = nullptr);
+                   unsigned* amax = nullptr, AmaxRef amax_qkv = {});
 
 // RlcdObjective.Compute (RlcdObjective.cs:57-155) with supplied standard-normal draws [groups][Σ K], all
 // operands on the device; grad [Σ K]; losses [4] = total, policy, cross-entropy, mean reward.
@@ -347,6 +360,7 @@ void decision_readout(laya_ctx* ctx, const float* scores, const int* opt_off, co
 // rows: the number of rows of qkv / context / dcontext (the dO·O row constants span all of them); amax
 // (optional): max|dqkv| folded into a magnitude word group.
 void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float* context, const float* lse,
-                   const float* dcontext, float* dqkv, unsigned* amax = nullptr);
+                   const float* dcontext, float* dqkv, unsigned* amax = nullptr, AmaxRef amax_qkv = {},
+                   AmaxRef amax_do = {});
 
 }  // namespace laya

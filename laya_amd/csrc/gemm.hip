@@ -998,14 +998,8 @@ struct PairScales {
     float sa = 1.0f, sb = 1.0f;
     int ex = 0;
     __device__ __forceinline__ PairScales() = default;
-    static __device__ __forceinline__ unsigned group_max(const unsigned* w) {
-        unsigned m = w[0];
-#pragma unroll
-        for (int i = 1; i < AMAX_SPREAD; ++i) m = max(m, w[i * AMAX_STRIDE]);
-        return m;
-    }
     __device__ __forceinline__ PairScales(const unsigned* amax_a, const unsigned* amax_b) {
-        const int ea = pair_scale_exp(group_max(amax_a)), eb = pair_scale_exp(group_max(amax_b));
+        const int ea = pair_scale_exp(amax_group_max(amax_a)), eb = pair_scale_exp(amax_group_max(amax_b));
         sa = exp2_int(ea);
         sb = exp2_int(eb);
         ex = -(ea + eb);
@@ -1115,7 +1109,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
 // and NaNs are left out, so the scale fits the finite values and the non-finite ones still reach the
 // products (an infinity's low piece is a NaN: outputs that an infinity reaches are non-finite, as in
 // fp32, though possibly NaN where fp32 gives an infinity).
-constexpr int AMAX_BLOCKS = 1024, AMAX_SLOTS = 4;
+constexpr int AMAX_BLOCKS = 1024, AMAX_SLOTS = 6;
 
 __global__ __launch_bounds__(256) void absmax_kernel(const float* __restrict__ x, int rows, int cols, long ld,
                                                      int vec, unsigned* out) {
@@ -2403,6 +2397,11 @@ int fill_splits(const laya_ctx* ctx, int tiles, int K, int min_k) {
 }
 
 }  // namespace
+
+const unsigned* operand_amax_ref(laya_ctx* ctx, AmaxRef r, int slot, const float* x, int rows, int cols, long ld) {
+    LAYA_REQUIRE(slot >= 0 && slot < AMAX_SLOTS, "operand_amax_ref: no such slot");
+    return operand_amax(ctx, r, slot, x, rows, cols, ld);
+}
 
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
           const float* B, long ldb, float* C, long ldc, const float* bias, const float* R, long ldr,

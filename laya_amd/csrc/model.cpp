@@ -184,8 +184,8 @@ struct laya_model {
 
     // max|operand| words of the two-piece fp16 products: one per parameter, one per product site for its
     // input (four per encoder layer: the QKV, Wo, Wi and MLP-output inputs; four per head layer; two for
-    // the scorer), and one per site for its output gradient; the host flags say which hold the current
-    // values. The weight and input words are cleared at each forward (a weight is measured once per step,
+    // the scorer; plus each attention's qkv), and one per site for its output gradient (plus each
+    // attention's context gradient); the host flags say which hold the current values. The weight and input words are cleared at each forward (a weight is measured once per step,
     // an input once per forward and reused by its backward product), the gradient words at each backward.
     unsigned* amax_words = nullptr;
     std::vector<unsigned char> amax_known;
@@ -203,9 +203,11 @@ struct laya_model {
         *r.known = 1;
         return r.word;
     }
-    int enc_site(int l, int k) const { return 4 * l + k; }
-    int head_site(int j, int k) const { return 4 * cfg.layers + 4 * j + k; }
-    int scorer_site(int k) const { return 4 * cfg.layers + 4 * cfg.head_layers + k; }
+    // Five sites per layer: k = 0 … 3 the four products (their inputs' words, and in the backward their
+    // output gradients'), k = 4 attention (qkv's word, and in the backward the context gradient's).
+    int enc_site(int l, int k) const { return 5 * l + k; }
+    int head_site(int j, int k) const { return 5 * cfg.layers + 5 * j + k; }
+    int scorer_site(int k) const { return 5 * cfg.layers + 5 * cfg.head_layers + k; }
 
     // ----- the batch of the last forward
     bool has_tape = false, training = false;
@@ -620,6 +622,7 @@ AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p
     a.scale = 1.0f / std::sqrt((float)(m->d() / m->head_heads));
     a.p_drop = p;
     a.seed = salt(seed, index, 0);
+    a.rows = m->T;
     return a;
 }
 
@@ -682,7 +685,7 @@ void encoder_forward(laya_model* m, int l, bool output = true) {
         linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv, a.normed16, m->aref(m->enc_site(l, 0)));
     }
     attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse, a.ctx16,
-                  m->produce(m->aref(m->enc_site(l, 1)), 7));
+                  m->produce(m->aref(m->enc_site(l, 1)), 7), m->aref(m->enc_site(l, 4)));
     linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res, a.ctx16, m->aref(m->enc_site(l, 1)));  // x1 = x + attn
     layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2, nullptr,
                   nullptr, nullptr, a.mlpn16, m->produce(m->aref(m->enc_site(l, 2)), 7));
@@ -729,7 +732,7 @@ void forward(laya_model* m, bool train, uint64_t seed) {
                       nullptr, nullptr, a.n1_16, m->produce(m->aref(m->head_site(j, 0)), 7));
         linear(m, a.n1, T, d, H.in_proj, H.in_proj_b, 3 * d, nullptr, a.qkv, a.n1_16, m->aref(m->head_site(j, 0)));
         attention_fwd(ctx, head_attention(m, a.qkv, j, p, seed), a.ctx, a.lse, a.ctx16,
-                      m->produce(m->aref(m->head_site(j, 1)), 7));
+                      m->produce(m->aref(m->head_site(j, 1)), 7), m->aref(m->head_site(j, 4)));
         if (p > 0.0f) {
             linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, nullptr, a.res, a.ctx16, m->aref(m->head_site(j, 1)));
             dropout(ctx, a.res, (size_t)T * d, p, salt(seed, j, 1));
@@ -790,7 +793,7 @@ void encoder_backward(laya_model* m, int l, bool need_input) {
                 m->produce(m->dref(m->enc_site(l, 1)), 6));
     linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx, nullptr, a.ctx16, m->enc_site(l, 1));
     attention_bwd(ctx, enc_attention(m, a.qkv, L.kind), T, a.ctx, a.lse, m->dctx, m->dqkv,
-                  m->produce(m->dref(m->enc_site(l, 0)), 6));
+                  m->produce(m->dref(m->enc_site(l, 0)), 6), m->aref(m->enc_site(l, 4)), m->dref(m->enc_site(l, 4)));
     const float* normed = L.attn_norm >= 0 ? a.normed : a.x;
     const int an = m->enc_site(l, 0);
     if (!need_input) {
@@ -837,7 +840,8 @@ void head_backward(laya_model* m, int j) {
     }
     linear_backward(m, a.ctx, datt, T, d, d, H.out_proj, H.out_proj_b, m->dctx, nullptr, a.ctx16,
                     m->head_site(j, 1));
-    attention_bwd(ctx, head_attention(m, a.qkv, j, p, m->seed), T, a.ctx, a.lse, m->dctx, m->dqkv);
+    attention_bwd(ctx, head_attention(m, a.qkv, j, p, m->seed), T, a.ctx, a.lse, m->dctx, m->dqkv, nullptr,
+                  m->aref(m->head_site(j, 4)), m->dref(m->head_site(j, 4)));
     linear_backward(m, a.n1, m->dqkv, T, d, 3 * d, H.in_proj, H.in_proj_b, m->dn, nullptr, a.n1_16,
                     m->head_site(j, 0));
     ln_backward(m, a.x, T, d, H.norm1, H.norm1_b, 1e-5f, m->dn, m->dS, a.mean1, a.rstd1);

@@ -46,9 +46,9 @@ class Context:
 
     # Products that take bf16 operands under each policy: forward (y = x·Wᵀ), input gradient (dx = dy·W),
     # weight gradient (dW += dyᵀ·x).
-    MATMUL_POLICIES = {"fp32": 0, "fp32-mfma": 8, "fp32-split3": 112, "fp32-split3-forward": 16,
-                       "fp32-split3-backward": 96, "bf16": 7, "bf16-forward": 1, "bf16-backward": 6,
-                       "bf16-weight-grad": 4}
+    MATMUL_POLICIES = {"fp32": 0, "fp32-mfma": 8, "fp32-split3": 240, "fp32-split3-forward": 16,
+                       "fp32-split3-backward": 96, "fp32-split3-attention": 128, "bf16": 7, "bf16-forward": 1,
+                       "bf16-backward": 6, "bf16-weight-grad": 4}
 
     def set_matmul_precision(self, precision: str) -> None:
         """The operand precision of the matrix products launched afterwards: 'fp32' (default: fp32-accurate

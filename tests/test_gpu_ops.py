@@ -308,11 +308,12 @@ ATTENTION_CASES = [
 ]
 
 
-@pytest.mark.parametrize("policy", ["fp32", "fp32-mfma"])
+@pytest.mark.parametrize("policy", ["fp32", "fp32-split3", "fp32-mfma"])
 @pytest.mark.parametrize("hd,heads,lengths,hw,theta,p", ATTENTION_CASES)
 def test_attention_forward_and_backward(ctx, hd, heads, lengths, hw, theta, p, policy):
-    """Both fp32 implementations (split products on the bf16 matrix cores for head_dim 64, the default;
-    the fp32 matrix cores) at the fp64 oracle's result to 1e-5."""
+    """Every fp32 implementation at the fp64 oracle's result to 1e-5: for head_dim 64 two-piece fp16
+    products of scaled operands (the default) or three-piece bf16 splits on the 16-bit matrix cores, else
+    (and under fp32-mfma) the fp32 matrix cores."""
     print(f"attention hd={hd} heads={heads} lengths={lengths} hw={hw} theta={theta} p={p} {policy}", flush=True)
     ctx.set_matmul_precision(policy)
     rng = np.random.default_rng(hd * 1000 + sum(lengths))
