@@ -40,10 +40,10 @@ def ctx():
     c.close()
 
 
-# The 256-wide kernels each fp32 policy runs: two-piece fp16 products (the default) or three-piece bf16
-# splits everywhere.
-KERNELS = {"fp32": ("gemm_bwd_pair_h2w", "gemm_nt_h2w", "gemm_nt_h2t"),
-           "fp32-split3": ("gemm_bwd_pair_x6w", "gemm_nt_x6w", "gemm_nt_x6t")}
+# The 256-wide GEMM kernels and the attention dK/dV kernel each fp32 policy runs: two-piece fp16 products
+# (the default) or three-piece bf16 splits everywhere.
+KERNELS = {"fp32": ("gemm_bwd_pair_h2w", "gemm_nt_h2w", "gemm_nt_h2t", "attention_bwd_dkv_h2"),
+           "fp32-split3": ("gemm_bwd_pair_x6w", "gemm_nt_x6w", "gemm_nt_x6t", "attention_bwd_dkv_x6")}
 
 
 def _step(ctx, workload, policy="fp32"):
@@ -93,7 +93,7 @@ def test_headline_batch_32x512_every_gradient_matches_fp64(ctx, policy):
     print(f"full size: ModernBERT-base 22 layers, batch 32 x 512 padded (14344 tokens), {policy}", flush=True)
     m, fx, batch, logits, prof = _step(ctx, "b32x512", policy)
     assert np.abs(logits - fx["logits"]).max() < 1e-4
-    pair, wide, tall = KERNELS[policy]
+    pair, wide, tall, _ = KERNELS[policy]
     # The wide kernels this workload's timing rests on are the ones under test.
     assert prof.get(pair, {}).get("launches", 0) >= 90, sorted(prof)
     # At 14,344 rows the 2304-wide products would need a third round of 256 × 256 tiles, so they and the
@@ -110,7 +110,7 @@ def test_long_context_batch_2x8192_every_gradient_matches_fp64(ctx, policy):
     print(f"full size: ModernBERT-base 22 layers, batch 2 x 8192 (16384 tokens), {policy}", flush=True)
     m, fx, batch, logits, prof = _step(ctx, "b2x8192", policy)
     assert np.abs(logits - fx["logits"]).max() < 1e-4
-    assert prof.get("attention_bwd_dkv_x6", {}).get("launches", 0) == 24, sorted(prof)
+    assert prof.get(KERNELS[policy][3], {}).get("launches", 0) == 24, sorted(prof)
     # 16,384 rows: the RoPE-fused QKV products run on 192 × 256 tiles (three rounds of 256 × 256 tiles
     # or five of 128 × 128 would take longer).
     assert prof.get(KERNELS[policy][2], {}).get("launches", 0) >= 22, sorted(prof)
