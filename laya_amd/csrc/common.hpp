@@ -245,6 +245,8 @@ enum class GemmEpilogue {
 
 // A16 / B16: optional bf16 copies of A / B (rounded to nearest even, same leading dimensions) that a bf16
 // product reads instead of rounding A / B itself; the result is the same.
+// amax_c / amax_dx (optional): the output's magnitude word group, folded in by the two-piece kernels'
+// epilogues or measured after the product.
 // A max|operand| word group (AMAX_GROUP words) kept by a caller for the two-piece fp16 products: `word`
 // on the device, `*known` on the host says whether it holds the operand's current value. A product that
 // needs it and finds it unknown measures the operand into it (and sets *known): an unknown group must
@@ -257,21 +259,25 @@ struct AmaxRef {
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
           const float* B, long ldb, float* C, long ldc, const float* bias = nullptr, const float* R = nullptr,
           long ldr = 0, const __bf16* A16 = nullptr, const __bf16* B16 = nullptr, AmaxRef amax_a = {},
-          AmaxRef amax_b = {});
+          AmaxRef amax_b = {}, unsigned* amax_c = nullptr);
 
 // y = x·Wᵀ + b for x [M, K], W [N, K] with RoPE applied in the epilogue to output columns [0, rope_cols)
 // taken as heads of 64 (d and d + 32 rotated at position pos[row]; tables [positions][32]). The fused
 // QKV projection: q and k leave the GEMM already rotated (Ops.cs:297-313).
 void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* B, float* C, const float* bias,
                const int* pos, const float* cos_t, const float* sin_t, int rope_cols, const __bf16* A16 = nullptr,
-               const __bf16* B16 = nullptr, AmaxRef amax_a = {}, AmaxRef amax_b = {});
+               const __bf16* B16 = nullptr, AmaxRef amax_a = {}, AmaxRef amax_b = {}, unsigned* amax_c = nullptr);
 
 // The two products of Ops.LinearBackward in one launch: dx = dy·W (+ dx_residual) and dW += dyᵀ·x,
 // for dy [rows, out], W [out, in], x [rows, in]; split-K partials of dW reduced in a fixed order.
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
                         float* dx, const float* dx_residual, float* dW, const __bf16* W16 = nullptr,
                         const __bf16* x16 = nullptr, AmaxRef amax_dy = {}, AmaxRef amax_W = {},
-                        AmaxRef amax_x = {});
+                        AmaxRef amax_x = {}, unsigned* amax_dx = nullptr);
+void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W,
+                             const float* x, float* dx, const float* dx_residual, float* dW, const __bf16* W16,
+                             const __bf16* x16, AmaxRef amax_dy, AmaxRef amax_W, AmaxRef amax_x, unsigned* amax_dx,
+                             bool* folded);
 
 // max|x| over the finite elements of a rows x cols operand (row stride ld), folded into the word group
 // at out by atomicMax as fp32 bit patterns (the two-piece products' operand scales).

@@ -67,6 +67,8 @@ struct GemmParams {
     // absmax_kernel before the product), from which each kernel takes its operands' power-of-two scales.
     const unsigned* amax_a;
     const unsigned* amax_b;
+    // Optional magnitude word group of C, folded in by the two-piece kernels' epilogues (max|stored value|).
+    unsigned* amax_c;
 };
 
 // ------------------------------------------------------------------------------ shared pieces
@@ -177,9 +179,10 @@ __device__ __forceinline__ void mma_stage(const float* As, const float* Bs, f32x
 // stores, so a load issued after stores waits for all of them, and interleaving load-add-store per
 // element would serialise the epilogue. Each element is read and written by its own lane only, so
 // this order is also right when R is C.
-template <bool AK, bool BKC, int MODE, bool RES, bool GUARD, bool VEC2, int NI>
+// AMX: also fold max|stored value| (amax_bits) into *am.
+template <bool AK, bool BKC, int MODE, bool RES, bool GUARD, bool VEC2, int NI, bool AMX = false>
 __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[NI][2], int wm,
-                                          int wn, int lr, int kh) {
+                                          int wn, int lr, int kh, unsigned* am = nullptr) {
     static_assert(AK || NI == 2, "three row groups are a k-contiguous layout");
     auto rowoff = [&](int i, int r) {
         const int q = 8 * (r >> 2) + kh + (r & 3);
@@ -228,8 +231,15 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
                 const int row = rowoff(i, r);
                 if (GUARD && c.m0 + row >= p.M) continue;
                 const float a = acc[i][0][r] + bj[0], b = acc[i][1][r] + bj[1];
-                if (!GUARD || c.n0 + coloff(0) < p.N) base[row * ldo + coloff(0)] = a * cs[r] - b * sn[r];
-                if (!GUARD || c.n0 + coloff(1) < p.N) base[row * ldo + coloff(1)] = b * cs[r] + a * sn[r];
+                const float v0 = a * cs[r] - b * sn[r], v1 = b * cs[r] + a * sn[r];
+                if (!GUARD || c.n0 + coloff(0) < p.N) {
+                    base[row * ldo + coloff(0)] = v0;
+                    if constexpr (AMX) *am = max(*am, amax_bits(v0));
+                }
+                if (!GUARD || c.n0 + coloff(1) < p.N) {
+                    base[row * ldo + coloff(1)] = v1;
+                    if constexpr (AMX) *am = max(*am, amax_bits(v1));
+                }
             }
         }
         return;
@@ -252,6 +262,7 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
                 f32x2 v = {acc[i][0][r] + bj[0], acc[i][1][r] + bj[1]};
                 if (READS) v += add[r];
                 *reinterpret_cast<f32x2*>(base + rowoff(i, r) * ldo + col) = v;
+                if constexpr (AMX) *am = max(*am, max(amax_bits(v[0]), amax_bits(v[1])));
             }
         }
         return;
@@ -277,6 +288,7 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, const TileCoord& 
                 float v = acc[i][j][r] + bj[j];
                 if (READS) v += add[j][r];
                 base[rowoff(i, r) * ldo + coloff(j)] = v;
+                if constexpr (AMX) *am = max(*am, amax_bits(v));
             }
     }
 }
@@ -1085,6 +1097,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     f32x16* park = reinterpret_cast<f32x16*>(&smem[0][0][0]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) park[q * WT_THREADS + te] = acc[1][q >> 1][q & 1];
+    unsigned am = 0;  // max|C| of the lane's stores, when the product keeps C's magnitude word
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         TileCoord cs = c;
@@ -1094,11 +1107,22 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) acc[1][q >> 1][q & 1] = park[q * WT_THREADS + te];
         }
-        if (cs.m0 + 128 <= p.M && c.n0 + WT <= p.N)
+        const bool full = cs.m0 + 128 <= p.M && c.n0 + WT <= p.N;
+        // (Not with the RoPE epilogue, whose registers it would spill: launch_wide measures C afterwards.)
+        if (NP == 2 && MODE != STORE_ROPE && p.amax_c) {
+            if (full)
+                store_acc<true, true, MODE, false, false, true, 2, true>(p, cs, acc[s], we >> 2, we & 3, le & 31,
+                                                                         (le >> 5) << 2, &am);
+            else
+                store_acc<true, true, MODE, false, true, true, 2, true>(p, cs, acc[s], we >> 2, we & 3, le & 31,
+                                                                        (le >> 5) << 2, &am);
+        } else if (full) {
             store_acc<true, true, MODE, false, false, true>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2);
-        else
+        } else {
             store_acc<true, true, MODE, false, true, true>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2);
+        }
     }
+    if constexpr (NP == 2) block_amax_fold(am, p.amax_c);
 }
 
 // ------------------------------------------------------------- operand magnitudes for two-piece products
@@ -1300,10 +1324,21 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     // wave's three groups at 96·wm + 32·i.
     TileCoord cs = c;
     cs.m0 = c.m0 + 32 * wme;
-    if (c.m0 + TM <= p.M && c.n0 + WT <= p.N)
+    const bool full = c.m0 + TM <= p.M && c.n0 + WT <= p.N;
+    unsigned am = 0;  // max|C| of the lane's stores, when the product keeps C's magnitude word
+    if (NP == 2 && p.amax_c) {
+        if (full)
+            store_acc<true, true, MODE, RES, false, true, 3, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2,
+                                                                   &am);
+        else
+            store_acc<true, true, MODE, RES, true, true, 3, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2,
+                                                                  &am);
+    } else if (full) {
         store_acc<true, true, MODE, RES, false, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
-    else
+    } else {
         store_acc<true, true, MODE, RES, true, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
+    }
+    if constexpr (NP == 2) block_amax_fold(am, p.amax_c);
 }
 
 // The fp32 product from bf16 pieces; accumulators in the k-contiguous layout whatever the operands' form.
@@ -1660,6 +1695,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         px = PairScales(nn.amax_a, nn.amax_b);
         pw = PairScales(nn.amax_a, tn.amax_b);
     }
+    unsigned am = 0;  // max|dX| of the lane's stores, when the product keeps dX's magnitude word
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];
     const int g = xcd_logical_block();
     const int count = s.q + (g < s.r ? 1 : 0);
@@ -1700,12 +1736,21 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
 #pragma unroll
                 for (int q = 0; q < 4; ++q) acc[1][q >> 1][q & 1] = park[q * WT_THREADS + te];
             }
-            if (cs.m0 + 128 <= nn.M && c.n0 + WT <= nn.N)
+            const bool full = cs.m0 + 128 <= nn.M && c.n0 + WT <= nn.N;
+            if (NP == 2 && !RES && nn.amax_c) {  // (with a residual the host measures dX afterwards)
+                if (full)
+                    store_acc<true, true, STORE, RES, false, true, 2, true>(nn, cs, acc[h], we >> 2, we & 3, le & 31,
+                                                                           (le >> 5) << 2, &am);
+                else
+                    store_acc<true, true, STORE, RES, true, true, 2, true>(nn, cs, acc[h], we >> 2, we & 3, le & 31,
+                                                                          (le >> 5) << 2, &am);
+            } else if (full) {
                 store_acc<true, true, STORE, RES, false, true>(nn, cs, acc[h], we >> 2, we & 3, le & 31,
                                                                (le >> 5) << 2);
-            else
+            } else {
                 store_acc<true, true, STORE, RES, true, true>(nn, cs, acc[h], we >> 2, we & 3, le & 31,
                                                               (le >> 5) << 2);
+            }
         }
         if constexpr (RES) lds_barrier();  // every park slot is read before the next stages overwrite them
     }
@@ -1726,6 +1771,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_pair_wide_kernel(GemmParam
         write_partial_w(s.partial + ((long)g * 2 + (u == lo ? 0 : 1)) * (WT * WT), acc);
         u += b0 - a0;
     }
+    if constexpr (NP == 2) block_amax_fold(am, nn.amax_c);
 }
 
 // dW += the partials of the workers that shared each wide dW tile, summed in worker order. Block (t, q)
@@ -2209,6 +2255,8 @@ void launch_wide(laya_ctx* ctx, GemmParams p) {
         else
             hipLaunchKernelGGL((gemm_x6w_kernel<STORE, 2>), g, b, 0, ctx->stream, p);
         check_launch("gemm_x6w_kernel");
+        // The RoPE epilogue does not fold C's magnitude in: measure it here.
+        if (p.mode == STORE_ROPE && p.amax_c) absmax_into(ctx, p.C, p.M, p.N, p.ldc, p.amax_c);
         return;
     }
     profile_rename("gemm_nt_x6w");
@@ -2405,7 +2453,7 @@ const unsigned* operand_amax_ref(laya_ctx* ctx, AmaxRef r, int slot, const float
 
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,
           const float* B, long ldb, float* C, long ldc, const float* bias, const float* R, long ldr,
-          const __bf16* A16, const __bf16* B16, AmaxRef amax_a, AmaxRef amax_b) {
+          const __bf16* A16, const __bf16* B16, AmaxRef amax_a, AmaxRef amax_b, unsigned* amax_c) {
     if (M == 0 || N == 0) return;
     GemmParams p = make_params(M, N, K, A, lda, B, ldb, C, ldc, bias, R, ldr);
     p.A16 = A16;
@@ -2428,8 +2476,12 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
     if (layout == GemmLayout::NT && (ctx->matmul_pair & 1) && !(ctx->matmul_bf16 & 1) && (ctx->matmul_split & 1) &&
         gemm_fits_h(p, true, true) && operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K) &&
         operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K) &&
-        (wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks)) || tall_tiles_pay(ctx, p)))
+        (wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks)) || tall_tiles_pay(ctx, p))) {
         prepare_pair_nt(ctx, p, amax_a, amax_b);
+        p.amax_c = amax_c;
+    }
+    // C's magnitude: folded in by a two-piece kernel's epilogue, else measured after the product.
+    const bool measure = amax_c && !p.amax_c;
     {
         static const char* names[3][3] = {{"gemm_nt", "gemm_nn", "gemm_tn"},
                                           {"gemm_nt_bf16", "gemm_nn_bf16", "gemm_tn_bf16"},
@@ -2449,57 +2501,64 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
         hipLaunchKernelGGL(splitk_store_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
                            p.splits, M, N, C, ldc, bias, R, ldr);
         check_launch("splitk_store_kernel");
-        return;
+    } else {
+        finish_accumulate(ctx, p, out, ldc);
     }
-    finish_accumulate(ctx, p, out, ldc);
+    if (measure) absmax_into(ctx, C, M, N, ldc, amax_c);
 }
 
 void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* B, float* C, const float* bias,
                const int* pos, const float* cos_t, const float* sin_t, int rope_cols, const __bf16* A16,
-               const __bf16* B16, AmaxRef amax_a, AmaxRef amax_b) {
+               const __bf16* B16, AmaxRef amax_a, AmaxRef amax_b, unsigned* amax_c) {
     if (M == 0 || N == 0) return;
     GemmParams p = make_params(M, N, K, A, K, B, K, C, N, bias, nullptr, 0);
-    p.A16 = A16;
-    p.B16 = B16;
-    LAYA_REQUIRE(gemm_fast(p, true, true), "gemm_rope: operands must allow the vectorised kernel");
-    LAYA_REQUIRE(rope_cols % 64 == 0 && rope_cols <= N && pos && cos_t && sin_t, "gemm_rope: bad rotary layout");
-    p.mode = STORE_ROPE;
-    p.rope_pos = pos;
-    p.rope_cos = cos_t;
-    p.rope_sin = sin_t;
-    p.rope_cols = rope_cols;
-    if (ctx->matmul_bf16 & 1) {
-        ProfileScope scope(ctx, "gemm_nt_bf16", 2.0 * M * N * (double)K, 0.0);
-        if (wide_tiles_pay(ctx, p, false)) {
-            launch_wide_h(ctx, p);
+    [&] {
+        p.A16 = A16;
+        p.B16 = B16;
+        LAYA_REQUIRE(gemm_fast(p, true, true), "gemm_rope: operands must allow the vectorised kernel");
+        LAYA_REQUIRE(rope_cols % 64 == 0 && rope_cols <= N && pos && cos_t && sin_t, "gemm_rope: bad rotary layout");
+        p.mode = STORE_ROPE;
+        p.rope_pos = pos;
+        p.rope_cos = cos_t;
+        p.rope_sin = sin_t;
+        p.rope_cols = rope_cols;
+        if (ctx->matmul_bf16 & 1) {
+            ProfileScope scope(ctx, "gemm_nt_bf16", 2.0 * M * N * (double)K, 0.0);
+            if (wide_tiles_pay(ctx, p, false)) {
+                launch_wide_h(ctx, p);
+                return;
+            }
+            hipLaunchKernelGGL((gemm_bf16_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
+                               dim3(THREADS), 0, ctx->stream, p);
+            check_launch("gemm_bf16_kernel");
             return;
         }
-        hipLaunchKernelGGL((gemm_bf16_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
-                           dim3(THREADS), 0, ctx->stream, p);
-        check_launch("gemm_bf16_kernel");
-        return;
-    }
-    if (ctx->matmul_split & 1) {
-        if ((ctx->matmul_pair & 1) && (wide_tiles_pay(ctx, p, false) || tall_tiles_pay(ctx, p)))
-            prepare_pair_nt(ctx, p, amax_a, amax_b);
-        ProfileScope scope(ctx, "gemm_nt_x6", 2.0 * M * N * (double)K, 0.0);
-        if (wide_tiles_pay(ctx, p, false)) {
-            launch_wide(ctx, p);
+        if (ctx->matmul_split & 1) {
+            if ((ctx->matmul_pair & 1) && (wide_tiles_pay(ctx, p, false) || tall_tiles_pay(ctx, p))) {
+                prepare_pair_nt(ctx, p, amax_a, amax_b);
+                p.amax_c = amax_c;
+            }
+            ProfileScope scope(ctx, "gemm_nt_x6", 2.0 * M * N * (double)K, 0.0);
+            if (wide_tiles_pay(ctx, p, false)) {
+                launch_wide(ctx, p);
+                return;
+            }
+            if (tall_tiles_pay(ctx, p)) {
+                launch_tall(ctx, p);
+                return;
+            }
+            hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
+                               dim3(THREADS), 0, ctx->stream, p);
+            check_launch("gemm_x6_kernel");
             return;
         }
-        if (tall_tiles_pay(ctx, p)) {
-            launch_tall(ctx, p);
-            return;
-        }
-        hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
-                           dim3(THREADS), 0, ctx->stream, p);
-        check_launch("gemm_x6_kernel");
-        return;
-    }
-    ProfileScope scope(ctx, "gemm_nt", 2.0 * M * N * (double)K, 0.0);
-    hipLaunchKernelGGL((gemm_kernel<true, true, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n), dim3(THREADS), 0,
-                       ctx->stream, p);
-    check_launch("gemm_kernel");
+        ProfileScope scope(ctx, "gemm_nt", 2.0 * M * N * (double)K, 0.0);
+        hipLaunchKernelGGL((gemm_kernel<true, true, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n), dim3(THREADS), 0,
+                           ctx->stream, p);
+        check_launch("gemm_kernel");
+    }();
+    // C's magnitude: folded in by a two-piece kernel's epilogue, else measured after the product.
+    if (amax_c && !p.amax_c) absmax_into(ctx, C, M, N, N, amax_c);
 }
 
 // The balanced static schedule of a backward pair, when every worker's whole dX tiles fit in its share of
@@ -2542,8 +2601,10 @@ bool make_pair_plan_wide(const laya_ctx* ctx, int n0, int out, int n1, int rows,
 
 // The wide pair for split products: dX without residual, dX's K a multiple of 16, dY k-contiguous in
 // float4s. Returns false (nothing launched) when the wide plan does not apply.
+// amax_dx (optional): dX's magnitude word group, folded in by the two-piece kernel (*folded set), else
+// left to the caller.
 bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, int in, int out, bool half,
-                        AmaxRef amax_dy, AmaxRef amax_W, AmaxRef amax_x) {
+                        AmaxRef amax_dy, AmaxRef amax_W, AmaxRef amax_x, unsigned* amax_dx, bool* folded) {
     const bool bh = half && nn.B16 && tn.B16;  // W and x from their bf16 copies
     if (out % BKQ != 0 || !operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) return false;
     const long lim = 1L << 31;  // buffer offsets of dY, W and x
@@ -2561,6 +2622,8 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
         nn.amax_a = tn.amax_a = operand_amax(ctx, amax_dy, 0, nn.A, rows, out, nn.lda);
         nn.amax_b = operand_amax(ctx, amax_W, 1, nn.B, out, in, nn.ldb);
         tn.amax_b = operand_amax(ctx, amax_x, 2, tn.B, rows, in, tn.ldb);
+        nn.amax_c = nn.R ? nullptr : amax_dx;
+        *folded = nn.amax_c != nullptr;
     }
     {
         ProfileScope scope(ctx, half ? "gemm_bwd_pair_bf16w" : pair ? "gemm_bwd_pair_h2w" : "gemm_bwd_pair_x6w",
@@ -2605,7 +2668,18 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
 
 void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W, const float* x,
                         float* dx, const float* dx_residual, float* dW, const __bf16* W16, const __bf16* x16,
-                        AmaxRef amax_dy, AmaxRef amax_W, AmaxRef amax_x) {
+                        AmaxRef amax_dy, AmaxRef amax_W, AmaxRef amax_x, unsigned* amax_dx) {
+    bool folded = false;
+    gemm_backward_pair_body(ctx, rows, in, out, dy, W, x, dx, dx_residual, dW, W16, x16, amax_dy, amax_W, amax_x,
+                            amax_dx, &folded);
+    // dX's magnitude: folded in by the two-piece pair's epilogue, else measured after the products.
+    if (amax_dx && !folded && rows > 0) absmax_into(ctx, dx, rows, in, in, amax_dx);
+}
+
+void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const float* dy, const float* W,
+                             const float* x, float* dx, const float* dx_residual, float* dW, const __bf16* W16,
+                             const __bf16* x16, AmaxRef amax_dy, AmaxRef amax_W, AmaxRef amax_x, unsigned* amax_dx,
+                             bool* folded) {
     if (rows == 0) return;
     // dx[rows, in] = dy[rows, out] · W[out, in]       (NN, K = out)
     GemmParams nn = make_params(rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual, in);
@@ -2620,7 +2694,9 @@ void gemm_backward_pair(laya_ctx* ctx, int rows, int in, int out, const float* d
                       gemm_fast(tn, false, false);
     const bool half = (ctx->matmul_bf16 & 6) == 6 && gemm_fits_h(nn, true, false) && gemm_fits_h(tn, false, false);
     tn.mode = ACCUMULATE;
-    if ((split || half) && backward_pair_wide(ctx, nn, tn, rows, in, out, half, amax_dy, amax_W, amax_x)) return;
+    if ((split || half) &&
+        backward_pair_wide(ctx, nn, tn, rows, in, out, half, amax_dy, amax_W, amax_x, amax_dx, folded))
+        return;
     tn.mode = STORE;
     const int n0 = nn.tiles_m * nn.tiles_n, n1 = tn.tiles_m * tn.tiles_n;
     PairPlan s{};

@@ -203,6 +203,12 @@ struct laya_model {
         *r.known = 1;
         return r.word;
     }
+    // The same for attention's operands (qkv, the context gradient), read as two-piece products.
+    unsigned* produce_attention(laya::AmaxRef r) {
+        if (!r.word || !ctx->attention_pair) return nullptr;
+        *r.known = 1;
+        return r.word;
+    }
     // Five sites per layer: k = 0 … 3 the four products (their inputs' words, and in the backward their
     // output gradients'), k = 4 attention (qkv's word, and in the backward the context gradient's).
     int enc_site(int l, int k) const { return 5 * l + k; }
@@ -626,25 +632,27 @@ AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p
     return a;
 }
 
-// x16: x's bf16 copy, or null; ax: x's magnitude word.
+// x16: x's bf16 copy, or null; ax: x's magnitude word; ay (optional): y's, to fold y into.
 void linear(laya_model* m, const float* x, int rows, int in, int wi, int bi, int out, const float* residual, float* y,
-            const __bf16* x16 = nullptr, AmaxRef ax = {}) {
+            const __bf16* x16 = nullptr, AmaxRef ax = {}, unsigned* ay = nullptr) {
     gemm(m->ctx, GemmLayout::NT, GemmEpilogue::Store, rows, out, in, x, in, m->W(wi), in, y, out, m->W(bi), residual,
-         out, x16, m->W16(wi), ax, m->wref(wi));
+         out, x16, m->W16(wi), ax, m->wref(wi), ay);
 }
 
 // Ops.LinearBackward (Ops.cs:33-69): dx = dy·W (overwrite; + residual when given), dW += dyᵀ·x, db += Σ dy.
-// site: the product's magnitude-word site (its input's word and its output gradient's), or -1.
+// site: the product's magnitude-word site (its input's word and its output gradient's), or -1; adx
+// (optional): dx's magnitude word, to fold dx into.
 void linear_backward(laya_model* m, const float* x, const float* dy, int rows, int in, int out, int wi, int bi,
-                     float* dx, const float* dx_residual = nullptr, const __bf16* x16 = nullptr, int site = -1) {
+                     float* dx, const float* dx_residual = nullptr, const __bf16* x16 = nullptr, int site = -1,
+                     unsigned* adx = nullptr) {
     float* dW = m->Gt(wi);
     if (dx && dW) {
         gemm_backward_pair(m->ctx, rows, in, out, dy, m->W(wi), x, dx, dx_residual, dW, m->W16(wi), x16,
                            site >= 0 ? m->dref(site) : AmaxRef{}, m->wref(wi),
-                           site >= 0 ? m->aref(site) : AmaxRef{});
+                           site >= 0 ? m->aref(site) : AmaxRef{}, adx);
     } else if (dx) {
         gemm(m->ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, m->W(wi), in, dx, in, nullptr,
-             dx_residual, in, nullptr, m->W16(wi));
+             dx_residual, in, nullptr, m->W16(wi), {}, {}, adx);
     } else if (dW) {
         gemm(m->ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr,
              0, nullptr, x16);
@@ -680,9 +688,11 @@ void encoder_forward(laya_model* m, int l, bool output = true) {
     if (fused_rope(m)) {
         const laya_rotary& r = L.kind == 0 ? m->rot_global : m->rot_local;
         gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->cur.pos, r.cos_t, r.sin_t,
-                  2 * d, a.normed16, m->W16(L.wqkv), m->aref(m->enc_site(l, 0)), m->wref(L.wqkv));
+                  2 * d, a.normed16, m->W16(L.wqkv), m->aref(m->enc_site(l, 0)), m->wref(L.wqkv),
+                  m->produce_attention(m->aref(m->enc_site(l, 4))));
     } else {
-        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv, a.normed16, m->aref(m->enc_site(l, 0)));
+        linear(m, normed, T, d, L.wqkv, L.wqkv_b, 3 * d, nullptr, a.qkv, a.normed16, m->aref(m->enc_site(l, 0)),
+               m->produce_attention(m->aref(m->enc_site(l, 4))));
     }
     attention_fwd(ctx, enc_attention(m, a.qkv, L.kind), a.ctx, a.lse, a.ctx16,
                   m->produce(m->aref(m->enc_site(l, 1)), 7), m->aref(m->enc_site(l, 4)));
@@ -730,7 +740,8 @@ void forward(laya_model* m, bool train, uint64_t seed) {
         float* out = j + 1 < m->cfg.head_layers ? m->ha[j + 1].x : m->head_out;
         layernorm_fwd(ctx, a.x, T, d, m->W(H.norm1), m->W(H.norm1_b), 1e-5f, a.n1, a.mean1, a.rstd1, nullptr,
                       nullptr, nullptr, a.n1_16, m->produce(m->aref(m->head_site(j, 0)), 7));
-        linear(m, a.n1, T, d, H.in_proj, H.in_proj_b, 3 * d, nullptr, a.qkv, a.n1_16, m->aref(m->head_site(j, 0)));
+        linear(m, a.n1, T, d, H.in_proj, H.in_proj_b, 3 * d, nullptr, a.qkv, a.n1_16, m->aref(m->head_site(j, 0)),
+               m->produce_attention(m->aref(m->head_site(j, 4))));
         attention_fwd(ctx, head_attention(m, a.qkv, j, p, seed), a.ctx, a.lse, a.ctx16,
                       m->produce(m->aref(m->head_site(j, 1)), 7), m->aref(m->head_site(j, 4)));
         if (p > 0.0f) {
@@ -791,7 +802,8 @@ void encoder_backward(laya_model* m, int l, bool need_input) {
     linear_backward(m, a.mlpn, m->dwide, T, d, 2 * I, L.wi, L.wi_b, m->dn, nullptr, a.mlpn16, m->enc_site(l, 2));
     ln_backward(m, a.res, T, d, L.mlp_norm, L.mlp_norm_b, eps, m->dn, m->dS, a.mean2, a.rstd2, nullptr,
                 m->produce(m->dref(m->enc_site(l, 1)), 6));
-    linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx, nullptr, a.ctx16, m->enc_site(l, 1));
+    linear_backward(m, a.ctx, m->dS, T, d, d, L.wo, L.wo_b, m->dctx, nullptr, a.ctx16, m->enc_site(l, 1),
+                    m->produce_attention(m->dref(m->enc_site(l, 4))));
     attention_bwd(ctx, enc_attention(m, a.qkv, L.kind), T, a.ctx, a.lse, m->dctx, m->dqkv,
                   m->produce(m->dref(m->enc_site(l, 0)), 6), m->aref(m->enc_site(l, 4)), m->dref(m->enc_site(l, 4)));
     const float* normed = L.attn_norm >= 0 ? a.normed : a.x;
@@ -839,7 +851,7 @@ void head_backward(laya_model* m, int j) {
         datt = m->dy;
     }
     linear_backward(m, a.ctx, datt, T, d, d, H.out_proj, H.out_proj_b, m->dctx, nullptr, a.ctx16,
-                    m->head_site(j, 1));
+                    m->head_site(j, 1), m->produce_attention(m->dref(m->head_site(j, 4))));
     attention_bwd(ctx, head_attention(m, a.qkv, j, p, m->seed), T, a.ctx, a.lse, m->dctx, m->dqkv, nullptr,
                   m->aref(m->head_site(j, 4)), m->dref(m->head_site(j, 4)));
     linear_backward(m, a.n1, m->dqkv, T, d, 3 * d, H.in_proj, H.in_proj_b, m->dn, nullptr, a.n1_16,
