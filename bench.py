@@ -55,7 +55,7 @@ def mfma_peaks(name: str):
     compute them from two-piece fp16 splits of power-of-two-scaled operands: three fp16 MFMA products per
     fp32 one (fp16 and bf16 share the 2.5 PFLOP/s dense peak), peak over three. *_bf16 / *_bf16w run bf16
     operands (one product each). The rest run the fp32 matrix cores."""
-    base = name[:-1] if name.endswith(("_x6w", "_x6t", "_bf16w", "_h2w", "_h2t")) else name
+    base = name[:-1] if name.endswith(("_x6w", "_x6t", "_bf16w", "_h2w", "_h2t", "_h2q")) else name
     if base.endswith("_x6"):
         return PEAK_BF16_MFMA / 6, 6.0
     if base.endswith("_h2"):

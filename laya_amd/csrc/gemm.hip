@@ -707,6 +707,36 @@ __device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord
     __syncthreads();
 }
 
+// The power-of-two operand scales 2^ea, 2^eb of a two-piece fp16 product; the accumulators are scaled
+// back by 2^-(ea+eb) with one exact ldexp each.
+struct PairScales {
+    float sa = 1.0f, sb = 1.0f;
+    int ex = 0;
+    __device__ __forceinline__ PairScales() = default;
+    __device__ __forceinline__ PairScales(const unsigned* amax_a, const unsigned* amax_b) {
+        const int ea = pair_scale_exp(amax_group_max(amax_a)), eb = pair_scale_exp(amax_group_max(amax_b));
+        sa = exp2_int(ea);
+        sb = exp2_int(eb);
+        ex = -(ea + eb);
+    }
+    __device__ __forceinline__ void unscale(f32x16& a) const {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) a[i] = __builtin_amdgcn_ldexpf(a[i], ex);
+    }
+    template <int A, int B>
+    __device__ __forceinline__ void unscale(f32x16 (&acc)[A][B]) const {
+#pragma unroll
+        for (int i = 0; i < A; ++i)
+#pragma unroll
+            for (int j = 0; j < B; ++j) unscale(acc[i][j]);
+    }
+    template <int A, int B, int C>
+    __device__ __forceinline__ void unscale(f32x16 (&acc)[A][B][C]) const {
+#pragma unroll
+        for (int i = 0; i < A; ++i) unscale(acc[i]);
+    }
+};
+
 // Split products with 16-deep K stages, three workgroups per CU: half the LDS (36 KB) and half the staging
 // registers of the 32-deep form, for grids that fill the chip in one round at three per CU but not at two
 // (e.g. 654 tiles: one round on 768 slots instead of two on 512). k-contiguous float4 operands only.
@@ -737,18 +767,50 @@ struct OperandQ {
             reg[i] = k < kend ? v : f32x4{0, 0, 0, 0};
         }
     }
-    __device__ __forceinline__ void store(__bf16* lds, int tid) const {
+    // NP = 3: the three split planes; NP = 2: the two fp16 planes of sc·x.
+    template <int NP = 3>
+    __device__ __forceinline__ void store(__bf16* lds, int tid, float sc = 1.0f) const {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            bf16x4 h1, h2, h3;
-            split3_4(reg[i], h1, h2, h3);
             const int o = ((tid >> 2) + 64 * i) * KPADQ + ((tid & 3) << 2);
-            *reinterpret_cast<bf16x4*>(lds + o) = h1;
-            *reinterpret_cast<bf16x4*>(lds + STAGE_Q + o) = h2;
-            *reinterpret_cast<bf16x4*>(lds + 2 * STAGE_Q + o) = h3;
+            if constexpr (NP == 2) {
+                f16x4 hi, lo;
+                split2h_4(reg[i], sc, hi, lo);
+                *reinterpret_cast<f16x4*>(lds + o) = hi;
+                *reinterpret_cast<f16x4*>(lds + STAGE_Q + o) = lo;
+            } else {
+                bf16x4 h1, h2, h3;
+                split3_4(reg[i], h1, h2, h3);
+                *reinterpret_cast<bf16x4*>(lds + o) = h1;
+                *reinterpret_cast<bf16x4*>(lds + STAGE_Q + o) = h2;
+                *reinterpret_cast<bf16x4*>(lds + 2 * STAGE_Q + o) = h3;
+            }
         }
     }
 };
+
+// The two-piece form of mma_stage_q: two fp16 planes, three products per block, the smallest first.
+__device__ __forceinline__ void mma_stage_q2(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2], int wm, int wn,
+                                             int lr, int half) {
+    f16x8 a[2][2], b[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl) {
+            a[i][pl] = *reinterpret_cast<const f16x8*>(A + pl * STAGE_Q + (wm * 64 + 32 * i + lr) * KPADQ + 8 * half);
+            b[i][pl] = *reinterpret_cast<const f16x8*>(B + pl * STAGE_Q + (wn * 64 + 32 * i + lr) * KPADQ + 8 * half);
+        }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            f32x16 c = acc[i][j];
+            c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][1], b[j][0], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][0], b[j][1], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][0], b[j][0], c, 0, 0, 0);
+            acc[i][j] = c;
+        }
+}
 
 __device__ __forceinline__ void mma_stage_q(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2], int wm, int wn,
                                             int lr, int half) {
@@ -775,9 +837,12 @@ __device__ __forceinline__ void mma_stage_q(const __bf16* A, const __bf16* B, f3
         }
 }
 
-template <int MODE, bool RES>
+// NP = 3: split products; NP = 2: two-piece fp16 products (p.amax_a, p.amax_b set).
+template <int MODE, bool RES, int NP = 3>
 __global__ __launch_bounds__(THREADS, 3) void gemm_x6q_kernel(GemmParams p) {
-    __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * STAGE_Q];
+    __shared__ __attribute__((aligned(16))) __bf16 smem[2][NP * STAGE_Q];
+    PairScales ps;
+    if constexpr (NP == 2) ps = PairScales(p.amax_a, p.amax_b);
     const TileCoord c = tile_coord(p, xcd_logical_block());
     const int len = max(0, c.ke - c.kb);
     const int nfull = len / BKQ, ntiles = nfull + (len % BKQ != 0 ? 1 : 0);
@@ -806,12 +871,16 @@ __global__ __launch_bounds__(THREADS, 3) void gemm_x6q_kernel(GemmParams p) {
     if (ntiles > 0) fetch(0);
     for (int j = 0; j < ntiles; ++j) {
         __syncthreads();
-        a.store(smem[0], tid);
-        b.store(smem[1], tid);
+        a.template store<NP>(smem[0], tid, ps.sa);
+        b.template store<NP>(smem[1], tid, ps.sb);
         __syncthreads();
         if (j + 1 < ntiles) fetch(j + 1);
-        mma_stage_q(smem[0], smem[1], acc, wm, wn, lr, half);
+        if constexpr (NP == 2)
+            mma_stage_q2(smem[0], smem[1], acc, wm, wn, lr, half);
+        else
+            mma_stage_q(smem[0], smem[1], acc, wm, wn, lr, half);
     }
+    if constexpr (NP == 2) ps.unscale(acc);
     tile_store<true, true, MODE, RES>(p, c, acc);
 }
 
@@ -1004,35 +1073,6 @@ struct WideK<true> {
     }
 };
 
-// The power-of-two operand scales 2^ea, 2^eb of a two-piece fp16 product; the accumulators are scaled
-// back by 2^-(ea+eb) with one exact ldexp each.
-struct PairScales {
-    float sa = 1.0f, sb = 1.0f;
-    int ex = 0;
-    __device__ __forceinline__ PairScales() = default;
-    __device__ __forceinline__ PairScales(const unsigned* amax_a, const unsigned* amax_b) {
-        const int ea = pair_scale_exp(amax_group_max(amax_a)), eb = pair_scale_exp(amax_group_max(amax_b));
-        sa = exp2_int(ea);
-        sb = exp2_int(eb);
-        ex = -(ea + eb);
-    }
-    __device__ __forceinline__ void unscale(f32x16& a) const {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) a[i] = __builtin_amdgcn_ldexpf(a[i], ex);
-    }
-    template <int A, int B>
-    __device__ __forceinline__ void unscale(f32x16 (&acc)[A][B]) const {
-#pragma unroll
-        for (int i = 0; i < A; ++i)
-#pragma unroll
-            for (int j = 0; j < B; ++j) unscale(acc[i][j]);
-    }
-    template <int A, int B, int C>
-    __device__ __forceinline__ void unscale(f32x16 (&acc)[A][B][C]) const {
-#pragma unroll
-        for (int i = 0; i < A; ++i) unscale(acc[i]);
-    }
-};
 
 // NP = 3: the split (fp32) product; NP = 2: the two-piece fp16 product (fp32-accurate, scaled operands);
 // NP = 1: the bf16 product, with AH / BH reading A / B from their bf16 copies.
@@ -2319,10 +2359,17 @@ template <bool AK, bool BKC> void launch_x6(laya_ctx* ctx, const GemmParams& p, 
             launch_tall(ctx, p);
         } else if (va && vb && p.mode == STORE && three_per_cu(ctx, blocks)) {
             const dim3 g(blocks), b(THREADS);
-            if (p.R)
+            if (p.amax_a) {
+                profile_rename("gemm_nt_h2q");
+                if (p.R)
+                    hipLaunchKernelGGL((gemm_x6q_kernel<STORE, true, 2>), g, b, 0, ctx->stream, p);
+                else
+                    hipLaunchKernelGGL((gemm_x6q_kernel<STORE, false, 2>), g, b, 0, ctx->stream, p);
+            } else if (p.R) {
                 hipLaunchKernelGGL((gemm_x6q_kernel<STORE, true>), g, b, 0, ctx->stream, p);
-            else
+            } else {
                 hipLaunchKernelGGL((gemm_x6q_kernel<STORE, false>), g, b, 0, ctx->stream, p);
+            }
             check_launch("gemm_x6q_kernel");
         } else if (va && vb) launch_x<KVEC, KVEC>(ctx, p, blocks);
         else if (va) launch_x<KVEC, KSCALAR>(ctx, p, blocks);
@@ -2476,9 +2523,13 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
     if (layout == GemmLayout::NT && (ctx->matmul_pair & 1) && !(ctx->matmul_bf16 & 1) && (ctx->matmul_split & 1) &&
         gemm_fits_h(p, true, true) && operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K) &&
         operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K) &&
-        (wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks)) || tall_tiles_pay(ctx, p))) {
+        (wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks)) || tall_tiles_pay(ctx, p) ||
+         (p.mode == STORE && three_per_cu(ctx, blocks)))) {
         prepare_pair_nt(ctx, p, amax_a, amax_b);
-        p.amax_c = amax_c;
+        // The 128 x 128 kernel does not fold C's magnitude in: it is measured after the product.
+        p.amax_c = (wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks)) || tall_tiles_pay(ctx, p))
+                       ? amax_c
+                       : nullptr;
     }
     // C's magnitude: folded in by a two-piece kernel's epilogue, else measured after the product.
     const bool measure = amax_c && !p.amax_c;
