@@ -38,10 +38,12 @@ PEAK_FP32_MFMA = 157.3e12
 PEAK_HBM = 8.0e12
 # HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE and calibrated against a
 # copy-like kernel of known size (the commands and the calibration sit in
-# profiles/gemm_bwd_pair_x6w_hbm_traffic_b32x512.md). Counters cannot be read from inside the process, so the
-# figure is carried here per (workload, kernel) it was measured on and is reported only when that kernel
+# profiles/gemm_bwd_pair_h2w_hbm_traffic_b32x512.md, and for the three-piece kernel in
+# profiles/gemm_bwd_pair_x6w_hbm_traffic_b32x512.md). Counters cannot be read from inside the process, so
+# the figure is carried here per (workload, kernel) it was measured on and is reported only when that kernel
 # is the dominant one of that workload; any other case reports null.
-MEASURED_TRAFFIC = {("b32x512", "gemm_bwd_pair_x6w"): 0.865e9}
+MEASURED_TRAFFIC = {("b32x512", "gemm_bwd_pair_x6w"): 0.865e9,
+                    ("b32x512", "gemm_bwd_pair_h2w"): 0.852e9}
 
 
 PEAK_BF16_MFMA = 2.5e15
@@ -300,7 +302,7 @@ def main():
                      f"{k['bytes'] / k['ms'] / 1e6:8.1f} GB/s"), file=sys.stderr)
         name, k = max(prof.items(), key=lambda kv: kv[1]["ms"])
         per_launch_s = k["ms"] / k["launches"] / 1e3
-        traffic = MEASURED_TRAFFIC.get((args.workload, name)) if matmul == w["matmul"] else None
+        traffic = MEASURED_TRAFFIC.get((args.workload, name))
         if k["flops"]:
             achieved = k["flops"] / k["launches"] / per_launch_s
             peak, issue = mfma_peaks(name)
@@ -310,6 +312,8 @@ def main():
                         "launches": k["launches"]}
             if issue:
                 roofline["bf16_pipe_frac"] = round(achieved * issue / PEAK_BF16_MFMA, 4)
+                # fp32 products from pieces: the same throughput against the fp32 matrix-core peak
+                roofline["vs_fp32_mfma_peak"] = round(achieved / PEAK_FP32_MFMA, 4)
         else:
             achieved = k["bytes"] / k["launches"] / per_launch_s
             roofline = {"bound": "hbm", "kernel": name, "achieved": round(achieved / 1e9, 1), "peak": 8000.0,
