@@ -282,6 +282,10 @@ void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const flo
 // max|x| over the finite elements of a rows x cols operand (row stride ld), folded into the word group
 // at out by atomicMax as fp32 bit patterns (the two-piece products' operand scales).
 void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, unsigned* out);
+// Several tensors' magnitudes in one launch: block b folds max|arena[off[b] … off[b] + len[b])| (offsets 16-byte
+// aligned, device arrays of `blocks` entries) into word group word[b] of `words`; `bytes` for the profile.
+void absmax_multi(laya_ctx* ctx, const float* arena, const long* off, const int* len, const int* word, int blocks,
+                  unsigned* words, double bytes);
 // An operand's magnitude word group: the caller's r (measured now if not known yet), or the context's
 // group `slot` (0 … 5), measured now.
 const unsigned* operand_amax_ref(laya_ctx* ctx, AmaxRef r, int slot, const float* x, int rows, int cols, long ld);

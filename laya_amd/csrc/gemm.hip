@@ -640,6 +640,45 @@ __device__ __forceinline__ void store_x3(const OperandH<KIND>& op, __bf16* lds0,
     }
 }
 
+// The two-piece form of store_x3 for float4 operands: the two fp16 planes of sc·x.
+__device__ __forceinline__ void store_x2(const OperandH<KVEC>& op, __bf16* lds0, __bf16* lds1, int tid, float sc) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f16x4 hi, lo;
+        split2h_4(op.reg[i], sc, hi, lo);
+        const int o = ((tid >> 3) + 32 * i) * KPADH + ((tid & 7) << 2);
+        *reinterpret_cast<f16x4*>(lds0 + o) = hi;
+        *reinterpret_cast<f16x4*>(lds1 + o) = lo;
+    }
+}
+
+// The two-piece form of mma_stage_x6: two fp16 planes, three products per block, the smallest first.
+__device__ __forceinline__ void mma_stage_x2(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2], int wm, int wn,
+                                             int lr, int half) {
+#pragma unroll
+    for (int ks = 0; ks < BK; ks += 16) {
+        const int k = ks + 8 * half;
+        f16x8 a[2][2], b[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int pl = 0; pl < 2; ++pl) {
+                a[i][pl] = *reinterpret_cast<const f16x8*>(A + pl * STAGE_H + (wm * 64 + 32 * i + lr) * KPADH + k);
+                b[i][pl] = *reinterpret_cast<const f16x8*>(B + pl * STAGE_H + (wn * 64 + 32 * i + lr) * KPADH + k);
+            }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                f32x16 c = acc[i][j];
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][1], b[j][0], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][0], b[j][1], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][0], b[j][0], c, 0, 0, 0);
+                acc[i][j] = c;
+            }
+    }
+}
+
 __device__ __forceinline__ void mma_stage_x6(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2], int wm, int wn,
                                              int lr, int half) {
 #pragma unroll
@@ -669,9 +708,11 @@ __device__ __forceinline__ void mma_stage_x6(const __bf16* A, const __bf16* B, f
     }
 }
 
-template <int AOP, int BOP>
+// NP = 2 (float4 operands only): two-piece products with the operands' scales sa, sb.
+template <int AOP, int BOP, int NP = 3>
 __device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord& c, __bf16 (*smem)[3 * STAGE_H],
-                                            f32x16 (&acc)[2][2]) {
+                                            f32x16 (&acc)[2][2], float sa = 1.0f, float sb = 1.0f) {
+    static_assert(NP == 3 || (AOP == KVEC && BOP == KVEC), "two-piece products take float4 operands");
     const int len = max(0, c.ke - c.kb);
     const int nfull = len / BK, ntiles = nfull + (len % BK != 0 ? 1 : 0);
     const int rot = nfull > 0 ? c.t % nfull : 0;
@@ -698,11 +739,19 @@ __device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord
     if (ntiles > 0) fetch(0);
     for (int j = 0; j < ntiles; ++j) {
         __syncthreads();
-        store_x3<AOP>(a, smem[0], smem[0] + STAGE_H, smem[0] + 2 * STAGE_H, tid);
-        store_x3<BOP>(b, smem[1], smem[1] + STAGE_H, smem[1] + 2 * STAGE_H, tid);
+        if constexpr (NP == 2) {
+            store_x2(a, smem[0], smem[0] + STAGE_H, tid, sa);
+            store_x2(b, smem[1], smem[1] + STAGE_H, tid, sb);
+        } else {
+            store_x3<AOP>(a, smem[0], smem[0] + STAGE_H, smem[0] + 2 * STAGE_H, tid);
+            store_x3<BOP>(b, smem[1], smem[1] + STAGE_H, smem[1] + 2 * STAGE_H, tid);
+        }
         __syncthreads();
         if (j + 1 < ntiles) fetch(j + 1);
-        mma_stage_x6(smem[0], smem[1], acc, wm, wn, lr, half);
+        if constexpr (NP == 2)
+            mma_stage_x2(smem[0], smem[1], acc, wm, wn, lr, half);
+        else
+            mma_stage_x6(smem[0], smem[1], acc, wm, wn, lr, half);
     }
     __syncthreads();
 }
@@ -1381,13 +1430,17 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     if constexpr (NP == 2) block_amax_fold(am, p.amax_c);
 }
 
-// The fp32 product from bf16 pieces; accumulators in the k-contiguous layout whatever the operands' form.
-template <int AOP, int BOP, int MODE, bool RES>
+// The fp32 product from bf16 pieces (NP = 3) or, for float4 operands, two-piece fp16 products (NP = 2);
+// accumulators in the k-contiguous layout whatever the operands' form.
+template <int AOP, int BOP, int MODE, bool RES, int NP = 3>
 __global__ __launch_bounds__(THREADS, 2) void gemm_x6_kernel(GemmParams p) {
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * STAGE_H];
+    PairScales ps;
+    if constexpr (NP == 2) ps = PairScales(p.amax_a, p.amax_b);
     const TileCoord c = tile_coord(p, xcd_logical_block());
     f32x16 acc[2][2];
-    tile_mma_x6<AOP, BOP>(p, c, smem, acc);
+    tile_mma_x6<AOP, BOP, NP>(p, c, smem, acc, ps.sa, ps.sb);
+    if constexpr (NP == 2) ps.unscale(acc);
     tile_store<true, true, MODE, RES>(p, c, acc);
 }
 
@@ -2216,7 +2269,30 @@ bool tall_tiles_pay(const laya_ctx* ctx, const GemmParams& p) {
     return t_tall < std::min(t_two, t_three);
 }
 
+// Several tensors' magnitudes in one launch: block b covers elements [off[b], off[b] + len[b]) of the
+// arena (16-byte aligned, len a multiple of 4 but for a tensor's last block) and folds them into word group
+// word[b] of `words`.
+__global__ __launch_bounds__(256) void absmax_multi_kernel(const float* __restrict__ arena, const long* __restrict__ off,
+                                                           const int* __restrict__ len, const int* __restrict__ word,
+                                                           unsigned* words) {
+    const long o = off[blockIdx.x];
+    const int n = len[blockIdx.x];
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(arena + o);
+    unsigned m = 0;
+    for (int i = threadIdx.x; i < n / 4; i += 256) m = max(m, amax_bits4(x4[i]));
+    for (int i = (n / 4) * 4 + threadIdx.x; i < n; i += 256) m = max(m, amax_bits(arena[o + i]));
+    block_amax_fold(m, words + (long)word[blockIdx.x] * AMAX_GROUP);
+}
+
 }  // namespace
+
+void absmax_multi(laya_ctx* ctx, const float* arena, const long* off, const int* len, const int* word, int blocks,
+                  unsigned* words, double bytes) {
+    if (blocks <= 0) return;
+    ProfileScope scope(ctx, "absmax", 0.0, bytes);
+    hipLaunchKernelGGL(absmax_multi_kernel, dim3(blocks), dim3(256), 0, ctx->stream, arena, off, len, word, words);
+    check_launch("absmax_multi_kernel");
+}
 
 // max|x| of a rows x cols operand folded into *out (0 beforehand for the operand's own maximum).
 void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, unsigned* out) {
@@ -2333,6 +2409,25 @@ void launch_wide_h(laya_ctx* ctx, GemmParams p) {
 
 template <int AOP, int BOP> void launch_x(laya_ctx* ctx, const GemmParams& p, int blocks) {
     const dim3 g(blocks), b(THREADS);
+    if constexpr (AOP == KVEC && BOP == KVEC) {
+        if (p.amax_a) {  // two-piece products (NT, float4 operands)
+            profile_rename("gemm_nt_h2");
+            switch (p.mode) {
+                case STORE:
+                    if (p.R)
+                        hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE, true, 2>), g, b, 0, ctx->stream, p);
+                    else
+                        hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE, false, 2>), g, b, 0, ctx->stream, p);
+                    break;
+                case ACCUMULATE:
+                    hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, ACCUMULATE, false, 2>), g, b, 0, ctx->stream, p);
+                    break;
+                default: hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, PARTIAL, false, 2>), g, b, 0, ctx->stream, p);
+            }
+            check_launch("gemm_x6_kernel");
+            return;
+        }
+    }
     switch (p.mode) {
         case STORE:
             if (p.R)
@@ -2520,13 +2615,13 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
         }
     }
     const int blocks = tiles * p.splits;
+    // Every NT product with float4 operands (wide, tall, three-per-CU and generic tiles) takes two-piece
+    // products under the pair policy.
     if (layout == GemmLayout::NT && (ctx->matmul_pair & 1) && !(ctx->matmul_bf16 & 1) && (ctx->matmul_split & 1) &&
         gemm_fits_h(p, true, true) && operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K) &&
-        operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K) &&
-        (wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks)) || tall_tiles_pay(ctx, p) ||
-         (p.mode == STORE && three_per_cu(ctx, blocks)))) {
+        operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K)) {
         prepare_pair_nt(ctx, p, amax_a, amax_b);
-        // The 128 x 128 kernel does not fold C's magnitude in: it is measured after the product.
+        // The 128 x 128 kernels do not fold C's magnitude in: it is measured after the product.
         p.amax_c = (wide_tiles_pay(ctx, p, p.mode == STORE && three_per_cu(ctx, blocks)) || tall_tiles_pay(ctx, p))
                        ? amax_c
                        : nullptr;

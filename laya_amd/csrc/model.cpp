@@ -189,6 +189,14 @@ struct laya_model {
     // an input once per forward and reused by its backward product), the gradient words at each backward.
     unsigned* amax_words = nullptr;
     std::vector<unsigned char> amax_known;
+    // The products' weights, measured together once per forward (absmax_multi): per block the arena
+    // offset, length and parameter index (device), and the parameter indices.
+    long* wm_off = nullptr;
+    int* wm_len = nullptr;
+    int* wm_word = nullptr;
+    int wm_blocks = 0;
+    double wm_bytes = 0;
+    std::vector<int> wm_params;
     size_t amax_sites() const { return (size_t)scorer_site(2); }
     laya::AmaxRef word(size_t k) {
         return amax_words ? laya::AmaxRef{amax_words + k * laya::AMAX_GROUP, &amax_known[k]} : laya::AmaxRef{};
@@ -458,6 +466,41 @@ void ensure_activations(laya_model* m, int T, int nmark, int nseg) {
     m->cap_segs = Sc;
 }
 
+// The products' weights measured in one launch (their words cleared beforehand): the block tables are
+// made on first use (the weights' layout never changes), 16,384 values per block.
+void measure_weights(laya_model* m) {
+    if (m->wm_params.empty()) {
+        for (const auto& L : m->enc)
+            for (int i : {L.wqkv, L.wo, L.wi, L.mlp_wo}) m->wm_params.push_back(i);
+        for (const auto& H : m->head)
+            for (int i : {H.in_proj, H.out_proj, H.linear1, H.linear2}) m->wm_params.push_back(i);
+        for (int i : {m->sc1, m->sc2}) m->wm_params.push_back(i);
+        std::vector<long> off;
+        std::vector<int> len, word;
+        constexpr long CHUNK = 16384;
+        for (int i : m->wm_params) {
+            const Param& p = m->params[i];
+            for (long c = 0; c < (long)p.numel; c += CHUNK) {
+                off.push_back((long)p.offset + c);
+                len.push_back((int)std::min<long>(CHUNK, (long)p.numel - c));
+                word.push_back(i);
+            }
+            m->wm_bytes += 4.0 * p.numel;
+        }
+        m->wm_blocks = (int)off.size();
+        m->wm_off = static_cast<long*>(m->ctx->alloc(sizeof(long) * off.size()));
+        m->wm_len = static_cast<int*>(m->ctx->alloc(sizeof(int) * len.size()));
+        m->wm_word = static_cast<int*>(m->ctx->alloc(sizeof(int) * word.size()));
+        LAYA_HIP(hipMemcpyAsync(m->wm_off, off.data(), sizeof(long) * off.size(), hipMemcpyHostToDevice, m->ctx->stream));
+        LAYA_HIP(hipMemcpyAsync(m->wm_len, len.data(), sizeof(int) * len.size(), hipMemcpyHostToDevice, m->ctx->stream));
+        LAYA_HIP(hipMemcpyAsync(m->wm_word, word.data(), sizeof(int) * word.size(), hipMemcpyHostToDevice,
+                                m->ctx->stream));
+        LAYA_HIP(hipStreamSynchronize(m->ctx->stream));  // the host vectors go out of scope
+    }
+    absmax_multi(m->ctx, m->P, m->wm_off, m->wm_len, m->wm_word, m->wm_blocks, m->amax_words, m->wm_bytes);
+    for (int i : m->wm_params) m->amax_known[i] = 1;
+}
+
 // After a host write of the weights: the bf16 copy is stale, and so are the weights' magnitude words
 // (cleared, to be measured again by the next product that reads them).
 void weights_changed(laya_model* m) {
@@ -720,6 +763,7 @@ void forward(laya_model* m, bool train, uint64_t seed) {
     const size_t nw = m->params.size() + m->amax_sites();  // weight and input words (+0.0f: all-zero bits)
     fill(ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_GROUP * nw);
     std::fill(m->amax_known.begin(), m->amax_known.begin() + nw, 0);
+    if (ctx->matmul_pair & 3) measure_weights(m);
 
     // Embedding gather fused into the embedding LayerNorm.
     float* x0 = m->cfg.layers > 0 ? m->ea[0].x : m->x_final;
@@ -1033,7 +1077,7 @@ int laya_model_destroy(laya_model* m) {
         for (auto& s : m->staged)
             if (s.block) ctx->release(s.block);
         for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part, (void*)m->WB,
-                        (void*)m->amax_words})
+                        (void*)m->amax_words, (void*)m->wm_off, (void*)m->wm_len, (void*)m->wm_word})
             if (p) ctx->release(p);
         free_rotary(ctx, &m->rot_global);
         free_rotary(ctx, &m->rot_local);
