@@ -1178,6 +1178,24 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
         lds_barrier();
     }
     if constexpr (NP == 2) ps.unscale(acc);
+    unsigned am = 0;  // max|C| of the lane's stores (or a bound on it), when the product keeps C's magnitude word
+    if constexpr (NP == 2 && MODE == STORE_ROPE) {
+        // The RoPE epilogue has no registers to spare for the stores' maximum: without a bias, C's word takes
+        // twice the largest product instead, a bound on the rotated values (a rotated pair is at most
+        // √2 × the larger of the two, plus rounding). The word only sets the power-of-two scale of the
+        // attention operands, which a bound within a factor 4 of the maximum keeps in fp16 range.
+        if (p.amax_c && !p.bias) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) am = max(am, amax_bits(acc[s][i][j][r]));
+            am = am == 0 ? 0u : am < 0x7f000000u ? am + 0x00800000u : 0x7f7fffffu;  // 2·max, finite
+        }
+    }
     // The epilogue's lane coordinates are taken again after the K loop, so its store offsets are computed
     // here rather than held across the loop (the RoPE epilogue measured fewer spills the other way).
     const int te = MODE == STORE_ROPE ? tid : opaque_tid(), le = te & 63, we = te >> 6;
@@ -1186,7 +1204,6 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     f32x16* park = reinterpret_cast<f32x16*>(&smem[0][0][0]);
 #pragma unroll
     for (int q = 0; q < 4; ++q) park[q * WT_THREADS + te] = acc[1][q >> 1][q & 1];
-    unsigned am = 0;  // max|C| of the lane's stores, when the product keeps C's magnitude word
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
         TileCoord cs = c;
@@ -1197,7 +1214,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
             for (int q = 0; q < 4; ++q) acc[1][q >> 1][q & 1] = park[q * WT_THREADS + te];
         }
         const bool full = cs.m0 + 128 <= p.M && c.n0 + WT <= p.N;
-        // (Not with the RoPE epilogue, whose registers it would spill: launch_wide measures C afterwards.)
+        // (Not with the RoPE epilogue, whose registers it would spill: the bound above, or launch_wide
+        // measures C afterwards when there is a bias.)
         if (NP == 2 && MODE != STORE_ROPE && p.amax_c) {
             if (full)
                 store_acc<true, true, MODE, false, false, true, 2, true>(p, cs, acc[s], we >> 2, we & 3, le & 31,
@@ -2371,8 +2389,8 @@ void launch_wide(laya_ctx* ctx, GemmParams p) {
         else
             hipLaunchKernelGGL((gemm_x6w_kernel<STORE, 2>), g, b, 0, ctx->stream, p);
         check_launch("gemm_x6w_kernel");
-        // The RoPE epilogue does not fold C's magnitude in: measure it here.
-        if (p.mode == STORE_ROPE && p.amax_c) absmax_into(ctx, p.C, p.M, p.N, p.ldc, p.amax_c);
+        // With a bias the RoPE epilogue does not fold C's magnitude (or a bound on it) in: measure it here.
+        if (p.mode == STORE_ROPE && p.amax_c && p.bias) absmax_into(ctx, p.C, p.M, p.N, p.ldc, p.amax_c);
         return;
     }
     profile_rename("gemm_nt_x6w");
