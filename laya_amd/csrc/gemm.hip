@@ -1178,13 +1178,16 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
         lds_barrier();
     }
     if constexpr (NP == 2) ps.unscale(acc);
-    unsigned am = 0;  // max|C| of the lane's stores (or a bound on it), when the product keeps C's magnitude word
+    unsigned am = 0;  // max|C| of the lane's stores, when the product keeps C's magnitude word
     if constexpr (NP == 2 && MODE == STORE_ROPE) {
         // The RoPE epilogue has no registers to spare for the stores' maximum: without a bias, C's word takes
         // twice the largest product instead, a bound on the rotated values (a rotated pair is at most
         // √2 × the larger of the two, plus rounding). The word only sets the power-of-two scale of the
         // attention operands, which a bound within a factor 4 of the maximum keeps in fp16 range.
         if (p.amax_c && !p.bias) {
+            // One max per value (NaNs drop out of fmaxf); an infinity among the products takes the exact
+            // finite maximum instead, so that the scale still fits the finite values.
+            float m4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -1192,9 +1195,23 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
 #pragma unroll
                     for (int j = 0; j < 2; ++j)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) am = max(am, amax_bits(acc[s][i][j][r]));
+                        for (int r = 0; r < 16; ++r) m4[r & 3] = fmaxf(m4[r & 3], fabsf(acc[s][i][j][r]));
+            am = __builtin_bit_cast(unsigned, fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3])));
+            if (am >= 0x7f800000u) {
+                am = 0;
+#pragma unroll
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) am = max(am, amax_bits(acc[s][i][j][r]));
+            }
             am = am == 0 ? 0u : am < 0x7f000000u ? am + 0x00800000u : 0x7f7fffffu;  // 2·max, finite
         }
+        // Folded here, so that no register holds it through the epilogue.
+        block_amax_fold(am, p.bias ? nullptr : p.amax_c);
     }
     // The epilogue's lane coordinates are taken again after the K loop, so its store offsets are computed
     // here rather than held across the loop (the RoPE epilogue measured fewer spills the other way).
@@ -1229,7 +1246,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
             store_acc<true, true, MODE, false, true, true>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2);
         }
     }
-    if constexpr (NP == 2) block_amax_fold(am, p.amax_c);
+    if constexpr (NP == 2 && MODE != STORE_ROPE) block_amax_fold(am, p.amax_c);
 }
 
 // ------------------------------------------------------------- operand magnitudes for two-piece products
