@@ -139,6 +139,42 @@ def test_wide_tile_forward_matches_the_oracle(ctx):
     assert rel_l2(o64.forward(batch, training=False, keep_tape=False), lg) < 1e-5
 
 
+def test_biased_encoder_on_wide_tiles_gradients_match_the_oracle(ctx):
+    """ModernBERT's optional biases (attention_bias, mlp_bias, norm_bias: ModernBertConfig) at 4448 tokens,
+    d = 768, one global layer: the QKV projection (bias, then RoPE, in its epilogue) and the GeGLU input
+    projection take 256 × 256 tiles, and qkv's magnitude for the two-piece attention is measured after the
+    biased product. Logits to 1e-5 and every gradient to max(1e-4, 4 × the fp32 oracle's error) of fp64."""
+    from laya_amd.model import TrainableDecisionModel
+    print("model: d=768, 1 global layer with biases, 4448 tokens", flush=True)
+    mc = mid_config(layers=1)
+    mc.encoder.attention_bias = mc.encoder.mlp_bias = mc.encoder.norm_bias = True
+    o = oracle.OracleModel(mc)
+    params = random_params(o.shapes, 3, std=0.02)
+    batch = mixed_batch(np.random.default_rng(4), [2048, 1500, 900], mc.encoder.vocab_size)
+    o64 = oracle.OracleModel(mc, double=True)
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    assert any(n.endswith("attn.Wqkv.bias") for n in m.names), m.names
+    dlogits = np.random.default_rng(5).standard_normal(batch.n_markers).astype(np.float32)
+    for ref in (o, o64):
+        ref.set_params(params)
+        ref.forward(batch, training=True, keep_tape=True, seed=11)
+        ref.backward(dlogits)
+    lg = m.forward(batch, training=True, seed=11)
+    assert rel_l2(o64.forward(batch, training=True, keep_tape=False, seed=11), lg) < 1e-5
+    m.backward(dlogits)
+    worst = 0.0
+    for name in m.names:
+        if name == "temperature" or name.startswith("act_head"):
+            continue
+        exact = o64.grad(name)
+        bar = max(1e-4, 4 * rel_l2(exact, o.grad(name)))
+        r = rel_l2(exact, m.grad(name))
+        worst = max(worst, r)
+        assert r < bar, (name, r, bar)
+    print(f"worst relative L2 vs fp64 over {len(m.names)} tensors: {worst:.2e}", flush=True)
+
+
 def _assert_step_matches(o, m, params, lr):
     """The weights after one optimizer step on the GPU against the oracle's step."""
     for name in m.names:
