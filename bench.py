@@ -8,7 +8,8 @@ Workload: ModernBERT-base (22 layers, d 768, 12 heads × 64, GeGLU 1152, vocab 5
 layer global, the rest a 128-token sliding window) plus the two-layer decision head, fp32, batch
 32 × seq 512 with a trailing-padding fraction U[0, 0.3] per sequence (padding is never computed:
 sequences are packed), items cycling choice K=8 / score K=4 / noul K=2, summed cross-entropy,
-AdamW lr 3e-5 wd 0.01, clip 1.0, head dropout 0.1. Weights N(0, 0.02) from a fixed seed.
+AdamW lr 3e-5 wd 0.01, clip 1.0, head dropout 0.1. Weights N(0, 0.02) from a fixed seed
+(laya_amd.model.synthetic_params), unit LayerNorm weights, zero biases.
 
 `--workload` selects another shape (batch 4 × 128; batch 32 × 1024 and a packed Zipf batch of 64
 sequences with the backward products in bf16; batch 2 × 8192); the default is the one above.
@@ -47,6 +48,10 @@ MEASURED_TRAFFIC = {("b32x512", "gemm_bwd_pair_x6w"): 0.865e9,
 
 
 PEAK_BF16_MFMA = 2.5e15
+# The parameters (laya_amd.model.synthetic_params with this seed) and the seed of timed step i (STEP_SEED0 + i,
+# warm-up steps first): tests/golden/make_fullsize_fixtures.py --bench-init reruns the first step on the oracle.
+PARAM_SEED = 42
+STEP_SEED0 = 1000
 
 
 def mfma_peaks(name: str):
@@ -221,7 +226,7 @@ def main():
 
     from laya_amd.config import modernbert_base
     from laya_amd.device import Context
-    from laya_amd.model import TrainableDecisionModel
+    from laya_amd.model import TrainableDecisionModel, synthetic_params
 
     w = WORKLOADS[args.workload]
     rng = np.random.default_rng(2024)
@@ -236,7 +241,8 @@ def main():
     ctx.set_matmul_precision(matmul)
     cpu_items = args.cpu_items or (16 if w["seq"] <= 512 else 1)
     long_workload = w["seq"] > 512
-    model = TrainableDecisionModel.synthetic(mc, seed=42, std=0.02, ctx=ctx)
+    model = TrainableDecisionModel(mc, ctx)
+    model.set_params(synthetic_params(model.shapes, PARAM_SEED))
     model.head_dropout = 0.1
     if args.no_bf16_copies:
         model.set_bf16_copies(False)
@@ -263,10 +269,10 @@ def main():
     def step(i):
         if by_value:
             b, t, a = by_value[i]
-            model.train_step(b, t, seed=1000 + i, ce_weight=1.0, loss_scale=scale(b), max_norm=1.0,
+            model.train_step(b, t, seed=STEP_SEED0 + i, ce_weight=1.0, loss_scale=scale(b), max_norm=1.0,
                              lr_encoder=3e-5, lr_head=3e-5, weight_decay=0.01, _args=a)
             return
-        model.train_step_staged(slots[i], seed=1000 + i, ce_weight=1.0, loss_scale=scale(batches[i][0]),
+        model.train_step_staged(slots[i], seed=STEP_SEED0 + i, ce_weight=1.0, loss_scale=scale(batches[i][0]),
                                 max_norm=1.0, lr_encoder=3e-5, lr_head=3e-5, weight_decay=0.01)
 
     print(f"warmup {args.warmup} steps", file=sys.stderr, flush=True)

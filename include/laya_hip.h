@@ -270,6 +270,12 @@ int laya_model_set_param(laya_model* model, int i, const float* host);
 int laya_model_get_param(laya_model* model, int i, float* host);
 int laya_model_get_grad(laya_model* model, int i, float* host);
 int laya_model_has_grad(laya_model* model, int i, int* has);
+/* Inspection of the last forward's saved head feed-forward activations (no counterpart in the reference, whose
+ * HeadLayerBackward recomputes them, TrainableDecisionModel.cs:605-624): the device address and float count
+ * ([tokens × head_ff]) of head layer `layer`'s linear1 output (which = 0, the ReLU's input) or of its
+ * ReLU-dropout output (which = 1, whose sign is the mask the backward applies). Valid until the next forward;
+ * LAYA_ERR_STATE before any forward. Tests use it to compare ReLU decisions with the oracle's. */
+int laya_model_head_activation(laya_model* model, int layer, int which, float** device, size_t* count);
 /* Synthetic init: matrices and embeddings N(0, std) from the counter RNG, norm weights 1, biases 0. */
 int laya_model_init_random(laya_model* model, uint64_t seed, float std);
 /* SetTrainableEncoderLayers (TrainableDecisionModel.cs:206-231); n < 0 trains everything. */
@@ -292,6 +298,14 @@ int laya_model_layer_checkpointing(laya_model* model, int* mode, int* recomputin
  * rounding fp32 operands on their way into LDS — the same values, half the bytes. on = 1 (default) keeps
  * them, 0 drops them (less memory). Results are the same either way. Takes effect at the next forward. */
 int laya_model_set_bf16_copies(laya_model* model, int on);
+/* bf16 weights, as PackedMatrixBf16 holds a projection weight (src/StructuredDecisions.Base/Numerics/
+ * PackedMatrixBf16.cs:7-21: a bf16 weight widened exactly to fp32 inside an fp32 product): with on = 1 every
+ * matrix product (the encoder's, head's and scorer's linears, forward and input gradient) reads each weight
+ * rounded to bf16 (nearest even) and widened back to fp32, under whatever precision policy the context sets
+ * for the product itself; activations, embeddings, norms and biases stay fp32, and the fp32 arena stays the
+ * master that AdamW updates (the rounded copy follows each update and each host write). Weight gradients are
+ * those of the rounded weights. Off (0) by default. Takes effect at the next forward. */
+int laya_model_set_bf16_weights(laya_model* model, int on);
 /* Parameter i's bf16 copy (numel uint16, the bf16 bit patterns); LAYA_ERR_STATE when no current copy exists. */
 int laya_model_get_param_bf16(laya_model* model, int i, uint16_t* host);
 /* Forward (TrainableDecisionModel.cs:248-353). Keeps what the backward needs resident in HBM (all of it,

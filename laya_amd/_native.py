@@ -136,12 +136,14 @@ SIGNATURES = {
     "laya_model_get_param": (c_int, [P, c_int, P]),
     "laya_model_get_grad": (c_int, [P, c_int, P]),
     "laya_model_has_grad": (c_int, [P, c_int, ctypes.POINTER(c_int)]),
+    "laya_model_head_activation": (c_int, [P, c_int, c_int, PP, ctypes.POINTER(c_size)]),
     "laya_model_init_random": (c_int, [P, c_u64, c_float]),
     "laya_model_set_trainable_encoder_layers": (c_int, [P, c_int]),
     "laya_model_set_head_dropout": (c_int, [P, c_float]),
     "laya_model_set_layer_checkpointing": (c_int, [P, c_int]),
     "laya_model_layer_checkpointing": (c_int, [P, P, P]),
     "laya_model_set_bf16_copies": (c_int, [P, c_int]),
+    "laya_model_set_bf16_weights": (c_int, [P, c_int]),
     "laya_model_get_param_bf16": (c_int, [P, c_int, P]),
     "laya_model_forward": (c_int, [P, ctypes.POINTER(BatchC), c_int, c_u64, P]),
     "laya_model_backward": (c_int, [P, P]),

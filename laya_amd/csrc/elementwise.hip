@@ -167,6 +167,13 @@ __global__ void to_bf16_kernel(const f32x4* __restrict__ src, bf16x4* __restrict
 __global__ void to_bf16_scalar_kernel(const float* __restrict__ src, __bf16* __restrict__ dst, size_t n) {
     GRID_STRIDE(i, n) dst[i] = (__bf16)src[i];
 }
+// dst = float(bf16(src)), rounded to nearest even: the bf16 value widened back to fp32 (exact).
+__global__ void round_bf16_kernel(const f32x4* __restrict__ src, f32x4* __restrict__ dst, size_t n4) {
+    GRID_STRIDE(i, n4) dst[i] = __builtin_convertvector(__builtin_convertvector(src[i], bf16x4), f32x4);
+}
+__global__ void round_bf16_scalar_kernel(const float* __restrict__ src, float* __restrict__ dst, size_t n) {
+    GRID_STRIDE(i, n) dst[i] = (float)(__bf16)src[i];
+}
 
 // The backward from the forward's output: an element passes its gradient (times 1/(1 − p)) exactly when
 // it was kept and its pre-activation was positive, i.e. when its output is positive. Same product as
@@ -468,6 +475,18 @@ void to_bf16(laya_ctx* ctx, const float* src, size_t n, __bf16* dst) {
     }
     hipLaunchKernelGGL(to_bf16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, src, dst, n);
     check_launch("to_bf16_scalar_kernel");
+}
+void round_bf16(laya_ctx* ctx, const float* src, size_t n, float* dst) {
+    if (!n) return;
+    ProfileScope scope(ctx, "round_bf16", 0.0, 8.0 * n);
+    if (n % 4 == 0 && vec4(src) && vec4(dst)) {
+        hipLaunchKernelGGL(round_bf16_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                           reinterpret_cast<const f32x4*>(src), reinterpret_cast<f32x4*>(dst), n / 4);
+        check_launch("round_bf16_kernel");
+        return;
+    }
+    hipLaunchKernelGGL(round_bf16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, src, dst, n);
+    check_launch("round_bf16_scalar_kernel");
 }
 void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide,
                unsigned* amax) {

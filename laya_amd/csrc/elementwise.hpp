@@ -14,6 +14,8 @@ void gelu_bwd(laya_ctx* ctx, const float* u, float* g, size_t n);
 void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, __bf16* act16 = nullptr,
                unsigned* amax = nullptr);
 void to_bf16(laya_ctx* ctx, const float* src, size_t n, __bf16* dst);
+// dst = float(bf16(src)) (round to nearest even; the widening back to fp32 is exact). dst may alias src.
+void round_bf16(laya_ctx* ctx, const float* src, size_t n, float* dst);
 void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide,
                unsigned* amax = nullptr);
 void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed);

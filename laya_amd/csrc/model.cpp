@@ -146,6 +146,11 @@ struct laya_model {
     bool copies = false;       // the activation arena's current layout has the copies
     __bf16* WB = nullptr;
     bool wb_fresh = false;
+    // bf16 weights (laya_model_set_bf16_weights): the products read PW, each weight rounded to bf16 and widened
+    // back to fp32 (exact), refreshed from the fp32 masters P when a host write or an update left it stale.
+    bool bf16_weights = false;
+    float* PW = nullptr;
+    bool pw_fresh = false;
     void* act_block = nullptr;
     struct EncAct {
         float *x, *normed, *mean1, *rstd1, *qkv, *ctx, *lse, *res, *mlpn, *mean2, *rstd2, *wide, *act;
@@ -251,6 +256,8 @@ struct laya_model {
     }
 
     float* W(int i) const { return i >= 0 ? P + params[i].offset : nullptr; }
+    // The weight matrix a product reads: the master, or its bf16 rounding under bf16 weights.
+    const float* PWt(int i) const { return i >= 0 ? (bf16_weights && PW ? PW : P) + params[i].offset : nullptr; }
     // The bf16 copy of parameter i when the products read copies (else null: they round W themselves).
     const __bf16* W16(int i) const { return i >= 0 && copies && WB && wb_fresh ? WB + params[i].offset : nullptr; }
     int find(const std::string& name) const {
@@ -497,7 +504,8 @@ void measure_weights(laya_model* m) {
                                 m->ctx->stream));
         LAYA_HIP(hipStreamSynchronize(m->ctx->stream));  // the host vectors go out of scope
     }
-    absmax_multi(m->ctx, m->P, m->wm_off, m->wm_len, m->wm_word, m->wm_blocks, m->amax_words, m->wm_bytes);
+    absmax_multi(m->ctx, m->bf16_weights && m->PW ? m->PW : m->P, m->wm_off, m->wm_len, m->wm_word, m->wm_blocks,
+                 m->amax_words, m->wm_bytes);
     for (int i : m->wm_params) m->amax_known[i] = 1;
 }
 
@@ -505,6 +513,7 @@ void measure_weights(laya_model* m) {
 // (cleared, to be measured again by the next product that reads them).
 void weights_changed(laya_model* m) {
     m->wb_fresh = false;
+    m->pw_fresh = false;
     if (m->amax_words) {
         fill(m->ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_GROUP * m->params.size());
         std::fill(m->amax_known.begin(), m->amax_known.begin() + m->params.size(), 0);
@@ -514,6 +523,16 @@ void weights_changed(laya_model* m) {
 // The weights' bf16 copy, when the products read copies: allocated on first use, refreshed from the fp32
 // masters when a host write or an update without it left it stale.
 void ensure_mirror(laya_model* m) {
+    if (m->bf16_weights) {
+        if (!m->PW) {
+            m->PW = static_cast<float*>(m->ctx->alloc(m->total * sizeof(float)));
+            m->pw_fresh = false;
+        }
+        if (!m->pw_fresh) {
+            round_bf16(m->ctx, m->P, m->total, m->PW);
+            m->pw_fresh = true;
+        }
+    }
     if (!m->copies) return;
     if (!m->WB) {
         m->WB = static_cast<__bf16*>(m->ctx->alloc(m->total * sizeof(__bf16)));
@@ -678,7 +697,7 @@ AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p
 // x16: x's bf16 copy, or null; ax: x's magnitude word; ay (optional): y's, to fold y into.
 void linear(laya_model* m, const float* x, int rows, int in, int wi, int bi, int out, const float* residual, float* y,
             const __bf16* x16 = nullptr, AmaxRef ax = {}, unsigned* ay = nullptr) {
-    gemm(m->ctx, GemmLayout::NT, GemmEpilogue::Store, rows, out, in, x, in, m->W(wi), in, y, out, m->W(bi), residual,
+    gemm(m->ctx, GemmLayout::NT, GemmEpilogue::Store, rows, out, in, x, in, m->PWt(wi), in, y, out, m->W(bi), residual,
          out, x16, m->W16(wi), ax, m->wref(wi), ay);
 }
 
@@ -690,11 +709,11 @@ void linear_backward(laya_model* m, const float* x, const float* dy, int rows, i
                      unsigned* adx = nullptr) {
     float* dW = m->Gt(wi);
     if (dx && dW) {
-        gemm_backward_pair(m->ctx, rows, in, out, dy, m->W(wi), x, dx, dx_residual, dW, m->W16(wi), x16,
+        gemm_backward_pair(m->ctx, rows, in, out, dy, m->PWt(wi), x, dx, dx_residual, dW, m->W16(wi), x16,
                            site >= 0 ? m->dref(site) : AmaxRef{}, m->wref(wi),
                            site >= 0 ? m->aref(site) : AmaxRef{}, adx);
     } else if (dx) {
-        gemm(m->ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, m->W(wi), in, dx, in, nullptr,
+        gemm(m->ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, m->PWt(wi), in, dx, in, nullptr,
              dx_residual, in, nullptr, m->W16(wi), {}, {}, adx);
     } else if (dW) {
         gemm(m->ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr,
@@ -730,7 +749,7 @@ void encoder_forward(laya_model* m, int l, bool output = true) {
     }
     if (fused_rope(m)) {
         const laya_rotary& r = L.kind == 0 ? m->rot_global : m->rot_local;
-        gemm_rope(ctx, T, 3 * d, d, normed, m->W(L.wqkv), a.qkv, m->W(L.wqkv_b), m->cur.pos, r.cos_t, r.sin_t,
+        gemm_rope(ctx, T, 3 * d, d, normed, m->PWt(L.wqkv), a.qkv, m->W(L.wqkv_b), m->cur.pos, r.cos_t, r.sin_t,
                   2 * d, a.normed16, m->W16(L.wqkv), m->aref(m->enc_site(l, 0)), m->wref(L.wqkv),
                   m->produce_attention(m->aref(m->enc_site(l, 4))));
     } else {
@@ -1018,7 +1037,14 @@ void adamw_step(laya_model* m, double lr_enc, double lr_head, double b1, double 
     adamw_arena(m->ctx, m->P, m->G, m->M1, m->M2, n, g, (float)b1, (float)b2, (float)eps, (float)std::sqrt(c2),
                 m->coef_valid ? m->d_coef : nullptr, zero_grads ? 1 : 0, mirror);
     if (!mirror) m->wb_fresh = false;
+    m->pw_fresh = false;  // the bf16 weights are rounded again before the next product reads them
     m->coef_valid = false;
+    // The update moved the weights, so their magnitude words no longer bound them: cleared (an unknown word
+    // holds zero), to be measured again by the next forward, or by a backward product that runs before one.
+    if (m->amax_words) {
+        fill(m->ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_GROUP * m->params.size());
+        std::fill(m->amax_known.begin(), m->amax_known.begin() + m->params.size(), 0);
+    }
 }
 
 laya_model* checked(laya_model* m) {
@@ -1076,7 +1102,7 @@ int laya_model_destroy(laya_model* m) {
             if (p) ctx->release(p);
         for (auto& s : m->staged)
             if (s.block) ctx->release(s.block);
-        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part, (void*)m->WB,
+        for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part, (void*)m->WB, (void*)m->PW,
                         (void*)m->amax_words, (void*)m->wm_off, (void*)m->wm_len, (void*)m->wm_word})
             if (p) ctx->release(p);
         free_rotary(ctx, &m->rot_global);
@@ -1152,6 +1178,20 @@ int laya_model_has_grad(laya_model* m, int i, int* has) {
     });
 }
 
+// The head layers' saved feed-forward activations of the last forward, by device address: which = 0 is
+// linear1's output (the ReLU's input), 1 the ReLU-dropout output the backward takes its mask from.
+int laya_model_head_activation(laya_model* m, int layer, int which, float** device, size_t* count) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(device && count && (which == 0 || which == 1), "head_activation: bad argument");
+        LAYA_REQUIRE(layer >= 0 && layer < m->cfg.head_layers, "head_activation: no such head layer");
+        if (!m->has_tape) throw Error(LAYA_ERR_STATE, "head_activation: no forward with saved activations");
+        const auto& a = m->ha[layer];
+        *device = which == 0 ? a.wide : a.drop;
+        *count = (size_t)m->T * m->cfg.head_ff;
+    });
+}
+
 int laya_model_init_random(laya_model* m, uint64_t seed, float std) {
     return guarded([&] {
         checked(m);
@@ -1204,6 +1244,21 @@ int laya_model_set_layer_checkpointing(laya_model* m, int mode) {
         if (m->act_block) m->ctx->release(m->act_block);
         m->act_block = nullptr;
         m->cap_tokens = m->cap_markers = m->cap_segs = 0;
+    });
+}
+
+int laya_model_set_bf16_weights(laya_model* m, int on) {
+    return guarded([&] {
+        checked(m);
+        if ((on != 0) == m->bf16_weights) return;
+        m->bf16_weights = on != 0;
+        m->pw_fresh = false;
+        // The weights the products read change: their magnitude words are measured again.
+        weights_changed(m);
+        if (!m->bf16_weights && m->PW) {
+            m->ctx->release(m->PW);
+            m->PW = nullptr;
+        }
     });
 }
 

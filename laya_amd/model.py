@@ -44,6 +44,25 @@ class _BatchArgs:
         self.struct = BatchC(batch.n_items, *[a.ctypes.data for a in self.arrays])
 
 
+def synthetic_params(shapes: Dict[str, tuple], seed: int = 0, std: float = 0.02) -> Dict[str, np.ndarray]:
+    """A host-side random init of the kind ``TrainableDecisionModel.synthetic`` makes on the device: N(0, std)
+    matrices and embeddings, unit LayerNorm weights (and the frozen temperatures), zero biases. Each tensor
+    draws from its own generator keyed by (seed, name), so a CPU restatement of the model fed the same shapes
+    gets the same values."""
+    import zlib
+    ones = ("norm.weight", "norm1.weight", "norm2.weight", "scorer.0.weight")
+    out = {}
+    for name, shape in shapes.items():
+        if name == "temperature" or name.endswith(ones):
+            out[name] = np.ones(shape, np.float32)
+        elif name.endswith("bias"):
+            out[name] = np.zeros(shape, np.float32)
+        else:
+            rng = np.random.default_rng([seed, zlib.crc32(name.encode())])
+            out[name] = (std * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+    return out
+
+
 def _as_batch(items) -> Batch:
     if isinstance(items, Batch):
         return items
@@ -211,6 +230,30 @@ class TrainableDecisionModel:
         check(lib().laya_model_get_grad(self.handle, self.index[name], out.ctypes.data))
         return out
 
+    def _head_activation(self, layer: int, which: int):
+        dev, n = ctypes.c_void_p(), ctypes.c_size_t()
+        check(lib().laya_model_head_activation(self.handle, int(layer), int(which), ctypes.byref(dev),
+                                               ctypes.byref(n)))
+        return dev.value, n.value
+
+    def head_activation(self, layer: int, which: str = "linear1") -> np.ndarray:
+        """The last forward's saved head feed-forward activation of head layer `layer`, [tokens, head_ff]:
+        "linear1" is linear1's output (the ReLU's input), "relu" the ReLU-dropout output whose sign is the
+        mask the backward applies."""
+        dev, n = self._head_activation(layer, {"linear1": 0, "relu": 1}[which])
+        out = np.empty(n, np.float32)
+        check(lib().laya_download(self.ctx.handle, out.ctypes.data, dev, out.nbytes))
+        return out.reshape(-1, self.config.head_ff)
+
+    def set_head_activation(self, layer: int, which: str, values: np.ndarray) -> None:
+        """Overwrites a saved head activation (see head_activation) before the backward reads it: tests use
+        it to put the ReLU decisions of ties within rounding of zero where the exact computation puts them."""
+        dev, n = self._head_activation(layer, {"linear1": 0, "relu": 1}[which])
+        a = np.ascontiguousarray(values, np.float32).reshape(-1)
+        if a.size != n:
+            raise ValueError(f"head activation: {a.size} values for {n}")
+        check(lib().laya_upload(self.ctx.handle, dev, a.ctypes.data, a.nbytes))
+
     def has_grad(self, name: str) -> bool:
         v = ctypes.c_int()
         check(lib().laya_model_has_grad(self.handle, self.index[name], ctypes.byref(v)))
@@ -260,6 +303,12 @@ class TrainableDecisionModel:
         if isinstance(mode, bool):
             mode = self.CHECKPOINT_RECOMPUTE if mode else self.CHECKPOINT_KEEP
         check(lib().laya_model_set_layer_checkpointing(self.handle, int(mode)))
+
+    def set_bf16_weights(self, on: bool = True) -> None:
+        """bf16 weights (PackedMatrixBf16's semantics, PackedMatrixBf16.cs:7-21): every matrix product reads each
+        weight rounded to bf16 and widened back to fp32; activations stay fp32 and the fp32 weights stay the
+        masters AdamW updates. Takes effect at the next forward."""
+        check(lib().laya_model_set_bf16_weights(self.handle, int(bool(on))))
 
     def set_bf16_copies(self, on: bool) -> None:
         """Keep bf16 copies of the weights (updated by AdamW) and of the saved activations for the bf16

@@ -205,23 +205,63 @@ class _LoopState:
 _STAGING, _RETIRED = ".new", ".old"
 
 
+def _fsync_tree(path: str) -> None:
+    """Flushes every file under `path`, then every directory (deepest first), to stable storage."""
+    for root, dirs, files in os.walk(path, topdown=False):
+        for name in files:
+            fd = os.open(os.path.join(root, name), os.O_RDONLY)
+            try:
+                os.fsync(fd)
+            finally:
+                os.close(fd)
+        _fsync_dir(root)
+
+
+def _fsync_dir(path: str) -> None:
+    fd = os.open(path, os.O_RDONLY)
+    try:
+        os.fsync(fd)
+    finally:
+        os.close(fd)
+
+
+def _state_complete(directory: str) -> bool:
+    """A checkpoint directory counts as complete when its loop state (written last) parses."""
+    try:
+        with open(os.path.join(directory, STATE_FILE)) as f:
+            json.load(f)
+        return True
+    except (OSError, ValueError):
+        return False
+
+
 def _swap_in(staging: str, rolling: str) -> None:
-    """Replaces `rolling` by the complete checkpoint in `staging` with two renames."""
+    """Replaces `rolling` by the complete checkpoint in `staging` with two renames. The staged files are on
+    stable storage before the renames, and the renames before the retired copy is removed, so a power loss at
+    any point leaves a complete checkpoint under `rolling` or `rolling.old`."""
     retired = rolling + _RETIRED
+    parent = os.path.dirname(os.path.abspath(rolling))
+    _fsync_tree(staging)
     shutil.rmtree(retired, ignore_errors=True)
     if os.path.exists(rolling):
         os.rename(rolling, retired)
     os.rename(staging, rolling)
+    _fsync_dir(parent)
     shutil.rmtree(retired, ignore_errors=True)
+    _fsync_dir(parent)
 
 
 def _recover_rolling(rolling: str) -> None:
-    """Finishes a swap an interruption cut short: a staged checkpoint whose loop state was written is
-    complete and wins; otherwise the retired one is restored."""
-    if os.path.exists(rolling):
-        return
+    """Finishes a swap an interruption cut short: a staged checkpoint whose loop state was written and parses
+    is complete and wins; otherwise the retired one is restored. A rolling checkpoint whose loop state does not
+    parse is replaced by the retired one when that exists."""
     staging, retired = rolling + _STAGING, rolling + _RETIRED
-    if os.path.exists(os.path.join(staging, STATE_FILE)):
+    if os.path.exists(rolling):
+        if not _state_complete(rolling) and _state_complete(retired):
+            shutil.rmtree(rolling)
+            os.rename(retired, rolling)
+        return
+    if _state_complete(staging):
         os.rename(staging, rolling)
     elif os.path.exists(retired):
         os.rename(retired, rolling)

@@ -67,6 +67,10 @@ def lib():
         L.orc_model_adamw.argtypes = [P, c_double, c_double, c_double, c_double, c_double, c_double]
         L.orc_model_adamw.restype = None
         L.orc_model_steps.argtypes = [P]
+        L.orc_model_set_capture_head.argtypes = [P, c_int]
+        L.orc_model_set_capture_head.restype = None
+        L.orc_model_head_preactivation.argtypes = [P, c_int, P]
+        L.orc_model_head_preactivation.restype = c_long
         L.orc_set_threads.argtypes = [c_int]
         L.orc_set_threads.restype = c_int
         L.orc_uniform.argtypes = [c_u64, c_u64]
@@ -218,6 +222,19 @@ class OracleModel:
 
     def zero_grad(self) -> None:
         lib().orc_model_zero_grad(self._h)
+
+    def capture_head_preactivations(self, on: bool = True) -> None:
+        """Keep each head layer's linear1 output (the ReLU's input) of the forwards that follow."""
+        lib().orc_model_set_capture_head(self._h, int(on))
+
+    def head_preactivation(self, layer: int) -> np.ndarray:
+        """Head layer `layer`'s linear1 output of the last forward, [tokens, head_ff], in double."""
+        n = lib().orc_model_head_preactivation(self._h, int(layer), None)
+        if n < 0:
+            raise RuntimeError("no head pre-activations kept (call capture_head_preactivations first)")
+        out = np.empty(n, np.float64)
+        lib().orc_model_head_preactivation(self._h, int(layer), ptr(out))
+        return out.reshape(-1, self.mc.head_ff)
 
     def clip(self, max_norm: float) -> float:
         return lib().orc_model_clip(self._h, float(max_norm))

@@ -507,6 +507,10 @@ struct ModelBase {
     bool embeddings_trainable = true;
     float head_dropout = 0.1f;
     int steps = 0;
+    // Diagnostics for the parity tests: when set, each head layer's linear1 output (the ReLU's input) of the
+    // last forward is kept here in double.
+    bool capture_head = false;
+    std::vector<std::vector<double>> captured_head;
     virtual void set_param(int i, const float* d) = 0;
     virtual void get_param(int i, double* out) = 0;
     virtual void get_grad(int i, double* out) = 0;
@@ -778,6 +782,10 @@ template <typename R> struct Model : ModelBase {
         layernorm(residual.data(), rows, d, P(H.norm2), P(H.norm2_b), eps, ff_normed.data());
         std::vector<R> wide((size_t)rows * ff);
         linear(ff_normed.data(), rows, d, P(H.linear1), ff, P(H.linear1_b), wide.data());
+        if (capture_head) {
+            if ((int)captured_head.size() < cfg.head_layers) captured_head.resize(cfg.head_layers);
+            captured_head[index].assign(wide.begin(), wide.end());
+        }
         std::vector<R> dropped = wide;
         for (auto& v : dropped) v = std::max(v, R(0));
         dropout(dropped.data(), (long)dropped.size(), dr, salt(seed, index, 2));
@@ -1190,6 +1198,16 @@ void orc_model_adamw(void* m, double lr_enc, double lr_head, double b1, double b
     M_(m)->adamw(lr_enc, lr_head, b1, b2, eps, wd);
 }
 int orc_model_steps(void* m) { return M_(m)->steps; }
+void orc_model_set_capture_head(void* m, int on) {
+    M_(m)->capture_head = on != 0;
+    if (!on) M_(m)->captured_head.clear();
+}
+long orc_model_head_preactivation(void* m, int layer, double* out) {
+    auto& c = M_(m)->captured_head;
+    if (layer < 0 || layer >= (int)c.size()) return -1;
+    if (out) std::copy(c[layer].begin(), c[layer].end(), out);
+    return (long)c[layer].size();
+}
 
 // The OpenMP thread count of the calls that follow (the CPU baseline's one-thread figure); returns the old one.
 int orc_set_threads(int n) {

@@ -56,6 +56,11 @@ double orc_model_clip(void* model, double max_norm);
 void orc_model_adamw(void* model, double lr_encoder, double lr_head, double beta1, double beta2, double eps,
                      double weight_decay);
 int orc_model_steps(void* model);
+/* Diagnostics: keep each head layer's linear1 output (the ReLU's input) of every later forward, in double;
+ * orc_model_head_preactivation copies layer `layer`'s [tokens × head_ff] values (out may be NULL) and
+ * returns their count, or -1 when none was kept. */
+void orc_model_set_capture_head(void* model, int on);
+long orc_model_head_preactivation(void* model, int layer, double* out);
 
 /* ---- ops (Ops.cs, SimdOps.cs), fp32 (_f32) and fp64 (_f64) */
 float orc_uniform(uint64_t seed, uint64_t index);

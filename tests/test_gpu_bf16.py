@@ -302,3 +302,130 @@ def test_adamw_keeps_the_bf16_weight_copy_current():
         m.close()
     finally:
         c.close()
+
+
+def _forward_backward(ctx, mc, params, batch, targets, seed, policy, bf16_weights=False):
+    from laya_amd.model import TrainableDecisionModel
+    ctx.set_matmul_precision(policy)
+    try:
+        m = TrainableDecisionModel(mc, ctx)
+        m.set_params(params)
+        m.head_dropout = 0.1
+        if bf16_weights:
+            m.set_bf16_weights(True)
+        logits = m.forward(batch, training=True, seed=seed)
+        _, g = oracle.cross_entropy(batch.n_options, logits, targets, 1.0, float(batch.n_items))
+        m.backward(g)
+        grads = {n: m.grad(n) for n in m.names if m.has_grad(n)}
+        m.close()
+    finally:
+        ctx.set_matmul_precision("bf16")
+    return logits, g, grads
+
+
+def _product_weights(names):
+    """The weights the matrix products read (the linears of the encoder, head and scorer)."""
+    return [n for n in names if n.endswith(("Wqkv.weight", "Wo.weight", "Wi.weight", "in_proj_weight",
+                                            "out_proj.weight", "linear1.weight", "linear2.weight",
+                                            "scorer.1.weight", "scorer.3.weight"))]
+
+
+def _modernbert_base_case(seed, n=4, length=256):
+    from laya_amd.batch import synthetic_batch
+    from laya_amd.config import modernbert_base
+    import helpers
+    mc = modernbert_base()
+    shapes = oracle.OracleModel(mc).shapes
+    rng = np.random.default_rng(seed)
+    opts, qt = _heads(n)
+    batch = synthetic_batch(rng, [length] * n, opts, qt, 50368)
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+    # Head linear1 biases away from the ReLU's kink (tests/helpers.fixture_params): no ReLU input lies within
+    # rounding of zero, so the comparison sees the products' rounding and nothing else.
+    return mc, shapes, helpers.fixture_params(shapes, seed), batch, targets
+
+
+def test_bf16_weights_match_the_oracle_fed_the_rounded_weights(ctx):
+    """bf16 weights as the reference's PackedMatrixBf16 keeps them (a bf16 weight widened exactly to fp32 inside
+    an fp32 product, PackedMatrixBf16.cs:7-21): ModernBERT-base, 22 layers, 4 × 256 tokens, every product
+    fp32-accurate (the default two-piece products) on fp32 activations, the products reading each weight
+    rounded to bf16. Against the oracle (fp32 and fp64) fed the same bf16-rounded weights: logits to 1e-5 and
+    every gradient within max(1e-4, 4 × the fp32 oracle's error) of fp64 — the fp32 bar. Then AdamW updates the
+    fp32 masters and the products follow the rounding of the updated weights."""
+    from laya_amd.config import modernbert_base  # noqa: F401
+    from laya_amd.model import TrainableDecisionModel
+    print("bf16 weights: ModernBERT-base 22 layers, 4 x 256, vs the oracle with bf16-rounded weights", flush=True)
+    mc, shapes, params, batch, targets = _modernbert_base_case(71)
+    rounded = dict(params)
+    pw = _product_weights(shapes)
+    assert len(pw) == 4 * 22 + 4 * 2 + 2
+    for n in pw:
+        rounded[n] = bf16(params[n])
+    seed = 71
+    logits, g, grads = _forward_backward(ctx, mc, params, batch, targets, seed, "fp32", bf16_weights=True)
+    o, o64 = oracle.OracleModel(mc), oracle.OracleModel(mc, double=True)
+    for r in (o, o64):
+        r.set_params(rounded)
+        r.set_head_dropout(0.1)
+        r.forward(batch, training=True, keep_tape=True, seed=seed)
+        r.backward(g)
+    lo = o64.forward(batch, training=True, keep_tape=False, seed=seed)
+    assert np.abs(logits - lo).max() < 1e-5
+    worst = (0.0, "")
+    for n in grads:
+        exact = o64.grad(n)
+        bar = max(1e-4, 4 * rel_l2(exact, o.grad(n)))
+        r = rel_l2(exact, grads[n])
+        assert r < bar, (n, r, bar)
+        if bar == 1e-4:
+            worst = max(worst, (r, n))
+    print(f"bf16 weights vs the oracle fed bf16-rounded weights: worst gradient rel-L2 {worst[0]:.2e} ({worst[1]})",
+          flush=True)
+    # The unrounded weights move the logits by the weights' rounding, not more.
+    lf = oracle.OracleModel(mc, double=True)
+    lf.set_params(params)
+    lf.set_head_dropout(0.1)
+    print(f"logits vs unrounded weights: rel-L2 {rel_l2(lf.forward(batch, True, False, seed), logits):.2e}",
+          flush=True)
+    # After an AdamW step the products read the rounding of the updated masters.
+    ctx.set_matmul_precision("fp32")
+    try:
+        m = TrainableDecisionModel(mc, ctx)
+        m.set_params(params)
+        m.set_bf16_weights(True)
+        m.forward(batch, training=True, seed=seed)
+        m.backward(g)
+        m.adamw_step(1e-3, 1e-3)
+        masters = {n: m.param(n) for n in shapes}
+        lg = m.forward(batch, training=False)
+        ref = oracle.OracleModel(mc, double=True)
+        ref.set_params({n: (bf16(v) if n in pw else v) for n, v in masters.items()})
+        assert np.abs(lg - ref.forward(batch, training=False, keep_tape=False)).max() < 1e-5
+        m.close()
+    finally:
+        ctx.set_matmul_precision("bf16")
+
+
+@pytest.mark.parametrize("weights", ["relu-clear", "generic"])
+def test_every_product_in_bf16_against_the_fp32_oracle(ctx, weights):
+    """Every product on bf16 operands (forward and backward, weights and activations rounded to bf16, fp32
+    accumulation, statistics and masters) against the fp32 oracle with the unrounded weights, at ModernBERT-base
+    (22 layers, 4 × 256). With head linear1 biases away from the ReLU's kink ("relu-clear") the difference is
+    the products' rounding alone and every gradient is held to the bf16 bar, 2e-2. With the benchmark's kind of
+    initialisation ("generic": zero biases, unit γ) ~10³ of the head's 6.3M ReLU inputs lie within bf16
+    rounding of zero and are decided the other way; that is measured and printed, held only to 1e-1."""
+    from laya_amd.model import synthetic_params
+    print(f"every product in bf16 vs the fp32 oracle, {weights} weights", flush=True)
+    mc, shapes, params, batch, targets = _modernbert_base_case(81)
+    if weights == "generic":
+        params = synthetic_params(shapes, 81)
+    seed = 81
+    logits, g, grads = _forward_backward(ctx, mc, params, batch, targets, seed, "bf16")
+    o = oracle.OracleModel(mc)
+    o.set_params(params)
+    o.set_head_dropout(0.1)
+    lo = o.forward(batch, training=True, keep_tape=True, seed=seed)
+    o.backward(g)
+    print(f"logits rel-L2 vs fp32: {rel_l2(lo, logits):.2e}", flush=True)
+    worst = _grads_match(list(grads), {n: o.grad(n) for n in grads}, grads, 2e-2 if weights == "relu-clear" else 1e-1)
+    print(f"every product in bf16 ({weights}): worst gradient rel-L2 vs the fp32 oracle {worst:.2e}", flush=True)

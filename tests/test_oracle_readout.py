@@ -60,3 +60,24 @@ def test_uniform_logits_give_the_closed_form_features():
         assert abs(feats[i, 1]) < 1e-7
         assert abs(feats[i, 2] - (1.0 if K >= 2 else 0.0)) < 1e-6
         assert abs(feats[i, 3] - max(2, K) / 255.0) < 1e-7
+
+
+def test_act_head_reads_the_pooled_row_and_features_in_order():
+    """Closed form: with the act head wired to pass one input slot through GELU to action logit 0 (logit 1 is
+    GELU(0) = 0), log(p0/p1) = GELU(slot value) for pooled columns 0, 1, 17, 63 of h[start] and the four
+    features, whose values are known without the read-out's formulas (tests/helpers.closed_form_readout_case).
+    A pooled row other than the item's first (its column 0 has the other sign), a pooled value taken before the
+    type embedding, or features in another order all fail."""
+    from helpers import READOUT_SLOTS, act_head_selecting, closed_form_readout_case
+    mc, params, batch, expected = closed_form_readout_case()
+    for double in (True, False):
+        for slot in READOUT_SLOTS:
+            o = oracle.OracleModel(mc, double=double)
+            o.set_params(act_head_selecting(params, slot))
+            o.forward(batch, training=False)
+            probs, feats, _ = o.readout()
+            got = np.log(probs[:, 0].astype(np.float64) / probs[:, 1])
+            x = expected[:, slot]
+            want = 0.5 * x * (1.0 + erf(x / np.sqrt(2.0)))
+            np.testing.assert_allclose(got, want, atol=2e-6, err_msg=f"slot {slot}")
+        np.testing.assert_allclose(feats, expected[:, 64:], atol=1e-6)

@@ -154,6 +154,8 @@ def test_build_config_keeps_unknown_keys(tmp_path):
 def test_rolling_checkpoint_swap_survives_an_interruption(tmp_path):
     """The rolling checkpoint is written whole into a sibling directory and swapped in by renames; an
     interruption at any point leaves one complete checkpoint that resume picks up."""
+    import json
+
     from laya_amd.trainer import STATE_FILE, _recover_rolling, _swap_in
 
     def make(d, epoch):
@@ -161,13 +163,14 @@ def test_rolling_checkpoint_swap_survives_an_interruption(tmp_path):
         with open(os.path.join(d, "model.safetensors"), "w") as f:
             f.write(f"weights {epoch}")
         with open(os.path.join(d, STATE_FILE), "w") as f:
-            f.write(f"state {epoch}")
+            json.dump({"next_epoch": epoch}, f)
 
     def epoch_of(d):
         a = open(os.path.join(d, "model.safetensors")).read().split()[1]
-        b = open(os.path.join(d, STATE_FILE)).read().split()[1]
-        assert a == b
-        return int(a)
+        with open(os.path.join(d, STATE_FILE)) as f:
+            b = json.load(f)["next_epoch"]
+        assert int(a) == b
+        return b
 
     rolling = str(tmp_path / "checkpoint_latest")
     make(rolling + ".new", 1)
@@ -186,6 +189,21 @@ def test_rolling_checkpoint_swap_survives_an_interruption(tmp_path):
         f.write("weights 3")
     _recover_rolling(rolling)
     assert epoch_of(rolling) == 2
+    # A staged loop state cut short (present but not parseable) does not count as complete.
+    shutil.rmtree(rolling + ".new", ignore_errors=True)
+    make(rolling + ".new", 3)
+    with open(os.path.join(rolling + ".new", STATE_FILE), "w") as f:
+        f.write('{"next_ep')
+    os.rename(rolling, rolling + ".old")
+    _recover_rolling(rolling)
+    assert epoch_of(rolling) == 2
+    # A rolling checkpoint whose loop state does not parse gives way to a complete retired one.
+    shutil.rmtree(rolling + ".old", ignore_errors=True)
+    shutil.copytree(rolling, rolling + ".old")
+    with open(os.path.join(rolling, STATE_FILE), "w") as f:
+        f.write("")
+    _recover_rolling(rolling)
+    assert epoch_of(rolling) == 2 and not os.path.exists(rolling + ".old")
 
 
 def test_safetensors_write_replaces_the_file_whole(tmp_path):
