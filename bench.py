@@ -12,7 +12,8 @@ AdamW lr 3e-5 wd 0.01, clip 1.0, head dropout 0.1. Weights N(0, 0.02) from a fix
 (laya_amd.model.synthetic_params), unit LayerNorm weights, zero biases.
 
 `--workload` selects another shape (batch 4 × 128; batch 32 × 1024 and a packed Zipf batch of 64
-sequences with the backward products in bf16; batch 2 × 8192); the default is the one above.
+sequences with bf16 weights and the backward products on bf16 operands; batch 2 × 8192); the default is the
+one above.
 
 Prints one JSON line. `value` counts real (unpadded) tokens per second over the timed steps, with
 every input already resident; `roofline` describes the kernel with the largest share of device
@@ -95,14 +96,18 @@ WORKLOADS = {
                    heads="choice5", summed=False, matmul="fp32"),
     "b32x512": dict(desc="batch 32 x seq 512, trailing padding U[0,0.3], heads choice8/score4/noul2, summed CE",
                     batch=32, seq=512, pad=0.3, heads="mixed", summed=True, matmul="fp32"),
-    "b32x1024-bf16": dict(desc="batch 32 x seq 1024, no padding, heads choice8/score4/noul2, summed CE, backward "
-                               "products in bf16 (fp32 master weights, accumulation, softmax and LayerNorm statistics)",
-                          batch=32, seq=1024, pad=0.0, heads="mixed", summed=True, matmul="bf16-backward"),
+    "b32x1024-bf16": dict(desc="batch 32 x seq 1024, no padding, heads choice8/score4/noul2, summed CE, bf16 weights "
+                               "(the forward's fp32-accurate products read them rounded to bf16), backward products "
+                               "on bf16 operands (fp32 master weights, accumulation, softmax and LayerNorm statistics)",
+                          batch=32, seq=1024, pad=0.0, heads="mixed", summed=True, matmul="bf16-backward",
+                          bf16_weights=True),
     "b2x8192": dict(desc="batch 2 x seq 8192, no padding, one choice head K=5, mean CE", batch=2, seq=8192, pad=0.0,
                     heads="choice5", summed=False, matmul="fp32"),
     "packed64-zipf-bf16": dict(desc="64 sequences of lengths U[16,2048] packed without padding, ids Zipf(1.1), heads "
-                                    "choice8/score4/noul2, summed CE, backward products in bf16",
-                               batch=64, seq=2048, pad=None, heads="mixed", summed=True, matmul="bf16-backward"),
+                                    "choice8/score4/noul2, summed CE, bf16 weights, backward products on bf16 "
+                                    "operands",
+                               batch=64, seq=2048, pad=None, heads="mixed", summed=True, matmul="bf16-backward",
+                               bf16_weights=True),
 }
 
 
@@ -209,6 +214,9 @@ def main():
                     help="fp32 products from three-piece bf16 splits in every kernel instead of two-piece fp16 "
                          "products in the 256-wide ones (for comparison)")
     ap.add_argument("--no-profile", action="store_true", help="time without per-launch events")
+    ap.add_argument("--all-bf16", action="store_true",
+                    help="bf16 workloads: every product on bf16 operands (forward too: bf16 weights and activations) "
+                         "instead of bf16 weights with fp32-accurate forward products (for comparison)")
     ap.add_argument("--no-bf16-copies", action="store_true",
                     help="bf16 workloads: round the fp32 weights and activations inside the products instead of "
                          "keeping bf16 copies (same results, less memory)")
@@ -238,12 +246,16 @@ def main():
         matmul = "fp32-mfma"
     elif matmul == "fp32" and args.split3:
         matmul = "fp32-split3"
+    elif matmul.startswith("bf16") and args.all_bf16:
+        matmul = "bf16"
     ctx.set_matmul_precision(matmul)
     cpu_items = args.cpu_items or (16 if w["seq"] <= 512 else 1)
     long_workload = w["seq"] > 512
     model = TrainableDecisionModel(mc, ctx)
     model.set_params(synthetic_params(model.shapes, PARAM_SEED))
     model.head_dropout = 0.1
+    if w.get("bf16_weights") and matmul != "bf16":
+        model.set_bf16_weights(True)
     if args.no_bf16_copies:
         model.set_bf16_copies(False)
     if args.traffic_probe:
@@ -363,7 +375,10 @@ def main():
     line = {"metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(elapsed / args.steps * 1e3, 3), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None,
-            "dtype": "fp32" if w["matmul"].startswith("fp32") else "fp32 (bf16 operands in the backward products)",
+            "dtype": ("fp32" if w["matmul"].startswith("fp32") else
+                      "bf16 (every product on bf16 operands, fp32 accumulation)" if matmul == "bf16" else
+                      "bf16 weights (fp32-accurate forward products), bf16 operands in the backward products, fp32 "
+                      "accumulation"),
             "data": "synthetic",
             "config": {"workload": f"ModernBERT-base Laya encoder + decision head fine-tune step, {w['desc']}, "
                                    "AdamW lr 3e-5 wd 0.01, clip 1.0",
@@ -374,7 +389,16 @@ def main():
                                                      "MFMA products each); fp32 accumulation",
                                             "fp32-split3": "fp32 products from exact three-piece bf16 splits (six "
                                                            "bf16 MFMA products each, fp32 accumulation)",
-                                            "fp32-mfma": "fp32 products on the fp32 MFMA"}.get(matmul, matmul),
+                                            "fp32-mfma": "fp32 products on the fp32 MFMA",
+                                            "bf16-backward": ("bf16 weights: the forward's fp32-accurate two-piece "
+                                                              "products read each weight rounded to bf16 (fp32 "
+                                                              "activations); the backward products (dX, dW) on bf16 "
+                                                              "operands; fp32 accumulation and masters"
+                                                              if w.get("bf16_weights") else
+                                                              "fp32-accurate forward products; the backward products "
+                                                              "on bf16 operands; fp32 accumulation"),
+                                            "bf16": "every product on bf16 operands (weights and activations), "
+                                                    "fp32 accumulation and masters"}.get(matmul, matmul),
                        "real_tokens_per_step": round(tokens / args.steps, 1),
                        "inputs": ("host arrays passed every step (PCIe-inclusive)" if args.by_value else
                                   "staged in HBM before the timed steps")},

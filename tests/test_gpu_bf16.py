@@ -429,3 +429,27 @@ def test_every_product_in_bf16_against_the_fp32_oracle(ctx, weights):
     print(f"logits rel-L2 vs fp32: {rel_l2(lo, logits):.2e}", flush=True)
     worst = _grads_match(list(grads), {n: o.grad(n) for n in grads}, grads, 2e-2 if weights == "relu-clear" else 1e-1)
     print(f"every product in bf16 ({weights}): worst gradient rel-L2 vs the fp32 oracle {worst:.2e}", flush=True)
+
+
+def test_bf16_weights_with_bf16_backward_products_against_the_oracle(ctx):
+    """The policy the bf16 benchmark workloads run: bf16 weights (each product reads the weight rounded to bf16,
+    PackedMatrixBf16.cs:7-21) with a forward of fp32-accurate products on fp32 activations, and the backward
+    products on bf16 operands (weights, output gradients and saved activations rounded to bf16, fp32
+    accumulation). ModernBERT-base, 22 layers, 4 × 256, the benchmark's kind of initialisation (zero biases,
+    unit γ), against the oracle fed the same bf16-rounded weights: logits to 1e-5 (the forward is the oracle's
+    function) and every gradient within the bf16 bar, 2e-2."""
+    from laya_amd.model import synthetic_params
+    print("bf16 weights + bf16 backward products vs the oracle with bf16-rounded weights", flush=True)
+    mc, shapes, _, batch, targets = _modernbert_base_case(91)
+    params = synthetic_params(shapes, 91)
+    rounded = {n: (bf16(v) if n in _product_weights(shapes) else v) for n, v in params.items()}
+    seed = 91
+    logits, g, grads = _forward_backward(ctx, mc, params, batch, targets, seed, "bf16-backward", bf16_weights=True)
+    o = oracle.OracleModel(mc)
+    o.set_params(rounded)
+    o.set_head_dropout(0.1)
+    lo = o.forward(batch, training=True, keep_tape=True, seed=seed)
+    assert np.abs(logits - lo).max() < 1e-5
+    o.backward(g)
+    worst = _grads_match(list(grads), {n: o.grad(n) for n in grads}, grads, 2e-2)
+    print(f"bf16 weights + bf16 backward products: worst gradient rel-L2 vs the oracle {worst:.2e}", flush=True)

@@ -65,9 +65,9 @@ def _step(ctx, workload, policy="fp32"):
     return m, fx, batch, logits, prof
 
 
-def _check_gradients(m, fx, only=None, bar_of=None):
+def _check_gradients(m, fx, only=None):
     """Every gradient (or those `only` keeps) against the fixture: rel-L2 ≤ max(1e-4, 4 × the fp32 oracle's
-    own distance from fp64) by default, or the bar `bar_of(name, fp32_err)` gives."""
+    own distance from fp64)."""
     names = [str(n) for n in fx["names"]]
     with_grad = [n for n in m.names if m.has_grad(n)]
     assert sorted(with_grad) == sorted(names)
@@ -77,7 +77,7 @@ def _check_gradients(m, fx, only=None, bar_of=None):
             continue
         g = m.grad(n)
         r = sketch_rel_l2(fx["sk/" + n], sketch(n, g))
-        bar = bar_of(n, float(fx["fp32_err"][i])) if bar_of else max(1e-4, 4 * float(fx["fp32_err"][i]))
+        bar = max(1e-4, 4 * float(fx["fp32_err"][i]))
         assert r < bar, (n, r, bar)
         if r >= 1e-4:
             bar_hits += 1
@@ -170,9 +170,10 @@ def test_benchmark_step_itself_matches_fp64(ctx, policy):
     Zero head biases put the head ReLU inputs around zero, so a few of ~88M may sit within rounding of it and
     be decided differently by any two fp32 implementations (the fp32 oracle too). The test proves that every
     GPU decision outside the exact ties agrees with fp64 and that the tie inputs themselves are within the
-    fp32 error bound; the gradients the backward forms before the first differing ReLU are held at 1e-4
-    directly, and every gradient is then held to the bar of the other full-size tests after the exact
-    decisions are put at the differing ties (values within rounding of zero) and the backward run again."""
+    fp32 error bound; the gradients the backward forms before the first differing ReLU are held directly to
+    the bar of the other full-size tests (1e-4, or 4 × the fp32 oracle's error for the output bias, whose exact
+    gradient is rounding noise), and every gradient is then held to that bar after the exact decisions are put
+    at the differing ties (values within rounding of zero) and the backward run again."""
     from laya_amd.config import modernbert_base
     from laya_amd.model import TrainableDecisionModel, synthetic_params
     print(f"full size: bench.py's own step (its parameters, batch 32 x 512, seed {BENCH_STEP_SEED}), {policy}",
@@ -199,8 +200,8 @@ def test_benchmark_step_itself_matches_fp64(ctx, policy):
             _check_gradients(m, fx)
         else:
             top = max(flipped)
-            print(f"gradients formed before head layer {top}'s ReLU, at 1e-4:", flush=True)
-            _check_gradients(m, fx, only=_unaffected_by(top), bar_of=lambda n, e: 1e-4)
+            print(f"gradients formed before head layer {top}'s ReLU, as they are:", flush=True)
+            _check_gradients(m, fx, only=_unaffected_by(top))
             m.zero_gradients()
             m.forward(batch, training=True, seed=BENCH_STEP_SEED)
             again = _relu_decisions(m, fx, BENCH_STEP_SEED)
