@@ -57,7 +57,13 @@ int laya_ctx_set_memory_cap(laya_ctx* ctx, size_t bytes);
  * the fp32 matrix-core path (within 1e-6 relative L2 of the fp64 product on every tested shape): the
  * 256-wide kernels (the large products) split each operand, scaled by a power of two taken from its
  * largest finite magnitude, into two fp16 pieces and add three piece products per fp32 product; the
- * other kernels split each operand exactly into three bf16 pieces and add six piece products.
+ * other kernels split each operand exactly into three bf16 pieces and add six piece products. The
+ * operand-wide scale bounds the two-piece products' accuracy row by row: an output row whose operand row
+ * lies 2^-k below the operand's largest keeps ≈ 2^(k-39) relative error (fp32 itself: 2^-24), so rows
+ * within 2^15 of the largest are fp32-accurate, rows 2^20 below it carry ≈ 2e-6, and rows below 2^-39 of it
+ * lose their precision. A caller whose rows span more selects LAYA_MATMUL_SPLIT3_* for that class; the
+ * model's backward does so by itself when the items' logit gradients span more than 2^14
+ * (laya_model_backward_fallback).
  * LAYA_MATMUL_SPLIT3_* keeps a class on the three-piece splits everywhere; LAYA_MATMUL_FP32_MFMA selects
  * the fp32 matrix cores instead. A bf16 class rounds both operands
  * to bf16 (nearest even) as they are staged and multiplies on the bf16 matrix cores with fp32
@@ -320,6 +326,13 @@ int laya_model_forward(laya_model* model, const laya_batch* batch, int training,
 int laya_model_readout(laya_model* model, float* logits_host, float* act_probs_host, float* features_host);
 /* Backward (TrainableDecisionModel.cs:479-549): dlogits_host has Σ n_options floats. */
 int laya_model_backward(laya_model* model, const float* dlogits_host);
+/* Whether the last backward ran its products (linears and attention) on three-piece bf16 splits instead of the
+ * two-piece fp16 products the precision policy selects: it does when the items' largest |dL/dlogit| span more
+ * than 2^14. Every activation-gradient row of an item scales with that item's logit gradients, and a two-piece
+ * product scales its operand from the operand's largest magnitude, so rows far below it would keep less than
+ * fp32's relative precision; the three-piece pieces carry fp32's exponent range. (No counterpart in the
+ * reference, whose fp32 products have no operand scale.) */
+int laya_model_backward_fallback(laya_model* model, int* split3);
 /* Gradients.ClipByGlobalNorm (AdamW.cs:103-130); norm_out (may be NULL) synchronises, and then a NaN or
  * infinite norm returns LAYA_ERR_NOT_FINITE (norm_out still written, gradients left unscaled as the
  * reference leaves them). */

@@ -147,6 +147,7 @@ SIGNATURES = {
     "laya_model_get_param_bf16": (c_int, [P, c_int, P]),
     "laya_model_forward": (c_int, [P, ctypes.POINTER(BatchC), c_int, c_u64, P]),
     "laya_model_backward": (c_int, [P, P]),
+    "laya_model_backward_fallback": (c_int, [P, ctypes.POINTER(c_int)]),
     "laya_model_readout": (c_int, [P, P, P, P]),
     "laya_model_objective_rlcd": (c_int, [P, P, P, c_int, c_double, c_double, c_double, c_double, c_double, P]),
     "laya_model_backward_from_objective": (c_int, [P]),

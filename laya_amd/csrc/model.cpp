@@ -17,6 +17,7 @@
 #include <cmath>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <vector>
 
 #include "elementwise.hpp"
@@ -66,6 +67,7 @@ struct BatchTables {
 struct StagedBatch {
     int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0;
     double keys_full = 0, keys_local = 0;
+    std::vector<int> opt_off;  // host copy: item i's options are logits [opt_off[i], opt_off[i + 1])
     void* block = nullptr;  // the tables, then the soft-CE targets
     BatchTables tables{};
     float* targets = nullptr;
@@ -174,6 +176,13 @@ struct laya_model {
     // passed by value; `cur` is what the kernels read (own, or a staged batch's tables)
     BatchTables own{}, cur{};
     std::vector<StagedBatch> staged;  // laya_model_stage_batch slots; a null block marks a free slot
+    // The current batch's option offsets on the host, and the logit gradients of the last backward read back
+    // for the range check below.
+    std::vector<int> opt_off_host;
+    std::vector<float> dl_host;
+    // The last backward ran its products on three-piece splits because the items' logit gradients spanned more
+    // than BACKWARD_RANGE (laya_model_backward_fallback).
+    bool backward_split3 = false;
     // LayerNorm dγ/dβ partials of one backward (a slice per LayerNorm) and their deferred reductions, run
     // as one launch at the end of the backward
     float* ln_part = nullptr;
@@ -634,6 +643,7 @@ template <typename B> void set_batch_sizes(laya_model* m, const B& b) {
     m->max_opts = b.max_opts;
     m->keys_full = b.keys_full;
     m->keys_local = b.keys_local;
+    m->opt_off_host = b.opt_off;
     ensure_activations(m, b.T, b.nmark, b.nseg);
     ensure_rotary(m, b.max_len);
 }
@@ -926,8 +936,61 @@ void backward_body(laya_model* m);
 
 // Backward (TrainableDecisionModel.cs:479-549), from dscores already on the device. The LayerNorm dγ/dβ
 // partials of every site are reduced in one launch at the end (each in its fixed order).
-void backward(laya_model* m) {
+// The backward is linear in the logit gradients and, apart from the parameter gradients' sums, separate per
+// item: every activation-gradient row of item i scales with item i's logit gradients. A two-piece product scales
+// its operand by one power of two from the operand's largest magnitude, so a row far below that largest loses
+// relative precision (a row 2^-k of it keeps ≈ 2^(k-39) relative error, from subnormal fp16 pieces). When the
+// items' largest |dL/dlogit| span more than this factor, the backward runs its products (linears and
+// attention) on exact three-piece bf16 splits, whose pieces carry fp32's exponent range.
+constexpr float BACKWARD_RANGE = 16384.0f;  // 2^14
+
+bool logit_range_too_wide(const laya_model* m, const float* dl) {
+    float hi = 0.0f, lo = INFINITY;
+    for (size_t i = 0; i + 1 < m->opt_off_host.size(); ++i) {
+        float a = 0.0f;
+        for (int o = m->opt_off_host[i]; o < m->opt_off_host[i + 1]; ++o) a = std::max(a, std::fabs(dl[o]));
+        if (!(a > 0.0f) || !std::isfinite(a)) continue;  // zero (or non-finite) items: no range to keep
+        hi = std::max(hi, a);
+        lo = std::min(lo, a);
+    }
+    return hi > 0.0f && hi > BACKWARD_RANGE * lo;
+}
+
+// Restores the context's two-piece choices when a backward that set them aside ends (or throws).
+struct PairPolicyScope {
+    laya_ctx* ctx;
+    int pair;
+    bool attention;
+    explicit PairPolicyScope(laya_ctx* c) : ctx(c), pair(c->matmul_pair), attention(c->attention_pair) {
+        ctx->matmul_pair &= ~(LAYA_MATMUL_BF16_INPUT_GRAD | LAYA_MATMUL_BF16_WEIGHT_GRAD);
+        ctx->attention_pair = false;
+    }
+    ~PairPolicyScope() {
+        ctx->matmul_pair = pair;
+        ctx->attention_pair = attention;
+    }
+};
+
+// dl_host: the logit gradients already on the host (else read back from ds_scores when the range check needs
+// them, which only the two-piece products do).
+void backward(laya_model* m, const float* dl_host = nullptr) {
     LAYA_REQUIRE(m->has_tape, "backward: run forward first");
+    laya_ctx* ctx = m->ctx;
+    bool wide = false;
+    if (m->nmark > 0 && ((ctx->matmul_pair & (LAYA_MATMUL_BF16_INPUT_GRAD | LAYA_MATMUL_BF16_WEIGHT_GRAD)) ||
+                         ctx->attention_pair)) {
+        if (!dl_host) {
+            m->dl_host.resize(m->nmark);
+            LAYA_HIP(hipMemcpyAsync(m->dl_host.data(), m->ds_scores, sizeof(float) * m->nmark,
+                                    hipMemcpyDeviceToHost, ctx->stream));
+            LAYA_HIP(hipStreamSynchronize(ctx->stream));
+            dl_host = m->dl_host.data();
+        }
+        wide = logit_range_too_wide(m, dl_host);
+    }
+    m->backward_split3 = wide;
+    std::unique_ptr<PairPolicyScope> scope;
+    if (wide) scope.reset(new PairPolicyScope(ctx));
     ensure_mirror(m);
     const int d = m->d();
     const size_t sites = 2 * (size_t)m->cfg.layers + 2 * (size_t)m->cfg.head_layers + 3;
@@ -1349,7 +1412,7 @@ int laya_model_backward(laya_model* m, const float* dlogits_host) {
         if (m->nmark)
             LAYA_HIP(hipMemcpyAsync(m->ds_scores, dlogits_host, sizeof(float) * m->nmark, hipMemcpyHostToDevice,
                                     m->ctx->stream));
-        backward(m);
+        backward(m, dlogits_host);
         LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
     });
 }
@@ -1463,6 +1526,7 @@ int laya_model_stage_batch(laya_model* m, const laya_batch* batch, const float* 
         s.max_opts = bp.max_opts;
         s.keys_full = bp.keys_full;
         s.keys_local = bp.keys_local;
+        s.opt_off = bp.opt_off;
         Carver cv;
         TableCarve tc;
         tc.add(cv, (size_t)bp.T, (size_t)std::max(bp.nmark, 1), (size_t)bp.nseg);
@@ -1513,6 +1577,14 @@ int laya_model_objective_rlcd(laya_model* m, const float* targets_host, const do
                                     m->ctx->stream));
             LAYA_HIP(hipStreamSynchronize(m->ctx->stream));
         }
+    });
+}
+
+int laya_model_backward_fallback(laya_model* m, int* split3) {
+    return guarded([&] {
+        checked(m);
+        LAYA_REQUIRE(split3, "backward_fallback: null argument");
+        *split3 = m->backward_split3 ? 1 : 0;
     });
 }
 

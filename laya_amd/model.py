@@ -367,6 +367,14 @@ class TrainableDecisionModel:
         d = np.ascontiguousarray(logit_gradients, np.float32)
         check(lib().laya_model_backward(self.handle, d.ctypes.data))
 
+    @property
+    def backward_fell_back(self) -> bool:
+        """Whether the last backward ran its products on three-piece splits because the items' logit gradients
+        spanned more than 2^14 (two-piece products would lose precision on the smallest items' rows)."""
+        v = ctypes.c_int()
+        check(lib().laya_model_backward_fallback(self.handle, ctypes.byref(v)))
+        return bool(v.value)
+
     def objective_rlcd(self, targets, draws, sigma: float, spherical_weight: float = 0.75, rps_weight: float = 1.0,
                        ce_weight: float = 1.0, scale: float = 1.0) -> tuple:
         """RlcdObjective.Compute on the last forward's logits, on the device (RlcdObjective.cs:57-155):

@@ -582,3 +582,62 @@ def test_readout_act_head_wiring_in_closed_form(ctx):
         np.testing.assert_allclose(got, 0.5 * x * (1.0 + erf(x / np.sqrt(2.0))), atol=2e-6, err_msg=f"slot {slot}")
     np.testing.assert_allclose(feats, expected[:, 64:], atol=1e-6)
     m.close()
+
+
+def test_backward_keeps_precision_for_items_with_tiny_logit_gradients(ctx):
+    """An item whose logit gradients sit 1e-9 below the others' (a confidently right item under a summed CE):
+    every activation-gradient row of that item is ≈1e-9 of the largest, below what a two-piece product's
+    tensor-wide scale represents to fp32 precision. The backward sees the span in the logit gradients and runs
+    its products on three-piece splits; the embedding-gradient rows of tokens only that item holds (tiny, and
+    outputs of the dX chain) then match fp64 row by row to 1e-4, and every gradient to the usual bar. With the
+    span removed the two-piece products run again."""
+    from helpers import fixture_params
+    from laya_amd.batch import Batch
+    from laya_amd.model import TrainableDecisionModel
+    mc = mid_config(layers=2)
+    o = oracle.OracleModel(mc)
+    params = fixture_params(o.shapes, 17)
+    rng = np.random.default_rng(18)
+    lengths = [200, 150, 90]
+    opts = [8, 4, 2]
+    # The last item's tokens come from ids [900, 1000), the others' from [0, 900).
+    tokens = np.concatenate([rng.integers(0, 900, 200), rng.integers(0, 900, 150), rng.integers(900, 1000, 90)])
+    batch = Batch(lengths=np.array(lengths, np.int32), tokens=tokens.astype(np.int32),
+                  n_options=np.array(opts, np.int32),
+                  markers=np.concatenate([1 + 2 * np.arange(k) for k in opts]).astype(np.int32),
+                  qtypes=np.array([0, 1, 2], np.int32))
+    dl = rng.standard_normal(batch.n_markers).astype(np.float32)
+    dl[-2:] *= np.float32(1e-9)
+    o64 = oracle.OracleModel(mc, double=True)
+    for ref in (o, o64):
+        ref.set_params(params)
+        ref.forward(batch, training=False, keep_tape=True)
+        ref.backward(dl)
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    m.forward(batch, training=False)
+    ctx.profile_begin()
+    m.backward(dl)
+    prof = ctx.profile_end()
+    assert m.backward_fell_back
+    assert not any(k.endswith(("_h2w", "_h2t", "_h2")) and k.startswith(("gemm_bwd", "attention_bwd"))
+                   for k in prof), sorted(prof)
+    emb = "encoder.embeddings.tok_embeddings.weight"
+    exact, got = o64.grad(emb), m.grad(emb)
+    only_small = np.unique(tokens[-90:])
+    num = np.linalg.norm(exact[only_small] - got[only_small], axis=1)
+    den = np.linalg.norm(exact[only_small], axis=1)
+    assert den.max() < 1e-6 * np.linalg.norm(exact[:900], axis=1).max()  # the rows really are tiny
+    print(f"tiny item's embedding rows: worst row relative error {float((num / den).max()):.2e}", flush=True)
+    assert (num / den).max() < 1e-4
+    for name in m.names:
+        if name == "temperature" or name.startswith("act_head"):
+            continue
+        e = o64.grad(name)
+        bar = max(1e-4, 4 * rel_l2(e, o.grad(name)))
+        assert rel_l2(e, m.grad(name)) < bar, name
+    m.zero_gradients()
+    dl2 = rng.standard_normal(batch.n_markers).astype(np.float32)
+    m.backward(dl2)
+    assert not m.backward_fell_back
+    m.close()
