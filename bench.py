@@ -195,6 +195,51 @@ def cpu_baseline(mc, batch, targets, items: int, summed: bool, extrapolate: bool
     return out
 
 
+def per_op_rate(ctx, mc, model, batches, w, args, scale):
+    """The same warm-up and timed steps composed from the per-op entry points alone (laya_amd.opmodel), from
+    the benchmark's initial weights, every batch's tables uploaded before the timed region."""
+    from laya_amd.model import synthetic_params
+    from laya_amd.opmodel import OpBatch, OpLevelModel
+    if w["matmul"] != "fp32" or w.get("bf16_weights"):
+        raise SystemExit("--per-op measures the fp32 workloads")
+    params = synthetic_params(model.shapes, PARAM_SEED)
+    om = OpLevelModel(mc, {n: params[n] for n in model.names}, ctx)
+    om.head_dropout = 0.1
+    obs = [OpBatch(ctx, b, t, mc.encoder.vocab_size) for b, t in batches]
+    ctx.sync()
+
+    def step(i):
+        om.train_step(obs[i], seed=STEP_SEED0 + i, ce_weight=1.0, loss_scale=scale(batches[i][0]), max_norm=1.0,
+                      lr_encoder=3e-5, lr_head=3e-5, weight_decay=0.01)
+
+    for i in range(args.warmup):
+        step(i)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, args.warmup + args.steps):
+        step(i)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    tokens = sum(b.n_tokens for b, _ in batches[args.warmup:])
+    print(f"per-op: timed {args.steps} steps in {dt:.3f} s", file=sys.stderr, flush=True)
+    if not args.no_profile:
+        ctx.profile_begin()
+        for i in range(args.warmup, args.warmup + args.steps):
+            step(i)
+        ctx.sync()
+        prof = ctx.profile_end()
+        total_ms = sum(k["ms"] for k in prof.values())
+        for name, k in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])[:16]:
+            print(f"  per-op {name:22s} {k['launches']:6d} launches {k['ms']:9.2f} ms {k['ms'] / total_ms * 100:5.1f}%",
+                  file=sys.stderr)
+    for ob in obs:
+        ob.close()
+    om.close()
+    return {"value": round(tokens / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt / args.steps * 1e3, 3),
+            "how": "the same steps composed from the per-op C-ABI entry points (laya_amd.opmodel), one call per "
+                   "Ops method in TrainableDecisionModel's order, from the same initial weights"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -223,6 +268,10 @@ def main():
     ap.add_argument("--by-value", action="store_true",
                     help="pass each batch as host arrays (laya_model_train_step: host planning and uploads inside "
                          "every step), to measure the PCIe-inclusive rate; the default stages batches first")
+    ap.add_argument("--per-op", action="store_true",
+                    help="also time the same steps composed from the per-op entry points alone (laya_amd.opmodel: what "
+                         "a host re-pointing Ops runs), from the same initial weights, and report it beside the model "
+                         "API's rate")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="before the steps, run one dst += src over 2^26 floats (add_kernel: 512 MiB read, 256 MiB "
                          "written) whose HBM counters calibrate FETCH_SIZE / WRITE_SIZE")
@@ -357,6 +406,11 @@ def main():
         breakdown["kernel_share"] = {n: round(k["ms"] / total_ms, 4) for n, k in
                                      sorted(prof.items(), key=lambda kv: -kv[1]["ms"])[:8]}
 
+    per_op = None
+    if args.per_op:
+        per_op = per_op_rate(ctx, mc, model, batches, w, args, scale)
+        per_op["vs_model_api"] = round(per_op["value"] / (tokens / elapsed), 4)
+
     cpu = None
     if not args.no_cpu:
         print(f"cpu baseline: oracle on {cpu_items} sequences", file=sys.stderr, flush=True)
@@ -403,6 +457,8 @@ def main():
                        "inputs": ("host arrays passed every step (PCIe-inclusive)" if args.by_value else
                                   "staged in HBM before the timed steps")},
             "roofline": roofline, "cpu_baseline": cpu, "breakdown": breakdown}
+    if per_op:
+        line["per_op"] = per_op
     print(json.dumps(line), flush=True)
     model.close()
     ctx.close()

@@ -210,6 +210,15 @@ int laya_embedding_bwd(laya_ctx* ctx, const int* sorted_pos, const int* unique_i
 int laya_gather_rows(laya_ctx* ctx, const float* src, const int* rows_idx, int n, int width, float* dst);
 int laya_scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows_idx, int n, int width, float* dst);
 
+/* Type embedding (TrainableDecisionModel.cs:300-304): states[r] += table[qtype_of_row[r]] for every row (the
+ * item's question type repeated over its rows, device int32 in [0, 3)); width a multiple of 4. */
+int laya_type_embedding_fwd(laya_ctx* ctx, float* states, const int* qtype_of_row, int rows, int width,
+                            const float* table);
+/* Its gradient (TrainableDecisionModel.cs:512-521): grad[q] += Σ dstates[r] over the rows of type q, each
+ * type's rows summed in a fixed order (deterministic); grad is [3, width], width a multiple of 4. */
+int laya_type_embedding_bwd(laya_ctx* ctx, const float* dstates, const int* qtype_of_row, int rows, int width,
+                            float* grad);
+
 /* Soft cross-entropy gradient of RlcdObjective (RlcdObjective.cs:139-148, 150), policy term off:
  * g_o = ce_weight·(p_o·Σt − t_o)/n_items·scale with p = softmax(logits). Device arrays; options
  * concatenated, option_offsets[n_items + 1]. loss (device, may be NULL) receives the cross-entropy. */

@@ -118,6 +118,8 @@ SIGNATURES = {
     "laya_embedding_plan": (c_int, [P, c_int, c_int, P, P, P, ctypes.POINTER(c_int)]),
     "laya_embedding_bwd": (c_int, [P, P, P, P, c_int, P, c_int, P]),
     "laya_gather_rows": (c_int, [P, P, P, c_int, c_int, P]),
+    "laya_type_embedding_fwd": (c_int, [P, P, P, c_int, c_int, P]),
+    "laya_type_embedding_bwd": (c_int, [P, P, P, c_int, c_int, P]),
     "laya_scatter_add_rows": (c_int, [P, P, P, c_int, c_int, P]),
     "laya_softmax_ce_bwd": (c_int, [P, P, P, P, c_int, c_float, c_float, P, P]),
     "laya_rlcd_objective": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P, c_double, c_double, c_double,

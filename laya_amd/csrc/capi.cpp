@@ -649,6 +649,24 @@ int laya_gather_rows(laya_ctx* ctx, const float* src, const int* rows_idx, int n
     });
 }
 
+int laya_type_embedding_fwd(laya_ctx* ctx, float* states, const int* qtype_of_row, int rows, int width,
+                            const float* table) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && width > 0 && states && qtype_of_row && table, "type_embedding_fwd: bad arguments");
+        add_indexed_rows(ctx, states, qtype_of_row, rows, width, table);
+    });
+}
+
+int laya_type_embedding_bwd(laya_ctx* ctx, const float* dstates, const int* qtype_of_row, int rows, int width,
+                            float* grad) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && width > 0 && dstates && qtype_of_row && grad, "type_embedding_bwd: bad arguments");
+        type_embedding_bwd(ctx, dstates, qtype_of_row, rows, width, grad);
+    });
+}
+
 int laya_scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows_idx, int n, int width, float* dst) {
     return guarded([&] {
         require_ctx(ctx);

@@ -94,8 +94,11 @@ struct laya_ctx {
     int matmul_pair = LAYA_MATMUL_SPLIT_ALL;
     // Attention's split products as two-piece fp16 products too (the default).
     bool attention_pair = true;
-    // max|operand| words of the two-piece products that no caller keeps (one per operand of a product).
+    // max|operand| words of the two-piece products that no caller keeps: a ring of AMAX_RING word groups, each
+    // measurement taking the next; the whole ring is cleared (one launch) each time it wraps. Stream order
+    // keeps this safe: every product that read a group was launched before the clear that recycles it.
     unsigned* amax = nullptr;
+    int amax_next = 0;
     std::vector<hipEvent_t> event_pool;
     std::vector<laya::LaunchRecord> launches;
     int next_event = 0;
@@ -178,6 +181,7 @@ __device__ inline double wave_sum_d(double v) {
 // sixteen memory lines rather than one (on one line the atomics serialise: a LayerNorm forward measured
 // 2.6 times slower); a group spans AMAX_GROUP words.
 constexpr int AMAX_SPREAD = 16, AMAX_STRIDE = 64, AMAX_GROUP = AMAX_SPREAD * AMAX_STRIDE;
+constexpr int AMAX_RING = 128;  // operand word groups the context measures into in turn (512 KB)
 __device__ inline unsigned amax_bits(float x) {
     const unsigned a = __builtin_bit_cast(unsigned, x) & 0x7fffffffu;
     return a < 0x7f800000u ? a : 0u;  // infinities and NaNs left out

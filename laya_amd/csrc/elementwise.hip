@@ -263,6 +263,16 @@ __global__ void gather_rows_kernel(const float* src, const int* rows, int n, int
     }
 }
 
+// dst[r] += table[idx[r]] over [rows, width] (float4 columns).
+__global__ void add_indexed_rows4_kernel(f32x4* __restrict__ dst, const int* __restrict__ idx, int rows, int w4,
+                                         const f32x4* __restrict__ table) {
+    const size_t total = (size_t)rows * w4;
+    GRID_STRIDE(i, total) {
+        const size_t r = i / w4, c = i - r * w4;
+        dst[i] += table[(size_t)idx[r] * w4 + c];
+    }
+}
+
 // dst[rows[r]] += src[r] for r in order (one thread per column; rows may repeat).
 __global__ void scatter_add_rows_kernel(const float* src, const int* rows, int n, int width, float* dst) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -648,6 +658,14 @@ void scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows, int n, i
     hipLaunchKernelGGL(scatter_add_rows_kernel, dim3((width + 255) / 256), dim3(256), 0, ctx->stream, src, rows, n,
                        width, dst);
     check_launch("scatter_add_rows_kernel");
+}
+void add_indexed_rows(laya_ctx* ctx, float* dst, const int* idx, int rows, int width, const float* table) {
+    if (rows <= 0 || width <= 0) return;
+    LAYA_REQUIRE(width % 4 == 0 && vec4(dst) && vec4(table), "add_indexed_rows: 16-byte aligned rows of a multiple of 4");
+    ProfileScope scope(ctx, "add_indexed_rows", 0.0, 8.0 * rows * (double)width);
+    hipLaunchKernelGGL(add_indexed_rows4_kernel, dim3(grid_for((size_t)rows * width / 4)), dim3(256), 0, ctx->stream,
+                       reinterpret_cast<f32x4*>(dst), idx, rows, width / 4, reinterpret_cast<const f32x4*>(table));
+    check_launch("add_indexed_rows4_kernel");
 }
 void type_embedding_bwd(laya_ctx* ctx, const float* d, const int* row_type, int rows, int width, float* grad) {
     if (rows <= 0) return;

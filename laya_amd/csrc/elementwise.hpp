@@ -33,6 +33,8 @@ void gather_rows(laya_ctx* ctx, const float* src, const int* rows, int n, int wi
 void scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows, int n, int width, float* dst);
 // grad[type] += Σ over rows r with row_type[r] == type of d[r] (TrainableDecisionModel.cs:512-521).
 void type_embedding_bwd(laya_ctx* ctx, const float* d, const int* row_type, int rows, int width, float* grad);
+// dst[r] += table[idx[r]] for rows r of width floats (the type embedding's add).
+void add_indexed_rows(laya_ctx* ctx, float* dst, const int* idx, int rows, int width, const float* table);
 // ReLU + dropout backward from the forward's output (positive exactly where the gradient passes).
 void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g, size_t n, float p);
 // out[type·n + c] += Σ rows of x[r][c] (per row type when row_type is given; types 1 or 3), in a fixed

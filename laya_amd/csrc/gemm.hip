@@ -2344,11 +2344,18 @@ void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, uns
 
 namespace {
 
-// max|x| of a rows x cols operand into the context's word group `slot` (cleared first); returns it.
+// max|x| of a rows x cols operand into the context's next word group (the ring is cleared, in one launch,
+// whenever it starts over); returns it. `slot` names the operand's role for the callers' bookkeeping only.
 const unsigned* operand_absmax(laya_ctx* ctx, int slot, const float* x, int rows, int cols, long ld) {
-    if (!ctx->amax) ctx->amax = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_SLOTS * AMAX_GROUP));
-    unsigned* out = ctx->amax + slot * AMAX_GROUP;
-    fill(ctx, reinterpret_cast<float*>(out), 0.0f, AMAX_GROUP);  // +0.0f is the all-zero word
+    (void)slot;
+    if (!ctx->amax) {
+        ctx->amax = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_RING * AMAX_GROUP));
+        ctx->amax_next = 0;
+    }
+    if (ctx->amax_next == 0)  // +0.0f is the all-zero word
+        fill(ctx, reinterpret_cast<float*>(ctx->amax), 0.0f, (size_t)AMAX_RING * AMAX_GROUP);
+    unsigned* out = ctx->amax + (size_t)ctx->amax_next * AMAX_GROUP;
+    ctx->amax_next = (ctx->amax_next + 1) % AMAX_RING;
     absmax_into(ctx, x, rows, cols, ld, out);
     return out;
 }

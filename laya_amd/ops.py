@@ -258,6 +258,20 @@ def scatter_add_rows(ctx: Context, src: DeviceArray, rows: DeviceArray, n: int, 
     check(lib().laya_scatter_add_rows(_h(ctx), src.ptr, rows.ptr, n, width, dst.ptr))
 
 
+def type_embedding(ctx: Context, states: DeviceArray, qtype_of_row: DeviceArray, rows: int, width: int,
+                   table: Parameter) -> None:
+    """TrainableDecisionModel.cs:300-304: each row gets its item's question-type vector added."""
+    check(lib().laya_type_embedding_fwd(_h(ctx), states.ptr, qtype_of_row.ptr, rows, width, table.data.ptr))
+
+
+def type_embedding_backward(ctx: Context, dstates: DeviceArray, qtype_of_row: DeviceArray, rows: int, width: int,
+                            table: Parameter) -> None:
+    """TrainableDecisionModel.cs:512-521: the type vectors' gradient, Σ of their rows' gradients."""
+    if table.trainable:
+        check(lib().laya_type_embedding_bwd(_h(ctx), dstates.ptr, qtype_of_row.ptr, rows, width,
+                                            table.gradient_buffer().ptr))
+
+
 def embedding_plan(ids: np.ndarray, vocab: int):
     """Token positions stably sorted by id, the unique ids and their run offsets."""
     import ctypes

@@ -168,3 +168,68 @@ def test_rotary_apply_matches_the_oracle(ctx):
         rot.apply(v, rows, pd, inverse=True)
         assert rel_l2(vec, v.numpy()) < 1e-6
         rot.close()
+
+
+def test_whole_step_from_op_entry_points_matches_the_oracle_and_the_model_driver(ctx):
+    """The whole training step composed from op entry points only (laya_amd.opmodel: what a host re-pointing
+    Ops runs, TrainableDecisionModel.cs:248-640 over Ops.cs), at ModernBERT-base widths with 3 encoder layers,
+    the two-layer head with dropout 0.1 and the scorer, on a batch of five ragged items. Every gradient against
+    the fp64 oracle at max(1e-4, 4 × the fp32 oracle's error), and the weights after a full step (soft CE,
+    clip, AdamW) equal to the reference's clip and AdamW formulas applied to the op path's own gradients."""
+    from helpers import fixture_params, mid_config, mixed_batch
+    from laya_amd.opmodel import OpBatch, OpLevelModel
+    mc = mid_config(layers=3)
+    o = oracle.OracleModel(mc)
+    params = fixture_params(o.shapes, 23)
+    batch = mixed_batch(np.random.default_rng(24), [300, 200, 129, 64, 17], mc.encoder.vocab_size)
+    rng = np.random.default_rng(25)
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+    seed, scale = 7, float(batch.n_items)
+    om = OpLevelModel(mc, {n: params[n] for n in o.names}, ctx)
+    ob = OpBatch(ctx, batch, targets, mc.encoder.vocab_size)
+    logits = om.forward(ob, seed, training=True).numpy()
+    _, g = oracle.cross_entropy(batch.n_options, logits, targets, 1.0, scale)
+    from laya_amd.device import DeviceArray
+    gd = DeviceArray.from_numpy(ctx, g)
+    om.backward(gd)
+    o64 = oracle.OracleModel(mc, double=True)
+    for ref in (o, o64):
+        ref.set_params(params)
+        ref.set_head_dropout(0.1)
+        ref.forward(batch, training=True, keep_tape=True, seed=seed)
+        ref.backward(g)
+    assert rel_l2(o64.forward(batch, training=True, keep_tape=False, seed=seed), logits) < 1e-5
+    worst = 0.0
+    for name in o.names:
+        if not o64.has_grad(name):
+            continue
+        exact = o64.grad(name)
+        bar = max(1e-4, 4 * rel_l2(exact, o.grad(name)))
+        r = rel_l2(exact, om.grad(name))
+        assert r < bar, (name, r, bar)
+        if bar == 1e-4:
+            worst = max(worst, r)
+    print(f"op-level step: worst gradient rel-L2 vs fp64 {worst:.2e}", flush=True)
+    # The rest of the step on the op path: the device soft-CE gradient, then ClipByGlobalNorm and AdamW.Step,
+    # against the reference's formulas applied on the host to the same gradients.
+    om.zero_gradients()
+    logits = om.forward(ob, seed, training=True)
+    dl = DeviceArray(ctx, (batch.n_markers,))
+    laya.softmax_ce_backward(ctx, logits, ob.targets, ob.offsets, batch.n_items, 1.0, scale, dl)
+    assert np.abs(dl.numpy() - g).max() <= 1e-6 * max(1.0, np.abs(g).max())
+    om.backward(dl)
+    trained = [n for n in o.names if o64.has_grad(n)]
+    grads = {n: om.grad(n) for n in trained}
+    clipped = {n: grads[n].copy() for n in trained}
+    oracle.clip(list(clipped.values()), 1.0)
+    lr = 1e-3
+    om.clip_and_step(1.0, lr, lr)
+    for name in o.names:
+        w = params[name].astype(np.float32).reshape(-1).copy()
+        if name != "temperature":
+            gr = clipped[name].reshape(-1) if name in clipped else np.zeros_like(w)
+            oracle.adamw_tensor(w, np.ascontiguousarray(gr), np.zeros_like(w), np.zeros_like(w), lr, 1)
+        assert np.abs(om.param(name).reshape(-1) - w).max() <= 1e-6 * max(1.0, np.abs(w).max()), name
+    assert not np.any(om.grad("scorer.1.weight"))  # the step cleared the gradients
+    ob.close()
+    om.close()
