@@ -1287,7 +1287,7 @@ const float* rotated_qkv(laya_ctx* ctx, const AttentionArgs& a) {
     const long threads = (long)a.max_len * (a.hidden / 2);
     dim3 grid((unsigned)((threads + 255) / 256), a.nseg);
     ProfileScope scope(ctx, "attention_rope", 0.0, 4.0 * 3.0 * a.hidden * (double)a.rows * 2.0);
-    hipLaunchKernelGGL(rope_rows_kernel, grid, dim3(256), 0, ctx->stream, a.qkv, a.seg_start, a.seg_len, a.hidden,
+    LAYA_LAUNCH(rope_rows_kernel, grid, dim3(256), 0, ctx->stream, a.qkv, a.seg_start, a.seg_len, a.hidden,
                        a.head_dim, a.cos_table, a.sin_table, out);
     check_launch("rope_rows_kernel");
     return out;
@@ -1333,17 +1333,17 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
         ProfileScope scope(ctx, pair ? "attention_fwd_h2" : split ? "attention_fwd_x6" : "attention_fwd",
                            4.0 * a.hidden * a.keys, 0.0);
         if (pair && p.p_drop > 0.0f)
-            hipLaunchKernelGGL((attn_fwd_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH((attn_fwd_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
         else if (pair)
-            hipLaunchKernelGGL((attn_fwd_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH((attn_fwd_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
         else if (split && p.p_drop > 0.0f)
-            hipLaunchKernelGGL((attn_fwd_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH((attn_fwd_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
         else if (split)
-            hipLaunchKernelGGL((attn_fwd_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH((attn_fwd_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
         else if (a.head_dim == 64)
-            hipLaunchKernelGGL(attn_fwd_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH(attn_fwd_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         else
-            hipLaunchKernelGGL(attn_fwd_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH(attn_fwd_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
         check_launch("attn_fwd_kernel");
     }
     if (context16 && !split) {
@@ -1380,16 +1380,16 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
             // dQ first: it forms each row's Σ dO·O and writes it for dK/dV.
             ProfileScope scope(ctx, "attention_bwd_dq_h2", 2.0 * fb, 0.0);
             if (p.p_drop > 0.0f)
-                hipLaunchKernelGGL((attn_bwd_dq_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+                LAYA_LAUNCH((attn_bwd_dq_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
             else
-                hipLaunchKernelGGL((attn_bwd_dq_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+                LAYA_LAUNCH((attn_bwd_dq_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
             check_launch("attn_bwd_dq_x6_kernel");
         }
         ProfileScope scope(ctx, "attention_bwd_dkv_h2", 2.0 * fb, 0.0);
         if (p.p_drop > 0.0f)
-            hipLaunchKernelGGL((attn_bwd_dkv_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH((attn_bwd_dkv_x6_kernel<64, true, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
         else
-            hipLaunchKernelGGL((attn_bwd_dkv_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH((attn_bwd_dkv_x6_kernel<64, false, 2>), grid, dim3(THREADS), 0, ctx->stream, p);
         check_launch("attn_bwd_dkv_x6_kernel");
         return;
     }
@@ -1399,43 +1399,43 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
             // dQ first: it forms each row's Σ dO·O and writes it for dK/dV.
             ProfileScope scope(ctx, "attention_bwd_dq_x6", 2.0 * fb, 0.0);
             if (p.p_drop > 0.0f)
-                hipLaunchKernelGGL((attn_bwd_dq_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
+                LAYA_LAUNCH((attn_bwd_dq_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
             else
-                hipLaunchKernelGGL((attn_bwd_dq_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
+                LAYA_LAUNCH((attn_bwd_dq_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
             check_launch("attn_bwd_dq_x6_kernel");
         }
         ProfileScope scope(ctx, "attention_bwd_dkv_x6", 2.0 * fb, 0.0);
         if (p.p_drop > 0.0f)
-            hipLaunchKernelGGL((attn_bwd_dkv_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH((attn_bwd_dkv_x6_kernel<64, true>), grid, dim3(THREADS), 0, ctx->stream, p);
         else
-            hipLaunchKernelGGL((attn_bwd_dkv_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH((attn_bwd_dkv_x6_kernel<64, false>), grid, dim3(THREADS), 0, ctx->stream, p);
         check_launch("attn_bwd_dkv_x6_kernel");
         return;
     }
     {
         ProfileScope scope(ctx, "attention_bwd_dots", 0.0, 8.0 * total);
         if (a.head_dim == 64)
-            hipLaunchKernelGGL(attn_dot_kernel<64>, dim3(dot_blocks), dim3(THREADS), 0, ctx->stream, dcontext, context,
+            LAYA_LAUNCH(attn_dot_kernel<64>, dim3(dot_blocks), dim3(THREADS), 0, ctx->stream, dcontext, context,
                                rows, a.hidden, a.heads, dots);
         else
-            hipLaunchKernelGGL(attn_dot_kernel<32>, dim3(dot_blocks), dim3(THREADS), 0, ctx->stream, dcontext, context,
+            LAYA_LAUNCH(attn_dot_kernel<32>, dim3(dot_blocks), dim3(THREADS), 0, ctx->stream, dcontext, context,
                                rows, a.hidden, a.heads, dots);
         check_launch("attn_dot_kernel");
     }
     {
         ProfileScope scope(ctx, "attention_bwd_dkv", 2.0 * fb, 0.0);
         if (a.head_dim == 64)
-            hipLaunchKernelGGL(attn_bwd_dkv_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH(attn_bwd_dkv_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         else
-            hipLaunchKernelGGL(attn_bwd_dkv_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH(attn_bwd_dkv_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
         check_launch("attn_bwd_dkv_kernel");
     }
     {
         ProfileScope scope(ctx, "attention_bwd_dq", 2.0 * fb, 0.0);
         if (a.head_dim == 64)
-            hipLaunchKernelGGL(attn_bwd_dq_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH(attn_bwd_dq_kernel<64>, grid, dim3(THREADS), 0, ctx->stream, p);
         else
-            hipLaunchKernelGGL(attn_bwd_dq_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
+            LAYA_LAUNCH(attn_bwd_dq_kernel<32>, grid, dim3(THREADS), 0, ctx->stream, p);
         check_launch("attn_bwd_dq_kernel");
     }
 }

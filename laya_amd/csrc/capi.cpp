@@ -84,9 +84,21 @@ ProfileScope::~ProfileScope() {
     try {
         const int stop = take_event(ctx);
         if (hipEventRecord(ctx->event_pool[stop], ctx->stream) == hipSuccess)
-            ctx->launches.push_back({name, start, stop, flops, bytes});
+            ctx->launches.push_back({name, start, stop, nested ? -1 : kstart, nested ? -1 : kstop, flops, bytes});
     } catch (...) {
     }
+}
+
+void profile_kernel_events(hipEvent_t* ev_start, hipEvent_t* ev_stop) {
+    ProfileScope* s = g_scope;
+    if (!s || s->start < 0 || !s->ctx->profiling) return;
+    for (ProfileScope* o = s->outer; o; o = o->outer) o->nested = true;
+    if (s->kstart < 0) {
+        s->kstart = take_event(s->ctx);
+        *ev_start = s->ctx->event_pool[s->kstart];
+    }
+    if (s->kstop < 0) s->kstop = take_event(s->ctx);
+    *ev_stop = s->ctx->event_pool[s->kstop];
 }
 
 // Rotary tables (Ops.cs:462-484): angles in double, cos/sin rounded to float.
@@ -297,7 +309,9 @@ int laya_profile_end(laya_ctx* ctx) {
         g_summary.clear();
         for (const auto& r : ctx->launches) {
             float ms = 0.0f;
-            LAYA_HIP(hipEventElapsedTime(&ms, ctx->event_pool[r.start], ctx->event_pool[r.stop]));
+            const bool own = r.kstart >= 0 && r.kstop >= 0;  // the kernels' own start and end
+            LAYA_HIP(hipEventElapsedTime(&ms, ctx->event_pool[own ? r.kstart : r.start],
+                                         ctx->event_pool[own ? r.kstop : r.stop]));
             auto it = std::find_if(g_summary.begin(), g_summary.end(),
                                    [&](const KernelSummary& k) { return k.name == r.name; });
             if (it == g_summary.end()) {

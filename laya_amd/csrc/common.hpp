@@ -1,6 +1,7 @@
 // Shared definitions of liblaya_hip: status handling, the context, and device helpers.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -68,7 +69,8 @@ struct Workspace {
 // (flops for matrix-core kernels, compulsory HBM bytes for memory-bound ones).
 struct LaunchRecord {
     const char* name;
-    int start, stop;  // indices into the context's event pool
+    int start, stop;    // indices into the context's event pool: the scope's markers
+    int kstart, kstop;  // the first and last kernel's own events (-1: time the scope by its markers)
     double flops, bytes;
 };
 
@@ -223,12 +225,31 @@ inline unsigned blocks_for(size_t n, unsigned per_block, unsigned cap = 65535u *
 struct ProfileScope {
     laya_ctx* ctx;
     int start = -1;
+    int kstart = -1, kstop = -1;  // events carried by the scope's own kernel dispatches (LAYA_LAUNCH)
+    bool nested = false;          // a scope inside this one launched kernels: time by the markers
     const char* name;
     double flops, bytes;
     ProfileScope* outer;
     ProfileScope(laya_ctx* c, const char* n, double f, double b);
     ~ProfileScope();
 };
+
+// The events the next kernel dispatch carries while a live profile runs (both null otherwise): the innermost
+// open scope's first dispatch records the scope's start, each dispatch its end.
+void profile_kernel_events(hipEvent_t* start, hipEvent_t* stop);
+
+// Every kernel launch goes through LAYA_LAUNCH: while a live profile runs, the innermost open profile scope's
+// dispatches carry its start and stop events in the dispatch itself (hipExtLaunchKernelGGL), so a scope is
+// timed by its kernels alone, without the dispatch gaps separate event packets would add.
+#define LAYA_LAUNCH(kernel, grid, block, shmem, stream, ...)                                               \
+    do {                                                                                                 \
+        hipEvent_t laya_ls_ = nullptr, laya_le_ = nullptr;                                               \
+        ::laya::profile_kernel_events(&laya_ls_, &laya_le_);                                             \
+        if (laya_le_)                                                                                    \
+            hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, laya_ls_, laya_le_, 0, __VA_ARGS__); \
+        else                                                                                             \
+            hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                         \
+    } while (0)
 
 // Renames the innermost open profile scope of this thread: a launcher that picks a kernel variant
 // below the scope's opener (the 256 × 256 tiles) tags the launch with that variant's name.

@@ -424,49 +424,49 @@ void fill(laya_ctx* ctx, float* dst, float v, size_t n) {
     if (!n) return;
     ProfileScope scope(ctx, "fill", 0.0, 4.0 * n);
     if (n % 4 == 0 && vec4(dst)) {
-        hipLaunchKernelGGL(fill4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(fill4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<f32x4*>(dst), v, n / 4);
         check_launch("fill4_kernel");
         return;
     }
-    hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, v, n);
+    LAYA_LAUNCH(fill_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, v, n);
     check_launch("fill_kernel");
 }
 void add(laya_ctx* ctx, float* dst, const float* src, size_t n) {
     if (!n) return;
     ProfileScope scope(ctx, "add", 0.0, 12.0 * n);
     if (n % 4 == 0 && vec4(dst) && vec4(src)) {
-        hipLaunchKernelGGL(add4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(add4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<f32x4*>(dst), reinterpret_cast<const f32x4*>(src), n / 4);
         check_launch("add4_kernel");
         return;
     }
-    hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, src, n);
+    LAYA_LAUNCH(add_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, src, n);
     check_launch("add_kernel");
 }
 void scale(laya_ctx* ctx, float* dst, float s, size_t n) {
     if (!n) return;
-    hipLaunchKernelGGL(scale_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, s, n);
+    LAYA_LAUNCH(scale_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, s, n);
     check_launch("scale_kernel");
 }
 void gelu_fwd(laya_ctx* ctx, const float* x, size_t n, float* y) {
     if (!n) return;
-    hipLaunchKernelGGL(gelu_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, x, n, y);
+    LAYA_LAUNCH(gelu_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, x, n, y);
     check_launch("gelu_fwd_kernel");
 }
 void gelu_bwd(laya_ctx* ctx, const float* u, float* g, size_t n) {
     if (!n) return;
-    hipLaunchKernelGGL(gelu_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, u, g, n);
+    LAYA_LAUNCH(gelu_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, u, g, n);
     check_launch("gelu_bwd_kernel");
 }
 void geglu_fwd(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, __bf16* act16, unsigned* amax) {
     if (rows <= 0 || inter <= 0) return;
     ProfileScope scope(ctx, "geglu_fwd", 0.0, (12.0 + (act16 ? 2.0 : 0.0)) * rows * (double)inter);
     if (inter % 4 == 0) {
-        hipLaunchKernelGGL(geglu_fwd_kernel, dim3(grid_for((size_t)rows * inter / 4)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(geglu_fwd_kernel, dim3(grid_for((size_t)rows * inter / 4)), dim3(256), 0, ctx->stream,
                            wide, rows, inter, act, act16, amax);
     } else {
-        hipLaunchKernelGGL(geglu_fwd_scalar_kernel, dim3(grid_for((size_t)rows * inter)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(geglu_fwd_scalar_kernel, dim3(grid_for((size_t)rows * inter)), dim3(256), 0, ctx->stream,
                            wide, rows, inter, act);
         if (act16) to_bf16(ctx, act, (size_t)rows * inter, act16);
         if (amax) absmax_into(ctx, act, rows, inter, inter, amax);
@@ -478,24 +478,24 @@ void to_bf16(laya_ctx* ctx, const float* src, size_t n, __bf16* dst) {
     if (!n) return;
     ProfileScope scope(ctx, "to_bf16", 0.0, 6.0 * n);
     if (n % 4 == 0 && vec4(src) && ((uintptr_t)dst & 7u) == 0) {
-        hipLaunchKernelGGL(to_bf16_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(to_bf16_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<const f32x4*>(src), reinterpret_cast<bf16x4*>(dst), n / 4);
         check_launch("to_bf16_kernel");
         return;
     }
-    hipLaunchKernelGGL(to_bf16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, src, dst, n);
+    LAYA_LAUNCH(to_bf16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, src, dst, n);
     check_launch("to_bf16_scalar_kernel");
 }
 void round_bf16(laya_ctx* ctx, const float* src, size_t n, float* dst) {
     if (!n) return;
     ProfileScope scope(ctx, "round_bf16", 0.0, 8.0 * n);
     if (n % 4 == 0 && vec4(src) && vec4(dst)) {
-        hipLaunchKernelGGL(round_bf16_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(round_bf16_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<const f32x4*>(src), reinterpret_cast<f32x4*>(dst), n / 4);
         check_launch("round_bf16_kernel");
         return;
     }
-    hipLaunchKernelGGL(round_bf16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, src, dst, n);
+    LAYA_LAUNCH(round_bf16_scalar_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, src, dst, n);
     check_launch("round_bf16_scalar_kernel");
 }
 void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide,
@@ -503,10 +503,10 @@ void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, in
     if (rows <= 0 || inter <= 0) return;
     ProfileScope scope(ctx, "geglu_bwd", 0.0, 20.0 * rows * (double)inter);
     if (inter % 4 == 0) {
-        hipLaunchKernelGGL(geglu_bwd_kernel, dim3(grid_for((size_t)rows * inter / 4)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(geglu_bwd_kernel, dim3(grid_for((size_t)rows * inter / 4)), dim3(256), 0, ctx->stream,
                            wide, dact, rows, inter, dwide, amax);
     } else {
-        hipLaunchKernelGGL(geglu_bwd_scalar_kernel, dim3(grid_for((size_t)rows * inter)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(geglu_bwd_scalar_kernel, dim3(grid_for((size_t)rows * inter)), dim3(256), 0, ctx->stream,
                            wide, dact, rows, inter, dwide);
         if (amax) absmax_into(ctx, dwide, rows, 2 * inter, 2 * inter, amax);
     }
@@ -516,12 +516,12 @@ void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed) {
     if (!n || p <= 0.0f) return;
     ProfileScope scope(ctx, "dropout", 0.0, 8.0 * n);
     if (n % 4 == 0 && vec4(v)) {
-        hipLaunchKernelGGL(dropout4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(dropout4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<f32x4*>(v), n / 4, p, 1.0f / (1.0f - p), seed);
         check_launch("dropout4_kernel");
         return;
     }
-    hipLaunchKernelGGL(dropout_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, v, n, p, 1.0f / (1.0f - p),
+    LAYA_LAUNCH(dropout_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, v, n, p, 1.0f / (1.0f - p),
                        seed);
     check_launch("dropout_kernel");
 }
@@ -533,7 +533,7 @@ void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p
         return;
     }
     ProfileScope scope(ctx, "dropout", 0.0, 8.0 * n);
-    hipLaunchKernelGGL(dropout_copy4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+    LAYA_LAUNCH(dropout_copy4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                        reinterpret_cast<const f32x4*>(src), reinterpret_cast<f32x4*>(dst), n / 4, p,
                        1.0f / (1.0f - p), seed);
     check_launch("dropout_copy4_kernel");
@@ -544,13 +544,13 @@ void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint6
     const float keep = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
     ProfileScope scope(ctx, "relu_dropout_fwd", 0.0, (8.0 + (dropped16 ? 2.0 : 0.0)) * n);
     if (n % 4 == 0 && vec4(wide) && vec4(dropped) && ((uintptr_t)dropped16 & 7u) == 0) {
-        hipLaunchKernelGGL(relu_dropout_fwd4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(relu_dropout_fwd4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<const f32x4*>(wide), n / 4, p, keep, seed,
                            reinterpret_cast<f32x4*>(dropped), reinterpret_cast<bf16x4*>(dropped16));
         check_launch("relu_dropout_fwd4_kernel");
         return;
     }
-    hipLaunchKernelGGL(relu_dropout_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, wide, n, p, keep, seed,
+    LAYA_LAUNCH(relu_dropout_fwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, wide, n, p, keep, seed,
                        dropped);
     check_launch("relu_dropout_fwd_kernel");
     if (dropped16) to_bf16(ctx, dropped, n, dropped16);
@@ -559,7 +559,7 @@ void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, floa
     if (!n) return;
     const float keep = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
     ProfileScope scope(ctx, "relu_dropout_bwd", 0.0, 12.0 * n);
-    hipLaunchKernelGGL(relu_dropout_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, wide, g, n, p, keep,
+    LAYA_LAUNCH(relu_dropout_bwd_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, wide, g, n, p, keep,
                        seed);
     check_launch("relu_dropout_bwd_kernel");
 }
@@ -568,7 +568,7 @@ void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g,
     LAYA_REQUIRE(n % 4 == 0 && vec4(dropped) && vec4(g), "relu_dropout_bwd: 16-byte aligned multiples of 4");
     const float keep = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
     ProfileScope scope(ctx, "relu_dropout_bwd", 0.0, 12.0 * n);
-    hipLaunchKernelGGL(relu_dropout_bwd_out4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+    LAYA_LAUNCH(relu_dropout_bwd_out4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                        reinterpret_cast<const f32x4*>(dropped), reinterpret_cast<f32x4*>(g), n / 4, keep);
     check_launch("relu_dropout_bwd_out4_kernel");
 }
@@ -585,10 +585,10 @@ void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_
     f32x4* part = static_cast<f32x4*>(ctx->workspace(slot, sizeof(f32x4) * (size_t)chunks * types * n4));
     ProfileScope scope(ctx, "column_sums", 0.0, 4.0 * (double)rows * n);
     if (types == 1)
-        hipLaunchKernelGGL(colsum_partial4_kernel<1>, dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(colsum_partial4_kernel<1>, dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
                            reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, nullptr, part);
     else
-        hipLaunchKernelGGL(colsum_partial4_kernel<3>, dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(colsum_partial4_kernel<3>, dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
                            reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, row_type, part);
     check_launch("colsum_partial4_kernel");
     column_reduce(ctx, reinterpret_cast<const float*>(part), chunks, types * n, out);
@@ -597,7 +597,7 @@ void column_reduce(laya_ctx* ctx, const float* part, int count, int n, float* ou
     LAYA_REQUIRE(n % 4 == 0 && vec4(part) && vec4(out), "column_reduce: 16-byte aligned rows of a multiple of 4");
     if (count <= 0 || n <= 0) return;
     const int w4 = n / 4;
-    hipLaunchKernelGGL(colsum_reduce4_kernel, dim3((w4 + 15) / 16), dim3(256), 0, ctx->stream,
+    LAYA_LAUNCH(colsum_reduce4_kernel, dim3((w4 + 15) / 16), dim3(256), 0, ctx->stream,
                        reinterpret_cast<const f32x4*>(part), count, w4, reinterpret_cast<f32x4*>(out));
     check_launch("colsum_reduce4_kernel");
 }
@@ -613,21 +613,21 @@ void column_reduce_batch(laya_ctx* ctx, const ColumnSumJobs& jobs) {
     double bytes = 0;
     for (int i = 0; i < jobs.n; ++i) bytes += 4.0 * jobs.job[i].n * (jobs.job[i].count + 2);
     ProfileScope scope(ctx, "column_sums_deferred", 0.0, bytes);
-    hipLaunchKernelGGL(colsum_reduce4_multi_kernel, dim3((max_w4 + 15) / 16, jobs.n), dim3(256), 0, ctx->stream, jobs);
+    LAYA_LAUNCH(colsum_reduce4_multi_kernel, dim3((max_w4 + 15) / 16, jobs.n), dim3(256), 0, ctx->stream, jobs);
     check_launch("colsum_reduce4_multi_kernel");
 }
 void rotary_apply(laya_ctx* ctx, const float* cos_t, const float* sin_t, int head_dim, float* vec, int rows,
                   const int* pos, int inverse) {
     if (rows <= 0) return;
     const int half = head_dim / 2;
-    hipLaunchKernelGGL(rotary_kernel, dim3(grid_for((size_t)rows * half)), dim3(256), 0, ctx->stream, cos_t, sin_t,
+    LAYA_LAUNCH(rotary_kernel, dim3(grid_for((size_t)rows * half)), dim3(256), 0, ctx->stream, cos_t, sin_t,
                        half, vec, rows, pos, inverse);
     check_launch("rotary_kernel");
 }
 void embedding_fwd(laya_ctx* ctx, const int* ids, int n, const float* E, int vocab, int hidden, float* out,
                    int* bad) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(embedding_fwd_kernel, dim3(grid_for((size_t)n * hidden)), dim3(256), 0, ctx->stream, ids, n,
+    LAYA_LAUNCH(embedding_fwd_kernel, dim3(grid_for((size_t)n * hidden)), dim3(256), 0, ctx->stream, ids, n,
                        E, vocab, hidden, out, bad);
     check_launch("embedding_fwd_kernel");
 }
@@ -637,25 +637,25 @@ void embedding_bwd(laya_ctx* ctx, const int* sorted_pos, const int* unique_ids, 
     ProfileScope scope(ctx, "embedding_bwd", 0.0, 0.0);
     if (hidden % 4 == 0 && vec4(d) && vec4(grad)) {
         const int h4 = hidden / 4;
-        hipLaunchKernelGGL(embedding_bwd4_kernel, dim3(n_unique), dim3(std::min(256, (h4 + 63) / 64 * 64)), 0,
+        LAYA_LAUNCH(embedding_bwd4_kernel, dim3(n_unique), dim3(std::min(256, (h4 + 63) / 64 * 64)), 0,
                            ctx->stream, sorted_pos, unique_ids, offsets, reinterpret_cast<const f32x4*>(d), h4,
                            reinterpret_cast<f32x4*>(grad));
         check_launch("embedding_bwd4_kernel");
         return;
     }
-    hipLaunchKernelGGL(embedding_bwd_kernel, dim3(n_unique), dim3(256), 0, ctx->stream, sorted_pos, unique_ids,
+    LAYA_LAUNCH(embedding_bwd_kernel, dim3(n_unique), dim3(256), 0, ctx->stream, sorted_pos, unique_ids,
                        offsets, d, hidden, grad);
     check_launch("embedding_bwd_kernel");
 }
 void gather_rows(laya_ctx* ctx, const float* src, const int* rows, int n, int width, float* dst) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(gather_rows_kernel, dim3(grid_for((size_t)n * width)), dim3(256), 0, ctx->stream, src, rows, n,
+    LAYA_LAUNCH(gather_rows_kernel, dim3(grid_for((size_t)n * width)), dim3(256), 0, ctx->stream, src, rows, n,
                        width, dst);
     check_launch("gather_rows_kernel");
 }
 void scatter_add_rows(laya_ctx* ctx, const float* src, const int* rows, int n, int width, float* dst) {
     if (n <= 0) return;
-    hipLaunchKernelGGL(scatter_add_rows_kernel, dim3((width + 255) / 256), dim3(256), 0, ctx->stream, src, rows, n,
+    LAYA_LAUNCH(scatter_add_rows_kernel, dim3((width + 255) / 256), dim3(256), 0, ctx->stream, src, rows, n,
                        width, dst);
     check_launch("scatter_add_rows_kernel");
 }
@@ -663,7 +663,7 @@ void add_indexed_rows(laya_ctx* ctx, float* dst, const int* idx, int rows, int w
     if (rows <= 0 || width <= 0) return;
     LAYA_REQUIRE(width % 4 == 0 && vec4(dst) && vec4(table), "add_indexed_rows: 16-byte aligned rows of a multiple of 4");
     ProfileScope scope(ctx, "add_indexed_rows", 0.0, 8.0 * rows * (double)width);
-    hipLaunchKernelGGL(add_indexed_rows4_kernel, dim3(grid_for((size_t)rows * width / 4)), dim3(256), 0, ctx->stream,
+    LAYA_LAUNCH(add_indexed_rows4_kernel, dim3(grid_for((size_t)rows * width / 4)), dim3(256), 0, ctx->stream,
                        reinterpret_cast<f32x4*>(dst), idx, rows, width / 4, reinterpret_cast<const f32x4*>(table));
     check_launch("add_indexed_rows4_kernel");
 }
@@ -679,13 +679,13 @@ void softmax_ce_bwd(laya_ctx* ctx, const float* logits, const float* targets, co
                     float ce_weight, float s, float* grad, float* loss) {
     if (n_items <= 0) return;
     double* terms = static_cast<double*>(ctx->workspace(1, sizeof(double) * (size_t)n_items));
-    hipLaunchKernelGGL(softmax_ce_kernel, dim3(1), dim3(CE_THREADS), 0, ctx->stream, logits, targets, offsets, n_items,
+    LAYA_LAUNCH(softmax_ce_kernel, dim3(1), dim3(CE_THREADS), 0, ctx->stream, logits, targets, offsets, n_items,
                        ce_weight, s, grad, loss, terms);
     check_launch("softmax_ce_kernel");
 }
 void init_param(laya_ctx* ctx, float* dst, size_t n, int kind, float std, uint64_t seed) {
     if (!n) return;
-    hipLaunchKernelGGL(init_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, n, kind, std, seed);
+    LAYA_LAUNCH(init_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, dst, n, kind, std, seed);
     check_launch("init_kernel");
 }
 

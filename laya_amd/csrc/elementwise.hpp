@@ -59,8 +59,20 @@ struct AdamGroups {
 };
 // Elements outside every group are left alone (frozen parameters); zero_grads clears all n gradients;
 // mirror (optional, n bf16) receives bf16(p) of every updated element.
+// The weights whose magnitude words the AdamW kernel folds the updated values into, so the next forward need
+// not measure them: tensor t spans float4s [begin[t], end[t]) of the arena (sorted, disjoint) and folds into
+// the word group at words + word[t]·AMAX_GROUP (cleared beforehand). block[b] says which tensor covers
+// workgroup b's 256 float4s whole (-1: none, -2: several or part of one: each lane looks its tensor up).
+struct AdamFold {
+    const int* block = nullptr;
+    const long* begin = nullptr;
+    const long* end = nullptr;
+    const int* word = nullptr;
+    int n = 0;
+    unsigned* words = nullptr;
+};
 void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n, const AdamGroups& groups,
                  float beta1, float beta2, float eps, float sqrt_c2, const float* coef, int zero_grads,
-                 __bf16* mirror = nullptr);
+                 __bf16* mirror = nullptr, const AdamFold* fold = nullptr);
 
 }  // namespace laya

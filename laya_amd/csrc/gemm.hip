@@ -2226,14 +2226,14 @@ template <int AOP, int BOP> void launch_h(laya_ctx* ctx, const GemmParams& p, in
     switch (p.mode) {
         case STORE:
             if (p.R)
-                hipLaunchKernelGGL((gemm_bf16_kernel<AOP, BOP, STORE, true>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_bf16_kernel<AOP, BOP, STORE, true>), g, b, 0, ctx->stream, p);
             else
-                hipLaunchKernelGGL((gemm_bf16_kernel<AOP, BOP, STORE, false>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_bf16_kernel<AOP, BOP, STORE, false>), g, b, 0, ctx->stream, p);
             break;
         case ACCUMULATE:
-            hipLaunchKernelGGL((gemm_bf16_kernel<AOP, BOP, ACCUMULATE, false>), g, b, 0, ctx->stream, p);
+            LAYA_LAUNCH((gemm_bf16_kernel<AOP, BOP, ACCUMULATE, false>), g, b, 0, ctx->stream, p);
             break;
-        default: hipLaunchKernelGGL((gemm_bf16_kernel<AOP, BOP, PARTIAL, false>), g, b, 0, ctx->stream, p);
+        default: LAYA_LAUNCH((gemm_bf16_kernel<AOP, BOP, PARTIAL, false>), g, b, 0, ctx->stream, p);
     }
     check_launch("gemm_bf16_kernel");
 }
@@ -2325,7 +2325,7 @@ void absmax_multi(laya_ctx* ctx, const float* arena, const long* off, const int*
                   unsigned* words, double bytes) {
     if (blocks <= 0) return;
     ProfileScope scope(ctx, "absmax", 0.0, bytes);
-    hipLaunchKernelGGL(absmax_multi_kernel, dim3(blocks), dim3(256), 0, ctx->stream, arena, off, len, word, words);
+    LAYA_LAUNCH(absmax_multi_kernel, dim3(blocks), dim3(256), 0, ctx->stream, arena, off, len, word, words);
     check_launch("absmax_multi_kernel");
 }
 
@@ -2337,7 +2337,7 @@ void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, uns
     const int vec = cols % 4 == 0 && ld % 4 == 0 && aligned16(x);
     const long per_block = 256L * 4 * 8;  // eight float4 per thread
     const int blocks = (int)std::max(1L, std::min<long>(AMAX_BLOCKS, (n + per_block - 1) / per_block));
-    hipLaunchKernelGGL(absmax_kernel, dim3(vec && ld == cols ? blocks : std::min(blocks, std::max(rows, 1))),
+    LAYA_LAUNCH(absmax_kernel, dim3(vec && ld == cols ? blocks : std::min(blocks, std::max(rows, 1))),
                        dim3(256), 0, ctx->stream, x, rows, cols, ld, vec, out);
     check_launch("absmax_kernel");
 }
@@ -2385,21 +2385,21 @@ void launch_tall(laya_ctx* ctx, GemmParams p) {
     if (p.amax_a) {
         profile_rename("gemm_nt_h2t");
         if (p.mode == STORE_ROPE)
-            hipLaunchKernelGGL((gemm_x6t_kernel<STORE_ROPE, false, 2>), g, b, 0, ctx->stream, p);
+            LAYA_LAUNCH((gemm_x6t_kernel<STORE_ROPE, false, 2>), g, b, 0, ctx->stream, p);
         else if (p.R)
-            hipLaunchKernelGGL((gemm_x6t_kernel<STORE, true, 2>), g, b, 0, ctx->stream, p);
+            LAYA_LAUNCH((gemm_x6t_kernel<STORE, true, 2>), g, b, 0, ctx->stream, p);
         else
-            hipLaunchKernelGGL((gemm_x6t_kernel<STORE, false, 2>), g, b, 0, ctx->stream, p);
+            LAYA_LAUNCH((gemm_x6t_kernel<STORE, false, 2>), g, b, 0, ctx->stream, p);
         check_launch("gemm_x6t_kernel");
         return;
     }
     profile_rename("gemm_nt_x6t");
     if (p.mode == STORE_ROPE)
-        hipLaunchKernelGGL((gemm_x6t_kernel<STORE_ROPE, false>), g, b, 0, ctx->stream, p);
+        LAYA_LAUNCH((gemm_x6t_kernel<STORE_ROPE, false>), g, b, 0, ctx->stream, p);
     else if (p.R)
-        hipLaunchKernelGGL((gemm_x6t_kernel<STORE, true>), g, b, 0, ctx->stream, p);
+        LAYA_LAUNCH((gemm_x6t_kernel<STORE, true>), g, b, 0, ctx->stream, p);
     else
-        hipLaunchKernelGGL((gemm_x6t_kernel<STORE, false>), g, b, 0, ctx->stream, p);
+        LAYA_LAUNCH((gemm_x6t_kernel<STORE, false>), g, b, 0, ctx->stream, p);
     check_launch("gemm_x6t_kernel");
 }
 
@@ -2409,9 +2409,9 @@ void launch_wide(laya_ctx* ctx, GemmParams p) {
     if (p.amax_a) {
         profile_rename("gemm_nt_h2w");
         if (p.mode == STORE_ROPE)
-            hipLaunchKernelGGL((gemm_x6w_kernel<STORE_ROPE, 2>), g, b, 0, ctx->stream, p);
+            LAYA_LAUNCH((gemm_x6w_kernel<STORE_ROPE, 2>), g, b, 0, ctx->stream, p);
         else
-            hipLaunchKernelGGL((gemm_x6w_kernel<STORE, 2>), g, b, 0, ctx->stream, p);
+            LAYA_LAUNCH((gemm_x6w_kernel<STORE, 2>), g, b, 0, ctx->stream, p);
         check_launch("gemm_x6w_kernel");
         // With a bias the RoPE epilogue does not fold C's magnitude (or a bound on it) in: measure it here.
         if (p.mode == STORE_ROPE && p.amax_c && p.bias) absmax_into(ctx, p.C, p.M, p.N, p.ldc, p.amax_c);
@@ -2419,9 +2419,9 @@ void launch_wide(laya_ctx* ctx, GemmParams p) {
     }
     profile_rename("gemm_nt_x6w");
     if (p.mode == STORE_ROPE)
-        hipLaunchKernelGGL((gemm_x6w_kernel<STORE_ROPE>), g, b, 0, ctx->stream, p);
+        LAYA_LAUNCH((gemm_x6w_kernel<STORE_ROPE>), g, b, 0, ctx->stream, p);
     else
-        hipLaunchKernelGGL((gemm_x6w_kernel<STORE>), g, b, 0, ctx->stream, p);
+        LAYA_LAUNCH((gemm_x6w_kernel<STORE>), g, b, 0, ctx->stream, p);
     check_launch("gemm_x6w_kernel");
 }
 
@@ -2433,13 +2433,13 @@ void launch_wide_h(laya_ctx* ctx, GemmParams p) {
     const bool ah = p.A16 != nullptr, bh = p.B16 != nullptr;
 #define WIDE_H(MODE)                                                                                         \
     if (ah && bh)                                                                                            \
-        hipLaunchKernelGGL((gemm_x6w_kernel<MODE, 1, true, true>), g, b, 0, ctx->stream, p);                 \
+        LAYA_LAUNCH((gemm_x6w_kernel<MODE, 1, true, true>), g, b, 0, ctx->stream, p);                 \
     else if (ah)                                                                                             \
-        hipLaunchKernelGGL((gemm_x6w_kernel<MODE, 1, true, false>), g, b, 0, ctx->stream, p);                \
+        LAYA_LAUNCH((gemm_x6w_kernel<MODE, 1, true, false>), g, b, 0, ctx->stream, p);                \
     else if (bh)                                                                                             \
-        hipLaunchKernelGGL((gemm_x6w_kernel<MODE, 1, false, true>), g, b, 0, ctx->stream, p);                \
+        LAYA_LAUNCH((gemm_x6w_kernel<MODE, 1, false, true>), g, b, 0, ctx->stream, p);                \
     else                                                                                                     \
-        hipLaunchKernelGGL((gemm_x6w_kernel<MODE, 1, false, false>), g, b, 0, ctx->stream, p);
+        LAYA_LAUNCH((gemm_x6w_kernel<MODE, 1, false, false>), g, b, 0, ctx->stream, p);
     if (p.mode == STORE_ROPE) {
         WIDE_H(STORE_ROPE)
     } else {
@@ -2457,14 +2457,14 @@ template <int AOP, int BOP> void launch_x(laya_ctx* ctx, const GemmParams& p, in
             switch (p.mode) {
                 case STORE:
                     if (p.R)
-                        hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE, true, 2>), g, b, 0, ctx->stream, p);
+                        LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE, true, 2>), g, b, 0, ctx->stream, p);
                     else
-                        hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE, false, 2>), g, b, 0, ctx->stream, p);
+                        LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE, false, 2>), g, b, 0, ctx->stream, p);
                     break;
                 case ACCUMULATE:
-                    hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, ACCUMULATE, false, 2>), g, b, 0, ctx->stream, p);
+                    LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, ACCUMULATE, false, 2>), g, b, 0, ctx->stream, p);
                     break;
-                default: hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, PARTIAL, false, 2>), g, b, 0, ctx->stream, p);
+                default: LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, PARTIAL, false, 2>), g, b, 0, ctx->stream, p);
             }
             check_launch("gemm_x6_kernel");
             return;
@@ -2473,14 +2473,14 @@ template <int AOP, int BOP> void launch_x(laya_ctx* ctx, const GemmParams& p, in
     switch (p.mode) {
         case STORE:
             if (p.R)
-                hipLaunchKernelGGL((gemm_x6_kernel<AOP, BOP, STORE, true>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_x6_kernel<AOP, BOP, STORE, true>), g, b, 0, ctx->stream, p);
             else
-                hipLaunchKernelGGL((gemm_x6_kernel<AOP, BOP, STORE, false>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_x6_kernel<AOP, BOP, STORE, false>), g, b, 0, ctx->stream, p);
             break;
         case ACCUMULATE:
-            hipLaunchKernelGGL((gemm_x6_kernel<AOP, BOP, ACCUMULATE, false>), g, b, 0, ctx->stream, p);
+            LAYA_LAUNCH((gemm_x6_kernel<AOP, BOP, ACCUMULATE, false>), g, b, 0, ctx->stream, p);
             break;
-        default: hipLaunchKernelGGL((gemm_x6_kernel<AOP, BOP, PARTIAL, false>), g, b, 0, ctx->stream, p);
+        default: LAYA_LAUNCH((gemm_x6_kernel<AOP, BOP, PARTIAL, false>), g, b, 0, ctx->stream, p);
     }
     check_launch("gemm_x6_kernel");
 }
@@ -2499,13 +2499,13 @@ template <bool AK, bool BKC> void launch_x6(laya_ctx* ctx, const GemmParams& p, 
             if (p.amax_a) {
                 profile_rename("gemm_nt_h2q");
                 if (p.R)
-                    hipLaunchKernelGGL((gemm_x6q_kernel<STORE, true, 2>), g, b, 0, ctx->stream, p);
+                    LAYA_LAUNCH((gemm_x6q_kernel<STORE, true, 2>), g, b, 0, ctx->stream, p);
                 else
-                    hipLaunchKernelGGL((gemm_x6q_kernel<STORE, false, 2>), g, b, 0, ctx->stream, p);
+                    LAYA_LAUNCH((gemm_x6q_kernel<STORE, false, 2>), g, b, 0, ctx->stream, p);
             } else if (p.R) {
-                hipLaunchKernelGGL((gemm_x6q_kernel<STORE, true>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_x6q_kernel<STORE, true>), g, b, 0, ctx->stream, p);
             } else {
-                hipLaunchKernelGGL((gemm_x6q_kernel<STORE, false>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_x6q_kernel<STORE, false>), g, b, 0, ctx->stream, p);
             }
             check_launch("gemm_x6q_kernel");
         } else if (va && vb) launch_x<KVEC, KVEC>(ctx, p, blocks);
@@ -2533,11 +2533,11 @@ template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int
     }
     if (!gemm_fast(p, AK, BKC)) {
         switch (p.mode) {
-            case STORE: hipLaunchKernelGGL((gemm_generic_kernel<AK, BKC, STORE>), g, b, 0, ctx->stream, p); break;
+            case STORE: LAYA_LAUNCH((gemm_generic_kernel<AK, BKC, STORE>), g, b, 0, ctx->stream, p); break;
             case ACCUMULATE:
-                hipLaunchKernelGGL((gemm_generic_kernel<AK, BKC, ACCUMULATE>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_generic_kernel<AK, BKC, ACCUMULATE>), g, b, 0, ctx->stream, p);
                 break;
-            default: hipLaunchKernelGGL((gemm_generic_kernel<AK, BKC, PARTIAL>), g, b, 0, ctx->stream, p);
+            default: LAYA_LAUNCH((gemm_generic_kernel<AK, BKC, PARTIAL>), g, b, 0, ctx->stream, p);
         }
         check_launch("gemm_generic_kernel");
         return;
@@ -2546,18 +2546,18 @@ template <bool AK, bool BKC> void launch(laya_ctx* ctx, const GemmParams& p, int
         case STORE:
             if (AK && BKC && three_per_cu(ctx, blocks)) {
                 if (p.R)
-                    hipLaunchKernelGGL((gemm3_kernel<AK, BKC, STORE, true>), g, b, 0, ctx->stream, p);
+                    LAYA_LAUNCH((gemm3_kernel<AK, BKC, STORE, true>), g, b, 0, ctx->stream, p);
                 else
-                    hipLaunchKernelGGL((gemm3_kernel<AK, BKC, STORE, false>), g, b, 0, ctx->stream, p);
+                    LAYA_LAUNCH((gemm3_kernel<AK, BKC, STORE, false>), g, b, 0, ctx->stream, p);
                 break;
             }
             if (p.R)
-                hipLaunchKernelGGL((gemm_kernel<AK, BKC, STORE, true>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_kernel<AK, BKC, STORE, true>), g, b, 0, ctx->stream, p);
             else
-                hipLaunchKernelGGL((gemm_kernel<AK, BKC, STORE, false>), g, b, 0, ctx->stream, p);
+                LAYA_LAUNCH((gemm_kernel<AK, BKC, STORE, false>), g, b, 0, ctx->stream, p);
             break;
-        case ACCUMULATE: hipLaunchKernelGGL((gemm_kernel<AK, BKC, ACCUMULATE, false>), g, b, 0, ctx->stream, p); break;
-        default: hipLaunchKernelGGL((gemm_kernel<AK, BKC, PARTIAL, false>), g, b, 0, ctx->stream, p);
+        case ACCUMULATE: LAYA_LAUNCH((gemm_kernel<AK, BKC, ACCUMULATE, false>), g, b, 0, ctx->stream, p); break;
+        default: LAYA_LAUNCH((gemm_kernel<AK, BKC, PARTIAL, false>), g, b, 0, ctx->stream, p);
     }
     check_launch("gemm_kernel");
 }
@@ -2614,7 +2614,7 @@ void finish_accumulate(laya_ctx* ctx, const GemmParams& p, float* out, long ldc)
     if (p.mode != PARTIAL) return;
     const long total = (long)p.M * p.N;
     ProfileScope scope(ctx, "gemm_splitk_reduce", 0.0, 4.0 * total * (p.splits + 2));
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
+    LAYA_LAUNCH(splitk_reduce_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
                        p.splits, p.M, p.N, out, ldc);
     check_launch("splitk_reduce_kernel");
 }
@@ -2686,7 +2686,7 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
     if (split_store) {
         const long total = (long)M * N;
         ProfileScope scope(ctx, "gemm_splitk_store", 0.0, 4.0 * total * (p.splits + 1 + (R ? 1 : 0)));
-        hipLaunchKernelGGL(splitk_store_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
+        LAYA_LAUNCH(splitk_store_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
                            p.splits, M, N, C, ldc, bias, R, ldr);
         check_launch("splitk_store_kernel");
     } else {
@@ -2716,7 +2716,7 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
                 launch_wide_h(ctx, p);
                 return;
             }
-            hipLaunchKernelGGL((gemm_bf16_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
+            LAYA_LAUNCH((gemm_bf16_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
                                dim3(THREADS), 0, ctx->stream, p);
             check_launch("gemm_bf16_kernel");
             return;
@@ -2735,13 +2735,13 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
                 launch_tall(ctx, p);
                 return;
             }
-            hipLaunchKernelGGL((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
+            LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
                                dim3(THREADS), 0, ctx->stream, p);
             check_launch("gemm_x6_kernel");
             return;
         }
         ProfileScope scope(ctx, "gemm_nt", 2.0 * M * N * (double)K, 0.0);
-        hipLaunchKernelGGL((gemm_kernel<true, true, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n), dim3(THREADS), 0,
+        LAYA_LAUNCH((gemm_kernel<true, true, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n), dim3(THREADS), 0,
                            ctx->stream, p);
         check_launch("gemm_kernel");
     }();
@@ -2818,21 +2818,21 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
                            2.0 * 2.0 * rows * (double)in * out, 0.0);
         const dim3 g(s.G), b(WT_THREADS);
         if (pair && nn.R)
-            hipLaunchKernelGGL((gemm_pair_wide_kernel<2, true>), g, b, 0, ctx->stream, nn, tn, s);
+            LAYA_LAUNCH((gemm_pair_wide_kernel<2, true>), g, b, 0, ctx->stream, nn, tn, s);
         else if (pair)
-            hipLaunchKernelGGL((gemm_pair_wide_kernel<2, false>), g, b, 0, ctx->stream, nn, tn, s);
+            LAYA_LAUNCH((gemm_pair_wide_kernel<2, false>), g, b, 0, ctx->stream, nn, tn, s);
         else if (bh && nn.R)
-            hipLaunchKernelGGL((gemm_pair_wide_kernel<1, true, true>), g, b, 0, ctx->stream, nn, tn, s);
+            LAYA_LAUNCH((gemm_pair_wide_kernel<1, true, true>), g, b, 0, ctx->stream, nn, tn, s);
         else if (bh)
-            hipLaunchKernelGGL((gemm_pair_wide_kernel<1, false, true>), g, b, 0, ctx->stream, nn, tn, s);
+            LAYA_LAUNCH((gemm_pair_wide_kernel<1, false, true>), g, b, 0, ctx->stream, nn, tn, s);
         else if (half && nn.R)
-            hipLaunchKernelGGL((gemm_pair_wide_kernel<1, true>), g, b, 0, ctx->stream, nn, tn, s);
+            LAYA_LAUNCH((gemm_pair_wide_kernel<1, true>), g, b, 0, ctx->stream, nn, tn, s);
         else if (half)
-            hipLaunchKernelGGL((gemm_pair_wide_kernel<1, false>), g, b, 0, ctx->stream, nn, tn, s);
+            LAYA_LAUNCH((gemm_pair_wide_kernel<1, false>), g, b, 0, ctx->stream, nn, tn, s);
         else if (nn.R)
-            hipLaunchKernelGGL((gemm_pair_wide_kernel<3, true>), g, b, 0, ctx->stream, nn, tn, s);
+            LAYA_LAUNCH((gemm_pair_wide_kernel<3, true>), g, b, 0, ctx->stream, nn, tn, s);
         else
-            hipLaunchKernelGGL((gemm_pair_wide_kernel<3, false>), g, b, 0, ctx->stream, nn, tn, s);
+            LAYA_LAUNCH((gemm_pair_wide_kernel<3, false>), g, b, 0, ctx->stream, nn, tn, s);
         check_launch("gemm_pair_wide_kernel");
     }
     long partials = 0, shared = 0;
@@ -2849,7 +2849,7 @@ bool backward_pair_wide(laya_ctx* ctx, GemmParams nn, GemmParams tn, int rows, i
         }
     }
     ProfileScope scope(ctx, "gemm_pair_fixup", 0.0, 4.0 * WT * WT * (double)(partials + 2 * shared));
-    hipLaunchKernelGGL(pair_fixup_w_kernel, dim3(n1, 32), dim3(WT_THREADS), 0, ctx->stream, tn, s);
+    LAYA_LAUNCH(pair_fixup_w_kernel, dim3(n1, 32), dim3(WT_THREADS), 0, ctx->stream, tn, s);
     check_launch("pair_fixup_w_kernel");
     return true;
 }
@@ -2898,34 +2898,34 @@ void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const flo
             if (half) {
                 const bool va = operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K);
                 if (va && dx_residual)
-                    hipLaunchKernelGGL((gemm_pair_planned_h_kernel<KVEC, true>), g, b, 0, ctx->stream, nn, tn, s);
+                    LAYA_LAUNCH((gemm_pair_planned_h_kernel<KVEC, true>), g, b, 0, ctx->stream, nn, tn, s);
                 else if (va)
-                    hipLaunchKernelGGL((gemm_pair_planned_h_kernel<KVEC, false>), g, b, 0, ctx->stream, nn, tn, s);
+                    LAYA_LAUNCH((gemm_pair_planned_h_kernel<KVEC, false>), g, b, 0, ctx->stream, nn, tn, s);
                 else if (dx_residual)
-                    hipLaunchKernelGGL((gemm_pair_planned_h_kernel<KSCALAR, true>), g, b, 0, ctx->stream, nn, tn, s);
+                    LAYA_LAUNCH((gemm_pair_planned_h_kernel<KSCALAR, true>), g, b, 0, ctx->stream, nn, tn, s);
                 else
-                    hipLaunchKernelGGL((gemm_pair_planned_h_kernel<KSCALAR, false>), g, b, 0, ctx->stream, nn, tn, s);
+                    LAYA_LAUNCH((gemm_pair_planned_h_kernel<KSCALAR, false>), g, b, 0, ctx->stream, nn, tn, s);
                 check_launch("gemm_pair_planned_h_kernel");
             } else if (split) {
                 if (operand_fast(nn.A, nn.lda, nn.vec_a, true, nn.M, nn.K)) {
                     if (dx_residual)
-                        hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KVEC, true>), g, b, 0, ctx->stream, nn, tn, s);
+                        LAYA_LAUNCH((gemm_pair_planned_x6_kernel<KVEC, true>), g, b, 0, ctx->stream, nn, tn, s);
                     else
-                        hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KVEC, false>), g, b, 0, ctx->stream, nn, tn, s);
+                        LAYA_LAUNCH((gemm_pair_planned_x6_kernel<KVEC, false>), g, b, 0, ctx->stream, nn, tn, s);
                 } else {
                     if (dx_residual)
-                        hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KSCALAR, true>), g, b, 0, ctx->stream, nn, tn,
+                        LAYA_LAUNCH((gemm_pair_planned_x6_kernel<KSCALAR, true>), g, b, 0, ctx->stream, nn, tn,
                                            s);
                     else
-                        hipLaunchKernelGGL((gemm_pair_planned_x6_kernel<KSCALAR, false>), g, b, 0, ctx->stream, nn, tn,
+                        LAYA_LAUNCH((gemm_pair_planned_x6_kernel<KSCALAR, false>), g, b, 0, ctx->stream, nn, tn,
                                            s);
                 }
                 check_launch("gemm_pair_planned_x6_kernel");
             } else {
                 if (dx_residual)
-                    hipLaunchKernelGGL((gemm_pair_planned_kernel<true>), g, b, 0, ctx->stream, nn, tn, s);
+                    LAYA_LAUNCH((gemm_pair_planned_kernel<true>), g, b, 0, ctx->stream, nn, tn, s);
                 else
-                    hipLaunchKernelGGL((gemm_pair_planned_kernel<false>), g, b, 0, ctx->stream, nn, tn, s);
+                    LAYA_LAUNCH((gemm_pair_planned_kernel<false>), g, b, 0, ctx->stream, nn, tn, s);
                 check_launch("gemm_pair_planned_kernel");
             }
         }
@@ -2948,9 +2948,9 @@ void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const flo
         }
         ProfileScope scope(ctx, "gemm_pair_fixup", 0.0, 4.0 * BM * BN * (double)(partials + 2 * shared));
         if (split || half)
-            hipLaunchKernelGGL(pair_fixup_kernel<true>, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
+            LAYA_LAUNCH(pair_fixup_kernel<true>, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
         else
-            hipLaunchKernelGGL(pair_fixup_kernel<false>, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
+            LAYA_LAUNCH(pair_fixup_kernel<false>, dim3(n1, 8), dim3(THREADS), 0, ctx->stream, tn, s);
         check_launch("pair_fixup_kernel");
         return;
     }
@@ -2988,14 +2988,14 @@ void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const flo
         const dim3 g(blocks), b(THREADS);
         if (tn.mode == ACCUMULATE) {
             if (dx_residual)
-                hipLaunchKernelGGL((gemm_pair_kernel<ACCUMULATE, true>), g, b, 0, ctx->stream, nn, tn, n0);
+                LAYA_LAUNCH((gemm_pair_kernel<ACCUMULATE, true>), g, b, 0, ctx->stream, nn, tn, n0);
             else
-                hipLaunchKernelGGL((gemm_pair_kernel<ACCUMULATE, false>), g, b, 0, ctx->stream, nn, tn, n0);
+                LAYA_LAUNCH((gemm_pair_kernel<ACCUMULATE, false>), g, b, 0, ctx->stream, nn, tn, n0);
         } else {
             if (dx_residual)
-                hipLaunchKernelGGL((gemm_pair_kernel<PARTIAL, true>), g, b, 0, ctx->stream, nn, tn, n0);
+                LAYA_LAUNCH((gemm_pair_kernel<PARTIAL, true>), g, b, 0, ctx->stream, nn, tn, n0);
             else
-                hipLaunchKernelGGL((gemm_pair_kernel<PARTIAL, false>), g, b, 0, ctx->stream, nn, tn, n0);
+                LAYA_LAUNCH((gemm_pair_kernel<PARTIAL, false>), g, b, 0, ctx->stream, nn, tn, n0);
         }
         check_launch("gemm_pair_kernel");
     }
@@ -3011,15 +3011,15 @@ void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out) 
     const int rows_per = 256;
     const int chunks = (rows + rows_per - 1) / rows_per;
     if (chunks <= 1) {
-        hipLaunchKernelGGL(column_sum_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, x, rows, n, out);
+        LAYA_LAUNCH(column_sum_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, x, rows, n, out);
         check_launch("column_sum_kernel");
         return;
     }
     float* part = static_cast<float*>(ctx->workspace(1, sizeof(float) * (size_t)chunks * n));
-    hipLaunchKernelGGL(column_partial_kernel, dim3((n + 255) / 256, chunks), dim3(256), 0, ctx->stream, x, rows, n,
+    LAYA_LAUNCH(column_partial_kernel, dim3((n + 255) / 256, chunks), dim3(256), 0, ctx->stream, x, rows, n,
                        rows_per, part);
     check_launch("column_partial_kernel");
-    hipLaunchKernelGGL(column_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, part, chunks, n, out);
+    LAYA_LAUNCH(column_reduce_kernel, dim3((n + 255) / 256), dim3(256), 0, ctx->stream, part, chunks, n, out);
     check_launch("column_reduce_kernel");
 }
 

@@ -211,6 +211,15 @@ struct laya_model {
     int wm_blocks = 0;
     double wm_bytes = 0;
     std::vector<int> wm_params;
+    // AdamW's fold of the updated weights' magnitudes (laya::AdamFold): the device tables, and the trainable
+    // flags they were made for (empty: not made).
+    int* fold_block = nullptr;
+    long* fold_begin = nullptr;
+    long* fold_end = nullptr;
+    int* fold_word = nullptr;
+    int fold_n = 0;
+    std::vector<int> fold_params;  // the parameter index of each folded tensor
+    std::vector<unsigned char> fold_for;
     size_t amax_sites() const { return (size_t)scorer_site(2); }
     laya::AmaxRef word(size_t k) {
         return amax_words ? laya::AmaxRef{amax_words + k * laya::AMAX_GROUP, &amax_known[k]} : laya::AmaxRef{};
@@ -789,10 +798,20 @@ void forward(laya_model* m, bool train, uint64_t seed) {
         m->amax_words = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_GROUP * n));
         m->amax_known.assign(n, 0);
     }
-    const size_t nw = m->params.size() + m->amax_sites();  // weight and input words (+0.0f: all-zero bits)
-    fill(ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_GROUP * nw);
-    std::fill(m->amax_known.begin(), m->amax_known.begin() + nw, 0);
-    if (ctx->matmul_pair & 3) measure_weights(m);
+    // The input words are cleared at every forward (+0.0f: all-zero bits); the weights' only when one of the
+    // product weights is not known (the AdamW step folds the trainable ones back in as it updates them).
+    const size_t np = m->params.size(), ns = m->amax_sites();
+    fill(ctx, reinterpret_cast<float*>(m->amax_words + AMAX_GROUP * np), 0.0f, AMAX_GROUP * ns);
+    std::fill(m->amax_known.begin() + np, m->amax_known.begin() + np + ns, 0);
+    if (ctx->matmul_pair & 3) {
+        bool known = !m->wm_params.empty();
+        for (int i : m->wm_params) known = known && m->amax_known[i];
+        if (!known) {
+            fill(ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_GROUP * np);
+            std::fill(m->amax_known.begin(), m->amax_known.begin() + np, 0);
+            measure_weights(m);
+        }
+    }
 
     // Embedding gather fused into the embedding LayerNorm.
     float* x0 = m->cfg.layers > 0 ? m->ea[0].x : m->x_final;
@@ -1088,6 +1107,66 @@ void ensure_moments(laya_model* m) {
     fill(m->ctx, m->M2, 0.0f, m->total);
 }
 
+// The AdamW fold's tables for the current trainable flags: the product weights that lie inside the update's
+// groups, and per workgroup of 256 float4s the tensor that covers it whole (-1 none, -2 several or in part).
+void ensure_fold(laya_model* m, const AdamGroups& g) {
+    std::vector<unsigned char> now(m->params.size());
+    for (size_t i = 0; i < m->params.size(); ++i) now[i] = m->params[i].trainable;
+    if (m->fold_block && now == m->fold_for) return;
+    auto inside = [&](size_t b, size_t e) {
+        for (int k = 0; k < g.n; ++k)
+            if (b >= g.begin[k] && e <= g.end[k]) return true;
+        return false;
+    };
+    std::vector<std::pair<long, int>> ts;  // (first float4, parameter)
+    for (int i : m->wm_params) {
+        const Param& p = m->params[i];
+        LAYA_REQUIRE(p.offset % 4 == 0, "adamw fold: tensors must start on a float4");
+        if (p.trainable && inside(p.offset, p.offset + p.numel)) ts.push_back({(long)(p.offset / 4), i});
+    }
+    std::sort(ts.begin(), ts.end());
+    std::vector<long> begin, end;
+    std::vector<int> word;
+    m->fold_params.clear();
+    for (auto& t : ts) {
+        const Param& p = m->params[t.second];
+        begin.push_back(t.first);
+        end.push_back(t.first + (long)(p.numel / 4));  // numel is a multiple of 4 for every product weight
+        word.push_back(t.second);
+        m->fold_params.push_back(t.second);
+        LAYA_REQUIRE(p.numel % 4 == 0, "adamw fold: product weights hold a multiple of 4 values");
+    }
+    const long n4 = (long)(m->total / 4);
+    const long blocks = (n4 + 255) / 256;
+    std::vector<int> blk(blocks, -1);
+    size_t t = 0;
+    for (long b = 0; b < blocks; ++b) {
+        const long lo = b * 256, hi = std::min(n4, lo + 256);
+        while (t < begin.size() && end[t] <= lo) ++t;
+        if (t >= begin.size() || begin[t] >= hi) continue;      // no tensor meets the block
+        blk[b] = begin[t] <= lo && end[t] >= hi ? (int)t : -2;  // whole, or a boundary inside
+    }
+    for (void* p : {(void*)m->fold_block, (void*)m->fold_begin, (void*)m->fold_end, (void*)m->fold_word})
+        if (p) m->ctx->release(p);
+    const size_t nt = std::max<size_t>(begin.size(), 1);
+    m->fold_block = static_cast<int*>(m->ctx->alloc(sizeof(int) * blocks));
+    m->fold_begin = static_cast<long*>(m->ctx->alloc(sizeof(long) * nt));
+    m->fold_end = static_cast<long*>(m->ctx->alloc(sizeof(long) * nt));
+    m->fold_word = static_cast<int*>(m->ctx->alloc(sizeof(int) * nt));
+    m->fold_n = (int)begin.size();
+    LAYA_HIP(hipMemcpyAsync(m->fold_block, blk.data(), sizeof(int) * blocks, hipMemcpyHostToDevice, m->ctx->stream));
+    if (m->fold_n) {
+        LAYA_HIP(hipMemcpyAsync(m->fold_begin, begin.data(), sizeof(long) * begin.size(), hipMemcpyHostToDevice,
+                                m->ctx->stream));
+        LAYA_HIP(hipMemcpyAsync(m->fold_end, end.data(), sizeof(long) * end.size(), hipMemcpyHostToDevice,
+                                m->ctx->stream));
+        LAYA_HIP(hipMemcpyAsync(m->fold_word, word.data(), sizeof(int) * word.size(), hipMemcpyHostToDevice,
+                                m->ctx->stream));
+    }
+    LAYA_HIP(hipStreamSynchronize(m->ctx->stream));  // the host vectors go out of scope
+    m->fold_for = now;
+}
+
 void adamw_step(laya_model* m, double lr_enc, double lr_head, double b1, double b2, double eps, double wd,
                 bool zero_grads) {
     ensure_moments(m);
@@ -1097,17 +1176,28 @@ void adamw_step(laya_model* m, double lr_enc, double lr_head, double b1, double 
     AdamGroups g = adam_groups(m, lr_enc, lr_head, wd, c1, &n);
     // The weights' bf16 copy is updated with them when the products read it; otherwise it goes stale.
     __bf16* mirror = m->copies && m->WB && m->wb_fresh ? m->WB : nullptr;
-    adamw_arena(m->ctx, m->P, m->G, m->M1, m->M2, n, g, (float)b1, (float)b2, (float)eps, (float)std::sqrt(c2),
-                m->coef_valid ? m->d_coef : nullptr, zero_grads ? 1 : 0, mirror);
-    if (!mirror) m->wb_fresh = false;
-    m->pw_fresh = false;  // the bf16 weights are rounded again before the next product reads them
-    m->coef_valid = false;
-    // The update moved the weights, so their magnitude words no longer bound them: cleared (an unknown word
-    // holds zero), to be measured again by the next forward, or by a backward product that runs before one.
+    // The update moves the weights, so their magnitude words no longer bound them: cleared (an unknown word
+    // holds zero). When the products read the fp32 weights themselves, the update folds the new magnitudes of
+    // the trainable product weights back in (the rest are measured again by the next forward, or by a backward
+    // product that runs before one).
+    const AdamFold* fold = nullptr;
+    AdamFold f{};
     if (m->amax_words) {
         fill(m->ctx, reinterpret_cast<float*>(m->amax_words), 0.0f, AMAX_GROUP * m->params.size());
         std::fill(m->amax_known.begin(), m->amax_known.begin() + m->params.size(), 0);
+        if (!m->bf16_weights && !m->wm_params.empty()) {
+            ensure_fold(m, g);
+            f = AdamFold{m->fold_block, m->fold_begin, m->fold_end, m->fold_word, m->fold_n, m->amax_words};
+            fold = &f;
+        }
     }
+    adamw_arena(m->ctx, m->P, m->G, m->M1, m->M2, n, g, (float)b1, (float)b2, (float)eps, (float)std::sqrt(c2),
+                m->coef_valid ? m->d_coef : nullptr, zero_grads ? 1 : 0, mirror, fold);
+    if (fold)
+        for (int k = 0; k < m->fold_n; ++k) m->amax_known[m->fold_params[k]] = 1;
+    if (!mirror) m->wb_fresh = false;
+    m->pw_fresh = false;  // the bf16 weights are rounded again before the next product reads them
+    m->coef_valid = false;
 }
 
 laya_model* checked(laya_model* m) {
@@ -1166,7 +1256,8 @@ int laya_model_destroy(laya_model* m) {
         for (auto& s : m->staged)
             if (s.block) ctx->release(s.block);
         for (void* p : {(void*)m->d_draws, (void*)m->d_rlcd_losses, (void*)m->ln_part, (void*)m->WB, (void*)m->PW,
-                        (void*)m->amax_words, (void*)m->wm_off, (void*)m->wm_len, (void*)m->wm_word})
+                        (void*)m->amax_words, (void*)m->wm_off, (void*)m->wm_len, (void*)m->wm_word,
+                        (void*)m->fold_block, (void*)m->fold_begin, (void*)m->fold_end, (void*)m->fold_word})
             if (p) ctx->release(p);
         free_rotary(ctx, &m->rot_global);
         free_rotary(ctx, &m->rot_local);

@@ -285,7 +285,7 @@ void layernorm_fwd(laya_ctx* ctx, const float* x, int rows, int n, const float* 
     ProfileScope scope(ctx, "layernorm_fwd", 0.0, (8.0 * n + (y16 ? 2.0 * n : 0.0) + 8.0) * rows + 4.0 * n * (b ? 2 : 1));
 #define LN_FWD(C)                                                                                                 \
     case C:                                                                                                       \
-        hipLaunchKernelGGL(ln_fwd_kernel<C>, grid, block, 0, ctx->stream, x, rows, n, w, b, eps, y, mean, rstd, \
+        LAYA_LAUNCH(ln_fwd_kernel<C>, grid, block, 0, ctx->stream, x, rows, n, w, b, eps, y, mean, rstd, \
                            gather_ids, gather_rows, add_table, add_index, y16, amax);                            \
         break;
     switch (nch) { LN_FWD(1) LN_FWD(2) LN_FWD(3) LN_FWD(4) LN_FWD(5) LN_FWD(6) LN_FWD(7) LN_FWD(8) }
@@ -319,7 +319,7 @@ static void layernorm_bwd_impl(laya_ctx* ctx, const float* x, int rows, int n, c
                            (16.0 * n + (mean ? 8.0 : 0.0)) * rows + 4.0 * n);
 #define LN_BWD(C)                                                                                                \
     case C:                                                                                                      \
-        hipLaunchKernelGGL(ln_bwd_kernel<C>, grid, block, lds, ctx->stream, x, rows, n, w, eps, dy, dx, mean,  \
+        LAYA_LAUNCH(ln_bwd_kernel<C>, grid, block, lds, ctx->stream, x, rows, n, w, eps, dy, dx, mean,  \
                            rstd, gather_ids, gather_rows, waves, pg, pb, amax);                                  \
         break;
         switch (nch) { LN_BWD(1) LN_BWD(2) LN_BWD(3) LN_BWD(4) LN_BWD(5) LN_BWD(6) LN_BWD(7) LN_BWD(8) }
@@ -348,11 +348,11 @@ static void layernorm_bwd_impl(laya_ctx* ctx, const float* x, int rows, int n, c
     ProfileScope scope(ctx, (pg || pb) && profile ? "layernorm_bwd_reduce" : nullptr, 0.0,
                        4.0 * n * (blocks + 2.0) * ((pg ? 1 : 0) + (pb ? 1 : 0)));
     if (pg) {
-        hipLaunchKernelGGL(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pg, blocks, n, dgamma);
+        LAYA_LAUNCH(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pg, blocks, n, dgamma);
         check_launch("partial_reduce_kernel");
     }
     if (pb) {
-        hipLaunchKernelGGL(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pb, blocks, n, dbeta);
+        LAYA_LAUNCH(partial_reduce_kernel, rgrid, rblock, 0, ctx->stream, pb, blocks, n, dbeta);
         check_launch("partial_reduce_kernel");
     }
 }

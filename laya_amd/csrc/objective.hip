@@ -196,7 +196,7 @@ void rlcd_objective(laya_ctx* ctx, const float* logits, const float* targets, co
     a.grad = grad;
     a.losses = losses;
     ProfileScope scope(ctx, "rlcd_objective", 0.0, 0.0);
-    hipLaunchKernelGGL(rlcd_kernel, dim3(1), dim3(THREADS), 0, ctx->stream, a);
+    LAYA_LAUNCH(rlcd_kernel, dim3(1), dim3(THREADS), 0, ctx->stream, a);
     check_launch("rlcd_kernel");
 }
 

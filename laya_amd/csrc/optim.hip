@@ -134,11 +134,40 @@ __device__ __forceinline__ int adam_group(const AdamGroups& groups, size_t i) {
     return grp;
 }
 
+// The tensor of fold that holds float4 i, or -1.
+__device__ __forceinline__ int fold_tensor(const AdamFold& f, long i) {
+    int lo = 0, hi = f.n - 1;
+    while (lo < hi) {  // the last tensor beginning at or before i
+        const int mid = (lo + hi + 1) >> 1;
+        if (f.begin[mid] <= i) lo = mid; else hi = mid - 1;
+    }
+    return f.n > 0 && f.begin[lo] <= i && i < f.end[lo] ? lo : -1;
+}
+
+// Folds the lane's max|w| (amax bits) into its tensor's word group: one atomic per wave when the wave's lanes
+// share a tensor, else one per lane. Every lane of the wave calls it.
+__device__ __forceinline__ void fold_wave(const AdamFold& f, int t, unsigned am) {
+    const int t0 = __shfl(t, 0, 64);
+    if (__all(t == t0)) {
+        if (t0 < 0) return;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) am = max(am, (unsigned)__shfl_xor((int)am, o, 64));
+        if ((threadIdx.x & 63) == 0 && am)
+            atomicMax(f.words + (size_t)f.word[t0] * AMAX_GROUP + (blockIdx.x & (AMAX_SPREAD - 1)) * AMAX_STRIDE, am);
+    } else if (t >= 0 && am) {
+        atomicMax(f.words + (size_t)f.word[t] * AMAX_GROUP + (blockIdx.x & (AMAX_SPREAD - 1)) * AMAX_STRIDE, am);
+    }
+}
+
+// With a fold, the grid covers the arena in one pass (one float4 per thread) and every lane reaches the fold.
 __global__ __launch_bounds__(256) void adamw4_kernel(f32x4* __restrict__ p, f32x4* __restrict__ g,
                                                      f32x4* __restrict__ m, f32x4* __restrict__ v, size_t n4,
                                                      AdamGroups groups, float b1, float b2, float eps, float sqrt_c2,
-                                                     const float* coef, int zero_grads, bf16x4* __restrict__ mirror) {
+                                                     const float* coef, int zero_grads, bf16x4* __restrict__ mirror,
+                                                     AdamFold fold) {
     const float cf = coef ? *coef : 1.0f;
+    unsigned am = 0;
+    int t = -1;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
         const int grp = adam_group(groups, i);
         const f32x4 gi = __builtin_nontemporal_load(g + i);
@@ -152,9 +181,15 @@ __global__ __launch_bounds__(256) void adamw4_kernel(f32x4* __restrict__ p, f32x
             __builtin_nontemporal_store(vo, v + i);
             // The bf16 copy of the updated weights (nearest even) that the bf16 products read.
             if (mirror) mirror[i] = __builtin_convertvector(wo, bf16x4);
+            if (fold.n) {
+                const int tb = fold.block[blockIdx.x];  // block-uniform
+                t = tb == -2 ? fold_tensor(fold, (long)i) : tb;
+                if (t >= 0) am = amax_bits4(wo);
+            }
         }
         if (zero_grads) __builtin_nontemporal_store(f32x4{0.0f, 0.0f, 0.0f, 0.0f}, g + i);
     }
+    if (fold.n) fold_wave(fold, t, am);
 }
 
 bool vec4_ok(const void* a) { return ((uintptr_t)a & 15u) == 0; }
@@ -168,21 +203,21 @@ void grad_norm(laya_ctx* ctx, const float* g, size_t n, double max_norm, double*
     if (chunk == 0) chunk = 1024;
     ProfileScope scope(ctx, "grad_norm", 0.0, 4.0 * n);
     if (n % 4 == 0 && vec4_ok(g)) {
-        hipLaunchKernelGGL(sumsq4_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx->stream,
+        LAYA_LAUNCH(sumsq4_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx->stream,
                            reinterpret_cast<const f32x4*>(g), n / 4, chunk / 4, partial);
         check_launch("sumsq4_kernel");
     } else {
-        hipLaunchKernelGGL(sumsq_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx->stream, g, n, chunk, partial);
+        LAYA_LAUNCH(sumsq_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx->stream, g, n, chunk, partial);
         check_launch("sumsq_kernel");
     }
-    hipLaunchKernelGGL(norm_finish_kernel, dim3(1), dim3(64), 0, ctx->stream, partial, NORM_BLOCKS, max_norm, norm,
+    LAYA_LAUNCH(norm_finish_kernel, dim3(1), dim3(64), 0, ctx->stream, partial, NORM_BLOCKS, max_norm, norm,
                        coef, nonfinite);
     check_launch("norm_finish_kernel");
 }
 
 void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n, const AdamGroups& groups,
                  float beta1, float beta2, float eps, float sqrt_c2, const float* coef, int zero_grads,
-                 __bf16* mirror) {
+                 __bf16* mirror, const AdamFold* fold) {
     LAYA_REQUIRE(groups.n >= 0 && groups.n <= 4, "adamw: at most 4 parameter groups");
     for (int k = 0; k < groups.n; ++k)
         LAYA_REQUIRE(groups.begin[k] <= groups.end[k] && groups.end[k] <= n, "adamw: group range outside the arena");
@@ -196,14 +231,21 @@ void adamw_arena(laya_ctx* ctx, float* p, float* g, float* m, float* v, size_t n
             g4.begin[k] = groups.begin[k] / 4;
             g4.end[k] = groups.end[k] / 4;
         }
-        hipLaunchKernelGGL(adamw4_kernel, dim3(blocks_for(n / 4, 256, 1u << 22)), dim3(256), 0, ctx->stream,
+        const unsigned blocks = blocks_for(n / 4, 256, 1u << 22);
+        AdamFold f{};
+        if (fold && fold->n > 0) {
+            LAYA_REQUIRE((size_t)blocks * 256 >= n / 4, "adamw: the weight fold needs one float4 per thread");
+            f = *fold;
+        }
+        LAYA_LAUNCH(adamw4_kernel, dim3(blocks), dim3(256), 0, ctx->stream,
                            reinterpret_cast<f32x4*>(p), reinterpret_cast<f32x4*>(g), reinterpret_cast<f32x4*>(m),
                            reinterpret_cast<f32x4*>(v), n / 4, g4, beta1, beta2, eps, sqrt_c2, coef, zero_grads,
-                           reinterpret_cast<bf16x4*>(mirror));
+                           reinterpret_cast<bf16x4*>(mirror), f);
         check_launch("adamw4_kernel");
         return;
     }
-    hipLaunchKernelGGL(adamw_kernel, dim3(blocks_for(n, 256, 8192)), dim3(256), 0, ctx->stream, p, g, m, v, n, groups,
+    LAYA_REQUIRE(!fold || fold->n == 0, "adamw: the weight fold needs 16-byte aligned arenas and float4 groups");
+    LAYA_LAUNCH(adamw_kernel, dim3(blocks_for(n, 256, 8192)), dim3(256), 0, ctx->stream, p, g, m, v, n, groups,
                        beta1, beta2, eps, sqrt_c2, coef, zero_grads, mirror);
     check_launch("adamw_kernel");
 }

@@ -99,7 +99,7 @@ void decision_readout(laya_ctx* ctx, const float* scores, const int* opt_off, co
     const size_t lds = sizeof(float) * (size_t)(d + 4 + a1 + na);
     LAYA_REQUIRE(lds <= 64 * 1024, "readout: act-head input too wide for one workgroup");
     ProfileScope scope(ctx, "decision_readout", 0.0, 4.0 * n_items * ((double)d + (double)a1 * (d + 4)));
-    hipLaunchKernelGGL(readout_kernel, dim3(n_items), dim3(RO_THREADS), lds, ctx->stream, scores, opt_off, seg_start,
+    LAYA_LAUNCH(readout_kernel, dim3(n_items), dim3(RO_THREADS), lds, ctx->stream, scores, opt_off, seg_start,
                        states, d, w1, b1, a1, w2, b2, na, probs, features);
     check_launch("readout_kernel");
 }

@@ -641,3 +641,37 @@ def test_backward_keeps_precision_for_items_with_tiny_logit_gradients(ctx):
     m.backward(dl2)
     assert not m.backward_fell_back
     m.close()
+
+
+def test_adamw_step_folds_the_weights_magnitudes_exactly(ctx):
+    """The AdamW step folds each updated product weight's max|w| into its magnitude word, so the next forward
+    measures nothing: its logits and gradients are bitwise those of a forward that measured the same weights
+    afresh (the weights written back unchanged from the host, which clears every word)."""
+    from laya_amd.model import TrainableDecisionModel
+    mc, o, params, batch = _mid_case(layers=2, lengths=(150, 90, 33))
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    rng = np.random.default_rng(9)
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+    d = rng.standard_normal(batch.n_markers).astype(np.float32)
+    for step in range(2):
+        m.train_step(batch, targets, 40 + step, loss_scale=float(batch.n_items), lr_encoder=1e-3, lr_head=1e-3)
+    ctx.profile_begin()
+    folded = m.forward(batch, training=True, seed=3)
+    prof_folded = ctx.profile_end()
+    m.zero_gradients()
+    m.backward(d)
+    g_folded = {n: m.grad(n) for n in m.names if m.has_grad(n)}
+    m.set_params({n: m.param(n) for n in m.names})  # unchanged values; the words are measured again
+    m.zero_gradients()
+    ctx.profile_begin()
+    measured = m.forward(batch, training=True, seed=3)
+    prof_measured = ctx.profile_end()
+    m.backward(d)
+    # The forward after the step skips the one launch that measures every weight.
+    launches = lambda p: p.get("absmax", {}).get("launches", 0)  # noqa: E731
+    assert launches(prof_folded) == launches(prof_measured) - 1, (prof_folded.get("absmax"), prof_measured["absmax"])
+    np.testing.assert_array_equal(folded, measured)
+    for n, g in g_folded.items():
+        np.testing.assert_array_equal(g, m.grad(n), err_msg=n)
+    m.close()
