@@ -948,6 +948,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     const float sq = exp2_int(eq), so = exp2_int(eo);
     const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
     const float udp = NP == 2 ? ldexpf(1.0f, -(eo + eq)) : 1.0f;
+    const float dsc = p.scale * udp;
     V8 kh[4][NP];
     const long krow = (long)(start + (kvalid ? key : 0)) * stride;
     split_lane_row<NP>(p.qkv + krow + kcol, kvalid, h, kh, sq);
@@ -993,7 +994,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
         commit_swz<BT, NP>(ost, Os, so);
         if (threadIdx.x < BT) {
             lse_s[threadIdx.x] = lse_n;
-            dot_s[threadIdx.x] = dot_n;
+            dot_s[threadIdx.x] = NP == 2 ? ldexpf(dot_n, eo + eq) : dot_n;  // in dP's scaled units
         }
         __syncthreads();
         if (qt0 + BT < qend) fetch(qt0 + BT);  // block-uniform
@@ -1010,10 +1011,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
             swz_row_frag<BLOCK_ROWS, NP>(Vs, wave * WAVE_ROWS + lr, ks, h, vh);
             dp = Pieces<NP>::mma(f, vh, dp);
         }
-        if constexpr (NP == 2) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) dp[r] *= udp;
-        }
+        // dP stays in its operands' scaled units (2^(eo + eq)), the row constants were staged in the same
+        // units and the units' factor sits in the softmax scale (dsc): the same values, bit for bit.
         float pm[16], ds[16];
         const int rel0 = qt0 + 4 * h - win.lo;  // query − lo of the lane's row r = 0
         if (!DROP) {
@@ -1023,7 +1022,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                     const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
                     const float pr = fast_exp2(s[r] * scale_log2 - lse_s[ql]);
                     pm[r] = pr;
-                    ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
+                    ds[r] = pr * (dp[r] - dot_s[ql]) * dsc;
                 }
             } else {
 #pragma unroll
@@ -1032,7 +1031,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                     const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
                     const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse_s[ql]) : 0.0f;
                     pm[r] = pr;
-                    ds[r] = pr * (dp[r] - dot_s[ql]) * p.scale;
+                    ds[r] = pr * (dp[r] - dot_s[ql]) * dsc;
                 }
             }
         } else {
@@ -1046,7 +1045,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                     uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
                 const float mask = ok ? drop : 1.0f;
                 pm[r] = pr * mask;
-                ds[r] = pr * (dp[r] * mask - dot_s[ql]) * p.scale;
+                ds[r] = pr * (dp[r] * mask - dot_s[ql]) * dsc;
             }
         }
         // dVᵀ += dOᵀ·(P∘M) and dKᵀ += Qᵀ·dS over the tile's 32 queries in two 16-query steps.
@@ -1136,6 +1135,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     }
     dot += __shfl_xor(dot, 32, 64);
     if (qvalid && h == 0) p.dots[(long)qs * p.heads + head] = dot;
+    const float dotu = NP == 2 ? ldexpf(dot, eo + eq) : dot;  // in dP's scaled units
+    const float dsc = p.scale * udp;
 
     int kbeg = 0, kend = L, wbeg = 0, wend = L;
     if (hw >= 0) {
@@ -1176,22 +1177,20 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
             swz_row_frag<BT, NP>(Vs, lr, ks, h, f);
             dp = Pieces<NP>::mma(f, oh[ks], dp);
         }
-        if constexpr (NP == 2) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) dp[r] *= udp;
-        }
+        // dP stays in its operands' scaled units (2^(eo + eq)); the row constant is taken into the same units
+        // (dotu) and the units' factor into the softmax scale (dsc): the same values, bit for bit.
         float ds[16];
         const int rel0 = kt0 + 4 * h - win.lo;  // key − lo of the lane's row r = 0
         if (!DROP) {
             if (subtile_inside(q0w, kt0, L, hw)) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * scale_log2 - lse) * (dp[r] - dot) * p.scale;
+                for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * scale_log2 - lse) * (dp[r] - dotu) * dsc;
             } else {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
                     const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse) : 0.0f;
-                    ds[r] = pr * (dp[r] - dot) * p.scale;
+                    ds[r] = pr * (dp[r] - dotu) * dsc;
                 }
             }
         } else {
@@ -1203,7 +1202,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
                 const float drop =
                     uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
                 const float mask = ok ? drop : 1.0f;
-                ds[r] = pr * (dp[r] * mask - dot) * p.scale;
+                ds[r] = pr * (dp[r] * mask - dotu) * dsc;
             }
         }
         // dQᵀ += Kᵀ·dSᵀ over the tile's 32 keys in two 16-key steps.
