@@ -161,11 +161,13 @@ def _unaffected_by(layer: int):
                                                         f"head.layers.{layer}.norm2."))
 
 
+@pytest.mark.parametrize("workload", ["b32x512", "b2x8192"])
 @pytest.mark.parametrize("policy", ["fp32", "fp32-split3"])
-def test_benchmark_step_itself_matches_fp64(ctx, policy):
+def test_benchmark_step_itself_matches_fp64(ctx, policy, workload):
     """The step bench.py times, as it times it: its parameters (synthetic_params with its seed: N(0, 0.02)
     matrices, unit γ, zero biases), its first batch and its first step's dropout seed, against the fp64 oracle
-    run on the same (tests/golden/make_fullsize_fixtures.py --bench-init).
+    run on the same (tests/golden/make_fullsize_fixtures.py --bench-init): the headline batch 32 × 512 and the
+    long-context batch 2 × 8192 (bench.py --workload b2x8192).
 
     Zero head biases put the head ReLU inputs around zero, so a few of ~88M may sit within rounding of it and
     be decided differently by any two fp32 implementations (the fp32 oracle too). The test proves that every
@@ -176,10 +178,10 @@ def test_benchmark_step_itself_matches_fp64(ctx, policy):
     at the differing ties (values within rounding of zero) and the backward run again."""
     from laya_amd.config import modernbert_base
     from laya_amd.model import TrainableDecisionModel, synthetic_params
-    print(f"full size: bench.py's own step (its parameters, batch 32 x 512, seed {BENCH_STEP_SEED}), {policy}",
+    print(f"full size: bench.py's own step (its parameters, {workload}, seed {BENCH_STEP_SEED}), {policy}",
           flush=True)
-    fx = np.load(fixture_path("b32x512", bench_init=True))
-    batch, _, _ = workload_batch("b32x512")
+    fx = np.load(fixture_path(workload, bench_init=True))
+    batch, _, _ = workload_batch(workload)
     assert int(fx["meta"][2]) == batch.n_tokens and int(fx["meta"][1]) == BENCH_STEP_SEED
     ctx.set_matmul_precision(policy)
     try:
@@ -192,9 +194,13 @@ def test_benchmark_step_itself_matches_fp64(ctx, policy):
         flips = _relu_decisions(m, fx, BENCH_STEP_SEED)
         m.backward(fx["dlogits"])
         prof = ctx.profile_end()
-        pair, _, tall, _ = KERNELS[policy]
-        assert prof.get(pair, {}).get("launches", 0) >= 90, sorted(prof)
-        assert prof.get(tall, {}).get("launches", 0) >= 88, sorted(prof)
+        pair, _, tall, dkv = KERNELS[policy]
+        if workload == "b32x512":
+            assert prof.get(pair, {}).get("launches", 0) >= 90, sorted(prof)
+            assert prof.get(tall, {}).get("launches", 0) >= 88, sorted(prof)
+        else:
+            assert prof.get(dkv, {}).get("launches", 0) == 24, sorted(prof)
+            assert prof.get(tall, {}).get("launches", 0) >= 22, sorted(prof)
         flipped = [j for j, (pos, _) in enumerate(flips) if pos.size]
         if not flipped:
             _check_gradients(m, fx)
