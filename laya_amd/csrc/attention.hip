@@ -342,12 +342,14 @@ template <> struct Pieces<3> {
     typedef bf16x8 V8;
     typedef bf16x4 V4;
     static __device__ __forceinline__ void split4(f32x4 x, float, V4 (&o)[3]) { split3_4(x, o[0], o[1], o[2]); }
+    static __device__ __forceinline__ void split4u(f32x4 x, float, V4 (&o)[3]) { split3_4(x, o[0], o[1], o[2]); }
     static __device__ __forceinline__ f32x16 mma(const V8 (&a)[3], const V8 (&b)[3], f32x16 c) { return mma6(a, b, c); }
 };
 template <> struct Pieces<2> {
     typedef f16x8 V8;
     typedef f16x4 V4;
     static __device__ __forceinline__ void split4(f32x4 x, float sc, V4 (&o)[2]) { split2h_4(x, sc, o[0], o[1]); }
+    static __device__ __forceinline__ void split4u(f32x4 x, float one, V4 (&o)[2]) { split2h_4u(x, one, o[0], o[1]); }
     static __device__ __forceinline__ f32x16 mma(const V8 (&a)[2], const V8 (&b)[2], f32x16 c) {
         c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], b[0], c, 0, 0, 0);
         c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b[1], c, 0, 0, 0);
@@ -359,14 +361,15 @@ template <> struct Pieces<2> {
 // products: a lane's 16 values, with its partner lane's (lanes l and l + 32 feed the same output column),
 // set the exponent 14 − ⌊log₂ max⌋; it only decreases over the tiles, and when it does the column's
 // accumulators are rescaled by the same exact power of two, so they always carry one factor 2^e.
-// Returns the new exponent (e0 = 126 before the first tile).
+// The operand is c·v for a positive constant c that the split applies (c·max|v| rounds to the largest
+// |c·v|, rounding being monotone). Returns the new exponent (e0 = 126 before the first tile).
 // (A NaN is passed over by the maximum; an infinity gives a tiny scale that keeps it infinite.)
 template <int N>
-__device__ __forceinline__ int lane_scale_update(const float (&v)[16], int e, f32x16 (&acc)[N]) {
+__device__ __forceinline__ int lane_scale_update(const float (&v)[16], int e, f32x16 (&acc)[N], float c = 1.0f) {
     float m = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) m = fmaxf(m, fabsf(v[r]));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64)) * c;
     const int et = pair_scale_exp(__builtin_bit_cast(unsigned, m));
     if (et < e) {
         const float f = ldexpf(1.0f, et - e);
@@ -387,6 +390,16 @@ __device__ __forceinline__ void split8(f32x4 lo, f32x4 hi, typename Pieces<NP>::
     for (int pl = 0; pl < NP; ++pl) out[pl] = cat8(a[pl], b[pl]);
 }
 
+// split8 at unit scale (split2h_4u for two-piece products).
+template <int NP>
+__device__ __forceinline__ void split8u(f32x4 lo, f32x4 hi, typename Pieces<NP>::V8 (&out)[NP], float one) {
+    typename Pieces<NP>::V4 a[NP], b[NP];
+    Pieces<NP>::split4u(lo, one, a);
+    Pieces<NP>::split4u(hi, one, b);
+#pragma unroll
+    for (int pl = 0; pl < NP; ++pl) out[pl] = cat8(a[pl], b[pl]);
+}
+
 // An R × 64 slice of one head (R = 32, 64 or 128 rows) in registers between its global fetch and its LDS
 // commit: thread t holds rows (R/16)·(t/16) + i (i < R/16) at d = 4·(t%16) … +3.
 template <int R>
@@ -395,14 +408,20 @@ struct RowStage {
     f32x4 v[N];
 };
 
+// Rows row0 … row0 + R − 1 (row0 ≥ 0, block-uniform) of a segment of L rows. The loads go through a buffer
+// resource that spans rows row0 … L − 1 only: a row at or past L lies beyond its record count and reads
+// as zeros, so no lane computes a 64-bit address or takes a branch (the host keeps L · stride · 4 < 2³¹).
 template <int R>
 __device__ __forceinline__ void fetch_rows(RowStage<R>& st, const float* base, long stride, int L, int row0) {
     constexpr int N = RowStage<R>::N;
     const int q = threadIdx.x >> 4, j = (threadIdx.x & 15) * 4;
+    const int bytes = row0 < L ? (L - row0) * (int)stride * 4 : 0;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(base + (long)row0 * stride), (short)0, bytes, 0x00020000);
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-        const int t = row0 + N * q + i;
-        st.v[i] = (t >= 0 && t < L) ? ld4(base + (long)t * stride + j) : f32x4{0, 0, 0, 0};
+        const int off = ((N * q + i) * (int)stride + j) * 4;
+        st.v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     }
 }
 
@@ -424,6 +443,12 @@ __device__ __forceinline__ void split_col16(const float (&v)[16], int u, typenam
                                             float sc = 1.0f) {
     split8<NP>(f32x4{v[8 * u], v[8 * u + 1], v[8 * u + 2], v[8 * u + 3]},
                f32x4{v[8 * u + 4], v[8 * u + 5], v[8 * u + 6], v[8 * u + 7]}, out, sc);
+}
+
+template <int NP>
+__device__ __forceinline__ void split_col16u(const float (&v)[16], int u, typename Pieces<NP>::V8 (&out)[NP], float one) {
+    split8u<NP>(f32x4{v[8 * u], v[8 * u + 1], v[8 * u + 2], v[8 * u + 3]},
+                f32x4{v[8 * u + 4], v[8 * u + 5], v[8 * u + 6], v[8 * u + 7]}, out, one);
 }
 
 // One LDS layout for every staged tile.
@@ -521,6 +546,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     }
     const float sq = exp2_int(eq);
     const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
+    float one = 1.0f;
+    asm volatile("" : "+s"(one));  // 1.0 that the compiler cannot fold (split2h_4u)
     V8 qh[4][NP];
     split_lane_row<NP>(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, qvalid, h, qh, sq);
 
@@ -566,23 +593,18 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
                 swz_row_frag<TILE, NP>(Ks, 32 * st + lr, ks, h, kf);
                 s = Pieces<NP>::mma(kf, qh[ks], s);
             }
-            float t[16];
+            // The maximum is taken over the raw scores and scaled once (the scale is positive and rounding
+            // monotone, so it is the largest scaled score); each exponent is one fused s·scale − mm.
             float mx = -1e30f;
-            if (subtile_inside(q0w, kbs, L, hw)) {
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    t[r] = s[r] * scale_log2;
-                    mx = fmaxf(mx, t[r]);
-                }
-            } else {
+            if (!subtile_inside(q0w, kbs, L, hw)) {
                 const int rel0 = kbs + 4 * h - win.lo;  // key − lo of the lane's row r = 0
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    t[r] = in_range(win, rel0 + 8 * (r >> 2) + (r & 3)) ? s[r] * scale_log2 : NEG_INF;
-                    mx = fmaxf(mx, t[r]);
-                }
+                for (int r = 0; r < 16; ++r)
+                    if (!in_range(win, rel0 + 8 * (r >> 2) + (r & 3))) s[r] = NEG_INF;
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * scale_log2;
             // The running max moves only when a score passes it by more than 2^LAZY_RESCALE (the
             // probabilities then stay below 2^LAZY_RESCALE): most subtiles rescale nothing.
             const bool grow = mx > m + LAZY_RESCALE;
@@ -611,7 +633,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
             float sum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                pr[r] = fast_exp2(t[r] - mm);
+                pr[r] = fast_exp2(__builtin_fmaf(s[r], scale_log2, -mm));
                 sum += pr[r];
             }
             l += sum;
@@ -627,7 +649,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 V8 ph[NP];
-                split_col16<NP>(pr, u, ph);
+                split_col16u<NP>(pr, u, ph, one);
 #pragma unroll
                 for (int dt = 0; dt < 2; ++dt) {
                     V8 vf[NP];
@@ -949,6 +971,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
     const float udp = NP == 2 ? ldexpf(1.0f, -(eo + eq)) : 1.0f;
     const float dsc = p.scale * udp;
+    const float dmul = NP == 2 ? 1.0f : dsc;
     V8 kh[4][NP];
     const long krow = (long)(start + (kvalid ? key : 0)) * stride;
     split_lane_row<NP>(p.qkv + krow + kcol, kvalid, h, kh, sq);
@@ -1012,7 +1035,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
             dp = Pieces<NP>::mma(f, vh, dp);
         }
         // dP stays in its operands' scaled units (2^(eo + eq)), the row constants were staged in the same
-        // units and the units' factor sits in the softmax scale (dsc): the same values, bit for bit.
+        // units and the units' factor sits in the softmax scale dsc, which the two-piece split applies
+        // (dmul = 1) and the three-piece form multiplies in (dmul = dsc).
         float pm[16], ds[16];
         const int rel0 = qt0 + 4 * h - win.lo;  // query − lo of the lane's row r = 0
         if (!DROP) {
@@ -1022,7 +1046,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                     const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
                     const float pr = fast_exp2(s[r] * scale_log2 - lse_s[ql]);
                     pm[r] = pr;
-                    ds[r] = pr * (dp[r] - dot_s[ql]) * dsc;
+                    ds[r] = pr * (dp[r] - dot_s[ql]) * dmul;
                 }
             } else {
 #pragma unroll
@@ -1031,7 +1055,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                     const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
                     const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse_s[ql]) : 0.0f;
                     pm[r] = pr;
-                    ds[r] = pr * (dp[r] - dot_s[ql]) * dsc;
+                    ds[r] = pr * (dp[r] - dot_s[ql]) * dmul;
                 }
             }
         } else {
@@ -1045,19 +1069,20 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
                     uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
                 const float mask = ok ? drop : 1.0f;
                 pm[r] = pr * mask;
-                ds[r] = pr * (dp[r] * mask - dot_s[ql]) * dsc;
+                ds[r] = pr * (dp[r] * mask - dot_s[ql]) * dmul;
             }
         }
-        // dVᵀ += dOᵀ·(P∘M) and dKᵀ += Qᵀ·dS over the tile's 32 queries in two 16-query steps.
+        // dVᵀ += dOᵀ·(P∘M) and dKᵀ += Qᵀ·dS over the tile's 32 queries in two 16-query steps; dS is
+        // ds·dsc, the constant applied by the split together with the lane's scale.
         if constexpr (NP == 2) {
             ep = lane_scale_update(pm, ep, dv);
-            eds = lane_scale_update(ds, eds, dk);
+            eds = lane_scale_update(ds, eds, dk, dsc);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             V8 ph[NP], dh[NP];
             split_col16<NP>(pm, u, ph, exp2_int(NP == 2 ? ep : 0));
-            split_col16<NP>(ds, u, dh, exp2_int(NP == 2 ? eds : 0));
+            split_col16<NP>(ds, u, dh, dsc * exp2_int(NP == 2 ? eds : 0));
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
                 V8 f[NP];
@@ -1137,6 +1162,7 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     if (qvalid && h == 0) p.dots[(long)qs * p.heads + head] = dot;
     const float dotu = NP == 2 ? ldexpf(dot, eo + eq) : dot;  // in dP's scaled units
     const float dsc = p.scale * udp;
+    const float dmul = NP == 2 ? 1.0f : dsc;
 
     int kbeg = 0, kend = L, wbeg = 0, wend = L;
     if (hw >= 0) {
@@ -1178,19 +1204,20 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
             dp = Pieces<NP>::mma(f, oh[ks], dp);
         }
         // dP stays in its operands' scaled units (2^(eo + eq)); the row constant is taken into the same units
-        // (dotu) and the units' factor into the softmax scale (dsc): the same values, bit for bit.
+        // (dotu) and the units' factor into the softmax scale dsc, which the two-piece split applies
+        // (dmul = 1) and the three-piece form multiplies in (dmul = dsc).
         float ds[16];
         const int rel0 = kt0 + 4 * h - win.lo;  // key − lo of the lane's row r = 0
         if (!DROP) {
             if (subtile_inside(q0w, kt0, L, hw)) {
 #pragma unroll
-                for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * scale_log2 - lse) * (dp[r] - dotu) * dsc;
+                for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r] * scale_log2 - lse) * (dp[r] - dotu) * dmul;
             } else {
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
                     const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse) : 0.0f;
-                    ds[r] = pr * (dp[r] - dotu) * dsc;
+                    ds[r] = pr * (dp[r] - dotu) * dmul;
                 }
             }
         } else {
@@ -1202,15 +1229,16 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
                 const float drop =
                     uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
                 const float mask = ok ? drop : 1.0f;
-                ds[r] = pr * (dp[r] * mask - dotu) * dsc;
+                ds[r] = pr * (dp[r] * mask - dotu) * dmul;
             }
         }
-        // dQᵀ += Kᵀ·dSᵀ over the tile's 32 keys in two 16-key steps.
-        if constexpr (NP == 2) eds = lane_scale_update(ds, eds, dq);
+        // dQᵀ += Kᵀ·dSᵀ over the tile's 32 keys in two 16-key steps; dS is ds·dsc, the constant applied by
+        // the split together with the lane's scale.
+        if constexpr (NP == 2) eds = lane_scale_update(ds, eds, dq, dsc);
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             V8 dh[NP];
-            split_col16<NP>(ds, u, dh, exp2_int(NP == 2 ? eds : 0));
+            split_col16<NP>(ds, u, dh, dsc * exp2_int(NP == 2 ? eds : 0));
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt) {
                 V8 f[NP];
@@ -1299,6 +1327,9 @@ void check_args(const AttentionArgs& a) {
     LAYA_REQUIRE(a.heads <= 65535 && a.nseg <= 65535, "attention: too many heads or segments for one launch");
     LAYA_REQUIRE(a.p_drop >= 0.0f && a.p_drop < 1.0f, "attention: dropout must be in [0, 1)");
     LAYA_REQUIRE(a.cos_table == nullptr || a.positions >= a.max_len, "attention: rotary table shorter than max_len");
+    // The split-product kernels address a segment's rows through 32-bit buffer offsets.
+    LAYA_REQUIRE(((long)a.max_len + BLOCK_ROWS) * 3L * a.hidden * 4L < (1L << 31),
+                 "attention: a segment's qkv rows exceed 2 GiB");
 }
 
 // Attention takes split products (fp32 results) unless the context asked for the fp32 matrix cores; the

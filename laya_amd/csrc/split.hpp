@@ -49,6 +49,18 @@ __device__ __forceinline__ void split2h_4(f32x4 x, float s, f16x4& hi, f16x4& lo
     lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x4), f16x4);
 }
 
+// The same split at unit scale: hi = f16(x), lo = f16(x − hi). `one` is 1.0 held where the compiler cannot
+// fold it, so the exact remainder x·1 − hi is one fused mix-precision multiply-add on the fp16 hi rather
+// than a convert back to fp32 and a subtraction.
+__device__ __forceinline__ void split2h_4u(f32x4 x, float one, f16x4& hi, f16x4& lo) {
+    hi = __builtin_convertvector(x, f16x4);
+    const f32x4 h = __builtin_convertvector(hi, f32x4);
+    f32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = __builtin_fmaf(x[i], one, -h[i]);
+    lo = __builtin_convertvector(r, f16x4);
+}
+
 // The scale exponent of an operand whose largest finite magnitude has the fp32 bit pattern `amax`:
 // s = 2^e with e = 14 − exponent(amax), clamped to [−126, 126] (an all-zero operand takes 2¹²⁶).
 __device__ __forceinline__ int pair_scale_exp(unsigned amax) {
