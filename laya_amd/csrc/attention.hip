@@ -1108,11 +1108,14 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     block_amax_fold(am, p.amax);
 }
 
+// Each wave owns 32 queries: q split once into registers, dO split once into the block's LDS planes (each
+// wave reads back only its own rows), which keeps the two-piece form within three waves per SIMD.
 template <int D, bool DROP, int NP = 3>
-__global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
+__global__ __launch_bounds__(THREADS, NP == 2 ? 3 : 2) void attn_bwd_dq_x6_kernel(Params p) {
     static_assert(D == 64, "split-product attention is written for head_dim 64");
     __shared__ __attribute__((aligned(16))) __bf16 Ks[NP * BT * 64];  // K tile, swizzled [key][d]
     __shared__ __attribute__((aligned(16))) __bf16 Vs[NP * BT * 64];  // V tile, swizzled [key][d]
+    __shared__ __attribute__((aligned(16))) __bf16 Ob[NP * BLOCK_ROWS * 64];  // the block's dO rows, swizzled
 
     const int seg = blockIdx.y, head = blockIdx.z;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
@@ -1140,10 +1143,18 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
     const float sq = exp2_int(eq), so = exp2_int(eo);
     const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
     const float udp = NP == 2 ? ldexpf(1.0f, -(eo + eq)) : 1.0f;
-    V8 qh[4][NP], oh[4][NP];
+    V8 qh[4][NP];
     const int qs = start + (qvalid ? q : 0);
     split_lane_row<NP>(p.qkv + (long)qs * stride + qcol, qvalid, h, qh, sq);
-    split_lane_row<NP>(p.dcontext + (long)qs * p.hidden + qcol, qvalid, h, oh, so);
+    {
+        V8 oh[4][NP];
+        split_lane_row<NP>(p.dcontext + (long)qs * p.hidden + qcol, qvalid, h, oh, so);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int pl = 0; pl < NP; ++pl)
+                *reinterpret_cast<V8*>(Ob + pl * BLOCK_ROWS * 64 + swz(wave * WAVE_ROWS + lr, 16 * ks + 8 * h)) = oh[ks][pl];
+    }
     const float lse = qvalid ? p.lse[(long)qs * p.heads + head] : __builtin_huge_valf();
     // The row constant Σ_d dO·O (Ops.cs:408-409) from the lane's half of the row and its partner's, written
     // for the dK/dV kernel, which runs after this one.
@@ -1200,8 +1211,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_x6_kernel(Params p) {
             V8 f[NP];
             swz_row_frag<BT, NP>(Ks, lr, ks, h, f);
             s = Pieces<NP>::mma(f, qh[ks], s);
+            V8 o[NP];
             swz_row_frag<BT, NP>(Vs, lr, ks, h, f);
-            dp = Pieces<NP>::mma(f, oh[ks], dp);
+            swz_row_frag<BLOCK_ROWS, NP>(Ob, wave * WAVE_ROWS + lr, ks, h, o);
+            dp = Pieces<NP>::mma(f, o, dp);
         }
         // dP stays in its operands' scaled units (2^(eo + eq)); the row constant is taken into the same units
         // (dotu) and the units' factor into the softmax scale dsc, which the two-piece split applies
