@@ -942,7 +942,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) __bf16 Qs[NP * BT * 64];
     __shared__ __attribute__((aligned(16))) __bf16 Os[NP * BT * 64];
     __shared__ __attribute__((aligned(16))) __bf16 Vs[NP * BLOCK_ROWS * 64];
-    __shared__ float lse_s[BT], dot_s[BT];
+    __shared__ __attribute__((aligned(16))) float lse_s[BT];
+    __shared__ __attribute__((aligned(16))) float dot_s[BT];
 
     const int seg = blockIdx.y, head = blockIdx.z;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
@@ -1039,34 +1040,30 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
         // (dmul = 1) and the three-piece form multiplies in (dmul = dsc).
         float pm[16], ds[16];
         const int rel0 = qt0 + 4 * h - win.lo;  // query − lo of the lane's row r = 0
-        if (!DROP) {
-            if (subtile_inside(qt0, k0w, L, hw)) {
+        // Outside the window the exponent is −∞ and the probability exactly 0 (no branch per score).
+        if constexpr (!DROP) {
+            const bool inside = subtile_inside(qt0, k0w, L, hw);
+            // The row constants of the lane's 16 queries, rows 8u + 4h … +3 for u < 4: one b128 read per u.
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
-                    const float pr = fast_exp2(s[r] * scale_log2 - lse_s[ql]);
-                    pm[r] = pr;
-                    ds[r] = pr * (dp[r] - dot_s[ql]) * dmul;
-                }
-            } else {
+            for (int u = 0; u < 4; ++u) {
+                const f32x4 lq = *reinterpret_cast<const f32x4*>(lse_s + 8 * u + 4 * h);
+                const f32x4 dq4 = *reinterpret_cast<const f32x4*>(dot_s + 8 * u + 4 * h);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
-                    const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
-                    const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse_s[ql]) : 0.0f;
-                    pm[r] = pr;
-                    ds[r] = pr * (dp[r] - dot_s[ql]) * dmul;
+                for (int i = 0; i < 4; ++i) {
+                    const int r = 4 * u + i;
+                    const bool ok = inside || in_range(win, rel0 + 8 * u + i);
+                    pm[r] = fast_exp2(ok ? s[r] * scale_log2 - lq[i] : NEG_INF);
+                    ds[r] = pm[r] * (dp[r] - dq4[i]) * dmul;
                 }
             }
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int ql = 8 * (r >> 2) + 4 * h + (r & 3);
-                const int qq = qt0 + ql;
                 const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
-                const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse_s[ql]) : 0.0f;
+                const float pr = fast_exp2(ok ? s[r] * scale_log2 - lse_s[ql] : NEG_INF);
                 const float drop =
-                    uniform01(p.seed, attn_dropout_index(head, start + qq, key)) < p.p_drop ? 0.0f : p.keep;
+                    uniform01(p.seed, attn_dropout_index(head, start + qt0 + ql, key)) < p.p_drop ? 0.0f : p.keep;
                 const float mask = ok ? drop : 1.0f;
                 pm[r] = pr * mask;
                 ds[r] = pr * (dp[r] * mask - dot_s[ql]) * dmul;
@@ -1229,7 +1226,7 @@ __global__ __launch_bounds__(THREADS, NP == 2 ? 3 : 2) void attn_bwd_dq_x6_kerne
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
-                    const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse) : 0.0f;
+                    const float pr = fast_exp2(ok ? s[r] * scale_log2 - lse : NEG_INF);
                     ds[r] = pr * (dp[r] - dotu) * dmul;
                 }
             }
@@ -1238,7 +1235,7 @@ __global__ __launch_bounds__(THREADS, NP == 2 ? 3 : 2) void attn_bwd_dq_x6_kerne
             for (int r = 0; r < 16; ++r) {
                 const int key = kt0 + 8 * (r >> 2) + 4 * h + (r & 3);
                 const bool ok = in_range(win, rel0 + 8 * (r >> 2) + (r & 3));
-                const float pr = ok ? fast_exp2(s[r] * scale_log2 - lse) : 0.0f;
+                const float pr = fast_exp2(ok ? s[r] * scale_log2 - lse : NEG_INF);
                 const float drop =
                     uniform01(p.seed, attn_dropout_index(head, start + q, key)) < p.p_drop ? 0.0f : p.keep;
                 const float mask = ok ? drop : 1.0f;
