@@ -1431,15 +1431,20 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     a.full(kof(min(1, nt - 1)));
     b.full(kof(min(1, nt - 1)));
     lds_barrier();
-    // Branch-free body: the last two iterations reload the last stage and fill a stage no one reads.
+    // Branch-free body: the last two iterations reload the last stage and fill a stage no one reads. The
+    // next stage is committed and the one after it requested before this stage's products, so the loads have
+    // the whole stage of products to arrive (the other buffer was last read before the barrier): measured
+    // faster on these tiles, slower on the 256 × 256 ones, whose split the compiler interleaves with the
+    // products.
     for (int j = 0; j < nt; ++j) {
         const int cur = j & 1;
         const int kn = kof(min(j + 2, nt - 1));
-        mma_stage_t<NP>(smem[cur], smem[cur] + 3 * STAGE_T, acc, wm, wn, lr, half);
         a.template store<NP>(smem[cur ^ 1], tid, ps.sa);
         b.template store<NP>(smem[cur ^ 1] + 3 * STAGE_T, tid, ps.sb);
         a.full(kn);
         b.full(kn);
+        __builtin_amdgcn_sched_barrier(0);  // the loads are issued before the products
+        mma_stage_t<NP>(smem[cur], smem[cur] + 3 * STAGE_T, acc, wm, wn, lr, half);
         lds_barrier();
     }
     if constexpr (NP == 2) ps.unscale(acc);
