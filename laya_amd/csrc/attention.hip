@@ -425,6 +425,26 @@ __device__ __forceinline__ void fetch_rows(RowStage<R>& st, const float* base, l
     }
 }
 
+// The lane's own row (d = 16s + 8h … +7 for s < 4), loaded, and split later: a kernel issues its first tile's
+// loads in between, so the two loads' latencies overlap. src is always a row of the segment (a lane past the
+// segment's end reads row 0): such a lane's column of every product is its own and is never stored, so its
+// values need no zeroing, and the loads need no predicate.
+struct LaneRow {
+    f32x4 v[8];
+    __device__ __forceinline__ void load(const float* src, int h) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            v[2 * s] = ld4(src + 16 * s + 8 * h);
+            v[2 * s + 1] = ld4(src + 16 * s + 8 * h + 4);
+        }
+    }
+    template <int NP>
+    __device__ __forceinline__ void split(typename Pieces<NP>::V8 (&out)[4][NP], float sc = 1.0f) const {
+#pragma unroll
+        for (int s = 0; s < 4; ++s) split8<NP>(v[2 * s], v[2 * s + 1], out[s], sc);
+    }
+};
+
 // The lane's own row (d = 16s + 8h … +7 for s < 4), split.
 template <int NP>
 __device__ __forceinline__ void split_lane_row(const float* src, bool valid, int h,
@@ -548,8 +568,8 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
     float one = 1.0f;
     asm volatile("" : "+s"(one));  // 1.0 that the compiler cannot fold (split2h_4u)
-    V8 qh[4][NP];
-    split_lane_row<NP>(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, qvalid, h, qh, sq);
+    LaneRow qrow;
+    qrow.load(p.qkv + (long)(start + (qvalid ? q : 0)) * stride + qcol, h);
 
     int kbeg = 0, kend = L;
     int wbeg = 0, wend = L;
@@ -571,6 +591,9 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     RowStage<TILE> kst, vst;
     fetch_rows<TILE>(kst, kbase, stride, L, kbeg);
     fetch_rows<TILE>(vst, vbase, stride, L, kbeg);
+    __builtin_amdgcn_sched_barrier(0);  // the tile's loads are issued before q's split waits for q
+    V8 qh[4][NP];
+    qrow.split<NP>(qh, sq);
     for (int kt0 = kbeg; kt0 < kend; kt0 += TILE) {
         __syncthreads();
         commit_swz<TILE, NP>(kst, Ks, sq);
@@ -1140,37 +1163,13 @@ __global__ __launch_bounds__(THREADS, NP == 2 ? 3 : 2) void attn_bwd_dq_x6_kerne
     const float sq = exp2_int(eq), so = exp2_int(eo);
     const float scale_log2 = NP == 2 ? ldexpf(p.scale_log2, -2 * eq) : p.scale_log2;
     const float udp = NP == 2 ? ldexpf(1.0f, -(eo + eq)) : 1.0f;
-    V8 qh[4][NP];
+    // The lane's q, dO and context rows, then the first K/V tile: the loads overlap before anything waits.
     const int qs = start + (qvalid ? q : 0);
-    split_lane_row<NP>(p.qkv + (long)qs * stride + qcol, qvalid, h, qh, sq);
-    {
-        V8 oh[4][NP];
-        split_lane_row<NP>(p.dcontext + (long)qs * p.hidden + qcol, qvalid, h, oh, so);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-            for (int pl = 0; pl < NP; ++pl)
-                *reinterpret_cast<V8*>(Ob + pl * BLOCK_ROWS * 64 + swz(wave * WAVE_ROWS + lr, 16 * ks + 8 * h)) = oh[ks][pl];
-    }
+    LaneRow qrow, orow, crow;
+    qrow.load(p.qkv + (long)qs * stride + qcol, h);
+    orow.load(p.dcontext + (long)qs * p.hidden + qcol, h);
+    crow.load(p.context + (long)qs * p.hidden + qcol, h);
     const float lse = qvalid ? p.lse[(long)qs * p.heads + head] : __builtin_huge_valf();
-    // The row constant Σ_d dO·O (Ops.cs:408-409) from the lane's half of the row and its partner's, written
-    // for the dK/dV kernel, which runs after this one.
-    float dot = 0.0f;
-    if (qvalid) {
-        const float* dor = p.dcontext + (long)qs * p.hidden + qcol;
-        const float* cr = p.context + (long)qs * p.hidden + qcol;
-#pragma unroll
-        for (int s4 = 0; s4 < 8; ++s4) {
-            const int d0 = 16 * (s4 >> 1) + 8 * h + 4 * (s4 & 1);
-            const f32x4 a = ld4(dor + d0), b = ld4(cr + d0);
-            dot += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
-        }
-    }
-    dot += __shfl_xor(dot, 32, 64);
-    if (qvalid && h == 0) p.dots[(long)qs * p.heads + head] = dot;
-    const float dotu = NP == 2 ? ldexpf(dot, eo + eq) : dot;  // in dP's scaled units
-    const float dsc = p.scale * udp;
-    const float dmul = NP == 2 ? 1.0f : dsc;
 
     int kbeg = 0, kend = L, wbeg = 0, wend = L;
     if (hw >= 0) {
@@ -1179,17 +1178,43 @@ __global__ __launch_bounds__(THREADS, NP == 2 ? 3 : 2) void attn_bwd_dq_x6_kerne
         wbeg = max(0, q0w - hw);
         wend = min(L, q0w + WAVE_ROWS + hw);
     }
+    const float* kbase = p.qkv + (long)start * stride + kcol;
+    const float* vbase = p.qkv + (long)start * stride + vcol;
+    RowStage<BT> kst, vst;
+    fetch_rows<BT>(kst, kbase, stride, L, kbeg);
+    fetch_rows<BT>(vst, vbase, stride, L, kbeg);
+    __builtin_amdgcn_sched_barrier(0);  // the tile's loads are issued before the rows' splits wait for them
+
+    V8 qh[4][NP];
+    qrow.split<NP>(qh, sq);
+    {
+        V8 oh[4][NP];
+        orow.split<NP>(oh, so);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int pl = 0; pl < NP; ++pl)
+                *reinterpret_cast<V8*>(Ob + pl * BLOCK_ROWS * 64 + swz(wave * WAVE_ROWS + lr, 16 * ks + 8 * h)) = oh[ks][pl];
+    }
+    // The row constant Σ_d dO·O (Ops.cs:408-409) from the lane's half of the row and its partner's, written
+    // for the dK/dV kernel, which runs after this one.
+    float dot = 0.0f;
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4) {
+        const f32x4 a = orow.v[s4], b = crow.v[s4];
+        dot += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+    }
+    dot += __shfl_xor(dot, 32, 64);
+    if (qvalid && h == 0) p.dots[(long)qs * p.heads + head] = dot;
+    const float dotu = NP == 2 ? ldexpf(dot, eo + eq) : dot;  // in dP's scaled units
+    const float dsc = p.scale * udp;
+    const float dmul = NP == 2 ? 1.0f : dsc;
 
     const WindowRange win = window_range(q, L, hw);
     f32x16 dq[2];
     dq[0] = f32x16{};
     dq[1] = f32x16{};
 
-    const float* kbase = p.qkv + (long)start * stride + kcol;
-    const float* vbase = p.qkv + (long)start * stride + vcol;
-    RowStage<BT> kst, vst;
-    fetch_rows<BT>(kst, kbase, stride, L, kbeg);
-    fetch_rows<BT>(vst, vbase, stride, L, kbeg);
     for (int kt0 = kbeg; kt0 < kend; kt0 += BT) {
         __syncthreads();
         commit_swz<BT, NP>(kst, Ks, sq);
