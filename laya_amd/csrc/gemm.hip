@@ -1777,7 +1777,42 @@ __device__ __forceinline__ void wide_mma(OA& a, OB& b, int kb, int ke, int rot, 
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) acc[s][i][j] = f32x16{};
-    if (nfull > 0) {
+    if (NP == 1 && nfull > 1) {
+        // bf16 products: one MFMA per block leaves a 16-deep stage short, so each LDS buffer holds two stages
+        // (the second in the plane the single-plane form leaves free) and a barrier serves both; (a, b) and
+        // (a1, b1) are the two register stages, each requested an iteration before its commit. (Three stages
+        // per buffer, in the third free plane, measured slower.)
+        OA a1 = a;
+        OB b1 = b;
+        auto fetch_to = [&](OA& x, OB& y, int j) {
+            const int q = j + rot;
+            const int k0 = kb + (q >= nfull ? q - nfull : q) * BKQ;
+            x.full(k0);
+            y.full(k0);
+        };
+        fetch_to(a, b, 0);
+        fetch_to(a1, b1, 1);
+        a.template store<NP>(smem[0][0], tid, sa);
+        b.template store<NP>(smem[0][1], tid, sb);
+        a1.template store<NP>(smem[0][0] + STAGE_W, tid, sa);
+        b1.template store<NP>(smem[0][1] + STAGE_W, tid, sb);
+        fetch_to(a, b, min(2, nfull - 1));
+        fetch_to(a1, b1, min(3, nfull - 1));
+        lds_barrier();
+        for (int j = 0; j < nfull; j += 2) {
+            const int cur = (j >> 1) & 1;
+            mma_stage_w<NP>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
+            a.template store<NP>(smem[cur ^ 1][0], tid, sa);
+            b.template store<NP>(smem[cur ^ 1][1], tid, sb);
+            fetch_to(a, b, min(j + 4, nfull - 1));
+            if (j + 1 < nfull)  // block-uniform
+                mma_stage_w<NP>(smem[cur][0] + STAGE_W, smem[cur][1] + STAGE_W, acc, wm, wn, lr, half);
+            a1.template store<NP>(smem[cur ^ 1][0] + STAGE_W, tid, sa);
+            b1.template store<NP>(smem[cur ^ 1][1] + STAGE_W, tid, sb);
+            fetch_to(a1, b1, min(j + 5, nfull - 1));
+            lds_barrier();
+        }
+    } else if (nfull > 0) {
         fetch(0);
         a.template store<NP>(smem[0][0], tid, sa);
         b.template store<NP>(smem[0][1], tid, sb);
