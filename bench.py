@@ -61,11 +61,15 @@ def mfma_peaks(name: str):
     Kernels named *_x6 / *_x6w / *_x6t compute fp32 products from exact three-piece bf16 splits: six bf16
     MFMA products per fp32 one, so their fp32-equivalent peak is the bf16 peak over six. *_h2w / *_h2t
     compute them from two-piece fp16 splits of power-of-two-scaled operands: three fp16 MFMA products per
-    fp32 one (fp16 and bf16 share the 2.5 PFLOP/s dense peak), peak over three. *_bf16 / *_bf16w run bf16
-    operands (one product each). The rest run the fp32 matrix cores."""
-    base = name[:-1] if name.endswith(("_x6w", "_x6t", "_bf16w", "_h2w", "_h2t", "_h2q")) else name
+    fp32 one (fp16 and bf16 share the 2.5 PFLOP/s dense peak), peak over three; *_h2b1 / *_h2b1w / *_h2b1t
+    the same with bf16-valued weights, which are one fp16 piece: two products, peak over two. *_bf16 /
+    *_bf16w run bf16 operands (one product each). The rest run the fp32 matrix cores."""
+    base = name[:-1] if name.endswith(("_x6w", "_x6t", "_bf16w", "_h2w", "_h2t", "_h2q", "_h2b1w",
+                                       "_h2b1t")) else name
     if base.endswith("_x6"):
         return PEAK_BF16_MFMA / 6, 6.0
+    if base.endswith("_h2b1"):
+        return PEAK_BF16_MFMA / 2, 2.0
     if base.endswith("_h2"):
         return PEAK_BF16_MFMA / 3, 3.0
     if base.endswith("_bf16"):

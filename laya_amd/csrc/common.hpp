@@ -279,6 +279,9 @@ enum class GemmEpilogue {
 struct AmaxRef {
     unsigned* word = nullptr;
     unsigned char* known = nullptr;
+    // The operand's values are bf16 values held in fp32 (a bf16-weights product's weights): a two-piece
+    // product takes them as one fp16 piece.
+    bool bf16 = false;
 };
 
 void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K, const float* A, long lda,

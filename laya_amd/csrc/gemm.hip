@@ -69,6 +69,9 @@ struct GemmParams {
     const unsigned* amax_b;
     // Optional magnitude word group of C, folded in by the two-piece kernels' epilogues (max|stored value|).
     unsigned* amax_c;
+    // Two-piece NT products: B's values are bf16 values (fp32 holding a bf16), so sb·B is one fp16 piece
+    // (see split1h_4) and the kernels that honour it skip B's low plane and its products.
+    int b_one;
 };
 
 // ------------------------------------------------------------------------------ shared pieces
@@ -640,21 +643,30 @@ __device__ __forceinline__ void store_x3(const OperandH<KIND>& op, __bf16* lds0,
     }
 }
 
-// The two-piece form of store_x3 for float4 operands: the two fp16 planes of sc·x.
+// The two-piece form of store_x3 for float4 operands: the two fp16 planes of sc·x (ONE: the hi plane only,
+// for bf16-valued operands).
+template <bool ONE = false>
 __device__ __forceinline__ void store_x2(const OperandH<KVEC>& op, __bf16* lds0, __bf16* lds1, int tid, float sc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        f16x4 hi, lo;
-        split2h_4(op.reg[i], sc, hi, lo);
         const int o = ((tid >> 3) + 32 * i) * KPADH + ((tid & 7) << 2);
-        *reinterpret_cast<f16x4*>(lds0 + o) = hi;
-        *reinterpret_cast<f16x4*>(lds1 + o) = lo;
+        if constexpr (ONE) {
+            *reinterpret_cast<f16x4*>(lds0 + o) = split1h_4(op.reg[i], sc);
+        } else {
+            f16x4 hi, lo;
+            split2h_4(op.reg[i], sc, hi, lo);
+            *reinterpret_cast<f16x4*>(lds0 + o) = hi;
+            *reinterpret_cast<f16x4*>(lds1 + o) = lo;
+        }
     }
 }
 
-// The two-piece form of mma_stage_x6: two fp16 planes, three products per block, the smallest first.
+// The two-piece form of mma_stage_x6: two fp16 planes, three products per block, the smallest first (B1: B
+// in one piece, two products).
+template <bool B1 = false>
 __device__ __forceinline__ void mma_stage_x2(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2], int wm, int wn,
                                              int lr, int half) {
+    constexpr int BP = B1 ? 1 : 2;
 #pragma unroll
     for (int ks = 0; ks < BK; ks += 16) {
         const int k = ks + 8 * half;
@@ -664,7 +676,8 @@ __device__ __forceinline__ void mma_stage_x2(const __bf16* A, const __bf16* B, f
 #pragma unroll
             for (int pl = 0; pl < 2; ++pl) {
                 a[i][pl] = *reinterpret_cast<const f16x8*>(A + pl * STAGE_H + (wm * 64 + 32 * i + lr) * KPADH + k);
-                b[i][pl] = *reinterpret_cast<const f16x8*>(B + pl * STAGE_H + (wn * 64 + 32 * i + lr) * KPADH + k);
+                if (pl < BP)
+                    b[i][pl] = *reinterpret_cast<const f16x8*>(B + pl * STAGE_H + (wn * 64 + 32 * i + lr) * KPADH + k);
             }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -672,7 +685,7 @@ __device__ __forceinline__ void mma_stage_x2(const __bf16* A, const __bf16* B, f
             for (int j = 0; j < 2; ++j) {
                 f32x16 c = acc[i][j];
                 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][1], b[j][0], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][0], b[j][1], c, 0, 0, 0);
+                if constexpr (!B1) c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][0], b[j][1], c, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i][0], b[j][0], c, 0, 0, 0);
                 acc[i][j] = c;
             }
@@ -708,8 +721,8 @@ __device__ __forceinline__ void mma_stage_x6(const __bf16* A, const __bf16* B, f
     }
 }
 
-// NP = 2 (float4 operands only): two-piece products with the operands' scales sa, sb.
-template <int AOP, int BOP, int NP = 3>
+// NP = 2 (float4 operands only): two-piece products with the operands' scales sa, sb (B1: B in one piece).
+template <int AOP, int BOP, int NP = 3, bool B1 = false>
 __device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord& c, __bf16 (*smem)[3 * STAGE_H],
                                             f32x16 (&acc)[2][2], float sa = 1.0f, float sb = 1.0f) {
     static_assert(NP == 3 || (AOP == KVEC && BOP == KVEC), "two-piece products take float4 operands");
@@ -741,7 +754,7 @@ __device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord
         __syncthreads();
         if constexpr (NP == 2) {
             store_x2(a, smem[0], smem[0] + STAGE_H, tid, sa);
-            store_x2(b, smem[1], smem[1] + STAGE_H, tid, sb);
+            store_x2<B1>(b, smem[1], smem[1] + STAGE_H, tid, sb);
         } else {
             store_x3<AOP>(a, smem[0], smem[0] + STAGE_H, smem[0] + 2 * STAGE_H, tid);
             store_x3<BOP>(b, smem[1], smem[1] + STAGE_H, smem[1] + 2 * STAGE_H, tid);
@@ -749,7 +762,7 @@ __device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord
         __syncthreads();
         if (j + 1 < ntiles) fetch(j + 1);
         if constexpr (NP == 2)
-            mma_stage_x2(smem[0], smem[1], acc, wm, wn, lr, half);
+            mma_stage_x2<B1>(smem[0], smem[1], acc, wm, wn, lr, half);
         else
             mma_stage_x6(smem[0], smem[1], acc, wm, wn, lr, half);
     }
@@ -971,14 +984,16 @@ struct OperandW {
         for (int i = 0; i < 2; ++i)
             reg[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off[i], k0 * 4, 0));
     }
-    // NP = 3: the three split planes; NP = 2: the two fp16 planes of s·x; NP = 1: one plane of the values
-    // rounded to bf16.
-    template <int NP = 3>
+    // NP = 3: the three split planes; NP = 2: the two fp16 planes of s·x (ONE: the hi plane only, for
+    // bf16-valued operands); NP = 1: one plane of the values rounded to bf16.
+    template <int NP = 3, bool ONE = false>
     __device__ __forceinline__ void store(__bf16* lds, int tid, float sc = 1.0f) const {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int o = ((tid >> 2) + 128 * i) * KPADQ + ((tid & 3) << 2);
-            if constexpr (NP == 2) {
+            if constexpr (NP == 2 && ONE) {
+                *reinterpret_cast<f16x4*>(lds + o) = split1h_4(reg[i], sc);
+            } else if constexpr (NP == 2) {
                 f16x4 hi, lo;
                 split2h_4(reg[i], sc, hi, lo);
                 *reinterpret_cast<f16x4*>(lds + o) = hi;
@@ -1014,7 +1029,7 @@ struct OperandW16 {
         for (int i = 0; i < 2; ++i) reg[i] = __builtin_amdgcn_raw_buffer_load_b64(rsrc, off[i], k0 * 2, 0);
     }
     __device__ __forceinline__ void tail(int k0, int) { full(k0); }
-    template <int NP = 1>
+    template <int NP = 1, bool = false>
     __device__ __forceinline__ void store(__bf16* lds, int tid, float = 1.0f) const {
         static_assert(NP == 1, "a bf16 copy feeds bf16 products");
 #pragma unroll
@@ -1043,9 +1058,20 @@ __device__ __forceinline__ void mma3h(const f16x8 (&a)[2], const f16x8 (&b)[2], 
     acc = c;
 }
 
-// Two-piece fp16 stage: the same fragment walk as mma_stage_w over two fp16 planes, three products each.
+// The two products of a two-piece block whose B is one piece (bf16-valued), smallest first.
+__device__ __forceinline__ void mma2h(const f16x8 (&a)[2], const f16x8 (&b)[2], f32x16& acc) {
+    f32x16 c = acc;
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], b[0], c, 0, 0, 0);
+    acc = c;
+}
+
+// Two-piece fp16 stage: the same fragment walk as mma_stage_w over two fp16 planes, three products each
+// (B1: B's one plane, two products each).
+template <bool B1 = false>
 __device__ __forceinline__ void mma_stage_w2(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2][2], int wm, int wn,
                                              int lr, int half) {
+    constexpr int BP = B1 ? 1 : 2;
     const _Float16* Ah = reinterpret_cast<const _Float16*>(A);
     const _Float16* Bh = reinterpret_cast<const _Float16*>(B);
     f16x8 b[2][2], a[2][2];
@@ -1058,25 +1084,30 @@ __device__ __forceinline__ void mma_stage_w2(const __bf16* A, const __bf16* B, f
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl)
+        for (int pl = 0; pl < BP; ++pl)
             b[j][pl] = *reinterpret_cast<const f16x8*>(Bh + pl * STAGE_W + (wn * 64 + 32 * j + lr) * KPADQ + 8 * half);
     rd_a(0, a[0]);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         if (g + 1 < 4) rd_a(g + 1, a[(g + 1) & 1]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) mma3h(a[g & 1], b[j], acc[g >> 1][g & 1][j]);
+        for (int j = 0; j < 2; ++j) {
+            if constexpr (B1)
+                mma2h(a[g & 1], b[j], acc[g >> 1][g & 1][j]);
+            else
+                mma3h(a[g & 1], b[j], acc[g >> 1][g & 1][j]);
+        }
     }
 }
 
 // One 16-deep stage of a wave's two subtiles: B fragments once, A fragments one 32-row group ahead.
 // NP = 3: six piece products per block (split products); NP = 2: three fp16 piece products (two-piece
-// products); NP = 1: one bf16 product.
-template <int NP = 3>
+// products; B1: B in one piece, two); NP = 1: one bf16 product.
+template <int NP = 3, bool B1 = false>
 __device__ __forceinline__ void mma_stage_w(const __bf16* A, const __bf16* B, f32x16 (&acc)[2][2][2], int wm, int wn,
                                             int lr, int half) {
     if constexpr (NP == 2) {
-        mma_stage_w2(A, B, acc, wm, wn, lr, half);
+        mma_stage_w2<B1>(A, B, acc, wm, wn, lr, half);
         return;
     }
     bf16x8 b[2][3], a[2][3];
@@ -1123,12 +1154,13 @@ struct WideK<true> {
 };
 
 
-// NP = 3: the split (fp32) product; NP = 2: the two-piece fp16 product (fp32-accurate, scaled operands);
-// NP = 1: the bf16 product, with AH / BH reading A / B from their bf16 copies.
-template <int MODE, int NP = 3, bool AH = false, bool BH = false>
+// NP = 3: the split (fp32) product; NP = 2: the two-piece fp16 product (fp32-accurate, scaled operands; B1:
+// B bf16-valued, in one piece); NP = 1: the bf16 product, with AH / BH reading A / B from their bf16 copies.
+template <int MODE, int NP = 3, bool AH = false, bool BH = false, bool B1 = false>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     static_assert(MODE == STORE || MODE == STORE_ROPE, "whole-K NT epilogues");
     static_assert(NP == 1 || !(AH || BH), "bf16 copies feed bf16 products");
+    static_assert(NP == 2 || !B1, "one-piece B is a two-piece product's");
     PairScales ps;
     if constexpr (NP == 2) ps = PairScales(p.amax_a, p.amax_b);
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][2][3 * STAGE_W];  // [stage][operand]
@@ -1162,7 +1194,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     a.full(kof(0));
     b.full(kof(0));
     a.template store<NP>(smem[0][0], tid, ps.sa);
-    b.template store<NP>(smem[0][1], tid, ps.sb);
+    b.template store<NP, B1>(smem[0][1], tid, ps.sb);
     a.full(kof(min(1, nt - 1)));
     b.full(kof(min(1, nt - 1)));
     lds_barrier();
@@ -1170,9 +1202,9 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     for (int j = 0; j < nt; ++j) {
         const int cur = j & 1;
         const int kn = kof(min(j + 2, nt - 1));
-        mma_stage_w<NP>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
+        mma_stage_w<NP, B1>(smem[cur][0], smem[cur][1], acc, wm, wn, lr, half);
         a.template store<NP>(smem[cur ^ 1][0], tid, ps.sa);
-        b.template store<NP>(smem[cur ^ 1][1], tid, ps.sb);
+        b.template store<NP, B1>(smem[cur ^ 1][1], tid, ps.sb);
         a.full(kn);
         b.full(kn);
         lds_barrier();
@@ -1337,9 +1369,11 @@ struct OperandT {
     }
 };
 
-// The two-piece fp16 form of mma_stage_t: two fp16 planes, three products per block.
+// The two-piece fp16 form of mma_stage_t: two fp16 planes, three products per block (B1: B's one plane, two).
+template <bool B1 = false>
 __device__ __forceinline__ void mma_stage_t2(const __bf16* A, const __bf16* B, f32x16 (&acc)[3][2], int wm, int wn,
                                              int lr, int half) {
+    constexpr int BP = B1 ? 1 : 2;
     const _Float16* Ah = reinterpret_cast<const _Float16*>(A);
     const _Float16* Bh = reinterpret_cast<const _Float16*>(B);
     f16x8 b[2][2], a[2][2];
@@ -1352,23 +1386,28 @@ __device__ __forceinline__ void mma_stage_t2(const __bf16* A, const __bf16* B, f
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int pl = 0; pl < 2; ++pl)
+        for (int pl = 0; pl < BP; ++pl)
             b[j][pl] = *reinterpret_cast<const f16x8*>(Bh + pl * STAGE_W + (wn * 64 + 32 * j + lr) * KPADQ + 8 * half);
     rd_a(0, a[0]);
 #pragma unroll
     for (int g = 0; g < 3; ++g) {
         if (g + 1 < 3) rd_a(g + 1, a[(g + 1) & 1]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) mma3h(a[g & 1], b[j], acc[g][j]);
+        for (int j = 0; j < 2; ++j) {
+            if constexpr (B1)
+                mma2h(a[g & 1], b[j], acc[g][j]);
+            else
+                mma3h(a[g & 1], b[j], acc[g][j]);
+        }
     }
 }
 
 // One 16-deep stage of a wave's 96 x 64: B fragments once, A fragments one 32-row group ahead.
-template <int NP = 3>
+template <int NP = 3, bool B1 = false>
 __device__ __forceinline__ void mma_stage_t(const __bf16* A, const __bf16* B, f32x16 (&acc)[3][2], int wm, int wn,
                                             int lr, int half) {
     if constexpr (NP == 2) {
-        mma_stage_t2(A, B, acc, wm, wn, lr, half);
+        mma_stage_t2<B1>(A, B, acc, wm, wn, lr, half);
         return;
     }
     bf16x8 b[2][3], a[2][3];
@@ -1392,10 +1431,11 @@ __device__ __forceinline__ void mma_stage_t(const __bf16* A, const __bf16* B, f3
     }
 }
 
-// NP = 3: split products; NP = 2: two-piece fp16 products.
-template <int MODE, bool RES, int NP = 3>
+// NP = 3: split products; NP = 2: two-piece fp16 products (B1: B bf16-valued, in one piece).
+template <int MODE, bool RES, int NP = 3, bool B1 = false>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     static_assert(MODE == STORE || (MODE == STORE_ROPE && !RES), "whole-K NT epilogues");
+    static_assert(NP == 2 || !B1, "one-piece B is a two-piece product's");
     PairScales ps;
     if constexpr (NP == 2) ps = PairScales(p.amax_a, p.amax_b);
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * (STAGE_T + STAGE_W)];  // [stage][A planes, B planes]
@@ -1427,7 +1467,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     a.full(kof(0));
     b.full(kof(0));
     a.template store<NP>(smem[0], tid, ps.sa);
-    b.template store<NP>(smem[0] + 3 * STAGE_T, tid, ps.sb);
+    b.template store<NP, B1>(smem[0] + 3 * STAGE_T, tid, ps.sb);
     a.full(kof(min(1, nt - 1)));
     b.full(kof(min(1, nt - 1)));
     lds_barrier();
@@ -1440,11 +1480,11 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
         const int cur = j & 1;
         const int kn = kof(min(j + 2, nt - 1));
         a.template store<NP>(smem[cur ^ 1], tid, ps.sa);
-        b.template store<NP>(smem[cur ^ 1] + 3 * STAGE_T, tid, ps.sb);
+        b.template store<NP, B1>(smem[cur ^ 1] + 3 * STAGE_T, tid, ps.sb);
         a.full(kn);
         b.full(kn);
         __builtin_amdgcn_sched_barrier(0);  // the loads are issued before the products
-        mma_stage_t<NP>(smem[cur], smem[cur] + 3 * STAGE_T, acc, wm, wn, lr, half);
+        mma_stage_t<NP, B1>(smem[cur], smem[cur] + 3 * STAGE_T, acc, wm, wn, lr, half);
         lds_barrier();
     }
     if constexpr (NP == 2) ps.unscale(acc);
@@ -1472,14 +1512,16 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
 
 // The fp32 product from bf16 pieces (NP = 3) or, for float4 operands, two-piece fp16 products (NP = 2);
 // accumulators in the k-contiguous layout whatever the operands' form.
-template <int AOP, int BOP, int MODE, bool RES, int NP = 3>
+// B1 (NP = 2): B bf16-valued, in one piece.
+template <int AOP, int BOP, int MODE, bool RES, int NP = 3, bool B1 = false>
 __global__ __launch_bounds__(THREADS, 2) void gemm_x6_kernel(GemmParams p) {
+    static_assert(NP == 2 || !B1, "one-piece B is a two-piece product's");
     __shared__ __attribute__((aligned(16))) __bf16 smem[2][3 * STAGE_H];
     PairScales ps;
     if constexpr (NP == 2) ps = PairScales(p.amax_a, p.amax_b);
     const TileCoord c = tile_coord(p, xcd_logical_block());
     f32x16 acc[2][2];
-    tile_mma_x6<AOP, BOP, NP>(p, c, smem, acc, ps.sa, ps.sb);
+    tile_mma_x6<AOP, BOP, NP, B1>(p, c, smem, acc, ps.sa, ps.sb);
     if constexpr (NP == 2) ps.unscale(acc);
     tile_store<true, true, MODE, RES>(p, c, acc);
 }
@@ -2416,12 +2458,24 @@ const unsigned* operand_amax(laya_ctx* ctx, AmaxRef r, int slot, const float* x,
 void prepare_pair_nt(laya_ctx* ctx, GemmParams& p, AmaxRef ra, AmaxRef rb) {
     p.amax_a = operand_amax(ctx, ra, 0, p.A, p.M, p.K, p.lda);
     p.amax_b = operand_amax(ctx, rb, 1, p.B, p.N, p.K, p.ldb);
+    p.b_one = rb.bf16 ? 1 : 0;
 }
 
 void launch_tall(laya_ctx* ctx, GemmParams p) {
     p.tiles_m = (p.M + TM - 1) / TM;
     p.tiles_n = (p.N + WT - 1) / WT;
     const dim3 g(p.tiles_m * p.tiles_n), b(WT_THREADS);
+    if (p.amax_a && p.b_one) {
+        profile_rename("gemm_nt_h2b1t");
+        if (p.mode == STORE_ROPE)
+            LAYA_LAUNCH((gemm_x6t_kernel<STORE_ROPE, false, 2, true>), g, b, 0, ctx->stream, p);
+        else if (p.R)
+            LAYA_LAUNCH((gemm_x6t_kernel<STORE, true, 2, true>), g, b, 0, ctx->stream, p);
+        else
+            LAYA_LAUNCH((gemm_x6t_kernel<STORE, false, 2, true>), g, b, 0, ctx->stream, p);
+        check_launch("gemm_x6t_kernel");
+        return;
+    }
     if (p.amax_a) {
         profile_rename("gemm_nt_h2t");
         if (p.mode == STORE_ROPE)
@@ -2447,9 +2501,13 @@ void launch_wide(laya_ctx* ctx, GemmParams p) {
     p.tiles_n = (p.N + WT - 1) / WT;
     const dim3 g(((p.M + WT - 1) / WT) * p.tiles_n), b(WT_THREADS);
     if (p.amax_a) {
-        profile_rename("gemm_nt_h2w");
-        if (p.mode == STORE_ROPE)
+        profile_rename(p.b_one ? "gemm_nt_h2b1w" : "gemm_nt_h2w");
+        if (p.mode == STORE_ROPE && p.b_one)
+            LAYA_LAUNCH((gemm_x6w_kernel<STORE_ROPE, 2, false, false, true>), g, b, 0, ctx->stream, p);
+        else if (p.mode == STORE_ROPE)
             LAYA_LAUNCH((gemm_x6w_kernel<STORE_ROPE, 2>), g, b, 0, ctx->stream, p);
+        else if (p.b_one)
+            LAYA_LAUNCH((gemm_x6w_kernel<STORE, 2, false, false, true>), g, b, 0, ctx->stream, p);
         else
             LAYA_LAUNCH((gemm_x6w_kernel<STORE, 2>), g, b, 0, ctx->stream, p);
         check_launch("gemm_x6w_kernel");
@@ -2493,11 +2551,15 @@ template <int AOP, int BOP> void launch_x(laya_ctx* ctx, const GemmParams& p, in
     const dim3 g(blocks), b(THREADS);
     if constexpr (AOP == KVEC && BOP == KVEC) {
         if (p.amax_a) {  // two-piece products (NT, float4 operands)
-            profile_rename("gemm_nt_h2");
+            profile_rename(p.mode == STORE && p.b_one ? "gemm_nt_h2b1" : "gemm_nt_h2");
             switch (p.mode) {
                 case STORE:
-                    if (p.R)
+                    if (p.R && p.b_one)
+                        LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE, true, 2, true>), g, b, 0, ctx->stream, p);
+                    else if (p.R)
                         LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE, true, 2>), g, b, 0, ctx->stream, p);
+                    else if (p.b_one)
+                        LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE, false, 2, true>), g, b, 0, ctx->stream, p);
                     else
                         LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE, false, 2>), g, b, 0, ctx->stream, p);
                     break;

@@ -224,7 +224,13 @@ struct laya_model {
     laya::AmaxRef word(size_t k) {
         return amax_words ? laya::AmaxRef{amax_words + k * laya::AMAX_GROUP, &amax_known[k]} : laya::AmaxRef{};
     }
-    laya::AmaxRef wref(int i) { return i < 0 ? laya::AmaxRef{} : word(i); }
+    // A weight's word; with bf16 weights the products read PW, whose values are bf16 values.
+    laya::AmaxRef wref(int i) {
+        if (i < 0) return laya::AmaxRef{};
+        laya::AmaxRef r = word(i);
+        r.bf16 = bf16_weights && PW && r.word;
+        return r;
+    }
     laya::AmaxRef aref(int site) { return word(params.size() + site); }
     laya::AmaxRef dref(int site) { return word(params.size() + amax_sites() + site); }
     // The word a producing kernel folds its output into, when a product of the classes `bits` will read it

@@ -49,6 +49,14 @@ __device__ __forceinline__ void split2h_4(f32x4 x, float s, f16x4& hi, f16x4& lo
     lo = __builtin_convertvector(v - __builtin_convertvector(hi, f32x4), f16x4);
 }
 
+// One fp16 piece of s·x for bf16-valued x (an fp32 whose low 16 bits are zero), s the operand's scale as
+// above: s·x carries 8 significant bits, so f16(s·x) is s·x exactly wherever |s·x| ≥ 2⁻¹⁷ (fp16's
+// subnormal spacing 2⁻²⁴ times 2⁷), i.e. for every element above 2⁻³¹ of the operand's largest; below
+// that it is within 2⁻²⁵, 2⁻³⁹ of the largest, the order of the two-piece form's own bound there. The
+// two-piece form's lo piece is then zero and its products with it add nothing: dropping them leaves the
+// same sums.
+__device__ __forceinline__ f16x4 split1h_4(f32x4 x, float s) { return __builtin_convertvector(x * s, f16x4); }
+
 // The same split at unit scale: hi = f16(x), lo = f16(x − hi). `one` is 1.0 held where the compiler cannot
 // fold it, so the exact remainder x·1 − hi is one fused mix-precision multiply-add on the fp16 hi rather
 // than a convert back to fp32 and a subtraction.

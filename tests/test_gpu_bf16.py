@@ -229,6 +229,57 @@ def test_bf16_at_64_packed_zipf_sequences(ctx):
     _bf16_at_full_size(synthetic_batch(rng, lengths, opts, qt, 50368, zipf=1.1), 61)
 
 
+@pytest.mark.parametrize("shape", ["32x1024", "64 packed zipf"])
+def test_bf16_weights_one_piece_products_equal_two_piece_ones(shape):
+    """With bf16 weights the forward's two-piece products take each weight as one fp16 piece and skip the
+    products of the low piece: a bf16 value scaled into fp16's range is exact there, so that piece is zero and
+    its products add nothing. At the bf16 workloads' full sizes (the 256 x 256, 192 x 256 and 128 x 128
+    kernels), under their policy (fp32-accurate forward, bf16 backward products), the step with bf16 weights
+    on equals bit for bit the step of the same model with bf16 weights off, its fp32 weights already holding
+    the bf16 values (products carrying both pieces)."""
+    from laya_amd.batch import synthetic_batch
+    from laya_amd.config import modernbert_base
+    from laya_amd.device import Context
+    from laya_amd.model import TrainableDecisionModel, synthetic_params
+    print(f"bf16 weights, one-piece vs two-piece forward products: {shape}", flush=True)
+    rng = np.random.default_rng(101)
+    if shape == "32x1024":
+        lengths = [1024] * 32
+        batch = synthetic_batch(rng, lengths, *_heads(32), 50368)
+    else:
+        lengths = rng.integers(16, 2049, 64)
+        batch = synthetic_batch(rng, lengths, *_heads(64), 50368, zipf=1.1)
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+    c = Context(0)
+    try:
+        c.set_matmul_precision("bf16-backward")
+        m = TrainableDecisionModel(modernbert_base(), c)
+        params = synthetic_params(m.shapes, 101)
+        pw = _product_weights(m.shapes)
+        m.set_params({n: (bf16(v) if n in pw else v) for n, v in params.items()})
+        m.head_dropout = 0.1
+        steps, ran = [], []
+        for on in (True, False):
+            m.set_bf16_weights(on)
+            m.zero_gradients()
+            c.profile_begin()
+            logits = m.forward(batch, training=True, seed=7)
+            ran.append(sorted(n for n in c.profile_end() if n.startswith("gemm_nt_h2")))
+            _, g = oracle.cross_entropy(batch.n_options, logits, targets, 1.0, float(batch.n_items))
+            m.backward(g)
+            steps.append((logits, {n: m.grad(n) for n in m.names if m.has_grad(n)}))
+        print(f"forward products: {ran[0]} against {ran[1]}", flush=True)
+        assert "gemm_nt_h2b1w" in ran[0] and not any("b1" in n for n in ran[1]), ran
+        (l1, g1), (l2, g2) = steps
+        np.testing.assert_array_equal(l1, l2)
+        for n in g1:
+            np.testing.assert_array_equal(g1[n], g2[n], err_msg=n)
+        print(f"{shape}: logits and {len(g1)} gradients equal bit for bit", flush=True)
+        m.close()
+    finally:
+        c.close()
+
+
 def _copies_step(m, batch, d, seed=5):
     m.zero_gradients()
     logits = m.forward(batch, training=True, seed=seed)
