@@ -30,7 +30,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int THREADS = 256;
 constexpr int WAVE_ROWS = 32;   // queries (or keys) owned by one wave
-constexpr int BLOCK_ROWS = 128; // 4 waves
+constexpr int BLOCK_ROWS = ATTENTION_BLOCK_ROWS;  // 4 waves
 constexpr int TILE = 64;        // rows of the streamed operand per LDS tile
 constexpr float NEG_INF = -__builtin_huge_valf();
 constexpr float LAZY_RESCALE = 8.0f;  // log2 headroom of the split-product forward's running max
@@ -55,7 +55,25 @@ struct Params {
     // take their power-of-two scales.
     const unsigned* amax_qkv;
     const unsigned* amax_do;
+    // Optional block list (AttentionArgs::blocks): the launch is one-dimensional, heads fastest.
+    const int* blocks;
 };
+
+// A workgroup's segment, head and first row (query or key). With a block list, workgroup i takes entry
+// i / heads (segment << 16 | row block), head i mod heads: every workgroup has rows, the longest segments'
+// blocks are dispatched first, and the row blocks of one (segment, head) fall heads apart in dispatch order
+// (on two XCDs for 12 heads rather than all eight). Without one, the grid is (row block, segment, head).
+struct BlockCoord {
+    int seg, head, row0;
+};
+__device__ __forceinline__ BlockCoord block_coord(const Params& p) {
+    if (p.blocks) {
+        const unsigned i = blockIdx.x / (unsigned)p.heads;
+        const int e = p.blocks[i];
+        return {e >> 16, (int)(blockIdx.x - i * (unsigned)p.heads), (e & 0xffff) * BLOCK_ROWS};
+    }
+    return {(int)blockIdx.y, (int)blockIdx.z, (int)blockIdx.x * BLOCK_ROWS};
+}
 
 template <int D> struct Shape {
     static constexpr int G = D / 8;     // float4 groups per lane (the lane's half of d)
@@ -191,9 +209,10 @@ __global__ __launch_bounds__(THREADS) void attn_fwd_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) float Ks[TILE * S::KS];
     __shared__ __attribute__((aligned(16))) float Vs[TILE * S::VS];
 
-    const int seg = blockIdx.y, head = blockIdx.z;
+    const BlockCoord bc = block_coord(p);
+    const int seg = bc.seg, head = bc.head;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
-    const int qb0 = blockIdx.x * BLOCK_ROWS;
+    const int qb0 = bc.row0;
     if (qb0 >= L) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
     const int q0w = qb0 + wave * WAVE_ROWS;
@@ -539,9 +558,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_fwd_x6_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) __bf16 Ks[NP * TILE * 64];  // K tile, swizzled [key][d]
     __shared__ __attribute__((aligned(16))) __bf16 Vs[NP * TILE * 64];  // V tile, swizzled [key][d]
 
-    const int seg = blockIdx.y, head = blockIdx.z;
+    const BlockCoord bc = block_coord(p);
+    const int seg = bc.seg, head = bc.head;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
-    const int qb0 = blockIdx.x * BLOCK_ROWS;
+    const int qb0 = bc.row0;
     if (qb0 >= L) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
     const int q0w = qb0 + wave * WAVE_ROWS;
@@ -724,9 +744,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_kernel(Params p) {
     __shared__ float lse_s[TILE], dot_s[TILE];
     __shared__ __attribute__((aligned(16))) float Ks[BLOCK_ROWS * S::KS];  // the block's keys
 
-    const int seg = blockIdx.y, head = blockIdx.z;
+    const BlockCoord bc = block_coord(p);
+    const int seg = bc.seg, head = bc.head;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
-    const int kb0 = blockIdx.x * BLOCK_ROWS;
+    const int kb0 = bc.row0;
     if (kb0 >= L) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
     const int k0w = kb0 + wave * WAVE_ROWS;
@@ -855,9 +876,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dq_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) float Ks[TILE * S::KS];
     __shared__ __attribute__((aligned(16))) float Vs[TILE * S::KS];
 
-    const int seg = blockIdx.y, head = blockIdx.z;
+    const BlockCoord bc = block_coord(p);
+    const int seg = bc.seg, head = bc.head;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
-    const int qb0 = blockIdx.x * BLOCK_ROWS;
+    const int qb0 = bc.row0;
     if (qb0 >= L) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
     const int q0w = qb0 + wave * WAVE_ROWS;
@@ -968,9 +990,10 @@ __global__ __launch_bounds__(THREADS, 2) void attn_bwd_dkv_x6_kernel(Params p) {
     __shared__ __attribute__((aligned(16))) float lse_s[BT];
     __shared__ __attribute__((aligned(16))) float dot_s[BT];
 
-    const int seg = blockIdx.y, head = blockIdx.z;
+    const BlockCoord bc = block_coord(p);
+    const int seg = bc.seg, head = bc.head;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
-    const int kb0 = blockIdx.x * BLOCK_ROWS;
+    const int kb0 = bc.row0;
     if (kb0 >= L) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
     const int k0w = kb0 + wave * WAVE_ROWS;
@@ -1137,9 +1160,10 @@ __global__ __launch_bounds__(THREADS, NP == 2 ? 3 : 2) void attn_bwd_dq_x6_kerne
     __shared__ __attribute__((aligned(16))) __bf16 Vs[NP * BT * 64];  // V tile, swizzled [key][d]
     __shared__ __attribute__((aligned(16))) __bf16 Ob[NP * BLOCK_ROWS * 64];  // the block's dO rows, swizzled
 
-    const int seg = blockIdx.y, head = blockIdx.z;
+    const BlockCoord bc = block_coord(p);
+    const int seg = bc.seg, head = bc.head;
     const int start = p.seg_start[seg], L = p.seg_len[seg];
-    const int qb0 = blockIdx.x * BLOCK_ROWS;
+    const int qb0 = bc.row0;
     if (qb0 >= L) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, h = lane >> 5, lr = lane & 31;
     const int q0w = qb0 + wave * WAVE_ROWS;
@@ -1326,6 +1350,7 @@ Params make_params(const AttentionArgs& a) {
     p.qkv = a.qkv;
     p.seg_start = a.seg_start;
     p.seg_len = a.seg_len;
+    p.blocks = a.blocks;
     p.hidden = a.hidden;
     p.heads = a.heads;
     p.half_window = a.half_window;
@@ -1355,11 +1380,20 @@ const float* rotated_qkv(laya_ctx* ctx, const AttentionArgs& a) {
     return out;
 }
 
+// The attention kernels' grid: one workgroup per listed block and head, else (row blocks, segments, heads).
+dim3 block_grid(const AttentionArgs& a) {
+    if (a.blocks) return dim3((unsigned)(a.n_blocks * a.heads));
+    return dim3((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
+}
+
 void check_args(const AttentionArgs& a) {
     LAYA_REQUIRE(a.heads > 0 && a.hidden == a.heads * a.head_dim, "attention: hidden must equal heads × head_dim");
     LAYA_REQUIRE(a.head_dim == 32 || a.head_dim == 64, "attention: head_dim must be 32 or 64");
     LAYA_REQUIRE(a.max_len >= 0 && a.nseg >= 0, "attention: negative size");
     LAYA_REQUIRE(a.heads <= 65535 && a.nseg <= 65535, "attention: too many heads or segments for one launch");
+    LAYA_REQUIRE(!a.blocks || (a.n_blocks > 0 && (long)a.n_blocks * a.heads < (1L << 31) &&
+                               (a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS <= 65536),
+                 "attention: bad block list");
     LAYA_REQUIRE(a.p_drop >= 0.0f && a.p_drop < 1.0f, "attention: dropout must be in [0, 1)");
     LAYA_REQUIRE(a.cos_table == nullptr || a.positions >= a.max_len, "attention: rotary table shorter than max_len");
     // The split-product kernels address a segment's rows through 32-bit buffer offsets.
@@ -1389,7 +1423,7 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
     p.context = context;
     p.lse = lse;
     p.amax = amax;
-    dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
+    const dim3 grid = block_grid(a);
     const bool split = a.head_dim == 64 && split_attention(ctx);
     const bool pair = split && ctx->attention_pair;
     p.context16 = split ? context16 : nullptr;
@@ -1433,7 +1467,7 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     p.dots = dots;
     const long total = (long)rows * a.hidden;
     const unsigned dot_blocks = (unsigned)((total + THREADS - 1) / THREADS);
-    dim3 grid((a.max_len + BLOCK_ROWS - 1) / BLOCK_ROWS, a.nseg, a.heads);
+    const dim3 grid = block_grid(a);
     // Model flops of the backward, 8·d·Σkeys, split as the kernels do the work: dK/dV (4 products of
     // which 2 recompute the forward's) and dQ (3 products, 2 recomputed).
     const double fb = 2.0 * a.hidden * a.keys;

@@ -371,7 +371,26 @@ struct AttentionArgs {
     bool rotated = false;  // q and k in qkv already carry RoPE (the model's fused projection)
     int rows = -1;         // rows of qkv, needed to rotate a copy when !rotated
     double keys;           // Σ over queries of the keys each one attends to (for the profile's flop count)
+    // Optional device list of the batch's row blocks of ATTENTION_BLOCK_ROWS rows, (segment << 16) | block,
+    // every block of every segment once (attention_block_list): the kernels then take one workgroup per
+    // entry and head, in list order. Null: a (max_len blocks, segments, heads) grid.
+    const int* blocks = nullptr;
+    int n_blocks = 0;
 };
+
+constexpr int ATTENTION_BLOCK_ROWS = 128;  // query or key rows per attention workgroup
+
+// The block list of segments of lengths len[0 .. n): the segments in decreasing length (ties in index
+// order), each segment's blocks in row order, so that a launch starts with its longest work.
+inline std::vector<int> attention_block_list(const std::vector<int>& len) {
+    std::vector<int> order(len.size());
+    for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return len[a] > len[b]; });
+    std::vector<int> out;
+    for (int s : order)
+        for (int b = 0; b * ATTENTION_BLOCK_ROWS < len[s]; ++b) out.push_back(s << 16 | b);
+    return out;
+}
 
 // Σ_q |window(q) ∩ segment| for one segment (Ops.cs:315-316).
 inline double window_keys(int L, int hw) {

@@ -60,12 +60,13 @@ struct Carver {
 
 // The device int32 tables of one batch (TrainableDecisionModel.cs:254-274 layout).
 struct BatchTables {
-    int *tokens, *seg_start, *seg_len, *row_type, *marker_rows, *qtypes, *opt_off, *sorted, *unique, *uoff, *pos;
+    int *tokens, *seg_start, *seg_len, *row_type, *marker_rows, *qtypes, *opt_off, *sorted, *unique, *uoff, *pos,
+        *blocks;
 };
 
 // A batch planned on the host and uploaded once, ahead of the steps that use it.
 struct StagedBatch {
-    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0;
+    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0, n_blocks = 0;
     double keys_full = 0, keys_local = 0;
     std::vector<int> opt_off;  // host copy: item i's options are logits [opt_off[i], opt_off[i + 1])
     void* block = nullptr;  // the tables, then the soft-CE targets
@@ -75,14 +76,14 @@ struct StagedBatch {
 
 // Host-side layout of one batch: every table the kernels read, before upload.
 struct BatchPlan {
-    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0;
+    int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0, n_blocks = 0;
     double keys_full = 0, keys_local = 0;
-    std::vector<int> tokens, start, len, marker_rows, qtypes, opt_off, row_type, sorted, unique, uoff, pos;
+    std::vector<int> tokens, start, len, marker_rows, qtypes, opt_off, row_type, sorted, unique, uoff, pos, blocks;
 };
 
 // The int tables of one batch inside a Carver, sized for Tz tokens, Mc markers and Sc items.
 struct TableCarve {
-    float *tok, *ps, *st, *ln, *rt, *mr, *qt, *oo, *so, *un, *uo;
+    float *tok, *ps, *st, *ln, *rt, *mr, *qt, *oo, *so, *un, *uo, *bl;
     void add(Carver& cv, size_t Tz, size_t Mc, size_t Sc) {
         cv.add(tok, Tz);
         cv.add(ps, Tz);
@@ -95,10 +96,11 @@ struct TableCarve {
         cv.add(so, Tz);
         cv.add(un, Tz + 1);
         cv.add(uo, Tz + 2);
+        cv.add(bl, Tz / laya::ATTENTION_BLOCK_ROWS + Sc + 1);  // Σ ⌈len / rows⌉ ≤ tokens / rows + segments
     }
     BatchTables bind() const {
         auto i = [](float* p) { return reinterpret_cast<int*>(p); };
-        return {i(tok), i(st), i(ln), i(rt), i(mr), i(qt), i(oo), i(so), i(un), i(uo), i(ps)};
+        return {i(tok), i(st), i(ln), i(rt), i(mr), i(qt), i(oo), i(so), i(un), i(uo), i(ps), i(bl)};
     }
 };
 
@@ -256,6 +258,7 @@ struct laya_model {
     bool has_tape = false, training = false;
     uint64_t seed = 0;
     int T = 0, nseg = 0, nmark = 0, max_len = 0, n_unique = 0, max_opts = 0;
+    int n_blocks = 0;  // entries of the current batch's attention block list
     double keys_full = 0, keys_local = 0;  // Σ_q attended keys of the batch, full and sliding window
     // RLCD objective: the draws of the last call (device, grown on demand) and its losses
     double* d_draws = nullptr;
@@ -612,6 +615,8 @@ BatchPlan plan_batch(const laya_model* m, const laya_batch* b) {
             bp.marker_rows[k] = bp.start[i] + pos;
         }
     }
+    bp.blocks = attention_block_list(bp.len);
+    bp.n_blocks = (int)bp.blocks.size();
     bp.row_type.assign(bp.T, 0);
     bp.pos.assign(bp.T, 0);
     for (int i = 0; i < n; ++i) {
@@ -646,6 +651,7 @@ void upload_tables(laya_model* m, const BatchTables& t, const BatchPlan& bp) {
     upload_ints(m, t.unique, bp.unique);
     upload_ints(m, t.uoff, bp.uoff);
     upload_ints(m, t.pos, bp.pos);
+    upload_ints(m, t.blocks, bp.blocks);
 }
 
 // Makes a batch's sizes the model's current ones and sizes the activations and rotary tables for it.
@@ -658,6 +664,7 @@ template <typename B> void set_batch_sizes(laya_model* m, const B& b) {
     m->max_opts = b.max_opts;
     m->keys_full = b.keys_full;
     m->keys_local = b.keys_local;
+    m->n_blocks = b.n_blocks;
     m->opt_off_host = b.opt_off;
     ensure_activations(m, b.T, b.nmark, b.nseg);
     ensure_rotary(m, b.max_len);
@@ -695,6 +702,8 @@ AttentionArgs enc_attention(laya_model* m, const float* qkv, int kind) {
     a.positions = r.positions;
     a.rotated = fused_rope(m);  // q and k left the QKV projection rotated
     a.rows = m->T;
+    a.blocks = m->cur.blocks;
+    a.n_blocks = m->n_blocks;
     return a;
 }
 
@@ -716,6 +725,8 @@ AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p
     a.p_drop = p;
     a.seed = salt(seed, index, 0);
     a.rows = m->T;
+    a.blocks = m->cur.blocks;
+    a.n_blocks = m->n_blocks;
     return a;
 }
 
@@ -1623,6 +1634,7 @@ int laya_model_stage_batch(laya_model* m, const laya_batch* batch, const float* 
         s.max_opts = bp.max_opts;
         s.keys_full = bp.keys_full;
         s.keys_local = bp.keys_local;
+        s.n_blocks = bp.n_blocks;
         s.opt_off = bp.opt_off;
         Carver cv;
         TableCarve tc;
