@@ -60,7 +60,7 @@ struct Params {
 };
 
 // A workgroup's segment, head and first row (query or key). With a block list, workgroup i takes entry
-// i / heads (segment << 16 | row block), head i mod heads: every workgroup has rows, the longest segments'
+// i / heads (segment · 2¹⁶ + row block, unsigned), head i mod heads: every workgroup has rows, the longest segments'
 // blocks are dispatched first, and the row blocks of one (segment, head) fall heads apart in dispatch order
 // (on two XCDs for 12 heads rather than all eight). Without one, the grid is (row block, segment, head).
 struct BlockCoord {
@@ -69,8 +69,8 @@ struct BlockCoord {
 __device__ __forceinline__ BlockCoord block_coord(const Params& p) {
     if (p.blocks) {
         const unsigned i = blockIdx.x / (unsigned)p.heads;
-        const int e = p.blocks[i];
-        return {e >> 16, (int)(blockIdx.x - i * (unsigned)p.heads), (e & 0xffff) * BLOCK_ROWS};
+        const unsigned e = (unsigned)p.blocks[i];
+        return {(int)(e >> 16), (int)(blockIdx.x - i * (unsigned)p.heads), (int)(e & 0xffffu) * BLOCK_ROWS};
     }
     return {(int)blockIdx.y, (int)blockIdx.z, (int)blockIdx.x * BLOCK_ROWS};
 }

@@ -523,14 +523,20 @@ int laya_segments_create(laya_ctx* ctx, const int* start, const int* length, int
             const size_t bytes = sizeof(int) * (size_t)std::max(nseg, 1);
             s->d_start = static_cast<int*>(ctx->alloc(bytes));
             s->d_len = static_cast<int*>(ctx->alloc(bytes));
+            s->blocks = attention_block_list(s->length);
+            if (!s->blocks.empty()) s->d_blocks = static_cast<int*>(ctx->alloc(sizeof(int) * s->blocks.size()));
             // The host vectors live as long as the handle, which outlives the copies (destroy synchronises).
             if (nseg) {
                 LAYA_HIP(hipMemcpyAsync(s->d_start, s->start.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
                 LAYA_HIP(hipMemcpyAsync(s->d_len, s->length.data(), bytes, hipMemcpyHostToDevice, ctx->stream));
             }
+            if (s->d_blocks)
+                LAYA_HIP(hipMemcpyAsync(s->d_blocks, s->blocks.data(), sizeof(int) * s->blocks.size(),
+                                        hipMemcpyHostToDevice, ctx->stream));
         } catch (...) {
             if (s->d_start) ctx->release(s->d_start);
             if (s->d_len) ctx->release(s->d_len);
+            if (s->d_blocks) ctx->release(s->d_blocks);
             delete s;
             throw;
         }
@@ -544,6 +550,7 @@ int laya_segments_destroy(laya_ctx* ctx, laya_segments* segs) {
         if (!segs) return;
         ctx->release(segs->d_start);  // release synchronises the stream first
         ctx->release(segs->d_len);
+        if (segs->d_blocks) ctx->release(segs->d_blocks);
         delete segs;
     });
 }
@@ -559,6 +566,8 @@ static AttentionArgs attention_args(const float* qkv, const laya_segments* segs,
     a.nseg = segs->nseg;
     a.max_len = segs->max_len;
     a.rows = segs->rows;
+    a.blocks = segs->d_blocks;
+    a.n_blocks = (int)segs->blocks.size();
     a.hidden = hidden;
     a.heads = heads;
     a.head_dim = hidden / heads;

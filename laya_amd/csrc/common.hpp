@@ -117,9 +117,10 @@ struct laya_ctx {
 // attention kernels read, and the host copy that sizes launches without reading the device back.
 struct laya_segments {
     int nseg = 0, max_len = 0, rows = 0;
-    std::vector<int> start, length;
+    std::vector<int> start, length, blocks;  // blocks: the attention block list (attention_block_list)
     int* d_start = nullptr;
     int* d_len = nullptr;
+    int* d_blocks = nullptr;
 };
 
 // Rotary tables on the device (Ops.cs:446-504).
@@ -371,9 +372,9 @@ struct AttentionArgs {
     bool rotated = false;  // q and k in qkv already carry RoPE (the model's fused projection)
     int rows = -1;         // rows of qkv, needed to rotate a copy when !rotated
     double keys;           // Σ over queries of the keys each one attends to (for the profile's flop count)
-    // Optional device list of the batch's row blocks of ATTENTION_BLOCK_ROWS rows, (segment << 16) | block,
-    // every block of every segment once (attention_block_list): the kernels then take one workgroup per
-    // entry and head, in list order. Null: a (max_len blocks, segments, heads) grid.
+    // Optional device list of the batch's row blocks of ATTENTION_BLOCK_ROWS rows, segment · 2¹⁶ + block as
+    // an unsigned 32-bit pattern, every block of every segment once (attention_block_list): the kernels then
+    // take one workgroup per entry and head, in list order. Null: a (max_len blocks, segments, heads) grid.
     const int* blocks = nullptr;
     int n_blocks = 0;
 };
@@ -381,14 +382,17 @@ struct AttentionArgs {
 constexpr int ATTENTION_BLOCK_ROWS = 128;  // query or key rows per attention workgroup
 
 // The block list of segments of lengths len[0 .. n): the segments in decreasing length (ties in index
-// order), each segment's blocks in row order, so that a launch starts with its longest work.
+// order), each segment's blocks in row order, so that a launch starts with its longest work. Segments
+// beyond 65535 or of 2²³ rows or more have no encoding; attention refuses such batches anyway.
 inline std::vector<int> attention_block_list(const std::vector<int>& len) {
     std::vector<int> order(len.size());
     for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
     std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return len[a] > len[b]; });
     std::vector<int> out;
+    if (len.size() > 65536) return out;
     for (int s : order)
-        for (int b = 0; b * ATTENTION_BLOCK_ROWS < len[s]; ++b) out.push_back(s << 16 | b);
+        for (int b = 0; b * ATTENTION_BLOCK_ROWS < len[s] && b < 65536; ++b)
+            out.push_back((int)((unsigned)s << 16 | (unsigned)b));
     return out;
 }
 

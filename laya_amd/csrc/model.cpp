@@ -702,7 +702,7 @@ AttentionArgs enc_attention(laya_model* m, const float* qkv, int kind) {
     a.positions = r.positions;
     a.rotated = fused_rope(m);  // q and k left the QKV projection rotated
     a.rows = m->T;
-    a.blocks = m->cur.blocks;
+    a.blocks = m->n_blocks > 0 ? m->cur.blocks : nullptr;
     a.n_blocks = m->n_blocks;
     return a;
 }
@@ -725,7 +725,7 @@ AttentionArgs head_attention(laya_model* m, const float* qkv, int index, float p
     a.p_drop = p;
     a.seed = salt(seed, index, 0);
     a.rows = m->T;
-    a.blocks = m->cur.blocks;
+    a.blocks = m->n_blocks > 0 ? m->cur.blocks : nullptr;
     a.n_blocks = m->n_blocks;
     return a;
 }
