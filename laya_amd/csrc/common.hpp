@@ -97,8 +97,10 @@ struct laya_ctx {
     // Attention's split products as two-piece fp16 products too (the default).
     bool attention_pair = true;
     // max|operand| words of the two-piece products that no caller keeps: a ring of AMAX_RING word groups, each
-    // measurement taking the next; the whole ring is cleared (one launch) each time it wraps. Stream order
-    // keeps this safe: every product that read a group was launched before the clear that recycles it.
+    // measurement taking the next; each half is cleared (one launch) as the measurements enter it. A product
+    // measures its operands one after another, so clearing only the half being entered keeps the group just
+    // measured for the same product; stream order does the rest: every product that read a group of the
+    // half being cleared was launched before the clear.
     unsigned* amax = nullptr;
     int amax_next = 0;
     std::vector<hipEvent_t> event_pool;

@@ -643,21 +643,28 @@ __device__ __forceinline__ void store_x3(const OperandH<KIND>& op, __bf16* lds0,
     }
 }
 
-// The two-piece form of store_x3 for float4 operands: the two fp16 planes of sc·x (ONE: the hi plane only,
-// for bf16-valued operands).
-template <bool ONE = false>
-__device__ __forceinline__ void store_x2(const OperandH<KVEC>& op, __bf16* lds0, __bf16* lds1, int tid, float sc) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int o = ((tid >> 3) + 32 * i) * KPADH + ((tid & 7) << 2);
+// The two-piece form of store_x3: the two fp16 planes of sc·x (ONE: the hi plane only, for bf16-valued
+// operands), in the same layout for every operand form.
+template <bool ONE = false, int KIND>
+__device__ __forceinline__ void store_x2(const OperandH<KIND>& op, __bf16* lds0, __bf16* lds1, int tid, float sc) {
+    auto put = [&](int o, f32x4 x) {
         if constexpr (ONE) {
-            *reinterpret_cast<f16x4*>(lds0 + o) = split1h_4(op.reg[i], sc);
+            *reinterpret_cast<f16x4*>(lds0 + o) = split1h_4(x, sc);
         } else {
             f16x4 hi, lo;
-            split2h_4(op.reg[i], sc, hi, lo);
+            split2h_4(x, sc, hi, lo);
             *reinterpret_cast<f16x4*>(lds0 + o) = hi;
             *reinterpret_cast<f16x4*>(lds1 + o) = lo;
         }
+    };
+    if constexpr (KIND == KVEC) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) put(((tid >> 3) + 32 * i) * KPADH + ((tid & 7) << 2), op.reg[i]);
+    } else {
+        const int o = (tid & 127) * KPADH + op.kq;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            put(o + 4 * q, f32x4{op.v[4 * q], op.v[4 * q + 1], op.v[4 * q + 2], op.v[4 * q + 3]});
     }
 }
 
@@ -725,7 +732,6 @@ __device__ __forceinline__ void mma_stage_x6(const __bf16* A, const __bf16* B, f
 template <int AOP, int BOP, int NP = 3, bool B1 = false>
 __device__ __forceinline__ void tile_mma_x6(const GemmParams& p, const TileCoord& c, __bf16 (*smem)[3 * STAGE_H],
                                             f32x16 (&acc)[2][2], float sa = 1.0f, float sb = 1.0f) {
-    static_assert(NP == 3 || (AOP == KVEC && BOP == KVEC), "two-piece products take float4 operands");
     const int len = max(0, c.ke - c.kb);
     const int nfull = len / BK, ntiles = nfull + (len % BK != 0 ? 1 : 0);
     const int rot = nfull > 0 ? c.t % nfull : 0;
@@ -2426,16 +2432,19 @@ void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, uns
 
 namespace {
 
-// max|x| of a rows x cols operand into the context's next word group (the ring is cleared, in one launch,
-// whenever it starts over); returns it. `slot` names the operand's role for the callers' bookkeeping only.
+// max|x| of a rows x cols operand into the context's next word group (each half of the ring is cleared, in
+// one launch, as the measurements enter it); returns it. `slot` names the operand's role for the callers'
+// bookkeeping only.
 const unsigned* operand_absmax(laya_ctx* ctx, int slot, const float* x, int rows, int cols, long ld) {
     (void)slot;
+    static_assert(AMAX_RING % 2 == 0 && AMAX_RING >= 4, "the ring is cleared a half at a time");
     if (!ctx->amax) {
         ctx->amax = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_RING * AMAX_GROUP));
         ctx->amax_next = 0;
     }
-    if (ctx->amax_next == 0)  // +0.0f is the all-zero word
-        fill(ctx, reinterpret_cast<float*>(ctx->amax), 0.0f, (size_t)AMAX_RING * AMAX_GROUP);
+    if (ctx->amax_next % (AMAX_RING / 2) == 0)  // +0.0f is the all-zero word
+        fill(ctx, reinterpret_cast<float*>(ctx->amax + (size_t)ctx->amax_next * AMAX_GROUP), 0.0f,
+             (size_t)(AMAX_RING / 2) * AMAX_GROUP);
     unsigned* out = ctx->amax + (size_t)ctx->amax_next * AMAX_GROUP;
     ctx->amax_next = (ctx->amax_next + 1) % AMAX_RING;
     absmax_into(ctx, x, rows, cols, ld, out);
@@ -2549,6 +2558,34 @@ void launch_wide_h(laya_ctx* ctx, GemmParams p) {
 
 template <int AOP, int BOP> void launch_x(laya_ctx* ctx, const GemmParams& p, int blocks) {
     const dim3 g(blocks), b(THREADS);
+    // Two-piece NN (dX = dY·W) and TN (dW += dYᵀ·X) products on 128 x 128 tiles: the backward of a linear
+    // whose rows are too few for the 256-wide pair.
+    if constexpr (AOP == KVEC && BOP == MNSCALAR) {
+        if (p.amax_a) {
+            profile_rename("gemm_nn_h2");
+            if (p.mode == STORE && p.R)
+                LAYA_LAUNCH((gemm_x6_kernel<KVEC, MNSCALAR, STORE, true, 2>), g, b, 0, ctx->stream, p);
+            else if (p.mode == STORE)
+                LAYA_LAUNCH((gemm_x6_kernel<KVEC, MNSCALAR, STORE, false, 2>), g, b, 0, ctx->stream, p);
+            else if (p.mode == PARTIAL)
+                LAYA_LAUNCH((gemm_x6_kernel<KVEC, MNSCALAR, PARTIAL, false, 2>), g, b, 0, ctx->stream, p);
+            else
+                LAYA_LAUNCH((gemm_x6_kernel<KVEC, MNSCALAR, ACCUMULATE, false, 2>), g, b, 0, ctx->stream, p);
+            check_launch("gemm_x6_kernel");
+            return;
+        }
+    }
+    if constexpr (AOP == MNSCALAR && BOP == MNSCALAR) {
+        if (p.amax_a && !p.R && p.mode != STORE) {
+            profile_rename("gemm_tn_h2");
+            if (p.mode == PARTIAL)
+                LAYA_LAUNCH((gemm_x6_kernel<MNSCALAR, MNSCALAR, PARTIAL, false, 2>), g, b, 0, ctx->stream, p);
+            else
+                LAYA_LAUNCH((gemm_x6_kernel<MNSCALAR, MNSCALAR, ACCUMULATE, false, 2>), g, b, 0, ctx->stream, p);
+            check_launch("gemm_x6_kernel");
+            return;
+        }
+    }
     if constexpr (AOP == KVEC && BOP == KVEC) {
         if (p.amax_a) {  // two-piece products (NT, float4 operands)
             profile_rename(p.mode == STORE && p.b_one ? "gemm_nt_h2b1" : "gemm_nt_h2");
@@ -2770,6 +2807,20 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
                        ? amax_c
                        : nullptr;
     }
+    // So do NN products with a float4 A (dX = dY·W: launch_x's KVEC x MNSCALAR form) and TN products into an
+    // accumulated C (dW += dYᵀ·X) under the input- and weight-gradient pair policies; each operand's
+    // magnitude over the array as stored (NN: B is K x N; TN: A is K x M, B is K x N).
+    const int cls = layout == GemmLayout::NN ? 2 : 4;
+    if (layout != GemmLayout::NT && (ctx->matmul_pair & cls) && !(ctx->matmul_bf16 & cls) &&
+        (ctx->matmul_split & cls) && gemm_fits_h(p, layout == GemmLayout::NN, false) &&
+        (layout == GemmLayout::TN ? ep == GemmEpilogue::Accumulate
+                                  : operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K))) {
+        if (layout == GemmLayout::NN)
+            p.amax_a = operand_amax(ctx, amax_a, 0, p.A, p.M, p.K, p.lda);
+        else
+            p.amax_a = operand_amax(ctx, amax_a, 0, p.A, p.K, p.M, p.lda);
+        p.amax_b = operand_amax(ctx, amax_b, 1, p.B, p.K, p.N, p.ldb);
+    }
     // C's magnitude: folded in by a two-piece kernel's epilogue, else measured after the product.
     const bool measure = amax_c && !p.amax_c;
     {
@@ -2824,9 +2875,10 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
             return;
         }
         if (ctx->matmul_split & 1) {
-            if ((ctx->matmul_pair & 1) && (wide_tiles_pay(ctx, p, false) || tall_tiles_pay(ctx, p))) {
+            const bool big = wide_tiles_pay(ctx, p, false) || tall_tiles_pay(ctx, p);
+            if (ctx->matmul_pair & 1) {
                 prepare_pair_nt(ctx, p, amax_a, amax_b);
-                p.amax_c = amax_c;
+                p.amax_c = big ? amax_c : nullptr;  // the 128 x 128 epilogue does not fold C's magnitude in
             }
             ProfileScope scope(ctx, "gemm_nt_x6", 2.0 * M * N * (double)K, 0.0);
             if (wide_tiles_pay(ctx, p, false)) {
@@ -2837,8 +2889,16 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
                 launch_tall(ctx, p);
                 return;
             }
-            LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false>), dim3(p.tiles_m * p.tiles_n),
-                               dim3(THREADS), 0, ctx->stream, p);
+            const dim3 g(p.tiles_m * p.tiles_n), b(THREADS);
+            if (p.amax_a && p.b_one) {
+                profile_rename("gemm_nt_h2b1");
+                LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false, 2, true>), g, b, 0, ctx->stream, p);
+            } else if (p.amax_a) {
+                profile_rename("gemm_nt_h2");
+                LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false, 2>), g, b, 0, ctx->stream, p);
+            } else {
+                LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, STORE_ROPE, false>), g, b, 0, ctx->stream, p);
+            }
             check_launch("gemm_x6_kernel");
             return;
         }
@@ -3058,8 +3118,9 @@ void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const flo
     }
     if (!fp32) {
         gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual,
-             in);
-        gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in);
+             in, nullptr, nullptr, amax_dy, amax_W);
+        gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr,
+             0, nullptr, nullptr, amax_dy, amax_x);
         return;
     }
     // Choose the dW split so its slices are as long as a dX tile's K loop, then minimise the rounds of

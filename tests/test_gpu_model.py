@@ -202,8 +202,15 @@ def test_full_train_step_matches_the_oracle(ctx):
     """fwd → soft-CE gradient → bwd → clip → AdamW (Trainer.cs:131-144). The gradients of the forward and
     backward are held directly to the fp64 oracle (max(1e-4, 4 × the fp32 oracle's error)); then the fused
     train_step, run from the same weights, must leave exactly the weights that the reference's clip and AdamW
-    formulas (AdamW.cs:29-73, 103-130) give when applied on the host to those GPU gradients."""
+    formulas (AdamW.cs:29-73, 103-130) give when applied on the host to those GPU gradients.
+
+    The logit gradient of the separate backward is the device's soft-CE kernel's (the fused step's own), held
+    to the oracle's at fp32 rounding: the two exponentials (the device's expf and the host's) may differ in the
+    last bit, and AdamW's first step, g / (|g| + ε), turns a last-bit difference in a gradient within a few ε
+    of zero into a visible weight difference."""
+    from laya_amd.device import DeviceArray
     from laya_amd.model import TrainableDecisionModel
+    import laya_amd.ops as laya
     mc, o, params, batch = _mid_case(layers=2, lengths=(150, 90, 33))
     o64 = oracle.OracleModel(mc, double=True)
     rng = np.random.default_rng(3)
@@ -213,7 +220,13 @@ def test_full_train_step_matches_the_oracle(ctx):
     m.set_params(params)
     lg = m.forward(batch, training=True, seed=seed)
     ce, g = oracle.cross_entropy(batch.n_options, lg, targets, 1.0, scale)
-    m.backward(g)
+    offsets = np.concatenate([[0], np.cumsum(batch.n_options)]).astype(np.int32)
+    gd = DeviceArray.from_numpy(ctx, np.zeros_like(lg))
+    laya.softmax_ce_backward(ctx, DeviceArray.from_numpy(ctx, lg), DeviceArray.from_numpy(ctx, targets),
+                             DeviceArray.from_numpy(ctx, offsets), len(batch.n_options), 1.0, scale, gd)
+    g_device = gd.numpy()
+    assert np.abs(g_device - g).max() <= 4 * np.finfo(np.float32).eps * np.abs(g).max()
+    m.backward(g_device)
     for ref in (o, o64):
         ref.set_params(params)
         ref.forward(batch, training=True, keep_tape=True, seed=seed)
@@ -223,6 +236,12 @@ def test_full_train_step_matches_the_oracle(ctx):
     grads = {}
     for name in trained:
         exact, grads[name] = o64.grad(name), m.grad(name)
+        if name == "scorer.3.bias":
+            # Σ of the soft-CE gradient over every option, exactly 0: rounding noise of that sum, which no
+            # relative error describes.
+            noise = 8 * np.finfo(np.float32).eps * np.abs(g_device).sum()
+            assert np.abs(grads[name] - exact).max() <= noise, (name, grads[name], exact, noise)
+            continue
         bar = max(1e-4, 4 * rel_l2(exact, o.grad(name)))
         assert rel_l2(exact, grads[name]) < bar, (name, rel_l2(exact, grads[name]), bar)
     m.close()

@@ -392,6 +392,40 @@ def test_attention_over_many_segments(ctx):
         assert rel_l2(dref[:, sl], got[:, sl]) < 1e-5, part
 
 
+def test_operand_magnitude_ring_keeps_each_products_words():
+    """Products whose callers keep no magnitude words (the per-op entry points) measure their operands into
+    the context's ring of word groups, one operand after the other. A fresh context, one attention forward
+    (one measurement) to set the parity, then 130 identical linears (two measurements each) put a product's
+    first measurement on every odd ring position, the wrap included; a second attention forward shifts them
+    onto the even ones. Every product equals the first bit for bit: recycling the ring never clears a word
+    that a pending product still reads."""
+    from laya_amd.device import Context
+    c = Context(0)
+    try:
+        rng = np.random.default_rng(128)
+        rows, inn, out = 200, 64, 128
+        x = rng.standard_normal((rows, inn)).astype(np.float32)
+        W = (0.05 * rng.standard_normal((out, inn))).astype(np.float32)
+        w, xd = laya.Parameter(c, "w", W, False), dev(c, x)
+        qkv = dev(c, rng.standard_normal((16, 3 * 64)).astype(np.float32))
+        segs = laya.Segments(c, [16])
+        shape = laya.AttentionShape(64, 1, laya.default_scale(64), -1, None, 0.0, 0)
+        first = None
+        for parity in range(2):
+            laya.attention_forward(qkv, segs, shape, dev(c, np.zeros((16, 64), np.float32)),
+                                   dev(c, np.zeros(16, np.float32)))
+            for i in range(130):
+                y = dev(c, np.zeros((rows, out), np.float32))
+                laya.linear(w, None, xd, rows, y)
+                got = y.numpy()
+                if first is None:
+                    first = got
+                    assert rel_l2(x.astype(np.float64) @ W.astype(np.float64).T, got) < 1e-6
+                np.testing.assert_array_equal(got, first, err_msg=f"parity {parity}, product {i}")
+    finally:
+        c.close()
+
+
 def test_attention_is_deterministic(ctx):
     rng = np.random.default_rng(5)
     lengths, heads, hd = [384, 100], 12, 64
