@@ -226,6 +226,15 @@ def per_op_rate(ctx, mc, model, batches, w, args, scale):
     dt = time.perf_counter() - t0
     tokens = sum(b.n_tokens for b, _ in batches[args.warmup:])
     print(f"per-op: timed {args.steps} steps in {dt:.3f} s", file=sys.stderr, flush=True)
+    # A non-finite value anywhere in a step reaches every weight through AdamW; the rate of steps on NaN data
+    # (which the matrix cores run at a different clock) is no rate of this path.
+    bad = [n for n in (model.names[1], model.names[len(model.names) // 2], model.names[-1])
+           if not np.isfinite(om.param(n)).all()]
+    if bad:
+        for ob in obs:
+            ob.close()
+        om.close()
+        raise RuntimeError(f"per-op path: {bad[0]} is not finite after the timed steps")
     if not args.no_profile:
         ctx.profile_begin()
         for i in range(args.warmup, args.warmup + args.steps):
