@@ -368,6 +368,14 @@ int laya_linear_bwd(laya_ctx* ctx, const float* x, const float* dy, int rows, in
         LAYA_REQUIRE(rows >= 0 && in > 0 && out > 0, "linear_bwd: bad size");
         LAYA_REQUIRE(dy && W, "linear_bwd: null tensor");
         LAYA_REQUIRE(!dW || x, "linear_bwd: dW needs x");
+        if (dx && dW && db) {
+            // The bias gradient's pass over dy takes dy's magnitude for the pair's two-piece products too.
+            unsigned* w = operand_ring_word(ctx);
+            column_sum_add(ctx, dy, rows, out, db, w);
+            unsigned char known = 1;
+            gemm_backward_pair(ctx, rows, in, out, dy, W, x, dx, nullptr, dW, nullptr, nullptr, AmaxRef{w, &known});
+            return;
+        }
         if (dx && dW)
             gemm_backward_pair(ctx, rows, in, out, dy, W, x, dx, nullptr, dW);
         else if (dx)

@@ -321,8 +321,12 @@ void absmax_multi(laya_ctx* ctx, const float* arena, const long* off, const int*
 // group `slot` (0 … 5), measured now.
 const unsigned* operand_amax_ref(laya_ctx* ctx, AmaxRef r, int slot, const float* x, int rows, int cols, long ld);
 
-// Σ over rows of a [rows, n] matrix added into out[n], deterministic (bias gradients).
-void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out);
+// Σ over rows of a [rows, n] matrix added into out[n], deterministic (bias gradients); amax (optional): max|x|
+// folded into that word group too, in the same pass where the sums take the float4 path.
+void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out, unsigned* amax = nullptr);
+// The context's next operand word group, cleared (the ring operand_amax_ref measures into when the caller keeps
+// no word), for a caller that folds an operand's magnitude into it itself.
+unsigned* operand_ring_word(laya_ctx* ctx);
 
 // y16 (optional): a bf16 copy of y (nearest even), for the bf16 products that read it; amax (optional):
 // max|y| folded into a magnitude word group (absmax_into).

@@ -283,11 +283,13 @@ __global__ void scatter_add_rows_kernel(const float* src, const int* rows, int n
 // Column sums in two deterministic stages (bias gradients, the type-embedding gradient, LayerNorm γ/β
 // partials). Stage 1: part[chunk][type][c] = Σ over the chunk's rows r with row_type[r] == type of x[r][c]
 // (one type when row_type is null); a block is 64 float4 columns × 4 row phases, phase k summing rows
-// k, k + 4, … in order, the phases combined in LDS in order.
-template <int TYPES>
+// k, k + 4, … in order, the phases combined in LDS in order. AMAX: max|x| over the values read folded into
+// the word group amax as well (the operand magnitude a two-piece product of x needs, in the same pass).
+template <int TYPES, bool AMAX = false>
 __global__ __launch_bounds__(256) void colsum_partial4_kernel(const f32x4* __restrict__ x, int rows, int n4,
                                                               int rows_per, const int* __restrict__ row_type,
-                                                              f32x4* __restrict__ part) {
+                                                              f32x4* __restrict__ part, unsigned* amax) {
+    static_assert(TYPES == 1 || !AMAX, "the magnitude rides on the one-type sums");
     __shared__ f32x4 red[TYPES][4][64];
     const int lc = threadIdx.x & 63, ph = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + lc;
@@ -295,12 +297,14 @@ __global__ __launch_bounds__(256) void colsum_partial4_kernel(const f32x4* __res
     f32x4 acc[TYPES];
 #pragma unroll
     for (int t = 0; t < TYPES; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    unsigned m = 0;
     if (c < n4) {
 #pragma unroll 4
         for (int r = r0 + ph; r < r1; r += 4) {
             const f32x4 v = x[(long)r * n4 + c];
             if (TYPES == 1) {
                 acc[0] += v;
+                if constexpr (AMAX) m = max(m, amax_bits4(v));
             } else {
                 const int ty = row_type[r];
 #pragma unroll
@@ -317,6 +321,7 @@ __global__ __launch_bounds__(256) void colsum_partial4_kernel(const f32x4* __res
         for (int t = 0; t < TYPES; ++t)
             part[((long)blockIdx.y * TYPES + t) * n4 + c] =
                 ((red[t][0][lc] + red[t][1][lc]) + red[t][2][lc]) + red[t][3][lc];
+    if constexpr (AMAX) block_amax_fold(m, amax);
 }
 
 // Stage 2: out[c] += Σ_k part[k][c] over `count` partials; a block is 16 float4 columns × 16 phases,
@@ -573,8 +578,9 @@ void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g,
     check_launch("relu_dropout_bwd_out4_kernel");
 }
 void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_type, int types, float* out,
-                 int slot) {
+                 int slot, unsigned* amax) {
     LAYA_REQUIRE(types == 1 || types == 3, "column_sums: one or three row types");
+    LAYA_REQUIRE(!amax || types == 1, "column_sums: the magnitude rides on the one-type sums");
     LAYA_REQUIRE(n % 4 == 0 && vec4(x) && vec4(out), "column_sums: 16-byte aligned rows of a multiple of 4");
     if (rows <= 0 || n <= 0) return;
     const int n4 = n / 4, cblocks = (n4 + 63) / 64;
@@ -584,12 +590,15 @@ void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_
     const int chunks = (rows + rows_per - 1) / rows_per;
     f32x4* part = static_cast<f32x4*>(ctx->workspace(slot, sizeof(f32x4) * (size_t)chunks * types * n4));
     ProfileScope scope(ctx, "column_sums", 0.0, 4.0 * (double)rows * n);
-    if (types == 1)
+    if (amax)
+        LAYA_LAUNCH((colsum_partial4_kernel<1, true>), dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
+                    reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, nullptr, part, amax);
+    else if (types == 1)
         LAYA_LAUNCH(colsum_partial4_kernel<1>, dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
-                           reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, nullptr, part);
+                           reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, nullptr, part, nullptr);
     else
         LAYA_LAUNCH(colsum_partial4_kernel<3>, dim3(cblocks, chunks), dim3(256), 0, ctx->stream,
-                           reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, row_type, part);
+                           reinterpret_cast<const f32x4*>(x), rows, n4, rows_per, row_type, part, nullptr);
     check_launch("colsum_partial4_kernel");
     column_reduce(ctx, reinterpret_cast<const float*>(part), chunks, types * n, out);
 }

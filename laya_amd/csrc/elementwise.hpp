@@ -39,7 +39,8 @@ void add_indexed_rows(laya_ctx* ctx, float* dst, const int* idx, int rows, int w
 void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g, size_t n, float p);
 // out[type·n + c] += Σ rows of x[r][c] (per row type when row_type is given; types 1 or 3), in a fixed
 // order, through workspace `slot`; n % 4 == 0, 16-byte aligned.
-void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_type, int types, float* out, int slot);
+void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_type, int types, float* out, int slot,
+                 unsigned* amax = nullptr);
 // out[c] += Σ_k part[k][c] for count partial rows of width n, in a fixed order.
 void column_reduce(laya_ctx* ctx, const float* part, int count, int n, float* out);
 // Several column reductions out[c] += Σ_k part[k][c] in one launch (each in column_reduce's order).

@@ -2432,21 +2432,11 @@ void absmax_into(laya_ctx* ctx, const float* x, int rows, int cols, long ld, uns
 
 namespace {
 
-// max|x| of a rows x cols operand into the context's next word group (each half of the ring is cleared, in
-// one launch, as the measurements enter it); returns it. `slot` names the operand's role for the callers'
-// bookkeeping only.
+// max|x| of a rows x cols operand into the context's next word group; returns it. `slot` names the operand's
+// role for the callers' bookkeeping only.
 const unsigned* operand_absmax(laya_ctx* ctx, int slot, const float* x, int rows, int cols, long ld) {
     (void)slot;
-    static_assert(AMAX_RING % 2 == 0 && AMAX_RING >= 4, "the ring is cleared a half at a time");
-    if (!ctx->amax) {
-        ctx->amax = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_RING * AMAX_GROUP));
-        ctx->amax_next = 0;
-    }
-    if (ctx->amax_next % (AMAX_RING / 2) == 0)  // +0.0f is the all-zero word
-        fill(ctx, reinterpret_cast<float*>(ctx->amax + (size_t)ctx->amax_next * AMAX_GROUP), 0.0f,
-             (size_t)(AMAX_RING / 2) * AMAX_GROUP);
-    unsigned* out = ctx->amax + (size_t)ctx->amax_next * AMAX_GROUP;
-    ctx->amax_next = (ctx->amax_next + 1) % AMAX_RING;
+    unsigned* out = operand_ring_word(ctx);
     absmax_into(ctx, x, rows, cols, ld, out);
     return out;
 }
@@ -2768,6 +2758,21 @@ int fill_splits(const laya_ctx* ctx, int tiles, int K, int min_k) {
 }
 
 }  // namespace
+
+// Each half of the ring is cleared, in one launch, as the measurements enter it.
+unsigned* operand_ring_word(laya_ctx* ctx) {
+    static_assert(AMAX_RING % 2 == 0 && AMAX_RING >= 4, "the ring is cleared a half at a time");
+    if (!ctx->amax) {
+        ctx->amax = static_cast<unsigned*>(ctx->alloc(sizeof(unsigned) * AMAX_RING * AMAX_GROUP));
+        ctx->amax_next = 0;
+    }
+    if (ctx->amax_next % (AMAX_RING / 2) == 0)  // +0.0f is the all-zero word
+        fill(ctx, reinterpret_cast<float*>(ctx->amax + (size_t)ctx->amax_next * AMAX_GROUP), 0.0f,
+             (size_t)(AMAX_RING / 2) * AMAX_GROUP);
+    unsigned* out = ctx->amax + (size_t)ctx->amax_next * AMAX_GROUP;
+    ctx->amax_next = (ctx->amax_next + 1) % AMAX_RING;
+    return out;
+}
 
 const unsigned* operand_amax_ref(laya_ctx* ctx, AmaxRef r, int slot, const float* x, int rows, int cols, long ld) {
     LAYA_REQUIRE(slot >= 0 && slot < AMAX_SLOTS, "operand_amax_ref: no such slot");
@@ -3165,12 +3170,13 @@ void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const flo
     finish_accumulate(ctx, tn, dW_out, in);
 }
 
-void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out) {
+void column_sum_add(laya_ctx* ctx, const float* x, int rows, int n, float* out, unsigned* amax) {
     if (rows <= 0 || n <= 0) return;
     if (n % 4 == 0 && aligned16(x) && aligned16(out) && rows > 256) {
-        column_sums(ctx, x, rows, n, nullptr, 1, out, 1);
+        column_sums(ctx, x, rows, n, nullptr, 1, out, 1, amax);
         return;
     }
+    if (amax) absmax_into(ctx, x, rows, n, n, amax);
     const int rows_per = 256;
     const int chunks = (rows + rows_per - 1) / rows_per;
     if (chunks <= 1) {
