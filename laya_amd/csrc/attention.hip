@@ -1318,31 +1318,40 @@ __global__ __launch_bounds__(THREADS, NP == 2 ? 3 : 2) void attn_bwd_dq_x6_kerne
 // RoPE at segment-local positions on the q and k columns of one segment's qkv rows, written to `out`
 // together with an unchanged copy of v (Gather, Ops.cs:297-313). One thread per float4 unit of a row:
 // the first hidden/4 units are (d, d + D/2) pairs of q and then k, the next hidden/4 copy v.
+// amax (optional): max|written value| folded into that word group (the magnitude the two-piece kernels take
+// their scale from, in the same pass).
 __global__ void rope_rows_kernel(const float* __restrict__ qkv, const int* __restrict__ seg_start,
                                  const int* __restrict__ seg_len, int hidden, int head_dim,
                                  const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                                 float* __restrict__ out) {
+                                 float* __restrict__ out, unsigned* amax) {
     const int seg = blockIdx.y;
     const int start = seg_start[seg], L = seg_len[seg];
     const int units = hidden / 2;  // per row
     const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
     const int t = (int)(idx / units), u = (int)(idx - (long)t * units);
-    if (t >= L) return;
-    const long row = (long)(start + t) * 3 * hidden;
-    const int half = head_dim / 2;
-    if (u < hidden / 4) {
-        const int per_part = hidden / 8;                 // float4 pair units in q (or k)
-        const int part = u / per_part, v = u - part * per_part;
-        const int head = v / (half / 4), j = (v - head * (half / 4)) * 4;
-        const long col = (long)part * hidden + head * head_dim + j;
-        const f32x4 a = ld4(qkv + row + col), b = ld4(qkv + row + col + half);
-        const f32x4 c = ld4(cos_t + (long)t * half + j), s = ld4(sin_t + (long)t * half + j);
-        st4(out + row + col, a * c - b * s);
-        st4(out + row + col + half, b * c + a * s);
-    } else {
-        const long col = 2L * hidden + (long)(u - hidden / 4) * 4;
-        st4(out + row + col, ld4(qkv + row + col));
+    unsigned m = 0;
+    if (t < L) {  // (no early return: the whole block reaches the fold)
+        const long row = (long)(start + t) * 3 * hidden;
+        const int half = head_dim / 2;
+        if (u < hidden / 4) {
+            const int per_part = hidden / 8;  // float4 pair units in q (or k)
+            const int part = u / per_part, v = u - part * per_part;
+            const int head = v / (half / 4), j = (v - head * (half / 4)) * 4;
+            const long col = (long)part * hidden + head * head_dim + j;
+            const f32x4 a = ld4(qkv + row + col), b = ld4(qkv + row + col + half);
+            const f32x4 c = ld4(cos_t + (long)t * half + j), s = ld4(sin_t + (long)t * half + j);
+            const f32x4 ra = a * c - b * s, rb = b * c + a * s;
+            st4(out + row + col, ra);
+            st4(out + row + col + half, rb);
+            m = max(amax_bits4(ra), amax_bits4(rb));
+        } else {
+            const long col = 2L * hidden + (long)(u - hidden / 4) * 4;
+            const f32x4 v = ld4(qkv + row + col);
+            st4(out + row + col, v);
+            m = amax_bits4(v);
+        }
     }
+    block_amax_fold(m, amax);
 }
 
 Params make_params(const AttentionArgs& a) {
@@ -1365,8 +1374,8 @@ Params make_params(const AttentionArgs& a) {
 }
 
 // The qkv the kernels read: `a.qkv` itself when RoPE is already applied (or absent), else a rotated
-// copy of its segment rows in workspace slot 4.
-const float* rotated_qkv(laya_ctx* ctx, const AttentionArgs& a) {
+// copy of its segment rows in workspace slot 4, its magnitude folded into `amax` when given.
+const float* rotated_qkv(laya_ctx* ctx, const AttentionArgs& a, unsigned* amax = nullptr) {
     if (a.cos_table == nullptr || a.rotated) return a.qkv;
     LAYA_REQUIRE(a.rows >= 0, "attention: row count needed to rotate q and k");
     LAYA_REQUIRE(a.hidden % 8 == 0 && (a.head_dim / 2) % 4 == 0, "attention: RoPE needs head_dim % 8 == 0");
@@ -1375,7 +1384,7 @@ const float* rotated_qkv(laya_ctx* ctx, const AttentionArgs& a) {
     dim3 grid((unsigned)((threads + 255) / 256), a.nseg);
     ProfileScope scope(ctx, "attention_rope", 0.0, 4.0 * 3.0 * a.hidden * (double)a.rows * 2.0);
     LAYA_LAUNCH(rope_rows_kernel, grid, dim3(256), 0, ctx->stream, a.qkv, a.seg_start, a.seg_len, a.hidden,
-                       a.head_dim, a.cos_table, a.sin_table, out);
+                       a.head_dim, a.cos_table, a.sin_table, out, amax);
     check_launch("rope_rows_kernel");
     return out;
 }
@@ -1419,15 +1428,20 @@ void attention_fwd(laya_ctx* ctx, const AttentionArgs& a, float* context, float*
     check_args(a);
     if (a.nseg == 0 || a.max_len == 0) return;
     Params p = make_params(a);
-    p.qkv = rotated_qkv(ctx, a);
+    const bool split = a.head_dim == 64 && split_attention(ctx);
+    const bool pair = split && ctx->attention_pair;
+    // A rotated copy folds its own magnitude in as it is written (no pass to measure it).
+    unsigned* rot_word = pair && a.cos_table && !a.rotated ? operand_ring_word(ctx) : nullptr;
+    p.qkv = rotated_qkv(ctx, a, rot_word);
     p.context = context;
     p.lse = lse;
     p.amax = amax;
     const dim3 grid = block_grid(a);
-    const bool split = a.head_dim == 64 && split_attention(ctx);
-    const bool pair = split && ctx->attention_pair;
     p.context16 = split ? context16 : nullptr;
-    if (pair) pair_inputs(ctx, a, p.qkv, amax_qkv, p);
+    if (pair && rot_word)
+        p.amax_qkv = rot_word;
+    else if (pair)
+        pair_inputs(ctx, a, p.qkv, amax_qkv, p);
     {
         ProfileScope scope(ctx, pair ? "attention_fwd_h2" : split ? "attention_fwd_x6" : "attention_fwd",
                            4.0 * a.hidden * a.keys, 0.0);
@@ -1459,7 +1473,9 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     p.amax = amax;
     AttentionArgs ar = a;
     if (ar.rows < 0) ar.rows = rows;
-    p.qkv = rotated_qkv(ctx, ar);
+    const bool pair = a.head_dim == 64 && split_attention(ctx) && ctx->attention_pair;
+    unsigned* rot_word = pair && a.cos_table && !a.rotated ? operand_ring_word(ctx) : nullptr;
+    p.qkv = rotated_qkv(ctx, ar, rot_word);
     p.lse = const_cast<float*>(lse);
     p.dcontext = dcontext;
     p.dqkv = dqkv;
@@ -1471,9 +1487,12 @@ void attention_bwd(laya_ctx* ctx, const AttentionArgs& a, int rows, const float*
     // Model flops of the backward, 8·d·Σkeys, split as the kernels do the work: dK/dV (4 products of
     // which 2 recompute the forward's) and dQ (3 products, 2 recomputed).
     const double fb = 2.0 * a.hidden * a.keys;
-    if (a.head_dim == 64 && split_attention(ctx) && ctx->attention_pair) {
+    if (pair) {
         p.context = const_cast<float*>(context);
-        pair_inputs(ctx, ar, p.qkv, amax_qkv, p);
+        if (rot_word)
+            p.amax_qkv = rot_word;
+        else
+            pair_inputs(ctx, ar, p.qkv, amax_qkv, p);
         p.amax_do = operand_amax_ref(ctx, amax_do, 4, dcontext, rows, a.hidden, a.hidden);
         {
             // dQ first: it forms each row's Σ dO·O and writes it for dK/dV.
