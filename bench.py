@@ -250,7 +250,9 @@ def per_op_rate(ctx, mc, model, batches, w, args, scale):
     om.close()
     return {"value": round(tokens / dt, 1), "unit": "tokens/s", "ms_per_step": round(dt / args.steps * 1e3, 3),
             "how": "the same steps composed from the per-op C-ABI entry points (laya_amd.opmodel), one call per "
-                   "Ops method in TrainableDecisionModel's order, from the same initial weights"}
+                   "Ops method in TrainableDecisionModel's order, from the same initial weights; the binding keeps "
+                   "the encoder operands' magnitude words (laya_hip.h's _w variants) as it keeps attention's "
+                   "context and LSE"}
 
 
 def main():

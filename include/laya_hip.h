@@ -251,6 +251,45 @@ int laya_adamw(laya_ctx* ctx, float* params, float* grads, float* m, float* v, i
                const size_t* end, const double* lr, double beta1, double beta2, double eps, double weight_decay,
                int step, const float* coef, int zero_grads);
 
+/* ---------------------------------------------- operand magnitude words (per-op binding state)
+ *
+ * No counterpart in the reference: state a binding may keep beside its device buffers, as it keeps
+ * attention's context and LSE (the `Ops` signatures stay as they are). The fp32-accurate products split
+ * each operand into two fp16 pieces scaled by a power of two from the operand's largest finite magnitude;
+ * an entry point above measures each operand with a pass over it. A magnitude word group is
+ * LAYA_AMAX_WORDS uint32 words of device memory (laya_alloc). The _w variants below, each the entry point of
+ * the same name with the same meaning otherwise, fill an output's group (cleared first) with the largest
+ * finite magnitude of what they write, and take an input's group in place of measuring that input. A group
+ * describes its buffer as the call that filled it left it: a binding passes it while nothing else has
+ * written the buffer since, and NULL (measure) otherwise. A NULL output group is not written. */
+#define LAYA_AMAX_WORDS 1024
+/* Fills `words` (cleared first) with max|x| over the finite elements of x[n]. */
+int laya_amax(laya_ctx* ctx, const float* x, size_t n, unsigned* words);
+int laya_linear_fwd_w(laya_ctx* ctx, const float* x, int rows, int in, const float* W, int out, const float* b,
+                      const float* residual, float* y, const unsigned* x_words, const unsigned* W_words,
+                      unsigned* y_words);
+int laya_linear_bwd_w(laya_ctx* ctx, const float* x, const float* dy, int rows, int in, int out, const float* W,
+                      float* dx, float* dW, float* db, const unsigned* x_words, const unsigned* dy_words,
+                      const unsigned* W_words, unsigned* dx_words);
+int laya_layernorm_fwd_w(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps,
+                         float* y, float* mean, float* rstd, unsigned* y_words);
+/* dx_words: of dx as written (laya_layernorm_bwd adds into dx). */
+int laya_layernorm_bwd_w(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
+                         float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
+                         unsigned* dx_words);
+int laya_geglu_fwd_w(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, unsigned* act_words);
+int laya_geglu_bwd_w(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide,
+                     unsigned* dwide_words);
+/* qkv_words: of qkv as stored (unused when a rotary table makes the kernels read a rotated copy, which
+ * measures itself as it is written). */
+int laya_attention_fwd_w(laya_ctx* ctx, const float* qkv, const laya_segments* segs, int hidden, int heads,
+                         float scale, int half_window, const laya_rotary* rot, float p_drop, uint64_t seed,
+                         float* context, float* lse, const unsigned* qkv_words, unsigned* context_words);
+int laya_attention_bwd_w(laya_ctx* ctx, const float* qkv, const laya_segments* segs, int hidden, int heads,
+                         float scale, int half_window, const laya_rotary* rot, float p_drop, uint64_t seed,
+                         const float* context, const float* lse, const float* dcontext, float* dqkv,
+                         const unsigned* qkv_words, const unsigned* dcontext_words, unsigned* dqkv_words);
+
 /* ---------------------------------------------- model (TrainableDecisionModel.cs, Trainer.cs) */
 
 typedef struct {

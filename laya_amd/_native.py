@@ -127,6 +127,16 @@ SIGNATURES = {
     "laya_grad_norm": (c_int, [P, P, c_size, c_double, P, P]),
     "laya_grad_norm_status": (c_int, [P]),
     "laya_adamw": (c_int, [P, P, P, P, P, c_int, P, P, P, c_double, c_double, c_double, c_double, c_int, P, c_int]),
+    "laya_amax": (c_int, [P, P, c_size, P]),
+    "laya_linear_fwd_w": (c_int, [P, P, c_int, c_int, P, c_int, P, P, P, P, P, P]),
+    "laya_linear_bwd_w": (c_int, [P, P, P, c_int, c_int, c_int, P, P, P, P, P, P, P, P]),
+    "laya_layernorm_fwd_w": (c_int, [P, P, c_int, c_int, P, P, c_float, P, P, P, P]),
+    "laya_layernorm_bwd_w": (c_int, [P, P, c_int, c_int, P, c_float, P, P, P, P, P, P, P]),
+    "laya_geglu_fwd_w": (c_int, [P, P, c_int, c_int, P, P]),
+    "laya_geglu_bwd_w": (c_int, [P, P, P, c_int, c_int, P, P]),
+    "laya_attention_fwd_w": (c_int, [P, P, P, c_int, c_int, c_float, c_int, P, c_float, c_u64, P, P, P, P]),
+    "laya_attention_bwd_w": (c_int, [P, P, P, c_int, c_int, c_float, c_int, P, c_float, c_u64, P, P, P, P, P, P,
+                                     P]),
     "laya_model_create": (c_int, [P, ctypes.POINTER(ModelConfigC), PP]),
     "laya_model_destroy": (c_int, [P]),
     "laya_model_num_params": (c_int, [P, ctypes.POINTER(c_int)]),

@@ -627,6 +627,157 @@ int laya_attention_bwd(laya_ctx* ctx, const float* qkv, const laya_segments* seg
     });
 }
 
+// ------------------------------------------------------------------ operand magnitude words
+//
+// The _w variants: the same work as the entry points above, with the binding's magnitude word groups in
+// place of measuring inputs, and the outputs' magnitudes folded into groups the call clears first.
+
+namespace {
+
+// An input's group as the two-piece products take it (known: no measuring pass), or none.
+struct Given {
+    unsigned char known = 1;
+    AmaxRef ref;
+    explicit Given(const unsigned* w) { ref = w ? AmaxRef{const_cast<unsigned*>(w), &known} : AmaxRef{}; }
+};
+
+// An output's group, cleared before the kernels that fold into it run (stream order).
+unsigned* cleared(laya_ctx* ctx, unsigned* w) {
+    if (w) fill(ctx, reinterpret_cast<float*>(w), 0.0f, (size_t)AMAX_GROUP);
+    return w;
+}
+
+}  // namespace
+
+int laya_amax(laya_ctx* ctx, const float* x, size_t n, unsigned* words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(words && (x || n == 0), "amax: null tensor");
+        LAYA_REQUIRE(n <= (size_t)INT32_MAX * 4, "amax: too many elements");
+        cleared(ctx, words);
+        // As rows of 4 when the count allows (float4 loads), else one row per element.
+        if (n % 4 == 0)
+            absmax_into(ctx, x, (int)(n / 4), 4, 4, words);
+        else
+            absmax_into(ctx, x, (int)n, 1, 1, words);
+    });
+}
+
+int laya_linear_fwd_w(laya_ctx* ctx, const float* x, int rows, int in, const float* W, int out, const float* b,
+                      const float* residual, float* y, const unsigned* x_words, const unsigned* W_words,
+                      unsigned* y_words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && in > 0 && out > 0, "linear: bad size");
+        LAYA_REQUIRE(x && W && y, "linear: null tensor");
+        const Given gx(x_words), gw(W_words);
+        gemm(ctx, GemmLayout::NT, GemmEpilogue::Store, rows, out, in, x, in, W, in, y, out, b, residual, out, nullptr,
+             nullptr, gx.ref, gw.ref, cleared(ctx, y_words));
+    });
+}
+
+int laya_linear_bwd_w(laya_ctx* ctx, const float* x, const float* dy, int rows, int in, int out, const float* W,
+                      float* dx, float* dW, float* db, const unsigned* x_words, const unsigned* dy_words,
+                      const unsigned* W_words, unsigned* dx_words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && in > 0 && out > 0, "linear_bwd: bad size");
+        LAYA_REQUIRE(dy && W, "linear_bwd: null tensor");
+        LAYA_REQUIRE(!dW || x, "linear_bwd: dW needs x");
+        LAYA_REQUIRE(!dx_words || dx, "linear_bwd: dx_words without dx");
+        unsigned* w_dy = const_cast<unsigned*>(dy_words);
+        if (db && !w_dy && dx && dW) {  // the bias gradient's pass measures dy for the pair, as laya_linear_bwd does
+            w_dy = operand_ring_word(ctx);
+            column_sum_add(ctx, dy, rows, out, db, w_dy);
+            db = nullptr;
+        }
+        const Given gdy(w_dy), gx(x_words), gw(W_words);
+        unsigned* wdx = cleared(ctx, dx_words);
+        if (dx && dW) {
+            gemm_backward_pair(ctx, rows, in, out, dy, W, x, dx, nullptr, dW, nullptr, nullptr, gdy.ref, gw.ref, gx.ref,
+                               wdx);
+        } else if (dx) {
+            gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in, nullptr, nullptr, 0,
+                 nullptr, nullptr, gdy.ref, gw.ref, wdx);
+        } else if (dW) {
+            gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr,
+                 0, nullptr, nullptr, gdy.ref, gx.ref);
+        }
+        if (db) column_sum_add(ctx, dy, rows, out, db);
+    });
+}
+
+int laya_layernorm_fwd_w(laya_ctx* ctx, const float* x, int rows, int n, const float* w, const float* b, float eps,
+                         float* y, float* mean, float* rstd, unsigned* y_words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && x && w && y, "layernorm: bad arguments");
+        layernorm_fwd(ctx, x, rows, n, w, b, eps, y, mean, rstd, nullptr, nullptr, nullptr, nullptr,
+                      cleared(ctx, y_words));
+    });
+}
+
+int laya_layernorm_bwd_w(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
+                         float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
+                         unsigned* dx_words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && x && w && dy && dx, "layernorm_bwd: bad arguments");
+        LAYA_REQUIRE((mean == nullptr) == (rstd == nullptr), "layernorm_bwd: pass both mean and rstd, or neither");
+        layernorm_bwd(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, nullptr, cleared(ctx, dx_words));
+    });
+}
+
+int laya_geglu_fwd_w(laya_ctx* ctx, const float* wide, int rows, int inter, float* act, unsigned* act_words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && inter > 0, "geglu: bad size");
+        geglu_fwd(ctx, wide, rows, inter, act, nullptr, cleared(ctx, act_words));
+    });
+}
+
+int laya_geglu_bwd_w(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide,
+                     unsigned* dwide_words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(rows >= 0 && inter > 0, "geglu_bwd: bad size");
+        geglu_bwd(ctx, wide, dact, rows, inter, dwide, cleared(ctx, dwide_words));
+    });
+}
+
+int laya_attention_fwd_w(laya_ctx* ctx, const float* qkv, const laya_segments* segs, int hidden, int heads,
+                         float scale, int half_window, const laya_rotary* rot, float p_drop, uint64_t seed,
+                         float* context, float* lse, const unsigned* qkv_words, unsigned* context_words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(context && lse, "attention: null output");
+        const AttentionArgs a = attention_args(qkv, segs, hidden, heads, scale, half_window, rot, p_drop, seed);
+        const Given gq(qkv_words);
+        attention_fwd(ctx, a, context, lse, nullptr, cleared(ctx, context_words), gq.ref);
+    });
+}
+
+int laya_attention_bwd_w(laya_ctx* ctx, const float* qkv, const laya_segments* segs, int hidden, int heads,
+                         float scale, int half_window, const laya_rotary* rot, float p_drop, uint64_t seed,
+                         const float* context, const float* lse, const float* dcontext, float* dqkv,
+                         const unsigned* qkv_words, const unsigned* dcontext_words, unsigned* dqkv_words) {
+    return guarded([&] {
+        require_ctx(ctx);
+        LAYA_REQUIRE(dcontext && dqkv, "attention_bwd: null tensor");
+        const AttentionArgs a = attention_args(qkv, segs, hidden, heads, scale, half_window, rot, p_drop, seed);
+        const Given gq(qkv_words), gdo(dcontext_words);
+        if (!context || !lse) {  // as laya_attention_bwd: the forward once more into scratch
+            const size_t rows = (size_t)std::max(a.rows, 1);
+            float* c = static_cast<float*>(ctx->workspace(6, sizeof(float) * rows * hidden));
+            float* l = static_cast<float*>(ctx->workspace(7, sizeof(float) * rows * heads));
+            attention_fwd(ctx, a, c, l, nullptr, nullptr, gq.ref);
+            context = c;
+            lse = l;
+        }
+        attention_bwd(ctx, a, a.rows, context, lse, dcontext, dqkv, cleared(ctx, dqkv_words), gq.ref, gdo.ref);
+    });
+}
+
 int laya_embedding_fwd(laya_ctx* ctx, const int* ids, int n, const float* E, int vocab, int hidden, float* out,
                        int* bad_count) {
     return guarded([&] {

@@ -356,7 +356,7 @@ void layernorm_bwd_deferred(laya_ctx* ctx, const float* x, int rows, int n, cons
                             unsigned* amax = nullptr);
 void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
                    float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
-                   const int* gather_ids = nullptr);
+                   const int* gather_ids = nullptr, unsigned* amax = nullptr);
 
 // The allocation-free LayerNorm backward: partials in a static device array whose per-device address
 // noalloc_scratch_init resolves once (laya_ctx_create calls it with the device current).

@@ -359,8 +359,9 @@ static void layernorm_bwd_impl(laya_ctx* ctx, const float* x, int rows, int n, c
 
 void layernorm_bwd(laya_ctx* ctx, const float* x, int rows, int n, const float* w, float eps, const float* dy,
                    float* dx, float* dgamma, float* dbeta, const float* mean, const float* rstd,
-                   const int* gather_ids) {
-    layernorm_bwd_impl(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, gather_ids, nullptr, true);
+                   const int* gather_ids, unsigned* amax) {
+    layernorm_bwd_impl(ctx, x, rows, n, w, eps, dy, dx, dgamma, dbeta, mean, rstd, gather_ids, nullptr, true,
+                       nullptr, amax);
 }
 
 int ln_bwd_partial_rows(int rows) { return ln_bwd_blocks(std::max(rows, 1)); }

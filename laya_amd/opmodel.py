@@ -139,6 +139,12 @@ class OpLevelModel:
         self.steps = 0
         self.head_dropout = 0.1
         self.carry_attention_state = True
+        # The operands' magnitude word groups, kept beside the encoder's buffers the host writes through the
+        # per-op calls (laya_hip.h's _w variants): the products read them instead of measuring (False: every
+        # product measures its operands, as a binding without them does).
+        self.carry_words = True
+        self._words: Dict[str, DeviceArray] = {}
+        self._dout_words_valid = False
         self.rot_global = laya.Rotary(ctx, config.encoder.head_dim, config.encoder.global_rope_theta, 1024)
         self.rot_local = laya.Rotary(ctx, config.encoder.head_dim, config.encoder.local_rope_theta, 1024)
         self.s = _Scratch(ctx)
@@ -146,6 +152,9 @@ class OpLevelModel:
 
     def close(self) -> None:
         self.s.free()
+        for w in self._words.values():
+            w.free()
+        self._words.clear()
         for a in self.arena.values():
             a.free()
         self.norm.free()
@@ -169,6 +178,14 @@ class OpLevelModel:
     def _head(self, j: int, what: str) -> _Param:
         return self.p.get(f"head.layers.{j}.{what}")
 
+    def _w(self, key: str) -> Optional[DeviceArray]:
+        """The magnitude word group kept for buffer `key`, or None when words are not carried."""
+        if not self.carry_words:
+            return None
+        if key not in self._words:
+            self._words[key] = laya.magnitude_words(self.ctx)
+        return self._words[key]
+
     def _salt(self, seed: int, layer: int, site: int) -> int:
         return laya.mix(seed, layer * 16 + site + 1)  # TrainableDecisionModel.cs:426
 
@@ -185,7 +202,7 @@ class OpLevelModel:
                                        .data.ptr, e.vocab_size, d, emb.ptr, None))
         x = s.get("x0", (T, d))
         laya.layer_norm(emb, T, d, self.p["encoder.embeddings.norm.weight"], self.p.get("encoder.embeddings.norm.bias"),
-                        eps, x, s.get("emb_mean", (T,)), s.get("emb_rstd", (T,)))
+                        eps, x, s.get("emb_mean", (T,)), s.get("emb_rstd", (T,)), y_words=self._w("x0"))
         for l in range(e.num_hidden_layers):
             x = self._encoder_layer(l, x)
         fin = s.get("final", (T, d))
@@ -227,27 +244,32 @@ class OpLevelModel:
         eps = self.config.encoder.norm_eps
         g = lambda k, shape: s.get(f"e{l}.{k}", shape)  # noqa: E731
         norm = self._enc(l, "attn_norm.weight")
+        w = lambda k: self._w(f"e{l}.{k}")  # noqa: E731
         if norm is None:
-            normed = x  # layer 0: nn.Identity
+            normed, wn = x, (self._w("x0") if l == 0 else None)  # layer 0: nn.Identity
         else:
-            normed = g("normed", (T, d))
+            normed, wn = g("normed", (T, d)), w("normed")
             laya.layer_norm(x, T, d, norm, self._enc(l, "attn_norm.bias"), eps, normed, g("mean1", (T,)),
-                            g("rstd1", (T,)))
+                            g("rstd1", (T,)), y_words=wn)
         qkv = g("qkv", (T, 3 * d))
-        laya.linear(self._enc(l, "attn.Wqkv.weight"), self._enc(l, "attn.Wqkv.bias"), normed, T, qkv)
+        laya.linear(self._enc(l, "attn.Wqkv.weight"), self._enc(l, "attn.Wqkv.bias"), normed, T, qkv, x_words=wn)
         context, lse = g("ctx", (T, d)), g("lse", (T * self.config.encoder.num_attention_heads,))
-        laya.attention_forward(qkv, b.segments, self._attention_shape(self.config.encoder.layer_kinds[l]), context, lse)
+        # (q and k are rotated into a copy that measures itself: qkv's own words would go unread)
+        laya.attention_forward(qkv, b.segments, self._attention_shape(self.config.encoder.layer_kinds[l]), context, lse,
+                               context_words=w("ctx"))
         res = g("res", (T, d))
-        laya.linear(self._enc(l, "attn.Wo.weight"), self._enc(l, "attn.Wo.bias"), context, T, res, residual=x)
+        laya.linear(self._enc(l, "attn.Wo.weight"), self._enc(l, "attn.Wo.bias"), context, T, res, residual=x,
+                    x_words=w("ctx"))
         mlpn = g("mlpn", (T, d))
         laya.layer_norm(res, T, d, self._enc(l, "mlp_norm.weight"), self._enc(l, "mlp_norm.bias"), eps, mlpn,
-                        g("mean2", (T,)), g("rstd2", (T,)))
+                        g("mean2", (T,)), g("rstd2", (T,)), y_words=w("mlpn"))
         wide = g("wide", (T, 2 * I))
-        laya.linear(self._enc(l, "mlp.Wi.weight"), self._enc(l, "mlp.Wi.bias"), mlpn, T, wide)
+        laya.linear(self._enc(l, "mlp.Wi.weight"), self._enc(l, "mlp.Wi.bias"), mlpn, T, wide, x_words=w("mlpn"))
         act = g("act", (T, I))
-        laya.geglu(ctx, wide, T, I, act)
+        laya.geglu(ctx, wide, T, I, act, act_words=w("act"))
         out = g("out", (T, d))
-        laya.linear(self._enc(l, "mlp.Wo.weight"), self._enc(l, "mlp.Wo.bias"), act, T, out, residual=res)
+        laya.linear(self._enc(l, "mlp.Wo.weight"), self._enc(l, "mlp.Wo.bias"), act, T, out, residual=res,
+                    x_words=w("act"))
         return out
 
     def _head_layer(self, j: int, x: _View, p: float, seed: int) -> _View:
@@ -317,7 +339,8 @@ class OpLevelModel:
         dx.fill(0.0)
         laya.layer_norm_backward(self.enc_out, T, d, self.p["encoder.final_norm.weight"],
                                  self.p.get("encoder.final_norm.bias"), eps, dstates, dx, s.get("fin_mean", (T,)),
-                                 s.get("fin_rstd", (T,)))
+                                 s.get("fin_rstd", (T,)), dx_words=self._w("dout"))
+        self._dout_words_valid = True
         for l in reversed(range(e.num_hidden_layers)):
             dx = self._encoder_layer_backward(l, dx)
         # Embedding norm and the token-order scatter (538-548)
@@ -337,31 +360,39 @@ class OpLevelModel:
         T, d, I = b.T, self.config.hidden, self.config.encoder.intermediate_size
         eps = self.config.encoder.norm_eps
         g = lambda k, shape: s.get(f"e{l}.{k}", shape)  # noqa: E731
+        w = lambda k: self._w(f"e{l}.{k}")  # noqa: E731
+        # dout's words while the last write to dout was a call that filled them
+        wdo = self._w("dout") if self._dout_words_valid else None
         d_act, d_wide, d_n = s.get("d_act", (T, I)), s.get("d_wide", (T, 2 * I)), s.get("d_n", (T, d))
         laya.linear_backward(self._enc(l, "mlp.Wo.weight"), self._enc(l, "mlp.Wo.bias"), g("act", (T, I)), dout, T,
-                             d_act)
-        laya.geglu_backward(ctx, g("wide", (T, 2 * I)), d_act, T, I, d_wide)
+                             d_act, x_words=w("act"), dy_words=wdo)
+        laya.geglu_backward(ctx, g("wide", (T, 2 * I)), d_act, T, I, d_wide, dwide_words=self._w("d_wide"))
         laya.linear_backward(self._enc(l, "mlp.Wi.weight"), self._enc(l, "mlp.Wi.bias"), g("mlpn", (T, d)), d_wide, T,
-                             d_n)
+                             d_n, x_words=w("mlpn"), dy_words=self._w("d_wide"))
         laya.layer_norm_backward(g("res", (T, d)), T, d, self._enc(l, "mlp_norm.weight"), self._enc(l, "mlp_norm.bias"),
-                                 eps, d_n, dout, g("mean2", (T,)), g("rstd2", (T,)))
+                                 eps, d_n, dout, g("mean2", (T,)), g("rstd2", (T,)), dx_words=self._w("dout"))
+        wdo = self._w("dout")
         d_ctx, d_qkv = s.get("d_ctx", (T, d)), s.get("d_qkv", (T, 3 * d))
         laya.linear_backward(self._enc(l, "attn.Wo.weight"), self._enc(l, "attn.Wo.bias"), g("ctx", (T, d)), dout, T,
-                             d_ctx)
+                             d_ctx, x_words=w("ctx"), dy_words=wdo, dx_words=self._w("d_ctx"))
         laya.attention_backward(g("qkv", (T, 3 * d)), b.segments,
                                 self._attention_shape(self.config.encoder.layer_kinds[l]), d_ctx, d_qkv,
-                                *self._saved(g, T, d, self.config.encoder.num_attention_heads))
+                                *self._saved(g, T, d, self.config.encoder.num_attention_heads),
+                                dcontext_words=self._w("d_ctx"), dqkv_words=self._w("d_qkv"))
         norm = self._enc(l, "attn_norm.weight")
         if norm is None:
             x_in = self.s.get("x0", (T, d)) if l == 0 else s.get(f"e{l - 1}.out", (T, d))
-            laya.linear_backward(self._enc(l, "attn.Wqkv.weight"), self._enc(l, "attn.Wqkv.bias"), x_in, d_qkv, T, d_n)
+            laya.linear_backward(self._enc(l, "attn.Wqkv.weight"), self._enc(l, "attn.Wqkv.bias"), x_in, d_qkv, T, d_n,
+                                 x_words=self._w("x0") if l == 0 else None, dy_words=self._w("d_qkv"))
             laya.add(ctx, dout, d_n)
+            self._dout_words_valid = False  # a plain add: dout's words no longer describe it
         else:
             laya.linear_backward(self._enc(l, "attn.Wqkv.weight"), self._enc(l, "attn.Wqkv.bias"), g("normed", (T, d)),
-                                 d_qkv, T, d_n)
+                                 d_qkv, T, d_n, x_words=w("normed"), dy_words=self._w("d_qkv"))
             x_in = self.s.get("x0", (T, d)) if l == 0 else s.get(f"e{l - 1}.out", (T, d))
             laya.layer_norm_backward(x_in, T, d, norm, self._enc(l, "attn_norm.bias"), eps, d_n, dout,
-                                     g("mean1", (T,)), g("rstd1", (T,)))
+                                     g("mean1", (T,)), g("rstd1", (T,)), dx_words=self._w("dout"))
+            self._dout_words_valid = True
         return dout
 
     def _head_layer_backward(self, j: int, dout: _View) -> _View:

@@ -46,42 +46,79 @@ def _h(ctx: Context):
     return ctx.handle
 
 
+# Operand magnitude words (laya_hip.h: LAYA_AMAX_WORDS): a group of uint32 device words a binding may keep
+# beside a buffer. The functions below take them as keyword arguments: an output's group receives the largest
+# finite magnitude of what the call writes, and an input's group stands for that input in place of a measuring
+# pass, while nothing else has written the input since the group was filled.
+AMAX_WORDS = 1024
+
+
+def magnitude_words(ctx: Context) -> DeviceArray:
+    """A magnitude word group on the device (zeroed)."""
+    return DeviceArray.from_numpy(ctx, np.zeros(AMAX_WORDS, np.uint32))
+
+
+def measure_words(ctx: Context, x: DeviceArray, words: DeviceArray) -> None:
+    """Fill `words` with max|x| over x's finite elements (laya_amax)."""
+    check(lib().laya_amax(_h(ctx), x.ptr, x.size, words.ptr))
+
+
 # ----------------------------------------------------------------------------------- linear
 
 def linear(weight: Parameter, bias: Optional[Parameter], x: DeviceArray, rows: int, y: DeviceArray,
-           residual: Optional[DeviceArray] = None) -> None:
+           residual: Optional[DeviceArray] = None, x_words: Optional[DeviceArray] = None,
+           y_words: Optional[DeviceArray] = None) -> None:
     """Ops.Linear (Ops.cs:22-27): y = x·Wᵀ + b (+ residual, the skip add fused into the epilogue)."""
     out, inn = weight.shape
-    check(lib().laya_linear_fwd(_h(weight.ctx), x.ptr, rows, inn, weight.data.ptr, out,
-                                None if bias is None else bias.data.ptr, ptr(residual), y.ptr))
+    b = None if bias is None else bias.data.ptr
+    if x_words is None and y_words is None:
+        check(lib().laya_linear_fwd(_h(weight.ctx), x.ptr, rows, inn, weight.data.ptr, out, b, ptr(residual), y.ptr))
+    else:
+        check(lib().laya_linear_fwd_w(_h(weight.ctx), x.ptr, rows, inn, weight.data.ptr, out, b, ptr(residual), y.ptr,
+                                      ptr(x_words), None, ptr(y_words)))
 
 
 def linear_backward(weight: Parameter, bias: Optional[Parameter], x: DeviceArray, dy: DeviceArray, rows: int,
-                    dx: Optional[DeviceArray]) -> None:
+                    dx: Optional[DeviceArray], x_words: Optional[DeviceArray] = None,
+                    dy_words: Optional[DeviceArray] = None, dx_words: Optional[DeviceArray] = None) -> None:
     """Ops.LinearBackward (Ops.cs:33-69): dx = dy·W (overwritten), dW += dyᵀ·x, db += Σ dy."""
     out, inn = weight.shape
     dW = weight.gradient_buffer().ptr if weight.trainable else None
     db = bias.gradient_buffer().ptr if (bias is not None and bias.trainable) else None
-    check(lib().laya_linear_bwd(_h(weight.ctx), x.ptr, dy.ptr, rows, inn, out, weight.data.ptr, ptr(dx), dW, db))
+    if x_words is None and dy_words is None and dx_words is None:
+        check(lib().laya_linear_bwd(_h(weight.ctx), x.ptr, dy.ptr, rows, inn, out, weight.data.ptr, ptr(dx), dW, db))
+    else:
+        check(lib().laya_linear_bwd_w(_h(weight.ctx), x.ptr, dy.ptr, rows, inn, out, weight.data.ptr, ptr(dx), dW, db,
+                                      ptr(x_words), ptr(dy_words), None, ptr(dx_words)))
 
 
 # ------------------------------------------------------------------------------- layer norm
 
 def layer_norm(x: DeviceArray, rows: int, n: int, weight: Parameter, bias: Optional[Parameter], epsilon: float,
-               y: DeviceArray, mean: Optional[DeviceArray] = None, rstd: Optional[DeviceArray] = None) -> None:
+               y: DeviceArray, mean: Optional[DeviceArray] = None, rstd: Optional[DeviceArray] = None,
+               y_words: Optional[DeviceArray] = None) -> None:
     """Ops.LayerNorm (Ops.cs:103-110); optionally keeps the row statistics for the backward."""
-    check(lib().laya_layernorm_fwd(_h(weight.ctx), x.ptr, rows, n, weight.data.ptr,
-                                   None if bias is None else bias.data.ptr, epsilon, y.ptr, ptr(mean), ptr(rstd)))
+    b = None if bias is None else bias.data.ptr
+    if y_words is None:
+        check(lib().laya_layernorm_fwd(_h(weight.ctx), x.ptr, rows, n, weight.data.ptr, b, epsilon, y.ptr, ptr(mean),
+                                       ptr(rstd)))
+    else:
+        check(lib().laya_layernorm_fwd_w(_h(weight.ctx), x.ptr, rows, n, weight.data.ptr, b, epsilon, y.ptr,
+                                         ptr(mean), ptr(rstd), y_words.ptr))
 
 
 def layer_norm_backward(x: DeviceArray, rows: int, n: int, weight: Parameter, bias: Optional[Parameter],
                         epsilon: float, dy: DeviceArray, dx: DeviceArray, mean: Optional[DeviceArray] = None,
-                        rstd: Optional[DeviceArray] = None) -> None:
+                        rstd: Optional[DeviceArray] = None, dx_words: Optional[DeviceArray] = None) -> None:
     """Ops.LayerNormBackward (Ops.cs:117-186): dx += …, dγ += Σ dy·x̂, dβ += Σ dy."""
     dg = weight.gradient_buffer().ptr if weight.trainable else None
     dbeta = bias.gradient_buffer().ptr if (bias is not None and bias.trainable) else None
-    check(lib().laya_layernorm_bwd(_h(weight.ctx), x.ptr, rows, n, weight.data.ptr, epsilon, dy.ptr, dx.ptr, dg,
-                                   dbeta, ptr(mean), ptr(rstd)))
+    if dx_words is None:
+        check(lib().laya_layernorm_bwd(_h(weight.ctx), x.ptr, rows, n, weight.data.ptr, epsilon, dy.ptr, dx.ptr, dg,
+                                       dbeta, ptr(mean), ptr(rstd)))
+    else:
+        check(lib().laya_layernorm_bwd_w(_h(weight.ctx), x.ptr, rows, n, weight.data.ptr, epsilon, dy.ptr, dx.ptr,
+                                         dg, dbeta, ptr(mean), ptr(rstd), dx_words.ptr))
 
 
 # ------------------------------------------------------------------------------ activations
@@ -96,13 +133,20 @@ def gelu_backward(ctx: Context, u: DeviceArray, grad: DeviceArray) -> None:
     check(lib().laya_gelu_bwd(_h(ctx), u.ptr, grad.ptr, grad.size))
 
 
-def geglu(ctx: Context, wide: DeviceArray, rows: int, intermediate: int, act: DeviceArray) -> None:
-    check(lib().laya_geglu_fwd(_h(ctx), wide.ptr, rows, intermediate, act.ptr))
+def geglu(ctx: Context, wide: DeviceArray, rows: int, intermediate: int, act: DeviceArray,
+          act_words: Optional[DeviceArray] = None) -> None:
+    if act_words is None:
+        check(lib().laya_geglu_fwd(_h(ctx), wide.ptr, rows, intermediate, act.ptr))
+    else:
+        check(lib().laya_geglu_fwd_w(_h(ctx), wide.ptr, rows, intermediate, act.ptr, act_words.ptr))
 
 
 def geglu_backward(ctx: Context, wide: DeviceArray, dact: DeviceArray, rows: int, intermediate: int,
-                   dwide: DeviceArray) -> None:
-    check(lib().laya_geglu_bwd(_h(ctx), wide.ptr, dact.ptr, rows, intermediate, dwide.ptr))
+                   dwide: DeviceArray, dwide_words: Optional[DeviceArray] = None) -> None:
+    if dwide_words is None:
+        check(lib().laya_geglu_bwd(_h(ctx), wide.ptr, dact.ptr, rows, intermediate, dwide.ptr))
+    else:
+        check(lib().laya_geglu_bwd_w(_h(ctx), wide.ptr, dact.ptr, rows, intermediate, dwide.ptr, dwide_words.ptr))
 
 
 def add(ctx: Context, dst: DeviceArray, src: DeviceArray) -> None:
@@ -221,26 +265,37 @@ def _hw(shape: AttentionShape) -> int:
 
 
 def attention_forward(qkv: DeviceArray, segments: Segments, shape: AttentionShape, context: DeviceArray,
-                      lse: DeviceArray) -> None:
+                      lse: DeviceArray, qkv_words: Optional[DeviceArray] = None,
+                      context_words: Optional[DeviceArray] = None) -> None:
     """Ops.AttentionForward (Ops.cs:275-277); also writes the row log-sum-exp the backward may reuse."""
     if shape.rotary is not None:
         shape.rotary.ensure(segments.max_len)
-    check(lib().laya_attention_fwd(_h(qkv.ctx), qkv.ptr, segments.handle, shape.hidden, shape.heads, shape.scale,
-                                   _hw(shape), None if shape.rotary is None else shape.rotary.handle, shape.dropout,
-                                   shape.seed & (2 ** 64 - 1), context.ptr, lse.ptr))
+    args = (_h(qkv.ctx), qkv.ptr, segments.handle, shape.hidden, shape.heads, shape.scale, _hw(shape),
+            None if shape.rotary is None else shape.rotary.handle, shape.dropout, shape.seed & (2 ** 64 - 1),
+            context.ptr, lse.ptr)
+    if qkv_words is None and context_words is None:
+        check(lib().laya_attention_fwd(*args))
+    else:
+        check(lib().laya_attention_fwd_w(*args, ptr(qkv_words), ptr(context_words)))
 
 
 def attention_backward(qkv: DeviceArray, segments: Segments, shape: AttentionShape, dcontext: DeviceArray,
                        dqkv: DeviceArray, context: Optional[DeviceArray] = None,
-                       lse: Optional[DeviceArray] = None) -> None:
+                       lse: Optional[DeviceArray] = None, qkv_words: Optional[DeviceArray] = None,
+                       dcontext_words: Optional[DeviceArray] = None,
+                       dqkv_words: Optional[DeviceArray] = None) -> None:
     """Ops.AttentionBackward (Ops.cs:280-282): dq, dk, dv written (not added) into dqkv. The forward's
     context and lse are reused when given; without them the row statistics are recomputed, as the
     reference recomputes each row's softmax."""
     if shape.rotary is not None:
         shape.rotary.ensure(segments.max_len)
-    check(lib().laya_attention_bwd(_h(qkv.ctx), qkv.ptr, segments.handle, shape.hidden, shape.heads, shape.scale,
-                                   _hw(shape), None if shape.rotary is None else shape.rotary.handle, shape.dropout,
-                                   shape.seed & (2 ** 64 - 1), ptr(context), ptr(lse), dcontext.ptr, dqkv.ptr))
+    args = (_h(qkv.ctx), qkv.ptr, segments.handle, shape.hidden, shape.heads, shape.scale, _hw(shape),
+            None if shape.rotary is None else shape.rotary.handle, shape.dropout, shape.seed & (2 ** 64 - 1),
+            ptr(context), ptr(lse), dcontext.ptr, dqkv.ptr)
+    if qkv_words is None and dcontext_words is None and dqkv_words is None:
+        check(lib().laya_attention_bwd(*args))
+    else:
+        check(lib().laya_attention_bwd_w(*args, ptr(qkv_words), ptr(dcontext_words), ptr(dqkv_words)))
 
 
 def default_scale(head_dim: int) -> float:

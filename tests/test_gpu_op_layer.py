@@ -233,3 +233,35 @@ def test_whole_step_from_op_entry_points_matches_the_oracle_and_the_model_driver
     assert not np.any(om.grad("scorer.1.weight"))  # the step cleared the gradients
     ob.close()
     om.close()
+
+
+def test_op_path_magnitude_words_change_nothing(ctx):
+    """A binding that keeps the encoder operands' magnitude words (the _w entry points: producers fill them, the
+    products read them instead of measuring) computes the same step as one that keeps none: each group holds
+    the same largest magnitude a measuring pass would find, so the scales, the products and every gradient
+    agree bit for bit (ModernBERT-base widths, 3 encoder layers, the head and scorer, five ragged items)."""
+    from helpers import fixture_params, mid_config, mixed_batch
+    from laya_amd.device import DeviceArray
+    from laya_amd.opmodel import OpBatch, OpLevelModel
+    mc = mid_config(layers=3)
+    o = oracle.OracleModel(mc)
+    params = fixture_params(o.shapes, 31)
+    batch = mixed_batch(np.random.default_rng(32), [300, 200, 129, 64, 17], mc.encoder.vocab_size)
+    rng = np.random.default_rng(33)
+    targets = np.concatenate([np.eye(k, dtype=np.float32)[rng.integers(k)] for k in batch.n_options])
+    runs = []
+    for words in (False, True):
+        om = OpLevelModel(mc, {n: params[n] for n in o.names}, ctx)
+        om.carry_words = words
+        ob = OpBatch(ctx, batch, targets, mc.encoder.vocab_size)
+        logits = om.forward(ob, 9, training=True)
+        dl = DeviceArray(ctx, (batch.n_markers,))
+        laya.softmax_ce_backward(ctx, logits, ob.targets, ob.offsets, batch.n_items, 1.0, float(batch.n_items), dl)
+        om.backward(dl)
+        runs.append((logits.numpy(), {n: om.grad(n) for n in o.names if o.has_grad(n)}))
+        ob.close()
+        om.close()
+    (l0, g0), (l1, g1) = runs
+    np.testing.assert_array_equal(l0, l1)
+    for n in g0:
+        np.testing.assert_array_equal(g0[n], g1[n], err_msg=n)
