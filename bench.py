@@ -362,6 +362,11 @@ def main():
     ctx.sync()
     elapsed = time.perf_counter() - t0
     tokens = sum(b.n_tokens for b, _ in batches[args.warmup:])
+    # As for the per-op leg: a rate of steps on non-finite weights is no rate of this path.
+    bad = [n for n in (model.names[1], model.names[len(model.names) // 2], model.names[-1])
+           if not np.isfinite(model.param(n)).all()]
+    if bad:
+        raise SystemExit(f"model API: {bad[0]} is not finite after the timed steps")
     prof = {}
     if not args.no_profile:
         # A separate pass over the same batches with HIP events around every launch, for the per-kernel
