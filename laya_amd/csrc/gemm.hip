@@ -39,7 +39,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // Epilogue modes, fixed at compile time so each kernel carries only its own store path.
-enum : int { STORE = 0, ACCUMULATE = 1, PARTIAL = 2, STORE_ROPE = 3 };
+enum : int { STORE = 0, ACCUMULATE = 1, PARTIAL = 2, STORE_ROPE = 3, STORE_GEGLU = 4 };
 
 struct GemmParams {
     const float* A;
@@ -72,6 +72,13 @@ struct GemmParams {
     // Two-piece NT products: B's values are bf16 values (fp32 holding a bf16), so sb·B is one fp16 piece
     // (see split1h_4) and the kernels that honour it skip B's low plane and its products.
     int b_one;
+    // STORE_GEGLU (the 256-wide NT kernels): C is GeGLU's input [M, 2·inter] (both halves stored, from B's
+    // rows taken in pairs, geglu_b_row), act [M, inter] receives gelu(first half)·(second half) beside it,
+    // act16 (optional) its bf16 copy, amax_act (optional) its magnitude word group.
+    float* act;
+    __bf16* act16;
+    unsigned* amax_act;
+    int inter;
 };
 
 // ------------------------------------------------------------------------------ shared pieces
@@ -973,6 +980,41 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* p, unsig
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)bytes, 0x00020000);
 }
 
+// GeGLU's product y = x·Wᵀ, W = [first half; second half] ([2·inter, K]), with the GeGLU applied in the epilogue
+// (STORE_GEGLU): a 256-wide tile covers 128 output columns a0 … a0 + 127 of both halves. Tile row ρ of B
+// (wave column wn = ρ / 64, block j = ρ / 32 mod 2, lane l = ρ mod 32) is W's row a (j = 0) or inter + a (j = 1),
+// a = a0 + 32·wn + l, so a wave's two column blocks hold the two halves of the same 32 columns, lane by lane.
+__device__ __forceinline__ int geglu_b_row(int rho, int a0, int inter) {
+    const int a = min(a0 + 32 * (rho >> 6) + (rho & 31), inter - 1);
+    return ((rho >> 5) & 1) ? inter + a : a;
+}
+
+// The STORE_GEGLU epilogue of one wave's rows (the accumulator layout store_acc takes for AK, BKC): both halves
+// into C at their own columns, and act = gelu(first)·second (geglu_fwd's arithmetic) with its bf16 copy; am
+// collects max|act|. c.n0 is the tile's first output column a0.
+template <bool GUARD, int NI>
+__device__ __forceinline__ void store_geglu(const GemmParams& p, const TileCoord& c, const f32x16 (&acc)[NI][2], int wm,
+                                            int wn, int lr, int kh, unsigned* am) {
+    const int a = c.n0 + 32 * wn + lr;
+    if (GUARD && a >= p.inter) return;
+    const float bg = p.bias ? p.bias[a] : 0.0f, bu = p.bias ? p.bias[p.inter + a] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = c.m0 + wm * 64 + 32 * i + 8 * (r >> 2) + kh + (r & 3);
+            if (GUARD && row >= p.M) continue;
+            const float g = acc[i][0][r] + bg, u = acc[i][1][r] + bu;
+            float* w = p.C + (long)row * p.ldc;
+            w[a] = g;
+            w[p.inter + a] = u;
+            const float v = gelu_f(g) * u;
+            p.act[(long)row * p.inter + a] = v;
+            if (p.act16) p.act16[(long)row * p.inter + a] = (__bf16)v;
+            *am = max(*am, amax_bits(v));
+        }
+}
+
 // A 256-row k-contiguous operand's 16-deep stage: thread t holds 4 consecutive k of rows t/4 and t/4 + 128.
 // Buffer loads: the per-thread row offset in a VGPR, the stage's k offset in the wave-uniform SGPR offset.
 struct OperandW {
@@ -984,6 +1026,13 @@ struct OperandW {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             off[i] = ((unsigned)min(mn0 + (tid >> 2) + 128 * i, MN - 1) * (unsigned)ldl + ((tid & 3) << 2)) * 4u;
+    }
+    // The GeGLU form (STORE_GEGLU): tile row ρ is B's row geglu_b_row(ρ, a0, inter).
+    __device__ __forceinline__ OperandW(const float* s, long ldl, int a0, int inter, int tid, unsigned bytes, bool)
+        : rsrc(buffer_of(s, bytes)) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            off[i] = ((unsigned)geglu_b_row((tid >> 2) + 128 * i, a0, inter) * (unsigned)ldl + ((tid & 3) << 2)) * 4u;
     }
     __device__ __forceinline__ void full(int k0) {
 #pragma unroll
@@ -1164,7 +1213,8 @@ struct WideK<true> {
 // B bf16-valued, in one piece); NP = 1: the bf16 product, with AH / BH reading A / B from their bf16 copies.
 template <int MODE, int NP = 3, bool AH = false, bool BH = false, bool B1 = false>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
-    static_assert(MODE == STORE || MODE == STORE_ROPE, "whole-K NT epilogues");
+    static_assert(MODE == STORE || MODE == STORE_ROPE || MODE == STORE_GEGLU, "whole-K NT epilogues");
+    static_assert(MODE != STORE_GEGLU || (NP == 2 && !BH), "the GeGLU epilogue is a two-piece product's");
     static_assert(NP == 1 || !(AH || BH), "bf16 copies feed bf16 products");
     static_assert(NP == 2 || !B1, "one-piece B is a two-piece product's");
     PairScales ps;
@@ -1176,7 +1226,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     c.split = 0;
     c.t = t;
     c.m0 = tm * WT;
-    c.n0 = (t - tm * p.tiles_n) * WT;
+    c.n0 = (t - tm * p.tiles_n) * (MODE == STORE_GEGLU ? WT / 2 : WT);  // GeGLU: output columns of act
     c.kb = 0;
     c.ke = p.K;
     const int nt = p.K / BKQ;
@@ -1185,7 +1235,12 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
     const int wm = wave >> 2, wn = wave & 3;
     const int lr = lane & 31, half = lane >> 5;
     typename WideK<AH>::T a = WideK<AH>::make(p.A, p.A16, p.lda, c.m0, p.M, tid);
-    typename WideK<BH>::T b = WideK<BH>::make(p.B, p.B16, p.ldb, c.n0, p.N, tid);
+    typename WideK<BH>::T b = [&] {
+        if constexpr (MODE == STORE_GEGLU)
+            return OperandW(p.B, p.ldb, c.n0, p.inter, tid, (unsigned)(p.N * p.ldb * 4), true);
+        else
+            return WideK<BH>::make(p.B, p.B16, p.ldb, c.n0, p.N, tid);
+    }();
     auto kof = [&](int j) {
         const int q = j + rot;
         return (q >= nt ? q - nt : q) * BKQ;
@@ -1268,6 +1323,13 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) acc[1][q >> 1][q & 1] = park[q * WT_THREADS + te];
         }
+        if constexpr (MODE == STORE_GEGLU) {
+            if (cs.m0 + 128 <= p.M && c.n0 + WT / 2 <= p.inter)
+                store_geglu<false, 2>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2, &am);
+            else
+                store_geglu<true, 2>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2, &am);
+            continue;
+        } else {
         const bool full = cs.m0 + 128 <= p.M && c.n0 + WT <= p.N;
         // (Not with the RoPE epilogue, whose registers it would spill: the bound above, or launch_wide
         // measures C afterwards when there is a bias.)
@@ -1283,8 +1345,12 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6w_kernel(GemmParams p) {
         } else {
             store_acc<true, true, MODE, false, true, true>(p, cs, acc[s], we >> 2, we & 3, le & 31, (le >> 5) << 2);
         }
+        }
     }
-    if constexpr (NP == 2 && MODE != STORE_ROPE) block_amax_fold(am, p.amax_c);
+    if constexpr (MODE == STORE_GEGLU)
+        block_amax_fold(am, p.amax_act);
+    else if constexpr (NP == 2 && MODE != STORE_ROPE)
+        block_amax_fold(am, p.amax_c);
 }
 
 // ------------------------------------------------------------- operand magnitudes for two-piece products
@@ -1440,7 +1506,8 @@ __device__ __forceinline__ void mma_stage_t(const __bf16* A, const __bf16* B, f3
 // NP = 3: split products; NP = 2: two-piece fp16 products (B1: B bf16-valued, in one piece).
 template <int MODE, bool RES, int NP = 3, bool B1 = false>
 __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
-    static_assert(MODE == STORE || (MODE == STORE_ROPE && !RES), "whole-K NT epilogues");
+    static_assert(MODE == STORE || ((MODE == STORE_ROPE || MODE == STORE_GEGLU) && !RES), "whole-K NT epilogues");
+    static_assert(MODE != STORE_GEGLU || NP == 2, "the GeGLU epilogue is a two-piece product's");
     static_assert(NP == 2 || !B1, "one-piece B is a two-piece product's");
     PairScales ps;
     if constexpr (NP == 2) ps = PairScales(p.amax_a, p.amax_b);
@@ -1451,7 +1518,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     c.split = 0;
     c.t = t;
     c.m0 = tm * TM;
-    c.n0 = (t - tm * p.tiles_n) * WT;
+    c.n0 = (t - tm * p.tiles_n) * (MODE == STORE_GEGLU ? WT / 2 : WT);  // GeGLU: output columns of act
     c.kb = 0;
     c.ke = p.K;
     const int nt = p.K / BKQ;
@@ -1460,7 +1527,8 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     const int wm = wave >> 2, wn = wave & 3;
     const int lr = lane & 31, half = lane >> 5;
     OperandT a(p.A, p.lda, c.m0, p.M, tid, (unsigned)(p.M * p.lda * 4));
-    OperandW b(p.B, p.ldb, c.n0, p.N, tid, (unsigned)(p.N * p.ldb * 4));
+    OperandW b = MODE == STORE_GEGLU ? OperandW(p.B, p.ldb, c.n0, p.inter, tid, (unsigned)(p.N * p.ldb * 4), true)
+                                     : OperandW(p.B, p.ldb, c.n0, p.N, tid, (unsigned)(p.N * p.ldb * 4));
     auto kof = [&](int j) {
         const int q = j + rot;
         return (q >= nt ? q - nt : q) * BKQ;
@@ -1499,8 +1567,16 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
     // wave's three groups at 96·wm + 32·i.
     TileCoord cs = c;
     cs.m0 = c.m0 + 32 * wme;
+    unsigned am = 0;  // max|C| (GeGLU: max|act|) of the lane's stores, when the product keeps that word
+    if constexpr (MODE == STORE_GEGLU) {
+        if (c.m0 + TM <= p.M && c.n0 + WT / 2 <= p.inter)
+            store_geglu<false, 3>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2, &am);
+        else
+            store_geglu<true, 3>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2, &am);
+        block_amax_fold(am, p.amax_act);
+        return;
+    } else {
     const bool full = c.m0 + TM <= p.M && c.n0 + WT <= p.N;
-    unsigned am = 0;  // max|C| of the lane's stores, when the product keeps C's magnitude word
     if (NP == 2 && p.amax_c) {
         if (full)
             store_acc<true, true, MODE, RES, false, true, 3, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2,
@@ -1514,6 +1590,7 @@ __global__ __launch_bounds__(WT_THREADS, 1) void gemm_x6t_kernel(GemmParams p) {
         store_acc<true, true, MODE, RES, true, true>(p, cs, acc, wme, we & 3, le & 31, (le >> 5) << 2);
     }
     if constexpr (NP == 2) block_amax_fold(am, p.amax_c);
+    }
 }
 
 // The fp32 product from bf16 pieces (NP = 3) or, for float4 operands, two-piece fp16 products (NP = 2);
@@ -2914,6 +2991,57 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
     }();
     // C's magnitude: folded in by a two-piece kernel's epilogue, else measured after the product.
     if (amax_c && !p.amax_c) absmax_into(ctx, C, M, N, N, amax_c);
+}
+
+void gemm_geglu(laya_ctx* ctx, int M, int inter, int K, const float* x, const float* W, const float* bias, float* wide,
+                float* act, __bf16* act16, const __bf16* x16, const __bf16* W16, AmaxRef amax_x, AmaxRef amax_W,
+                unsigned* amax_act) {
+    if (M == 0) return;
+    const int N = 2 * inter;
+    GemmParams p = make_params(M, N, K, x, K, W, K, wide, N, bias, nullptr, 0);
+    p.A16 = x16;
+    p.B16 = W16;
+    p.mode = STORE;
+    const int blocks = p.tiles_m * p.tiles_n;
+    // Where gemm() itself would run the product as two-piece products on 256-wide tiles (launch_x6's choice).
+    bool fuse = (ctx->matmul_pair & 1) && !(ctx->matmul_bf16 & 1) && (ctx->matmul_split & 1) && inter % 4 == 0 &&
+                set_splits(p, fill_splits(ctx, blocks, K, 128)) == 1 && gemm_fits_h(p, true, true) &&
+                operand_fast(p.A, p.lda, p.vec_a, true, p.M, p.K) && operand_fast(p.B, p.ldb, p.vec_b, true, p.N, p.K);
+    const bool wide_tiles = fuse && wide_tiles_pay(ctx, p, three_per_cu(ctx, blocks));
+    fuse = fuse && (wide_tiles || tall_tiles_pay(ctx, p));
+    if (!fuse) {
+        gemm(ctx, GemmLayout::NT, GemmEpilogue::Store, M, N, K, x, K, W, K, wide, N, bias, nullptr, 0, x16, W16, amax_x,
+             amax_W);
+        geglu_fwd(ctx, wide, M, inter, act, act16, amax_act);
+        return;
+    }
+    prepare_pair_nt(ctx, p, amax_x, amax_W);
+    p.mode = STORE_GEGLU;
+    p.act = act;
+    p.act16 = act16;
+    p.amax_act = amax_act;
+    p.inter = inter;
+    p.tiles_n = (inter + WT / 2 - 1) / (WT / 2);
+    ProfileScope scope(ctx, "gemm_nt_x6", 2.0 * M * N * (double)K, 0.0);
+    if (wide_tiles) {
+        p.tiles_m = (M + WT - 1) / WT;
+        const dim3 g(p.tiles_m * p.tiles_n), b(WT_THREADS);
+        profile_rename(p.b_one ? "gemm_nt_geglu_h2b1w" : "gemm_nt_geglu_h2w");
+        if (p.b_one)
+            LAYA_LAUNCH((gemm_x6w_kernel<STORE_GEGLU, 2, false, false, true>), g, b, 0, ctx->stream, p);
+        else
+            LAYA_LAUNCH((gemm_x6w_kernel<STORE_GEGLU, 2>), g, b, 0, ctx->stream, p);
+        check_launch("gemm_x6w_kernel");
+    } else {
+        p.tiles_m = (M + TM - 1) / TM;
+        const dim3 g(p.tiles_m * p.tiles_n), b(WT_THREADS);
+        profile_rename(p.b_one ? "gemm_nt_geglu_h2b1t" : "gemm_nt_geglu_h2t");
+        if (p.b_one)
+            LAYA_LAUNCH((gemm_x6t_kernel<STORE_GEGLU, false, 2, true>), g, b, 0, ctx->stream, p);
+        else
+            LAYA_LAUNCH((gemm_x6t_kernel<STORE_GEGLU, false, 2>), g, b, 0, ctx->stream, p);
+        check_launch("gemm_x6t_kernel");
+    }
 }
 
 // The balanced static schedule of a backward pair, when every worker's whole dX tiles fit in its share of

@@ -797,8 +797,8 @@ void encoder_forward(laya_model* m, int l, bool output = true) {
     linear(m, a.ctx, T, d, L.wo, L.wo_b, d, a.x, a.res, a.ctx16, m->aref(m->enc_site(l, 1)));  // x1 = x + attn
     layernorm_fwd(ctx, a.res, T, d, m->W(L.mlp_norm), m->W(L.mlp_norm_b), eps, a.mlpn, a.mean2, a.rstd2, nullptr,
                   nullptr, nullptr, a.mlpn16, m->produce(m->aref(m->enc_site(l, 2)), 7));
-    linear(m, a.mlpn, T, d, L.wi, L.wi_b, 2 * I, nullptr, a.wide, a.mlpn16, m->aref(m->enc_site(l, 2)));
-    geglu_fwd(ctx, a.wide, T, I, a.act, a.act16, m->produce(m->aref(m->enc_site(l, 3)), 7));
+    gemm_geglu(ctx, T, I, d, a.mlpn, m->PWt(L.wi), m->W(L.wi_b), a.wide, a.act, a.act16, a.mlpn16, m->W16(L.wi),
+               m->aref(m->enc_site(l, 2)), m->wref(L.wi), m->produce(m->aref(m->enc_site(l, 3)), 7));
     if (output)  // x2 = x1 + mlp
         linear(m, a.act, T, I, L.mlp_wo, L.mlp_wo_b, d, a.res, out, a.act16, m->aref(m->enc_site(l, 3)));
 }

@@ -45,6 +45,16 @@ def ctx():
 # (the default) or three-piece bf16 splits everywhere.
 KERNELS = {"fp32": ("gemm_bwd_pair_h2w", "gemm_nt_h2w", "gemm_nt_h2t", "attention_bwd_dkv_h2"),
            "fp32-split3": ("gemm_bwd_pair_x6w", "gemm_nt_x6w", "gemm_nt_x6t", "attention_bwd_dkv_x6")}
+# The GeGLU input product with the GeGLU in its epilogue, on 192 x 256 tiles (two-piece products only; the
+# three-piece policy runs the product on the tall kernel and GeGLU after it).
+GEGLU_TALL = {"fp32": "gemm_nt_geglu_h2t", "fp32-split3": "gemm_nt_x6t"}
+
+
+def _tall_launches(prof, policy):
+    """Launches of the 192 x 256 NT kernels: the plain products and the GeGLU-fused ones."""
+    tall = KERNELS[policy][2]
+    fused = GEGLU_TALL[policy]
+    return prof.get(tall, {}).get("launches", 0) + (prof.get(fused, {}).get("launches", 0) if fused != tall else 0)
 
 
 def _step(ctx, workload, policy="fp32"):
@@ -98,14 +108,16 @@ def test_headline_batch_32x512_every_gradient_matches_fp64(ctx, policy):
     print(f"full size: ModernBERT-base 22 layers, batch 32 x 512 padded (14344 tokens), {policy}", flush=True)
     m, fx, batch, logits, prof = _step(ctx, "b32x512", policy)
     assert np.abs(logits - fx["logits"]).max() < 1e-4
-    pair, wide, tall, _ = KERNELS[policy]
+    pair, wide, _, _ = KERNELS[policy]
     # The wide kernels this workload's timing rests on are the ones under test.
     assert prof.get(pair, {}).get("launches", 0) >= 90, sorted(prof)
     # At 14,344 rows the 2304-wide products would need a third round of 256 × 256 tiles, so they and the
     # 768-wide ones (RoPE and residual epilogues included) run on 192 × 256 tiles; the head's 3072-wide
     # products take the wide forward kernel.
     assert prof.get(wide, {}).get("launches", 0) >= 2, sorted(prof)
-    assert prof.get(tall, {}).get("launches", 0) >= 88, sorted(prof)
+    assert _tall_launches(prof, policy) >= 88, sorted(prof)
+    # One GeGLU-fused input product per layer.
+    assert prof.get(GEGLU_TALL[policy], {}).get("launches", 0) >= 22, sorted(prof)
     _check_gradients(m, fx)
     m.close()
 
@@ -197,7 +209,7 @@ def test_benchmark_step_itself_matches_fp64(ctx, policy, workload):
         pair, _, tall, dkv = KERNELS[policy]
         if workload == "b32x512":
             assert prof.get(pair, {}).get("launches", 0) >= 90, sorted(prof)
-            assert prof.get(tall, {}).get("launches", 0) >= 88, sorted(prof)
+            assert _tall_launches(prof, policy) >= 88, sorted(prof)
         else:
             assert prof.get(dkv, {}).get("launches", 0) == 24, sorted(prof)
             assert prof.get(tall, {}).get("launches", 0) >= 22, sorted(prof)

@@ -127,9 +127,10 @@ def test_modernbert_base_width_gradients_match_the_oracle(ctx):
 
 def test_wide_tile_forward_matches_the_oracle(ctx):
     """4448 tokens at d = 768: the QKV projection (RoPE in its epilogue, no bias: qkv's magnitude is a bound
-    folded in before the epilogue) and the GeGLU input projection run on 256 × 256 tiles (asserted from the
-    live profile); the logits match the fp64 oracle to 1e-5, and every gradient of a backward that reads those
-    activations (attention reads qkv's magnitude word) is within max(1e-4, 4 × the fp32 oracle's error) of fp64."""
+    folded in before the epilogue) runs on 256 × 256 tiles and the GeGLU input projection with GeGLU in its
+    epilogue (both asserted from the live profile); the logits match the fp64 oracle to 1e-5, and every gradient
+    of a backward that reads those activations (attention reads qkv's magnitude word) is within max(1e-4, 4 ×
+    the fp32 oracle's error) of fp64."""
     from laya_amd.model import TrainableDecisionModel
     print("model: d=768, 1 global layer, 4448 tokens", flush=True)
     mc, o, params, batch = _mid_case(layers=1, lengths=(2048, 1500, 900))
@@ -145,6 +146,7 @@ def test_wide_tile_forward_matches_the_oracle(ctx):
     lg = m.forward(batch, training=False)
     prof = ctx.profile_end()
     assert prof.get("gemm_nt_h2w", {}).get("launches", 0) >= 2, sorted(prof)
+    assert any(k.startswith("gemm_nt_geglu_") for k in prof) and "geglu_fwd" not in prof, sorted(prof)
     assert rel_l2(o64.forward(batch, training=False, keep_tape=False), lg) < 1e-5
     m.backward(dlogits)
     worst = 0.0
@@ -161,9 +163,10 @@ def test_wide_tile_forward_matches_the_oracle(ctx):
 
 def test_biased_encoder_on_wide_tiles_gradients_match_the_oracle(ctx):
     """ModernBERT's optional biases (attention_bias, mlp_bias, norm_bias: ModernBertConfig) at 4448 tokens,
-    d = 768, one global layer: the QKV projection (bias, then RoPE, in its epilogue) and the GeGLU input
-    projection take 256 × 256 tiles, and qkv's magnitude for the two-piece attention is measured after the
-    biased product. Logits to 1e-5 and every gradient to max(1e-4, 4 × the fp32 oracle's error) of fp64."""
+    d = 768, one global layer: the QKV projection (bias, then RoPE, in its epilogue) takes 256 × 256 tiles, the
+    GeGLU input projection has bias, then GeGLU, in its epilogue, and qkv's magnitude for the two-piece
+    attention is measured after the biased product. Logits to 1e-5 and every gradient to max(1e-4, 4 × the
+    fp32 oracle's error) of fp64."""
     from laya_amd.model import TrainableDecisionModel
     print("model: d=768, 1 global layer with biases, 4448 tokens", flush=True)
     mc = mid_config(layers=1)
@@ -184,6 +187,7 @@ def test_biased_encoder_on_wide_tiles_gradients_match_the_oracle(ctx):
     lg = m.forward(batch, training=True, seed=11)
     prof = ctx.profile_end()
     assert prof.get("gemm_nt_h2w", {}).get("launches", 0) >= 2, sorted(prof)
+    assert any(k.startswith("gemm_nt_geglu_") for k in prof) and "geglu_fwd" not in prof, sorted(prof)
     assert rel_l2(o64.forward(batch, training=True, keep_tape=False, seed=11), lg) < 1e-5
     m.backward(dlogits)
     worst = 0.0
@@ -196,6 +200,48 @@ def test_biased_encoder_on_wide_tiles_gradients_match_the_oracle(ctx):
         worst = max(worst, r)
         assert r < bar, (name, r, bar)
     print(f"worst relative L2 vs fp64 over {len(m.names)} tensors: {worst:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("inter,lengths", [(1100, (2048, 1500, 900)), (1000, (2000, 2000, 1500, 1500))])
+def test_geglu_fused_product_on_partial_tiles_matches_the_oracle(ctx, inter, lengths):
+    """The GeGLU input product with GeGLU in its epilogue where neither its rows nor its output columns fill the
+    last tile: GeGLU widths of 1100 and 1000 (128-column tiles end part-way), with mlp_bias, at 4448 and 7000
+    tokens (the 192 x 256 and the 256 x 256 kernels on 256 CUs). Logits to 1e-5 and every gradient (the backward reads
+    GeGLU's stored input and output) to max(1e-4, 4 × the fp32 oracle's error) of fp64."""
+    from laya_amd.model import TrainableDecisionModel
+    print(f"model: d=768, 1 global layer, GeGLU {inter}, {sum(lengths)} tokens", flush=True)
+    mc = mid_config(layers=1, inter=inter)
+    mc.encoder.mlp_bias = True
+    o = oracle.OracleModel(mc)
+    params = random_params(o.shapes, 7, std=0.02)
+    batch = mixed_batch(np.random.default_rng(8), list(lengths), mc.encoder.vocab_size)
+    o64 = oracle.OracleModel(mc, double=True)
+    m = TrainableDecisionModel(mc, ctx)
+    m.set_params(params)
+    dlogits = np.random.default_rng(9).standard_normal(batch.n_markers).astype(np.float32)
+    for ref in (o, o64):
+        ref.set_params(params)
+        ref.forward(batch, training=True, keep_tape=True, seed=13)
+        ref.backward(dlogits)
+    ctx.profile_begin()
+    lg = m.forward(batch, training=True, seed=13)
+    prof = ctx.profile_end()
+    fused = sorted(k for k in prof if k.startswith("gemm_nt_geglu_"))
+    print(f"fused GeGLU products: {fused}", flush=True)
+    assert fused and "geglu_fwd" not in prof, sorted(prof)
+    assert rel_l2(o64.forward(batch, training=True, keep_tape=False, seed=13), lg) < 1e-5
+    m.backward(dlogits)
+    worst = 0.0
+    for name in m.names:
+        if name == "temperature" or name.startswith("act_head"):
+            continue
+        exact = o64.grad(name)
+        bar = max(1e-4, 4 * rel_l2(exact, o.grad(name)))
+        r = rel_l2(exact, m.grad(name))
+        worst = max(worst, r)
+        assert r < bar, (name, r, bar)
+    print(f"worst relative L2 vs fp64 over {len(m.names)} tensors: {worst:.2e}", flush=True)
+    m.close()
 
 
 def test_full_train_step_matches_the_oracle(ctx):
