@@ -2327,6 +2327,37 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ P, int splits, in
     }
 }
 
+// The same two sums, four consecutive columns per thread (N, ldc and ldr multiples of 4, 16-byte aligned arrays),
+// the partial loads of several splits in flight at once; the per-element order of the additions is unchanged.
+__device__ __forceinline__ f32x4 splitk_sum4(const float* __restrict__ P, int splits, long total, long e) {
+    f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+    for (int k = 0; k < splits; ++k) s += *reinterpret_cast<const f32x4*>(P + (long)k * total + e);
+    return s;
+}
+
+__global__ void splitk_store4_kernel(const float* __restrict__ P, int splits, int M, int N, float* C, long ldc,
+                                     const float* __restrict__ bias, const float* R, long ldr) {
+    const long total = (long)M * N, quads = total >> 2;
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < quads; i += (long)gridDim.x * blockDim.x) {
+        const long e = i * 4, m = e / N, n = e - m * N;
+        f32x4 s = splitk_sum4(P, splits, total, e);
+        if (bias) s += *reinterpret_cast<const f32x4*>(bias + n);
+        if (R) s += *reinterpret_cast<const f32x4*>(R + m * ldr + n);
+        *reinterpret_cast<f32x4*>(C + m * ldc + n) = s;
+    }
+}
+
+__global__ void splitk_reduce4_kernel(const float* __restrict__ P, int splits, int M, int N, float* C, long ldc) {
+    const long total = (long)M * N, quads = total >> 2;
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < quads; i += (long)gridDim.x * blockDim.x) {
+        const long e = i * 4, m = e / N, n = e - m * N;
+        const f32x4 s = splitk_sum4(P, splits, total, e);
+        f32x4* c = reinterpret_cast<f32x4*>(C + m * ldc + n);
+        *c = *c + s;
+    }
+}
+
 __global__ void column_sum_kernel(const float* __restrict__ x, int rows, int n, float* out) {
     // One thread per column; rows summed in order (bias gradients are small: n ≤ a few thousand).
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -2820,6 +2851,12 @@ void finish_accumulate(laya_ctx* ctx, const GemmParams& p, float* out, long ldc)
     if (p.mode != PARTIAL) return;
     const long total = (long)p.M * p.N;
     ProfileScope scope(ctx, "gemm_splitk_reduce", 0.0, 4.0 * total * (p.splits + 2));
+    if (p.N % 4 == 0 && ldc % 4 == 0 && aligned16(p.C) && aligned16(out)) {
+        LAYA_LAUNCH(splitk_reduce4_kernel, dim3(blocks_for(total / 4, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
+                    p.splits, p.M, p.N, out, ldc);
+        check_launch("splitk_reduce4_kernel");
+        return;
+    }
     LAYA_LAUNCH(splitk_reduce_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
                        p.splits, p.M, p.N, out, ldc);
     check_launch("splitk_reduce_kernel");
@@ -2921,9 +2958,16 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
     if (split_store) {
         const long total = (long)M * N;
         ProfileScope scope(ctx, "gemm_splitk_store", 0.0, 4.0 * total * (p.splits + 1 + (R ? 1 : 0)));
-        LAYA_LAUNCH(splitk_store_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
-                           p.splits, M, N, C, ldc, bias, R, ldr);
-        check_launch("splitk_store_kernel");
+        if (N % 4 == 0 && ldc % 4 == 0 && aligned16(p.C) && aligned16(C) && (!bias || aligned16(bias)) &&
+            (!R || (ldr % 4 == 0 && aligned16(R)))) {
+            LAYA_LAUNCH(splitk_store4_kernel, dim3(blocks_for(total / 4, 256, 4096)), dim3(256), 0, ctx->stream,
+                        p.C, p.splits, M, N, C, ldc, bias, R, ldr);
+            check_launch("splitk_store4_kernel");
+        } else {
+            LAYA_LAUNCH(splitk_store_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
+                        p.splits, M, N, C, ldc, bias, R, ldr);
+            check_launch("splitk_store_kernel");
+        }
     } else {
         finish_accumulate(ctx, p, out, ldc);
     }
