@@ -2358,6 +2358,51 @@ __global__ void splitk_reduce4_kernel(const float* __restrict__ P, int splits, i
     }
 }
 
+// The split-K epilogue of the QKV projection with RoPE (gemm_rope on 128 x 128 tiles): each thread takes V
+// consecutive rotation pairs (columns 64h + d … and 64h + d + 32 … of row m, V = 4 with float4 access), sums
+// their partials in split order and adds the bias (splitk_store_kernel's order), rotates each pair when it
+// lies in the first rope_cols columns (the STORE_ROPE epilogue's arithmetic: a·cos − b·sin, b·cos + a·sin at
+// the row's position) and stores them; amax (optional) receives max|C|. N a multiple of 64.
+template <int V>
+__global__ __launch_bounds__(256) void splitk_store_rope_kernel(const float* __restrict__ P, int splits, int M, int N,
+                                                                float* __restrict__ C, const float* __restrict__ bias,
+                                                                const int* __restrict__ pos,
+                                                                const float* __restrict__ cos_t,
+                                                                const float* __restrict__ sin_t, int rope_cols,
+                                                                unsigned* amax) {
+    typedef float vec __attribute__((ext_vector_type(V)));
+    const long total = (long)M * N, units = total / (2 * V);
+    const int per_row = N / (2 * V), per_head = 32 / V;
+    unsigned am = 0;
+    for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < units; i += (long)gridDim.x * blockDim.x) {
+        const long m = i / per_row;
+        const int r = (int)(i - m * per_row), d = (r % per_head) * V, c0 = (r / per_head) * 64 + d, c1 = c0 + 32;
+        const long e0 = m * N + c0, e1 = m * N + c1;
+        vec a = {}, b = {};
+        for (int k = 0; k < splits; ++k) {
+            a += *reinterpret_cast<const vec*>(P + (long)k * total + e0);
+            b += *reinterpret_cast<const vec*>(P + (long)k * total + e1);
+        }
+        if (bias) {
+            a += *reinterpret_cast<const vec*>(bias + c0);
+            b += *reinterpret_cast<const vec*>(bias + c1);
+        }
+        vec v0 = a, v1 = b;
+        if (c0 < rope_cols) {
+            const int q = pos[m];
+            const vec cs = *reinterpret_cast<const vec*>(cos_t + q * 32 + d);
+            const vec sn = *reinterpret_cast<const vec*>(sin_t + q * 32 + d);
+            v0 = a * cs - b * sn;
+            v1 = b * cs + a * sn;
+        }
+        *reinterpret_cast<vec*>(C + e0) = v0;
+        *reinterpret_cast<vec*>(C + e1) = v1;
+#pragma unroll
+        for (int j = 0; j < V; ++j) am = max(am, max(amax_bits(v0[j]), amax_bits(v1[j])));
+    }
+    block_amax_fold(am, amax);
+}
+
 __global__ void column_sum_kernel(const float* __restrict__ x, int rows, int n, float* out) {
     // One thread per column; rows summed in order (bias gradients are small: n ≤ a few thousand).
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
@@ -3006,6 +3051,32 @@ void gemm_rope(laya_ctx* ctx, int M, int N, int K, const float* A, const float* 
                 prepare_pair_nt(ctx, p, amax_a, amax_b);
                 p.amax_c = big ? amax_c : nullptr;  // the 128 x 128 epilogue does not fold C's magnitude in
             }
+            // Two-piece products on 128 x 128 tiles that would not fill the chip (few rows) split K: partials,
+            // then one pass that sums them, adds the bias, rotates and measures C.
+            const int tiles = p.tiles_m * p.tiles_n;
+            if (!big && p.amax_a && N % 64 == 0 && set_splits(p, fill_splits(ctx, tiles, K, 128)) > 1) {
+                float* part = static_cast<float*>(ctx->workspace(0, sizeof(float) * (size_t)p.splits * M * N));
+                p.mode = PARTIAL;
+                p.C = part;
+                {
+                    ProfileScope scope(ctx, "gemm_nt_h2", 2.0 * M * N * (double)K, 0.0);
+                    LAYA_LAUNCH((gemm_x6_kernel<KVEC, KVEC, PARTIAL, false, 2>), dim3(tiles * p.splits),
+                                dim3(THREADS), 0, ctx->stream, p);
+                    check_launch("gemm_x6_kernel");
+                }
+                ProfileScope scope(ctx, "gemm_splitk_store", 0.0, 4.0 * (double)M * N * (p.splits + 1));
+                if (aligned16(C) && (!bias || aligned16(bias)) && aligned16(cos_t) && aligned16(sin_t))
+                    LAYA_LAUNCH(splitk_store_rope_kernel<4>, dim3(blocks_for((size_t)M * N / 8, 256, 4096)), dim3(256),
+                                0, ctx->stream, part, p.splits, M, N, C, bias, pos, cos_t, sin_t, rope_cols, amax_c);
+                else
+                    LAYA_LAUNCH(splitk_store_rope_kernel<1>, dim3(blocks_for((size_t)M * N / 2, 256, 4096)), dim3(256),
+                                0, ctx->stream, part, p.splits, M, N, C, bias, pos, cos_t, sin_t, rope_cols, amax_c);
+                check_launch("splitk_store_rope_kernel");
+                p.amax_c = amax_c;  // folded by the store pass
+                return;
+            }
+            p.splits = 1;
+            p.k_per_split = std::max(BK, (K + BK - 1) / BK * BK);
             ProfileScope scope(ctx, "gemm_nt_x6", 2.0 * M * N * (double)K, 0.0);
             if (wide_tiles_pay(ctx, p, false)) {
                 launch_wide(ctx, p);
