@@ -292,12 +292,13 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
           long ldr = 0, const __bf16* A16 = nullptr, const __bf16* B16 = nullptr, AmaxRef amax_a = {},
           AmaxRef amax_b = {}, unsigned* amax_c = nullptr);
 
-// GeGLU's input product and GeGLU (TrainableDecisionModel.cs:393-399 with Ops.cs's GeGLU): wide = x·Wᵀ + b for
-// x [M, K], W [2·inter, K] (the first half's rows, then the second's), and act = gelu(first half)·(second half)
-// [M, inter] with its bf16 copy act16 and magnitude amax_act (both optional): one launch where the product runs
-// as two-piece products on 256-wide tiles (the GeGLU in its epilogue), else the product and geglu_fwd. Both
-// forms take the same operand scales and the same GeGLU arithmetic; the products' K order (a tile's starting
-// stage) may differ between them, which moves a value by fp32 rounding only.
+// GeGLU's input product and GeGLU (TrainableDecisionModel.cs:388-397: Ops.Linear, then SimdOps.Gelu of each
+// row's first half times its second half): wide = x·Wᵀ + b for x [M, K], W [2·inter, K] (the first half's
+// rows, then the second's), and act = gelu(first half)·(second half) [M, inter] with its bf16 copy act16 and
+// magnitude amax_act (both optional): one launch where the product runs as two-piece products on 256-wide
+// tiles (the GeGLU in its epilogue), else the product and geglu_fwd. Both forms take the same operand scales
+// and the same GeGLU arithmetic; the products' K order (a tile's starting stage) may differ between them,
+// which moves a value by fp32 rounding only.
 void gemm_geglu(laya_ctx* ctx, int M, int inter, int K, const float* x, const float* W, const float* bias, float* wide,
                 float* act, __bf16* act16, const __bf16* x16 = nullptr, const __bf16* W16 = nullptr,
                 AmaxRef amax_x = {}, AmaxRef amax_W = {}, unsigned* amax_act = nullptr);
