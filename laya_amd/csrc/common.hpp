@@ -158,10 +158,33 @@ __host__ __device__ inline uint64_t attn_dropout_index(int head, int row, int ke
     return ((uint64_t)head << 42) | ((uint64_t)(uint32_t)row << 21) | (uint64_t)(uint32_t)key;
 }
 
-// Exact GELU x·Φ(x) and its derivative Φ(x) + x·φ(x), on ROCm's device erff / expf.
-__device__ inline float gelu_f(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f)); }
+// erf as the reference's float GELU evaluates it (SimdOps.cs:329-356): the Numerical Recipes rational form of
+// erfc (Press et al., Numerical Recipes in C, 2nd ed., §6.2, erfcc; fractional error below 1.2e-7),
+// erf = sign(x)·(1 − t·exp(P(t) − x²)) with t = 1 / (1 + |x|/2), and ±1 beyond |x| = 6. Branch-free: one
+// reciprocal, ten FMAs and one base-2 hardware exponential, each within an ulp or two, so the result stays
+// within a few 1e-7 of erf (ROCm's erff evaluates two polynomial branches, both where a wave's lanes differ).
+__device__ inline float erf_nr(float x) {
+    const float ax = fabsf(x);
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.5f, ax, 1.0f));
+    float p = 0.17087277f;
+    p = fmaf(p, t, -0.82215223f);
+    p = fmaf(p, t, 1.48851587f);
+    p = fmaf(p, t, -1.13520398f);
+    p = fmaf(p, t, 0.27886807f);
+    p = fmaf(p, t, -0.18628806f);
+    p = fmaf(p, t, 0.09678418f);
+    p = fmaf(p, t, 0.37409196f);
+    p = fmaf(p, t, 1.00002368f);
+    p = fmaf(p, t, -1.26551223f);
+    p = fmaf(-ax, ax, p);
+    const float y = t * __builtin_amdgcn_exp2f(p * 1.44269504088896341f);
+    return copysignf(ax > 6.0f ? 1.0f : 1.0f - y, x);
+}
+
+// Exact GELU x·Φ(x) and its derivative Φ(x) + x·φ(x) (SimdOps.cs:305-323, Ops.cs:194-218).
+__device__ inline float gelu_f(float x) { return 0.5f * x * (1.0f + erf_nr(x * 0.70710678118654752f)); }
 __device__ inline float gelu_grad_f(float x) {
-    float cdf = 0.5f * (1.0f + erff(x * 0.70710678118654752f));
+    float cdf = 0.5f * (1.0f + erf_nr(x * 0.70710678118654752f));
     float pdf = 0.39894228040143268f * __expf(-0.5f * x * x);
     return cdf + x * pdf;
 }
