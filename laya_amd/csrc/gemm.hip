@@ -2336,16 +2336,20 @@ __device__ __forceinline__ f32x4 splitk_sum4(const float* __restrict__ P, int sp
     return s;
 }
 
+// amax (optional): max|C| folded in (C's magnitude word).
 __global__ void splitk_store4_kernel(const float* __restrict__ P, int splits, int M, int N, float* C, long ldc,
-                                     const float* __restrict__ bias, const float* R, long ldr) {
+                                     const float* __restrict__ bias, const float* R, long ldr, unsigned* amax) {
     const long total = (long)M * N, quads = total >> 2;
+    unsigned am = 0;
     for (long i = blockIdx.x * (long)blockDim.x + threadIdx.x; i < quads; i += (long)gridDim.x * blockDim.x) {
         const long e = i * 4, m = e / N, n = e - m * N;
         f32x4 s = splitk_sum4(P, splits, total, e);
         if (bias) s += *reinterpret_cast<const f32x4*>(bias + n);
         if (R) s += *reinterpret_cast<const f32x4*>(R + m * ldr + n);
         *reinterpret_cast<f32x4*>(C + m * ldc + n) = s;
+        am = max(am, amax_bits4(s));
     }
+    block_amax_fold(am, amax);
 }
 
 __global__ void splitk_reduce4_kernel(const float* __restrict__ P, int splits, int M, int N, float* C, long ldc) {
@@ -2986,7 +2990,7 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
         p.amax_b = operand_amax(ctx, amax_b, 1, p.B, p.K, p.N, p.ldb);
     }
     // C's magnitude: folded in by a two-piece kernel's epilogue, else measured after the product.
-    const bool measure = amax_c && !p.amax_c;
+    bool measure = amax_c && !p.amax_c;
     {
         static const char* names[3][3] = {{"gemm_nt", "gemm_nn", "gemm_tn"},
                                           {"gemm_nt_bf16", "gemm_nn_bf16", "gemm_tn_bf16"},
@@ -3006,8 +3010,9 @@ void gemm(laya_ctx* ctx, GemmLayout layout, GemmEpilogue ep, int M, int N, int K
         if (N % 4 == 0 && ldc % 4 == 0 && aligned16(p.C) && aligned16(C) && (!bias || aligned16(bias)) &&
             (!R || (ldr % 4 == 0 && aligned16(R)))) {
             LAYA_LAUNCH(splitk_store4_kernel, dim3(blocks_for(total / 4, 256, 4096)), dim3(256), 0, ctx->stream,
-                        p.C, p.splits, M, N, C, ldc, bias, R, ldr);
+                        p.C, p.splits, M, N, C, ldc, bias, R, ldr, measure ? amax_c : nullptr);
             check_launch("splitk_store4_kernel");
+            measure = false;  // folded by the store pass
         } else {
             LAYA_LAUNCH(splitk_store_kernel, dim3(blocks_for(total, 256, 4096)), dim3(256), 0, ctx->stream, p.C,
                         p.splits, M, N, C, ldc, bias, R, ldr);
@@ -3365,8 +3370,10 @@ void gemm_backward_pair_body(laya_ctx* ctx, int rows, int in, int out, const flo
         return;
     }
     if (!fp32) {
+        // dX's magnitude: folded by the split-K store pass, or measured after the product, inside gemm().
         gemm(ctx, GemmLayout::NN, GemmEpilogue::Store, rows, in, out, dy, out, W, in, dx, in, nullptr, dx_residual,
-             in, nullptr, nullptr, amax_dy, amax_W);
+             in, nullptr, nullptr, amax_dy, amax_W, amax_dx);
+        if (folded) *folded = amax_dx != nullptr;
         gemm(ctx, GemmLayout::TN, GemmEpilogue::Accumulate, out, in, rows, dy, out, x, in, dW, in, nullptr, nullptr,
              0, nullptr, nullptr, amax_dy, amax_x);
         return;
