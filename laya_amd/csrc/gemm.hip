@@ -2078,6 +2078,17 @@ __global__ __launch_bounds__(WT_THREADS) void pair_fixup_w_kernel(GemmParams tn,
     __shared__ int slots[FIXUP_MAX_WORKERS];
     __shared__ int wave_count[WT_THREADS / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, kh = (lane >> 5) << 2;
+    const int sq = q >> 4, i = (q >> 3) & 1, j = (q >> 2) & 1, r4 = q & 3;
+    const int tm = t / tn.tiles_n;
+    const int row0 = tm * WT + 128 * sq + wm * 64 + 32 * i + 8 * r4 + kh;
+    const int col = (t - tm * tn.tiles_n) * WT + wn * 64 + 32 * j + lr;
+    // dW's current values are requested first, so their latency overlaps the slot list's set-up and the
+    // partials' loads.
+    float cur[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        cur[e] = col < tn.N && row0 + e < tn.M ? tn.C[(long)(row0 + e) * tn.ldc + col] : 0.0f;
     for (int g = tid; g <= s.G; g += WT_THREADS) run_lo[g] = plan_tn_lo(s, g);
     __syncthreads();
     int base = 0;
@@ -2101,16 +2112,7 @@ __global__ __launch_bounds__(WT_THREADS) void pair_fixup_w_kernel(GemmParams tn,
         __syncthreads();
     }
     const int n = base;
-    const int wm = wave >> 2, wn = wave & 3, lr = lane & 31, kh = (lane >> 5) << 2;
-    const int sq = q >> 4, i = (q >> 3) & 1, j = (q >> 2) & 1, r4 = q & 3;
-    const int tm = t / tn.tiles_n;
-    const int row0 = tm * WT + 128 * sq + wm * 64 + 32 * i + 8 * r4 + kh;
-    const int col = (t - tm * tn.tiles_n) * WT + wn * 64 + 32 * j + lr;
     if (col >= tn.N) return;  // no barrier follows
-    // dW's current values are requested first, so their latency overlaps the partials'.
-    float cur[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) cur[e] = row0 + e < tn.M ? tn.C[(long)(row0 + e) * tn.ldc + col] : 0.0f;
     const long off = (long)q * WT_THREADS + tid;
     f32x4 sum = f32x4{0, 0, 0, 0};
     for (int k0 = 0; k0 < n; k0 += 16) {
