@@ -145,8 +145,10 @@ __global__ void dropout_copy4_kernel(const f32x4* src, f32x4* dst, size_t n4, fl
     }
 }
 
+// amax (optional): max|dropped| folded in (its magnitude word).
 __global__ void relu_dropout_fwd4_kernel(const f32x4* wide, size_t n4, float p, float keep, uint64_t seed,
-                                         f32x4* dropped, bf16x4* dropped16) {
+                                         f32x4* dropped, bf16x4* dropped16, unsigned* amax) {
+    unsigned m = 0;
     GRID_STRIDE(i, n4) {
         const f32x4 w = wide[i];
         f32x4 o;
@@ -157,7 +159,9 @@ __global__ void relu_dropout_fwd4_kernel(const f32x4* wide, size_t n4, float p, 
         }
         dropped[i] = o;
         if (dropped16) dropped16[i] = __builtin_convertvector(o, bf16x4);
+        m = max(m, amax_bits4(o));
     }
+    block_amax_fold(m, amax);
 }
 
 // dst = bf16(src), nearest even: the bf16 copies of weights and activations the bf16 products read.
@@ -178,14 +182,18 @@ __global__ void round_bf16_scalar_kernel(const float* __restrict__ src, float* _
 // The backward from the forward's output: an element passes its gradient (times 1/(1 − p)) exactly when
 // it was kept and its pre-activation was positive, i.e. when its output is positive. Same product as
 // recomputing the mask from the pre-activation, without the per-element hash.
-__global__ void relu_dropout_bwd_out4_kernel(const f32x4* dropped, f32x4* g, size_t n4, float keep) {
+// amax (optional): max|g| (after) folded in (its magnitude word).
+__global__ void relu_dropout_bwd_out4_kernel(const f32x4* dropped, f32x4* g, size_t n4, float keep, unsigned* amax) {
+    unsigned m = 0;
     GRID_STRIDE(i, n4) {
         const f32x4 d = dropped[i];
         f32x4 v = g[i];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = d[e] > 0.0f ? v[e] * keep : 0.0f;
         g[i] = v;
+        m = max(m, amax_bits4(v));
     }
+    block_amax_fold(m, amax);
 }
 
 // Rotary.Apply (Ops.cs:489-503) over rows of [rows, head_dim].
@@ -544,14 +552,14 @@ void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p
     check_launch("dropout_copy4_kernel");
 }
 void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped,
-                      __bf16* dropped16) {
+                      __bf16* dropped16, unsigned* amax) {
     if (!n) return;
     const float keep = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
     ProfileScope scope(ctx, "relu_dropout_fwd", 0.0, (8.0 + (dropped16 ? 2.0 : 0.0)) * n);
     if (n % 4 == 0 && vec4(wide) && vec4(dropped) && ((uintptr_t)dropped16 & 7u) == 0) {
         LAYA_LAUNCH(relu_dropout_fwd4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
                            reinterpret_cast<const f32x4*>(wide), n / 4, p, keep, seed,
-                           reinterpret_cast<f32x4*>(dropped), reinterpret_cast<bf16x4*>(dropped16));
+                           reinterpret_cast<f32x4*>(dropped), reinterpret_cast<bf16x4*>(dropped16), amax);
         check_launch("relu_dropout_fwd4_kernel");
         return;
     }
@@ -559,6 +567,10 @@ void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint6
                        dropped);
     check_launch("relu_dropout_fwd_kernel");
     if (dropped16) to_bf16(ctx, dropped, n, dropped16);
+    if (amax) {
+        LAYA_REQUIRE(n <= (size_t)INT32_MAX, "relu_dropout_fwd: too many elements to measure");
+        absmax_into(ctx, dropped, 1, (int)n, (long)n, amax);
+    }
 }
 void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, float p, uint64_t seed) {
     if (!n) return;
@@ -568,13 +580,13 @@ void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, floa
                        seed);
     check_launch("relu_dropout_bwd_kernel");
 }
-void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g, size_t n, float p) {
+void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g, size_t n, float p, unsigned* amax) {
     if (!n) return;
     LAYA_REQUIRE(n % 4 == 0 && vec4(dropped) && vec4(g), "relu_dropout_bwd: 16-byte aligned multiples of 4");
     const float keep = p > 0.0f ? 1.0f / (1.0f - p) : 1.0f;
     ProfileScope scope(ctx, "relu_dropout_bwd", 0.0, 12.0 * n);
     LAYA_LAUNCH(relu_dropout_bwd_out4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
-                       reinterpret_cast<const f32x4*>(dropped), reinterpret_cast<f32x4*>(g), n / 4, keep);
+                       reinterpret_cast<const f32x4*>(dropped), reinterpret_cast<f32x4*>(g), n / 4, keep, amax);
     check_launch("relu_dropout_bwd_out4_kernel");
 }
 void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_type, int types, float* out,

@@ -22,7 +22,7 @@ void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed);
 // dst = Dropout(src) out of place (one pass).
 void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p, uint64_t seed);
 void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped,
-                      __bf16* dropped16 = nullptr);
+                      __bf16* dropped16 = nullptr, unsigned* amax = nullptr);
 void relu_dropout_bwd(laya_ctx* ctx, const float* wide, float* g, size_t n, float p, uint64_t seed);
 void rotary_apply(laya_ctx* ctx, const float* cos_t, const float* sin_t, int head_dim, float* vec, int rows,
                   const int* pos, int inverse);
@@ -36,7 +36,8 @@ void type_embedding_bwd(laya_ctx* ctx, const float* d, const int* row_type, int 
 // dst[r] += table[idx[r]] for rows r of width floats (the type embedding's add).
 void add_indexed_rows(laya_ctx* ctx, float* dst, const int* idx, int rows, int width, const float* table);
 // ReLU + dropout backward from the forward's output (positive exactly where the gradient passes).
-void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g, size_t n, float p);
+void relu_dropout_bwd_from_output(laya_ctx* ctx, const float* dropped, float* g, size_t n, float p,
+                                  unsigned* amax = nullptr);
 // out[type·n + c] += Σ rows of x[r][c] (per row type when row_type is given; types 1 or 3), in a fixed
 // order, through workspace `slot`; n % 4 == 0, 16-byte aligned.
 void column_sums(laya_ctx* ctx, const float* x, int rows, int n, const int* row_type, int types, float* out, int slot,

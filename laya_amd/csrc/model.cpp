@@ -863,7 +863,8 @@ void forward(laya_model* m, bool train, uint64_t seed) {
         layernorm_fwd(ctx, a.res, T, d, m->W(H.norm2), m->W(H.norm2_b), 1e-5f, a.n2, a.mean2, a.rstd2, nullptr,
                       nullptr, nullptr, a.n2_16, m->produce(m->aref(m->head_site(j, 2)), 7));
         linear(m, a.n2, T, d, H.linear1, H.linear1_b, ff, nullptr, a.wide, a.n2_16, m->aref(m->head_site(j, 2)));
-        relu_dropout_fwd(ctx, a.wide, (size_t)T * ff, p, salt(seed, j, 2), a.drop, a.drop16);
+        relu_dropout_fwd(ctx, a.wide, (size_t)T * ff, p, salt(seed, j, 2), a.drop, a.drop16,
+                         m->produce(m->aref(m->head_site(j, 3)), 7));
         if (p > 0.0f) {
             linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, nullptr, out, a.drop16, m->aref(m->head_site(j, 3)));
             dropout(ctx, out, (size_t)T * d, p, salt(seed, j, 3));
@@ -948,7 +949,8 @@ void head_backward(laya_model* m, int j) {
     linear_backward(m, a.drop, dy, T, ff, d, H.linear2, H.linear2_b, m->dact, nullptr, a.drop16,
                     m->head_site(j, 3));
     if (ff % 4 == 0)
-        relu_dropout_bwd_from_output(ctx, a.drop, m->dact, (size_t)T * ff, p);
+        relu_dropout_bwd_from_output(ctx, a.drop, m->dact, (size_t)T * ff, p,
+                                     m->produce(m->dref(m->head_site(j, 2)), 6));
     else
         relu_dropout_bwd(ctx, a.wide, m->dact, (size_t)T * ff, p, salt(m->seed, j, 2));
     linear_backward(m, a.n2, m->dact, T, d, ff, H.linear1, H.linear1_b, m->dn, nullptr, a.n2_16,
