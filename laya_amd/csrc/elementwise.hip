@@ -136,6 +136,17 @@ __global__ void dropout4_kernel(f32x4* v, size_t n4, float p, float keep, uint64
     }
 }
 
+// v = Dropout(v) + r in one pass (the same two operations as dropout4_kernel then add4_kernel).
+__global__ void dropout_add4_kernel(f32x4* v, const f32x4* r, size_t n4, float p, float keep, uint64_t seed) {
+    GRID_STRIDE(i, n4) {
+        f32x4 x = v[i];
+        const f32x4 y = r[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = uniform01(seed, 4 * i + e) < p ? 0.0f : x[e] * keep;
+        v[i] = x + y;
+    }
+}
+
 __global__ void dropout_copy4_kernel(const f32x4* src, f32x4* dst, size_t n4, float p, float keep, uint64_t seed) {
     GRID_STRIDE(i, n4) {
         f32x4 x = src[i];
@@ -537,6 +548,18 @@ void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed) {
     LAYA_LAUNCH(dropout_kernel, dim3(grid_for(n)), dim3(256), 0, ctx->stream, v, n, p, 1.0f / (1.0f - p),
                        seed);
     check_launch("dropout_kernel");
+}
+void dropout_add(laya_ctx* ctx, float* v, const float* r, size_t n, float p, uint64_t seed) {
+    if (!n) return;
+    if (p > 0.0f && n % 4 == 0 && vec4(v) && vec4(r)) {
+        ProfileScope scope(ctx, "dropout_add", 0.0, 12.0 * n);
+        LAYA_LAUNCH(dropout_add4_kernel, dim3(grid_for(n / 4)), dim3(256), 0, ctx->stream,
+                    reinterpret_cast<f32x4*>(v), reinterpret_cast<const f32x4*>(r), n / 4, p, 1.0f / (1.0f - p), seed);
+        check_launch("dropout_add4_kernel");
+        return;
+    }
+    dropout(ctx, v, n, p, seed);
+    add(ctx, v, r, n);
 }
 void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p, uint64_t seed) {
     if (!n) return;

@@ -19,6 +19,8 @@ void round_bf16(laya_ctx* ctx, const float* src, size_t n, float* dst);
 void geglu_bwd(laya_ctx* ctx, const float* wide, const float* dact, int rows, int inter, float* dwide,
                unsigned* amax = nullptr);
 void dropout(laya_ctx* ctx, float* v, size_t n, float p, uint64_t seed);
+// v = Dropout(v) + r (one pass where the arrays allow float4 access).
+void dropout_add(laya_ctx* ctx, float* v, const float* r, size_t n, float p, uint64_t seed);
 // dst = Dropout(src) out of place (one pass).
 void dropout_copy(laya_ctx* ctx, const float* src, float* dst, size_t n, float p, uint64_t seed);
 void relu_dropout_fwd(laya_ctx* ctx, const float* wide, size_t n, float p, uint64_t seed, float* dropped,

@@ -855,8 +855,7 @@ void forward(laya_model* m, bool train, uint64_t seed) {
                       m->produce(m->aref(m->head_site(j, 1)), 7), m->aref(m->head_site(j, 4)));
         if (p > 0.0f) {
             linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, nullptr, a.res, a.ctx16, m->aref(m->head_site(j, 1)));
-            dropout(ctx, a.res, (size_t)T * d, p, salt(seed, j, 1));
-            add(ctx, a.res, a.x, (size_t)T * d);
+            dropout_add(ctx, a.res, a.x, (size_t)T * d, p, salt(seed, j, 1));
         } else {
             linear(m, a.ctx, T, d, H.out_proj, H.out_proj_b, d, a.x, a.res, a.ctx16, m->aref(m->head_site(j, 1)));
         }
@@ -867,8 +866,7 @@ void forward(laya_model* m, bool train, uint64_t seed) {
                          m->produce(m->aref(m->head_site(j, 3)), 7));
         if (p > 0.0f) {
             linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, nullptr, out, a.drop16, m->aref(m->head_site(j, 3)));
-            dropout(ctx, out, (size_t)T * d, p, salt(seed, j, 3));
-            add(ctx, out, a.res, (size_t)T * d);
+            dropout_add(ctx, out, a.res, (size_t)T * d, p, salt(seed, j, 3));
         } else {
             linear(m, a.drop, T, ff, H.linear2, H.linear2_b, d, a.res, out, a.drop16, m->aref(m->head_site(j, 3)));
         }
